@@ -1,0 +1,214 @@
+"""Benchmark of the silogic gate-layer hot path on one MI355X.
+
+Workload ("config 2"): LogicNet(784 -> 10000 x 6,
+gate16, TopK k=8, GroupSum 10 classes, tau 10), seeded random parameters
+(torch.manual_seed(0), seed=0), synthetic Bernoulli(0.2) inputs. One step =
+``forward_hard`` on B = 65536 samples (bit-packed circuit, 64 samples per
+word) + soft ``forward`` on the first 4096 of them. Inputs are resident in
+HBM before timing starts.
+
+``value`` = hard-circuit Ggate-evals/s = 65536 * 60000 / t_hard (the
+reference's gate count, models.py:103-104); the soft rate is reported beside
+it (``soft_samples_per_s``). ``roofline`` is that of the fused hard-network
+kernel (HBM: it must read the fp32 input), with the bit-op view in
+``roofline_valu``; ``roofline_soft`` is the soft Top-K layer kernel's.
+``cpu_baseline`` times the oracle (the reference's PyTorch CPU path restated)
+on a bounded sample on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs]
+"""
+import argparse
+import json
+import os
+import platform
+import statistics
+import subprocess
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0                      # MI355X HBM3E
+VALU_BITOPS_PEAK = 256 * 64 * 2.4e9 * 32   # CUs x lanes x clock x bits = 1.258e15
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _events_ms(fn, reps):
+    """Average device time of ``fn`` on the current stream (HIP events)."""
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        fn()
+    e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_baseline(sd, x_hard, x_soft, gates):
+    """Oracle (reference PyTorch CPU path) on bounded samples of the workload."""
+    from oracle import torch_ref
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    from silogic_amd.synthetic import CONFIGS
+    spec = ("LogicNet", CONFIGS[2][1])
+    nh, ns = 4096, 512
+    xh, xs = x_hard[:nh].contiguous(), x_soft[:ns].contiguous()
+
+    def timed(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts), max(ts) - min(ts)
+
+    th, sh = timed(lambda: torch_ref.forward_hard(spec, sd, xh))
+    tsft, ss = timed(lambda: torch_ref.forward(spec, sd, xs))
+    cpu = "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        cpu = next((l.split(":", 1)[1].strip() for l in out.splitlines()
+                    if l.startswith("Model name")), cpu)
+    except Exception:
+        pass
+    return {
+        "value": round(nh * gates / th / 1e9, 4), "unit": "Ggate-evals/s",
+        "cores": threads, "kind": "port",
+        "sample": (f"oracle forward_hard on {nh} of the 65536 hard samples (median of 3 "
+                   f"after 1 warm-up, spread {sh:.3f}s, {th:.3f}s each); soft forward on "
+                   f"{ns} samples: {ns / tsft:.1f} samples/s ({tsft:.3f}s, spread {ss:.3f}s)"),
+        "soft_samples_per_s": round(ns / tsft, 2),
+        "host": {"cpu": cpu, "os_cpu_count": os.cpu_count(), "torch": torch.__version__,
+                 "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+                 "python": platform.python_version()},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(the workload shards by batch; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import silogic_amd as sl
+    from silogic_amd import ops
+    from silogic_amd.synthetic import build_config, config_inputs, BATCHES
+
+    dev = torch.device("cuda:0")
+    log("building config 2 (seeded construction) ...")
+    model = build_config(2, sl).eval()
+    sd_cpu = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(dev)
+    B_soft, B_hard, _, _ = BATCHES[2]
+    x_hard_cpu = config_inputs(2, B_hard)
+    x_hard = x_hard_cpu.to(dev)
+    x_soft = x_hard[:B_soft].contiguous()
+    gates = model.num_gates()                       # 60000 per sample
+    torch.cuda.synchronize()
+
+    def step():
+        with torch.no_grad():
+            h = model.forward_hard(x_hard)
+            s = model(x_soft)
+        return h, s
+
+    log(f"warmup {args.warmup} ...")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly K steps between synchronisations ----
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        with torch.no_grad():
+            model.forward_hard(x_hard)
+            ev[i][1].record(stream)
+            model(x_soft)
+            ev[i][2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_hard = statistics.median(a.elapsed_time(b) for a, b, _ in ev) / 1e3
+    t_soft = statistics.median(b.elapsed_time(c) for _, b, c in ev) / 1e3
+    log(f"step {wall / args.steps * 1e3:.3f} ms; hard {t_hard * 1e6:.1f} us; soft {t_soft * 1e6:.1f} us")
+
+    # ---- dominant kernels alone, HIP events on the launch stream ----
+    with torch.no_grad():
+        codes = [l.hard_codes() for l in model.layers]
+        reps = 20
+        fn_net = lambda: ops.fc_hard_net(x_hard, 0, B_hard, 784, codes, 10)   # noqa: E731
+        fn_net()
+        k_hard = _events_ms(fn_net, reps) / 1e3
+        L = model.layers[1]
+        x_mid = torch.rand(B_soft, 10000, device=dev)
+        cand, w, npar = L.soft_params(False)
+        fn_soft = lambda: ops.fc_soft(x_mid, cand, w, npar, ops.GATE16)       # noqa: E731
+        fn_soft()
+        k_soft = _events_ms(fn_soft, reps) / 1e3
+    hard_bytes = B_hard * 784 * 4 + sum(c.numel() * 4 for c in codes) + B_hard * 10 * 4
+    soft_bytes = B_soft * 10000 * 4 * 2 + 10000 * 144
+    hard_gbs = hard_bytes / k_hard / 1e9
+    soft_gbs = soft_bytes / k_soft / 1e9
+    bitops = B_hard * gates / k_hard
+
+    result = {
+        "metric": "hard-circuit Ggate-evals/s + soft fwd samples/s; % HBM/VALU roofline, 1 GPU",
+        "value": round(B_hard * gates / t_hard / 1e9, 3),
+        "unit": "Ggate-evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: LogicNet(784, 10000, 6, gate16, TopK k=8, GroupSum 10, "
+                               "tau=10); forward_hard B=65536 Bernoulli(0.2) + soft forward "
+                               "B=4096", "hard_batch": B_hard, "soft_batch": B_soft,
+                   "gates_per_sample": gates},
+        "soft_samples_per_s": round(B_soft / t_soft, 1),
+        "soft_dtype": "f32",
+        "t_hard_us": round(t_hard * 1e6, 2),
+        "t_soft_us": round(t_soft * 1e6, 2),
+        "roofline": {"kernel": "fc_hard_net_kernel (6 layers + GroupSum, fused)",
+                     "bound": "hbm", "achieved": round(hard_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes": hard_bytes,
+                     "avg_kernel_us": round(k_hard * 1e6, 2)},
+        "roofline_valu": {"kernel": "fc_hard_net_kernel", "achieved_bitops_per_s": bitops,
+                          "peak": VALU_BITOPS_PEAK, "frac": round(bitops / VALU_BITOPS_PEAK, 4)},
+        "roofline_soft": {"kernel": "fc_soft_kernel (gate16, K=8, IN=OUT=10000, B=4096)",
+                          "bound": "hbm", "achieved": round(soft_gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
+                          "algorithmic_bytes": soft_bytes, "avg_kernel_us": round(k_soft * 1e6, 2)},
+    }
+    if not args.no_cpu:
+        log("cpu baseline (oracle on host cores) ...")
+        result["cpu_baseline"] = cpu_baseline(sd_cpu, x_hard_cpu, x_hard_cpu[:B_soft], gates)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

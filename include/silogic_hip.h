@@ -1,0 +1,234 @@
+/*
+ * silogic_hip.h — C ABI of the MI355X (gfx950) gate-layer library
+ * (libsilogic_hip.so).
+ *
+ * Conventions for every entry point:
+ *   - All array pointers are DEVICE pointers owned by the caller, dense
+ *     row-major (C order) unless stated. Sizes are int64_t.
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream). Entry
+ *     points enqueue work on it and return without host synchronisation.
+ *   - Return 0 on success, a negative SLG_E_* code for a rejected argument or
+ *     shape (nothing is launched), or a positive hipError_t from the launch.
+ *     slg_last_error() returns a thread-local message for the last failure.
+ *   - No entry point allocates device memory. Workspace, where needed, is a
+ *     caller argument whose size is given by the matching *_workspace call.
+ *   - Floating-point math is IEEE fp32 (no fast-math); hard paths are exact.
+ *
+ * Bit-packed layout ("packed"): a [D, nw] array of uint64 words,
+ * nw = ceil(B / 64); sample b of feature d is bit (b % 64) of word
+ * [d, b / 64]. Byte-identical to the reference's int64 layout
+ * (silogic/bitpacking/ops.py:1-49). Conv activations are [C, H, W, nw]
+ * (the reference's B-packed [C, H*W, nw], packed_layer.py:184-214).
+ *
+ * Per-output hard FC code ("slg_code2", 8 bytes): x = index of input a,
+ * y = (index of input b) | (tt << 28), where bit g of the 4-bit tt is the
+ * gate output at address g = (a << 1) | b (silogic/nodes.py:100-106).
+ */
+#ifndef SILOGIC_HIP_H
+#define SILOGIC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* slg_stream_t;
+
+enum {
+  SLG_OK = 0,
+  SLG_E_ARG = -1,        /* null pointer / invalid enum */
+  SLG_E_SHAPE = -2,      /* size out of the supported range */
+  SLG_E_UNSUPPORTED = -3 /* valid but not implemented combination */
+};
+
+/* node kinds of the FC soft kernel */
+enum {
+  SLG_NODE_GATE16 = 0,      /* y = c0 + c1 a + c2 b + c3 ab, param = coef [OUT,4] */
+  SLG_NODE_WALSH = 1,       /* y = sigmoid((c0 + c1 a + c2 b + c3 ab) * inv_tau)  */
+  SLG_NODE_MULTILINEAR2 = 2 /* y = sum_P s_P prod_j(...), param = sigmoid(l) [OUT,4] */
+};
+
+const char* slg_last_error(void);
+int slg_version(void);
+/* number of compute units of the current device (for launch sizing) */
+int slg_device_cus(void);
+
+/* ---------------------------------------------------------------------- */
+/* FC soft forward                                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces silogic/kernels/dense.py:123-125 `dense_logic(x, ca, cb, wa, wb,
+ * coef)` (called at silogic/layers.py:121-122): x [B,IN] fp32, ca/cb [OUT,K]
+ * int32, wa/wb [OUT,K] fp32 post-softmax weights, coef [OUT,4]; out [B,OUT]
+ * = c0 + c1 a + c2 b + c3 ab with a = sum_k wa[o,k] x[b, ca[o,k]]. */
+int slg_dense_logic_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                        const int32_t* ca, const int32_t* cb, const float* wa,
+                        const float* wb, const float* coef, float* out,
+                        slg_stream_t stream);
+
+/* Replaces silogic/kernels/warp.py:104-105 `warp_logic(x, ca, cb, wa, wb,
+ * coef, inv_tau)` (called at silogic/layers.py:123): as dense_logic, then
+ * out = sigmoid(z * inv_tau). */
+int slg_warp_logic_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                       const int32_t* ca, const int32_t* cb, const float* wa,
+                       const float* wb, const float* coef, float inv_tau, float* out,
+                       slg_stream_t stream);
+
+/* General FC soft layer on the module's native layouts (replaces the
+ * LogicLayer._fused dispatch, silogic/layers.py:111-123, for gate16, walsh
+ * and multilinear arity 2): cand [OUT,2,K] int32, w [OUT,2,K] fp32,
+ * node_param [OUT,4] (coef for gate16/walsh, sigmoid(logits) for
+ * multilinear2). tile_samples / threads: 0 = automatic. */
+int slg_fc_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                    const int32_t* cand, const float* w, int32_t node_kind,
+                    const float* node_param, float inv_tau, float* out,
+                    int32_t tile_samples, int32_t threads, slg_stream_t stream);
+
+/* Soft parameter preparation for one FC layer (replaces the torch ops of
+ * TopKConnectome.weights, connectomes.py:114-119, and Gate16Node.coef /
+ * WalshNode.coef, nodes.py:82-84,138-143; sigmoid(logits), nodes.py:178):
+ *   conn [OUT,2,K] -> w = softmax over K;
+ *   gate16: raw [OUT,16] -> coef = softmax(raw) @ BASIS;
+ *   walsh:  raw [OUT,4] theta -> coef (change of variables);
+ *   multilinear2: raw [OUT,4] logits -> sigmoid(raw).
+ * conn may be NULL (K=1 fixed wiring: w = 1). */
+int slg_fc_soft_prep(const float* conn, int64_t OUT, int32_t K, int32_t node_kind,
+                     const float* raw, float* w, float* node_param, slg_stream_t stream);
+
+/* GroupSum.forward (silogic/heads.py:34-39): x [B,W] -> logits [B,C] =
+ * sum over class block of (ste ? (x > 0.5) : x), divided by tau. */
+int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau,
+                      int32_t ste, float* logits, slg_stream_t stream);
+
+/* GroupSum.forward_hard (silogic/heads.py:41-45) on unpacked features:
+ * x [B,W] (dtype 0 = fp32, 1 = uint8) -> logits [B,C] fp32 block sums. */
+int slg_groupsum_hard(const void* x, int32_t dtype, int64_t B, int64_t W, int32_t C,
+                      float* logits, slg_stream_t stream);
+
+/* OrPool.forward / forward_hard (silogic/layers.py:548-563): 2x2 max pool
+ * with floor on x [B,C,H,W] (dtype 0 = fp32, 1 = uint8) -> out. */
+int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W,
+               void* out, slg_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Hard (bit-packed) path                                                   */
+/* ---------------------------------------------------------------------- */
+
+/* LogicLayer.forward_hard input cast (layers.py:133) fused with packing:
+ * x [B,D] (dtype 0 = fp32, 1 = uint8) -> xp [D, ceil(B/64)] uint64; bit set
+ * iff uint8(x) != 0 (fp32: x >= 1). Padding bits are zero. Replaces
+ * silogic/bitpacking/ops.py:32-49 pack_bits. */
+int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, uint64_t* xp,
+                  slg_stream_t stream);
+
+/* Inverse of slg_pack_bits to uint8 [B,D] (ops.py:52-63 unpack_bits). */
+int slg_unpack_bits(const uint64_t* xp, int64_t B, int64_t D, uint8_t* out,
+                    slg_stream_t stream);
+
+/* Image packing is slg_pack_bits with D = C*H*W: [B,C,H,W] -> [C,H,W,nw],
+ * the reference's B-packed conv layout (packed_layer.py:184-214). */
+
+/* Hard FC codes for one arity-2 layer (convert.py:61-97,126-136 semantics):
+ * wiring from cand [OUT,2,K] int32 + conn [OUT,2,K] (argmax, first index on
+ * ties), or from idx [OUT,2] int32 when conn == NULL (fixed); truth table
+ * from raw: gate16 logits [OUT,16] (argmax), walsh theta [OUT,4] (corner
+ * sign of ((t0 +- t1) +- t2) +- t3), multilinear2 logits [OUT,4] (> 0).
+ * Indices are clamped into [0, IN). */
+int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_t K,
+                     int64_t IN, int32_t node_kind, const float* raw, uint32_t* codes,
+                     slg_stream_t stream);
+
+/* One packed FC layer (replaces BitpackedFCLayer.forward,
+ * packed_layer.py:85-116, and LogicLayer.forward_hard, layers.py:131-135):
+ * xin [IN,nw] -> xout [OUT,nw] with xout[o] = tt_o(xin[a_o], xin[b_o]). */
+int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw,
+                      const uint32_t* codes, int64_t OUT, uint64_t* xout,
+                      slg_stream_t stream);
+
+/* Depth-fused packed FC network + GroupSum (replaces LogicNet.forward_hard,
+ * models.py:99-101, with GroupSum.forward_hard, heads.py:41-45). Input x:
+ * in_kind 0 = fp32 rows [B,IN0], 1 = uint8 rows [B,IN0] (packed on the fly,
+ * bit = uint8(x) != 0), 2 = packed [IN0, ceil(B/64)] uint64. It runs
+ * n_layers arity-2 layers whose widths and device code arrays (from
+ * slg_fc_hard_prep) are given by the host arrays widths[n_layers] and
+ * codes[n_layers], then writes logits [B,C] fp32 = per-class popcounts of
+ * the last layer (no tau). One workgroup keeps a 64-sample (or, for wide
+ * layers, 32-sample) column of every activation in LDS across all layers.
+ * wire_r > 0 replaces the first wire_r outputs of a same-width layer by its
+ * inputs (models.py:88-94). Returns SLG_E_UNSUPPORTED when the widths do not
+ * fit LDS (see slg_fc_hard_net_supported). */
+int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
+                    const int64_t* widths, const uint32_t* const* codes, int32_t C,
+                    int64_t wire_r, float* logits, slg_stream_t stream);
+/* 64 or 32 = samples per workgroup slg_fc_hard_net would use, 0 = unsupported. */
+int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C);
+
+/* Packed GroupSum.forward_hard on xp [W,nw] (W % C == 0): logits [B,C] fp32
+ * raw counts (ops.py:66-104 without the /tau, as heads.py:41-45). */
+int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C,
+                        float* logits, slg_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Conv (ConvLogicTree + OrPool)                                            */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces silogic/kernels/conv_topk.py:175-189 `tree_conv_topk(x, coef, w,
+ * cm, ch, cw, depth, K, stride, pad, Ho, Wo)` (layers.py:458-463) and, with
+ * K = 1 and w = NULL, kernels/conv.py:399-400 `tree_conv` (layers.py:453-
+ * 457): x [B,C,H,W] fp32; coef [N, 2^depth-1, 4]; w [N, 2^depth, K];
+ * cm/ch/cw [N, 2^depth, K] int32; out [B,N,Ho,Wo]. depth in 1..4. */
+int slg_tree_conv_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                      int64_t N, int32_t depth, int32_t K, const float* coef,
+                      const float* w, const int32_t* cm, const int32_t* ch,
+                      const int32_t* cw, int32_t stride, int32_t pad, int64_t Ho,
+                      int64_t Wo, float* out, slg_stream_t stream);
+
+/* ConvLogicTree.forward + OrPool.forward fused (layers.py:448-485 and
+ * 558-559): as above for stride 1, with either a gate16 tree (node_kind 0,
+ * node_param = coef [N, 2^depth-1, 4]) or a depth-1 multilinear LUT over
+ * `arity` leaves (node_kind 2, node_param = sigmoid(logits) [N, 2^arity],
+ * arity <= 6); writes only the 2x2-max-pooled map out [B,N,Ho/2,Wo/2]
+ * (floor). pool = 0 writes the unpooled [B,N,Ho,Wo] instead. */
+int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                      int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
+                      int32_t K, const float* node_param, const float* w,
+                      const int32_t* cm, const int32_t* ch, const int32_t* cw,
+                      int32_t pad, int32_t pool, float* out, slg_stream_t stream);
+
+/* Soft conv parameters (replaces ConvLogicTree._topk_w, layers.py:487-497,
+ * _basis_coef, 408-417, and sigmoid(logits) of the LUT node, nodes.py:178):
+ * conn [N,leaves,K] -> w = softmax over K (conn == NULL: w = 1);
+ * gate16: raw [N, 2^depth-1, 16] -> param = softmax(raw) @ BASIS [N,nodes,4];
+ * multilinear: raw [N, 2^arity] -> param = sigmoid(raw). */
+int slg_conv_soft_prep(const float* conn, int64_t N, int32_t leaves, int32_t K,
+                       int32_t node_kind, int32_t depth, int32_t arity, const float* raw,
+                       float* w, float* node_param, slg_stream_t stream);
+
+/* Hard conv parameters (layers.py:505-527 + nodes.py:183-189 semantics):
+ * leaf (cm,ch,cw) by argmax over conn [N,leaves,K] (conn == NULL: K = 1,
+ * fixed) -> leaf [N, leaves] int32 packed as cm<<8 | ch<<4 | cw;
+ * tt is one uint64 per channel, [N]:
+ * gate16: raw = concatenated per-level gate logits [N, 2^depth-1, 16] ->
+ * node j's 4-bit truth table (argmax gate) in bits 4j..4j+3 (depth <= 4);
+ * multilinear (depth 1): raw [N, 2^arity] logits -> bit p = logits[p] > 0. */
+int slg_conv_hard_prep(const int32_t* cm, const int32_t* ch, const int32_t* cw,
+                       const float* conn, int64_t N, int32_t leaves, int32_t K,
+                       int32_t node_kind, int32_t depth, int32_t arity, const float* raw,
+                       int32_t* leaf, uint64_t* tt, slg_stream_t stream);
+
+/* ConvLogicTree.forward_hard + OrPool.forward_hard fused on packed
+ * activations (replaces layers.py:529-541,561-563 and the reference's
+ * packed_unfold / BitpackedConvTreeLayer / packed_or_pool,
+ * packed_layer.py:224-432): xp [C,H,W,nw] -> out [N,Ho/2,Wo/2,nw]
+ * (pool = 1) or [N,H,W,nw] (pool = 0); stride 1, zero padding `pad`. */
+int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64_t nw,
+                      int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
+                      const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
+                      int32_t pool, uint64_t* out, slg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SILOGIC_HIP_H */

@@ -1,0 +1,102 @@
+"""ctypes binding of ``libsilogic_hip.so`` (declared in ``include/silogic_hip.h``).
+
+The library is loaded from ``silogic_amd/lib`` (built in-tree by
+``__graft_entry__.build()``) or from the path in ``SILOGIC_HIP_LIB``. There is
+no fallback: if the library cannot be loaded, :func:`lib` raises and every
+GPU forward of the package raises with it.
+"""
+import ctypes as C
+import os
+import threading
+
+from . import _build
+
+_P, _I32, _I64, _F32 = C.c_void_p, C.c_int32, C.c_int64, C.c_float
+
+# name -> (restype, argtypes); mirrors include/silogic_hip.h one to one
+SIGNATURES = {
+    "slg_last_error": (C.c_char_p, []),
+    "slg_version": (C.c_int, []),
+    "slg_device_cus": (C.c_int, []),
+    "slg_dense_logic_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "slg_warp_logic_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _F32, _P, _P]),
+    "slg_fc_soft_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _F32, _P, _I32,
+                                  _I32, _P]),
+    "slg_fc_soft_prep": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "slg_groupsum_soft": (C.c_int, [_P, _I64, _I64, _I32, _F32, _I32, _P, _P]),
+    "slg_groupsum_hard": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
+    "slg_orpool": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P]),
+    "slg_pack_bits": (C.c_int, [_P, _I32, _I64, _I64, _P, _P]),
+    "slg_unpack_bits": (C.c_int, [_P, _I64, _I64, _P, _P]),
+    "slg_fc_hard_prep": (C.c_int, [_P, _P, _I64, _I32, _I64, _I32, _P, _P, _P]),
+    "slg_fc_hard_layer": (C.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),
+    "slg_fc_hard_net": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _I32, _I64, _P, _P]),
+    "slg_fc_hard_net_supported": (C.c_int, [_I64, _I32, _P, _I32]),
+    "slg_groupsum_packed": (C.c_int, [_P, _I64, _I64, _I32, _P, _P]),
+    "slg_tree_conv_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P,
+                                    _P, _I32, _I32, _I64, _I64, _P, _P]),
+    "slg_conv_soft_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P,
+                                    _P, _P, _P, _P, _I32, _I32, _P, _P]),
+    "slg_conv_soft_prep": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "slg_conv_hard_prep": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P,
+                                     _P, _P]),
+    "slg_conv_hard_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P,
+                                    _I32, _I32, _I32, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+_load_error = None
+
+
+def library_path():
+    return os.environ.get("SILOGIC_HIP_LIB", _build.LIB)
+
+
+def lib():
+    """Load (once) and return the library; raise ``ImportError`` if absent."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not os.path.exists(path):
+            _load_error = f"{path} not found: build it with __graft_entry__.build()"
+            raise ImportError("silogic_amd HIP library unavailable: " + _load_error)
+        try:
+            h = C.CDLL(path)
+        except OSError as e:
+            _load_error = str(e)
+            raise ImportError("silogic_amd HIP library failed to load: " + _load_error) from e
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+        return _lib
+
+
+def available():
+    try:
+        lib()
+        return True
+    except ImportError:
+        return False
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = lib().slg_last_error().decode(errors="replace")
+        raise HipError(f"{what} failed (code {rc}): {msg}")
+
+
+def call(name, *args):
+    """Call entry point ``name``; raise :class:`HipError` on a non-zero code."""
+    fn = getattr(lib(), name)
+    check(fn(*args), name)

@@ -1,0 +1,539 @@
+// ConvLogicTree + OrPool for gfx950: soft (fp32) and hard (bit-packed), each
+// with the 2x2 OR-pool fused so only the pooled map is written.
+//
+// Soft design: a workgroup owns S samples and every output channel. It stages
+// the S input images in LDS in a zero-padded layout whose right padding is
+// shared with the next row's left padding (row stride W+pad, plane
+// (H+2pad)(W+pad)+pad floats), so every tap of every output position is one
+// LDS read at base(position) + off(tap) with no bounds test. Waves take
+// tasks = (output channel, 64 consecutive (sample, position) pairs); the
+// channel is wave-uniform, so tap offsets, leaf weights and node
+// coefficients come from scalar loads. Each lane evaluates the tree at the
+// 2x2 positions of its pooled output and keeps the max.
+//
+// Hard design: B-packed activations [C,H,W,nw] (64 samples per word).
+// Threads walk (pooled position, word) with the word index fastest, so
+// neighbouring lanes read neighbouring words of the same pixel; the output
+// channel is the grid's y index, so leaf taps and truth tables are uniform.
+#include <math.h>
+
+#include "slg_common.h"
+
+namespace slg {
+
+__device__ inline float sigmoidc(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+constexpr int kMaxK = 8;
+
+// NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree) or
+// SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1).
+template <int NODE, int NLEAF, bool POOL>
+__global__ void __launch_bounds__(256)
+conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
+                 int pad, const float* __restrict__ np, const float* __restrict__ wts,
+                 const int* __restrict__ cm, const int* __restrict__ ch, const int* __restrict__ cw,
+                 int S, float* __restrict__ out, int Ho, int Wo) {
+  extern __shared__ float lds[];
+  const int RS = W + pad;
+  const int plane = (H + 2 * pad) * RS + pad;
+  const int SST = C * plane;
+  const int b0 = blockIdx.x * S;
+  const int ns = min(S, B - b0);
+
+  for (int sc = 0; sc < ns * C; ++sc) {  // stage images, zero padding included
+    const float* src = x + ((int64_t)b0 * C + sc) * H * W;
+    float* dst = lds + sc * plane;
+    for (int q = threadIdx.x; q < plane; q += blockDim.x) {
+      const int yy = q / RS - pad;
+      const int xx = q - (yy + pad) * RS - pad;
+      float v = 0.0f;
+      if (yy >= 0 && yy < H && xx >= 0 && xx < W) v = src[yy * W + xx];
+      dst[q] = v;
+    }
+  }
+  __syncthreads();
+
+  const int P = Ho * Wo;
+  const int per_n = (ns * P + 63) / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
+  constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
+
+  for (int task = wave; task < N * per_n; task += nwaves) {
+    const int n = __builtin_amdgcn_readfirstlane(task / per_n);
+    const int sp = (task - n * per_n) * 64 + lane;
+    const bool active = sp < ns * P;
+    const int s = active ? sp / P : 0;
+    const int p = active ? sp - s * P : 0;
+    const int oy = (p / Wo) * (POOL ? 2 : 1);
+    const int ox = (p - (p / Wo) * Wo) * (POOL ? 2 : 1);
+    const int base = s * SST + oy * RS + ox;
+
+    int off[NLEAF][kMaxK];
+    float wt[NLEAF][kMaxK];
+#pragma unroll
+    for (int l = 0; l < NLEAF; ++l) {
+#pragma unroll
+      for (int k = 0; k < kMaxK; ++k) {
+        if (k < K) {
+          const int idx = (n * NLEAF + l) * K + k;
+          const int c_ = min(max(cm[idx], 0), C - 1);
+          const int h_ = min(max(ch[idx], 0), kernel - 1);
+          const int w_ = min(max(cw[idx], 0), kernel - 1);
+          off[l][k] = c_ * plane + h_ * RS + w_;
+          wt[l][k] = wts ? wts[idx] : 1.0f;
+        } else {
+          off[l][k] = 0;
+          wt[l][k] = 0.0f;
+        }
+      }
+    }
+    float prm[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) prm[i] = np[(int64_t)n * NP + i];
+    float dif[(NODE == SLG_NODE_GATE16) ? 1 : (1 << (NLEAF - 1))];
+    if constexpr (NODE != SLG_NODE_GATE16) {
+#pragma unroll
+      for (int m = 0; m < (1 << (NLEAF - 1)); ++m) dif[m] = prm[2 * m + 1] - prm[2 * m];
+    }
+
+    float best = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < (POOL ? 4 : 1); ++q) {
+      const int pb = base + (q >> 1) * RS + (q & 1);
+      float v[NLEAF];
+#pragma unroll
+      for (int l = 0; l < NLEAF; ++l) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kMaxK; ++k)
+          if (k < K) acc = fmaf(wt[l][k], lds[pb + off[l][k]], acc);
+        v[l] = acc;
+      }
+      float val;
+      if constexpr (NODE == SLG_NODE_GATE16) {
+        // level i combines children 2m (a) and 2m+1 (b), node ids level-major
+        // (silogic/layers.py:388-401, 408-417)
+        int nb = 0;
+#pragma unroll
+        for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
+#pragma unroll
+          for (int m = 0; m < cnt / 2; ++m) {
+            const float a = v[2 * m], b = v[2 * m + 1];
+            const float* c = prm + 4 * (nb + m);
+            v[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+          }
+          nb += cnt / 2;
+        }
+        val = v[0];
+      } else {
+        // multilinear interpolation of s over the leaves (corner bit j = leaf j),
+        // silogic/nodes.py:174-178, as a lerp tree
+        float t[1 << (NLEAF - 1)];
+#pragma unroll
+        for (int m = 0; m < (1 << (NLEAF - 1)); ++m) t[m] = fmaf(v[0], dif[m], prm[2 * m]);
+#pragma unroll
+        for (int j = 1; j < NLEAF; ++j) {
+#pragma unroll
+          for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
+            t[m] = fmaf(v[j], t[2 * m + 1] - t[2 * m], t[2 * m]);
+        }
+        val = t[0];
+      }
+      best = fmaxf(best, val);
+    }
+    if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
+  }
+}
+
+template <int NODE, int NLEAF, bool POOL>
+__global__ void __launch_bounds__(256)
+conv_hard_kernel(const uint64_t* __restrict__ xp, int C, int H, int W, int nw, int N,
+                 const int* __restrict__ leaf, const uint64_t* __restrict__ tt, int kernel, int pad,
+                 uint64_t* __restrict__ out, int Ho, int Wo) {
+  const int n = blockIdx.y;
+  const int P = Ho * Wo;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)P * nw) return;
+  const int p = (int)(i / nw), w = (int)(i - (int64_t)p * nw);
+  const int oy = (p / Wo) * (POOL ? 2 : 1);
+  const int ox = (p % Wo) * (POOL ? 2 : 1);
+  int lc[NLEAF], lh[NLEAF], lw[NLEAF];
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l) {
+    const int code = leaf[n * NLEAF + l];
+    lc[l] = min(max(code >> 8, 0), C - 1);
+    lh[l] = min((code >> 4) & 15, kernel - 1);
+    lw[l] = min(code & 15, kernel - 1);
+  }
+  const uint64_t T = tt[n];
+  uint64_t acc = 0;
+#pragma unroll
+  for (int q = 0; q < (POOL ? 4 : 1); ++q) {
+    const int py = oy + (q >> 1), px = ox + (q & 1);
+    uint64_t v[NLEAF];
+#pragma unroll
+    for (int l = 0; l < NLEAF; ++l) {
+      const int iy = py + lh[l] - pad, ix = px + lw[l] - pad;
+      v[l] = (iy >= 0 && iy < H && ix >= 0 && ix < W)
+                 ? xp[(((int64_t)lc[l] * H + iy) * W + ix) * nw + w]
+                 : 0ull;
+    }
+    uint64_t val;
+    if constexpr (NODE == SLG_NODE_GATE16) {
+      int nb = 0;
+#pragma unroll
+      for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
+#pragma unroll
+        for (int m = 0; m < cnt / 2; ++m) {
+          const uint32_t g = (uint32_t)(T >> (4 * (nb + m))) & 15u;
+          const uint64_t a = v[2 * m], b = v[2 * m + 1];
+          const uint64_t t0 = 0ull - (uint64_t)(g & 1u), t1 = 0ull - (uint64_t)((g >> 1) & 1u);
+          const uint64_t t2 = 0ull - (uint64_t)((g >> 2) & 1u), t3 = 0ull - (uint64_t)((g >> 3) & 1u);
+          v[m] = (a & ((b & t3) | (~b & t2))) | (~a & ((b & t1) | (~b & t0)));
+        }
+        nb += cnt / 2;
+      }
+      val = v[0];
+    } else {
+      // Shannon mux tree over address bits (leaf j = address bit j),
+      // silogic/nodes.py:183-189
+      uint64_t t[1 << (NLEAF - 1)];
+#pragma unroll
+      for (int m = 0; m < (1 << (NLEAF - 1)); ++m) {
+        const uint64_t e0 = 0ull - ((T >> (2 * m)) & 1ull);
+        const uint64_t e1 = 0ull - ((T >> (2 * m + 1)) & 1ull);
+        t[m] = (v[0] & e1) | (~v[0] & e0);
+      }
+#pragma unroll
+      for (int j = 1; j < NLEAF; ++j) {
+#pragma unroll
+        for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
+          t[m] = (v[j] & t[2 * m + 1]) | (~v[j] & t[2 * m]);
+      }
+      val = t[0];
+    }
+    acc |= val;
+  }
+  out[((int64_t)n * P + p) * nw + w] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// prep kernels
+// ---------------------------------------------------------------------------
+__constant__ float c_basis_conv[16][4] = {
+    {0, 0, 0, 0}, {0, 0, 0, 1}, {0, 1, 0, -1}, {0, 1, 0, 0}, {0, 0, 1, -1}, {0, 0, 1, 0},
+    {0, 1, 1, -2}, {0, 1, 1, -1}, {1, -1, -1, 1}, {1, -1, -1, 2}, {1, 0, -1, 0},
+    {1, 0, -1, 1}, {1, -1, 0, 0}, {1, -1, 0, 1}, {1, 0, 0, -1}, {1, 0, 0, 0}};
+__constant__ uint8_t c_tt16_conv[16] = {0x0, 0x8, 0x4, 0xC, 0x2, 0xA, 0x6, 0xE,
+                                        0x1, 0x9, 0x5, 0xD, 0x3, 0xB, 0x7, 0xF};
+
+__global__ void conv_soft_prep_kernel(const float* __restrict__ conn, int N, int leaves, int K,
+                                      int node, int nodes, int arity, const float* __restrict__ raw,
+                                      float* __restrict__ w, float* __restrict__ np) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  for (int l = 0; l < leaves; ++l) {
+    const int64_t base = ((int64_t)n * leaves + l) * K;
+    if (!conn) {
+      for (int k = 0; k < K; ++k) w[base + k] = 1.0f;
+      continue;
+    }
+    float m = conn[base];
+    for (int k = 1; k < K; ++k) m = fmaxf(m, conn[base + k]);
+    float sum = 0.f;
+    for (int k = 0; k < K; ++k) sum += expf(conn[base + k] - m);
+    for (int k = 0; k < K; ++k) w[base + k] = expf(conn[base + k] - m) / sum;
+  }
+  if (node == SLG_NODE_GATE16) {
+    for (int j = 0; j < nodes; ++j) {
+      const float* g = raw + ((int64_t)n * nodes + j) * 16;
+      float m = g[0];
+      for (int i = 1; i < 16; ++i) m = fmaxf(m, g[i]);
+      float e[16], sum = 0.f;
+      for (int i = 0; i < 16; ++i) { e[i] = expf(g[i] - m); sum += e[i]; }
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 16; ++i) {
+        const float pr = e[i] / sum;
+        for (int q = 0; q < 4; ++q) acc[q] += pr * c_basis_conv[i][q];
+      }
+      for (int q = 0; q < 4; ++q) np[((int64_t)n * nodes + j) * 4 + q] = acc[q];
+    }
+  } else {
+    const int P = 1 << arity;
+    for (int q = 0; q < P; ++q) np[(int64_t)n * P + q] = sigmoidc(raw[(int64_t)n * P + q]);
+  }
+}
+
+__global__ void conv_hard_prep_kernel(const int* __restrict__ cm, const int* __restrict__ ch,
+                                      const int* __restrict__ cw, const float* __restrict__ conn,
+                                      int N, int leaves, int K, int node, int nodes, int arity,
+                                      const float* __restrict__ raw, int* __restrict__ leaf,
+                                      uint64_t* __restrict__ tt) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  for (int l = 0; l < leaves; ++l) {
+    const int64_t base = ((int64_t)n * leaves + l) * K;
+    int k = 0;
+    if (conn) {  // first index of the max, as torch.argmax (layers.py:511-513)
+      float bv = conn[base];
+      for (int j = 1; j < K; ++j)
+        if (conn[base + j] > bv) { bv = conn[base + j]; k = j; }
+    }
+    leaf[n * leaves + l] = (cm[base + k] << 8) | ((ch[base + k] & 15) << 4) | (cw[base + k] & 15);
+  }
+  uint64_t t = 0;
+  if (node == SLG_NODE_GATE16) {
+    for (int j = 0; j < nodes; ++j) {
+      const float* g = raw + ((int64_t)n * nodes + j) * 16;
+      int bi = 0;
+      float bv = g[0];
+      for (int i = 1; i < 16; ++i)
+        if (g[i] > bv) { bv = g[i]; bi = i; }
+      t |= (uint64_t)c_tt16_conv[bi] << (4 * j);
+    }
+  } else {
+    const int P = 1 << arity;
+    for (int q = 0; q < P; ++q)
+      if (raw[(int64_t)n * P + q] > 0.0f) t |= 1ull << q;
+  }
+  tt[n] = t;
+}
+
+template <typename T>
+__global__ void orpool_kernel(const T* __restrict__ x, int64_t BC, int H, int W, T* __restrict__ out) {
+  const int Ho = H / 2, Wo = W / 2;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= BC * Ho * Wo) return;
+  const int64_t bc = i / (Ho * Wo);
+  const int r = (int)(i - bc * Ho * Wo);
+  const int py = r / Wo, px = r - (r / Wo) * Wo;
+  const T* src = x + bc * H * W + (2 * py) * W + 2 * px;
+  T m = src[0];
+  m = m > src[1] ? m : src[1];
+  m = m > src[W] ? m : src[W];
+  m = m > src[W + 1] ? m : src[W + 1];
+  out[i] = m;
+}
+
+// ---------------------------------------------------------------------------
+// launch helpers
+// ---------------------------------------------------------------------------
+struct ConvSoftArgs {
+  const float* x; int64_t B, C, H, W, N; int K, kernel, pad;
+  const float* np; const float* w; const int* cm; const int* ch; const int* cw;
+  float* out; int64_t Ho, Wo;
+};
+
+template <int NODE, int NLEAF, bool POOL>
+static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
+  const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
+  const int64_t per_sample = a.C * plane * 4;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  SLG_REQUIRE(per_sample <= cap, SLG_E_UNSUPPORTED, "conv_soft: one image (%lld B) exceeds LDS",
+              (long long)per_sample);
+  // samples per workgroup: enough (sample, position) pairs for a wave, while
+  // keeping at least 2 workgroups per CU when the image is small
+  const int64_t P = a.Ho * a.Wo;
+  int64_t S = std::max<int64_t>(1, cdiv(64, P));
+  S = std::min<int64_t>(S, std::max<int64_t>(1, cap / per_sample));
+  S = std::min<int64_t>(S, a.B);
+  const size_t lds = (size_t)(S * per_sample);
+  auto kern = conv_soft_kernel<NODE, NLEAF, POOL>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("conv_soft: LDS %zu: %s", lds, hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(256), lds, st, a.x, (int)a.B,
+                     (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, a.np, a.w, a.cm,
+                     a.ch, a.cw, (int)S, a.out, (int)a.Ho, (int)a.Wo);
+  SLG_LAUNCH_CHECK("conv_soft");
+  return 0;
+}
+
+template <bool POOL>
+static int conv_soft_dispatch(const ConvSoftArgs& a, int node, int nleaf, hipStream_t st) {
+  if (node == SLG_NODE_GATE16) {
+    switch (nleaf) {
+      case 2: return launch_conv_soft<SLG_NODE_GATE16, 2, POOL>(a, st);
+      case 4: return launch_conv_soft<SLG_NODE_GATE16, 4, POOL>(a, st);
+      case 8: return launch_conv_soft<SLG_NODE_GATE16, 8, POOL>(a, st);
+      case 16: return launch_conv_soft<SLG_NODE_GATE16, 16, POOL>(a, st);
+      default: break;
+    }
+  } else {
+    switch (nleaf) {
+      case 2: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 2, POOL>(a, st);
+      case 3: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 3, POOL>(a, st);
+      case 4: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 4, POOL>(a, st);
+      case 5: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 5, POOL>(a, st);
+      case 6: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 6, POOL>(a, st);
+      default: break;
+    }
+  }
+  set_error("conv_soft: unsupported leaves %d", nleaf);
+  return SLG_E_UNSUPPORTED;
+}
+
+template <int NODE, int NLEAF, bool POOL>
+static int launch_conv_hard(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64_t nw,
+                            int64_t N, const int* leaf, const uint64_t* tt, int kernel, int pad,
+                            uint64_t* out, int64_t Ho, int64_t Wo, hipStream_t st) {
+  const int64_t n = Ho * Wo * nw;
+  SLG_REQUIRE(n < (1LL << 40) && N < 65536, SLG_E_SHAPE, "conv_hard: too large");
+  hipLaunchKernelGGL((conv_hard_kernel<NODE, NLEAF, POOL>), dim3((unsigned)cdiv(n, 256), (unsigned)N),
+                     dim3(256), 0, st, xp, (int)C, (int)H, (int)W, (int)nw, (int)N, leaf, tt,
+                     kernel, pad, out, (int)Ho, (int)Wo);
+  SLG_LAUNCH_CHECK("conv_hard");
+  return 0;
+}
+
+template <bool POOL>
+static int conv_hard_dispatch(int node, int nleaf, const uint64_t* xp, int64_t C, int64_t H,
+                              int64_t W, int64_t nw, int64_t N, const int* leaf, const uint64_t* tt,
+                              int kernel, int pad, uint64_t* out, int64_t Ho, int64_t Wo,
+                              hipStream_t st) {
+#define SLG_CH(ND, NL) \
+  return launch_conv_hard<ND, NL, POOL>(xp, C, H, W, nw, N, leaf, tt, kernel, pad, out, Ho, Wo, st)
+  if (node == SLG_NODE_GATE16) {
+    switch (nleaf) {
+      case 2: SLG_CH(SLG_NODE_GATE16, 2);
+      case 4: SLG_CH(SLG_NODE_GATE16, 4);
+      case 8: SLG_CH(SLG_NODE_GATE16, 8);
+      case 16: SLG_CH(SLG_NODE_GATE16, 16);
+      default: break;
+    }
+  } else {
+    switch (nleaf) {
+      case 2: SLG_CH(SLG_NODE_MULTILINEAR2, 2);
+      case 3: SLG_CH(SLG_NODE_MULTILINEAR2, 3);
+      case 4: SLG_CH(SLG_NODE_MULTILINEAR2, 4);
+      case 5: SLG_CH(SLG_NODE_MULTILINEAR2, 5);
+      case 6: SLG_CH(SLG_NODE_MULTILINEAR2, 6);
+      default: break;
+    }
+  }
+#undef SLG_CH
+  set_error("conv_hard: unsupported leaves %d", nleaf);
+  return SLG_E_UNSUPPORTED;
+}
+
+static int node_leaves(int node, int depth, int arity) {
+  if (node == SLG_NODE_GATE16) return (depth >= 1 && depth <= 4) ? (1 << depth) : -1;
+  if (node == SLG_NODE_MULTILINEAR2) return (depth == 1 && arity >= 2 && arity <= 6) ? arity : -1;
+  return -1;
+}
+
+}  // namespace slg
+
+using namespace slg;
+
+extern "C" {
+
+int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                      int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                      const float* node_param, const float* w, const int32_t* cm, const int32_t* ch,
+                      const int32_t* cw, int32_t pad, int32_t pool, float* out, slg_stream_t stream) {
+  SLG_REQUIRE(x && node_param && cm && ch && cw && out, SLG_E_ARG, "conv_soft: null pointer");
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
+              "conv_soft: node_kind %d", node_kind);
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft: K=%d outside 1..%d", K, kMaxK);
+  SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && N > 0 && pad >= 0 && pad <= 4 &&
+                  B < (1LL << 31) && N < (1LL << 20) && C < (1LL << 20) && H < 4096 && W < 4096,
+              SLG_E_SHAPE, "conv_soft: bad sizes");
+  const int kernel = 2 * pad + 1;  // 'same' convolution, stride 1 (models.py:222)
+  const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
+  const int64_t Ho = pool ? Hf / 2 : Hf, Wo = pool ? Wf / 2 : Wf;
+  if (B == 0 || Ho == 0 || Wo == 0) return 0;
+  ConvSoftArgs a{x, B, C, H, W, N, K, kernel, pad, node_param, w, cm, ch, cw, out, Ho, Wo};
+  return pool ? conv_soft_dispatch<true>(a, node_kind, nleaf, as_stream(stream))
+              : conv_soft_dispatch<false>(a, node_kind, nleaf, as_stream(stream));
+}
+
+int slg_tree_conv_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                      int32_t depth, int32_t K, const float* coef, const float* w, const int32_t* cm,
+                      const int32_t* ch, const int32_t* cw, int32_t stride, int32_t pad, int64_t Ho,
+                      int64_t Wo, float* out, slg_stream_t stream) {
+  SLG_REQUIRE(stride == 1, SLG_E_UNSUPPORTED, "tree_conv: stride %d (only 1)", stride);
+  SLG_REQUIRE(Ho == H && Wo == W, SLG_E_UNSUPPORTED,
+              "tree_conv: only 'same' convolutions (kernel = 2*pad+1) are supported");
+  return slg_conv_soft_fwd(x, B, C, H, W, N, SLG_NODE_GATE16, depth, 2, K, coef, w, cm, ch, cw,
+                           pad, 0, out, stream);
+}
+
+int slg_conv_soft_prep(const float* conn, int64_t N, int32_t leaves, int32_t K, int32_t node_kind,
+                       int32_t depth, int32_t arity, const float* raw, float* w, float* node_param,
+                       slg_stream_t stream) {
+  SLG_REQUIRE(raw && w && node_param, SLG_E_ARG, "conv_soft_prep: null pointer");
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0 && nleaf == leaves, SLG_E_UNSUPPORTED, "conv_soft_prep: leaves %d", leaves);
+  SLG_REQUIRE(N > 0 && N < (1LL << 31) && K >= 1 && K <= 64, SLG_E_SHAPE, "conv_soft_prep: sizes");
+  hipLaunchKernelGGL(conv_soft_prep_kernel, dim3((unsigned)cdiv(N, 128)), dim3(128), 0,
+                     as_stream(stream), conn, (int)N, leaves, K, node_kind, nleaf - 1, arity, raw, w,
+                     node_param);
+  SLG_LAUNCH_CHECK("conv_soft_prep");
+  return 0;
+}
+
+int slg_conv_hard_prep(const int32_t* cm, const int32_t* ch, const int32_t* cw, const float* conn,
+                       int64_t N, int32_t leaves, int32_t K, int32_t node_kind, int32_t depth,
+                       int32_t arity, const float* raw, int32_t* leaf, uint64_t* tt,
+                       slg_stream_t stream) {
+  SLG_REQUIRE(cm && ch && cw && raw && leaf && tt, SLG_E_ARG, "conv_hard_prep: null pointer");
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0 && nleaf == leaves, SLG_E_UNSUPPORTED, "conv_hard_prep: leaves %d", leaves);
+  SLG_REQUIRE(N > 0 && N < (1LL << 31) && K >= 1 && K <= 64, SLG_E_SHAPE, "conv_hard_prep: sizes");
+  hipLaunchKernelGGL(conv_hard_prep_kernel, dim3((unsigned)cdiv(N, 128)), dim3(128), 0,
+                     as_stream(stream), cm, ch, cw, conn, (int)N, leaves, K, node_kind, nleaf - 1,
+                     arity, raw, leaf, tt);
+  SLG_LAUNCH_CHECK("conv_hard_prep");
+  return 0;
+}
+
+int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64_t nw, int64_t N,
+                      int32_t node_kind, int32_t depth, int32_t arity, const int32_t* leaf,
+                      const uint64_t* tt, int32_t kernel, int32_t pad, int32_t pool, uint64_t* out,
+                      slg_stream_t stream) {
+  SLG_REQUIRE(xp && leaf && tt && out, SLG_E_ARG, "conv_hard: null pointer");
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_hard: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(C > 0 && H > 0 && W > 0 && nw >= 0 && N > 0 && kernel >= 1 && kernel <= 15 &&
+                  pad >= 0 && H < 4096 && W < 4096 && C < (1LL << 23),
+              SLG_E_SHAPE, "conv_hard: bad sizes");
+  const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
+  SLG_REQUIRE(Hf > 0 && Wf > 0, SLG_E_SHAPE, "conv_hard: empty output");
+  const int64_t Ho = pool ? Hf / 2 : Hf, Wo = pool ? Wf / 2 : Wf;
+  if (nw == 0 || Ho == 0 || Wo == 0) return 0;
+  hipStream_t st = as_stream(stream);
+  return pool ? conv_hard_dispatch<true>(node_kind, nleaf, xp, C, H, W, nw, N, leaf, tt, kernel,
+                                         pad, out, Ho, Wo, st)
+              : conv_hard_dispatch<false>(node_kind, nleaf, xp, C, H, W, nw, N, leaf, tt, kernel,
+                                          pad, out, Ho, Wo, st);
+}
+
+int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W, void* out,
+               slg_stream_t stream) {
+  SLG_REQUIRE(x && out, SLG_E_ARG, "orpool: null pointer");
+  SLG_REQUIRE(dtype == 0 || dtype == 1, SLG_E_ARG, "orpool: dtype %d", dtype);
+  SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && B * C * H * W < (1LL << 46), SLG_E_SHAPE,
+              "orpool: bad sizes");
+  const int64_t n = B * C * (H / 2) * (W / 2);
+  if (n == 0) return 0;
+  if (dtype == 0)
+    hipLaunchKernelGGL(orpool_kernel<float>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                       as_stream(stream), (const float*)x, B * C, (int)H, (int)W, (float*)out);
+  else
+    hipLaunchKernelGGL(orpool_kernel<uint8_t>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                       as_stream(stream), (const uint8_t*)x, B * C, (int)H, (int)W, (uint8_t*)out);
+  SLG_LAUNCH_CHECK("orpool");
+  return 0;
+}
+
+}  // extern "C"

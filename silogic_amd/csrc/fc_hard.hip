@@ -1,0 +1,448 @@
+// Bit-packed hard path for gfx950: packing, hard-parameter prep, packed FC
+// layers, the depth-fused FC network with its GroupSum popcount, and the
+// packed GroupSum.
+//
+// Packed words carry 64 samples (one wavefront ballot). A gate16 node on two
+// words is three bit-field-inserts per 32-bit half:
+//   out = bfi(a, bfi(b, T3, T2), bfi(b, T1, T0)),  T_g = tt bit g ? ~0 : 0,
+// so one output word costs the same whatever the gate, with no branching.
+#include "slg_common.h"
+
+namespace slg {
+
+template <typename WT>
+__device__ inline WT gate_word(WT a, WT b, uint32_t tt) {
+  const WT t0 = (WT)0 - (WT)(tt & 1u);
+  const WT t1 = (WT)0 - (WT)((tt >> 1) & 1u);
+  const WT t2 = (WT)0 - (WT)((tt >> 2) & 1u);
+  const WT t3 = (WT)0 - (WT)((tt >> 3) & 1u);
+  const WT hi = (b & t3) | (~b & t2);  // a = 1: addresses 3 (b=1), 2 (b=0)
+  const WT lo = (b & t1) | (~b & t0);  // a = 0: addresses 1 (b=1), 0 (b=0)
+  return (a & hi) | (~a & lo);
+}
+
+// 64x64 bit transpose across a wavefront: lane r holds row r; afterwards
+// lane r holds column r (bit c of the result = bit r of lane c's input).
+// Stage s swaps bit s of the row index with bit s of the column index.
+__device__ inline uint64_t transpose64(uint64_t v, int lane) {
+  const uint64_t masks[6] = {0x00000000FFFFFFFFull, 0x0000FFFF0000FFFFull,
+                             0x00FF00FF00FF00FFull, 0x0F0F0F0F0F0F0F0Full,
+                             0x3333333333333333ull, 0x5555555555555555ull};
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int s = 32 >> i;
+    const uint64_t m = masks[i];
+    const uint32_t lo = __shfl_xor((uint32_t)v, s);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), s);
+    const uint64_t other = ((uint64_t)hi << 32) | lo;
+    if (lane & s) v = (v & ~m) | ((other & ~m) >> s);
+    else v = (v & m) | ((other & m) << s);
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// pack / unpack
+// ---------------------------------------------------------------------------
+// Tile: 64 samples (one output word) x 64 features. Coalesced row reads into
+// LDS, then one ballot per feature.
+template <typename T>
+__global__ void __launch_bounds__(256) pack_kernel(const T* __restrict__ x, int B, int D, int nw,
+                                                   int dtiles, uint64_t* __restrict__ xp) {
+  __shared__ uint8_t tile[64][68];
+  const int w = (int)(blockIdx.x / (uint32_t)dtiles);
+  const int d0 = (int)(blockIdx.x % (uint32_t)dtiles) * 64;
+  const int c = threadIdx.x & 63;
+  for (int r = threadIdx.x >> 6; r < 64; r += 4) {
+    const int b = w * 64 + r, d = d0 + c;
+    uint8_t bit = 0;
+    if (b < B && d < D) {
+      const T v = x[(int64_t)b * D + d];
+      if constexpr (sizeof(T) == 1) bit = (v != 0);
+      else bit = (v >= (T)1);
+    }
+    tile[r][c] = bit;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int j = 0; j < 16; ++j) {
+    const int cc = wave * 16 + j;
+    const uint64_t m = __ballot(tile[lane][cc] != 0);
+    if (lane == 0 && d0 + cc < D) xp[(int64_t)(d0 + cc) * nw + w] = m;
+  }
+}
+
+__global__ void __launch_bounds__(256) unpack_kernel(const uint64_t* __restrict__ xp, int B, int D,
+                                                     int nw, uint8_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * D) return;
+  const int b = (int)(i / D), d = (int)(i % D);
+  out[i] = (uint8_t)((xp[(int64_t)d * nw + (b >> 6)] >> (b & 63)) & 1ull);
+}
+
+// ---------------------------------------------------------------------------
+// hard parameter prep (FC)
+// ---------------------------------------------------------------------------
+// TRUTH_TABLES of silogic/functional.py:50-69 as 4-bit codes (bit g = output
+// at address g = (a<<1)|b): code = c0 | (c0+c2)<<1 | (c0+c1)<<2 | (sum)<<3.
+__constant__ uint8_t c_tt16[16] = {0x0, 0x8, 0x4, 0xC, 0x2, 0xA, 0x6, 0xE,
+                                   0x1, 0x9, 0x5, 0xD, 0x3, 0xB, 0x7, 0xF};
+
+__device__ inline int argmax_first(const float* p, int n) {
+  int bi = 0;
+  float bv = p[0];
+  for (int i = 1; i < n; ++i)
+    if (p[i] > bv) { bv = p[i]; bi = i; }
+  return bi;
+}
+
+__global__ void fc_hard_prep_kernel(const int32_t* __restrict__ cand, const float* __restrict__ conn,
+                                    int OUT, int K, int IN, int node, const float* __restrict__ raw,
+                                    uint2* __restrict__ codes) {
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= OUT) return;
+  int idx[2];
+  for (int s = 0; s < 2; ++s) {
+    if (conn) {  // TopK: cand[o, s, argmax conn[o, s, :]] (connectomes.py:129-132)
+      const int64_t base = ((int64_t)o * 2 + s) * K;
+      idx[s] = cand[base + argmax_first(conn + base, K)];
+    } else {     // fixed: idx[o, s]
+      idx[s] = cand[(int64_t)o * 2 + s];
+    }
+    idx[s] = min(max(idx[s], 0), IN - 1);
+  }
+  uint32_t tt = 0;
+  if (node == SLG_NODE_GATE16) {  // nodes.py:100-106
+    tt = c_tt16[argmax_first(raw + (int64_t)o * 16, 16)];
+  } else if (node == SLG_NODE_WALSH) {
+    // nodes.py:152-156: z = ((t0*1 + t1*u0) + t2*u1) + t3*u0*u1, u = 2x-1,
+    // summed left to right in fp32 as torch's CPU sum over the size-4 dim.
+    const float t0 = raw[o * 4 + 0], t1 = raw[o * 4 + 1], t2 = raw[o * 4 + 2], t3 = raw[o * 4 + 3];
+    for (int g = 0; g < 4; ++g) {
+      const float u0 = (g >> 1) ? 1.0f : -1.0f;  // a
+      const float u1 = (g & 1) ? 1.0f : -1.0f;   // b
+      float z = t0;  // products by +-1 are exact, so contraction cannot change z
+      z = z + t1 * u0;
+      z = z + t2 * u1;
+      z = z + t3 * (u0 * u1);
+      if (z > 0.0f) tt |= 1u << g;
+    }
+  } else {  // multilinear arity 2: bit g = logits[a + 2b] > 0 (nodes.py:183-189)
+    for (int g = 0; g < 4; ++g) {
+      const int a = g >> 1, b = g & 1;
+      if (raw[o * 4 + a + 2 * b] > 0.0f) tt |= 1u << g;
+    }
+  }
+  codes[o] = make_uint2((uint32_t)idx[0], (uint32_t)idx[1] | (tt << 28));
+}
+
+// ---------------------------------------------------------------------------
+// one packed FC layer
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) fc_hard_layer_kernel(const uint64_t* __restrict__ xin, int nw,
+                                                            const uint2* __restrict__ codes, int OUT,
+                                                            uint64_t* __restrict__ xout) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)OUT * nw) return;
+  const int o = (int)(i / nw), w = (int)(i % nw);
+  const uint2 c = codes[o];
+  const uint64_t a = xin[(int64_t)c.x * nw + w];
+  const uint64_t b = xin[(int64_t)(c.y & 0x0FFFFFFFu) * nw + w];
+  xout[i] = gate_word<uint64_t>(a, b, c.y >> 28);
+}
+
+// ---------------------------------------------------------------------------
+// depth-fused FC network + GroupSum
+// ---------------------------------------------------------------------------
+constexpr int kMaxLayers = 16;
+struct NetDesc {
+  const uint2* codes[kMaxLayers];
+  int width[kMaxLayers];
+  int n_layers, in0, C, wire_r, maxw;
+};
+
+template <int IN_KIND, typename WT>
+__global__ void __launch_bounds__(1024) fc_hard_net_kernel(const void* __restrict__ xv, int B, int nw_in,
+                                                           NetDesc d, float* __restrict__ logits) {
+  constexpr int SPW = (int)sizeof(WT) * 8;  // samples per tile
+  constexpr int FPL = 64 / SPW;             // features per ballot
+  extern __shared__ __align__(16) unsigned char smem[];
+  WT* cur = reinterpret_cast<WT*>(smem);
+  WT* nxt = cur + d.maxw;
+  int* cnt = reinterpret_cast<int*>(nxt + d.maxw);  // [C][64]
+  const int tile = blockIdx.x;
+  const int b0 = tile * SPW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+
+  for (int i = threadIdx.x; i < d.C * 64; i += blockDim.x) cnt[i] = 0;
+
+  // ---- prologue: this tile's input column into `cur` ----
+  if constexpr (IN_KIND == 2) {
+    const uint64_t* xp = static_cast<const uint64_t*>(xv);
+    for (int i = threadIdx.x; i < d.in0; i += blockDim.x) {
+      if constexpr (SPW == 64) cur[i] = xp[(int64_t)i * nw_in + tile];
+      else cur[i] = (WT)(xp[(int64_t)i * nw_in + (tile >> 1)] >> (32 * (tile & 1)));
+    }
+  } else {
+    // Each lane owns one sample (lane % SPW) and 16 consecutive features; a
+    // ballot per feature packs the wave's samples.
+    const int s = lane % SPW;
+    const int fo = (lane / SPW) * 16;
+    const int b = b0 + s;
+    for (int f0 = wave * 16 * FPL; f0 < d.in0; f0 += nwaves * 16 * FPL) {
+      float v[16];
+      const int fb = f0 + fo;
+      if constexpr (IN_KIND == 0) {
+        const float* row = static_cast<const float*>(xv) + (int64_t)b * d.in0;
+        if (b < B && fb + 16 <= d.in0 && (d.in0 & 3) == 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 t = *reinterpret_cast<const float4*>(row + fb + 4 * q);
+            v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) v[j] = (b < B && fb + j < d.in0) ? row[fb + j] : 0.0f;
+        }
+      } else {
+        const uint8_t* row = static_cast<const uint8_t*>(xv) + (int64_t)b * d.in0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = (b < B && fb + j < d.in0 && row[fb + j] != 0) ? 1.0f : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint64_t m = __ballot(v[j] >= 1.0f);
+        if (lane == 0) {
+          if constexpr (SPW == 64) {
+            if (f0 + j < d.in0) cur[f0 + j] = (WT)m;
+          } else {
+            if (f0 + j < d.in0) cur[f0 + j] = (WT)m;
+            if (f0 + 16 + j < d.in0) cur[f0 + 16 + j] = (WT)(m >> 32);
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- layers, ping-pong between the two LDS buffers ----
+  int cur_w = d.in0;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const uint2* __restrict__ codes = d.codes[l];
+    const int W = d.width[l];
+    const int keep = (d.wire_r > 0 && cur_w == W) ? d.wire_r : 0;
+    for (int o = threadIdx.x; o < W; o += blockDim.x) {
+      WT r;
+      if (o < keep) {
+        r = cur[o];
+      } else {
+        const uint2 c = codes[o];
+        r = gate_word<WT>(cur[c.x], cur[c.y & 0x0FFFFFFFu], c.y >> 28);
+      }
+      nxt[o] = r;
+    }
+    __syncthreads();
+    WT* t = cur; cur = nxt; nxt = t;
+    cur_w = W;
+  }
+
+  // ---- GroupSum: per class, 64-word chunks -> bit transpose -> popcount ----
+  const int G = cur_w / d.C;
+  const int chunks = (G + 63) / 64;
+  for (int task = wave; task < d.C * chunks; task += nwaves) {
+    const int c = task / chunks, j0 = (task % chunks) * 64;
+    uint64_t v = (j0 + lane < G) ? (uint64_t)cur[c * G + j0 + lane] : 0ull;
+    v = transpose64(v, lane);
+    const int pc = __popcll(v);
+    if (pc) atomicAdd(&cnt[c * 64 + lane], pc);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < SPW * d.C; i += blockDim.x) {
+    const int s = i / d.C, c = i % d.C;
+    const int b = b0 + s;
+    if (b < B) logits[(int64_t)b * d.C + c] = (float)cnt[c * 64 + s];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// packed GroupSum (layer-wise path): one workgroup per 64-sample word column
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) groupsum_packed_kernel(const uint64_t* __restrict__ xp, int W,
+                                                              int nw, int B, int C,
+                                                              float* __restrict__ logits) {
+  extern __shared__ int gcnt[];  // [C][64]
+  const int w = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  for (int i = threadIdx.x; i < C * 64; i += blockDim.x) gcnt[i] = 0;
+  __syncthreads();
+  const int G = W / C;
+  const int chunks = (G + 63) / 64;
+  for (int task = wave; task < C * chunks; task += nwaves) {
+    const int c = task / chunks, j0 = (task % chunks) * 64;
+    uint64_t v = (j0 + lane < G) ? xp[(int64_t)(c * G + j0 + lane) * nw + w] : 0ull;
+    v = transpose64(v, lane);
+    const int pc = __popcll(v);
+    if (pc) atomicAdd(&gcnt[c * 64 + lane], pc);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * C; i += blockDim.x) {
+    const int s = i / C, c = i % C;
+    const int b = w * 64 + s;
+    if (b < B) logits[(int64_t)b * C + c] = (float)gcnt[c * 64 + s];
+  }
+}
+
+static int net_spw(int64_t IN0, int n_layers, const int64_t* widths, int C) {
+  if (n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
+  int64_t maxw = IN0;
+  for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
+  const int64_t lds = device_lds_bytes();
+  if (2 * maxw * 8 + (int64_t)C * 256 <= lds) return 64;
+  if (2 * maxw * 4 + (int64_t)C * 256 <= lds) return 32;
+  return 0;
+}
+
+}  // namespace slg
+
+using namespace slg;
+
+extern "C" {
+
+int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, uint64_t* xp,
+                  slg_stream_t stream) {
+  SLG_REQUIRE(x && xp, SLG_E_ARG, "pack_bits: null pointer");
+  SLG_REQUIRE(dtype == 0 || dtype == 1, SLG_E_ARG, "pack_bits: dtype %d", dtype);
+  SLG_REQUIRE(B >= 0 && D > 0 && B < (1LL << 31) && D < (1LL << 31) && B * D < (1LL << 46),
+              SLG_E_SHAPE, "pack_bits: bad sizes");
+  if (B == 0) return 0;
+  const int64_t nw = cdiv(B, 64);
+  const int64_t dtiles = cdiv(D, 64);
+  SLG_REQUIRE(nw * dtiles < (1LL << 31), SLG_E_SHAPE, "pack_bits: too many tiles");
+  dim3 grid((unsigned)(nw * dtiles));
+  if (dtype == 0)
+    hipLaunchKernelGGL(pack_kernel<float>, grid, dim3(256), 0, as_stream(stream), (const float*)x,
+                       (int)B, (int)D, (int)nw, (int)dtiles, xp);
+  else
+    hipLaunchKernelGGL(pack_kernel<uint8_t>, grid, dim3(256), 0, as_stream(stream),
+                       (const uint8_t*)x, (int)B, (int)D, (int)nw, (int)dtiles, xp);
+  SLG_LAUNCH_CHECK("pack_bits");
+  return 0;
+}
+
+int slg_unpack_bits(const uint64_t* xp, int64_t B, int64_t D, uint8_t* out, slg_stream_t stream) {
+  SLG_REQUIRE(xp && out, SLG_E_ARG, "unpack_bits: null pointer");
+  SLG_REQUIRE(B >= 0 && D > 0 && B < (1LL << 31) && D < (1LL << 31), SLG_E_SHAPE,
+              "unpack_bits: bad sizes");
+  if (B == 0) return 0;
+  const int64_t n = B * D;
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, as_stream(stream),
+                     xp, (int)B, (int)D, (int)cdiv(B, 64), out);
+  SLG_LAUNCH_CHECK("unpack_bits");
+  return 0;
+}
+
+int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_t K, int64_t IN,
+                     int32_t node_kind, const float* raw, uint32_t* codes, slg_stream_t stream) {
+  SLG_REQUIRE(cand && raw && codes, SLG_E_ARG, "fc_hard_prep: null pointer");
+  SLG_REQUIRE(OUT > 0 && OUT < (1LL << 31) && IN > 0 && IN <= (1LL << 28) && K >= 1 && K <= 64,
+              SLG_E_SHAPE, "fc_hard_prep: bad sizes");
+  SLG_REQUIRE(node_kind >= 0 && node_kind <= 2, SLG_E_ARG, "fc_hard_prep: node_kind %d", node_kind);
+  SLG_REQUIRE(((uintptr_t)codes % 8) == 0, SLG_E_ARG, "fc_hard_prep: codes alignment");
+  hipLaunchKernelGGL(fc_hard_prep_kernel, dim3((unsigned)cdiv(OUT, 256)), dim3(256), 0,
+                     as_stream(stream), cand, conn, (int)OUT, K, (int)IN, node_kind, raw,
+                     reinterpret_cast<uint2*>(codes));
+  SLG_LAUNCH_CHECK("fc_hard_prep");
+  return 0;
+}
+
+int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw, const uint32_t* codes,
+                      int64_t OUT, uint64_t* xout, slg_stream_t stream) {
+  SLG_REQUIRE(xin && codes && xout, SLG_E_ARG, "fc_hard_layer: null pointer");
+  SLG_REQUIRE(IN > 0 && nw >= 0 && OUT > 0 && OUT * nw < (1LL << 40) && nw < (1LL << 31),
+              SLG_E_SHAPE, "fc_hard_layer: bad sizes");
+  if (nw == 0) return 0;
+  const int64_t n = OUT * nw;
+  hipLaunchKernelGGL(fc_hard_layer_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                     as_stream(stream), xin, (int)nw, reinterpret_cast<const uint2*>(codes),
+                     (int)OUT, xout);
+  SLG_LAUNCH_CHECK("fc_hard_layer");
+  return 0;
+}
+
+int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C) {
+  if (!widths || n_layers < 1 || n_layers > kMaxLayers || C < 1) return 0;
+  if (widths[n_layers - 1] % C != 0) return 0;
+  return net_spw(IN0, n_layers, widths, C);
+}
+
+int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
+                    const int64_t* widths, const uint32_t* const* codes, int32_t C, int64_t wire_r,
+                    float* logits, slg_stream_t stream) {
+  SLG_REQUIRE(x && widths && codes && logits, SLG_E_ARG, "fc_hard_net: null pointer");
+  SLG_REQUIRE(in_kind >= 0 && in_kind <= 2, SLG_E_ARG, "fc_hard_net: in_kind %d", in_kind);
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE, "fc_hard_net: %d layers", n_layers);
+  SLG_REQUIRE(B >= 0 && B < (1LL << 31) && IN0 > 0 && IN0 < (1LL << 28), SLG_E_SHAPE,
+              "fc_hard_net: bad sizes");
+  NetDesc d{};
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(codes[l] && widths[l] > 0 && widths[l] < (1LL << 28), SLG_E_ARG,
+                "fc_hard_net: layer %d", l);
+    d.codes[l] = reinterpret_cast<const uint2*>(codes[l]);
+    d.width[l] = (int)widths[l];
+  }
+  SLG_REQUIRE(C > 0 && widths[n_layers - 1] % C == 0, SLG_E_SHAPE,
+              "fc_hard_net: last width %lld not divisible by %d classes",
+              (long long)widths[n_layers - 1], C);
+  const int spw = net_spw(IN0, n_layers, widths, C);
+  SLG_REQUIRE(spw > 0, SLG_E_UNSUPPORTED, "fc_hard_net: widths do not fit LDS");
+  if (B == 0) return 0;
+  d.n_layers = n_layers; d.in0 = (int)IN0; d.C = C; d.wire_r = (int)std::max<int64_t>(0, wire_r);
+  int64_t maxw = IN0;
+  for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
+  d.maxw = (int)((maxw + 1) & ~1LL);
+  const size_t lds = (size_t)2 * d.maxw * (spw / 8) + (size_t)C * 256;
+  const int64_t tiles = cdiv(B, spw);
+  const int nw_in = (int)cdiv(B, 64);
+  hipStream_t st = as_stream(stream);
+#define SLG_NET_LAUNCH(KIND, WT)                                                              \
+  do {                                                                                        \
+    auto kern = fc_hard_net_kernel<KIND, WT>;                                                 \
+    hipError_t e = hipFuncSetAttribute((const void*)kern,                                     \
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+    if (e != hipSuccess) {                                                                    \
+      set_error("fc_hard_net: LDS %zu: %s", lds, hipGetErrorString(e));                       \
+      return (int)e;                                                                          \
+    }                                                                                         \
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(1024), lds, st, x, (int)B, nw_in, d,  \
+                       logits);                                                               \
+  } while (0)
+  if (spw == 64) {
+    if (in_kind == 0) SLG_NET_LAUNCH(0, uint64_t);
+    else if (in_kind == 1) SLG_NET_LAUNCH(1, uint64_t);
+    else SLG_NET_LAUNCH(2, uint64_t);
+  } else {
+    if (in_kind == 0) SLG_NET_LAUNCH(0, uint32_t);
+    else if (in_kind == 1) SLG_NET_LAUNCH(1, uint32_t);
+    else SLG_NET_LAUNCH(2, uint32_t);
+  }
+#undef SLG_NET_LAUNCH
+  SLG_LAUNCH_CHECK("fc_hard_net");
+  return 0;
+}
+
+int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C, float* logits,
+                        slg_stream_t stream) {
+  SLG_REQUIRE(xp && logits, SLG_E_ARG, "groupsum_packed: null pointer");
+  SLG_REQUIRE(C > 0 && C <= 64 && W > 0 && W % C == 0 && W < (1LL << 31) && B >= 0 &&
+                  B < (1LL << 31),
+              SLG_E_SHAPE, "groupsum_packed: bad sizes");
+  if (B == 0) return 0;
+  const int64_t nw = cdiv(B, 64);
+  hipLaunchKernelGGL(groupsum_packed_kernel, dim3((unsigned)nw), dim3(256), (size_t)C * 256,
+                     as_stream(stream), xp, (int)W, (int)nw, (int)B, C, logits);
+  SLG_LAUNCH_CHECK("groupsum_packed");
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,53 @@
+// Shared helpers of the gfx950 gate-layer library: error reporting, launch
+// checks, device queries and small device utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/silogic_hip.h"
+
+namespace slg {
+
+void set_error(const char* fmt, ...);
+
+// Argument / shape rejection: records the message and returns the code.
+#define SLG_REQUIRE(cond, code, ...)            \
+  do {                                          \
+    if (!(cond)) {                              \
+      ::slg::set_error(__VA_ARGS__);            \
+      return (code);                            \
+    }                                           \
+  } while (0)
+
+// After a launch: report a launch failure as a positive hipError_t.
+#define SLG_LAUNCH_CHECK(what)                                              \
+  do {                                                                      \
+    hipError_t e_ = hipGetLastError();                                      \
+    if (e_ != hipSuccess) {                                                 \
+      ::slg::set_error("%s: launch failed: %s", what, hipGetErrorString(e_)); \
+      return (int)e_;                                                       \
+    }                                                                       \
+  } while (0)
+
+inline hipStream_t as_stream(slg_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Compute units of the current device (cached per device id).
+int device_cus();
+// Max dynamic LDS bytes per workgroup of the current device.
+int device_lds_bytes();
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Workgroup id remapped so that consecutive logical ids share an XCD.
+// The hardware dispatches workgroup i to XCD (i % 8); when the grid is a
+// multiple of 8, logical = (i % 8) * (grid / 8) + i / 8 is a bijection that
+// keeps runs of consecutive logical ids on one XCD (one L2).
+__device__ inline uint32_t xcd_logical_id(uint32_t i, uint32_t grid) {
+  if ((grid & 7u) != 0u) return i;
+  return (i & 7u) * (grid >> 3) + (i >> 3);
+}
+
+}  // namespace slg

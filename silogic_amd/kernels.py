@@ -1,0 +1,57 @@
+"""Drop-in for the reference's ``silogic.kernels`` dispatch module
+(silogic/kernels/__init__.py:21-55): the same function names, argument
+meaning and ``HAS_*`` capability flags, implemented by the HIP library.
+
+* :func:`dense_logic` — silogic/kernels/dense.py:123-125
+* :func:`warp_logic`  — silogic/kernels/warp.py:104-105
+* :func:`tree_conv`   — silogic/kernels/conv.py:399-400 (stride 1, 'same')
+* :func:`tree_conv_topk` — silogic/kernels/conv_topk.py:175-189
+
+The flags are True when ``libsilogic_hip.so`` loads; the hybrid-node kernels
+(``multilinear_logic``, ``conv_hybrid``) are not provided.
+"""
+import torch
+
+from . import _lib, ops
+
+_OK = _lib.available()
+HAS_DENSE = HAS_WARP = HAS_CONV = HAS_CONV_TOPK = _OK
+HAS_MULTILINEAR = HAS_CONV_HYBRID = False
+
+
+def _pack_ab(ca, cb, wa, wb):
+    cand = torch.stack([ca, cb], dim=1)
+    w = torch.stack([wa, wb], dim=1)
+    return cand, w
+
+
+def dense_logic(x, ca, cb, wa, wb, coef):
+    """x[B,IN], ca/cb[OUT,K] int32, wa/wb[OUT,K], coef[OUT,4] -> [B,OUT]."""
+    cand, w = _pack_ab(ca, cb, wa, wb)
+    return ops.fc_soft(x, cand, w, coef, ops.GATE16, 1.0)
+
+
+def warp_logic(x, ca, cb, wa, wb, coef, inv_tau):
+    """As :func:`dense_logic`, then ``sigmoid(z * inv_tau)``."""
+    cand, w = _pack_ab(ca, cb, wa, wb)
+    return ops.fc_soft(x, cand, w, coef, ops.WALSH, float(inv_tau))
+
+
+def _check_same(stride, pad, H, W, Ho, Wo):
+    if stride != 1 or Ho != H or Wo != W:
+        raise NotImplementedError("tree_conv on MI355X: stride 1, 'same' padding only")
+
+
+def tree_conv(x, coef, cm, ch, cw, depth, stride, pad, Ho, Wo):
+    """Fixed-wiring gate tree conv: coef [N,2^d-1,4], cm/ch/cw [N,2^d]."""
+    _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
+    N, leaves = cm.shape
+    w = torch.ones(N, leaves, 1, device=x.device)
+    return ops.conv_soft(x, coef, w, cm.unsqueeze(-1), ch.unsqueeze(-1), cw.unsqueeze(-1),
+                         ops.GATE16, depth, 2, 1, pad, False)
+
+
+def tree_conv_topk(x, coef, w, cm, ch, cw, depth, K, stride, pad, Ho, Wo):
+    """Top-K gate tree conv: w/cm/ch/cw [N,2^d,K]."""
+    _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
+    return ops.conv_soft(x, coef, w, cm, ch, cw, ops.GATE16, depth, 2, K, pad, False)

@@ -1,0 +1,345 @@
+"""Logic layers (mirror of silogic/layers.py): ``LogicLayer`` and its presets,
+``ConvLogicTree`` (alias ``ConvLogicLayer``) and ``OrPool``.
+
+Construction, parameter names and ``state_dict`` layout follow the reference
+(silogic/layers.py:51-75, 271-373) so checkpoints and seeds carry over.
+Compute runs on the HIP kernels of ``libsilogic_hip.so``:
+
+* ``LogicLayer.forward`` -> Top-K gather + node (``slg_fc_soft_fwd``), with
+  ``softmax(conn)`` and the node coefficients prepared by
+  ``slg_fc_soft_prep`` when no gradient is needed, or by differentiable torch
+  ops (the reference's ``_fused`` split, layers.py:111-123) when it is.
+* ``LogicLayer.forward_hard`` -> pack, one packed layer, unpack.
+* ``ConvLogicTree.forward`` -> ``slg_conv_soft_fwd``; networks call
+  ``forward_pooled``, which fuses the following ``OrPool``.
+
+There is no CPU path: CPU inputs raise.
+"""
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .connectomes import build_connectome, FixedConnectome
+from .functional import BASIS_COEFFS, TRUTH_TABLES, GATE_A, gate_probs
+from .nodes import build_node, _NODE_ALIASES
+
+
+def _needs_grad(module, *xs):
+    if not torch.is_grad_enabled():
+        return False
+    if any(x is not None and x.requires_grad for x in xs):
+        return True
+    return any(p.requires_grad for p in module.parameters())
+
+
+class LogicLayer(nn.Module):
+    """A layer of logic nodes: connectome (input wiring) + node (gate
+    parameterization). Arguments as silogic.layers.LogicLayer; the HIP path
+    covers arity-2 nodes (gate16, walsh, multilinear) with top-k / block-top-k
+    / fixed wiring. ``use_triton`` is accepted for API compatibility and
+    ignored (the HIP kernels always run)."""
+
+    def __init__(self, in_dim, out_dim, node="gate16", connectome="topk", arity=2,
+                 k=8, gate_eval="basis", residual_p=0.0, seed=None,
+                 window=0, tau=1.0, degree=None, gate_select="softmax",
+                 gumbel_tau=1.0, use_triton=True):
+        super().__init__()
+        self._node_name = _NODE_ALIASES.get(str(node).lower(), node)
+        if self._node_name == "gate16":
+            arity = 2
+        self.in_dim = in_dim
+        self.out_dim = out_dim
+        self.arity = arity
+        self.k = k
+        self.gate_eval = gate_eval
+        self.use_triton = use_triton
+        self.connectome = connectome
+        self._conn = build_connectome(connectome, in_dim, out_dim, arity, k, seed, window)
+        if gate_select == "hard" and hasattr(self._conn, "ste"):
+            self._conn.ste = True
+        self.node = build_node(node, out_dim, arity, gate_eval=gate_eval, tau=tau,
+                               degree=degree, gate_select=gate_select, gumbel_tau=gumbel_tau)
+        if residual_p > 0:
+            self.node.residual_init(residual_p)
+
+    # -- compatibility accessors ---------------------------------------------
+    @property
+    def gate_logits(self):
+        return self.node.gate_logits
+
+    @property
+    def theta(self):
+        return self.node.theta
+
+    @property
+    def conn_a(self):
+        return self._conn.conn[:, 0]
+
+    @property
+    def conn_b(self):
+        return self._conn.conn[:, 1]
+
+    # -- HIP dispatch ----------------------------------------------------------
+    def _check_supported(self):
+        if self.arity != 2:
+            raise NotImplementedError(
+                f"LogicLayer arity {self.arity}: the MI355X FC kernels take arity-2 nodes")
+
+    def _inv_tau(self):
+        return self.node.inv_tau if self._node_name == "walsh" else 1.0
+
+    def soft_params(self, grad):
+        """``(cand_i32, w, node_param)`` for the soft kernel."""
+        conn = self._conn
+        cand = conn.candidates_i32()
+        plain = self.node.plain_softmax() and not getattr(conn, "ste", False)
+        if grad or not plain:
+            if self._node_name == "walsh" and not self.node.plain_softmax():
+                raise NotImplementedError("walsh Gumbel smoothing in training is not on the "
+                                          "MI355X path")
+            return cand, conn.weights(), self.node.kernel_param()
+        raw_conn = None if isinstance(conn, FixedConnectome) else conn.conn
+        w, npar = ops.fc_soft_prep(raw_conn, self.node.raw(), self.node.kind, self.out_dim,
+                                   conn.k)
+        return cand, w, npar
+
+    def forward(self, x):
+        self._check_supported()
+        ops.require_gpu(x)
+        cand, w, npar = self.soft_params(_needs_grad(self, x))
+        return ops.fc_soft(x, cand, w, npar, self.node.kind, self._inv_tau())
+
+    def hard_codes(self):
+        """Per-output ``(a, b | tt << 28)`` codes [out, 2] int32 (HIP prep)."""
+        self._check_supported()
+        cand, conn = self._conn.hard_inputs()
+        return ops.fc_hard_codes(cand, conn, self.node.raw(), self.node.kind, self.in_dim)
+
+    @torch.no_grad()
+    def forward_hard(self, x):
+        ops.require_gpu(x)
+        B = x.shape[0]
+        xp = ops.pack_bits(x)
+        return ops.unpack_bits(ops.fc_hard_layer(xp, self.hard_codes()), B)
+
+
+class WARPLayer(LogicLayer):
+    """2-input Walsh (WARP) node with Top-K connectivity (preset)."""
+
+    def __init__(self, in_dim, out_dim, k=8, tau=1.0, residual_p=0.0, seed=None,
+                 gate_select="softmax"):
+        super().__init__(in_dim, out_dim, node="walsh", connectome="topk", arity=2,
+                         k=k, tau=tau, residual_p=residual_p, seed=seed,
+                         gate_select=gate_select)
+
+    def _z(self, a, b):
+        return self.node._z(a, b)
+
+    def _coef(self):
+        return self.node.coef()
+
+
+class ConvLogicTree(nn.Module):
+    """Logic-gate-tree convolution (arguments as silogic.layers.ConvLogicTree).
+
+    The HIP path covers gate16 trees of depth 1-4 and depth-1 multilinear LUT
+    nodes of arity 2-6, stride 1 with ``padding = kernel // 2``."""
+
+    def __init__(self, in_channels, out_channels, kernel=3, tree_depth=None,
+                 stride=1, padding=1, connect="topk", k=4, n_chan=2,
+                 residual_init=True, seed=0, node="gate16",
+                 arity=4, tau=1.0, degree=None, gate_select="softmax",
+                 gumbel_tau=1.0, use_triton=True):
+        super().__init__()
+        self.node_name = _NODE_ALIASES.get(str(node).lower(), node)
+        self.gate_select = gate_select
+        self.gumbel_tau = gumbel_tau
+        self.node_arity = 2 if self.node_name in ("gate16", "walsh") else arity
+        if tree_depth is None:
+            tree_depth = 2 if self.node_arity == 2 else 1
+        self.cin = in_channels
+        self.n = out_channels
+        self.kh = self.kw = kernel
+        self.d = tree_depth
+        self.leaves = self.node_arity ** tree_depth
+        self.stride = stride
+        self.padding = padding
+        self.connect = connect
+        self.k = k
+        self.tau = tau
+        self.use_triton = use_triton
+        if self.node_name not in ("gate16", "multilinear"):
+            raise NotImplementedError(f"conv node {node!r} is not on the MI355X path")
+        if self.node_name == "multilinear" and (tree_depth != 1 or not 2 <= arity <= 6):
+            raise NotImplementedError("multilinear conv trees: depth 1, arity 2..6")
+        if stride != 1 or 2 * padding + 1 != kernel:
+            raise NotImplementedError("conv trees: stride 1 with padding = kernel // 2")
+        gen = torch.Generator().manual_seed(seed)
+
+        # Each tree observes n_chan random input channels; its leaf candidates
+        # are those channels' receptive-field positions (flat c*k*k + dy*k + dx).
+        pool_sz = n_chan * kernel * kernel
+        cand_pool = []
+        for _ in range(out_channels):
+            chans = torch.randperm(in_channels, generator=gen)[:n_chan]
+            idxs = []
+            for c in chans:
+                base = int(c) * kernel * kernel
+                idxs.extend(range(base, base + kernel * kernel))
+            cand_pool.append(torch.tensor(idxs))
+        cand_pool = torch.stack(cand_pool)
+        kk2 = kernel * kernel
+        if connect == "fixed":
+            sel = torch.stack([
+                cand_pool[i][torch.randint(0, pool_sz, (self.leaves,), generator=gen)]
+                for i in range(out_channels)])
+            self.register_buffer("leaf_idx", sel)
+            self.register_buffer("cm_idx", (sel // kk2).to(torch.int32))
+            rem = sel % kk2
+            self.register_buffer("ch_idx", (rem // kernel).to(torch.int32))
+            self.register_buffer("cw_idx", (rem % kernel).to(torch.int32))
+        else:
+            kk = min(k, pool_sz)
+            self.k = kk
+            cand = torch.stack([
+                torch.stack([cand_pool[i][torch.randperm(pool_sz, generator=gen)[:kk]]
+                             for _ in range(self.leaves)])
+                for i in range(out_channels)])
+            self.register_buffer("leaf_cand", cand)
+            self.conn = nn.Parameter(torch.randn(out_channels, self.leaves, kk))
+            self.register_buffer("lc_cm", (cand // kk2).to(torch.int32))
+            rem = cand % kk2
+            self.register_buffer("lc_ch", (rem // kernel).to(torch.int32))
+            self.register_buffer("lc_cw", (rem % kernel).to(torch.int32))
+
+        if self.node_name == "gate16":
+            self.gate_logits = nn.ParameterList()
+            for i in range(tree_depth):
+                nodes = 2 ** (tree_depth - 1 - i)
+                w = torch.zeros(out_channels, nodes, 16)
+                if residual_init:
+                    w[:, :, GATE_A] = 5.0
+                else:
+                    w.normal_(0, 0.1)
+                self.gate_logits.append(nn.Parameter(w))
+            self.register_buffer("basis", BASIS_COEFFS.clone())
+            self.register_buffer("truth", TRUTH_TABLES.clone())
+        else:
+            self.tree_nodes = nn.ModuleList()
+            for i in range(tree_depth):
+                m = self.node_arity ** (tree_depth - 1 - i)
+                nd = build_node(self.node_name, out_channels * m, arity=self.node_arity,
+                                tau=tau, degree=degree, gate_select=gate_select,
+                                gumbel_tau=gumbel_tau)
+                if residual_init:
+                    nd.residual_init(0.9)
+                self.tree_nodes.append(nd)
+
+    # -- parameters --------------------------------------------------------------
+    @property
+    def gates_per_output(self):
+        k = self.node_arity
+        return (k ** self.d - 1) // (k - 1)
+
+    def _hw_out(self, H, W):
+        Ho = (H + 2 * self.padding - self.kh) // self.stride + 1
+        Wo = (W + 2 * self.padding - self.kw) // self.stride + 1
+        return Ho, Wo
+
+    def _taps(self):
+        if self.connect == "fixed":
+            return (self.cm_idx.unsqueeze(-1), self.ch_idx.unsqueeze(-1),
+                    self.cw_idx.unsqueeze(-1))
+        return self.lc_cm, self.lc_ch, self.lc_cw
+
+    def _kind(self):
+        return ops.GATE16 if self.node_name == "gate16" else ops.MULTILINEAR2
+
+    def _raw(self):
+        if self.node_name == "gate16":
+            return torch.cat([g for g in self.gate_logits], dim=1)   # [n, nodes, 16]
+        return self.tree_nodes[0].logits                             # [n, 2^arity]
+
+    def _topk_w(self):
+        w = F.softmax(self.conn, dim=2)
+        if self.gate_select == "hard":
+            hard = F.one_hot(self.conn.argmax(dim=2), w.shape[-1]).to(w.dtype)
+            w = hard + w - w.detach()
+        return w
+
+    def _basis_coef(self):
+        gl = torch.cat([g for g in self.gate_logits], dim=1)
+        p = gate_probs(gl, self.training, dim=2, gate_select=self.gate_select,
+                       gumbel_tau=self.gumbel_tau)
+        return p @ self.basis
+
+    def soft_params(self, grad):
+        K = 1 if self.connect == "fixed" else self.k
+        plain = self.gate_select == "softmax" or (
+            not self.training and self.gate_select != "hard")
+        if grad or not plain:
+            w = (torch.ones(self.n, self.leaves, 1, device=self.cm_idx.device)
+                 if self.connect == "fixed" else self._topk_w())
+            npar = (self._basis_coef() if self.node_name == "gate16"
+                    else torch.sigmoid(self.tree_nodes[0].logits))
+            return w, npar
+        conn = None if self.connect == "fixed" else self.conn
+        return ops.conv_soft_prep(conn, self._raw(), self._kind(), self.n, self.leaves, K,
+                                  self.d, self.node_arity)
+
+    def _soft(self, x, pool):
+        ops.require_gpu(x)
+        w, npar = self.soft_params(_needs_grad(self, x))
+        cm, ch, cw = self._taps()
+        K = cm.shape[-1]
+        return ops.conv_soft(x, npar, w, cm, ch, cw, self._kind(), self.d, self.node_arity, K,
+                             self.padding, pool)
+
+    def forward(self, x):
+        return self._soft(x, pool=False)
+
+    def forward_pooled(self, x):
+        """``OrPool(2)(self(x))`` in one kernel (only the pooled map is written)."""
+        return self._soft(x, pool=True)
+
+    def hard_params(self):
+        cm, ch, cw = self._taps()
+        conn = None if self.connect == "fixed" else self.conn
+        return ops.conv_hard_prep(cm, ch, cw, conn, self._raw(), self._kind(), self.d,
+                                  self.node_arity)
+
+    def packed_forward(self, xp, chw, pool):
+        """Packed ``[C,H,W,nw]`` -> ``[n,Ho,Wo,nw]`` (2x2 OR-pooled if ``pool``)."""
+        leaf, tt = self.hard_params()
+        return ops.conv_hard(xp, chw, leaf, tt, self._kind(), self.d, self.node_arity,
+                             self.kh, self.padding, pool)
+
+    @torch.no_grad()
+    def forward_hard(self, x):
+        ops.require_gpu(x)
+        B, C, H, W = x.shape
+        xp = ops.pack_bits(x.reshape(B, -1))
+        yp = self.packed_forward(xp, (C, H, W), pool=False)
+        Ho, Wo = self._hw_out(H, W)
+        return ops.unpack_bits(yp.view(-1, yp.shape[-1]), B).view(B, self.n, Ho, Wo)
+
+
+ConvLogicLayer = ConvLogicTree
+
+
+class OrPool(nn.Module):
+    """Logical OR pooling = spatial 2x2 max-pool (floor)."""
+
+    def __init__(self, size=2):
+        super().__init__()
+        if size != 2:
+            raise NotImplementedError("OrPool: size 2 only on the MI355X path")
+        self.size = size
+
+    def forward(self, x):
+        return ops.orpool(x)
+
+    @torch.no_grad()
+    def forward_hard(self, x):
+        return ops.orpool(x.to(torch.uint8))

@@ -1,0 +1,200 @@
+"""Networks (mirror of silogic/models.py): ``LogicNet`` (+ ``WARPNet``,
+``LUTkNet``, ``LUTNodeNet`` presets) and ``LogicConvNet`` / ``LogicTreeNet``.
+
+Construction and ``state_dict`` keys follow the reference (per-layer seeds
+``seed*seed_mult+i``, conv block seeds ``seed*17+i``, head seeds ``seed*31+j``;
+silogic/models.py:59-86, 208-246).
+
+``forward`` runs layer by layer on the HIP soft kernels (conv blocks with
+their OrPool fused). ``forward_hard`` runs the network as one bit-packed
+circuit: 64 samples per word, the FC stack depth-fused in LDS with the
+GroupSum popcount at the end (``slg_fc_hard_net``), conv blocks as packed
+tree + OR-pool kernels. It returns the same raw integer counts as the
+reference's ``GroupSum.forward_hard`` (heads.py:41-45).
+"""
+import torch
+import torch.nn as nn
+
+from . import ops
+from .heads import build_decoder
+from .layers import LogicLayer, ConvLogicTree, OrPool
+
+
+def _per_layer(v, i):
+    return v[i] if isinstance(v, (list, tuple)) else v
+
+
+def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
+    """Run arity-2 FC layers as a packed circuit and return class counts."""
+    codes = [layer.hard_codes() for layer in layers]
+    widths = [c.shape[0] for c in codes]
+    if ops.fc_hard_net_supported(in_dim, widths, C):
+        return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
+    xp = x if in_kind == 2 else ops.pack_bits(x)
+    for c in codes:
+        yp = ops.fc_hard_layer(xp, c)
+        if wire_r and yp.shape[0] == xp.shape[0]:
+            yp[:wire_r] = xp[:wire_r]
+        xp = yp
+    return ops.groupsum_packed(xp, B, C)
+
+
+class LogicNet(nn.Module):
+    """Stack of logic layers followed by a GroupSum head (arguments as
+    silogic.models.LogicNet)."""
+
+    def __init__(self, in_dim, width, depth, num_classes=10, node="gate16",
+                 connectome="topk", arity=2, k=8, tau=1.0, gate_eval="basis",
+                 node_tau=1.0, residual_p=0.0, seed=0,
+                 wire_residual=0.0, decoder="groupsum", degree=None, seed_mult=1000,
+                 gate_select="softmax", gumbel_tau=1.0, decoder_ste=True,
+                 use_triton=True):
+        super().__init__()
+        layers = []
+        d_in = in_dim
+        for i in range(depth):
+            layers.append(LogicLayer(
+                d_in, width, node=_per_layer(node, i), connectome=connectome,
+                arity=arity, k=k, gate_eval=gate_eval, residual_p=residual_p,
+                degree=degree, tau=node_tau,
+                gate_select=_per_layer(gate_select, i), gumbel_tau=gumbel_tau,
+                use_triton=use_triton,
+                seed=None if seed is None else seed * seed_mult + i))
+            d_in = width
+        self.layers = nn.ModuleList(layers)
+        self.head = build_decoder(decoder, width, num_classes, tau, feature_ste=decoder_ste)
+        self.width = width
+        self.depth = depth
+        self.node = node
+        self.connectome = connectome
+        self.k = k
+        self.decoder_kind = decoder
+        self.wire_r = int(width * wire_residual)
+
+    def _run(self, x):
+        for layer in self.layers:
+            y = layer(x)
+            if self.wire_r and x.shape[1] == y.shape[1]:
+                y = torch.cat([x[:, :self.wire_r], y[:, self.wire_r:]], dim=1)
+            x = y
+        return x
+
+    def forward(self, x):
+        ops.require_gpu(x)
+        return self.head(self._run(x))
+
+    @torch.no_grad()
+    def forward_hard(self, x):
+        ops.require_gpu(x)
+        x, kind = ops._in_kind(x)
+        return _hard_fc_stack(self.layers, x, kind, x.shape[0], x.shape[1],
+                              self.head.num_classes, self.wire_r)
+
+    def num_gates(self):
+        return self.width * self.depth
+
+
+class WARPNet(LogicNet):
+    """Stack of 2-input Walsh (WARP) layers + GroupSum head (tau 20)."""
+
+    def __init__(self, in_dim, width, depth, num_classes=10, k=8, tau=1.0,
+                 residual_p=0.0, seed=0, gate_select="softmax"):
+        super().__init__(in_dim, width, depth, num_classes=num_classes, node="walsh",
+                         arity=2, k=k, node_tau=tau, tau=20.0, residual_p=residual_p,
+                         seed=seed, gate_select=gate_select)
+
+
+class LogicConvNet(nn.Module):
+    """Convolutional logic-gate-tree network with a logic head (arguments as
+    silogic.models.LogicConvNet)."""
+
+    def __init__(self, in_channels, in_hw, channels, head_width=None,
+                 num_classes=10, tree_depth=None, kernel=3, connect="topk",
+                 k=4, head_connect="topk", head_k=8, head_depth=2,
+                 n_chan=2, residual_init=True, tau=100.0, seed=0,
+                 wire_residual=0.0, head_widths=None,
+                 decoder="groupsum", node="gate16", arity=2, node_tau=1.0,
+                 degree=None, gate_select="softmax", gumbel_tau=1.0,
+                 decoder_ste=True, use_triton=True):
+        super().__init__()
+        self.blocks = nn.ModuleList()
+        c = in_channels
+        for i, n in enumerate(channels):
+            self.blocks.append(ConvLogicTree(
+                c, n, kernel=kernel, tree_depth=tree_depth, stride=1,
+                padding=kernel // 2, connect=connect, k=k, n_chan=n_chan,
+                residual_init=residual_init, seed=seed * 17 + i,
+                node=node, arity=arity, tau=node_tau, degree=degree,
+                gate_select=gate_select, gumbel_tau=gumbel_tau, use_triton=use_triton))
+            self.blocks.append(OrPool(2))
+            c = n
+            in_hw = in_hw // 2
+        self.feat_dim = c * in_hw * in_hw
+        if head_widths is None:
+            head_widths = [head_width] * head_depth
+        layers = []
+        d_in = self.feat_dim
+        for j, w in enumerate(head_widths):
+            layers.append(LogicLayer(d_in, w, connectome=head_connect, k=head_k, node=node,
+                                     gate_select=gate_select, use_triton=use_triton,
+                                     seed=seed * 31 + j))
+            d_in = w
+        self.head_layers = nn.ModuleList(layers)
+        self.head = build_decoder(decoder, head_widths[-1], num_classes, tau,
+                                  feature_ste=decoder_ste)
+        self.decoder_kind = decoder
+        self._head_widths = head_widths
+        self.wire_residual = wire_residual
+
+    def _convs(self):
+        return [self.blocks[i] for i in range(0, len(self.blocks), 2)]
+
+    def _apply_blocks(self, x):
+        for conv in self._convs():
+            if self.wire_residual > 0:
+                x_in = x
+                y = conv(x)
+                r = min(int(conv.n * self.wire_residual), x_in.shape[1])
+                if r > 0:
+                    y = torch.cat([x_in[:, :r], y[:, r:]], dim=1)
+                x = ops.orpool(y)
+            else:
+                x = conv.forward_pooled(x)
+        return x
+
+    def forward(self, x):
+        ops.require_gpu(x)
+        x = self._apply_blocks(x).flatten(1)
+        for layer in self.head_layers:
+            x = layer(x)
+        return self.head(x)
+
+    @torch.no_grad()
+    def forward_hard(self, x):
+        ops.require_gpu(x)
+        if self.wire_residual > 0:
+            raise NotImplementedError("wire_residual conv nets are not on the packed MI355X path")
+        B, C, H, W = x.shape
+        xp = ops.pack_bits(x.reshape(B, -1))                  # [C*H*W, nw] = [C,H,W,nw]
+        for conv in self._convs():
+            xp = conv.packed_forward(xp, (C, H, W), pool=True)
+            Ho, Wo = conv._hw_out(H, W)
+            C, H, W = conv.n, Ho // 2, Wo // 2
+        xp = xp.view(-1, xp.shape[-1])                        # flatten (n, h, w)
+        return _hard_fc_stack(self.head_layers, xp, 2, B, xp.shape[0],
+                              self.head.num_classes, 0)
+
+    def gate_count(self, in_hw):
+        total = 0
+        hw = in_hw
+        for blk in self.blocks:
+            if isinstance(blk, ConvLogicTree):
+                total += blk.n * hw * hw * blk.gates_per_output
+            elif isinstance(blk, OrPool):
+                hw = hw // 2
+        total += sum(self._head_widths)
+        return total
+
+
+class LogicTreeNet(LogicConvNet):
+    """Convolutional logic-gate-tree network preset (Top-K wiring)."""

@@ -1,0 +1,415 @@
+"""Torch-level wrappers of the HIP entry points.
+
+Every function here takes CUDA (HIP) tensors, allocates its outputs with
+torch, and launches the kernels of ``libsilogic_hip.so`` on torch's current
+stream. Nothing here computes on the CPU: a CPU tensor or a missing library
+raises.
+
+Autograd: the soft ops are ``torch.autograd.Function`` s whose forward is
+the HIP kernel. Their backward recomputes the op with differentiable torch
+GPU ops and backpropagates through that (a composite backward, the analogue
+of the reference's backward kernels in silogic/kernels/*.py, which are not
+part of this build's hot path).
+"""
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+GATE16, WALSH, MULTILINEAR2 = 0, 1, 2
+NODE_KINDS = {"gate16": GATE16, "walsh": WALSH, "multilinear": MULTILINEAR2}
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "silogic_amd computes on the GPU only (HIP kernels, no CPU fallback): "
+                "move the module and its inputs to a ROCm device with .cuda()")
+    _lib.lib()
+
+
+def _c(t, dtype=None):
+    if t is None:
+        return None
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def _as_f32(x):
+    if x.dtype != torch.float32:
+        x = x.float()
+    return x.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# FC soft
+# ---------------------------------------------------------------------------
+def fc_soft_prep(conn, raw, node_kind, out_dim, K):
+    """HIP prep: softmax(conn) -> w [OUT,2,K]; node param [OUT,4]."""
+    require_gpu(raw)
+    w = torch.empty((out_dim, 2, K), device=raw.device, dtype=torch.float32)
+    npar = torch.empty((out_dim, 4), device=raw.device, dtype=torch.float32)
+    conn = _c(conn, torch.float32)
+    raw = _c(raw, torch.float32)
+    _lib.call("slg_fc_soft_prep", _p(conn), out_dim, K, node_kind, _p(raw), _p(w), _p(npar),
+              _stream(raw))
+    return w, npar
+
+
+def _fc_soft_launch(x, cand, w, npar, node_kind, inv_tau, tile=0, threads=0):
+    B, IN = x.shape
+    OUT, two, K = cand.shape
+    if two != 2 or w.shape != cand.shape or npar.shape != (OUT, 4):
+        raise ValueError(f"fc_soft: cand {tuple(cand.shape)}, w {tuple(w.shape)}, "
+                         f"node_param {tuple(npar.shape)} are inconsistent")
+    y = torch.empty((B, OUT), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_soft_fwd", _p(x), B, IN, OUT, K, _p(cand), _p(w), node_kind, _p(npar),
+              float(inv_tau), _p(y), int(tile), int(threads), _stream(x))
+    return y
+
+
+def fc_soft_torch(x, cand, w, npar, node_kind, inv_tau):
+    """Differentiable torch expression of the FC soft op (backward only)."""
+    g = x[:, cand.long()]                        # [B, OUT, 2, K]
+    ops = (g * w.unsqueeze(0)).sum(-1)           # [B, OUT, 2]
+    a, b = ops[..., 0], ops[..., 1]
+    c = npar
+    if node_kind == MULTILINEAR2:
+        ua, ub = 1 - a, 1 - b
+        return (ua * ub) * c[:, 0] + (a * ub) * c[:, 1] + (ua * b) * c[:, 2] + (a * b) * c[:, 3]
+    z = c[:, 0] + c[:, 1] * a + c[:, 2] * b + c[:, 3] * (a * b)
+    return torch.sigmoid(z * inv_tau) if node_kind == WALSH else z
+
+
+class FCSoftFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, cand, w, npar, node_kind, inv_tau):
+        x = _as_f32(x)
+        cand, w, npar = _c(cand, torch.int32), _c(w, torch.float32), _c(npar, torch.float32)
+        ctx.save_for_backward(x, cand, w, npar)
+        ctx.meta = (node_kind, inv_tau)
+        return _fc_soft_launch(x, cand, w, npar, node_kind, inv_tau)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, cand, w, npar = ctx.saved_tensors
+        node_kind, inv_tau = ctx.meta
+        need = ctx.needs_input_grad
+        with torch.enable_grad():
+            xs = x.detach().requires_grad_(need[0])
+            ws = w.detach().requires_grad_(need[2])
+            ns = npar.detach().requires_grad_(need[3])
+            y = fc_soft_torch(xs, cand, ws, ns, node_kind, inv_tau)
+            inputs = [t for t, n in ((xs, need[0]), (ws, need[2]), (ns, need[3])) if n]
+            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
+        gx = grads.pop(0) if need[0] else None
+        gw = grads.pop(0) if need[2] else None
+        gn = grads.pop(0) if need[3] else None
+        return gx, None, gw, gn, None, None
+
+
+def fc_soft(x, cand, w, npar, node_kind, inv_tau=1.0):
+    """``[B,IN] -> [B,OUT]`` soft FC layer (autograd-aware)."""
+    require_gpu(x, cand, w, npar)
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or npar.requires_grad):
+        return FCSoftFn.apply(x, cand, w, npar, node_kind, inv_tau)
+    return _fc_soft_launch(_as_f32(x), _c(cand, torch.int32), _c(w, torch.float32),
+                           _c(npar, torch.float32), node_kind, inv_tau)
+
+
+# ---------------------------------------------------------------------------
+# GroupSum / OrPool
+# ---------------------------------------------------------------------------
+class GroupSumSoftFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, C, tau, ste):
+        x = _as_f32(x)
+        B, W = x.shape
+        out = torch.empty((B, C), device=x.device, dtype=torch.float32)
+        _lib.call("slg_groupsum_soft", _p(x), B, W, C, float(tau), int(bool(ste)), _p(out),
+                  _stream(x))
+        ctx.meta = (W, C, tau)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        # both the plain sum and the straight-through (x>0.5) + x - x.detach()
+        # have d logit / d x = 1/tau on the class block (silogic/heads.py:34-39)
+        W, C, tau = ctx.meta
+        gx = (g / tau).unsqueeze(2).expand(g.shape[0], C, W // C).reshape(g.shape[0], W)
+        return gx, None, None, None
+
+
+def groupsum_soft(x, C, tau, ste):
+    require_gpu(x)
+    return GroupSumSoftFn.apply(x, C, tau, ste)
+
+
+def groupsum_hard(x, C):
+    require_gpu(x)
+    if x.dtype == torch.bool:
+        x = x.to(torch.uint8)
+    dtype = 1 if x.dtype == torch.uint8 else 0
+    x = x.contiguous() if dtype == 1 else _as_f32(x)
+    B, W = x.shape
+    out = torch.empty((B, C), device=x.device, dtype=torch.float32)
+    _lib.call("slg_groupsum_hard", _p(x), dtype, B, W, C, _p(out), _stream(x))
+    return out
+
+
+class OrPoolFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        out = _orpool_launch(x)
+        ctx.save_for_backward(x)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (x,) = ctx.saved_tensors
+        with torch.enable_grad():
+            xs = x.detach().requires_grad_(True)
+            y = F.max_pool2d(xs, 2, 2)
+            (gx,) = torch.autograd.grad(y, [xs], g)
+        return gx
+
+
+def _orpool_launch(x):
+    dtype = 1 if x.dtype == torch.uint8 else 0
+    x = x.contiguous() if dtype == 1 else _as_f32(x)
+    B, Cc, H, W = x.shape
+    out = torch.empty((B, Cc, H // 2, W // 2), device=x.device, dtype=x.dtype)
+    _lib.call("slg_orpool", _p(x), dtype, B, Cc, H, W, _p(out), _stream(x))
+    return out
+
+
+def orpool(x):
+    require_gpu(x)
+    if x.dtype == torch.bool:
+        x = x.to(torch.uint8)
+    if torch.is_grad_enabled() and x.requires_grad:
+        return OrPoolFn.apply(x)
+    return _orpool_launch(x)
+
+
+# ---------------------------------------------------------------------------
+# hard (bit-packed)
+# ---------------------------------------------------------------------------
+def n_words(B):
+    return (B + 63) >> 6
+
+
+def _in_kind(x):
+    if x.dtype == torch.bool:
+        x = x.to(torch.uint8)
+    if x.dtype == torch.uint8:
+        return x.contiguous(), 1
+    return _as_f32(x), 0
+
+
+def pack_bits(x):
+    """``[B, D]`` {0,1} -> packed ``[D, ceil(B/64)]`` (int64 storage of uint64)."""
+    require_gpu(x)
+    x, kind = _in_kind(x.reshape(x.shape[0], -1))
+    B, D = x.shape
+    xp = torch.empty((D, n_words(B)), device=x.device, dtype=torch.int64)
+    _lib.call("slg_pack_bits", _p(x), kind, B, D, _p(xp), _stream(x))
+    return xp
+
+
+def unpack_bits(xp, B):
+    require_gpu(xp)
+    D = xp.shape[0]
+    out = torch.empty((B, D), device=xp.device, dtype=torch.uint8)
+    _lib.call("slg_unpack_bits", _p(xp), B, D, _p(out), _stream(xp))
+    return out
+
+
+def fc_hard_codes(cand, conn, raw, node_kind, in_dim):
+    """Per-output packed codes ``[OUT, 2]`` int32 (a, b | tt<<28).
+
+    ``cand`` [OUT,2,K] int32 with ``conn`` [OUT,2,K], or ``cand`` = idx
+    [OUT,2] int32 with ``conn`` None (fixed wiring)."""
+    require_gpu(cand, raw)
+    cand = _c(cand, torch.int32)
+    OUT = cand.shape[0]
+    K = cand.shape[2] if cand.dim() == 3 else 1
+    codes = torch.empty((OUT, 2), device=cand.device, dtype=torch.int32)
+    _lib.call("slg_fc_hard_prep", _p(cand), _p(_c(conn, torch.float32)), OUT, K, in_dim,
+              node_kind, _p(_c(raw, torch.float32)), _p(codes), _stream(cand))
+    return codes
+
+
+def fc_hard_layer(xp, codes):
+    require_gpu(xp, codes)
+    IN, nw = xp.shape
+    OUT = codes.shape[0]
+    if codes.shape != (OUT, 2) or codes.dtype != torch.int32:
+        raise ValueError("fc_hard_layer: codes must be [OUT, 2] int32 from fc_hard_codes")
+    out = torch.empty((OUT, nw), device=xp.device, dtype=torch.int64)
+    _lib.call("slg_fc_hard_layer", _p(xp), IN, nw, _p(codes), OUT, _p(out), _stream(xp))
+    return out
+
+
+def fc_hard_net_supported(in_dim, widths, C):
+    arr = (ctypes.c_int64 * len(widths))(*widths)
+    return _lib.lib().slg_fc_hard_net_supported(in_dim, len(widths), arr, C)
+
+
+def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
+    """Depth-fused packed FC network + GroupSum -> logits ``[B, C]``."""
+    require_gpu(x, *codes)
+    widths = [c.shape[0] for c in codes]
+    w_arr = (ctypes.c_int64 * len(widths))(*widths)
+    c_arr = (ctypes.c_void_p * len(codes))(*[c.data_ptr() for c in codes])
+    out = torch.empty((B, C), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_hard_net", _p(x), in_kind, B, in_dim, len(codes), w_arr, c_arr, C,
+              int(wire_r), _p(out), _stream(x))
+    return out
+
+
+def groupsum_packed(xp, B, C):
+    require_gpu(xp)
+    W = xp.shape[0]
+    out = torch.empty((B, C), device=xp.device, dtype=torch.float32)
+    _lib.call("slg_groupsum_packed", _p(xp), W, B, C, _p(out), _stream(xp))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# conv
+# ---------------------------------------------------------------------------
+def conv_soft_prep(conn, raw, node_kind, N, leaves, K, depth, arity):
+    require_gpu(raw)
+    w = torch.empty((N, leaves, K), device=raw.device, dtype=torch.float32)
+    if node_kind == GATE16:
+        npar = torch.empty((N, leaves - 1, 4), device=raw.device, dtype=torch.float32)
+    else:
+        npar = torch.empty((N, 2 ** arity), device=raw.device, dtype=torch.float32)
+    _lib.call("slg_conv_soft_prep", _p(_c(conn, torch.float32)), N, leaves, K, node_kind, depth,
+              arity, _p(_c(raw, torch.float32)), _p(w), _p(npar), _stream(raw))
+    return w, npar
+
+
+def _conv_soft_launch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
+    B, Cc, H, W = x.shape
+    N = cm.shape[0]
+    leaves = 2 ** depth if node_kind == GATE16 else arity
+    nparam = (N, leaves - 1, 4) if node_kind == GATE16 else (N, 2 ** arity)
+    if (cm.shape != (N, leaves, K) or ch.shape != cm.shape or cw.shape != cm.shape
+            or w.shape != cm.shape or tuple(npar.shape) != nparam):
+        raise ValueError("conv_soft: tap / weight / node parameter shapes are inconsistent")
+    kern = 2 * pad + 1
+    Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
+    Ho, Wo = (Hf // 2, Wf // 2) if pool else (Hf, Wf)
+    out = torch.empty((B, N, Ho, Wo), device=x.device, dtype=torch.float32)
+    _lib.call("slg_conv_soft_fwd", _p(x), B, Cc, H, W, N, node_kind, depth, arity, K, _p(npar),
+              _p(w), _p(cm), _p(ch), _p(cw), pad, int(bool(pool)), _p(out), _stream(x))
+    return out
+
+
+def conv_soft_torch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
+    """Differentiable torch expression of the fused conv op (backward only)."""
+    B, Cc, H, W = x.shape
+    N, leaves = cm.shape[0], cm.shape[1]
+    kern = 2 * pad + 1
+    patches = F.unfold(x, (kern, kern), padding=pad)                  # [B, C*k*k, L]
+    flat = (cm.long() * kern * kern + ch.long() * kern + cw.long()).reshape(-1)
+    g = patches[:, flat, :].view(B, N, leaves, K, -1)
+    vals = (g * w.view(1, N, leaves, K, 1)).sum(3)                    # [B, N, leaves, L]
+    if node_kind == GATE16:
+        nb, cnt = 0, leaves
+        while cnt > 1:
+            c = npar[:, nb:nb + cnt // 2, :].unsqueeze(0).unsqueeze(-1)
+            a, b = vals[:, :, 0::2, :], vals[:, :, 1::2, :]
+            vals = c[:, :, :, 0] + c[:, :, :, 1] * a + c[:, :, :, 2] * b + c[:, :, :, 3] * (a * b)
+            nb += cnt // 2
+            cnt //= 2
+        out = vals[:, :, 0, :]
+    else:
+        corners = torch.tensor([[(p >> j) & 1 for j in range(arity)] for p in range(2 ** arity)],
+                               dtype=x.dtype, device=x.device)
+        a = vals.permute(0, 1, 3, 2).unsqueeze(3)                    # [B, N, L, 1, A]
+        c = corners.view(1, 1, 1, -1, arity)
+        prod = (c * a + (1 - c) * (1 - a)).prod(-1)                   # [B, N, L, P]
+        out = (prod * npar.view(1, N, 1, -1)).sum(-1)
+    Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
+    out = out.view(B, N, Hf, Wf)
+    return F.max_pool2d(out, 2, 2) if pool else out
+
+
+class ConvSoftFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
+        x = _as_f32(x)
+        npar, w = _c(npar, torch.float32), _c(w, torch.float32)
+        ctx.save_for_backward(x, npar, w, cm, ch, cw)
+        ctx.meta = (node_kind, depth, arity, K, pad, pool)
+        return _conv_soft_launch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, npar, w, cm, ch, cw = ctx.saved_tensors
+        meta = ctx.meta
+        need = ctx.needs_input_grad
+        with torch.enable_grad():
+            xs = x.detach().requires_grad_(need[0])
+            ns = npar.detach().requires_grad_(need[1])
+            ws = w.detach().requires_grad_(need[2])
+            y = conv_soft_torch(xs, ns, ws, cm, ch, cw, *meta)
+            inputs = [t for t, n in ((xs, need[0]), (ns, need[1]), (ws, need[2])) if n]
+            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
+        gx = grads.pop(0) if need[0] else None
+        gn = grads.pop(0) if need[1] else None
+        gw = grads.pop(0) if need[2] else None
+        return (gx, gn, gw) + (None,) * 9
+
+
+def conv_soft(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
+    require_gpu(x, npar, w, cm)
+    cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or npar.requires_grad):
+        return ConvSoftFn.apply(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool)
+    return _conv_soft_launch(_as_f32(x), _c(npar, torch.float32), _c(w, torch.float32), cm, ch,
+                             cw, node_kind, depth, arity, K, pad, pool)
+
+
+def conv_hard_prep(cm, ch, cw, conn, raw, node_kind, depth, arity):
+    require_gpu(cm, raw)
+    cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
+    N, leaves, K = cm.shape
+    leaf = torch.empty((N, leaves), device=cm.device, dtype=torch.int32)
+    tt = torch.empty((N,), device=cm.device, dtype=torch.int64)
+    _lib.call("slg_conv_hard_prep", _p(cm), _p(ch), _p(cw), _p(_c(conn, torch.float32)), N,
+              leaves, K, node_kind, depth, arity, _p(_c(raw, torch.float32)), _p(leaf), _p(tt),
+              _stream(cm))
+    return leaf, tt
+
+
+def conv_hard(xp, shape_chw, leaf, tt, node_kind, depth, arity, kernel, pad, pool):
+    """Packed conv: ``xp`` [C,H,W,nw] -> [N,Ho,Wo,nw] (pooled if ``pool``)."""
+    require_gpu(xp, leaf, tt)
+    Cc, H, W = shape_chw
+    nw = xp.shape[-1]
+    N = leaf.shape[0]
+    leaves = 2 ** depth if node_kind == GATE16 else arity
+    if xp.numel() != Cc * H * W * nw or leaf.shape != (N, leaves) or tt.shape != (N,):
+        raise ValueError("conv_hard: packed input / leaf / truth-table shapes are inconsistent")
+    Hf, Wf = H + 2 * pad - kernel + 1, W + 2 * pad - kernel + 1
+    Ho, Wo = (Hf // 2, Wf // 2) if pool else (Hf, Wf)
+    out = torch.empty((N, Ho, Wo, nw), device=xp.device, dtype=torch.int64)
+    _lib.call("slg_conv_hard_fwd", _p(xp), Cc, H, W, nw, N, node_kind, depth, arity, _p(leaf),
+              _p(tt), kernel, pad, int(bool(pool)), _p(out), _stream(xp))
+    return out

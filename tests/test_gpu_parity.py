@@ -1,0 +1,379 @@
+"""HIP path vs the oracle / the reference's golden vectors (GPU).
+
+Bars: hard outputs and every integer / packed value bit-exact; soft fp32
+values within |got - ref| <= RTOL*|ref| + ATOL with RTOL = 1e-5 (the north
+star's 1e-5 relative; ATOL = 1e-6 only covers values near 0, soft values live
+in [0, 1]). Soft logits with the feature STE count (x > 0.5): they must equal
+the count of the kernel's own features, and any feature whose side of 0.5
+differs from the oracle must lie within the soft tolerance of 0.5.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import silogic_amd as sl
+from conftest import build_product, load_fixture, random_bits
+from oracle import packed_ref, torch_ref
+from silogic_amd import ops
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 1e-5, 1e-6
+DEV = "cuda"
+
+
+def assert_soft_close(got, ref, what):
+    got, ref = got.detach().float().cpu(), ref.detach().float().cpu()
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    err = (got - ref).abs()
+    bound = RTOL * ref.abs() + ATOL
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} values outside tolerance, "
+                           f"max err {err.max().item():.3e}")
+
+
+def assert_ste_logits(logits, feats, feats_ref, C, tau):
+    logits, feats, feats_ref = logits.cpu(), feats.cpu(), feats_ref.cpu()
+    B, W = feats.shape
+    own = (feats > 0.5).float().view(B, C, W // C).sum(2) / tau
+    assert torch.equal(logits, own)
+    flips = (feats > 0.5) != (feats_ref > 0.5)
+    if flips.any():
+        assert ((feats_ref[flips] - 0.5).abs() <= RTOL * 0.5 + ATOL).all()
+
+
+def _gpu_model(fx):
+    model = build_product(fx.spec)
+    model.load_state_dict(fx.sd, strict=True)   # the reference's own parameters
+    return model.to(DEV).eval()
+
+
+# --------------------------------------------------------------------------
+# golden fixtures (tiny versions of the five configs)
+# --------------------------------------------------------------------------
+def test_fixture_soft_layers(fixture):
+    """Each layer on the reference's own previous activation (isolates every
+    kernel launch), then the chained forward."""
+    model = _gpu_model(fixture)
+    A = fixture.arrays
+    with torch.no_grad():
+        if fixture.kind == "fc":
+            h = fixture.x
+            for i, layer in enumerate(model.layers):
+                y = layer(h.to(DEV))
+                assert_soft_close(y, A[f"act/{i}"], f"act/{i}")
+                h = A[f"act/{i}"]
+        else:
+            h = fixture.x
+            convs = model._convs()
+            for i, conv in enumerate(convs):
+                assert_soft_close(conv(h.to(DEV)), A[f"conv/{i}"], f"conv/{i}")
+                assert_soft_close(conv.forward_pooled(h.to(DEV)), A[f"pool/{i}"], f"pool/{i}")
+                assert_soft_close(model.blocks[2 * i + 1](A[f"conv/{i}"].to(DEV)), A[f"pool/{i}"],
+                                  f"orpool/{i}")
+                h = A[f"pool/{i}"]
+            h = h.flatten(1)
+            for j, layer in enumerate(model.head_layers):
+                assert_soft_close(layer(h.to(DEV)), A[f"act/{j}"], f"act/{j}")
+                h = A[f"act/{j}"]
+        last = h
+        head = model.head
+        assert_ste_logits(head(last.to(DEV)), last, last, head.num_classes, head.tau)
+        model.head.feature_ste = False
+        assert_soft_close(model(fixture.x.to(DEV)), A["logits_soft_noste"], "logits (no STE)")
+        model.head.feature_ste = True
+        out = model(fixture.x.to(DEV))
+    assert out.shape == A["logits_soft"].shape
+    # STE logits of the chained run: recompute the kernel's own final features
+    feats = _soft_features(model, fixture.x.to(DEV))
+    assert_soft_close(feats, last, "chained final features")
+    assert_ste_logits(out, feats, last, model.head.num_classes, model.head.tau)
+
+
+def _soft_features(model, x):
+    with torch.no_grad():
+        if hasattr(model, "layers"):
+            return model._run(x)
+        h = model._apply_blocks(x).flatten(1)
+        for layer in model.head_layers:
+            h = layer(h)
+        return h
+
+
+def test_fixture_hard_bit_exact(fixture):
+    model = _gpu_model(fixture)
+    A = fixture.arrays
+    out = model.forward_hard(fixture.x.to(DEV)).cpu()
+    assert torch.equal(out, A["logits_hard"])
+    # uint8 input path gives the same circuit (tests/test_warp.py:55-63)
+    out8 = model.forward_hard(fixture.x.to(torch.uint8).to(DEV)).cpu()
+    assert torch.equal(out8, A["logits_hard"])
+    # per-layer forward_hard on the reference's previous hard activation
+    if fixture.kind == "fc":
+        h = fixture.x
+        for i, layer in enumerate(model.layers):
+            assert torch.equal(layer.forward_hard(h.to(DEV)).cpu(), A[f"hact/{i}"]), i
+            h = A[f"hact/{i}"]
+    else:
+        h = fixture.x
+        for i, conv in enumerate(model._convs()):
+            y = conv.forward_hard(h.to(DEV)).cpu()
+            assert torch.equal(y, A[f"hconv/{i}"]), i
+            h = model.blocks[2 * i + 1].forward_hard(A[f"hconv/{i}"].to(DEV)).cpu()
+            assert torch.equal(h, torch_ref.orpool_hard(A[f"hconv/{i}"]))
+        h = h.flatten(1)
+        for j, layer in enumerate(model.head_layers):
+            assert torch.equal(layer.forward_hard(h.to(DEV)).cpu(), A[f"hact/{j}"]), j
+            h = A[f"hact/{j}"]
+    assert torch.equal(model.head.forward_hard(h.to(DEV)).cpu(), A["logits_hard"])
+
+
+# --------------------------------------------------------------------------
+# kernels against the oracle on crafted / edge inputs
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("B,D", [(1, 1), (63, 8), (64, 64), (65, 257), (200, 784), (1000, 33)])
+def test_pack_matches_reference_layout(B, D):
+    x = random_bits(B, D)
+    xp = ops.pack_bits(x.to(DEV)).cpu().numpy()
+    np.testing.assert_array_equal(xp, packed_ref.pack_bits(x.numpy().astype(np.uint8)))
+    np.testing.assert_array_equal(ops.unpack_bits(torch.from_numpy(xp).to(DEV), B).cpu().numpy(),
+                                  x.numpy().astype(np.uint8))
+    xp8 = ops.pack_bits(x.to(torch.uint8).to(DEV)).cpu().numpy()
+    np.testing.assert_array_equal(xp8, xp)
+
+
+def test_all_sixteen_gates_packed():
+    """Each gate g as a one-hot gate16 layer: packed kernel == truth table."""
+    B, IN = 130, 2
+    x = torch.tensor([[i & 1, (i >> 1) & 1] for i in range(B)], dtype=torch.float32)
+    layer = sl.LogicLayer(IN, 16, connectome="fixed", seed=0)
+    with torch.no_grad():
+        layer._conn.idx.copy_(torch.tensor([[1, 0]] * 16))   # a = x[:,1], b = x[:,0]
+        layer._conn.cand_i32.copy_(layer._conn.idx.unsqueeze(-1).int())
+        layer.node.gate_logits.copy_(torch.eye(16) * 5.0)
+    layer = layer.to(DEV)
+    y = layer.forward_hard(x.to(DEV)).cpu()
+    a, b = x[:, 1].long(), x[:, 0].long()
+    for g in range(16):
+        ref = torch_ref.TRUTH[g][(a << 1) | b]
+        assert torch.equal(y[:, g], ref), g
+    # soft path of the same hardened layer agrees on {0,1} inputs
+    with torch.no_grad():
+        layer.node.gate_logits.copy_(torch.eye(16, device=DEV) * 40.0)
+        assert (layer(x.to(DEV)).cpu() - y.float()).abs().max() < 1e-6
+
+
+def test_walsh_hard_truth_table_near_ties():
+    """Corner sums that cancel to (near) zero take the sign of the fp32
+    left-to-right sum, as torch's CPU reduction does."""
+    L = dict(prefix="", node="walsh", arity=2, node_tau=1.0, conn="fixed", d_in=2, d_out=0)
+    g = torch.Generator().manual_seed(3)
+    th = torch.randn(4000, 4, generator=g)
+    th[:1000, 3] = -(th[:1000, 0] - th[:1000, 1] - th[:1000, 2])   # corner (0,0) cancels
+    th[1000:2000] = torch.tensor([0.1, 0.2, 0.3, 0.0])
+    th[1000:2000, 3] = -(th[1000:2000, 0] + th[1000:2000, 1] + th[1000:2000, 2])
+    th[2000:2100] = torch.tensor([1e-8, 1.0, -1.0, 0.5])
+    layer = sl.LogicLayer(2, 4000, node="walsh", connectome="fixed", seed=0)
+    with torch.no_grad():
+        layer.node.theta.copy_(th)
+        layer._conn.idx.copy_(torch.tensor([[1, 0]] * 4000))
+        layer._conn.cand_i32.copy_(layer._conn.idx.unsqueeze(-1).int())
+    layer = layer.to(DEV)
+    x = torch.tensor([[0., 0], [1, 0], [0, 1], [1, 1]])            # (b, a) columns
+    y = layer.forward_hard(x.to(DEV)).cpu()
+    ops_ = torch.stack([x[:, 1], x[:, 0]], dim=1).unsqueeze(1).expand(4, 4000, 2)
+    ref = torch_ref.node_hard(dict(L, d_out=4000), {"node.theta": th}, ops_)
+    assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("node", ["gate16", "walsh", "multilinear"])
+@pytest.mark.parametrize("conn", ["topk", "fixed"])
+@pytest.mark.parametrize("B", [1, 37, 130])
+def test_fc_layer_soft_and_hard(node, conn, B):
+    spec = ("LogicNet", dict(in_dim=300, width=70, depth=1, num_classes=10, node=node,
+                             connectome=conn, k=8, tau=3.0))
+    model = build_product(spec)
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV).eval()
+    x = random_bits(B, 300)
+    L = torch_ref.structure(spec)["layers"][0]
+    with torch.no_grad():
+        assert_soft_close(model.layers[0](x.to(DEV)), torch_ref.fc_layer_soft(L, sd, x), "soft")
+    assert torch.equal(model.layers[0].forward_hard(x.to(DEV)).cpu(),
+                       torch_ref.fc_layer_hard(L, sd, x))
+    assert torch.equal(model.forward_hard(x.to(DEV)).cpu(), torch_ref.forward_hard(spec, sd, x))
+
+
+@pytest.mark.parametrize("tile", [1, 2, 4, 8, 16])
+def test_fc_soft_every_tile_size(tile):
+    spec = ("LogicNet", dict(in_dim=500, width=130, depth=1, k=8))
+    model = build_product(spec)
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV)
+    x = torch.rand(45, 500)
+    layer = model.layers[0]
+    with torch.no_grad():
+        cand, w, npar = layer.soft_params(False)
+        y = ops._fc_soft_launch(x.to(DEV), cand, w, npar, ops.GATE16, 1.0, tile=tile)
+    L = torch_ref.structure(spec)["layers"][0]
+    assert_soft_close(y, torch_ref.fc_layer_soft(L, sd, x), f"tile {tile}")
+
+
+def test_empty_batch():
+    net = sl.LogicNet(32, 40, 2, k=4).to(DEV).eval()
+    x = torch.zeros(0, 32, device=DEV)
+    with torch.no_grad():
+        assert net(x).shape == (0, 10)
+        assert net.forward_hard(x).shape == (0, 10)
+
+
+def test_fused_net_equals_layerwise_path_and_wide_32bit_tiles():
+    """Two independent hard pipelines agree: the depth-fused LDS kernel
+    (64- and 32-sample tiles) and the layer-by-layer packed kernels."""
+    for width in (1000, 12000):   # 12000 words x 8B x 2 exceeds LDS -> 32-sample tiles
+        spec = ("LogicNet", dict(in_dim=200, width=width, depth=3, k=8))
+        model = build_product(spec)
+        sd = {k: v.clone() for k, v in model.state_dict().items()}
+        model = model.to(DEV).eval()
+        x = random_bits(333, 200)
+        xd = x.to(DEV)
+        codes = [l.hard_codes() for l in model.layers]
+        fused = ops.fc_hard_net(xd, 0, 333, 200, codes, 10)
+        xp = ops.pack_bits(xd)
+        for c in codes:
+            xp = ops.fc_hard_layer(xp, c)
+        layerwise = ops.groupsum_packed(xp, 333, 10)
+        assert torch.equal(fused.cpu(), layerwise.cpu())
+        assert torch.equal(fused.cpu(), torch_ref.forward_hard(spec, sd, x))
+
+
+def test_wire_residual_hard_and_soft():
+    spec = ("LogicNet", dict(in_dim=40, width=40, depth=3, k=8, wire_residual=0.25))
+    model = build_product(spec)
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV).eval()
+    x = random_bits(70, 40)
+    assert torch.equal(model.forward_hard(x.to(DEV)).cpu(), torch_ref.forward_hard(spec, sd, x))
+    with torch.no_grad():
+        model.head.feature_ste = False
+        assert_soft_close(model(x.to(DEV)), torch_ref.forward(spec, sd, x, ste=False), "logits")
+
+
+@pytest.mark.parametrize("depth", [1, 2, 3])
+@pytest.mark.parametrize("connect", ["topk", "fixed"])
+def test_conv_gate16_depths(depth, connect):
+    conv = sl.ConvLogicTree(6, 12, kernel=3, tree_depth=depth, connect=connect, k=4, n_chan=2,
+                            residual_init=False, seed=1)
+    sd = {k: v.clone() for k, v in conv.state_dict().items()}
+    blk = dict(prefix="", cin=6, n=12, kernel=3, depth=depth, stride=1, padding=1,
+               connect=connect, k=conv.k, node="gate16", node_arity=2, leaves=2 ** depth)
+    conv = conv.to(DEV).eval()
+    x = torch.rand(5, 6, 9, 11)
+    with torch.no_grad():
+        assert_soft_close(conv(x.to(DEV)), torch_ref.conv_soft(blk, sd, x), "conv")
+        assert_soft_close(conv.forward_pooled(x.to(DEV)),
+                          torch_ref.orpool_soft(torch_ref.conv_soft(blk, sd, x)), "pooled")
+    xb = random_bits(70, 6, 9, 11)
+    assert torch.equal(conv.forward_hard(xb.to(DEV)).cpu(), torch_ref.conv_hard(blk, sd, xb))
+
+
+@pytest.mark.parametrize("arity", [2, 3, 4, 5, 6])
+def test_conv_multilinear_lut(arity):
+    conv = sl.ConvLogicTree(5, 10, kernel=3, tree_depth=1, connect="topk", k=4, n_chan=2,
+                            node="multilinear", arity=arity, residual_init=False, seed=2)
+    sd = {k: v.clone() for k, v in conv.state_dict().items()}
+    blk = dict(prefix="", cin=5, n=10, kernel=3, depth=1, stride=1, padding=1, connect="topk",
+               k=conv.k, node="multilinear", node_arity=arity, leaves=arity)
+    conv = conv.to(DEV).eval()
+    x = torch.rand(3, 5, 8, 7)
+    with torch.no_grad():
+        assert_soft_close(conv(x.to(DEV)), torch_ref.conv_soft(blk, sd, x), "conv")
+    xb = random_bits(66, 5, 8, 7)
+    assert torch.equal(conv.forward_hard(xb.to(DEV)).cpu(), torch_ref.conv_hard(blk, sd, xb))
+
+
+def test_kernels_module_drop_ins():
+    """silogic.kernels-compatible entry points (tests/test_triton.py analogues)."""
+    layer = sl.LogicLayer(256, 512, connectome="TopK", k=8, seed=0)
+    sd = {k: v.clone() for k, v in layer.state_dict().items()}
+    layer = layer.to(DEV).eval()
+    x = random_bits(64, 256)
+    with torch.no_grad():
+        w = layer._conn.weights()
+        ca = layer._conn.cand_i32
+        coef = layer.node.coef()
+        y = sl.kernels.dense_logic(x.to(DEV), ca[:, 0].contiguous(), ca[:, 1].contiguous(),
+                                   w[:, 0].contiguous(), w[:, 1].contiguous(), coef)
+    L = dict(prefix="", node="gate16", arity=2, conn="topk")
+    assert_soft_close(y, torch_ref.fc_layer_soft(L, sd, x), "dense_logic")
+
+    wl = sl.WARPLayer(256, 512, k=8, tau=0.5, seed=1)
+    sdw = {k: v.clone() for k, v in wl.state_dict().items()}
+    wl = wl.to(DEV)
+    with torch.no_grad():
+        w = wl._conn.weights()
+        ca = wl._conn.cand_i32
+        y = sl.kernels.warp_logic(x.to(DEV), ca[:, 0].contiguous(), ca[:, 1].contiguous(),
+                                  w[:, 0].contiguous(), w[:, 1].contiguous(), wl._coef(),
+                                  wl.node.inv_tau)
+    Lw = dict(prefix="", node="walsh", arity=2, conn="topk", node_tau=0.5)
+    assert_soft_close(y, torch_ref.fc_layer_soft(Lw, sdw, x), "warp_logic")
+
+    conv = sl.ConvLogicTree(6, 16, kernel=3, tree_depth=3, connect="topk", k=4, n_chan=2,
+                            seed=1, residual_init=False)
+    sdc = {k: v.clone() for k, v in conv.state_dict().items()}
+    conv = conv.to(DEV)
+    xi = random_bits(4, 6, 16, 16)
+    blk = dict(prefix="", n=16, kernel=3, depth=3, stride=1, padding=1, connect="topk",
+               k=conv.k, node="gate16", node_arity=2, leaves=8)
+    with torch.no_grad():
+        yk = sl.kernels.tree_conv_topk(xi.to(DEV), conv._basis_coef().contiguous(),
+                                       conv._topk_w(), conv.lc_cm, conv.lc_ch, conv.lc_cw, 3,
+                                       conv.k, 1, 1, 16, 16)
+    assert_soft_close(yk, torch_ref.conv_soft(blk, sdc, xi), "tree_conv_topk")
+    convf = sl.ConvLogicTree(6, 16, kernel=3, tree_depth=2, connect="fixed", n_chan=2, seed=0)
+    sdf = {k: v.clone() for k, v in convf.state_dict().items()}
+    convf = convf.to(DEV)
+    blkf = dict(blk, depth=2, connect="fixed", k=1, leaves=4)
+    with torch.no_grad():
+        yf = sl.kernels.tree_conv(xi.to(DEV), convf._basis_coef().contiguous(), convf.cm_idx,
+                                  convf.ch_idx, convf.cw_idx, 2, 1, 1, 16, 16)
+    assert_soft_close(yf, torch_ref.conv_soft(blkf, sdf, xi), "tree_conv")
+
+
+def test_groupsum_and_orpool_modules():
+    x = torch.rand(9, 60)
+    gs = sl.GroupSum(10, tau=4.0, feature_ste=False).to(DEV)
+    head = dict(C=10, tau=4.0, ste=False)
+    assert_soft_close(gs(x.to(DEV)), torch_ref.groupsum_soft(head, x), "groupsum")
+    xb = random_bits(9, 60)
+    assert torch.equal(gs.forward_hard(xb.to(DEV)).cpu(), torch_ref.groupsum_hard(head, xb))
+    assert torch.equal(gs.forward_hard(xb.to(torch.uint8).to(DEV)).cpu(),
+                       torch_ref.groupsum_hard(head, xb.to(torch.uint8)))
+    xi = torch.rand(2, 3, 7, 9)
+    pool = sl.OrPool(2)
+    assert torch.equal(pool(xi.to(DEV)).cpu(), F.max_pool2d(xi, 2, 2))
+    xu = random_bits(2, 3, 7, 9)
+    assert torch.equal(pool.forward_hard(xu.to(DEV)).cpu(), torch_ref.orpool_hard(xu))
+
+
+def test_gradients_match_the_oracle():
+    """Composite backward through the HIP forward: gradients w.r.t. input,
+    connections and gate logits match autograd through the oracle (the
+    reference's fused-kernel gradient bar is 1e-3, tests/test_triton.py)."""
+    spec = ("LogicNet", dict(in_dim=64, width=40, depth=2, k=8, tau=4.0, decoder_ste=False))
+    model = build_product(spec)
+    params = {k: v.clone().requires_grad_(v.is_floating_point())
+              for k, v in model.state_dict().items()}
+    x = torch.rand(16, 64)
+    xr = x.clone().requires_grad_(True)
+    ref = torch_ref.groupsum_soft(dict(C=10, tau=4.0, ste=False),
+                                  torch_ref.forward_features(torch_ref.structure(spec), params, xr,
+                                                             hard=False))
+    ref.pow(2).sum().backward()
+    model = model.to(DEV).train()
+    xg = x.to(DEV).requires_grad_(True)
+    model(xg).pow(2).sum().backward()
+    assert (xg.grad.cpu() - xr.grad).abs().max() < 1e-4
+    for name, p in model.named_parameters():
+        assert (p.grad.cpu() - params[name].grad).abs().max() < 1e-4, name

@@ -1,0 +1,117 @@
+"""Host-side checks that need no GPU: RNG-faithful construction and
+``state_dict`` layout against the reference's golden vectors, the C ABI
+library loads and exports every declared entry point, and the product path
+refuses to compute on the CPU."""
+import ctypes
+import hashlib
+import json
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import silogic_amd
+from conftest import GOLDEN, ROOT, build_product
+from silogic_amd import _lib, synthetic
+
+
+def test_tiny_construction_matches_reference_state_dict(fixture):
+    model = build_product(fixture.spec)
+    sd = model.state_dict()
+    assert set(sd) == set(fixture.sd), set(sd) ^ set(fixture.sd)
+    for k, v in fixture.sd.items():
+        assert sd[k].dtype == v.dtype and torch.equal(sd[k], v), k
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_full_size_construction_matches_reference_hashes(cfg):
+    """Exact construction of the five BASELINE configs (SHA-256 of every
+    state_dict tensor of the reference-built model)."""
+    with open(os.path.join(GOLDEN, "construct_sha256.json")) as fh:
+        ref = json.load(fh)[f"cfg{cfg}"]
+    ctor, args = synthetic.CONFIGS[cfg]
+    assert ref["ctor"] == ctor and ref["args"] == json.loads(json.dumps(args))
+    model = synthetic.build_config(cfg)
+    sd = model.state_dict()
+    assert set(sd) == set(ref["tensors"])
+    for k, v in sd.items():
+        a = np.ascontiguousarray(v.detach().cpu().numpy())
+        assert list(a.shape) == ref["tensors"][k]["shape"], k
+        assert hashlib.sha256(a.tobytes()).hexdigest() == ref["tensors"][k]["sha256"], k
+
+
+def _declared_symbols():
+    with open(os.path.join(ROOT, "include", "silogic_hip.h")) as fh:
+        text = fh.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(slg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    path = _lib.library_path()
+    if not os.path.exists(path):
+        pytest.fail(f"{path} missing: run __graft_entry__.build()")
+    h = ctypes.CDLL(path)
+    declared = _declared_symbols()
+    assert len(declared) >= 20
+    missing = [s for s in declared if not hasattr(h, s)]
+    assert not missing, missing
+    assert set(declared) == set(_lib.SIGNATURES), set(declared) ^ set(_lib.SIGNATURES)
+    assert h.slg_version() >= 1
+
+
+def test_entry_points_reject_bad_arguments_without_a_gpu():
+    """Argument validation runs before any device work and reports a message."""
+    L = _lib.lib()
+    rc = L.slg_fc_soft_fwd(None, 4, 8, 8, 8, None, None, 0, None, 1.0, None, 0, 0, None)
+    assert rc == -1 and b"null" in L.slg_last_error()
+    rc = L.slg_groupsum_soft(ctypes.c_void_p(16), 4, 25, 10, 1.0, 1, ctypes.c_void_p(16), None)
+    assert rc == -2 and b"divisible" in L.slg_last_error()
+    rc = L.slg_conv_soft_fwd(ctypes.c_void_p(16), 1, 1, 4, 4, 1, 0, 5, 2, 1, ctypes.c_void_p(16),
+                             None, ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                             1, 1, ctypes.c_void_p(16), None)
+    assert rc == -3
+
+
+def test_cpu_inputs_are_refused():
+    net = silogic_amd.LogicNet(16, 20, 2, k=4)
+    x = torch.zeros(3, 16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        net(x)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        net.forward_hard(x)
+
+
+def test_missing_library_fails_loudly():
+    code = ("import silogic_amd, silogic_amd._lib as L\n"
+            "try:\n    L.lib()\nexcept ImportError as e:\n    print('IMPORT_ERROR', e)\n"
+            "print('HAS_DENSE', silogic_amd.kernels.HAS_DENSE)\n")
+    env = dict(os.environ, SILOGIC_HIP_LIB="/nonexistent/libsilogic_hip.so")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True,
+                       text=True, timeout=120)
+    assert "IMPORT_ERROR" in r.stdout and "HAS_DENSE False" in r.stdout, r.stdout + r.stderr
+
+
+def test_unsupported_components_are_rejected_at_construction():
+    with pytest.raises(NotImplementedError):
+        silogic_amd.LogicLayer(8, 8, connectome="dense")
+    with pytest.raises(NotImplementedError):
+        silogic_amd.LogicLayer(8, 8, node="hybrid")
+    with pytest.raises(NotImplementedError):
+        silogic_amd.LogicNet(8, 20, 2, decoder="linear")
+
+
+def test_public_api_names_mirror_the_reference():
+    for name in ["LogicLayer", "LogicNet", "WARPNet", "WARPLayer", "LogicConvNet",
+                 "LogicTreeNet", "ConvLogicTree", "ConvLogicLayer", "OrPool", "GroupSum",
+                 "BASIS_COEFFS", "TRUTH_TABLES", "build_connectome", "build_node",
+                 "build_decoder", "gate_probs", "binarize_ste"]:
+        assert hasattr(silogic_amd, name), name
+    for name in ["dense_logic", "warp_logic", "tree_conv", "tree_conv_topk", "HAS_DENSE",
+                 "HAS_WARP", "HAS_CONV", "HAS_CONV_TOPK"]:
+        assert hasattr(silogic_amd.kernels, name), name
