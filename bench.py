@@ -92,13 +92,54 @@ def cpu_baseline(sd, x_hard, x_soft, gates):
     }
 
 
+def load_traffic():
+    """HBM bytes per launch of the dominant kernels, measured with rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE and scaled by the same counters' reading for
+    a plain copy of known size (profiles/hbm_traffic.json; see --kernels-only)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as fh:
+        return json.load(fh)
+
+
+def kernels_only(reps=3):
+    """Workload for counter passes: a 256 MiB copy (calibration), then the
+    fused hard network and one soft hidden layer of config 2, ``reps`` times."""
+    import silogic_amd as sl
+    from silogic_amd import ops
+    from silogic_amd.synthetic import build_config, config_inputs
+    dev = torch.device("cuda:0")
+    src = torch.ones(64 << 20, device=dev)          # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    model = build_config(2, sl).eval().to(dev)
+    xh = config_inputs(2, 65536).to(dev)
+    with torch.no_grad():
+        codes = [l.hard_codes() for l in model.layers]
+        for _ in range(reps):
+            ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
+        x_mid = torch.rand(4096, 10000, device=dev)
+        cand, w, npar = model.layers[1].soft_params(False)
+        for _ in range(reps):
+            ops.fc_soft(x_mid, cand, w, npar, ops.GATE16)
+    torch.cuda.synchronize()
+    log("kernels-only done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the copy calibration and the dominant kernels (for --pmc)")
     args = ap.parse_args()
+    if args.kernels_only:
+        kernels_only()
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -156,7 +197,7 @@ def main():
     with torch.no_grad():
         codes = [l.hard_codes() for l in model.layers]
         reps = 20
-        fn_net = lambda: ops.fc_hard_net(x_hard, 0, B_hard, 784, codes, 10)   # noqa: E731
+        fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, 784, codes, 10)  # noqa: E731
         fn_net()
         k_hard = _events_ms(fn_net, reps) / 1e3
         L = model.layers[1]
@@ -170,6 +211,7 @@ def main():
     hard_gbs = hard_bytes / k_hard / 1e9
     soft_gbs = soft_bytes / k_soft / 1e9
     bitops = B_hard * gates / k_hard
+    traffic = load_traffic()
 
     result = {
         "metric": "hard-circuit Ggate-evals/s + soft fwd samples/s; % HBM/VALU roofline, 1 GPU",
@@ -192,16 +234,18 @@ def main():
         "soft_dtype": "f32",
         "t_hard_us": round(t_hard * 1e6, 2),
         "t_soft_us": round(t_soft * 1e6, 2),
-        "roofline": {"kernel": "fc_hard_net_kernel (6 layers + GroupSum, fused)",
+        "roofline": {"kernel": "fc_hard_net_rows_kernel (packing + 6 layers + GroupSum)",
                      "bound": "hbm", "achieved": round(hard_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": hard_bytes,
+                     "traffic": traffic.get("fc_hard_net_rows_kernel"),
+                     "algorithmic_bytes": hard_bytes,
                      "avg_kernel_us": round(k_hard * 1e6, 2)},
         "roofline_valu": {"kernel": "fc_hard_net_kernel", "achieved_bitops_per_s": bitops,
                           "peak": VALU_BITOPS_PEAK, "frac": round(bitops / VALU_BITOPS_PEAK, 4)},
         "roofline_soft": {"kernel": "fc_soft_kernel (gate16, K=8, IN=OUT=10000, B=4096)",
                           "bound": "hbm", "achieved": round(soft_gbs, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
+                          "traffic": traffic.get("fc_soft_kernel"),
                           "algorithmic_bytes": soft_bytes, "avg_kernel_us": round(k_soft * 1e6, 2)},
     }
     if not args.no_cpu:

@@ -10,8 +10,9 @@
  *   - Return 0 on success, a negative SLG_E_* code for a rejected argument or
  *     shape (nothing is launched), or a positive hipError_t from the launch.
  *     slg_last_error() returns a thread-local message for the last failure.
- *   - No entry point allocates device memory. Workspace, where needed, is a
- *     caller argument whose size is given by the matching *_workspace call.
+ *   - No entry point allocates device memory or needs a workspace: every
+ *     intermediate lives in registers or LDS, or in an output array the
+ *     caller passes.
  *   - Floating-point math is IEEE fp32 (no fast-math); hard paths are exact.
  *
  * Bit-packed layout ("packed"): a [D, nw] array of uint64 words,
@@ -116,11 +117,12 @@ int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, in
 /* ---------------------------------------------------------------------- */
 
 /* LogicLayer.forward_hard input cast (layers.py:133) fused with packing:
- * x [B,D] (dtype 0 = fp32, 1 = uint8) -> xp [D, ceil(B/64)] uint64; bit set
- * iff uint8(x) != 0 (fp32: x >= 1). Padding bits are zero. Replaces
- * silogic/bitpacking/ops.py:32-49 pack_bits. */
-int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, uint64_t* xp,
-                  slg_stream_t stream);
+ * x [B,D] (dtype 0 = fp32, 1 = uint8) -> packed words, bit set iff
+ * uint8(x) != 0 (fp32: x >= 1); padding bits are zero. layout 0 writes the
+ * reference layout [D, ceil(B/64)] (replaces silogic/bitpacking/ops.py:32-49
+ * pack_bits); layout 1 writes word-major [ceil(B/64), D]. */
+int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, int32_t layout,
+                  uint64_t* xp, slg_stream_t stream);
 
 /* Inverse of slg_pack_bits to uint8 [B,D] (ops.py:52-63 unpack_bits). */
 int slg_unpack_bits(const uint64_t* xp, int64_t B, int64_t D, uint8_t* out,
@@ -149,7 +151,8 @@ int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw,
 /* Depth-fused packed FC network + GroupSum (replaces LogicNet.forward_hard,
  * models.py:99-101, with GroupSum.forward_hard, heads.py:41-45). Input x:
  * in_kind 0 = fp32 rows [B,IN0], 1 = uint8 rows [B,IN0] (packed on the fly,
- * bit = uint8(x) != 0), 2 = packed [IN0, ceil(B/64)] uint64. It runs
+ * bit = uint8(x) != 0; needs IN0 <= 1024 and 64-sample tiles), 2 = packed
+ * [IN0, ceil(B/64)] uint64, 3 = packed word-major [ceil(B/64), IN0]. It runs
  * n_layers arity-2 layers whose widths and device code arrays (from
  * slg_fc_hard_prep) are given by the host arrays widths[n_layers] and
  * codes[n_layers], then writes logits [B,C] fp32 = per-class popcounts of

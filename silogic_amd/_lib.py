@@ -26,7 +26,7 @@ SIGNATURES = {
     "slg_groupsum_soft": (C.c_int, [_P, _I64, _I64, _I32, _F32, _I32, _P, _P]),
     "slg_groupsum_hard": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_orpool": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P]),
-    "slg_pack_bits": (C.c_int, [_P, _I32, _I64, _I64, _P, _P]),
+    "slg_pack_bits": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_unpack_bits": (C.c_int, [_P, _I64, _I64, _P, _P]),
     "slg_fc_hard_prep": (C.c_int, [_P, _P, _I64, _I32, _I64, _I32, _P, _P, _P]),
     "slg_fc_hard_layer": (C.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),

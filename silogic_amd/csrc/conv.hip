@@ -439,7 +439,8 @@ int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
                       int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
                       const float* node_param, const float* w, const int32_t* cm, const int32_t* ch,
                       const int32_t* cw, int32_t pad, int32_t pool, float* out, slg_stream_t stream) {
-  SLG_REQUIRE(x && node_param && cm && ch && cw && out, SLG_E_ARG, "conv_soft: null pointer");
+  SLG_REQUIRE(node_param && cm && ch && cw && ((x && out) || B == 0), SLG_E_ARG,
+              "conv_soft: null pointer");
   SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
               "conv_soft: node_kind %d", node_kind);
   const int nleaf = node_leaves(node_kind, depth, arity);
@@ -501,7 +502,7 @@ int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64
                       int32_t node_kind, int32_t depth, int32_t arity, const int32_t* leaf,
                       const uint64_t* tt, int32_t kernel, int32_t pad, int32_t pool, uint64_t* out,
                       slg_stream_t stream) {
-  SLG_REQUIRE(xp && leaf && tt && out, SLG_E_ARG, "conv_hard: null pointer");
+  SLG_REQUIRE(leaf && tt && ((xp && out) || nw == 0), SLG_E_ARG, "conv_hard: null pointer");
   const int nleaf = node_leaves(node_kind, depth, arity);
   SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_hard: depth %d / arity %d", depth, arity);
   SLG_REQUIRE(C > 0 && H > 0 && W > 0 && nw >= 0 && N > 0 && kernel >= 1 && kernel <= 15 &&
@@ -520,7 +521,7 @@ int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64
 
 int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W, void* out,
                slg_stream_t stream) {
-  SLG_REQUIRE(x && out, SLG_E_ARG, "orpool: null pointer");
+  SLG_REQUIRE((x && out) || B == 0, SLG_E_ARG, "orpool: null pointer");
   SLG_REQUIRE(dtype == 0 || dtype == 1, SLG_E_ARG, "orpool: dtype %d", dtype);
   SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && B * C * H * W < (1LL << 46), SLG_E_SHAPE,
               "orpool: bad sizes");

@@ -45,8 +45,10 @@ __device__ inline uint64_t transpose64(uint64_t v, int lane) {
 // pack / unpack
 // ---------------------------------------------------------------------------
 // Tile: 64 samples (one output word) x 64 features. Coalesced row reads into
-// LDS, then one ballot per feature.
-template <typename T>
+// LDS, then one ballot per feature. LAYOUT 0 writes the reference layout
+// [D][nw]; LAYOUT 1 writes word-major [nw][D], where one 64-sample column of
+// all features is contiguous (the fused network kernel's input).
+template <typename T, int LAYOUT>
 __global__ void __launch_bounds__(256) pack_kernel(const T* __restrict__ x, int B, int D, int nw,
                                                    int dtiles, uint64_t* __restrict__ xp) {
   __shared__ uint8_t tile[64][68];
@@ -68,7 +70,10 @@ __global__ void __launch_bounds__(256) pack_kernel(const T* __restrict__ x, int 
   for (int j = 0; j < 16; ++j) {
     const int cc = wave * 16 + j;
     const uint64_t m = __ballot(tile[lane][cc] != 0);
-    if (lane == 0 && d0 + cc < D) xp[(int64_t)(d0 + cc) * nw + w] = m;
+    if (lane == 0 && d0 + cc < D) {
+      if constexpr (LAYOUT == 0) xp[(int64_t)(d0 + cc) * nw + w] = m;
+      else xp[(int64_t)w * D + d0 + cc] = m;
+    }
   }
 }
 
@@ -151,106 +156,70 @@ __global__ void __launch_bounds__(256) fc_hard_layer_kernel(const uint64_t* __re
   xout[i] = gate_word<uint64_t>(a, b, c.y >> 28);
 }
 
+
 // ---------------------------------------------------------------------------
 // depth-fused FC network + GroupSum
 // ---------------------------------------------------------------------------
+// One workgroup of 1024 threads owns a column of SPW samples (a 64- or 32-bit
+// word per feature) and keeps the whole activation column in LDS, ping-
+// ponging between two buffers of max-width words, through every layer. Per
+// layer each thread owns outputs tid, tid+1024, ...: it holds their codes in
+// registers (prefetched one layer ahead: codes do not depend on the data),
+// reads its two operand words from LDS and writes the result word. The
+// GroupSum counts come from 64x64 bit transposes + popcount per class.
 constexpr int kMaxLayers = 16;
+constexpr int kNetThreads = 1024;
 struct NetDesc {
   const uint2* codes[kMaxLayers];
   int width[kMaxLayers];
   int n_layers, in0, C, wire_r, maxw;
 };
 
-template <int IN_KIND, typename WT>
-__global__ void __launch_bounds__(1024) fc_hard_net_kernel(const void* __restrict__ xv, int B, int nw_in,
-                                                           NetDesc d, float* __restrict__ logits) {
-  constexpr int SPW = (int)sizeof(WT) * 8;  // samples per tile
-  constexpr int FPL = 64 / SPW;             // features per ballot
-  extern __shared__ __align__(16) unsigned char smem[];
-  WT* cur = reinterpret_cast<WT*>(smem);
-  WT* nxt = cur + d.maxw;
-  int* cnt = reinterpret_cast<int*>(nxt + d.maxw);  // [C][64]
-  const int tile = blockIdx.x;
-  const int b0 = tile * SPW;
+template <int MAXO>
+__device__ inline void load_codes(uint2 (&cb)[MAXO], const uint2* __restrict__ codes, int W) {
+#pragma unroll
+  for (int j = 0; j < MAXO; ++j) {
+    const int o = threadIdx.x + j * kNetThreads;
+    cb[j] = (o < W) ? codes[o] : make_uint2(0u, 0u);
+  }
+}
+
+// One layer on the LDS column: lds[nxt + o] = gate_o(lds[cur + a_o], lds[cur + b_o])
+// for this thread's outputs o = tid + j*1024. Whole rows of 1024 outputs take
+// a uniform branch; only row W/1024 tests o < W per lane.
+template <typename WT, int MAXO>
+__device__ inline void layer_step(WT* lds, int cur, int nxt, int W, const uint2 (&cb)[MAXO]) {
+  const int nfull = W / kNetThreads;
+#pragma unroll
+  for (int j = 0; j < MAXO; ++j) {
+    const int o = threadIdx.x + j * kNetThreads;
+    if (j < nfull || (j == nfull && o < W)) {
+      const uint2 c = cb[j];
+      lds[nxt + o] = gate_word<WT>(lds[cur + c.x], lds[cur + (c.y & 0x0FFFFFFFu)], c.y >> 28);
+    }
+  }
+}
+
+// wire residual (models.py:88-94): the first `keep` outputs copy the inputs
+template <typename WT, int MAXO>
+__device__ inline void keep_inputs(WT* lds, int cur, int nxt, int keep) {
+#pragma unroll
+  for (int j = 0; j < MAXO; ++j) {
+    const int o = threadIdx.x + j * kNetThreads;
+    if (o < keep) lds[nxt + o] = lds[cur + o];
+  }
+}
+
+// Per-class popcounts of a tile: cnt [C][64] must be zero on entry.
+template <typename WT>
+__device__ inline void groupsum_tile(const WT* cur, int W, int C, int* cnt, int b0, int B,
+                                     float* __restrict__ logits) {
+  constexpr int SPW = (int)sizeof(WT) * 8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
-
-  for (int i = threadIdx.x; i < d.C * 64; i += blockDim.x) cnt[i] = 0;
-
-  // ---- prologue: this tile's input column into `cur` ----
-  if constexpr (IN_KIND == 2) {
-    const uint64_t* xp = static_cast<const uint64_t*>(xv);
-    for (int i = threadIdx.x; i < d.in0; i += blockDim.x) {
-      if constexpr (SPW == 64) cur[i] = xp[(int64_t)i * nw_in + tile];
-      else cur[i] = (WT)(xp[(int64_t)i * nw_in + (tile >> 1)] >> (32 * (tile & 1)));
-    }
-  } else {
-    // Each lane owns one sample (lane % SPW) and 16 consecutive features; a
-    // ballot per feature packs the wave's samples.
-    const int s = lane % SPW;
-    const int fo = (lane / SPW) * 16;
-    const int b = b0 + s;
-    for (int f0 = wave * 16 * FPL; f0 < d.in0; f0 += nwaves * 16 * FPL) {
-      float v[16];
-      const int fb = f0 + fo;
-      if constexpr (IN_KIND == 0) {
-        const float* row = static_cast<const float*>(xv) + (int64_t)b * d.in0;
-        if (b < B && fb + 16 <= d.in0 && (d.in0 & 3) == 0) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float4 t = *reinterpret_cast<const float4*>(row + fb + 4 * q);
-            v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) v[j] = (b < B && fb + j < d.in0) ? row[fb + j] : 0.0f;
-        }
-      } else {
-        const uint8_t* row = static_cast<const uint8_t*>(xv) + (int64_t)b * d.in0;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = (b < B && fb + j < d.in0 && row[fb + j] != 0) ? 1.0f : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint64_t m = __ballot(v[j] >= 1.0f);
-        if (lane == 0) {
-          if constexpr (SPW == 64) {
-            if (f0 + j < d.in0) cur[f0 + j] = (WT)m;
-          } else {
-            if (f0 + j < d.in0) cur[f0 + j] = (WT)m;
-            if (f0 + 16 + j < d.in0) cur[f0 + 16 + j] = (WT)(m >> 32);
-          }
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- layers, ping-pong between the two LDS buffers ----
-  int cur_w = d.in0;
-  for (int l = 0; l < d.n_layers; ++l) {
-    const uint2* __restrict__ codes = d.codes[l];
-    const int W = d.width[l];
-    const int keep = (d.wire_r > 0 && cur_w == W) ? d.wire_r : 0;
-    for (int o = threadIdx.x; o < W; o += blockDim.x) {
-      WT r;
-      if (o < keep) {
-        r = cur[o];
-      } else {
-        const uint2 c = codes[o];
-        r = gate_word<WT>(cur[c.x], cur[c.y & 0x0FFFFFFFu], c.y >> 28);
-      }
-      nxt[o] = r;
-    }
-    __syncthreads();
-    WT* t = cur; cur = nxt; nxt = t;
-    cur_w = W;
-  }
-
-  // ---- GroupSum: per class, 64-word chunks -> bit transpose -> popcount ----
-  const int G = cur_w / d.C;
+  const int nwaves = kNetThreads >> 6;
+  const int G = W / C;
   const int chunks = (G + 63) / 64;
-  for (int task = wave; task < d.C * chunks; task += nwaves) {
+  for (int task = wave; task < C * chunks; task += nwaves) {
     const int c = task / chunks, j0 = (task % chunks) * 64;
     uint64_t v = (j0 + lane < G) ? (uint64_t)cur[c * G + j0 + lane] : 0ull;
     v = transpose64(v, lane);
@@ -258,10 +227,133 @@ __global__ void __launch_bounds__(1024) fc_hard_net_kernel(const void* __restric
     if (pc) atomicAdd(&cnt[c * 64 + lane], pc);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < SPW * d.C; i += blockDim.x) {
-    const int s = i / d.C, c = i % d.C;
+  for (int i = threadIdx.x; i < SPW * C; i += kNetThreads) {
+    const int s = i / C, c = i % C;
     const int b = b0 + s;
-    if (b < B) logits[(int64_t)b * d.C + c] = (float)cnt[c * 64 + s];
+    if (b < B) logits[(int64_t)b * C + c] = (float)cnt[c * 64 + s];
+  }
+}
+
+// Pre-packed input: LAYOUT 0 = [in0][nw] (reference layout), 1 = [nw][in0].
+template <int LAYOUT, typename WT, int MAXO>
+__global__ void __launch_bounds__(kNetThreads)
+fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDesc d,
+                          float* __restrict__ logits) {
+  constexpr int SPW = (int)sizeof(WT) * 8;
+  extern __shared__ __align__(16) unsigned char smem[];
+  WT* lds = reinterpret_cast<WT*>(smem);
+  int* cnt = reinterpret_cast<int*>(lds + 2 * d.maxw);
+  const int tile = blockIdx.x;
+  uint2 cb[MAXO];
+  load_codes(cb, d.codes[0], d.width[0]);
+  for (int i = threadIdx.x; i < d.C * 64; i += kNetThreads) cnt[i] = 0;
+  const int w64 = tile / (64 / SPW);
+  for (int i = threadIdx.x; i < d.in0; i += kNetThreads) {
+    const uint64_t word = LAYOUT == 0 ? xp[(int64_t)i * nw + w64] : xp[(int64_t)w64 * d.in0 + i];
+    if constexpr (SPW == 64) lds[i] = (WT)word;
+    else lds[i] = (WT)(word >> (32 * (tile & 1)));
+  }
+  __syncthreads();
+  int cur = 0, nxt = d.maxw, cur_w = d.in0;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const int W = d.width[l];
+    uint2 nb[MAXO];
+    if (l + 1 < d.n_layers) load_codes(nb, d.codes[l + 1], d.width[l + 1]);
+    layer_step<WT, MAXO>(lds, cur, nxt, W, cb);
+    if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
+    __syncthreads();
+    const int t = cur; cur = nxt; nxt = t;
+    cur_w = W;
+#pragma unroll
+    for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
+  }
+  groupsum_tile<WT>(lds + cur, cur_w, d.C, cnt, tile * SPW, B, logits);
+}
+
+// Unpacked rows [B][in0] (fp32, or uint8) with the packing fused: thread f
+// owns feature f (in0 <= 1024) and builds its 64-sample word with coalesced
+// row reads (lanes = consecutive features). Workgroups are persistent; the
+// next tile's rows stream in during the current tile's layers, one chunk of
+// samples per layer, issued after that layer's code prefetch so that waiting
+// for the codes never waits for input bytes (vector loads retire in order).
+// Addresses are clamped to valid rows/features and the bits masked after, so
+// the loads carry no per-lane branches.
+template <typename IT>
+__device__ inline bool input_bit(IT v) {
+  if constexpr (sizeof(IT) == 1) return v != 0;
+  else return v >= (IT)1;
+}
+
+template <typename IT, int MAXO, int SPL>
+__global__ void __launch_bounds__(kNetThreads)
+fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
+                        float* __restrict__ logits) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* lds = reinterpret_cast<uint64_t*>(smem);
+  int* cnt = reinterpret_cast<int*>(lds + 2 * d.maxw);
+  const int f = threadIdx.x;
+  const bool fv = f < d.in0;
+  const IT* xf = x + min(f, d.in0 - 1);
+  const int L = d.n_layers;
+  const int spl = min(SPL, (64 + L - 1) / L);  // samples streamed per layer
+
+  int tile = blockIdx.x;
+  uint64_t word = 0;
+  for (int s0 = 0; s0 < 64; s0 += 16) {  // first tile: 16 loads in flight per batch
+    IT v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = xf[(int64_t)min(tile * 64 + s0 + j, B - 1) * d.in0];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (input_bit(v[j]) && tile * 64 + s0 + j < B) word |= 1ull << (s0 + j);
+  }
+  uint2 cb[MAXO];
+  load_codes(cb, d.codes[0], d.width[0]);
+
+  for (; tile < n_tiles; tile += gridDim.x) {
+    if (fv) lds[f] = word;
+    for (int i = threadIdx.x; i < d.C * 64; i += kNetThreads) cnt[i] = 0;
+    __syncthreads();
+    const int nb0 = (tile + gridDim.x) * 64;  // first sample of the next tile
+    uint64_t nword = 0;
+    IT val[SPL];
+    int cur = 0, nxt = d.maxw, cur_w = d.in0;
+    for (int l = 0; l < L; ++l) {
+      const int W = d.width[l];
+      const int ln = (l + 1 < L) ? l + 1 : 0;  // after the last layer: layer 0 of the next tile
+      uint2 nb[MAXO];
+      load_codes(nb, d.codes[ln], d.width[ln]);
+      if (l > 0) {  // fold the chunk issued during the previous layer
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+          const int s = (l - 1) * spl + j;
+          if (j < spl && s < 64 && input_bit(val[j]) && nb0 + s < B) nword |= 1ull << s;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        const int s = l * spl + j;
+        if (j < spl && s < 64) val[j] = xf[(int64_t)min(nb0 + s, B - 1) * d.in0];
+      }
+      layer_step<uint64_t, MAXO>(lds, cur, nxt, W, cb);
+      if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
+      __syncthreads();
+      const int t = cur; cur = nxt; nxt = t;
+      cur_w = W;
+#pragma unroll
+      for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
+    }
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+      const int s = (L - 1) * spl + j;
+      if (j < spl && s < 64 && input_bit(val[j]) && nb0 + s < B) nword |= 1ull << s;
+    }
+    for (int s = L * spl; s < 64; ++s) {  // samples left over when L * spl < 64
+      if (input_bit(xf[(int64_t)min(nb0 + s, B - 1) * d.in0]) && nb0 + s < B) nword |= 1ull << s;
+    }
+    groupsum_tile<uint64_t>(lds + cur, cur_w, d.C, cnt, tile * 64, B, logits);
+    __syncthreads();
+    word = fv ? nword : 0ull;
   }
 }
 
@@ -293,14 +385,82 @@ __global__ void __launch_bounds__(256) groupsum_packed_kernel(const uint64_t* __
   }
 }
 
+
 static int net_spw(int64_t IN0, int n_layers, const int64_t* widths, int C) {
-  if (n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
+  if (!widths || n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
   int64_t maxw = IN0;
   for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
+  maxw = (maxw + 1) & ~1LL;
+  if (maxw > 16 * kNetThreads) return 0;
   const int64_t lds = device_lds_bytes();
   if (2 * maxw * 8 + (int64_t)C * 256 <= lds) return 64;
   if (2 * maxw * 4 + (int64_t)C * 256 <= lds) return 32;
   return 0;
+}
+
+static int pick_maxo(int64_t maxw) {
+  const int64_t m = cdiv(maxw, kNetThreads);
+  for (int c : {2, 4, 8, 10, 16})
+    if (m <= c) return c;
+  return 0;
+}
+
+template <typename K>
+static int set_lds(K kern, size_t lds, const char* what) {
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)lds);
+  if (e != hipSuccess) {
+    set_error("%s: LDS %zu: %s", what, lds, hipGetErrorString(e));
+    return (int)e;
+  }
+  return 0;
+}
+
+template <int LAYOUT, typename WT, int MAXO>
+static int launch_net_packed(const uint64_t* xp, int B, const NetDesc& d, size_t lds, int64_t tiles,
+                             float* logits, hipStream_t st) {
+  auto kern = fc_hard_net_packed_kernel<LAYOUT, WT, MAXO>;
+  if (int rc = set_lds(kern, lds, "fc_hard_net")) return rc;
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kNetThreads), lds, st, xp, B,
+                     (int)cdiv(B, 64), d, logits);
+  SLG_LAUNCH_CHECK("fc_hard_net");
+  return 0;
+}
+
+template <int LAYOUT, typename WT>
+static int net_packed_maxo(int maxo, const uint64_t* xp, int B, const NetDesc& d, size_t lds,
+                           int64_t tiles, float* logits, hipStream_t st) {
+  switch (maxo) {
+    case 2: return launch_net_packed<LAYOUT, WT, 2>(xp, B, d, lds, tiles, logits, st);
+    case 4: return launch_net_packed<LAYOUT, WT, 4>(xp, B, d, lds, tiles, logits, st);
+    case 8: return launch_net_packed<LAYOUT, WT, 8>(xp, B, d, lds, tiles, logits, st);
+    case 10: return launch_net_packed<LAYOUT, WT, 10>(xp, B, d, lds, tiles, logits, st);
+    default: return launch_net_packed<LAYOUT, WT, 16>(xp, B, d, lds, tiles, logits, st);
+  }
+}
+
+template <typename IT, int MAXO>
+static int launch_net_rows(const IT* x, int B, const NetDesc& d, size_t lds, float* logits,
+                           hipStream_t st) {
+  const int64_t tiles = cdiv(B, 64);
+  const int64_t grid = std::min<int64_t>(tiles, device_cus());
+  auto kern = fc_hard_net_rows_kernel<IT, MAXO, 16>;
+  if (int rc = set_lds(kern, lds, "fc_hard_net_rows")) return rc;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kNetThreads), lds, st, x, B, (int)tiles, d,
+                     logits);
+  SLG_LAUNCH_CHECK("fc_hard_net_rows");
+  return 0;
+}
+
+template <typename IT>
+static int net_rows_maxo(int maxo, const IT* x, int B, const NetDesc& d, size_t lds, float* logits,
+                         hipStream_t st) {
+  switch (maxo) {
+    case 2: return launch_net_rows<IT, 2>(x, B, d, lds, logits, st);
+    case 4: return launch_net_rows<IT, 4>(x, B, d, lds, logits, st);
+    case 8: return launch_net_rows<IT, 8>(x, B, d, lds, logits, st);
+    default: return launch_net_rows<IT, 10>(x, B, d, lds, logits, st);
+  }
 }
 
 }  // namespace slg
@@ -309,10 +469,11 @@ using namespace slg;
 
 extern "C" {
 
-int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, uint64_t* xp,
+int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, int32_t layout, uint64_t* xp,
                   slg_stream_t stream) {
-  SLG_REQUIRE(x && xp, SLG_E_ARG, "pack_bits: null pointer");
+  SLG_REQUIRE((x && xp) || B == 0, SLG_E_ARG, "pack_bits: null pointer");
   SLG_REQUIRE(dtype == 0 || dtype == 1, SLG_E_ARG, "pack_bits: dtype %d", dtype);
+  SLG_REQUIRE(layout == 0 || layout == 1, SLG_E_ARG, "pack_bits: layout %d", layout);
   SLG_REQUIRE(B >= 0 && D > 0 && B < (1LL << 31) && D < (1LL << 31) && B * D < (1LL << 46),
               SLG_E_SHAPE, "pack_bits: bad sizes");
   if (B == 0) return 0;
@@ -320,18 +481,21 @@ int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, uint64_t* 
   const int64_t dtiles = cdiv(D, 64);
   SLG_REQUIRE(nw * dtiles < (1LL << 31), SLG_E_SHAPE, "pack_bits: too many tiles");
   dim3 grid((unsigned)(nw * dtiles));
-  if (dtype == 0)
-    hipLaunchKernelGGL(pack_kernel<float>, grid, dim3(256), 0, as_stream(stream), (const float*)x,
-                       (int)B, (int)D, (int)nw, (int)dtiles, xp);
-  else
-    hipLaunchKernelGGL(pack_kernel<uint8_t>, grid, dim3(256), 0, as_stream(stream),
-                       (const uint8_t*)x, (int)B, (int)D, (int)nw, (int)dtiles, xp);
+  hipStream_t st = as_stream(stream);
+#define SLG_PACK(T, LY)                                                                    \
+  hipLaunchKernelGGL((pack_kernel<T, LY>), grid, dim3(256), 0, st, (const T*)x, (int)B, (int)D, \
+                     (int)nw, (int)dtiles, xp)
+  if (dtype == 0 && layout == 0) SLG_PACK(float, 0);
+  else if (dtype == 0) SLG_PACK(float, 1);
+  else if (layout == 0) SLG_PACK(uint8_t, 0);
+  else SLG_PACK(uint8_t, 1);
+#undef SLG_PACK
   SLG_LAUNCH_CHECK("pack_bits");
   return 0;
 }
 
 int slg_unpack_bits(const uint64_t* xp, int64_t B, int64_t D, uint8_t* out, slg_stream_t stream) {
-  SLG_REQUIRE(xp && out, SLG_E_ARG, "unpack_bits: null pointer");
+  SLG_REQUIRE((xp && out) || B == 0, SLG_E_ARG, "unpack_bits: null pointer");
   SLG_REQUIRE(B >= 0 && D > 0 && B < (1LL << 31) && D < (1LL << 31), SLG_E_SHAPE,
               "unpack_bits: bad sizes");
   if (B == 0) return 0;
@@ -358,7 +522,7 @@ int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_
 
 int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw, const uint32_t* codes,
                       int64_t OUT, uint64_t* xout, slg_stream_t stream) {
-  SLG_REQUIRE(xin && codes && xout, SLG_E_ARG, "fc_hard_layer: null pointer");
+  SLG_REQUIRE(codes && ((xin && xout) || nw == 0), SLG_E_ARG, "fc_hard_layer: null pointer");
   SLG_REQUIRE(IN > 0 && nw >= 0 && OUT > 0 && OUT * nw < (1LL << 40) && nw < (1LL << 31),
               SLG_E_SHAPE, "fc_hard_layer: bad sizes");
   if (nw == 0) return 0;
@@ -379,8 +543,8 @@ int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widt
 int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
                     const int64_t* widths, const uint32_t* const* codes, int32_t C, int64_t wire_r,
                     float* logits, slg_stream_t stream) {
-  SLG_REQUIRE(x && widths && codes && logits, SLG_E_ARG, "fc_hard_net: null pointer");
-  SLG_REQUIRE(in_kind >= 0 && in_kind <= 2, SLG_E_ARG, "fc_hard_net: in_kind %d", in_kind);
+  SLG_REQUIRE(widths && codes && ((x && logits) || B == 0), SLG_E_ARG, "fc_hard_net: null pointer");
+  SLG_REQUIRE(in_kind >= 0 && in_kind <= 3, SLG_E_ARG, "fc_hard_net: in_kind %d", in_kind);
   SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE, "fc_hard_net: %d layers", n_layers);
   SLG_REQUIRE(B >= 0 && B < (1LL << 31) && IN0 > 0 && IN0 < (1LL << 28), SLG_E_SHAPE,
               "fc_hard_net: bad sizes");
@@ -396,44 +560,33 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
               (long long)widths[n_layers - 1], C);
   const int spw = net_spw(IN0, n_layers, widths, C);
   SLG_REQUIRE(spw > 0, SLG_E_UNSUPPORTED, "fc_hard_net: widths do not fit LDS");
+  const bool rows = in_kind <= 1;
+  SLG_REQUIRE(!rows || (spw == 64 && IN0 <= kNetThreads), SLG_E_UNSUPPORTED,
+              "fc_hard_net: unpacked rows need 64-sample tiles and IN0 <= %d; pack first",
+              kNetThreads);
   if (B == 0) return 0;
   d.n_layers = n_layers; d.in0 = (int)IN0; d.C = C; d.wire_r = (int)std::max<int64_t>(0, wire_r);
   int64_t maxw = IN0;
   for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
   d.maxw = (int)((maxw + 1) & ~1LL);
+  const int maxo = pick_maxo(maxw);
+  SLG_REQUIRE(maxo > 0, SLG_E_UNSUPPORTED, "fc_hard_net: width too large");
   const size_t lds = (size_t)2 * d.maxw * (spw / 8) + (size_t)C * 256;
-  const int64_t tiles = cdiv(B, spw);
-  const int nw_in = (int)cdiv(B, 64);
   hipStream_t st = as_stream(stream);
-#define SLG_NET_LAUNCH(KIND, WT)                                                              \
-  do {                                                                                        \
-    auto kern = fc_hard_net_kernel<KIND, WT>;                                                 \
-    hipError_t e = hipFuncSetAttribute((const void*)kern,                                     \
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
-    if (e != hipSuccess) {                                                                    \
-      set_error("fc_hard_net: LDS %zu: %s", lds, hipGetErrorString(e));                       \
-      return (int)e;                                                                          \
-    }                                                                                         \
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(1024), lds, st, x, (int)B, nw_in, d,  \
-                       logits);                                                               \
-  } while (0)
-  if (spw == 64) {
-    if (in_kind == 0) SLG_NET_LAUNCH(0, uint64_t);
-    else if (in_kind == 1) SLG_NET_LAUNCH(1, uint64_t);
-    else SLG_NET_LAUNCH(2, uint64_t);
-  } else {
-    if (in_kind == 0) SLG_NET_LAUNCH(0, uint32_t);
-    else if (in_kind == 1) SLG_NET_LAUNCH(1, uint32_t);
-    else SLG_NET_LAUNCH(2, uint32_t);
-  }
-#undef SLG_NET_LAUNCH
-  SLG_LAUNCH_CHECK("fc_hard_net");
-  return 0;
+  if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
+  if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
+  const int64_t tiles = cdiv(B, spw);
+  const uint64_t* xp = (const uint64_t*)x;
+  if (in_kind == 2)
+    return spw == 64 ? net_packed_maxo<0, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
+                     : net_packed_maxo<0, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
+  return spw == 64 ? net_packed_maxo<1, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
+                   : net_packed_maxo<1, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
 }
 
 int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C, float* logits,
                         slg_stream_t stream) {
-  SLG_REQUIRE(xp && logits, SLG_E_ARG, "groupsum_packed: null pointer");
+  SLG_REQUIRE((xp && logits) || B == 0, SLG_E_ARG, "groupsum_packed: null pointer");
   SLG_REQUIRE(C > 0 && C <= 64 && W > 0 && W % C == 0 && W < (1LL << 31) && B >= 0 &&
                   B < (1LL << 31),
               SLG_E_SHAPE, "groupsum_packed: bad sizes");

@@ -18,33 +18,52 @@
 
 namespace slg {
 
+// Native vector types: one ds_read_b64 / ds_read_b128 per gather (HIP's
+// float2/float4 structs are split into scalar LDS reads by the compiler).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int V> struct vecf;
 template <> struct vecf<1> { using t = float; };
-template <> struct vecf<2> { using t = float2; };
-template <> struct vecf<4> { using t = float4; };
+template <> struct vecf<2> { using t = f32x2; };
+template <> struct vecf<4> { using t = f32x4; };
 
 __device__ inline float lanev(float v, int) { return v; }
-__device__ inline float lanev(float2 v, int i) { return i == 0 ? v.x : v.y; }
+__device__ inline float lanev(f32x2 v, int i) { return v[i]; }
+__device__ inline float lanev(f32x4 v, int i) { return v[i]; }
 __device__ inline float lanev(float4 v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 __device__ inline void fma_acc(float& acc, float w, float v) { acc = fmaf(w, v, acc); }
-__device__ inline void fma_acc(float2& acc, float w, float2 v) {
-  acc.x = fmaf(w, v.x, acc.x);
-  acc.y = fmaf(w, v.y, acc.y);
+template <typename VT>
+__device__ inline void fma_acc(VT& acc, float w, VT v) {
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(VT) / 4); ++i) acc[i] = fmaf(w, v[i], acc[i]);
 }
-__device__ inline void fma_acc(float4& acc, float w, float4 v) {
-  acc.x = fmaf(w, v.x, acc.x);
-  acc.y = fmaf(w, v.y, acc.y);
-  acc.z = fmaf(w, v.z, acc.z);
-  acc.w = fmaf(w, v.w, acc.w);
-}
-template <typename T> __device__ inline T zero_vec();
-template <> __device__ inline float zero_vec<float>() { return 0.f; }
-template <> __device__ inline float2 zero_vec<float2>() { return make_float2(0.f, 0.f); }
-template <> __device__ inline float4 zero_vec<float4>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+template <typename T> __device__ inline T zero_vec() { return (T)0.0f; }
 
 __device__ inline float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+template <int V> __device__ inline typename vecf<V>::t make_vec(const float (&e)[V]);
+template <> __device__ inline float make_vec<1>(const float (&e)[1]) { return e[0]; }
+template <> __device__ inline f32x2 make_vec<2>(const float (&e)[2]) { return f32x2{e[0], e[1]}; }
+template <> __device__ inline f32x4 make_vec<4>(const float (&e)[4]) {
+  return f32x4{e[0], e[1], e[2], e[3]};
+}
+
+// 16-byte streaming (non-temporal) load: the input rows are read once.
+__device__ inline float4 ld_stream4(const float* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// LDS slot of (input i, sample group g). Rows of G > 1 groups are G*16 bytes
+// apart, a multiple of 32 B, so random rows would hit only 64/(4G) of the
+// bank groups; XOR-ing g with the low bits of i spreads them over all.
+template <int G>
+__device__ inline int slot(int i, int g) {
+  if constexpr (G == 1) return i;
+  else return i * G + (g ^ (i & (G - 1)));
+}
 
 // Node evaluation on the two gathered operands (silogic/nodes.py:86-91 for
 // gate16, the warp_logic form of kernels/warp.py:14-31 for walsh,
@@ -62,9 +81,56 @@ __device__ inline float node_eval(float a, float b, const float4& p, float inv_t
   }
 }
 
+// Per-output parameters held in registers: 2K candidate indices, 2K weights,
+// 4 node coefficients (144 bytes for K = 8).
+template <int KM>
+struct FcParams {
+  int ia[KM], ib[KM];
+  float fa[KM], fb[KM];
+  float4 p;
+};
+
 // KC = compile-time candidate count (0 = runtime K <= 16, scalar loads).
+template <int KC, int KM>
+__device__ inline void load_params(FcParams<KM>& P, int o, int K, const int* __restrict__ ca,
+                                   const int* __restrict__ cb, int cstride,
+                                   const float* __restrict__ wa, const float* __restrict__ wb,
+                                   int wstride, const float* __restrict__ np) {
+  if constexpr (KC > 0 && (KC % 4) == 0) {
+#pragma unroll
+    for (int q = 0; q < KC / 4; ++q) {
+      const int4 a4 = *reinterpret_cast<const int4*>(ca + (int64_t)o * cstride + 4 * q);
+      const int4 b4 = *reinterpret_cast<const int4*>(cb + (int64_t)o * cstride + 4 * q);
+      const float4 u4 = *reinterpret_cast<const float4*>(wa + (int64_t)o * wstride + 4 * q);
+      const float4 v4 = *reinterpret_cast<const float4*>(wb + (int64_t)o * wstride + 4 * q);
+      P.ia[4 * q + 0] = a4.x; P.ia[4 * q + 1] = a4.y; P.ia[4 * q + 2] = a4.z; P.ia[4 * q + 3] = a4.w;
+      P.ib[4 * q + 0] = b4.x; P.ib[4 * q + 1] = b4.y; P.ib[4 * q + 2] = b4.z; P.ib[4 * q + 3] = b4.w;
+      P.fa[4 * q + 0] = u4.x; P.fa[4 * q + 1] = u4.y; P.fa[4 * q + 2] = u4.z; P.fa[4 * q + 3] = u4.w;
+      P.fb[4 * q + 0] = v4.x; P.fb[4 * q + 1] = v4.y; P.fb[4 * q + 2] = v4.z; P.fb[4 * q + 3] = v4.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      if (k < K) {
+        P.ia[k] = ca[(int64_t)o * cstride + k];
+        P.ib[k] = cb[(int64_t)o * cstride + k];
+        P.fa[k] = wa ? wa[(int64_t)o * wstride + k] : 1.0f;
+        P.fb[k] = wb ? wb[(int64_t)o * wstride + k] : 1.0f;
+      } else {
+        P.ia[k] = 0; P.ib[k] = 0; P.fa[k] = 0.f; P.fb[k] = 0.f;
+      }
+    }
+  }
+  P.p = reinterpret_cast<const float4*>(np)[o];
+}
+
+// Widest workgroup per variant: 1024 threads keeps <= 128 VGPRs per lane,
+// which fits the lean variants; the others get 512 threads and more registers.
+template <int KC, int S>
+constexpr int soft_max_threads() { return (KC == 0 || S >= 8) ? 512 : 1024; }
+
 template <int NODE, int KC, int S>
-__global__ void __launch_bounds__(1024)
+__global__ void __launch_bounds__((soft_max_threads<KC, S>()))
 fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr,
                const int* __restrict__ ca, const int* __restrict__ cb, int cstride,
                const float* __restrict__ wa, const float* __restrict__ wb, int wstride,
@@ -82,76 +148,92 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr,
   const int tile = (int)(lid / (uint32_t)n_chunks);
   const int ch = (int)(lid % (uint32_t)n_chunks);
   const int b0 = tile * S;
+  const int o_begin = ch * chunk;
+  const int o_end = min(OUT, o_begin + chunk);
 
-  // Stage S rows transposed: lds[i*G + g] = samples b0+gV .. b0+gV+V-1 of input i.
+  // First output's parameters are in flight while the tile is staged.
+  int o = o_begin + threadIdx.x;
+  FcParams<KM> P;
+  if (o < o_end) load_params<KC>(P, o, K, ca, cb, cstride, wa, wb, wstride, np);
+
+  // Stage S rows transposed: slot(i, g) holds samples b0+gV .. b0+gV+V-1 of
+  // input i. Threads load float4 runs of 4 inputs from each of the V rows of
+  // a group (4 batches in flight), then scatter them to the 4 input slots.
+  const bool vec_rows = (IN & 3) == 0;
   for (int g = 0; g < G; ++g) {
-    for (int i = threadIdx.x; i < IN; i += blockDim.x) {
-      float t[V];
+    if (vec_rows) {
+      const int n4 = IN >> 2;
+      constexpr int NBAT = V == 4 ? 2 : 4;  // float4 batches in flight per thread
+      for (int q0 = threadIdx.x; q0 < n4; q0 += NBAT * blockDim.x) {
+        float4 t[NBAT][V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const int b = b0 + g * V + v;
-        t[v] = (b < B) ? __builtin_nontemporal_load(x + (int64_t)b * IN + i) : 0.0f;
+        for (int u = 0; u < NBAT; ++u) {
+          const int q = q0 + u * blockDim.x;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const int b = b0 + g * V + v;
+            t[u][v] = (b < B && q < n4)
+                          ? ld_stream4(x + (int64_t)b * IN + 4 * q)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < NBAT; ++u) {
+          const int q = q0 + u * blockDim.x;
+          if (q < n4) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              float e[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) e[v] = lanev(t[u][v], c);
+              const int i = 4 * q + c;
+              lds[slot<G>(i, g)] = make_vec<V>(e);
+            }
+          }
+        }
       }
-      vt val;
-      if constexpr (V == 1) val = t[0];
-      else if constexpr (V == 2) val = make_float2(t[0], t[1]);
-      else val = make_float4(t[0], t[1], t[2], t[3]);
-      lds[i * G + g] = val;
+    } else {
+      for (int i = threadIdx.x; i < IN; i += blockDim.x) {
+        float e[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const int b = b0 + g * V + v;
+          e[v] = (b < B) ? __builtin_nontemporal_load(x + (int64_t)b * IN + i) : 0.0f;
+        }
+        lds[slot<G>(i, g)] = make_vec<V>(e);
+      }
     }
   }
   __syncthreads();
 
-  const int o_begin = ch * chunk;
-  const int o_end = min(OUT, o_begin + chunk);
-  for (int o = o_begin + threadIdx.x; o < o_end; o += blockDim.x) {
+  while (o < o_end) {
+    // prefetch the next output's parameters; they land while this one computes
+    const int on = o + blockDim.x;
+    FcParams<KM> Q;
+    if (on < o_end) load_params<KC>(Q, on, K, ca, cb, cstride, wa, wb, wstride, np);
     int ia[KM], ib[KM];
-    float fa[KM], fb[KM];
-    if constexpr (KC > 0 && (KC % 4) == 0) {
 #pragma unroll
-      for (int q = 0; q < KC / 4; ++q) {
-        const int4 a4 = *reinterpret_cast<const int4*>(ca + (int64_t)o * cstride + 4 * q);
-        const int4 b4 = *reinterpret_cast<const int4*>(cb + (int64_t)o * cstride + 4 * q);
-        const float4 u4 = *reinterpret_cast<const float4*>(wa + (int64_t)o * wstride + 4 * q);
-        const float4 v4 = *reinterpret_cast<const float4*>(wb + (int64_t)o * wstride + 4 * q);
-        ia[4 * q + 0] = a4.x; ia[4 * q + 1] = a4.y; ia[4 * q + 2] = a4.z; ia[4 * q + 3] = a4.w;
-        ib[4 * q + 0] = b4.x; ib[4 * q + 1] = b4.y; ib[4 * q + 2] = b4.z; ib[4 * q + 3] = b4.w;
-        fa[4 * q + 0] = u4.x; fa[4 * q + 1] = u4.y; fa[4 * q + 2] = u4.z; fa[4 * q + 3] = u4.w;
-        fb[4 * q + 0] = v4.x; fb[4 * q + 1] = v4.y; fb[4 * q + 2] = v4.z; fb[4 * q + 3] = v4.w;
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < KM; ++k) {
-        if (k < K) {
-          ia[k] = ca[(int64_t)o * cstride + k];
-          ib[k] = cb[(int64_t)o * cstride + k];
-          fa[k] = wa ? wa[(int64_t)o * wstride + k] : 1.0f;
-          fb[k] = wb ? wb[(int64_t)o * wstride + k] : 1.0f;
-        } else {
-          ia[k] = 0; ib[k] = 0; fa[k] = 0.f; fb[k] = 0.f;
-        }
-      }
+    for (int k = 0; k < KM; ++k) {  // clamp into the staged rows
+      ia[k] = min(max(P.ia[k], 0), IN - 1);
+      ib[k] = min(max(P.ib[k], 0), IN - 1);
     }
-#pragma unroll
-    for (int k = 0; k < KM; ++k) {  // clamp into the staged rows, scale to slots
-      ia[k] = min(max(ia[k], 0), IN - 1) * G;
-      ib[k] = min(max(ib[k], 0), IN - 1) * G;
-    }
-    const float4 p = reinterpret_cast<const float4*>(np)[o];
     for (int g = 0; g < G; ++g) {
       vt A = zero_vec<vt>(), Bv = zero_vec<vt>();
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
         if (KC > 0 || k < K) {
-          fma_acc(A, fa[k], lds[ia[k] + g]);
-          fma_acc(Bv, fb[k], lds[ib[k] + g]);
+          fma_acc(A, P.fa[k], lds[slot<G>(ia[k], g)]);
+          fma_acc(Bv, P.fb[k], lds[slot<G>(ib[k], g)]);
         }
       }
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const int b = b0 + g * V + v;
-        if (b < B) y[(int64_t)b * OUT + o] = node_eval<NODE>(lanev(A, v), lanev(Bv, v), p, inv_tau);
+        if (b < B) y[(int64_t)b * OUT + o] = node_eval<NODE>(lanev(A, v), lanev(Bv, v), P.p, inv_tau);
       }
     }
+    P = Q;
+    o = on;
   }
 }
 
@@ -177,6 +259,7 @@ static int launch_soft_s(const SoftArgs& a, hipStream_t st) {
   const int64_t grid = tiles * n_chunks;
   SLG_REQUIRE(grid < (1LL << 31), SLG_E_SHAPE, "fc_soft: grid too large");
   auto kern = fc_soft_kernel<NODE, KC, S>;
+  const int threads = std::min(a.threads, soft_max_threads<KC, S>());
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -185,7 +268,7 @@ static int launch_soft_s(const SoftArgs& a, hipStream_t st) {
       return (int)e;
     }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(a.threads), lds, st, a.x, (int)a.B,
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), lds, st, a.x, (int)a.B,
                      (int)a.IN, (int)a.OUT, a.K, a.ca, a.cb, a.cstride, a.wa, a.wb, a.wstride,
                      a.np, a.inv_tau, a.y, (int)n_chunks, (int)chunk);
   SLG_LAUNCH_CHECK("fc_soft");
@@ -218,16 +301,29 @@ static int launch_soft_node(const SoftArgs& a, hipStream_t st) {
   return launch_soft_k<NODE, 0>(a, st);
 }
 
+// Samples per workgroup tile and workgroup size, from a sweep on MI355X
+// (B = 4096, OUT = 10000-16380, K = 8): IN = 784 -> 4 samples / 256 threads,
+// IN = 4096 -> 8 / 512, IN = 10000 -> 4 / 1024, IN = 16380 -> 2 / 1024. The
+// tile takes the largest power of two <= 8 whose rows fit 160 KB of LDS (4 for
+// narrow inputs, where more, smaller workgroups per CU win).
 static int pick_tile(int64_t IN, int requested) {
   if (requested > 0) return requested;
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
-  for (int s : {16, 8, 4, 2, 1})
-    if (IN * s * 4 <= cap && (s <= 4 || IN * s * 4 <= cap / 2)) return s;
+  if (IN <= 1280) return 4;
+  for (int s : {8, 4, 2, 1})
+    if (IN * s * 4 <= cap) return s;
   return 0;
 }
 
+static int pick_threads(int64_t IN, int S, int requested) {
+  if (requested > 0) return requested;
+  const int64_t lds = IN * S * 4;
+  if (lds <= 40 * 1024) return 256;
+  return 1024;  // capped per variant by soft_max_threads
+}
+
 static int fc_soft_dispatch(SoftArgs a, int node_kind, hipStream_t st) {
-  SLG_REQUIRE(a.x && a.ca && a.cb && a.np && a.y, SLG_E_ARG, "fc_soft: null pointer");
+  SLG_REQUIRE(a.ca && a.cb && a.np && ((a.x && a.y) || a.B == 0), SLG_E_ARG, "fc_soft: null pointer");
   SLG_REQUIRE(a.B >= 0 && a.IN > 0 && a.OUT > 0, SLG_E_SHAPE, "fc_soft: bad sizes B=%lld IN=%lld OUT=%lld",
               (long long)a.B, (long long)a.IN, (long long)a.OUT);
   SLG_REQUIRE(a.K >= 1 && a.K <= 16, SLG_E_SHAPE, "fc_soft: K=%d outside 1..16", a.K);
@@ -238,7 +334,7 @@ static int fc_soft_dispatch(SoftArgs a, int node_kind, hipStream_t st) {
   a.S = pick_tile(a.IN, a.S);
   SLG_REQUIRE(a.S > 0 && (int64_t)a.IN * a.S * 4 <= device_lds_bytes(), SLG_E_SHAPE,
               "fc_soft: IN=%lld does not fit LDS", (long long)a.IN);
-  if (a.threads <= 0) a.threads = ((int64_t)a.IN * a.S * 4 > 80 * 1024) ? 1024 : 512;
+  a.threads = pick_threads(a.IN, a.S, a.threads);
   SLG_REQUIRE(a.threads % 64 == 0 && a.threads <= 1024, SLG_E_ARG, "fc_soft: threads=%d", a.threads);
   switch (node_kind) {
     case SLG_NODE_GATE16: return launch_soft_node<SLG_NODE_GATE16>(a, st);
@@ -303,28 +399,22 @@ __global__ void fc_soft_prep_kernel(const float* __restrict__ conn, int OUT, int
 // GroupSum (silogic/heads.py:16-45): one workgroup per sample.
 // ---------------------------------------------------------------------------
 template <typename T, bool STE>
-__global__ void groupsum_kernel(const T* __restrict__ x, int W, int C, float tau,
-                                float* __restrict__ logits) {
-  const int b = blockIdx.x;
+__global__ void __launch_bounds__(256) groupsum_kernel(const T* __restrict__ x, int B, int W, int C,
+                                                       float tau, float* __restrict__ logits) {
+  // one wave per (sample, class): coalesced reads of the class block, wave sum
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (task >= B * C) return;
+  const int b = task / C, c = task % C;
   const int G = W / C;
-  __shared__ float red[1024 / 64];
-  const T* row = x + (int64_t)b * W;
-  for (int c = 0; c < C; ++c) {
-    float part = 0.f;
-    for (int j = threadIdx.x; j < G; j += blockDim.x) {
-      const float v = (float)row[c * G + j];
-      part += STE ? (v > 0.5f ? 1.0f : 0.0f) : v;
-    }
-    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float s = 0.f;
-      for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += red[i];
-      logits[(int64_t)b * C + c] = s / tau;
-    }
-    __syncthreads();
+  const T* row = x + (int64_t)b * W + (int64_t)c * G;
+  float part = 0.f;
+  for (int j = lane; j < G; j += 64) {
+    const float v = (float)row[j];
+    part += STE ? (v > 0.5f ? 1.0f : 0.0f) : v;
   }
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+  if (lane == 0) logits[task] = part / tau;
 }
 
 }  // namespace slg
@@ -375,32 +465,34 @@ int slg_fc_soft_prep(const float* conn, int64_t OUT, int32_t K, int32_t node_kin
 
 int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau, int32_t ste,
                       float* logits, slg_stream_t stream) {
-  SLG_REQUIRE(x && logits, SLG_E_ARG, "groupsum_soft: null pointer");
-  SLG_REQUIRE(B >= 0 && B < (1LL << 31) && C > 0 && W > 0 && W % C == 0 && W < (1LL << 31),
+  SLG_REQUIRE((x && logits) || B == 0, SLG_E_ARG, "groupsum_soft: null pointer");
+  SLG_REQUIRE(B >= 0 && B * C < (1LL << 31) && C > 0 && W > 0 && W % C == 0 && W < (1LL << 31),
               SLG_E_SHAPE, "groupsum_soft: W=%lld not divisible by C=%d", (long long)W, C);
   if (B == 0) return 0;
+  const unsigned grid = (unsigned)cdiv(B * C, 4);
   if (ste)
-    hipLaunchKernelGGL((groupsum_kernel<float, true>), dim3((unsigned)B), dim3(256), 0,
-                       as_stream(stream), x, (int)W, C, tau, logits);
+    hipLaunchKernelGGL((groupsum_kernel<float, true>), dim3(grid), dim3(256), 0, as_stream(stream), x,
+                       (int)B, (int)W, C, tau, logits);
   else
-    hipLaunchKernelGGL((groupsum_kernel<float, false>), dim3((unsigned)B), dim3(256), 0,
-                       as_stream(stream), x, (int)W, C, tau, logits);
+    hipLaunchKernelGGL((groupsum_kernel<float, false>), dim3(grid), dim3(256), 0, as_stream(stream),
+                       x, (int)B, (int)W, C, tau, logits);
   SLG_LAUNCH_CHECK("groupsum_soft");
   return 0;
 }
 
 int slg_groupsum_hard(const void* x, int32_t dtype, int64_t B, int64_t W, int32_t C,
                       float* logits, slg_stream_t stream) {
-  SLG_REQUIRE(x && logits, SLG_E_ARG, "groupsum_hard: null pointer");
-  SLG_REQUIRE(B >= 0 && B < (1LL << 31) && C > 0 && W > 0 && W % C == 0 && W < (1LL << 31),
+  SLG_REQUIRE((x && logits) || B == 0, SLG_E_ARG, "groupsum_hard: null pointer");
+  SLG_REQUIRE(B >= 0 && B * C < (1LL << 31) && C > 0 && W > 0 && W % C == 0 && W < (1LL << 31),
               SLG_E_SHAPE, "groupsum_hard: W=%lld not divisible by C=%d", (long long)W, C);
   if (B == 0) return 0;
+  const unsigned grid = (unsigned)cdiv(B * C, 4);
   if (dtype == 1)
-    hipLaunchKernelGGL((groupsum_kernel<uint8_t, false>), dim3((unsigned)B), dim3(256), 0,
-                       as_stream(stream), (const uint8_t*)x, (int)W, C, 1.0f, logits);
+    hipLaunchKernelGGL((groupsum_kernel<uint8_t, false>), dim3(grid), dim3(256), 0,
+                       as_stream(stream), (const uint8_t*)x, (int)B, (int)W, C, 1.0f, logits);
   else
-    hipLaunchKernelGGL((groupsum_kernel<float, false>), dim3((unsigned)B), dim3(256), 0,
-                       as_stream(stream), (const float*)x, (int)W, C, 1.0f, logits);
+    hipLaunchKernelGGL((groupsum_kernel<float, false>), dim3(grid), dim3(256), 0,
+                       as_stream(stream), (const float*)x, (int)B, (int)W, C, 1.0f, logits);
   SLG_LAUNCH_CHECK("groupsum_hard");
   return 0;
 }

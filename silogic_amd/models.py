@@ -25,12 +25,20 @@ def _per_layer(v, i):
 
 
 def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
-    """Run arity-2 FC layers as a packed circuit and return class counts."""
+    """Run arity-2 FC layers as a packed circuit and return class counts.
+
+    ``in_kind`` is ROWS_F32 / ROWS_U8 for ``[B, in_dim]`` inputs or PACKED for
+    ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
+    fused into it when the input is at most 1024 features wide; otherwise one
+    packed kernel per layer."""
     codes = [layer.hard_codes() for layer in layers]
     widths = [c.shape[0] for c in codes]
-    if ops.fc_hard_net_supported(in_dim, widths, C):
+    spw = ops.fc_hard_net_supported(in_dim, widths, C)
+    if spw:
+        if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
+            x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
-    xp = x if in_kind == 2 else ops.pack_bits(x)
+    xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
     for c in codes:
         yp = ops.fc_hard_layer(xp, c)
         if wire_r and yp.shape[0] == xp.shape[0]:
@@ -181,7 +189,7 @@ class LogicConvNet(nn.Module):
             Ho, Wo = conv._hw_out(H, W)
             C, H, W = conv.n, Ho // 2, Wo // 2
         xp = xp.view(-1, xp.shape[-1])                        # flatten (n, h, w)
-        return _hard_fc_stack(self.head_layers, xp, 2, B, xp.shape[0],
+        return _hard_fc_stack(self.head_layers, xp, ops.PACKED, B, xp.shape[0],
                               self.head.num_classes, 0)
 
     def gate_count(self, in_hw):

@@ -219,13 +219,15 @@ def _in_kind(x):
     return _as_f32(x), 0
 
 
-def pack_bits(x):
-    """``[B, D]`` {0,1} -> packed ``[D, ceil(B/64)]`` (int64 storage of uint64)."""
+def pack_bits(x, word_major=False):
+    """``[B, D]`` {0,1} -> packed ``[D, ceil(B/64)]`` (int64 storage of uint64),
+    or ``[ceil(B/64), D]`` with ``word_major``."""
     require_gpu(x)
     x, kind = _in_kind(x.reshape(x.shape[0], -1))
     B, D = x.shape
-    xp = torch.empty((D, n_words(B)), device=x.device, dtype=torch.int64)
-    _lib.call("slg_pack_bits", _p(x), kind, B, D, _p(xp), _stream(x))
+    shape = (n_words(B), D) if word_major else (D, n_words(B))
+    xp = torch.empty(shape, device=x.device, dtype=torch.int64)
+    _lib.call("slg_pack_bits", _p(x), kind, B, D, int(word_major), _p(xp), _stream(x))
     return xp
 
 
@@ -268,8 +270,14 @@ def fc_hard_net_supported(in_dim, widths, C):
     return _lib.lib().slg_fc_hard_net_supported(in_dim, len(widths), arr, C)
 
 
+ROWS_F32, ROWS_U8, PACKED, PACKED_WORD_MAJOR = 0, 1, 2, 3
+
+
 def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
-    """Depth-fused packed FC network + GroupSum -> logits ``[B, C]``."""
+    """Depth-fused packed FC network + GroupSum -> logits ``[B, C]``.
+
+    ``in_kind``: ROWS_F32 / ROWS_U8 ([B, in_dim], packed inside the kernel),
+    PACKED ([in_dim, nw]) or PACKED_WORD_MAJOR ([nw, in_dim])."""
     require_gpu(x, *codes)
     widths = [c.shape[0] for c in codes]
     w_arr = (ctypes.c_int64 * len(widths))(*widths)

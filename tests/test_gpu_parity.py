@@ -238,13 +238,37 @@ def test_fused_net_equals_layerwise_path_and_wide_32bit_tiles():
         x = random_bits(333, 200)
         xd = x.to(DEV)
         codes = [l.hard_codes() for l in model.layers]
-        fused = ops.fc_hard_net(xd, 0, 333, 200, codes, 10)
+        outs = []
+        if width == 1000:   # unpacked rows, packing fused (fp32 and uint8)
+            outs.append(ops.fc_hard_net(xd, ops.ROWS_F32, 333, 200, codes, 10))
+            outs.append(ops.fc_hard_net(xd.to(torch.uint8), ops.ROWS_U8, 333, 200, codes, 10))
+        outs.append(ops.fc_hard_net(ops.pack_bits(xd), ops.PACKED, 333, 200, codes, 10))
+        outs.append(ops.fc_hard_net(ops.pack_bits(xd, word_major=True), ops.PACKED_WORD_MAJOR,
+                                    333, 200, codes, 10))
         xp = ops.pack_bits(xd)
         for c in codes:
             xp = ops.fc_hard_layer(xp, c)
         layerwise = ops.groupsum_packed(xp, 333, 10)
-        assert torch.equal(fused.cpu(), layerwise.cpu())
-        assert torch.equal(fused.cpu(), torch_ref.forward_hard(spec, sd, x))
+        ref = torch_ref.forward_hard(spec, sd, x)
+        assert torch.equal(layerwise.cpu(), ref)
+        for o in outs:
+            assert torch.equal(o.cpu(), ref)
+
+
+@pytest.mark.parametrize("depth", [1, 2, 3, 6])
+def test_fused_rows_kernel_many_tiles(depth):
+    """More 64-sample tiles than CUs (persistent loop, streamed next-tile input)
+    and a ragged last tile; depths below 4 use the leftover-sample tail."""
+    spec = ("LogicNet", dict(in_dim=100, width=60, depth=depth, k=8))
+    model = build_product(spec)
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV).eval()
+    B = 64 * 600 + 37
+    x = random_bits(B, 100)
+    out = model.forward_hard(x.to(DEV)).cpu()
+    ref = torch_ref.forward_hard(spec, sd, x)
+    assert torch.equal(out, ref)
+    assert torch.equal(model.forward_hard(x.to(torch.uint8).to(DEV)).cpu(), ref)
 
 
 def test_wire_residual_hard_and_soft():
