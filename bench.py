@@ -117,13 +117,13 @@ def kernels_only(reps=3):
     model = build_config(2, sl).eval().to(dev)
     xh = config_inputs(2, 65536).to(dev)
     with torch.no_grad():
-        codes = [l.hard_codes() for l in model.layers]
+        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers])
         for _ in range(reps):
             ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
         x_mid = torch.rand(4096, 10000, device=dev)
-        cand, w, npar = model.layers[1].soft_params(False)
+        rec = ops.fc_soft_records([model.layers[1].record_spec()], 8)[0]
         for _ in range(reps):
-            ops.fc_soft(x_mid, cand, w, npar, ops.GATE16)
+            ops.fc_soft_rec(x_mid, rec, 10000, 8, ops.GATE16)
     torch.cuda.synchronize()
     log("kernels-only done")
 
@@ -195,15 +195,15 @@ def main():
 
     # ---- dominant kernels alone, HIP events on the launch stream ----
     with torch.no_grad():
-        codes = [l.hard_codes() for l in model.layers]
+        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers])
         reps = 20
         fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, 784, codes, 10)  # noqa: E731
         fn_net()
         k_hard = _events_ms(fn_net, reps) / 1e3
         L = model.layers[1]
         x_mid = torch.rand(B_soft, 10000, device=dev)
-        cand, w, npar = L.soft_params(False)
-        fn_soft = lambda: ops.fc_soft(x_mid, cand, w, npar, ops.GATE16)       # noqa: E731
+        rec = ops.fc_soft_records([L.record_spec()], 8)[0]
+        fn_soft = lambda: ops.fc_soft_rec(x_mid, rec, 10000, 8, ops.GATE16)          # noqa: E731
         fn_soft()
         k_soft = _events_ms(fn_soft, reps) / 1e3
     hard_bytes = B_hard * 784 * 4 + sum(c.numel() * 4 for c in codes) + B_hard * 10 * 4

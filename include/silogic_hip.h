@@ -97,6 +97,53 @@ int slg_fc_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
 int slg_fc_soft_prep(const float* conn, int64_t OUT, int32_t K, int32_t node_kind,
                      const float* raw, float* w, float* node_param, slg_stream_t stream);
 
+/* The soft parameters of n_layers (<= 16) FC layers in one launch, as one
+ * record per output: 4(K+1) 32-bit words idx_a[K], idx_b[K] (int32,
+ * clamped into [0, in_dim)), w_a[K], w_b[K] (fp32 softmax over K),
+ * node_param[4] (fp32, as slg_fc_soft_prep), stored as K+1 quads of 4 words
+ * in a chunk-major layout: quad q of output o at quad index
+ * ((o / 64) * (K+1) + q) * 64 + o % 64. rec[l] holds ceil(out_dim/64)*64
+ * records (the padding repeats the last output). The inputs of layer l are
+ * cand[l] [out_dim,2,K] int32, conn[l] [out_dim,2,K] (NULL = fixed wiring)
+ * and raw[l] as in slg_fc_soft_prep; order (may be NULL, or hold NULLs) gives
+ * per layer a gather order [out_dim,2,K] uint8 from slg_fc_soft_schedule:
+ * step t of slot s reads candidate order[o][s][t]. Host arrays of device
+ * pointers, as slg_fc_hard_net's codes. Replaces, for a whole LogicNet, the
+ * per-forward torch ops of TopKConnectome.weights (connectomes.py:114-119)
+ * and the node coefficients (nodes.py:82-84, 138-143, 178). */
+int slg_fc_soft_records(int32_t n_layers, const int32_t* const* cand, const float* const* conn,
+                        const float* const* raw, const int64_t* in_dim, const int64_t* out_dim,
+                        int32_t K, const int32_t* node_kind, const uint8_t* const* order,
+                        float* const* rec, slg_stream_t stream);
+
+/* Bank-aware gather order for one layer's candidates cand [OUT,2,K] int32
+ * (K <= 16) read from an IN-wide input: order [OUT,2,K] uint8, a
+ * permutation of 0..K-1 per (output, slot) that spreads the LDS reads of
+ * each step over distinct banks. Depends only on cand and IN, so a caller
+ * computes it once per candidate table. No counterpart in the reference
+ * (its kernels read candidates in index order); results change only by the
+ * fp32 summation order. */
+int slg_fc_soft_schedule(const int32_t* cand, int64_t OUT, int32_t K, int64_t IN, uint8_t* order,
+                         slg_stream_t stream);
+
+/* slg_fc_soft_fwd on records from slg_fc_soft_records (the forward of
+ * LogicLayer, layers.py:107-123, without gradients). */
+int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                            const float* rec, int32_t node_kind, float inv_tau, float* out,
+                            int32_t tile_samples, int32_t threads, slg_stream_t stream);
+
+/* The last LogicLayer of a LogicNet fused with its GroupSum head with the
+ * feature STE (layers.py:107-123 then heads.py:34-39, as models.py:96-97
+ * runs them): logits [B,C] = per-class count of (y > 0.5) / tau; the layer
+ * output y is not written. Exact: the counts are integers. Returns
+ * SLG_E_UNSUPPORTED when slg_fc_soft_groupsum_supported says 0. */
+int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                             const float* rec, int32_t node_kind, float inv_tau, int32_t C,
+                             float tau, float* logits, slg_stream_t stream);
+/* 1 if slg_fc_soft_fwd_groupsum runs this shape (one workgroup holds every
+ * output of its sample tile), else 0. */
+int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C);
+
 /* GroupSum.forward (silogic/heads.py:34-39): x [B,W] -> logits [B,C] =
  * sum over class block of (ste ? (x > 0.5) : x), divided by tau. */
 int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau,
@@ -140,6 +187,14 @@ int slg_unpack_bits(const uint64_t* xp, int64_t B, int64_t D, uint8_t* out,
 int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_t K,
                      int64_t IN, int32_t node_kind, const float* raw, uint32_t* codes,
                      slg_stream_t stream);
+
+/* slg_fc_hard_prep for n_layers (<= 16) layers in one launch: host arrays
+ * of length n_layers with the arguments of each layer (conn[l] NULL = fixed
+ * wiring, K[l] = 1). */
+int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const float* const* conn,
+                         const float* const* raw, const int64_t* in_dim, const int64_t* out_dim,
+                         const int32_t* K, const int32_t* node_kind, uint32_t* const* codes,
+                         slg_stream_t stream);
 
 /* One packed FC layer (replaces BitpackedFCLayer.forward,
  * packed_layer.py:85-116, and LogicLayer.forward_hard, layers.py:131-135):

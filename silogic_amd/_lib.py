@@ -23,12 +23,20 @@ SIGNATURES = {
     "slg_fc_soft_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _F32, _P, _I32,
                                   _I32, _P]),
     "slg_fc_soft_prep": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "slg_fc_soft_records": (C.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
+    "slg_fc_soft_schedule": (C.c_int, [_P, _I64, _I32, _I64, _P, _P]),
+    "slg_fc_soft_fwd_records": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I32, _F32, _P, _I32,
+                                          _I32, _P]),
+    "slg_fc_soft_fwd_groupsum": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I32, _F32, _I32,
+                                           _F32, _P, _P]),
+    "slg_fc_soft_groupsum_supported": (C.c_int, [_I64, _I64, _I64, _I32]),
     "slg_groupsum_soft": (C.c_int, [_P, _I64, _I64, _I32, _F32, _I32, _P, _P]),
     "slg_groupsum_hard": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_orpool": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P]),
     "slg_pack_bits": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_unpack_bits": (C.c_int, [_P, _I64, _I64, _P, _P]),
     "slg_fc_hard_prep": (C.c_int, [_P, _P, _I64, _I32, _I64, _I32, _P, _P, _P]),
+    "slg_fc_hard_prep_net": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "slg_fc_hard_layer": (C.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "slg_fc_hard_net": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _I32, _I64, _P, _P]),
     "slg_fc_hard_net_supported": (C.c_int, [_I64, _I32, _P, _I32]),
@@ -71,7 +79,11 @@ def lib():
             _load_error = str(e)
             raise ImportError("silogic_amd HIP library failed to load: " + _load_error) from e
         for name, (res, args) in SIGNATURES.items():
-            fn = getattr(h, name)
+            try:
+                fn = getattr(h, name)
+            except AttributeError as e:
+                _load_error = f"{path} lacks {name}: rebuild it with __graft_entry__.build()"
+                raise ImportError("silogic_amd HIP library is stale: " + _load_error) from e
             fn.restype = res
             fn.argtypes = args
         _lib = h

@@ -101,11 +101,10 @@ __device__ inline int argmax_first(const float* p, int n) {
   return bi;
 }
 
-__global__ void fc_hard_prep_kernel(const int32_t* __restrict__ cand, const float* __restrict__ conn,
-                                    int OUT, int K, int IN, int node, const float* __restrict__ raw,
-                                    uint2* __restrict__ codes) {
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= OUT) return;
+// Hard code of output o: wiring by argmax over the K candidates (first index
+// on ties), truth table of the node, indices clamped into [0, IN).
+__device__ inline uint2 hard_code(const int32_t* __restrict__ cand, const float* __restrict__ conn,
+                                  int o, int K, int IN, int node, const float* __restrict__ raw) {
   int idx[2];
   for (int s = 0; s < 2; ++s) {
     if (conn) {  // TopK: cand[o, s, argmax conn[o, s, :]] (connectomes.py:129-132)
@@ -138,7 +137,39 @@ __global__ void fc_hard_prep_kernel(const int32_t* __restrict__ cand, const floa
       if (raw[o * 4 + a + 2 * b] > 0.0f) tt |= 1u << g;
     }
   }
-  codes[o] = make_uint2((uint32_t)idx[0], (uint32_t)idx[1] | (tt << 28));
+  return make_uint2((uint32_t)idx[0], (uint32_t)idx[1] | (tt << 28));
+}
+
+__global__ void fc_hard_prep_kernel(const int32_t* __restrict__ cand, const float* __restrict__ conn,
+                                    int OUT, int K, int IN, int node, const float* __restrict__ raw,
+                                    uint2* __restrict__ codes) {
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= OUT) return;
+  codes[o] = hard_code(cand, conn, o, K, IN, node, raw);
+}
+
+// Codes of several layers in one launch; each workgroup serves one layer.
+constexpr int kMaxPrepLayers = 16;
+struct HardPrepLayer {
+  const int32_t* cand;
+  const float* conn;
+  const float* raw;
+  uint2* codes;
+  int in_dim, out_dim, K, node;
+};
+struct HardPrepNet {
+  HardPrepLayer L[kMaxPrepLayers];
+  int blk_start[kMaxPrepLayers + 1];
+  int n;
+};
+
+__global__ void __launch_bounds__(256) fc_hard_prep_net_kernel(HardPrepNet net) {
+  int l = 0;
+  while (l + 1 < net.n && (int)blockIdx.x >= net.blk_start[l + 1]) ++l;
+  const HardPrepLayer& L = net.L[l];
+  const int o = ((int)blockIdx.x - net.blk_start[l]) * blockDim.x + threadIdx.x;
+  if (o >= L.out_dim) return;
+  L.codes[o] = hard_code(L.cand, L.conn, o, L.K, L.in_dim, L.node, L.raw);
 }
 
 // ---------------------------------------------------------------------------
@@ -517,6 +548,38 @@ int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_
                      as_stream(stream), cand, conn, (int)OUT, K, (int)IN, node_kind, raw,
                      reinterpret_cast<uint2*>(codes));
   SLG_LAUNCH_CHECK("fc_hard_prep");
+  return 0;
+}
+
+int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const float* const* conn,
+                         const float* const* raw, const int64_t* in_dim, const int64_t* out_dim,
+                         const int32_t* K, const int32_t* node_kind, uint32_t* const* codes,
+                         slg_stream_t stream) {
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxPrepLayers, SLG_E_SHAPE,
+              "fc_hard_prep_net: n_layers=%d outside 1..%d", n_layers, kMaxPrepLayers);
+  SLG_REQUIRE(cand && conn && raw && in_dim && out_dim && K && node_kind && codes, SLG_E_ARG,
+              "fc_hard_prep_net: null array");
+  HardPrepNet net{};
+  net.n = n_layers;
+  const int th = 256;
+  int64_t blocks = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(cand[l] && raw[l] && codes[l], SLG_E_ARG, "fc_hard_prep_net: null pointer, layer %d", l);
+    SLG_REQUIRE(out_dim[l] > 0 && out_dim[l] < (1LL << 28) && in_dim[l] > 0 &&
+                    in_dim[l] <= (1LL << 28) && K[l] >= 1 && K[l] <= 64, SLG_E_SHAPE,
+                "fc_hard_prep_net: bad sizes, layer %d", l);
+    SLG_REQUIRE(node_kind[l] >= 0 && node_kind[l] <= 2, SLG_E_ARG,
+                "fc_hard_prep_net: node_kind %d", node_kind[l]);
+    SLG_REQUIRE(((uintptr_t)codes[l] % 8) == 0, SLG_E_ARG, "fc_hard_prep_net: codes alignment");
+    net.L[l] = HardPrepLayer{cand[l], conn[l], raw[l], reinterpret_cast<uint2*>(codes[l]),
+                             (int)in_dim[l], (int)out_dim[l], K[l], node_kind[l]};
+    net.blk_start[l] = (int)blocks;
+    blocks += cdiv(out_dim[l], th);
+  }
+  net.blk_start[n_layers] = (int)blocks;
+  hipLaunchKernelGGL(fc_hard_prep_net_kernel, dim3((unsigned)blocks), dim3(th), 0,
+                     as_stream(stream), net);
+  SLG_LAUNCH_CHECK("fc_hard_prep_net");
   return 0;
 }
 

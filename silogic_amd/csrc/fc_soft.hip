@@ -3,15 +3,19 @@
 //
 // Design (one layer, x [B,IN] -> y [B,OUT]):
 //   * A workgroup owns a tile of S consecutive samples and a chunk of
-//     outputs. It stages the S input rows in LDS transposed and
-//     sample-interleaved, lds[i][g] = float4 of samples 4g..4g+3 of input i
-//     (S = 1, 2 use float / float2), so one ds_read_b128 per candidate
-//     fetches 4 samples. Random-address b128 reads measured on gfx950 reach
-//     ~80 B/clk/CU, b64 ~68, b32 ~33: wider is better for random gathers.
-//   * Lanes walk outputs. Each lane holds its output's 2K candidate indices,
-//     2K weights and 4 node coefficients in registers and reuses them for all
-//     S samples, so parameter traffic is 144/S bytes per sample-output.
-//   * Output stores are coalesced along the output dimension.
+//     outputs. It stages the S input rows in LDS transposed, group-major:
+//     lds[g][i] = the V = min(S,4) samples 4g..4g+V-1 of input i, so one
+//     ds_read_b128 per candidate fetches 4 samples. Random-address b128
+//     reads are the widest LDS gather gfx950 has; b64 and b32 move fewer
+//     bytes per LDS cycle.
+//   * Lanes walk outputs. Each lane loads its output's 2K candidate indices,
+//     2K weights and 4 node coefficients (144 B at K = 8) with 16-byte loads
+//     and reuses them for all S samples. With the per-output record layout
+//     (slg_fc_soft_records) the 144 B are contiguous.
+//   * Output stores are coalesced along the output dimension. The fused
+//     GroupSum variant stores nothing per output: it counts (y > 0.5) per
+//     class with a wave ballot + popcount into LDS counters and writes the
+//     [S, C] logits of its tile at the end.
 //   * The tile/chunk index is remapped so chunks of one tile run on the same
 //     XCD and share its L2 copy of the input rows.
 #include "slg_common.h"
@@ -22,6 +26,7 @@ namespace slg {
 // float2/float4 structs are split into scalar LDS reads by the compiler).
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 template <int V> struct vecf;
 template <> struct vecf<1> { using t = float; };
 template <> struct vecf<2> { using t = f32x2; };
@@ -56,15 +61,6 @@ __device__ inline float4 ld_stream4(const float* p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
-// LDS slot of (input i, sample group g). Rows of G > 1 groups are G*16 bytes
-// apart, a multiple of 32 B, so random rows would hit only 64/(4G) of the
-// bank groups; XOR-ing g with the low bits of i spreads them over all.
-template <int G>
-__device__ inline int slot(int i, int g) {
-  if constexpr (G == 1) return i;
-  else return i * G + (g ^ (i & (G - 1)));
-}
-
 // Node evaluation on the two gathered operands (silogic/nodes.py:86-91 for
 // gate16, the warp_logic form of kernels/warp.py:14-31 for walsh,
 // nodes.py:174-178 with n = 2 for multilinear).
@@ -81,8 +77,21 @@ __device__ inline float node_eval(float a, float b, const float4& p, float inv_t
   }
 }
 
+// Where one layer's parameters live: separate arrays (cand [OUT,2,K], w
+// [OUT,2,K], node_param [OUT,4]) or one record per output (strides in 32-bit
+// words; see slg_fc_soft_records).
+struct ParamView {
+  const int* ca;
+  const int* cb;
+  const float* wa;
+  const float* wb;
+  const float* np;
+  int cstride, wstride, npstride;
+  const float* rec;  // records (REC kernels): [ceil(OUT/64)][K+1][64][4] words
+};
+
 // Per-output parameters held in registers: 2K candidate indices, 2K weights,
-// 4 node coefficients (144 bytes for K = 8).
+// 4 node coefficients.
 template <int KM>
 struct FcParams {
   int ia[KM], ib[KM];
@@ -91,57 +100,115 @@ struct FcParams {
 };
 
 // KC = compile-time candidate count (0 = runtime K <= 16, scalar loads).
-template <int KC, int KM>
-__device__ inline void load_params(FcParams<KM>& P, int o, int K, const int* __restrict__ ca,
-                                   const int* __restrict__ cb, int cstride,
-                                   const float* __restrict__ wa, const float* __restrict__ wb,
-                                   int wstride, const float* __restrict__ np) {
+// The loads are unconditional straight-line code, so the compiler's wait
+// counts stay exact across loop iterations.
+//
+// Records (REC): output o's K+1 quads of 4 words live at quad index
+// ((o / 64) * (K+1) + q) * 64 + o % 64, so one 16-byte load per quad moves
+// 1 KB of contiguous memory for the 64 outputs of a wave. Quads 0..K/4-1 hold
+// idx_a, then idx_b, w_a, w_b, and quad K the node parameters.
+template <int KC, int KM, bool REC>
+__device__ inline void load_params(FcParams<KM>& P, int o, int K, const ParamView& pv) {
+  if constexpr (REC) {
+    const f32x4* r = reinterpret_cast<const f32x4*>(pv.rec) +
+                     ((int64_t)(o >> 6) * (K + 1)) * 64 + (o & 63);
+    if constexpr (KC > 0 && (KC % 4) == 0) {
+      constexpr int Q = KC / 4;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const i32x4 a4 = __builtin_bit_cast(i32x4, r[(0 * Q + q) * 64]);
+        const i32x4 b4 = __builtin_bit_cast(i32x4, r[(1 * Q + q) * 64]);
+        const f32x4 u4 = r[(2 * Q + q) * 64];
+        const f32x4 v4 = r[(3 * Q + q) * 64];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          P.ia[4 * q + e] = a4[e];
+          P.ib[4 * q + e] = b4[e];
+          P.fa[4 * q + e] = u4[e];
+          P.fb[4 * q + e] = v4[e];
+        }
+      }
+    } else {
+      const float* rw = reinterpret_cast<const float*>(r - (o & 63));  // quad 0 of lane 0
+      const int l = o & 63;
+      auto word = [&](int w) { return rw[((w >> 2) * 64 + l) * 4 + (w & 3)]; };
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        if (k < K) {
+          P.ia[k] = __float_as_int(word(k));
+          P.ib[k] = __float_as_int(word(K + k));
+          P.fa[k] = word(2 * K + k);
+          P.fb[k] = word(3 * K + k);
+        } else {
+          P.ia[k] = 0; P.ib[k] = 0; P.fa[k] = 0.f; P.fb[k] = 0.f;
+        }
+      }
+    }
+    const f32x4 p4 = r[K * 64];
+    P.p = make_float4(p4[0], p4[1], p4[2], p4[3]);
+    return;
+  }
   if constexpr (KC > 0 && (KC % 4) == 0) {
+    const int* ca = pv.ca + (int64_t)o * pv.cstride;
+    const int* cb = pv.cb + (int64_t)o * pv.cstride;
+    const float* wa = pv.wa + (int64_t)o * pv.wstride;
+    const float* wb = pv.wb + (int64_t)o * pv.wstride;
 #pragma unroll
     for (int q = 0; q < KC / 4; ++q) {
-      const int4 a4 = *reinterpret_cast<const int4*>(ca + (int64_t)o * cstride + 4 * q);
-      const int4 b4 = *reinterpret_cast<const int4*>(cb + (int64_t)o * cstride + 4 * q);
-      const float4 u4 = *reinterpret_cast<const float4*>(wa + (int64_t)o * wstride + 4 * q);
-      const float4 v4 = *reinterpret_cast<const float4*>(wb + (int64_t)o * wstride + 4 * q);
-      P.ia[4 * q + 0] = a4.x; P.ia[4 * q + 1] = a4.y; P.ia[4 * q + 2] = a4.z; P.ia[4 * q + 3] = a4.w;
-      P.ib[4 * q + 0] = b4.x; P.ib[4 * q + 1] = b4.y; P.ib[4 * q + 2] = b4.z; P.ib[4 * q + 3] = b4.w;
-      P.fa[4 * q + 0] = u4.x; P.fa[4 * q + 1] = u4.y; P.fa[4 * q + 2] = u4.z; P.fa[4 * q + 3] = u4.w;
-      P.fb[4 * q + 0] = v4.x; P.fb[4 * q + 1] = v4.y; P.fb[4 * q + 2] = v4.z; P.fb[4 * q + 3] = v4.w;
+      const i32x4 a4 = *reinterpret_cast<const i32x4*>(ca + 4 * q);
+      const i32x4 b4 = *reinterpret_cast<const i32x4*>(cb + 4 * q);
+      const f32x4 u4 = *reinterpret_cast<const f32x4*>(wa + 4 * q);
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(wb + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        P.ia[4 * q + e] = a4[e];
+        P.ib[4 * q + e] = b4[e];
+        P.fa[4 * q + e] = u4[e];
+        P.fb[4 * q + e] = v4[e];
+      }
     }
   } else {
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
       if (k < K) {
-        P.ia[k] = ca[(int64_t)o * cstride + k];
-        P.ib[k] = cb[(int64_t)o * cstride + k];
-        P.fa[k] = wa ? wa[(int64_t)o * wstride + k] : 1.0f;
-        P.fb[k] = wb ? wb[(int64_t)o * wstride + k] : 1.0f;
+        P.ia[k] = pv.ca[(int64_t)o * pv.cstride + k];
+        P.ib[k] = pv.cb[(int64_t)o * pv.cstride + k];
+        P.fa[k] = pv.wa[(int64_t)o * pv.wstride + k];
+        P.fb[k] = pv.wb[(int64_t)o * pv.wstride + k];
       } else {
         P.ia[k] = 0; P.ib[k] = 0; P.fa[k] = 0.f; P.fb[k] = 0.f;
       }
     }
   }
-  P.p = reinterpret_cast<const float4*>(np)[o];
+  const f32x4 p4 = *reinterpret_cast<const f32x4*>(pv.np + (int64_t)o * pv.npstride);
+  P.p = make_float4(p4[0], p4[1], p4[2], p4[3]);
 }
+
+// Fused GroupSum head (heads.py:34-39 with the feature STE): per-class
+// counts of (y > 0.5), logits = count / tau.
+struct HeadArgs {
+  float* logits;
+  int C;
+  int per;  // OUT / C outputs per class
+  float tau;
+};
 
 // Widest workgroup per variant: 1024 threads keeps <= 128 VGPRs per lane,
 // which fits the lean variants; the others get 512 threads and more registers.
 template <int KC, int S>
 constexpr int soft_max_threads() { return (KC == 0 || S >= 8) ? 512 : 1024; }
 
-template <int NODE, int KC, int S>
+template <int NODE, int KC, int S, bool HEAD, bool REC>
 __global__ void __launch_bounds__((soft_max_threads<KC, S>()))
-fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr,
-               const int* __restrict__ ca, const int* __restrict__ cb, int cstride,
-               const float* __restrict__ wa, const float* __restrict__ wb, int wstride,
-               const float* __restrict__ np, float inv_tau, float* __restrict__ y,
-               int n_chunks, int chunk) {
+fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, ParamView pv,
+               float inv_tau, float* __restrict__ y, int n_chunks, int chunk, HeadArgs hd) {
   constexpr int V = S >= 4 ? 4 : S;
   constexpr int G = S / V;
   constexpr int KM = KC > 0 ? KC : 16;
   using vt = typename vecf<V>::t;
   extern __shared__ __align__(16) unsigned char smem[];
   vt* lds = reinterpret_cast<vt*>(smem);
+  unsigned* cnt = reinterpret_cast<unsigned*>(smem + (size_t)IN * S * sizeof(float));
   const int K = KC > 0 ? KC : Kr;
 
   const uint32_t lid = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -151,16 +218,16 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr,
   const int o_begin = ch * chunk;
   const int o_end = min(OUT, o_begin + chunk);
 
-  // First output's parameters are in flight while the tile is staged.
-  int o = o_begin + threadIdx.x;
-  FcParams<KM> P;
-  if (o < o_end) load_params<KC>(P, o, K, ca, cb, cstride, wa, wb, wstride, np);
+  if constexpr (HEAD) {
+    for (int t = threadIdx.x; t < S * hd.C; t += blockDim.x) cnt[t] = 0u;
+  }
 
-  // Stage S rows transposed: slot(i, g) holds samples b0+gV .. b0+gV+V-1 of
-  // input i. Threads load float4 runs of 4 inputs from each of the V rows of
-  // a group (4 batches in flight), then scatter them to the 4 input slots.
+  // Stage S rows transposed: lds[g * IN + i] holds samples b0+gV .. b0+gV+V-1
+  // of input i. Threads load float4 runs of 4 inputs from each of the V rows
+  // of a group (NBAT batches in flight), then scatter them to 4 input slots.
   const bool vec_rows = (IN & 3) == 0;
   for (int g = 0; g < G; ++g) {
+    vt* dst = lds + g * IN;
     if (vec_rows) {
       const int n4 = IN >> 2;
       constexpr int NBAT = V == 4 ? 2 : 4;  // float4 batches in flight per thread
@@ -186,8 +253,7 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr,
               float e[V];
 #pragma unroll
               for (int v = 0; v < V; ++v) e[v] = lanev(t[u][v], c);
-              const int i = 4 * q + c;
-              lds[slot<G>(i, g)] = make_vec<V>(e);
+              dst[4 * q + c] = make_vec<V>(e);
             }
           }
         }
@@ -200,66 +266,171 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr,
           const int b = b0 + g * V + v;
           e[v] = (b < B) ? __builtin_nontemporal_load(x + (int64_t)b * IN + i) : 0.0f;
         }
-        lds[slot<G>(i, g)] = make_vec<V>(e);
+        dst[i] = make_vec<V>(e);
       }
     }
   }
   __syncthreads();
 
-  while (o < o_end) {
-    // prefetch the next output's parameters; they land while this one computes
-    const int on = o + blockDim.x;
-    FcParams<KM> Q;
-    if (on < o_end) load_params<KC>(Q, on, K, ca, cb, cstride, wa, wb, wstride, np);
-    int ia[KM], ib[KM];
+  const uint32_t lim = (uint32_t)IN - 1u;
+  const bool full = b0 + S <= B;
+  const int lane = threadIdx.x & 63;
+
+  // Each wave owns a contiguous run of 64-output chunks; lane = output
+  // within a chunk. The next chunk's parameters are loaded while this one
+  // computes (two register sets, no copies); loads past the end re-read the
+  // last output, so every load is in bounds and unconditional.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int nwaves = blockDim.x >> 6;
+  const int n64 = (o_end - o_begin + 63) >> 6;
+  const int cpw = (n64 + nwaves - 1) / nwaves;
+  const int j_begin = wave * cpw, j_end = min(n64, j_begin + cpw);
+  const int o_last = o_end - 1;
+
+  // Fused head: per-sample counts of the current class in scalar registers,
+  // added to the LDS counters when the chunk run leaves the class. A chunk
+  // that straddles a class boundary counts lane by lane with LDS atomics.
+  int cur_c = 0, hi_b = 0;
+  unsigned acc[S];
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {  // clamp into the staged rows
-      ia[k] = min(max(P.ia[k], 0), IN - 1);
-      ib[k] = min(max(P.ib[k], 0), IN - 1);
+  for (int s = 0; s < S; ++s) acc[s] = 0u;
+  if constexpr (HEAD) {
+    if (j_begin < j_end) {
+      cur_c = (o_begin + j_begin * 64) / hd.per;
+      hi_b = (cur_c + 1) * hd.per;
     }
+  }
+
+  auto chunk_body = [&](const FcParams<KM>& P, int jj) {
+    const int oc0 = o_begin + jj * 64;
+    const int o = oc0 + lane;
+    const bool valid = o < o_end;
+    // clamp into the staged rows (unsigned min also maps negatives to IN-1)
+    uint32_t ia[KM], ib[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      ia[k] = min((uint32_t)P.ia[k], lim);
+      ib[k] = min((uint32_t)P.ib[k], lim);
+    }
+    float yv[S];
+#pragma unroll
     for (int g = 0; g < G; ++g) {
+      const vt* src = lds + g * IN;
+      // slot a, then slot b: at most K gathers in flight per wave keeps the
+      // two parameter sets and the gathered vectors within 128 VGPRs
       vt A = zero_vec<vt>(), Bv = zero_vec<vt>();
 #pragma unroll
-      for (int k = 0; k < KM; ++k) {
-        if (KC > 0 || k < K) {
-          fma_acc(A, P.fa[k], lds[slot<G>(ia[k], g)]);
-          fma_acc(Bv, P.fb[k], lds[slot<G>(ib[k], g)]);
+      for (int k = 0; k < KM; ++k)
+        if (KC > 0 || k < K) fma_acc(A, P.fa[k], src[ia[k]]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < KM; ++k)
+        if (KC > 0 || k < K) fma_acc(Bv, P.fb[k], src[ib[k]]);
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        yv[g * V + v] = node_eval<NODE>(lanev(A, v), lanev(Bv, v), P.p, inv_tau);
+    }
+    if constexpr (HEAD) {
+      const int oc1 = min(oc0 + 63, o_last);
+      if (oc1 < hi_b) {  // the whole chunk lies in class cur_c (wave-uniform)
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+          acc[s] += (unsigned)__popcll(__ballot(valid && b0 + s < B && yv[s] > 0.5f));
+      } else {
+        if (lane == 0) {
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            if (acc[s]) atomicAdd(&cnt[s * hd.C + cur_c], acc[s]);
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0u;
+        if (valid) {
+          const int c = o / hd.per;
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            if (b0 + s < B && yv[s] > 0.5f) atomicAdd(&cnt[s * hd.C + c], 1u);
+        }
+        cur_c = (oc1 + 1) / hd.per;  // class of the wave's next output
+        hi_b = (cur_c + 1) * hd.per;
+      }
+    } else {
+      float* yo = y + (int64_t)b0 * OUT + o;
+      if (valid) {
+        if (full) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) yo[(int64_t)s * OUT] = yv[s];
+        } else {
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            if (b0 + s < B) yo[(int64_t)s * OUT] = yv[s];
         }
       }
+    }
+  };
+
+  if (j_begin < j_end) {
+    FcParams<KM> P, Q;
+    int jj = j_begin;
+    load_params<KC, KM, REC>(P, min(o_begin + jj * 64 + lane, o_last), K, pv);
+    while (true) {
+      load_params<KC, KM, REC>(Q, min(o_begin + (jj + 1) * 64 + lane, o_last), K, pv);
+      chunk_body(P, jj);
+      if (++jj >= j_end) break;
+      load_params<KC, KM, REC>(P, min(o_begin + (jj + 1) * 64 + lane, o_last), K, pv);
+      chunk_body(Q, jj);
+      if (++jj >= j_end) break;
+    }
+    if constexpr (HEAD) {
+      if (lane == 0) {
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const int b = b0 + g * V + v;
-        if (b < B) y[(int64_t)b * OUT + o] = node_eval<NODE>(lanev(A, v), lanev(Bv, v), P.p, inv_tau);
+        for (int s = 0; s < S; ++s)
+          if (acc[s]) atomicAdd(&cnt[s * hd.C + cur_c], acc[s]);
       }
     }
-    P = Q;
-    o = on;
+  }
+  if constexpr (HEAD) {
+    __syncthreads();
+    for (int t = threadIdx.x; t < S * hd.C; t += blockDim.x) {
+      const int s = t / hd.C, c = t % hd.C;
+      if (b0 + s < B) hd.logits[(int64_t)(b0 + s) * hd.C + c] = (float)cnt[t] / hd.tau;
+    }
   }
 }
 
 struct SoftArgs {
   const float* x; int64_t B, IN, OUT; int K;
-  const int* ca; const int* cb; int cstride;
-  const float* wa; const float* wb; int wstride;
-  const float* np; float inv_tau; float* y;
+  ParamView pv;
+  float inv_tau; float* y;
   int S, threads;
+  HeadArgs hd;  // hd.logits != nullptr: fused GroupSum, y unused
 };
 
-template <int NODE, int KC, int S>
-static int launch_soft_s(const SoftArgs& a, hipStream_t st) {
-  const int64_t tiles = cdiv(a.B, S);
-  const int cus = device_cus();
-  const size_t lds = (size_t)a.IN * S * sizeof(float);
+// Output chunks per sample tile: enough workgroups to fill the chip twice
+// over (at the LDS-limited occupancy), whole 64-output wave runs per chunk.
+static void soft_grid(const SoftArgs& a, int64_t* n_chunks_out, int64_t* chunk_out) {
+  const int64_t tiles = cdiv(a.B, a.S);
+  const size_t lds = (size_t)a.IN * a.S * sizeof(float);
   const int per_cu = (int)std::max<int64_t>(1, (int64_t)device_lds_bytes() / std::max<size_t>(lds, 1));
-  const int64_t target = (int64_t)cus * std::min(per_cu, 4) * 2;
+  const int64_t target = (int64_t)device_cus() * std::min(per_cu, 4) * 2;
   int64_t n_chunks = std::max<int64_t>(1, cdiv(target, tiles));
   n_chunks = std::min<int64_t>(n_chunks, std::max<int64_t>(1, cdiv(a.OUT, 64)));
-  int64_t chunk = cdiv(cdiv(a.OUT, n_chunks), 64) * 64;
-  n_chunks = cdiv(a.OUT, chunk);
-  const int64_t grid = tiles * n_chunks;
+  const int64_t chunk = cdiv(cdiv(a.OUT, n_chunks), 64) * 64;
+  *n_chunks_out = cdiv(a.OUT, chunk);
+  *chunk_out = chunk;
+}
+
+template <int NODE, int KC, int S, bool HEAD, bool REC>
+static int launch_soft_s(const SoftArgs& a, hipStream_t st) {
+  int64_t n_chunks, chunk;
+  soft_grid(a, &n_chunks, &chunk);
+  SLG_REQUIRE(!HEAD || n_chunks == 1, SLG_E_UNSUPPORTED,
+              "fc_soft: fused GroupSum needs one output chunk per tile");
+  const int64_t grid = cdiv(a.B, S) * n_chunks;
   SLG_REQUIRE(grid < (1LL << 31), SLG_E_SHAPE, "fc_soft: grid too large");
-  auto kern = fc_soft_kernel<NODE, KC, S>;
+  auto kern = fc_soft_kernel<NODE, KC, S, HEAD, REC>;
   const int threads = std::min(a.threads, soft_max_threads<KC, S>());
+  const size_t lds = (size_t)a.IN * S * sizeof(float) + (HEAD ? (size_t)S * a.hd.C * 4 : 0);
+  SLG_REQUIRE(lds <= (size_t)device_lds_bytes(), SLG_E_SHAPE, "fc_soft: %zu B LDS needed", lds);
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -269,46 +440,55 @@ static int launch_soft_s(const SoftArgs& a, hipStream_t st) {
     }
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), lds, st, a.x, (int)a.B,
-                     (int)a.IN, (int)a.OUT, a.K, a.ca, a.cb, a.cstride, a.wa, a.wb, a.wstride,
-                     a.np, a.inv_tau, a.y, (int)n_chunks, (int)chunk);
+                     (int)a.IN, (int)a.OUT, a.K, a.pv, a.inv_tau, a.y, (int)n_chunks, (int)chunk,
+                     a.hd);
   SLG_LAUNCH_CHECK("fc_soft");
   return 0;
 }
 
-template <int NODE, int KC>
+template <int NODE, int KC, bool HEAD, bool REC>
 static int launch_soft_k(const SoftArgs& a, hipStream_t st) {
   switch (a.S) {
-    case 1: return launch_soft_s<NODE, KC, 1>(a, st);
-    case 2: return launch_soft_s<NODE, KC, 2>(a, st);
-    case 4: return launch_soft_s<NODE, KC, 4>(a, st);
-    case 8: return launch_soft_s<NODE, KC, 8>(a, st);
-    case 16: return launch_soft_s<NODE, KC, 16>(a, st);
+    case 1: return launch_soft_s<NODE, KC, 1, HEAD, REC>(a, st);
+    case 2: return launch_soft_s<NODE, KC, 2, HEAD, REC>(a, st);
+    case 4: return launch_soft_s<NODE, KC, 4, HEAD, REC>(a, st);
+    case 8: return launch_soft_s<NODE, KC, 8, HEAD, REC>(a, st);
     default: break;
   }
-  set_error("fc_soft: unsupported tile_samples %d (1,2,4,8,16)", a.S);
+  set_error("fc_soft: unsupported tile_samples %d (1, 2, 4, 8)", a.S);
   return SLG_E_ARG;
 }
 
-template <int NODE>
+static bool al16(const void* p) { return ((uintptr_t)p % 16) == 0; }
+
+template <int NODE, bool HEAD>
 static int launch_soft_node(const SoftArgs& a, hipStream_t st) {
-  const bool aligned = ((uintptr_t)a.ca % 16 == 0) && ((uintptr_t)a.cb % 16 == 0) &&
-                       ((uintptr_t)a.wa % 16 == 0) && ((uintptr_t)a.wb % 16 == 0) &&
-                       (a.cstride % 4 == 0) && (a.wstride % 4 == 0) && a.wa && a.wb;
-  if (a.K == 8 && aligned) return launch_soft_k<NODE, 8>(a, st);
-  if (a.K == 4 && aligned) return launch_soft_k<NODE, 4>(a, st);
-  if (a.K == 1) return launch_soft_k<NODE, 1>(a, st);
-  if (a.K == 2) return launch_soft_k<NODE, 2>(a, st);
-  return launch_soft_k<NODE, 0>(a, st);
+  const ParamView& v = a.pv;
+  if (v.rec) {  // records are 16-byte aligned by construction
+    if (a.K == 8) return launch_soft_k<NODE, 8, HEAD, true>(a, st);
+    if (a.K == 4) return launch_soft_k<NODE, 4, HEAD, true>(a, st);
+    return launch_soft_k<NODE, 0, HEAD, true>(a, st);
+  }
+  if constexpr (!HEAD) {
+    const bool vec = al16(v.ca) && al16(v.cb) && al16(v.wa) && al16(v.wb) &&
+                     v.cstride % 4 == 0 && v.wstride % 4 == 0;
+    if (a.K == 8 && vec) return launch_soft_k<NODE, 8, false, false>(a, st);
+    if (a.K == 4 && vec) return launch_soft_k<NODE, 4, false, false>(a, st);
+    return launch_soft_k<NODE, 0, false, false>(a, st);
+  }
+  set_error("fc_soft: the fused GroupSum takes records");
+  return SLG_E_ARG;
 }
 
 // Samples per workgroup tile and workgroup size, from a sweep on MI355X
 // (B = 4096, OUT = 10000-16380, K = 8): IN = 784 -> 4 samples / 256 threads,
 // IN = 4096 -> 8 / 512, IN = 10000 -> 4 / 1024, IN = 16380 -> 2 / 1024. The
-// tile takes the largest power of two <= 8 whose rows fit 160 KB of LDS (4 for
-// narrow inputs, where more, smaller workgroups per CU win).
+// tile takes the largest power of two <= 8 whose rows fit 160 KB of LDS less
+// 1 KB for the fused head's counters (4 for narrow inputs, where more,
+// smaller workgroups per CU win).
 static int pick_tile(int64_t IN, int requested) {
   if (requested > 0) return requested;
-  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024) - 1024;
   if (IN <= 1280) return 4;
   for (int s : {8, 4, 2, 1})
     if (IN * s * 4 <= cap) return s;
@@ -323,24 +503,41 @@ static int pick_threads(int64_t IN, int S, int requested) {
 }
 
 static int fc_soft_dispatch(SoftArgs a, int node_kind, hipStream_t st) {
-  SLG_REQUIRE(a.ca && a.cb && a.np && ((a.x && a.y) || a.B == 0), SLG_E_ARG, "fc_soft: null pointer");
+  const ParamView& v = a.pv;
+  const bool head = a.hd.logits != nullptr;
+  SLG_REQUIRE((v.rec || (v.ca && v.cb && v.wa && v.wb && v.np)) &&
+                  ((a.x && (a.y || head)) || a.B == 0), SLG_E_ARG, "fc_soft: null pointer");
   SLG_REQUIRE(a.B >= 0 && a.IN > 0 && a.OUT > 0, SLG_E_SHAPE, "fc_soft: bad sizes B=%lld IN=%lld OUT=%lld",
               (long long)a.B, (long long)a.IN, (long long)a.OUT);
   SLG_REQUIRE(a.K >= 1 && a.K <= 16, SLG_E_SHAPE, "fc_soft: K=%d outside 1..16", a.K);
   SLG_REQUIRE(a.B < (1LL << 31) && a.IN < (1LL << 28) && a.OUT < (1LL << 31), SLG_E_SHAPE,
               "fc_soft: sizes exceed 32-bit indexing");
-  SLG_REQUIRE(((uintptr_t)a.np % 16) == 0, SLG_E_ARG, "fc_soft: node_param must be 16-byte aligned");
+  SLG_REQUIRE(v.rec ? al16(v.rec) : (al16(v.np) && v.npstride % 4 == 0), SLG_E_ARG,
+              "fc_soft: node parameters must be 16-byte aligned");
+  if (head)
+    SLG_REQUIRE(a.hd.C > 0 && a.OUT % a.hd.C == 0 && a.B * a.hd.C < (1LL << 31), SLG_E_SHAPE,
+                "fc_soft: OUT=%lld not divisible by C=%d", (long long)a.OUT, a.hd.C);
   if (a.B == 0) return 0;
   a.S = pick_tile(a.IN, a.S);
   SLG_REQUIRE(a.S > 0 && (int64_t)a.IN * a.S * 4 <= device_lds_bytes(), SLG_E_SHAPE,
               "fc_soft: IN=%lld does not fit LDS", (long long)a.IN);
   a.threads = pick_threads(a.IN, a.S, a.threads);
   SLG_REQUIRE(a.threads % 64 == 0 && a.threads <= 1024, SLG_E_ARG, "fc_soft: threads=%d", a.threads);
-  switch (node_kind) {
-    case SLG_NODE_GATE16: return launch_soft_node<SLG_NODE_GATE16>(a, st);
-    case SLG_NODE_WALSH: return launch_soft_node<SLG_NODE_WALSH>(a, st);
-    case SLG_NODE_MULTILINEAR2: return launch_soft_node<SLG_NODE_MULTILINEAR2>(a, st);
-    default: break;
+  if (head) {
+    a.hd.per = (int)(a.OUT / a.hd.C);
+    switch (node_kind) {
+      case SLG_NODE_GATE16: return launch_soft_node<SLG_NODE_GATE16, true>(a, st);
+      case SLG_NODE_WALSH: return launch_soft_node<SLG_NODE_WALSH, true>(a, st);
+      case SLG_NODE_MULTILINEAR2: return launch_soft_node<SLG_NODE_MULTILINEAR2, true>(a, st);
+      default: break;
+    }
+  } else {
+    switch (node_kind) {
+      case SLG_NODE_GATE16: return launch_soft_node<SLG_NODE_GATE16, false>(a, st);
+      case SLG_NODE_WALSH: return launch_soft_node<SLG_NODE_WALSH, false>(a, st);
+      case SLG_NODE_MULTILINEAR2: return launch_soft_node<SLG_NODE_MULTILINEAR2, false>(a, st);
+      default: break;
+    }
   }
   set_error("fc_soft: unknown node_kind %d", node_kind);
   return SLG_E_ARG;
@@ -355,25 +552,23 @@ __constant__ float c_basis[16][4] = {
     {0, 1, 1, -2}, {0, 1, 1, -1}, {1, -1, -1, 1}, {1, -1, -1, 2}, {1, 0, -1, 0},
     {1, 0, -1, 1}, {1, -1, 0, 0}, {1, -1, 0, 1}, {1, 0, 0, -1}, {1, 0, 0, 0}};
 
-__global__ void fc_soft_prep_kernel(const float* __restrict__ conn, int OUT, int K, int node,
-                                    const float* __restrict__ raw, float* __restrict__ w,
-                                    float* __restrict__ np) {
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= OUT) return;
-  for (int s = 0; s < 2; ++s) {  // softmax over the K candidates of slot s
-    const int64_t base = ((int64_t)o * 2 + s) * K;
-    if (!conn) {
-      for (int k = 0; k < K; ++k) w[base + k] = 1.0f;
-      continue;
-    }
-    float m = conn[base];
-    for (int k = 1; k < K; ++k) m = fmaxf(m, conn[base + k]);
-    float sum = 0.f;
-    for (int k = 0; k < K; ++k) sum += expf(conn[base + k] - m);
-    for (int k = 0; k < K; ++k) w[base + k] = expf(conn[base + k] - m) / sum;
+// Softmax of conn[0..K) into w[0..K) (connectomes.py:114-119); conn == null
+// means fixed wiring (w = 1).
+__device__ inline void softmax_k(const float* conn, int K, float* w) {
+  if (!conn) {
+    for (int k = 0; k < K; ++k) w[k] = 1.0f;
+    return;
   }
-  float4 c;
-  if (node == SLG_NODE_GATE16) {
+  float m = conn[0];
+  for (int k = 1; k < K; ++k) m = fmaxf(m, conn[k]);
+  float sum = 0.f;
+  for (int k = 0; k < K; ++k) sum += expf(conn[k] - m);
+  for (int k = 0; k < K; ++k) w[k] = expf(conn[k] - m) / sum;
+}
+
+// The 4 node coefficients of output o from its raw parameters.
+__device__ inline float4 node_param(int node, const float* raw, int o) {
+  if (node == SLG_NODE_GATE16) {  // softmax(gate_logits) @ BASIS (nodes.py:82-84)
     const float* g = raw + (int64_t)o * 16;
     float m = g[0];
     for (int i = 1; i < 16; ++i) m = fmaxf(m, g[i]);
@@ -384,19 +579,158 @@ __global__ void fc_soft_prep_kernel(const float* __restrict__ conn, int OUT, int
       const float p = e[i] / sum;
       for (int j = 0; j < 4; ++j) acc[j] += p * c_basis[i][j];
     }
-    c = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  } else if (node == SLG_NODE_WALSH) {  // nodes.py:138-143
-    const float t0 = raw[o * 4 + 0], t1 = raw[o * 4 + 1], t2 = raw[o * 4 + 2], t3 = raw[o * 4 + 3];
-    c = make_float4(((t0 - t1) - t2) + t3, 2.0f * (t1 - t3), 2.0f * (t2 - t3), 4.0f * t3);
-  } else {
-    c = make_float4(sigmoidf_(raw[o * 4 + 0]), sigmoidf_(raw[o * 4 + 1]),
-                    sigmoidf_(raw[o * 4 + 2]), sigmoidf_(raw[o * 4 + 3]));
+    return make_float4(acc[0], acc[1], acc[2], acc[3]);
   }
-  reinterpret_cast<float4*>(np)[o] = c;
+  const float* r = raw + (int64_t)o * 4;
+  if (node == SLG_NODE_WALSH) {  // nodes.py:138-143
+    const float t0 = r[0], t1 = r[1], t2 = r[2], t3 = r[3];
+    return make_float4(((t0 - t1) - t2) + t3, 2.0f * (t1 - t3), 2.0f * (t2 - t3), 4.0f * t3);
+  }
+  return make_float4(sigmoidf_(r[0]), sigmoidf_(r[1]), sigmoidf_(r[2]), sigmoidf_(r[3]));
+}
+
+__global__ void fc_soft_prep_kernel(const float* __restrict__ conn, int OUT, int K, int node,
+                                    const float* __restrict__ raw, float* __restrict__ w,
+                                    float* __restrict__ np) {
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= OUT) return;
+  for (int s = 0; s < 2; ++s) {
+    const int64_t base = ((int64_t)o * 2 + s) * K;
+    softmax_k(conn ? conn + base : nullptr, K, w + base);
+  }
+  reinterpret_cast<float4*>(np)[o] = node_param(node, raw, o);
+}
+
+// Records of several layers in one launch. Output o's record is 4(K+1)
+// 32-bit words: idx_a[K] idx_b[K] (int32, clamped into [0, IN)), w_a[K]
+// w_b[K] (softmax), param[4], stored as K+1 quads in the chunk-major layout
+// read by load_params<.., REC = true>; outputs past OUT up to the next
+// multiple of 64 repeat output OUT-1. With a gather order (from
+// slg_fc_soft_schedule), step t of slot s holds candidate order[o][s][t].
+// Each workgroup serves one layer.
+constexpr int kMaxRecLayers = 16;
+struct RecLayer {
+  const int* cand;
+  const float* conn;
+  const float* raw;
+  const uint8_t* order;
+  float* rec;
+  int in_dim, out_dim, node;
+};
+struct RecNet {
+  RecLayer L[kMaxRecLayers];
+  int blk_start[kMaxRecLayers + 1];
+  int n, K;
+};
+
+__global__ void __launch_bounds__(256) fc_soft_records_kernel(RecNet net) {
+  int l = 0;
+  while (l + 1 < net.n && (int)blockIdx.x >= net.blk_start[l + 1]) ++l;
+  const RecLayer& L = net.L[l];
+  const int op = ((int)blockIdx.x - net.blk_start[l]) * blockDim.x + threadIdx.x;  // padded
+  const int n_pad = (L.out_dim + 63) & ~63;
+  if (op >= n_pad) return;
+  const int o = min(op, L.out_dim - 1);
+  const int K = net.K;
+  float* base = L.rec + ((int64_t)(op >> 6) * (K + 1) * 64 + (op & 63)) * 4;
+  auto put = [&](int w, float v) { base[(w >> 2) * 256 + (w & 3)] = v; };
+  for (int s = 0; s < 2; ++s) {
+    const int64_t cb = ((int64_t)o * 2 + s) * K;
+    float w[16];
+    softmax_k(L.conn ? L.conn + cb : nullptr, K, w);
+    for (int t = 0; t < K; ++t) {
+      const int k = L.order ? min((int)L.order[cb + t], K - 1) : t;
+      const int idx = min(max(L.cand[cb + k], 0), L.in_dim - 1);
+      put(s * K + t, __int_as_float(idx));
+      put(2 * K + s * K + t, w[k]);
+    }
+  }
+  const float4 p = node_param(L.node, L.raw, o);
+  put(4 * K + 0, p.x);
+  put(4 * K + 1, p.y);
+  put(4 * K + 2, p.z);
+  put(4 * K + 3, p.w);
+}
+
+// Bank-aware gather order. The soft kernel gathers one candidate per lane
+// and step from the LDS tile, whose slots are 16 B (4 samples), 8 B or 4 B
+// wide. gfx950's LDS has 64 four-byte banks: a ds_read_b128 serves 16 lanes
+// per cycle, conflict-free when their slots differ mod 16 (b64: 32 lanes,
+// mod 32; b32: 64 lanes, mod 64). For each group of N consecutive outputs
+// (N = lanes served per cycle) and each slot, this picks the step at which
+// each output reads each of its K candidates so that few reads of one step
+// share a bank: a greedy pass per step (least-used bank first, ties to the
+// bank with the most reads left), then pairwise step swaps within a lane
+// while they lower the summed per-step maximum. The sum over k is the same;
+// only the fp32 summation order changes.
+template <int N>
+__global__ void __launch_bounds__(64) fc_soft_schedule_kernel(const int* __restrict__ cand, int OUT,
+                                                              int K, uint8_t* __restrict__ order) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int ngroups = (OUT + N - 1) / N;
+  if (t >= ngroups * 2) return;
+  const int grp = t >> 1, s = t & 1;
+  const int o0 = grp * N, n = min(N, OUT - o0);
+  uint8_t bank[N][16];
+  uint8_t ord[N][16];
+  uint16_t used[N];
+  int demand[N];
+  uint8_t cnt[16][N];
+  for (int b = 0; b < N; ++b) demand[b] = 0;
+  for (int l = 0; l < n; ++l) {
+    used[l] = 0;
+    for (int k = 0; k < K; ++k) {
+      const int b = cand[((int64_t)(o0 + l) * 2 + s) * K + k] & (N - 1);
+      bank[l][k] = (uint8_t)b;
+      ++demand[b];
+    }
+  }
+  for (int st = 0; st < K; ++st) {
+    for (int b = 0; b < N; ++b) cnt[st][b] = 0;
+    for (int l = 0; l < n; ++l) {
+      int best = -1, bc = 0, bd = 0;
+      for (int k = 0; k < K; ++k) {
+        if (used[l] & (1u << k)) continue;
+        const int b = bank[l][k], c = cnt[st][b], d = demand[b];
+        if (best < 0 || c < bc || (c == bc && d > bd)) { best = k; bc = c; bd = d; }
+      }
+      used[l] |= (uint16_t)(1u << best);
+      ord[l][st] = (uint8_t)best;
+      ++cnt[st][bank[l][best]];
+      --demand[bank[l][best]];
+    }
+  }
+  auto step_max = [&](int st) {
+    int m = 0;
+    for (int b = 0; b < N; ++b) m = max(m, (int)cnt[st][b]);
+    return m;
+  };
+  for (int pass = 0; pass < 8; ++pass) {
+    bool improved = false;
+    for (int l = 0; l < n; ++l)
+      for (int t1 = 0; t1 < K; ++t1)
+        for (int t2 = t1 + 1; t2 < K; ++t2) {
+          const int b1 = bank[l][ord[l][t1]], b2 = bank[l][ord[l][t2]];
+          if (b1 == b2) continue;
+          const int before = step_max(t1) + step_max(t2);
+          --cnt[t1][b1]; ++cnt[t1][b2]; --cnt[t2][b2]; ++cnt[t2][b1];
+          if (step_max(t1) + step_max(t2) < before) {
+            const uint8_t tmp = ord[l][t1];
+            ord[l][t1] = ord[l][t2];
+            ord[l][t2] = tmp;
+            improved = true;
+          } else {
+            ++cnt[t1][b1]; --cnt[t1][b2]; ++cnt[t2][b2]; --cnt[t2][b1];
+          }
+        }
+    if (!improved) break;
+  }
+  for (int l = 0; l < n; ++l)
+    for (int st = 0; st < K; ++st) order[((int64_t)(o0 + l) * 2 + s) * K + st] = ord[l][st];
 }
 
 // ---------------------------------------------------------------------------
-// GroupSum (silogic/heads.py:16-45): one workgroup per sample.
+// GroupSum (silogic/heads.py:16-45).
 // ---------------------------------------------------------------------------
 template <typename T, bool STE>
 __global__ void __launch_bounds__(256) groupsum_kernel(const T* __restrict__ x, int B, int W, int C,
@@ -417,6 +751,15 @@ __global__ void __launch_bounds__(256) groupsum_kernel(const T* __restrict__ x, 
   if (lane == 0) logits[task] = part / tau;
 }
 
+static ParamView arrays_view(const int32_t* ca, const int32_t* cb, int cstride, const float* wa,
+                             const float* wb, int wstride, const float* np) {
+  return ParamView{ca, cb, wa, wb, np, cstride, wstride, 4, nullptr};
+}
+
+static ParamView records_view(const float* rec) {
+  return ParamView{nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, rec};
+}
+
 }  // namespace slg
 
 using namespace slg;
@@ -428,24 +771,24 @@ int slg_fc_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
                     const float* node_param, float inv_tau, float* out, int32_t tile_samples,
                     int32_t threads, slg_stream_t stream) {
   SLG_REQUIRE(cand && w, SLG_E_ARG, "fc_soft_fwd: null cand/w");
-  SoftArgs a{x, B, IN, OUT, K, cand, cand + K, 2 * K, w, w + K, 2 * K, node_param, inv_tau,
-             out, tile_samples, threads};
+  SoftArgs a{x, B, IN, OUT, K, arrays_view(cand, cand + K, 2 * K, w, w + K, 2 * K, node_param),
+             inv_tau, out, tile_samples, threads, HeadArgs{nullptr, 0, 0, 1.0f}};
   return fc_soft_dispatch(a, node_kind, as_stream(stream));
 }
 
 int slg_dense_logic_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
                         const int32_t* ca, const int32_t* cb, const float* wa, const float* wb,
                         const float* coef, float* out, slg_stream_t stream) {
-  SLG_REQUIRE(wa && wb, SLG_E_ARG, "dense_logic: null weights");
-  SoftArgs a{x, B, IN, OUT, K, ca, cb, K, wa, wb, K, coef, 1.0f, out, 0, 0};
+  SoftArgs a{x, B, IN, OUT, K, arrays_view(ca, cb, K, wa, wb, K, coef), 1.0f, out, 0, 0,
+             HeadArgs{nullptr, 0, 0, 1.0f}};
   return fc_soft_dispatch(a, SLG_NODE_GATE16, as_stream(stream));
 }
 
 int slg_warp_logic_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
                        const int32_t* ca, const int32_t* cb, const float* wa, const float* wb,
                        const float* coef, float inv_tau, float* out, slg_stream_t stream) {
-  SLG_REQUIRE(wa && wb, SLG_E_ARG, "warp_logic: null weights");
-  SoftArgs a{x, B, IN, OUT, K, ca, cb, K, wa, wb, K, coef, inv_tau, out, 0, 0};
+  SoftArgs a{x, B, IN, OUT, K, arrays_view(ca, cb, K, wa, wb, K, coef), inv_tau, out, 0, 0,
+             HeadArgs{nullptr, 0, 0, 1.0f}};
   return fc_soft_dispatch(a, SLG_NODE_WALSH, as_stream(stream));
 }
 
@@ -461,6 +804,95 @@ int slg_fc_soft_prep(const float* conn, int64_t OUT, int32_t K, int32_t node_kin
                      as_stream(stream), conn, (int)OUT, K, node_kind, raw, w, node_param);
   SLG_LAUNCH_CHECK("fc_soft_prep");
   return 0;
+}
+
+int slg_fc_soft_records(int32_t n_layers, const int32_t* const* cand, const float* const* conn,
+                        const float* const* raw, const int64_t* in_dim, const int64_t* out_dim,
+                        int32_t K, const int32_t* node_kind, const uint8_t* const* order,
+                        float* const* rec, slg_stream_t stream) {
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxRecLayers, SLG_E_SHAPE,
+              "fc_soft_records: n_layers=%d outside 1..%d", n_layers, kMaxRecLayers);
+  SLG_REQUIRE(cand && conn && raw && in_dim && out_dim && node_kind && rec, SLG_E_ARG,
+              "fc_soft_records: null array");
+  SLG_REQUIRE(K >= 1 && K <= 16, SLG_E_SHAPE, "fc_soft_records: K=%d outside 1..16", K);
+  RecNet net{};
+  net.n = n_layers;
+  net.K = K;
+  const int th = 256;
+  int64_t blocks = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(cand[l] && raw[l] && rec[l], SLG_E_ARG, "fc_soft_records: null pointer, layer %d", l);
+    SLG_REQUIRE(in_dim[l] > 0 && in_dim[l] < (1LL << 28) && out_dim[l] > 0 &&
+                    out_dim[l] < (1LL << 28), SLG_E_SHAPE, "fc_soft_records: bad sizes, layer %d", l);
+    SLG_REQUIRE(node_kind[l] >= 0 && node_kind[l] <= 2, SLG_E_ARG,
+                "fc_soft_records: node_kind %d", node_kind[l]);
+    SLG_REQUIRE(((uintptr_t)rec[l] % 16) == 0, SLG_E_ARG, "fc_soft_records: rec alignment");
+    net.L[l] = RecLayer{cand[l], conn[l], raw[l], order ? order[l] : nullptr, rec[l],
+                        (int)in_dim[l], (int)out_dim[l], node_kind[l]};
+    net.blk_start[l] = (int)blocks;
+    blocks += cdiv(cdiv(out_dim[l], 64) * 64, th);
+  }
+  net.blk_start[n_layers] = (int)blocks;
+  hipLaunchKernelGGL(fc_soft_records_kernel, dim3((unsigned)blocks), dim3(th), 0,
+                     as_stream(stream), net);
+  SLG_LAUNCH_CHECK("fc_soft_records");
+  return 0;
+}
+
+int slg_fc_soft_schedule(const int32_t* cand, int64_t OUT, int32_t K, int64_t IN, uint8_t* order,
+                         slg_stream_t stream) {
+  SLG_REQUIRE(cand && order, SLG_E_ARG, "fc_soft_schedule: null pointer");
+  SLG_REQUIRE(OUT > 0 && OUT < (1LL << 28) && IN > 0 && K >= 1 && K <= 16, SLG_E_SHAPE,
+              "fc_soft_schedule: bad sizes");
+  const int S = pick_tile(IN, 0);
+  const int lanes = S >= 4 ? 16 : (S == 2 ? 32 : 64);
+  const int64_t threads = cdiv(OUT, lanes) * 2;
+  const unsigned grid = (unsigned)cdiv(threads, 64);
+  hipStream_t st = as_stream(stream);
+  if (lanes == 16)
+    hipLaunchKernelGGL(fc_soft_schedule_kernel<16>, dim3(grid), dim3(64), 0, st, cand, (int)OUT, K, order);
+  else if (lanes == 32)
+    hipLaunchKernelGGL(fc_soft_schedule_kernel<32>, dim3(grid), dim3(64), 0, st, cand, (int)OUT, K, order);
+  else
+    hipLaunchKernelGGL(fc_soft_schedule_kernel<64>, dim3(grid), dim3(64), 0, st, cand, (int)OUT, K, order);
+  SLG_LAUNCH_CHECK("fc_soft_schedule");
+  return 0;
+}
+
+int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                            const float* rec, int32_t node_kind, float inv_tau, float* out,
+                            int32_t tile_samples, int32_t threads, slg_stream_t stream) {
+  SLG_REQUIRE(rec, SLG_E_ARG, "fc_soft_fwd_records: null rec");
+  SLG_REQUIRE(K >= 1 && K <= 16, SLG_E_SHAPE, "fc_soft_fwd_records: K=%d outside 1..16", K);
+  SoftArgs a{x, B, IN, OUT, K, records_view(rec), inv_tau, out, tile_samples, threads,
+             HeadArgs{nullptr, 0, 0, 1.0f}};
+  return fc_soft_dispatch(a, node_kind, as_stream(stream));
+}
+
+int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C) {
+  if (B <= 0 || IN <= 0 || OUT <= 0 || C <= 0 || OUT % C != 0) return 0;
+  if (B >= (1LL << 31) || IN >= (1LL << 28) || OUT >= (1LL << 31)) return 0;
+  SoftArgs a{};
+  a.B = B; a.IN = IN; a.OUT = OUT;
+  a.S = pick_tile(IN, 0);
+  if (a.S <= 0 || IN * a.S * 4 + (int64_t)a.S * C * 4 > device_lds_bytes()) return 0;
+  int64_t n_chunks, chunk;
+  soft_grid(a, &n_chunks, &chunk);
+  return n_chunks == 1 ? 1 : 0;
+}
+
+int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                             const float* rec, int32_t node_kind, float inv_tau, int32_t C,
+                             float tau, float* logits, slg_stream_t stream) {
+  SLG_REQUIRE(rec && (logits || B == 0), SLG_E_ARG, "fc_soft_fwd_groupsum: null pointer");
+  SLG_REQUIRE(K >= 1 && K <= 16, SLG_E_SHAPE, "fc_soft_fwd_groupsum: K=%d outside 1..16", K);
+  if (B == 0) return 0;
+  SLG_REQUIRE(slg_fc_soft_groupsum_supported(B, IN, OUT, C), SLG_E_UNSUPPORTED,
+              "fc_soft_fwd_groupsum: B=%lld IN=%lld OUT=%lld C=%d needs the unfused path",
+              (long long)B, (long long)IN, (long long)OUT, C);
+  SoftArgs a{x, B, IN, OUT, K, records_view(rec), inv_tau, nullptr, 0, 0,
+             HeadArgs{logits, C, 0, tau}};
+  return fc_soft_dispatch(a, node_kind, as_stream(stream));
 }
 
 int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau, int32_t ste,

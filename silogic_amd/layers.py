@@ -5,10 +5,12 @@ Construction, parameter names and ``state_dict`` layout follow the reference
 (silogic/layers.py:51-75, 271-373) so checkpoints and seeds carry over.
 Compute runs on the HIP kernels of ``libsilogic_hip.so``:
 
-* ``LogicLayer.forward`` -> Top-K gather + node (``slg_fc_soft_fwd``), with
-  ``softmax(conn)`` and the node coefficients prepared by
-  ``slg_fc_soft_prep`` when no gradient is needed, or by differentiable torch
-  ops (the reference's ``_fused`` split, layers.py:111-123) when it is.
+* ``LogicLayer.forward`` -> Top-K gather + node. Without gradients the
+  parameters (``softmax(conn)``, node coefficients, clamped indices) are
+  packed into one record per output by ``slg_fc_soft_records`` and the layer
+  runs on ``slg_fc_soft_fwd_records``; with gradients they come from
+  differentiable torch ops (the reference's ``_fused`` split,
+  layers.py:111-123) and the layer runs on ``slg_fc_soft_fwd``.
 * ``LogicLayer.forward_hard`` -> pack, one packed layer, unpack.
 * ``ConvLogicTree.forward`` -> ``slg_conv_soft_fwd``; networks call
   ``forward_pooled``, which fuses the following ``OrPool``.
@@ -104,17 +106,58 @@ class LogicLayer(nn.Module):
                                    conn.k)
         return cand, w, npar
 
+    def record_spec(self):
+        """``(cand, conn, raw, in_dim, node_kind, order)`` for
+        ``ops.fc_soft_records`` when the forward without gradients is a plain
+        softmax selection, else ``None``."""
+        self._check_supported()
+        conn = self._conn
+        if not self.node.plain_softmax() or getattr(conn, "ste", False):
+            return None
+        raw_conn = None if isinstance(conn, FixedConnectome) else conn.conn
+        cand = conn.candidates_i32()
+        return cand, raw_conn, self.node.raw(), self.in_dim, self.node.kind, self.gather_order(cand)
+
+    @property
+    def n_candidates(self):
+        return self._conn.k
+
+    def gather_order(self, cand=None):
+        """Bank-aware order in which the soft kernel gathers each output's
+        candidates (``slg_fc_soft_schedule``). It depends only on the
+        candidate table, a buffer that training does not change, so it is
+        computed once per table (a new device, a loaded state dict or any
+        in-place change of the buffer recomputes it). ``None`` for K = 1."""
+        cand = self._conn.candidates_i32() if cand is None else cand
+        if cand.shape[-1] < 2:
+            return None
+        key = (cand.data_ptr(), cand._version, str(cand.device), self.in_dim)
+        cached = getattr(self, "_order_cache", None)
+        if cached is None or cached[0] != key:
+            self._order_cache = (key, ops.fc_soft_schedule(cand, self.in_dim))
+        return self._order_cache[1]
+
     def forward(self, x):
         self._check_supported()
         ops.require_gpu(x)
-        cand, w, npar = self.soft_params(_needs_grad(self, x))
+        grad = _needs_grad(self, x)
+        spec = None if grad else self.record_spec()
+        if spec is not None:
+            K = self.n_candidates
+            rec = ops.fc_soft_records([spec], K)[0]
+            return ops.fc_soft_rec(x, rec, self.out_dim, K, self.node.kind, self._inv_tau())
+        cand, w, npar = self.soft_params(grad)
         return ops.fc_soft(x, cand, w, npar, self.node.kind, self._inv_tau())
+
+    def hard_spec(self):
+        """``(cand, conn, raw, node_kind, in_dim)`` for the hard-code prep."""
+        self._check_supported()
+        cand, conn = self._conn.hard_inputs()
+        return cand, conn, self.node.raw(), self.node.kind, self.in_dim
 
     def hard_codes(self):
         """Per-output ``(a, b | tt << 28)`` codes [out, 2] int32 (HIP prep)."""
-        self._check_supported()
-        cand, conn = self._conn.hard_inputs()
-        return ops.fc_hard_codes(cand, conn, self.node.raw(), self.node.kind, self.in_dim)
+        return ops.fc_hard_codes(*self.hard_spec())
 
     @torch.no_grad()
     def forward_hard(self, x):

@@ -6,7 +6,10 @@ Construction and ``state_dict`` keys follow the reference (per-layer seeds
 silogic/models.py:59-86, 208-246).
 
 ``forward`` runs layer by layer on the HIP soft kernels (conv blocks with
-their OrPool fused). ``forward_hard`` runs the network as one bit-packed
+their OrPool fused). Without gradients, the parameters of every FC layer are
+prepared in one launch (per-output records) and the last FC layer is fused
+with the GroupSum head when the head thresholds its features (the feature
+STE, on by default). ``forward_hard`` runs the network as one bit-packed
 circuit: 64 samples per word, the FC stack depth-fused in LDS with the
 GroupSum popcount at the end (``slg_fc_hard_net``), conv blocks as packed
 tree + OR-pool kernels. It returns the same raw integer counts as the
@@ -16,12 +19,37 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .heads import build_decoder
-from .layers import LogicLayer, ConvLogicTree, OrPool
+from .heads import GroupSum, build_decoder
+from .layers import LogicLayer, ConvLogicTree, OrPool, _needs_grad
 
 
 def _per_layer(v, i):
     return v[i] if isinstance(v, (list, tuple)) else v
+
+
+def _soft_fc_stack(layers, head, x, wire_r):
+    """Soft forward of arity-2 FC layers + GroupSum head on records (no
+    gradients). Returns ``None`` when a layer needs the autograd path (a
+    non-softmax selection) so the caller runs layer by layer."""
+    specs = [layer.record_spec() for layer in layers]
+    Ks = {layer.n_candidates for layer in layers}
+    if not layers or any(s is None for s in specs) or len(Ks) != 1:
+        return None
+    K = Ks.pop()
+    recs = ops.fc_soft_records(specs, K)
+    h = x
+    for i, (layer, rec) in enumerate(zip(layers, recs)):
+        kind, inv_tau = layer.node.kind, layer._inv_tau()
+        if i == len(layers) - 1 and isinstance(head, GroupSum) and head.feature_ste and not (
+                wire_r and h.shape[1] == layer.out_dim) and ops.fc_soft_groupsum_supported(
+                    h.shape[0], h.shape[1], layer.out_dim, head.num_classes):
+            return ops.fc_soft_rec_groupsum(h, rec, layer.out_dim, K, kind, inv_tau,
+                                            head.num_classes, head.tau)
+        y = ops.fc_soft_rec(h, rec, layer.out_dim, K, kind, inv_tau)
+        if wire_r and h.shape[1] == y.shape[1]:
+            y = torch.cat([h[:, :wire_r], y[:, wire_r:]], dim=1)
+        h = y
+    return head(h)
 
 
 def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
@@ -31,7 +59,7 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
     fused into it when the input is at most 1024 features wide; otherwise one
     packed kernel per layer."""
-    codes = [layer.hard_codes() for layer in layers]
+    codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers])
     widths = [c.shape[0] for c in codes]
     spw = ops.fc_hard_net_supported(in_dim, widths, C)
     if spw:
@@ -89,6 +117,10 @@ class LogicNet(nn.Module):
 
     def forward(self, x):
         ops.require_gpu(x)
+        if not _needs_grad(self, x):
+            out = _soft_fc_stack(self.layers, self.head, x, self.wire_r)
+            if out is not None:
+                return out
         return self.head(self._run(x))
 
     @torch.no_grad()
@@ -173,6 +205,10 @@ class LogicConvNet(nn.Module):
     def forward(self, x):
         ops.require_gpu(x)
         x = self._apply_blocks(x).flatten(1)
+        if not _needs_grad(self, x):
+            out = _soft_fc_stack(self.head_layers, self.head, x, 0)
+            if out is not None:
+                return out
         for layer in self.head_layers:
             x = layer(x)
         return self.head(x)

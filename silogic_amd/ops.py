@@ -129,6 +129,104 @@ def fc_soft(x, cand, w, npar, node_kind, inv_tau=1.0):
                            _c(npar, torch.float32), node_kind, inv_tau)
 
 
+MAX_RECORD_LAYERS = 16
+
+
+def _ptrs(ts):
+    return (ctypes.c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
+
+
+def fc_soft_schedule(cand, in_dim):
+    """Bank-aware gather order ``[OUT,2,K]`` uint8 for ``cand [OUT,2,K]``."""
+    require_gpu(cand)
+    cand = _c(cand, torch.int32)
+    OUT, two, K = cand.shape
+    order = torch.empty((OUT, 2, K), device=cand.device, dtype=torch.uint8)
+    _lib.call("slg_fc_soft_schedule", _p(cand), OUT, K, int(in_dim), _p(order), _stream(cand))
+    return order
+
+
+def fc_soft_records(specs, K):
+    """Per-output parameter records of several FC soft layers, one launch per
+    16 layers. ``specs``: ``(cand [OUT,2,K], conn [OUT,2,K] or None, raw,
+    in_dim, node_kind, order or None)`` per layer (``raw``: gate logits
+    [OUT,16], walsh theta or multilinear logits [OUT,4]; ``order`` from
+    :func:`fc_soft_schedule`). Returns ``[ceil(OUT/64), K+1, 64, 4]`` float32
+    tensors (the chunk-major record layout; index words reinterpreted)."""
+    recs = []
+    for g in range(0, len(specs), MAX_RECORD_LAYERS):
+        part = specs[g:g + MAX_RECORD_LAYERS]
+        cands, conns, raws, ins, outs, kinds, orders = [], [], [], [], [], [], []
+        for cand, conn, raw, in_dim, kind, order in part:
+            require_gpu(cand, conn, raw, order)
+            OUT = cand.shape[0]
+            if tuple(cand.shape) != (OUT, 2, K) or (conn is not None and conn.shape != cand.shape):
+                raise ValueError(f"fc_soft_records: cand {tuple(cand.shape)} / conn "
+                                 f"{None if conn is None else tuple(conn.shape)} for K={K}")
+            if raw.shape != (OUT, 16 if kind == GATE16 else 4):
+                raise ValueError(f"fc_soft_records: raw {tuple(raw.shape)} for node kind {kind}")
+            if order is not None and (order.shape != cand.shape or order.dtype != torch.uint8):
+                raise ValueError("fc_soft_records: order must be uint8 shaped like cand")
+            cands.append(_c(cand, torch.int32))
+            conns.append(_c(conn, torch.float32))
+            raws.append(_c(raw, torch.float32))
+            orders.append(_c(order))
+            ins.append(int(in_dim))
+            outs.append(OUT)
+            kinds.append(int(kind))
+        dev = raws[0].device
+        out = [torch.empty(((o + 63) // 64, K + 1, 64, 4), device=dev, dtype=torch.float32)
+               for o in outs]
+        n = len(part)
+        _lib.call("slg_fc_soft_records", n, _ptrs(cands), _ptrs(conns), _ptrs(raws),
+                  (ctypes.c_int64 * n)(*ins), (ctypes.c_int64 * n)(*outs), K,
+                  (ctypes.c_int32 * n)(*kinds), _ptrs(orders), _ptrs(out), _stream(raws[0]))
+        recs.extend(out)
+    return recs
+
+
+def record_words(rec, out_dim):
+    """``[OUT, 4(K+1)]`` view of chunk-major records (for inspection)."""
+    n64, K1 = rec.shape[0], rec.shape[1]
+    return rec.permute(0, 2, 1, 3).reshape(n64 * 64, 4 * K1)[:out_dim]
+
+
+def _check_rec(x, rec, out_dim, K):
+    if rec.dim() != 4 or tuple(rec.shape) != ((out_dim + 63) // 64, K + 1, 64, 4) or \
+            rec.dtype != torch.float32 or not rec.is_contiguous():
+        raise ValueError(f"fc_soft: records {tuple(rec.shape)} {rec.dtype} for OUT={out_dim}, K={K}")
+    if x.dim() != 2:
+        raise ValueError(f"fc_soft: x must be [B, IN], got {tuple(x.shape)}")
+
+
+def fc_soft_rec(x, rec, out_dim, K, node_kind, inv_tau=1.0, tile=0, threads=0):
+    """Soft FC layer on records (no autograd): ``[B,IN] -> [B,OUT]``."""
+    require_gpu(x, rec)
+    x = _as_f32(x)
+    _check_rec(x, rec, out_dim, K)
+    B, IN = x.shape
+    y = torch.empty((B, out_dim), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_soft_fwd_records", _p(x), B, IN, out_dim, K, _p(rec), node_kind,
+              float(inv_tau), _p(y), int(tile), int(threads), _stream(x))
+    return y
+
+
+def fc_soft_groupsum_supported(B, IN, OUT, C):
+    return bool(_lib.lib().slg_fc_soft_groupsum_supported(B, IN, OUT, C))
+
+
+def fc_soft_rec_groupsum(x, rec, out_dim, K, node_kind, inv_tau, C, tau):
+    """Last soft layer fused with the STE GroupSum head: ``[B,IN] -> [B,C]``."""
+    require_gpu(x, rec)
+    x = _as_f32(x)
+    _check_rec(x, rec, out_dim, K)
+    B, IN = x.shape
+    logits = torch.empty((B, C), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_soft_fwd_groupsum", _p(x), B, IN, out_dim, K, _p(rec), node_kind,
+              float(inv_tau), int(C), float(tau), _p(logits), _stream(x))
+    return logits
+
+
 # ---------------------------------------------------------------------------
 # GroupSum / OrPool
 # ---------------------------------------------------------------------------
@@ -252,6 +350,40 @@ def fc_hard_codes(cand, conn, raw, node_kind, in_dim):
     _lib.call("slg_fc_hard_prep", _p(cand), _p(_c(conn, torch.float32)), OUT, K, in_dim,
               node_kind, _p(_c(raw, torch.float32)), _p(codes), _stream(cand))
     return codes
+
+
+def fc_hard_codes_net(specs):
+    """Codes of several layers, one launch per 16 layers. ``specs``:
+    ``(cand, conn or None, raw, node_kind, in_dim)`` per layer, as
+    :func:`fc_hard_codes`. Returns ``[OUT, 2]`` int32 tensors."""
+    out = []
+    for g in range(0, len(specs), MAX_RECORD_LAYERS):
+        part = specs[g:g + MAX_RECORD_LAYERS]
+        cands, conns, raws, ins, outs, Ks, kinds = [], [], [], [], [], [], []
+        for cand, conn, raw, kind, in_dim in part:
+            require_gpu(cand, conn, raw)
+            cand = _c(cand, torch.int32)
+            OUT = cand.shape[0]
+            K = cand.shape[2] if cand.dim() == 3 else 1
+            if (conn is None) != (cand.dim() == 2) or (conn is not None and conn.shape != cand.shape):
+                raise ValueError("fc_hard_codes_net: cand/conn shapes are inconsistent")
+            if raw.shape != (OUT, 16 if kind == GATE16 else 4):
+                raise ValueError(f"fc_hard_codes_net: raw {tuple(raw.shape)} for node kind {kind}")
+            cands.append(cand)
+            conns.append(_c(conn, torch.float32))
+            raws.append(_c(raw, torch.float32))
+            ins.append(int(in_dim))
+            outs.append(OUT)
+            Ks.append(K)
+            kinds.append(int(kind))
+        codes = [torch.empty((o, 2), device=raws[0].device, dtype=torch.int32) for o in outs]
+        n = len(part)
+        _lib.call("slg_fc_hard_prep_net", n, _ptrs(cands), _ptrs(conns), _ptrs(raws),
+                  (ctypes.c_int64 * n)(*ins), (ctypes.c_int64 * n)(*outs),
+                  (ctypes.c_int32 * n)(*Ks), (ctypes.c_int32 * n)(*kinds), _ptrs(codes),
+                  _stream(raws[0]))
+        out.extend(codes)
+    return out
 
 
 def fc_hard_layer(xp, codes):
