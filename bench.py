@@ -117,7 +117,7 @@ def kernels_only(reps=3):
     model = build_config(2, sl).eval().to(dev)
     xh = config_inputs(2, 65536).to(dev)
     with torch.no_grad():
-        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers])
+        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
         for _ in range(reps):
             ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
         x_mid = torch.rand(4096, 10000, device=dev)
@@ -195,7 +195,7 @@ def main():
 
     # ---- dominant kernels alone, HIP events on the launch stream ----
     with torch.no_grad():
-        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers])
+        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
         reps = 20
         fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, 784, codes, 10)  # noqa: E731
         fn_net()

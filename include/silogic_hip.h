@@ -190,11 +190,13 @@ int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_
 
 /* slg_fc_hard_prep for n_layers (<= 16) layers in one launch: host arrays
  * of length n_layers with the arguments of each layer (conn[l] NULL = fixed
- * wiring, K[l] = 1). */
+ * wiring, K[l] = 1). compact = 0 writes slg_code2 codes [out_dim, 2];
+ * compact = 1 writes the depth-fused network's 4-byte codes [out_dim]
+ * (b | a << 14 | tt << 28, inputs at most 16384 wide) for slg_fc_hard_net. */
 int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const float* const* conn,
                          const float* const* raw, const int64_t* in_dim, const int64_t* out_dim,
-                         const int32_t* K, const int32_t* node_kind, uint32_t* const* codes,
-                         slg_stream_t stream);
+                         const int32_t* K, const int32_t* node_kind, int32_t compact,
+                         uint32_t* const* codes, slg_stream_t stream);
 
 /* One packed FC layer (replaces BitpackedFCLayer.forward,
  * packed_layer.py:85-116, and LogicLayer.forward_hard, layers.py:131-135):
@@ -204,13 +206,14 @@ int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw,
                       slg_stream_t stream);
 
 /* Depth-fused packed FC network + GroupSum (replaces LogicNet.forward_hard,
- * models.py:99-101, with GroupSum.forward_hard, heads.py:41-45). Input x:
+ * models.py:99-101, with GroupSum.forward_hard, heads.py:41-45). codes[l]
+ * are compact 4-byte codes [width_l] from slg_fc_hard_prep_net(compact = 1);
+ * operand indices are clamped to the layer's input width. Input x:
  * in_kind 0 = fp32 rows [B,IN0], 1 = uint8 rows [B,IN0] (packed on the fly,
  * bit = uint8(x) != 0; needs IN0 <= 1024 and 64-sample tiles), 2 = packed
  * [IN0, ceil(B/64)] uint64, 3 = packed word-major [ceil(B/64), IN0]. It runs
- * n_layers arity-2 layers whose widths and device code arrays (from
- * slg_fc_hard_prep) are given by the host arrays widths[n_layers] and
- * codes[n_layers], then writes logits [B,C] fp32 = per-class popcounts of
+ * n_layers arity-2 layers whose widths and device code arrays are given
+ * by the host arrays widths[n_layers] and codes[n_layers], then writes logits [B,C] fp32 = per-class popcounts of
  * the last layer (no tau). One workgroup keeps a 64-sample (or, for wide
  * layers, 32-sample) column of every activation in LDS across all layers.
  * wire_r > 0 replaces the first wire_r outputs of a same-width layer by its

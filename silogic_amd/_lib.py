@@ -36,7 +36,7 @@ SIGNATURES = {
     "slg_pack_bits": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_unpack_bits": (C.c_int, [_P, _I64, _I64, _P, _P]),
     "slg_fc_hard_prep": (C.c_int, [_P, _P, _I64, _I32, _I64, _I32, _P, _P, _P]),
-    "slg_fc_hard_prep_net": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "slg_fc_hard_prep_net": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P]),
     "slg_fc_hard_layer": (C.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "slg_fc_hard_net": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _I32, _I64, _P, _P]),
     "slg_fc_hard_net_supported": (C.c_int, [_I64, _I32, _P, _I32]),

@@ -12,10 +12,12 @@ namespace slg {
 
 template <typename WT>
 __device__ inline WT gate_word(WT a, WT b, uint32_t tt) {
-  const WT t0 = (WT)0 - (WT)(tt & 1u);
-  const WT t1 = (WT)0 - (WT)((tt >> 1) & 1u);
-  const WT t2 = (WT)0 - (WT)((tt >> 2) & 1u);
-  const WT t3 = (WT)0 - (WT)((tt >> 3) & 1u);
+  // T_g = all-ones iff tt bit g (sign-extending 1-bit field extract; the
+  // builtin's result type is unsigned, so widen through int)
+  const WT t0 = (WT)(int64_t)(int)__builtin_amdgcn_sbfe((int)tt, 0, 1);
+  const WT t1 = (WT)(int64_t)(int)__builtin_amdgcn_sbfe((int)tt, 1, 1);
+  const WT t2 = (WT)(int64_t)(int)__builtin_amdgcn_sbfe((int)tt, 2, 1);
+  const WT t3 = (WT)(int64_t)(int)__builtin_amdgcn_sbfe((int)tt, 3, 1);
   const WT hi = (b & t3) | (~b & t2);  // a = 1: addresses 3 (b=1), 2 (b=0)
   const WT lo = (b & t1) | (~b & t0);  // a = 0: addresses 1 (b=1), 0 (b=0)
   return (a & hi) | (~a & lo);
@@ -150,6 +152,7 @@ __global__ void fc_hard_prep_kernel(const int32_t* __restrict__ cand, const floa
 
 // Codes of several layers in one launch; each workgroup serves one layer.
 constexpr int kMaxPrepLayers = 16;
+constexpr int kMaxCompactIn = 1 << 14;
 struct HardPrepLayer {
   const int32_t* cand;
   const float* conn;
@@ -163,13 +166,21 @@ struct HardPrepNet {
   int n;
 };
 
-__global__ void __launch_bounds__(256) fc_hard_prep_net_kernel(HardPrepNet net) {
+// Compact code of the depth-fused network (inputs at most 16384 wide):
+// b | a << 14 | tt << 28, 4 bytes per output.
+__device__ inline uint32_t compact_code(uint2 c) {
+  return (c.y & 0x3FFFu) | ((c.x & 0x3FFFu) << 14) | (c.y & 0xF0000000u);
+}
+
+__global__ void __launch_bounds__(256) fc_hard_prep_net_kernel(HardPrepNet net, int compact) {
   int l = 0;
   while (l + 1 < net.n && (int)blockIdx.x >= net.blk_start[l + 1]) ++l;
   const HardPrepLayer& L = net.L[l];
   const int o = ((int)blockIdx.x - net.blk_start[l]) * blockDim.x + threadIdx.x;
   if (o >= L.out_dim) return;
-  L.codes[o] = hard_code(L.cand, L.conn, o, L.K, L.in_dim, L.node, L.raw);
+  const uint2 c = hard_code(L.cand, L.conn, o, L.K, L.in_dim, L.node, L.raw);
+  if (compact) reinterpret_cast<uint32_t*>(L.codes)[o] = compact_code(c);
+  else L.codes[o] = c;
 }
 
 // ---------------------------------------------------------------------------
@@ -201,32 +212,59 @@ __global__ void __launch_bounds__(256) fc_hard_layer_kernel(const uint64_t* __re
 constexpr int kMaxLayers = 16;
 constexpr int kNetThreads = 1024;
 struct NetDesc {
-  const uint2* codes[kMaxLayers];
+  const uint32_t* codes[kMaxLayers];  // compact codes, one word per output
   int width[kMaxLayers];
   int n_layers, in0, C, wire_r, maxw;
 };
 
 template <int MAXO>
-__device__ inline void load_codes(uint2 (&cb)[MAXO], const uint2* __restrict__ codes, int W) {
+__device__ inline void load_codes(uint32_t (&cb)[MAXO], const uint32_t* __restrict__ codes, int W) {
 #pragma unroll
   for (int j = 0; j < MAXO; ++j) {
     const int o = threadIdx.x + j * kNetThreads;
-    cb[j] = (o < W) ? codes[o] : make_uint2(0u, 0u);
+    cb[j] = codes[min(o, W - 1)];  // unconditional: exact wait counts
+  }
+}
+
+__device__ inline uint32_t bfi32(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }
+
+// gate16 on words from a compact code: T_g = all-ones iff tt bit g, read by
+// a sign-extending 1-bit field extract; out = a ? (b ? T3 : T2) : (b ? T1 : T0).
+template <typename WT>
+__device__ inline WT gate_compact(WT a, WT b, uint32_t c) {
+  const uint32_t t0 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 28, 1);
+  const uint32_t t1 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 29, 1);
+  const uint32_t t2 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 30, 1);
+  const uint32_t t3 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 31, 1);
+  if constexpr (sizeof(WT) == 8) {
+    const uint32_t al = (uint32_t)a, ah = (uint32_t)(a >> 32);
+    const uint32_t bl = (uint32_t)b, bh = (uint32_t)(b >> 32);
+    const uint32_t lo = bfi32(al, bfi32(bl, t3, t2), bfi32(bl, t1, t0));
+    const uint32_t hi = bfi32(ah, bfi32(bh, t3, t2), bfi32(bh, t1, t0));
+    return ((uint64_t)hi << 32) | lo;
+  } else {
+    return bfi32(a, bfi32(b, t3, t2), bfi32(b, t1, t0));
   }
 }
 
 // One layer on the LDS column: lds[nxt + o] = gate_o(lds[cur + a_o], lds[cur + b_o])
-// for this thread's outputs o = tid + j*1024. Whole rows of 1024 outputs take
-// a uniform branch; only row W/1024 tests o < W per lane.
+// for this thread's outputs o = tid + j*1024. Operand indices are clamped to
+// the layer's input width. Whole rows of 1024 outputs take a uniform branch;
+// only row W/1024 tests o < W per lane.
 template <typename WT, int MAXO>
-__device__ inline void layer_step(WT* lds, int cur, int nxt, int W, const uint2 (&cb)[MAXO]) {
+__device__ inline void layer_step(WT* lds, int cur, int nxt, int W, int in_w,
+                                  const uint32_t (&cb)[MAXO]) {
   const int nfull = W / kNetThreads;
+  const uint32_t lim = (uint32_t)in_w - 1u;
+  const WT* src = lds + cur;
 #pragma unroll
   for (int j = 0; j < MAXO; ++j) {
     const int o = threadIdx.x + j * kNetThreads;
     if (j < nfull || (j == nfull && o < W)) {
-      const uint2 c = cb[j];
-      lds[nxt + o] = gate_word<WT>(lds[cur + c.x], lds[cur + (c.y & 0x0FFFFFFFu)], c.y >> 28);
+      const uint32_t c = cb[j];
+      const uint32_t ia = min((c >> 14) & 0x3FFFu, lim);
+      const uint32_t ib = min(c & 0x3FFFu, lim);
+      lds[nxt + o] = gate_compact<WT>(src[ia], src[ib], c);
     }
   }
 }
@@ -275,7 +313,7 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
   WT* lds = reinterpret_cast<WT*>(smem);
   int* cnt = reinterpret_cast<int*>(lds + 2 * d.maxw);
   const int tile = blockIdx.x;
-  uint2 cb[MAXO];
+  uint32_t cb[MAXO];
   load_codes(cb, d.codes[0], d.width[0]);
   for (int i = threadIdx.x; i < d.C * 64; i += kNetThreads) cnt[i] = 0;
   const int w64 = tile / (64 / SPW);
@@ -288,9 +326,10 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
   int cur = 0, nxt = d.maxw, cur_w = d.in0;
   for (int l = 0; l < d.n_layers; ++l) {
     const int W = d.width[l];
-    uint2 nb[MAXO];
-    if (l + 1 < d.n_layers) load_codes(nb, d.codes[l + 1], d.width[l + 1]);
-    layer_step<WT, MAXO>(lds, cur, nxt, W, cb);
+    uint32_t nb[MAXO];
+    const int ln = (l + 1 < d.n_layers) ? l + 1 : l;
+    load_codes(nb, d.codes[ln], d.width[ln]);
+    layer_step<WT, MAXO>(lds, cur, nxt, W, cur_w, cb);
     if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
     __syncthreads();
     const int t = cur; cur = nxt; nxt = t;
@@ -304,18 +343,57 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
 // Unpacked rows [B][in0] (fp32, or uint8) with the packing fused: thread f
 // owns feature f (in0 <= 1024) and builds its 64-sample word with coalesced
 // row reads (lanes = consecutive features). Workgroups are persistent; the
-// next tile's rows stream in during the current tile's layers, one chunk of
-// samples per layer, issued after that layer's code prefetch so that waiting
-// for the codes never waits for input bytes (vector loads retire in order).
-// Addresses are clamped to valid rows/features and the bits masked after, so
-// the loads carry no per-lane branches.
+// next tile's rows stream in during the current tile's layers: layer l
+// issues chunk l (spl samples) and folds chunk l-2, so each chunk has two
+// layers of time to arrive from HBM; chunks are issued after the layer's
+// code prefetch so that waiting for codes never waits for input bytes
+// (vector loads retire in order). The rows are read through a raw buffer
+// resource spanning the tile's samples that exist: the hardware returns 0
+// for any offset past it (the padding samples of the last tile read as 0,
+// bit 0), so the loads need no clamps or branches.
 template <typename IT>
 __device__ inline bool input_bit(IT v) {
   if constexpr (sizeof(IT) == 1) return v != 0;
   else return v >= (IT)1;
 }
 
-template <typename IT, int MAXO, int SPL>
+constexpr int kBufferWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit data format
+
+template <typename IT>
+__device__ inline __amdgpu_buffer_rsrc_t tile_rows(const IT* x, int B, int in0, int b0) {
+  const int64_t rows = max(0, min(64, B - b0));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<IT*>(x + (int64_t)min(b0, B) * in0), (short)0,
+                                           (int)(rows * in0 * (int64_t)sizeof(IT)), kBufferWord3);
+}
+
+template <typename IT>
+__device__ inline IT load_row(__amdgpu_buffer_rsrc_t r, int voff) {
+  if constexpr (sizeof(IT) == 1) return (IT)__builtin_amdgcn_raw_buffer_load_b8(r, voff, 0, 0);
+  else return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+
+// The next tile streams as 4 chunks of 16 samples: chunk c is issued during
+// layer c and folded during layer c + 2 (or after the last layer); networks
+// with fewer than 4 layers load the remaining chunks after their last layer.
+constexpr int kChunk = 16, kChunks = 4;
+
+template <typename IT>
+__device__ inline void issue_chunk(IT (&val)[kChunk], __amdgpu_buffer_rsrc_t r, int voff0,
+                                   int rowb, int chunk) {
+  const int v = voff0 + chunk * kChunk * rowb;
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) val[j] = load_row<IT>(r, v + j * rowb);
+}
+
+template <typename IT>
+__device__ inline void fold_chunk(uint64_t& word, const IT (&val)[kChunk], int chunk) {
+  uint32_t bits = 0;
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) bits |= (input_bit(val[j]) ? 1u : 0u) << j;
+  word |= (uint64_t)bits << (chunk * kChunk);
+}
+
+template <typename IT, int MAXO>
 __global__ void __launch_bounds__(kNetThreads)
 fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
                         float* __restrict__ logits) {
@@ -324,49 +402,42 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
   int* cnt = reinterpret_cast<int*>(lds + 2 * d.maxw);
   const int f = threadIdx.x;
   const bool fv = f < d.in0;
-  const IT* xf = x + min(f, d.in0 - 1);
+  const int voff0 = f * (int)sizeof(IT);
+  const int rowb = d.in0 * (int)sizeof(IT);
   const int L = d.n_layers;
-  const int spl = min(SPL, (64 + L - 1) / L);  // samples streamed per layer
-
+  IT val0[kChunk], val1[kChunk];
   int tile = blockIdx.x;
   uint64_t word = 0;
-  for (int s0 = 0; s0 < 64; s0 += 16) {  // first tile: 16 loads in flight per batch
-    IT v[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = xf[(int64_t)min(tile * 64 + s0 + j, B - 1) * d.in0];
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (input_bit(v[j]) && tile * 64 + s0 + j < B) word |= 1ull << (s0 + j);
+  {
+    const __amdgpu_buffer_rsrc_t r = tile_rows(x, B, d.in0, tile * 64);
+    for (int c = 0; c < kChunks; ++c) {  // first tile
+      issue_chunk(val0, r, voff0, rowb, c);
+      fold_chunk(word, val0, c);
+    }
   }
-  uint2 cb[MAXO];
+  uint32_t cb[MAXO];
   load_codes(cb, d.codes[0], d.width[0]);
 
   for (; tile < n_tiles; tile += gridDim.x) {
     if (fv) lds[f] = word;
     for (int i = threadIdx.x; i < d.C * 64; i += kNetThreads) cnt[i] = 0;
     __syncthreads();
-    const int nb0 = (tile + gridDim.x) * 64;  // first sample of the next tile
+    const __amdgpu_buffer_rsrc_t r = tile_rows(x, B, d.in0, (tile + gridDim.x) * 64);
     uint64_t nword = 0;
-    IT val[SPL];
     int cur = 0, nxt = d.maxw, cur_w = d.in0;
     for (int l = 0; l < L; ++l) {
       const int W = d.width[l];
       const int ln = (l + 1 < L) ? l + 1 : 0;  // after the last layer: layer 0 of the next tile
-      uint2 nb[MAXO];
+      uint32_t nb[MAXO];
       load_codes(nb, d.codes[ln], d.width[ln]);
-      if (l > 0) {  // fold the chunk issued during the previous layer
-#pragma unroll
-        for (int j = 0; j < SPL; ++j) {
-          const int s = (l - 1) * spl + j;
-          if (j < spl && s < 64 && input_bit(val[j]) && nb0 + s < B) nword |= 1ull << s;
-        }
+      if (l & 1) {
+        if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val1, l - 2);
+        if (l < kChunks) issue_chunk(val1, r, voff0, rowb, l);
+      } else {
+        if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val0, l - 2);
+        if (l < kChunks) issue_chunk(val0, r, voff0, rowb, l);
       }
-#pragma unroll
-      for (int j = 0; j < SPL; ++j) {
-        const int s = l * spl + j;
-        if (j < spl && s < 64) val[j] = xf[(int64_t)min(nb0 + s, B - 1) * d.in0];
-      }
-      layer_step<uint64_t, MAXO>(lds, cur, nxt, W, cb);
+      layer_step<uint64_t, MAXO>(lds, cur, nxt, W, cur_w, cb);
       if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
       __syncthreads();
       const int t = cur; cur = nxt; nxt = t;
@@ -374,13 +445,14 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
 #pragma unroll
       for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
     }
-#pragma unroll
-    for (int j = 0; j < SPL; ++j) {
-      const int s = (L - 1) * spl + j;
-      if (j < spl && s < 64 && input_bit(val[j]) && nb0 + s < B) nword |= 1ull << s;
+    // chunks issued during the last two layers, then chunks no layer issued
+    for (int c = max(0, L - 2); c < min(L, kChunks); ++c) {
+      if (c & 1) fold_chunk(nword, val1, c);
+      else fold_chunk(nword, val0, c);
     }
-    for (int s = L * spl; s < 64; ++s) {  // samples left over when L * spl < 64
-      if (input_bit(xf[(int64_t)min(nb0 + s, B - 1) * d.in0]) && nb0 + s < B) nword |= 1ull << s;
+    for (int c = L; c < kChunks; ++c) {
+      issue_chunk(val0, r, voff0, rowb, c);
+      fold_chunk(nword, val0, c);
     }
     groupsum_tile<uint64_t>(lds + cur, cur_w, d.C, cnt, tile * 64, B, logits);
     __syncthreads();
@@ -475,7 +547,7 @@ static int launch_net_rows(const IT* x, int B, const NetDesc& d, size_t lds, flo
                            hipStream_t st) {
   const int64_t tiles = cdiv(B, 64);
   const int64_t grid = std::min<int64_t>(tiles, device_cus());
-  auto kern = fc_hard_net_rows_kernel<IT, MAXO, 16>;
+  auto kern = fc_hard_net_rows_kernel<IT, MAXO>;
   if (int rc = set_lds(kern, lds, "fc_hard_net_rows")) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kNetThreads), lds, st, x, B, (int)tiles, d,
                      logits);
@@ -553,8 +625,8 @@ int slg_fc_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_
 
 int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const float* const* conn,
                          const float* const* raw, const int64_t* in_dim, const int64_t* out_dim,
-                         const int32_t* K, const int32_t* node_kind, uint32_t* const* codes,
-                         slg_stream_t stream) {
+                         const int32_t* K, const int32_t* node_kind, int32_t compact,
+                         uint32_t* const* codes, slg_stream_t stream) {
   SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxPrepLayers, SLG_E_SHAPE,
               "fc_hard_prep_net: n_layers=%d outside 1..%d", n_layers, kMaxPrepLayers);
   SLG_REQUIRE(cand && conn && raw && in_dim && out_dim && K && node_kind && codes, SLG_E_ARG,
@@ -570,7 +642,10 @@ int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const flo
                 "fc_hard_prep_net: bad sizes, layer %d", l);
     SLG_REQUIRE(node_kind[l] >= 0 && node_kind[l] <= 2, SLG_E_ARG,
                 "fc_hard_prep_net: node_kind %d", node_kind[l]);
-    SLG_REQUIRE(((uintptr_t)codes[l] % 8) == 0, SLG_E_ARG, "fc_hard_prep_net: codes alignment");
+    SLG_REQUIRE(((uintptr_t)codes[l] % (compact ? 4 : 8)) == 0, SLG_E_ARG,
+                "fc_hard_prep_net: codes alignment");
+    SLG_REQUIRE(!compact || in_dim[l] <= kMaxCompactIn, SLG_E_SHAPE,
+                "fc_hard_prep_net: compact codes need inputs <= %d wide (layer %d)", kMaxCompactIn, l);
     net.L[l] = HardPrepLayer{cand[l], conn[l], raw[l], reinterpret_cast<uint2*>(codes[l]),
                              (int)in_dim[l], (int)out_dim[l], K[l], node_kind[l]};
     net.blk_start[l] = (int)blocks;
@@ -578,7 +653,7 @@ int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const flo
   }
   net.blk_start[n_layers] = (int)blocks;
   hipLaunchKernelGGL(fc_hard_prep_net_kernel, dim3((unsigned)blocks), dim3(th), 0,
-                     as_stream(stream), net);
+                     as_stream(stream), net, compact ? 1 : 0);
   SLG_LAUNCH_CHECK("fc_hard_prep_net");
   return 0;
 }
@@ -615,7 +690,7 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
   for (int l = 0; l < n_layers; ++l) {
     SLG_REQUIRE(codes[l] && widths[l] > 0 && widths[l] < (1LL << 28), SLG_E_ARG,
                 "fc_hard_net: layer %d", l);
-    d.codes[l] = reinterpret_cast<const uint2*>(codes[l]);
+    d.codes[l] = codes[l];
     d.width[l] = (int)widths[l];
   }
   SLG_REQUIRE(C > 0 && widths[n_layers - 1] % C == 0, SLG_E_SHAPE,

@@ -59,13 +59,15 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
     fused into it when the input is at most 1024 features wide; otherwise one
     packed kernel per layer."""
-    codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers])
-    widths = [c.shape[0] for c in codes]
+    specs = [layer.hard_spec() for layer in layers]
+    widths = [layer.out_dim for layer in layers]
     spw = ops.fc_hard_net_supported(in_dim, widths, C)
     if spw:
+        codes = ops.fc_hard_codes_net(specs, compact=True)
         if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
+    codes = ops.fc_hard_codes_net(specs)
     xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
     for c in codes:
         yp = ops.fc_hard_layer(xp, c)

@@ -352,10 +352,15 @@ def fc_hard_codes(cand, conn, raw, node_kind, in_dim):
     return codes
 
 
-def fc_hard_codes_net(specs):
+MAX_COMPACT_IN = 1 << 14
+
+
+def fc_hard_codes_net(specs, compact=False):
     """Codes of several layers, one launch per 16 layers. ``specs``:
     ``(cand, conn or None, raw, node_kind, in_dim)`` per layer, as
-    :func:`fc_hard_codes`. Returns ``[OUT, 2]`` int32 tensors."""
+    :func:`fc_hard_codes`. Returns ``[OUT, 2]`` int32 tensors, or with
+    ``compact`` the depth-fused network's ``[OUT]`` int32 codes
+    (b | a << 14 | tt << 28; inputs at most 16384 wide)."""
     out = []
     for g in range(0, len(specs), MAX_RECORD_LAYERS):
         part = specs[g:g + MAX_RECORD_LAYERS]
@@ -376,12 +381,13 @@ def fc_hard_codes_net(specs):
             outs.append(OUT)
             Ks.append(K)
             kinds.append(int(kind))
-        codes = [torch.empty((o, 2), device=raws[0].device, dtype=torch.int32) for o in outs]
+        shape = (lambda o: (o,)) if compact else (lambda o: (o, 2))
+        codes = [torch.empty(shape(o), device=raws[0].device, dtype=torch.int32) for o in outs]
         n = len(part)
         _lib.call("slg_fc_hard_prep_net", n, _ptrs(cands), _ptrs(conns), _ptrs(raws),
                   (ctypes.c_int64 * n)(*ins), (ctypes.c_int64 * n)(*outs),
-                  (ctypes.c_int32 * n)(*Ks), (ctypes.c_int32 * n)(*kinds), _ptrs(codes),
-                  _stream(raws[0]))
+                  (ctypes.c_int32 * n)(*Ks), (ctypes.c_int32 * n)(*kinds), int(bool(compact)),
+                  _ptrs(codes), _stream(raws[0]))
         out.extend(codes)
     return out
 
@@ -409,8 +415,11 @@ def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
     """Depth-fused packed FC network + GroupSum -> logits ``[B, C]``.
 
     ``in_kind``: ROWS_F32 / ROWS_U8 ([B, in_dim], packed inside the kernel),
-    PACKED ([in_dim, nw]) or PACKED_WORD_MAJOR ([nw, in_dim])."""
+    PACKED ([in_dim, nw]) or PACKED_WORD_MAJOR ([nw, in_dim]). ``codes``:
+    compact per-layer codes from ``fc_hard_codes_net(..., compact=True)``."""
     require_gpu(x, *codes)
+    if any(c.dim() != 1 or c.dtype != torch.int32 for c in codes):
+        raise ValueError("fc_hard_net: codes must be compact [OUT] int32 codes")
     widths = [c.shape[0] for c in codes]
     w_arr = (ctypes.c_int64 * len(widths))(*widths)
     c_arr = (ctypes.c_void_p * len(codes))(*[c.data_ptr() for c in codes])

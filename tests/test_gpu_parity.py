@@ -343,7 +343,14 @@ def test_fused_net_equals_layerwise_path_and_wide_32bit_tiles():
         x = random_bits(333, 200)
         xd = x.to(DEV)
         codes = [l.hard_codes() for l in model.layers]
+        ccodes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
+        for c, cc in zip(codes, ccodes):   # compact code = b | a << 14 | tt << 28
+            c, cc = c.cpu().long() & 0xFFFFFFFF, cc.cpu().long() & 0xFFFFFFFF
+            assert torch.equal(cc & 0x3FFF, c[:, 1] & 0x3FFF)
+            assert torch.equal((cc >> 14) & 0x3FFF, c[:, 0])
+            assert torch.equal(cc >> 28, c[:, 1] >> 28)
         outs = []
+        codes_l, codes = codes, ccodes
         if width == 1000:   # unpacked rows, packing fused (fp32 and uint8)
             outs.append(ops.fc_hard_net(xd, ops.ROWS_F32, 333, 200, codes, 10))
             outs.append(ops.fc_hard_net(xd.to(torch.uint8), ops.ROWS_U8, 333, 200, codes, 10))
@@ -351,7 +358,7 @@ def test_fused_net_equals_layerwise_path_and_wide_32bit_tiles():
         outs.append(ops.fc_hard_net(ops.pack_bits(xd, word_major=True), ops.PACKED_WORD_MAJOR,
                                     333, 200, codes, 10))
         xp = ops.pack_bits(xd)
-        for c in codes:
+        for c in codes_l:
             xp = ops.fc_hard_layer(xp, c)
         layerwise = ops.groupsum_packed(xp, 333, 10)
         ref = torch_ref.forward_hard(spec, sd, x)
@@ -363,7 +370,8 @@ def test_fused_net_equals_layerwise_path_and_wide_32bit_tiles():
 @pytest.mark.parametrize("depth", [1, 2, 3, 6])
 def test_fused_rows_kernel_many_tiles(depth):
     """More 64-sample tiles than CUs (persistent loop, streamed next-tile input)
-    and a ragged last tile; depths below 4 use the leftover-sample tail."""
+    and a ragged last tile; depths below 4 load the chunks no layer streamed
+    after the last layer."""
     spec = ("LogicNet", dict(in_dim=100, width=60, depth=depth, k=8))
     model = build_product(spec)
     sd = {k: v.clone() for k, v in model.state_dict().items()}
