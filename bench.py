@@ -15,7 +15,12 @@ kernel (HBM: it must read the fp32 input), with the bit-op view in
 ``cpu_baseline`` times the oracle (the reference's PyTorch CPU path restated)
 on a bounded sample on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs]
+``--config N`` measures BASELINE config N (1-5) the same way: its forward_hard
+and soft forward at the config's batch sizes, the dominant soft kernel (the
+widest FC layer, or the first conv block with its OrPool) and, for FC
+networks, the fused hard-network kernel.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N] [--no-cpu]
 """
 import argparse
 import json
@@ -51,14 +56,20 @@ def _events_ms(fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
-def cpu_baseline(sd, x_hard, x_soft, gates):
+# bounded CPU samples (hard samples, soft samples) per config: about 10-30 s of
+# CPU work at most, chunk sizes as BASELINE.md's CPU plan suggests
+CPU_SAMPLE = {1: (256, 256), 2: (4096, 512), 3: (64, 16), 4: (512, 128), 5: (64, 4)}
+
+
+def cpu_baseline(cfg, sd, x_hard, x_soft, gates):
     """Oracle (reference PyTorch CPU path) on bounded samples of the workload."""
     from oracle import torch_ref
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     from silogic_amd.synthetic import CONFIGS
-    spec = ("LogicNet", CONFIGS[2][1])
-    nh, ns = 4096, 512
+    spec = CONFIGS[cfg]
+    nh, ns = CPU_SAMPLE[cfg]
+    nh, ns = min(nh, x_hard.shape[0]), min(ns, x_soft.shape[0])
     xh, xs = x_hard[:nh].contiguous(), x_soft[:ns].contiguous()
 
     def timed(fn, reps=3):
@@ -82,8 +93,8 @@ def cpu_baseline(sd, x_hard, x_soft, gates):
     return {
         "value": round(nh * gates / th / 1e9, 4), "unit": "Ggate-evals/s",
         "cores": threads, "kind": "port",
-        "sample": (f"oracle forward_hard on {nh} of the 65536 hard samples (median of 3 "
-                   f"after 1 warm-up, spread {sh:.3f}s, {th:.3f}s each); soft forward on "
+        "sample": (f"oracle forward_hard on {nh} of the {x_hard.shape[0]} hard samples (median "
+                   f"of 3 after 1 warm-up, spread {sh:.3f}s, {th:.3f}s each); soft forward on "
                    f"{ns} samples: {ns / tsft:.1f} samples/s ({tsft:.3f}s, spread {ss:.3f}s)"),
         "soft_samples_per_s": round(ns / tsft, 2),
         "host": {"cpu": cpu, "os_cpu_count": os.cpu_count(), "torch": torch.__version__,
@@ -128,46 +139,72 @@ def kernels_only(reps=3):
     log("kernels-only done")
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--kernels-only", action="store_true",
-                    help="run only the copy calibration and the dominant kernels (for --pmc)")
-    args = ap.parse_args()
-    if args.kernels_only:
-        kernels_only()
-        return
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the workload shards by batch; see DESIGN.md). Run with --gpus 1.",
-              file=sys.stderr)
-        sys.exit(2)
+WORKLOADS = {
+    1: "cfg1: LogicNet(784, 2000, 4, gate16, TopK k=8, GroupSum 10, tau=10); forward_hard + "
+       "soft forward, B=256 Bernoulli(0.5)",
+    2: "cfg2: LogicNet(784, 10000, 6, gate16, TopK k=8, GroupSum 10, tau=10); forward_hard "
+       "B=65536 Bernoulli(0.2) + soft forward B=4096",
+    3: "cfg3: LogicTreeNet 28x28x7 (5 thermometer + 2 edge planes), channels [64,128,256], "
+       "gate16 trees depth 2, TopK k=4, OrPool, head [2560,2560], GroupSum 10; B=1024",
+    4: "cfg4: WARPNet(4096, 16380, 4, walsh, TopK k=8, GroupSum 10, tau=20); forward_hard + "
+       "soft forward, B=4096 Bernoulli(0.5)",
+    5: "cfg5: LogicConvNet 32x32x9 (3 channels x 3 thresholds), channels [128,256], "
+       "multilinear LUT6 trees depth 1, TopK k=4, OrPool, head [1280], GroupSum 10; B=512",
+}
 
+
+def dominant_soft_kernel(cfg, model, B_soft, x_soft, dev):
+    """(name, launch function, algorithmic bytes per launch) of the soft
+    kernel that dominates config ``cfg``'s forward: the widest FC layer on
+    records, or the first (largest) conv block with its OrPool."""
+    from silogic_amd import ops
+    if hasattr(model, "layers"):
+        L = model.layers[1] if len(model.layers) > 1 else model.layers[0]
+        x_mid = torch.rand(B_soft, L.in_dim, device=dev)
+        rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
+        K, OUT = L.n_candidates, L.out_dim
+        fn = lambda: ops.fc_soft_rec(x_mid, rec, OUT, K, L.node.kind, L._inv_tau())  # noqa: E731
+        nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * (K + 1)
+        name = f"fc_soft_kernel ({L._node_name}, K={K}, IN={L.in_dim}, OUT={OUT}, B={B_soft})"
+        return name, fn, nbytes
+    conv = model._convs()[0]
+    B, C, H, W = x_soft.shape
+    fn = lambda: conv.forward_pooled(x_soft)  # noqa: E731
+    nbytes = B * C * H * W * 4 + B * conv.n * (H // 2) * (W // 2) * 4
+    name = (f"conv_soft_kernel (block 0: {C}->{conv.n} channels, {H}x{W}, "
+            f"{conv.node_name}, pooled, B={B})")
+    return name, fn, nbytes
+
+
+def hard_units(cfg, model):
+    """Gate evaluations per sample (the reference's counts, models.py:103-104, 277-288)."""
+    if hasattr(model, "layers"):
+        return model.num_gates()
+    from silogic_amd.synthetic import CONFIGS
+    return model.gate_count(CONFIGS[cfg][1]["in_hw"])
+
+
+def measure(cfg, args):
     import silogic_amd as sl
     from silogic_amd import ops
     from silogic_amd.synthetic import build_config, config_inputs, BATCHES
 
     dev = torch.device("cuda:0")
-    log("building config 2 (seeded construction) ...")
-    model = build_config(2, sl).eval()
+    log(f"building config {cfg} (seeded construction) ...")
+    model = build_config(cfg, sl).eval()
     sd_cpu = {k: v.clone() for k, v in model.state_dict().items()}
     model = model.to(dev)
-    B_soft, B_hard, _, _ = BATCHES[2]
-    x_hard_cpu = config_inputs(2, B_hard)
+    B_soft, B_hard, _, _ = BATCHES[cfg]
+    x_hard_cpu = config_inputs(cfg, B_hard)
     x_hard = x_hard_cpu.to(dev)
     x_soft = x_hard[:B_soft].contiguous()
-    gates = model.num_gates()                       # 60000 per sample
+    gates = hard_units(cfg, model)
     torch.cuda.synchronize()
 
     def step():
         with torch.no_grad():
-            h = model.forward_hard(x_hard)
-            s = model(x_soft)
-        return h, s
+            model.forward_hard(x_hard)
+            model(x_soft)
 
     log(f"warmup {args.warmup} ...")
     for _ in range(args.warmup):
@@ -194,24 +231,28 @@ def main():
     log(f"step {wall / args.steps * 1e3:.3f} ms; hard {t_hard * 1e6:.1f} us; soft {t_soft * 1e6:.1f} us")
 
     # ---- dominant kernels alone, HIP events on the launch stream ----
+    reps = 20
+    hard = None
     with torch.no_grad():
-        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
-        reps = 20
-        fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, 784, codes, 10)  # noqa: E731
-        fn_net()
-        k_hard = _events_ms(fn_net, reps) / 1e3
-        L = model.layers[1]
-        x_mid = torch.rand(B_soft, 10000, device=dev)
-        rec = ops.fc_soft_records([L.record_spec()], 8)[0]
-        fn_soft = lambda: ops.fc_soft_rec(x_mid, rec, 10000, 8, ops.GATE16)          # noqa: E731
+        if hasattr(model, "layers"):
+            specs = [l.hard_spec() for l in model.layers]
+            widths = [l.out_dim for l in model.layers]
+            C = model.head.num_classes
+            in_dim = x_hard.shape[1]
+            if ops.fc_hard_net_supported(in_dim, widths, C) == 64 and in_dim <= 1024:
+                codes = ops.fc_hard_codes_net(specs, compact=True)
+                fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, in_dim, codes, C)  # noqa: E731
+                fn_net()
+                k_hard = _events_ms(fn_net, reps) / 1e3
+                hard_bytes = B_hard * in_dim * 4 + sum(w * 4 for w in widths) + B_hard * C * 4
+                hard = ("fc_hard_net_rows_kernel (packing + %d layers + GroupSum)" % len(widths),
+                        k_hard, hard_bytes)
+        name, fn_soft, soft_bytes = dominant_soft_kernel(cfg, model, B_soft, x_soft, dev)
         fn_soft()
         k_soft = _events_ms(fn_soft, reps) / 1e3
-    hard_bytes = B_hard * 784 * 4 + sum(c.numel() * 4 for c in codes) + B_hard * 10 * 4
-    soft_bytes = B_soft * 10000 * 4 * 2 + 10000 * 144
-    hard_gbs = hard_bytes / k_hard / 1e9
     soft_gbs = soft_bytes / k_soft / 1e9
-    bitops = B_hard * gates / k_hard
-    traffic = load_traffic()
+    traffic = load_traffic() if cfg == 2 else {}
+    bitops = B_hard * gates / t_hard
 
     result = {
         "metric": "hard-circuit Ggate-evals/s + soft fwd samples/s; % HBM/VALU roofline, 1 GPU",
@@ -226,32 +267,59 @@ def main():
         "vs_baseline": None,
         "dtype": "u64",
         "data": "synthetic",
-        "config": {"workload": "cfg2: LogicNet(784, 10000, 6, gate16, TopK k=8, GroupSum 10, "
-                               "tau=10); forward_hard B=65536 Bernoulli(0.2) + soft forward "
-                               "B=4096", "hard_batch": B_hard, "soft_batch": B_soft,
+        "config": {"workload": WORKLOADS[cfg], "hard_batch": B_hard, "soft_batch": B_soft,
                    "gates_per_sample": gates},
         "soft_samples_per_s": round(B_soft / t_soft, 1),
         "soft_dtype": "f32",
         "t_hard_us": round(t_hard * 1e6, 2),
         "t_soft_us": round(t_soft * 1e6, 2),
-        "roofline": {"kernel": "fc_hard_net_rows_kernel (packing + 6 layers + GroupSum)",
-                     "bound": "hbm", "achieved": round(hard_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("fc_hard_net_rows_kernel"),
-                     "algorithmic_bytes": hard_bytes,
-                     "avg_kernel_us": round(k_hard * 1e6, 2)},
-        "roofline_valu": {"kernel": "fc_hard_net_kernel", "achieved_bitops_per_s": bitops,
-                          "peak": VALU_BITOPS_PEAK, "frac": round(bitops / VALU_BITOPS_PEAK, 4)},
-        "roofline_soft": {"kernel": "fc_soft_kernel (gate16, K=8, IN=OUT=10000, B=4096)",
-                          "bound": "hbm", "achieved": round(soft_gbs, 1), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
-                          "traffic": traffic.get("fc_soft_kernel"),
-                          "algorithmic_bytes": soft_bytes, "avg_kernel_us": round(k_soft * 1e6, 2)},
     }
+    soft_roof = {"kernel": name, "bound": "hbm", "achieved": round(soft_gbs, 1),
+                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
+                 "traffic": traffic.get("fc_soft_kernel"), "algorithmic_bytes": soft_bytes,
+                 "avg_kernel_us": round(k_soft * 1e6, 2)}
+    if hard is not None:
+        hname, k_hard, hard_bytes = hard
+        hard_gbs = hard_bytes / k_hard / 1e9
+        result["roofline"] = {"kernel": hname, "bound": "hbm", "achieved": round(hard_gbs, 1),
+                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
+                              "traffic": traffic.get("fc_hard_net_rows_kernel"),
+                              "algorithmic_bytes": hard_bytes,
+                              "avg_kernel_us": round(k_hard * 1e6, 2)}
+        result["roofline_soft"] = soft_roof
+    else:
+        result["roofline"] = soft_roof
+    result["roofline_valu"] = {"kernel": "forward_hard (whole packed circuit)",
+                               "achieved_bitops_per_s": bitops, "peak": VALU_BITOPS_PEAK,
+                               "frac": round(bitops / VALU_BITOPS_PEAK, 4)}
     if not args.no_cpu:
         log("cpu baseline (oracle on host cores) ...")
-        result["cpu_baseline"] = cpu_baseline(sd_cpu, x_hard_cpu, x_hard_cpu[:B_soft], gates)
+        result["cpu_baseline"] = cpu_baseline(cfg, sd_cpu, x_hard_cpu, x_hard_cpu[:B_soft], gates)
     print(json.dumps(result), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
+                    help="BASELINE config to measure (default 2, the headline workload)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the copy calibration and the dominant kernels (for --pmc)")
+    args = ap.parse_args()
+    if args.kernels_only:
+        kernels_only()
+        return
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(the workload shards by batch; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    measure(args.config, args)
 
 
 if __name__ == "__main__":

@@ -27,7 +27,14 @@ constexpr int kMaxK = 8;
 
 // NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree) or
 // SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1).
-template <int NODE, int NLEAF, bool POOL>
+//
+// Work split: wave w takes output channels n = w, w + nwaves, ...; for each
+// channel it sets up the tap offsets, leaf weights and node parameters once
+// (wave-uniform, scalar registers) and then walks every chunk of 64
+// (sample, pooled position) pairs of the workgroup's S samples. A lane
+// evaluates the 2x2 window of its pooled position: for each tap, two LDS
+// reads of adjacent pairs (rows y and y+1), four FMAs.
+template <int NODE, int NLEAF, bool POOL, int KM>
 __global__ void __launch_bounds__(256)
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
                  int pad, const float* __restrict__ np, const float* __restrict__ wts,
@@ -35,49 +42,51 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
                  int S, float* __restrict__ out, int Ho, int Wo) {
   extern __shared__ float lds[];
   const int RS = W + pad;
-  const int plane = (H + 2 * pad) * RS + pad;
+  const int rows = H + 2 * pad;
+  const int plane = rows * RS + pad;
   const int SST = C * plane;
   const int b0 = blockIdx.x * S;
   const int ns = min(S, B - b0);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
 
-  for (int sc = 0; sc < ns * C; ++sc) {  // stage images, zero padding included
-    const float* src = x + ((int64_t)b0 * C + sc) * H * W;
-    float* dst = lds + sc * plane;
-    for (int q = threadIdx.x; q < plane; q += blockDim.x) {
-      const int yy = q / RS - pad;
-      const int xx = q - (yy + pad) * RS - pad;
-      float v = 0.0f;
-      if (yy >= 0 && yy < H && xx >= 0 && xx < W) v = src[yy * W + xx];
-      dst[q] = v;
+  // Stage the images: one padded row per wave step, lanes along the row.
+  // Row r of plane (s, c) holds input row r - pad at columns pad..pad+W-1;
+  // columns 0..pad-1 are the shared zero padding (also the right padding of
+  // the previous row), and each plane ends with pad zeros.
+  for (int r = wave; r < ns * C * rows; r += nwaves) {
+    const int sc = r / rows, yy = r - sc * rows - pad;
+    const float* src = x + ((int64_t)b0 * C + sc) * H * W + (int64_t)yy * W;
+    float* dst = lds + sc * plane + (yy + pad) * RS;
+    const bool row_in = yy >= 0 && yy < H;
+    for (int q = lane; q < RS; q += 64) {
+      const int xx = q - pad;
+      dst[q] = (row_in && xx >= 0) ? src[xx] : 0.0f;
     }
+    if (yy + pad == rows - 1 && lane < pad) lds[sc * plane + rows * RS + lane] = 0.0f;
   }
   __syncthreads();
 
   const int P = Ho * Wo;
-  const int per_n = (ns * P + 63) / 64;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int nchunks = (ns * P + 63) / 64;
   constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
   constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
 
-  for (int task = wave; task < N * per_n; task += nwaves) {
-    const int n = __builtin_amdgcn_readfirstlane(task / per_n);
-    const int sp = (task - n * per_n) * 64 + lane;
-    const bool active = sp < ns * P;
-    const int s = active ? sp / P : 0;
-    const int p = active ? sp - s * P : 0;
-    const int oy = (p / Wo) * (POOL ? 2 : 1);
-    const int ox = (p - (p / Wo) * Wo) * (POOL ? 2 : 1);
-    const int base = s * SST + oy * RS + ox;
-
-    int off[NLEAF][kMaxK];
-    float wt[NLEAF][kMaxK];
+  for (int n = wave; n < N; n += nwaves) {
+    // Channel parameters: the same for every lane, but loaded with a vector
+    // index so they live in VGPRs (there are too many for the scalar file,
+    // and an FMA can take only one scalar operand on gfx9).
+    int nv;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
+    int off[NLEAF][KM];
+    float wt[NLEAF][KM];
 #pragma unroll
     for (int l = 0; l < NLEAF; ++l) {
 #pragma unroll
-      for (int k = 0; k < kMaxK; ++k) {
+      for (int k = 0; k < KM; ++k) {
         if (k < K) {
-          const int idx = (n * NLEAF + l) * K + k;
+          const int idx = (nv * NLEAF + l) * K + k;
           const int c_ = min(max(cm[idx], 0), C - 1);
           const int h_ = min(max(ch[idx], 0), kernel - 1);
           const int w_ = min(max(cw[idx], 0), kernel - 1);
@@ -91,59 +100,86 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
     }
     float prm[NP];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) prm[i] = np[(int64_t)n * NP + i];
+    for (int i = 0; i < NP; ++i) prm[i] = np[(int64_t)nv * NP + i];
     float dif[(NODE == SLG_NODE_GATE16) ? 1 : (1 << (NLEAF - 1))];
     if constexpr (NODE != SLG_NODE_GATE16) {
 #pragma unroll
       for (int m = 0; m < (1 << (NLEAF - 1)); ++m) dif[m] = prm[2 * m + 1] - prm[2 * m];
     }
 
-    float best = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < (POOL ? 4 : 1); ++q) {
-      const int pb = base + (q >> 1) * RS + (q & 1);
-      float v[NLEAF];
+    for (int chunk = 0; chunk < nchunks; ++chunk) {
+      const int sp = chunk * 64 + lane;
+      const bool active = sp < ns * P;
+      const int s = active ? sp / P : 0;
+      const int p = active ? sp - s * P : 0;
+      const int py = p / Wo;
+      const int oy = py * (POOL ? 2 : 1);
+      const int ox = (p - py * Wo) * (POOL ? 2 : 1);
+      const float* base = lds + s * SST + oy * RS + ox;
+
+      constexpr int NQ = POOL ? 4 : 1;
+      float v[NQ][NLEAF];
 #pragma unroll
       for (int l = 0; l < NLEAF; ++l) {
-        float acc = 0.0f;
+        float acc[NQ];
 #pragma unroll
-        for (int k = 0; k < kMaxK; ++k)
-          if (k < K) acc = fmaf(wt[l][k], lds[pb + off[l][k]], acc);
-        v[l] = acc;
-      }
-      float val;
-      if constexpr (NODE == SLG_NODE_GATE16) {
-        // level i combines children 2m (a) and 2m+1 (b), node ids level-major
-        // (silogic/layers.py:388-401, 408-417)
-        int nb = 0;
+        for (int q = 0; q < NQ; ++q) acc[q] = 0.0f;
 #pragma unroll
-        for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
-#pragma unroll
-          for (int m = 0; m < cnt / 2; ++m) {
-            const float a = v[2 * m], b = v[2 * m + 1];
-            const float* c = prm + 4 * (nb + m);
-            v[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+        for (int k = 0; k < KM; ++k) {
+          if (k < K) {
+            const float* t0 = base + off[l][k];
+            acc[0] = fmaf(wt[l][k], t0[0], acc[0]);
+            if constexpr (POOL) {
+              const float* t1 = t0 + RS;
+              acc[1] = fmaf(wt[l][k], t0[1], acc[1]);
+              acc[2] = fmaf(wt[l][k], t1[0], acc[2]);
+              acc[3] = fmaf(wt[l][k], t1[1], acc[3]);
+            }
           }
-          nb += cnt / 2;
         }
-        val = v[0];
-      } else {
-        // multilinear interpolation of s over the leaves (corner bit j = leaf j),
-        // silogic/nodes.py:174-178, as a lerp tree
-        float t[1 << (NLEAF - 1)];
 #pragma unroll
-        for (int m = 0; m < (1 << (NLEAF - 1)); ++m) t[m] = fmaf(v[0], dif[m], prm[2 * m]);
-#pragma unroll
-        for (int j = 1; j < NLEAF; ++j) {
-#pragma unroll
-          for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
-            t[m] = fmaf(v[j], t[2 * m + 1] - t[2 * m], t[2 * m]);
-        }
-        val = t[0];
+        for (int q = 0; q < NQ; ++q) v[q][l] = acc[q];
       }
-      best = fmaxf(best, val);
+      float best = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        float val;
+        if constexpr (NODE == SLG_NODE_GATE16) {
+          // level i combines children 2m (a) and 2m+1 (b), node ids level-major
+          // (silogic/layers.py:388-401, 408-417)
+          float u[NLEAF];
+#pragma unroll
+          for (int l = 0; l < NLEAF; ++l) u[l] = v[q][l];
+          int nb = 0;
+#pragma unroll
+          for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
+#pragma unroll
+            for (int m = 0; m < cnt / 2; ++m) {
+              const float a = u[2 * m], b = u[2 * m + 1];
+              const float* c = prm + 4 * (nb + m);
+              u[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+            }
+            nb += cnt / 2;
+          }
+          val = u[0];
+        } else {
+          // multilinear interpolation of s over the leaves (corner bit j =
+          // leaf j), silogic/nodes.py:174-178, as a lerp tree
+          float t[1 << (NLEAF - 1)];
+#pragma unroll
+          for (int m = 0; m < (1 << (NLEAF - 1)); ++m) t[m] = fmaf(v[q][0], dif[m], prm[2 * m]);
+#pragma unroll
+          for (int j = 1; j < NLEAF; ++j) {
+#pragma unroll
+            for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
+              t[m] = fmaf(v[q][j], t[2 * m + 1] - t[2 * m], t[2 * m]);
+          }
+          val = t[0];
+        }
+        best = fmaxf(best, val);
+      }
+      if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
     }
-    if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
   }
 }
 
@@ -326,21 +362,23 @@ struct ConvSoftArgs {
   float* out; int64_t Ho, Wo;
 };
 
-template <int NODE, int NLEAF, bool POOL>
-static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
+template <int NODE, int NLEAF, bool POOL, int KM>
+static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
   const int64_t per_sample = a.C * plane * 4;
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
   SLG_REQUIRE(per_sample <= cap, SLG_E_UNSUPPORTED, "conv_soft: one image (%lld B) exceeds LDS",
               (long long)per_sample);
-  // samples per workgroup: enough (sample, position) pairs for a wave, while
-  // keeping at least 2 workgroups per CU when the image is small
+  // samples per workgroup: whole 64-lane chunks of (sample, position) pairs
+  // where the images are small, up to half the LDS so that two workgroups
+  // share a CU, and enough workgroups to fill the chip
   const int64_t P = a.Ho * a.Wo;
-  int64_t S = std::max<int64_t>(1, cdiv(64, P));
-  S = std::min<int64_t>(S, std::max<int64_t>(1, cap / per_sample));
+  int64_t S = std::max<int64_t>(1, cdiv(128, P));
+  S = std::min<int64_t>(S, std::max<int64_t>(1, cap / 2 / per_sample));
+  S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / (2 * device_cus())));
   S = std::min<int64_t>(S, a.B);
   const size_t lds = (size_t)(S * per_sample);
-  auto kern = conv_soft_kernel<NODE, NLEAF, POOL>;
+  auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -354,6 +392,13 @@ static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
                      a.ch, a.cw, (int)S, a.out, (int)a.Ho, (int)a.Wo);
   SLG_LAUNCH_CHECK("conv_soft");
   return 0;
+}
+
+template <int NODE, int NLEAF, bool POOL>
+static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
+  // taps per leaf: 4 registers when K <= 4 (TopK k=4, fixed wiring), else 8
+  return a.K <= 4 ? launch_conv_soft_k<NODE, NLEAF, POOL, 4>(a, st)
+                  : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK>(a, st);
 }
 
 template <bool POOL>

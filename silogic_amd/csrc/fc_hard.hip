@@ -214,16 +214,22 @@ constexpr int kNetThreads = 1024;
 struct NetDesc {
   const uint32_t* codes[kMaxLayers];  // compact codes, one word per output
   int width[kMaxLayers];
-  int n_layers, in0, C, wire_r, maxw;
+  int n_layers, in0, C, wire_r;
+  int maxw;  // words per activation buffer: the widest layer + kGuard
 };
 
+constexpr int kBufferWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit data format
+
+// Codes of this thread's outputs o = tid + j*1024 of a W-wide layer, read
+// through a raw buffer resource of W codes: offsets past it read 0 (a valid
+// code), so the loads need no clamp.
 template <int MAXO>
 __device__ inline void load_codes(uint32_t (&cb)[MAXO], const uint32_t* __restrict__ codes, int W) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(codes), (short)0, W * 4, kBufferWord3);
+  const int v = threadIdx.x * 4;
 #pragma unroll
-  for (int j = 0; j < MAXO; ++j) {
-    const int o = threadIdx.x + j * kNetThreads;
-    cb[j] = codes[min(o, W - 1)];  // unconditional: exact wait counts
-  }
+  for (int j = 0; j < MAXO; ++j) cb[j] = __builtin_amdgcn_raw_buffer_load_b32(r, v + j * kNetThreads * 4, 0, 0);
 }
 
 __device__ inline uint32_t bfi32(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }
@@ -248,23 +254,47 @@ __device__ inline WT gate_compact(WT a, WT b, uint32_t c) {
 }
 
 // One layer on the LDS column: lds[nxt + o] = gate_o(lds[cur + a_o], lds[cur + b_o])
-// for this thread's outputs o = tid + j*1024. Operand indices are clamped to
-// the layer's input width. Whole rows of 1024 outputs take a uniform branch;
-// only row W/1024 tests o < W per lane.
-template <typename WT, int MAXO>
+// for this thread's outputs o = tid + j*1024, in groups of GRP outputs: all
+// operand reads of a group are issued before its results are computed
+// (operand indices are clamped to the layer's input width), so the LDS
+// latency of a thread's gates overlaps; the group's gate math runs between
+// its reads and its writes, with no LDS access in between. Lanes of the last,
+// partial row past W write to a per-lane guard word after the layer's
+// outputs (kGuard words follow each buffer) instead of being masked off.
+constexpr int kGuard = 64;
+
+template <typename WT, int MAXO, int GRP>
 __device__ inline void layer_step(WT* lds, int cur, int nxt, int W, int in_w,
                                   const uint32_t (&cb)[MAXO]) {
+  static_assert(MAXO % GRP == 0, "groups must tile MAXO");
+  const int rows = (W + kNetThreads - 1) / kNetThreads;
   const int nfull = W / kNetThreads;
   const uint32_t lim = (uint32_t)in_w - 1u;
   const WT* src = lds + cur;
+  const int guard = W + (int)(threadIdx.x & 63);
 #pragma unroll
-  for (int j = 0; j < MAXO; ++j) {
-    const int o = threadIdx.x + j * kNetThreads;
-    if (j < nfull || (j == nfull && o < W)) {
-      const uint32_t c = cb[j];
-      const uint32_t ia = min((c >> 14) & 0x3FFFu, lim);
-      const uint32_t ib = min(c & 0x3FFFu, lim);
-      lds[nxt + o] = gate_compact<WT>(src[ia], src[ib], c);
+  for (int g0 = 0; g0 < MAXO; g0 += GRP) {
+    WT va[GRP] = {}, vb[GRP] = {};
+#pragma unroll
+    for (int u = 0; u < GRP; ++u) {
+      if (g0 + u < rows) {
+        const uint32_t c = cb[g0 + u];
+        va[u] = src[min((c >> 14) & 0x3FFFu, lim)];
+        vb[u] = src[min(c & 0x3FFFu, lim)];
+      }
+    }
+    // all gate math, then all writes: no LDS access between the computes
+    WT r[GRP];
+#pragma unroll
+    for (int u = 0; u < GRP; ++u) r[u] = gate_compact<WT>(va[u], vb[u], cb[g0 + u]);
+#pragma unroll
+    for (int u = 0; u < GRP; ++u) {
+      const int j = g0 + u;
+      if (j < rows) {
+        const int o = threadIdx.x + j * kNetThreads;
+        if (j < nfull) lds[nxt + o] = r[u];
+        else lds[nxt + (o < W ? o : guard)] = r[u];
+      }
     }
   }
 }
@@ -329,7 +359,7 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
     uint32_t nb[MAXO];
     const int ln = (l + 1 < d.n_layers) ? l + 1 : l;
     load_codes(nb, d.codes[ln], d.width[ln]);
-    layer_step<WT, MAXO>(lds, cur, nxt, W, cur_w, cb);
+    layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cur_w, cb);
     if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
     __syncthreads();
     const int t = cur; cur = nxt; nxt = t;
@@ -356,8 +386,6 @@ __device__ inline bool input_bit(IT v) {
   if constexpr (sizeof(IT) == 1) return v != 0;
   else return v >= (IT)1;
 }
-
-constexpr int kBufferWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit data format
 
 template <typename IT>
 __device__ inline __amdgpu_buffer_rsrc_t tile_rows(const IT* x, int B, int in0, int b0) {
@@ -437,7 +465,7 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
         if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val0, l - 2);
         if (l < kChunks) issue_chunk(val0, r, voff0, rowb, l);
       }
-      layer_step<uint64_t, MAXO>(lds, cur, nxt, W, cur_w, cb);
+      layer_step<uint64_t, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(lds, cur, nxt, W, cur_w, cb);
       if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
       __syncthreads();
       const int t = cur; cur = nxt; nxt = t;
@@ -493,11 +521,11 @@ static int net_spw(int64_t IN0, int n_layers, const int64_t* widths, int C) {
   if (!widths || n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
   int64_t maxw = IN0;
   for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
-  maxw = (maxw + 1) & ~1LL;
   if (maxw > 16 * kNetThreads) return 0;
+  const int64_t words = ((maxw + 1) & ~1LL) + kGuard;  // per activation buffer
   const int64_t lds = device_lds_bytes();
-  if (2 * maxw * 8 + (int64_t)C * 256 <= lds) return 64;
-  if (2 * maxw * 4 + (int64_t)C * 256 <= lds) return 32;
+  if (2 * words * 8 + (int64_t)C * 256 <= lds) return 64;
+  if (2 * words * 4 + (int64_t)C * 256 <= lds) return 32;
   return 0;
 }
 
@@ -706,7 +734,7 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
   d.n_layers = n_layers; d.in0 = (int)IN0; d.C = C; d.wire_r = (int)std::max<int64_t>(0, wire_r);
   int64_t maxw = IN0;
   for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
-  d.maxw = (int)((maxw + 1) & ~1LL);
+  d.maxw = (int)(((maxw + 1) & ~1LL) + kGuard);
   const int maxo = pick_maxo(maxw);
   SLG_REQUIRE(maxo > 0, SLG_E_UNSUPPORTED, "fc_hard_net: width too large");
   const size_t lds = (size_t)2 * d.maxw * (spw / 8) + (size_t)C * 256;

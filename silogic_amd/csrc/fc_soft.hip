@@ -661,8 +661,8 @@ __global__ void __launch_bounds__(256) fc_soft_records_kernel(RecNet net) {
 // each output reads each of its K candidates so that few reads of one step
 // share a bank: a greedy pass per step (least-used bank first, ties to the
 // bank with the most reads left), then pairwise step swaps within a lane
-// while they lower the summed per-step maximum. The sum over k is the same;
-// only the fp32 summation order changes.
+// that even out the per-step bank counts. The sum over k is the same; only
+// the fp32 summation order changes.
 template <int N>
 __global__ void __launch_bounds__(64) fc_soft_schedule_kernel(const int* __restrict__ cand, int OUT,
                                                               int K, uint8_t* __restrict__ order) {
@@ -700,11 +700,9 @@ __global__ void __launch_bounds__(64) fc_soft_schedule_kernel(const int* __restr
       --demand[bank[l][best]];
     }
   }
-  auto step_max = [&](int st) {
-    int m = 0;
-    for (int b = 0; b < N; ++b) m = max(m, (int)cnt[st][b]);
-    return m;
-  };
+  // Pairwise step swaps within a lane while they lower the sum of squared
+  // per-step bank counts of the two steps (O(1) per test; spreading the
+  // counts evenly lowers their maxima).
   for (int pass = 0; pass < 8; ++pass) {
     bool improved = false;
     for (int l = 0; l < n; ++l)
@@ -712,15 +710,12 @@ __global__ void __launch_bounds__(64) fc_soft_schedule_kernel(const int* __restr
         for (int t2 = t1 + 1; t2 < K; ++t2) {
           const int b1 = bank[l][ord[l][t1]], b2 = bank[l][ord[l][t2]];
           if (b1 == b2) continue;
-          const int before = step_max(t1) + step_max(t2);
-          --cnt[t1][b1]; ++cnt[t1][b2]; --cnt[t2][b2]; ++cnt[t2][b1];
-          if (step_max(t1) + step_max(t2) < before) {
+          if ((int)cnt[t1][b2] - (int)cnt[t1][b1] + (int)cnt[t2][b1] - (int)cnt[t2][b2] + 2 < 0) {
+            --cnt[t1][b1]; ++cnt[t1][b2]; --cnt[t2][b2]; ++cnt[t2][b1];
             const uint8_t tmp = ord[l][t1];
             ord[l][t1] = ord[l][t2];
             ord[l][t2] = tmp;
             improved = true;
-          } else {
-            ++cnt[t1][b1]; --cnt[t1][b2]; ++cnt[t2][b2]; --cnt[t2][b1];
           }
         }
     if (!improved) break;
