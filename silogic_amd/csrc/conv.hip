@@ -27,19 +27,105 @@ constexpr int kMaxK = 8;
 
 // NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree) or
 // SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1).
-//
+template <int NODE, int NLEAF>
+struct ConvNode {
+  static constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
+  // parameters kept per channel: gate16 coefficients [NN][4], or for the LUT
+  // the even corner values s[2m] and the differences s[2m+1] - s[2m]
+  static constexpr int NPR = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
+  static constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);  // raw params
+};
+
+// One output channel's parameters in registers: LDS tap offsets, leaf
+// weights and node parameters.
+template <int NODE, int NLEAF, int KM>
+struct ConvParams {
+  int off[NLEAF][KM];
+  float wt[NLEAF][KM];
+  float par[ConvNode<NODE, NLEAF>::NPR];
+};
+
+// Record of one channel (slg_conv_soft_records): the fields of ConvParams in
+// order, padded to a multiple of 4 floats.
+template <int NODE, int NLEAF, int KM>
+constexpr int conv_rec_floats() {
+  return (2 * NLEAF * KM + ConvNode<NODE, NLEAF>::NPR + 3) & ~3;
+}
+
+// Channel parameters from separate arrays (slg_conv_soft_fwd). The index nv
+// is a vector register (the same value in every lane), so the loads are
+// vector loads and the parameters stay in VGPRs: there are too many for the
+// scalar file, and an FMA takes one scalar operand on gfx9.
+template <int NODE, int NLEAF, int KM>
+__device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM>& P, int nv, int K, int C,
+                                          int kernel, int plane, int RS, const float* np,
+                                          const float* wts, const int* cm, const int* ch,
+                                          const int* cw) {
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l) {
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      if (k < K) {
+        const int idx = (nv * NLEAF + l) * K + k;
+        const int c_ = min(max(cm[idx], 0), C - 1);
+        const int h_ = min(max(ch[idx], 0), kernel - 1);
+        const int w_ = min(max(cw[idx], 0), kernel - 1);
+        P.off[l][k] = c_ * plane + h_ * RS + w_;
+        P.wt[l][k] = wts ? wts[idx] : 1.0f;
+      } else {
+        P.off[l][k] = 0;
+        P.wt[l][k] = 0.0f;
+      }
+    }
+  }
+  constexpr int NP = ConvNode<NODE, NLEAF>::NP;
+  if constexpr (NODE == SLG_NODE_GATE16) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) P.par[i] = np[(int64_t)nv * NP + i];
+  } else {
+    constexpr int H2 = 1 << (NLEAF - 1);
+#pragma unroll
+    for (int m = 0; m < H2; ++m) {
+      const float e = np[(int64_t)nv * NP + 2 * m], o = np[(int64_t)nv * NP + 2 * m + 1];
+      P.par[m] = e;
+      P.par[H2 + m] = o - e;
+    }
+  }
+}
+
+// Channel parameters from a record: contiguous 16-byte vector loads.
+template <int NODE, int NLEAF, int KM>
+__device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM>& P, const float* rec, int nv) {
+  constexpr int R = conv_rec_floats<NODE, NLEAF, KM>();
+  float v[R];
+  const float4* r4 = reinterpret_cast<const float4*>(rec + (int64_t)nv * R);
+#pragma unroll
+  for (int q = 0; q < R / 4; ++q) {
+    const float4 t = r4[q];
+    v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+  }
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      P.off[l][k] = __float_as_int(v[l * KM + k]);
+      P.wt[l][k] = v[NLEAF * KM + l * KM + k];
+    }
+#pragma unroll
+  for (int i = 0; i < ConvNode<NODE, NLEAF>::NPR; ++i) P.par[i] = v[2 * NLEAF * KM + i];
+}
+
 // Work split: wave w takes output channels n = w, w + nwaves, ...; for each
-// channel it sets up the tap offsets, leaf weights and node parameters once
-// (wave-uniform, scalar registers) and then walks every chunk of 64
-// (sample, pooled position) pairs of the workgroup's S samples. A lane
+// channel it holds the channel's parameters in registers and walks every chunk
+// of 64 (sample, pooled position) pairs of the workgroup's S samples. A lane
 // evaluates the 2x2 window of its pooled position: for each tap, two LDS
 // reads of adjacent pairs (rows y and y+1), four FMAs.
-template <int NODE, int NLEAF, bool POOL, int KM>
+template <int NODE, int NLEAF, bool POOL, int KM, bool REC>
 __global__ void __launch_bounds__(256)
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
                  int pad, const float* __restrict__ np, const float* __restrict__ wts,
                  const int* __restrict__ cm, const int* __restrict__ ch, const int* __restrict__ cw,
-                 int S, float* __restrict__ out, int Ho, int Wo) {
+                 const float* __restrict__ rec, int S, float* __restrict__ out, int Ho, int Wo) {
   extern __shared__ float lds[];
   const int RS = W + pad;
   const int rows = H + 2 * pad;
@@ -51,61 +137,68 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
 
-  // Stage the images: one padded row per wave step, lanes along the row.
-  // Row r of plane (s, c) holds input row r - pad at columns pad..pad+W-1;
-  // columns 0..pad-1 are the shared zero padding (also the right padding of
-  // the previous row), and each plane ends with pad zeros.
-  for (int r = wave; r < ns * C * rows; r += nwaves) {
-    const int sc = r / rows, yy = r - sc * rows - pad;
-    const float* src = x + ((int64_t)b0 * C + sc) * H * W + (int64_t)yy * W;
-    float* dst = lds + sc * plane + (yy + pad) * RS;
-    const bool row_in = yy >= 0 && yy < H;
-    for (int q = lane; q < RS; q += 64) {
-      const int xx = q - pad;
-      dst[q] = (row_in && xx >= 0) ? src[xx] : 0.0f;
+  // Stage the images. Plane (s, c) holds row r - pad of the input in row r
+  // at columns pad..pad+W-1; columns 0..pad-1 are the shared zero padding
+  // (also the right padding of the previous row), rows 0..pad-1 and
+  // H+pad..rows-1 are zero, and each plane ends with pad zeros. The ns*C*H*W
+  // input floats are contiguous: every thread issues kStage loads before it
+  // writes them, so that the copy is not one load latency per row.
+  {
+    const int HW = H * W;
+    const int total = ns * C * HW;
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + (int64_t)b0 * C * HW), (short)0, total * 4, kBufferWord3);
+    const float inv_hw = 1.0f / (float)HW, inv_w = 1.0f / (float)W;
+    constexpr int kStage = 8;
+    for (int e0 = threadIdx.x; e0 < total; e0 += kStage * blockDim.x) {
+      float v[kStage];
+#pragma unroll
+      for (int u = 0; u < kStage; ++u)  // offsets past the images read 0
+        v[u] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(src, (e0 + u * (int)blockDim.x) * 4, 0, 0));
+#pragma unroll
+      for (int u = 0; u < kStage; ++u) {
+        const int e = e0 + u * (int)blockDim.x;
+        const int sc = div_small(e, HW, inv_hw);
+        const int rem = e - sc * HW;
+        const int r = div_small(rem, W, inv_w);
+        if (e < total) lds[sc * plane + (r + pad) * RS + pad + (rem - r * W)] = v[u];
+      }
     }
-    if (yy + pad == rows - 1 && lane < pad) lds[sc * plane + rows * RS + lane] = 0.0f;
+    // zero slots of one plane: top rows, bottom rows, left pads, tail
+    const int ztop = pad * RS, zleft = H * pad;
+    const int Z = 2 * ztop + zleft + pad;
+    const float inv_z = 1.0f / (float)max(Z, 1), inv_pad = 1.0f / (float)max(pad, 1);
+    for (int z = threadIdx.x; z < ns * C * Z; z += blockDim.x) {
+      const int sc = div_small(z, Z, inv_z);
+      int k = z - sc * Z, at;
+      if (k < 2 * ztop) {
+        at = k < ztop ? k : (H + pad) * RS + (k - ztop);
+      } else if ((k -= 2 * ztop) < zleft) {
+        const int r = div_small(k, pad, inv_pad);
+        at = (r + pad) * RS + (k - r * pad);
+      } else {
+        at = rows * RS + (k - zleft);
+      }
+      lds[sc * plane + at] = 0.0f;
+    }
   }
   __syncthreads();
 
   const int P = Ho * Wo;
   const int nchunks = (ns * P + 63) / 64;
-  constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
-  constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
+  constexpr int H2 = (NODE == SLG_NODE_GATE16) ? 1 : (1 << (NLEAF - 1));
 
-  for (int n = wave; n < N; n += nwaves) {
-    // Channel parameters: the same for every lane, but loaded with a vector
-    // index so they live in VGPRs (there are too many for the scalar file,
-    // and an FMA can take only one scalar operand on gfx9).
-    int nv;
+  auto load = [&](ConvParams<NODE, NLEAF, KM>& Pr, int n) {
+    int nv;  // the channel in a vector register: vector loads, VGPR parameters
     asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
-    int off[NLEAF][KM];
-    float wt[NLEAF][KM];
-#pragma unroll
-    for (int l = 0; l < NLEAF; ++l) {
-#pragma unroll
-      for (int k = 0; k < KM; ++k) {
-        if (k < K) {
-          const int idx = (nv * NLEAF + l) * K + k;
-          const int c_ = min(max(cm[idx], 0), C - 1);
-          const int h_ = min(max(ch[idx], 0), kernel - 1);
-          const int w_ = min(max(cw[idx], 0), kernel - 1);
-          off[l][k] = c_ * plane + h_ * RS + w_;
-          wt[l][k] = wts ? wts[idx] : 1.0f;
-        } else {
-          off[l][k] = 0;
-          wt[l][k] = 0.0f;
-        }
-      }
-    }
-    float prm[NP];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) prm[i] = np[(int64_t)nv * NP + i];
-    float dif[(NODE == SLG_NODE_GATE16) ? 1 : (1 << (NLEAF - 1))];
-    if constexpr (NODE != SLG_NODE_GATE16) {
-#pragma unroll
-      for (int m = 0; m < (1 << (NLEAF - 1)); ++m) dif[m] = prm[2 * m + 1] - prm[2 * m];
-    }
+    if constexpr (REC) conv_params_record<NODE, NLEAF, KM>(Pr, rec, nv);
+    else conv_params_arrays<NODE, NLEAF, KM>(Pr, nv, K, C, kernel, plane, RS, np, wts, cm, ch, cw);
+  };
+
+  ConvParams<NODE, NLEAF, KM> Pc;
+  if (wave < N) load(Pc, wave);
+  for (int n = wave; n < N; n += nwaves) {
 
     for (int chunk = 0; chunk < nchunks; ++chunk) {
       const int sp = chunk * 64 + lane;
@@ -127,13 +220,13 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
           if (k < K) {
-            const float* t0 = base + off[l][k];
-            acc[0] = fmaf(wt[l][k], t0[0], acc[0]);
+            const float* t0 = base + Pc.off[l][k];
+            acc[0] = fmaf(Pc.wt[l][k], t0[0], acc[0]);
             if constexpr (POOL) {
               const float* t1 = t0 + RS;
-              acc[1] = fmaf(wt[l][k], t0[1], acc[1]);
-              acc[2] = fmaf(wt[l][k], t1[0], acc[2]);
-              acc[3] = fmaf(wt[l][k], t1[1], acc[3]);
+              acc[1] = fmaf(Pc.wt[l][k], t0[1], acc[1]);
+              acc[2] = fmaf(Pc.wt[l][k], t1[0], acc[2]);
+              acc[3] = fmaf(Pc.wt[l][k], t1[1], acc[3]);
             }
           }
         }
@@ -156,7 +249,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
 #pragma unroll
             for (int m = 0; m < cnt / 2; ++m) {
               const float a = u[2 * m], b = u[2 * m + 1];
-              const float* c = prm + 4 * (nb + m);
+              const float* c = Pc.par + 4 * (nb + m);
               u[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
             }
             nb += cnt / 2;
@@ -165,9 +258,9 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
         } else {
           // multilinear interpolation of s over the leaves (corner bit j =
           // leaf j), silogic/nodes.py:174-178, as a lerp tree
-          float t[1 << (NLEAF - 1)];
+          float t[H2];
 #pragma unroll
-          for (int m = 0; m < (1 << (NLEAF - 1)); ++m) t[m] = fmaf(v[q][0], dif[m], prm[2 * m]);
+          for (int m = 0; m < H2; ++m) t[m] = fmaf(v[q][0], Pc.par[H2 + m], Pc.par[m]);
 #pragma unroll
           for (int j = 1; j < NLEAF; ++j) {
 #pragma unroll
@@ -180,6 +273,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       }
       if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
     }
+    if (n + nwaves < N) load(Pc, n + nwaves);
   }
 }
 
@@ -302,6 +396,78 @@ __global__ void conv_soft_prep_kernel(const float* __restrict__ conn, int N, int
   }
 }
 
+// Per-channel records for conv_soft_kernel<..., REC = true>, R floats per
+// channel: [0, L*KM) LDS offsets of the KM taps of every leaf (clamped taps;
+// taps k >= K get offset 0 and weight 0), [L*KM, 2*L*KM) softmax leaf
+// weights, then the node parameters (gate16: softmax(logits) @ BASIS per
+// node; LUT: sigmoid(s) of the even corners, then odd - even differences),
+// zeros to R. One thread per record word, so that the loads of different
+// words overlap.
+__global__ void conv_soft_records_kernel(const float* __restrict__ conn, const int* __restrict__ cm,
+                                         const int* __restrict__ ch, const int* __restrict__ cw,
+                                         int N, int leaves, int K, int KM, int node, int arity,
+                                         const float* __restrict__ raw, int C, int kernel,
+                                         int plane, int RS, int R, float* __restrict__ rec) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)N * R) return;
+  const int n = (int)(t / R), slot = (int)(t - (int64_t)n * R);
+  const int LK = leaves * KM;
+  float v = 0.0f;
+  if (slot < 2 * LK) {
+    const int lk = slot < LK ? slot : slot - LK;
+    const int l = lk / KM, k = lk - l * KM;
+    const int64_t base = ((int64_t)n * leaves + l) * K;
+    if (k < K) {
+      if (slot < LK) {
+        const int c_ = min(max(cm[base + k], 0), C - 1);
+        const int h_ = min(max(ch[base + k], 0), kernel - 1);
+        const int w_ = min(max(cw[base + k], 0), kernel - 1);
+        v = __int_as_float(c_ * plane + h_ * RS + w_);
+      } else if (!conn) {
+        v = 1.0f;
+      } else {
+        float c[kMaxK];
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j) c[j] = j < K ? conn[base + j] : -INFINITY;
+        float m = c[0];
+#pragma unroll
+        for (int j = 1; j < kMaxK; ++j) m = fmaxf(m, c[j]);
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j) sum += j < K ? expf(c[j] - m) : 0.f;
+        v = expf(conn[base + k] - m) / sum;
+      }
+    }
+  } else if (node == SLG_NODE_GATE16) {
+    const int q = slot - 2 * LK, j = q >> 2;
+    if (j < leaves - 1) {
+      const float* g = raw + ((int64_t)n * (leaves - 1) + j) * 16;
+      float e[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) e[i] = g[i];
+      float m = e[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) m = fmaxf(m, e[i]);
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { e[i] = expf(e[i] - m); sum += e[i]; }
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc += (e[i] / sum) * c_basis_conv[i][q & 3];
+      v = acc;
+    }
+  } else {
+    const int H2 = 1 << (arity - 1), q = slot - 2 * LK;
+    const float* s_ = raw + (int64_t)n * 2 * H2;
+    if (q < H2) {
+      v = sigmoidc(s_[2 * q]);
+    } else if (q < 2 * H2) {
+      v = sigmoidc(s_[2 * (q - H2) + 1]) - sigmoidc(s_[2 * (q - H2)]);
+    }
+  }
+  rec[t] = v;
+}
+
 __global__ void conv_hard_prep_kernel(const int* __restrict__ cm, const int* __restrict__ ch,
                                       const int* __restrict__ cw, const float* __restrict__ conn,
                                       int N, int leaves, int K, int node, int nodes, int arity,
@@ -360,25 +526,15 @@ struct ConvSoftArgs {
   const float* x; int64_t B, C, H, W, N; int K, kernel, pad;
   const float* np; const float* w; const int* cm; const int* ch; const int* cw;
   float* out; int64_t Ho, Wo;
+  const float* rec;  // records (REC kernels) or null
 };
 
-template <int NODE, int NLEAF, bool POOL, int KM>
-static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
+template <int NODE, int NLEAF, bool POOL, int KM, bool REC>
+static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st, int64_t S) {
   const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
   const int64_t per_sample = a.C * plane * 4;
-  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
-  SLG_REQUIRE(per_sample <= cap, SLG_E_UNSUPPORTED, "conv_soft: one image (%lld B) exceeds LDS",
-              (long long)per_sample);
-  // samples per workgroup: whole 64-lane chunks of (sample, position) pairs
-  // where the images are small, up to half the LDS so that two workgroups
-  // share a CU, and enough workgroups to fill the chip
-  const int64_t P = a.Ho * a.Wo;
-  int64_t S = std::max<int64_t>(1, cdiv(128, P));
-  S = std::min<int64_t>(S, std::max<int64_t>(1, cap / 2 / per_sample));
-  S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / (2 * device_cus())));
-  S = std::min<int64_t>(S, a.B);
   const size_t lds = (size_t)(S * per_sample);
-  auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM>;
+  auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -389,16 +545,42 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(256), lds, st, a.x, (int)a.B,
                      (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, a.np, a.w, a.cm,
-                     a.ch, a.cw, (int)S, a.out, (int)a.Ho, (int)a.Wo);
+                     a.ch, a.cw, a.rec, (int)S, a.out, (int)a.Ho, (int)a.Wo);
   SLG_LAUNCH_CHECK("conv_soft");
   return 0;
+}
+
+// Samples per workgroup: whole 64-lane chunks of (sample, position) pairs
+// where the images are small, up to half the LDS so that two workgroups
+// share a CU, and enough workgroups to fill the chip.
+static int64_t conv_soft_samples(const ConvSoftArgs& a) {
+  const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
+  const int64_t per_sample = a.C * plane * 4;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  const int64_t P = a.Ho * a.Wo;
+  int64_t S = std::max<int64_t>(1, cdiv(128, P));
+  S = std::min<int64_t>(S, std::max<int64_t>(1, cap / 2 / per_sample));
+  S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / (2 * device_cus())));
+  return std::min<int64_t>(S, a.B);
+}
+
+template <int NODE, int NLEAF, bool POOL, int KM>
+static int launch_conv_soft_km(const ConvSoftArgs& a, hipStream_t st) {
+  const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
+  const int64_t per_sample = a.C * plane * 4;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  SLG_REQUIRE(per_sample <= cap, SLG_E_UNSUPPORTED, "conv_soft: one image (%lld B) exceeds LDS",
+              (long long)per_sample);
+  const int64_t S = conv_soft_samples(a);
+  return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, KM, true>(a, st, S)
+               : launch_conv_soft_k<NODE, NLEAF, POOL, KM, false>(a, st, S);
 }
 
 template <int NODE, int NLEAF, bool POOL>
 static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
   // taps per leaf: 4 registers when K <= 4 (TopK k=4, fixed wiring), else 8
-  return a.K <= 4 ? launch_conv_soft_k<NODE, NLEAF, POOL, 4>(a, st)
-                  : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK>(a, st);
+  return a.K <= 4 ? launch_conv_soft_km<NODE, NLEAF, POOL, 4>(a, st)
+                  : launch_conv_soft_km<NODE, NLEAF, POOL, kMaxK>(a, st);
 }
 
 template <bool POOL>
@@ -498,7 +680,60 @@ int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
   const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
   const int64_t Ho = pool ? Hf / 2 : Hf, Wo = pool ? Wf / 2 : Wf;
   if (B == 0 || Ho == 0 || Wo == 0) return 0;
-  ConvSoftArgs a{x, B, C, H, W, N, K, kernel, pad, node_param, w, cm, ch, cw, out, Ho, Wo};
+  ConvSoftArgs a{x, B, C, H, W, N, K, kernel, pad, node_param, w, cm, ch, cw, out, Ho, Wo, nullptr};
+  return pool ? conv_soft_dispatch<true>(a, node_kind, nleaf, as_stream(stream))
+              : conv_soft_dispatch<false>(a, node_kind, nleaf, as_stream(stream));
+}
+
+int64_t slg_conv_soft_record_floats(int32_t node_kind, int32_t depth, int32_t arity, int32_t K) {
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  if (nleaf <= 0 || K < 1 || K > kMaxK) return -1;
+  const int km = K <= 4 ? 4 : kMaxK;
+  const int npr = node_kind == SLG_NODE_GATE16 ? 4 * (nleaf - 1) : (1 << nleaf);
+  return (2 * nleaf * km + npr + 3) & ~3;
+}
+
+int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* ch,
+                          const int32_t* cw, int64_t N, int32_t K, int32_t node_kind, int32_t depth,
+                          int32_t arity, const float* raw, int64_t C, int64_t H, int64_t W,
+                          int32_t pad, float* rec, slg_stream_t stream) {
+  SLG_REQUIRE(cm && ch && cw && raw && rec, SLG_E_ARG, "conv_soft_records: null pointer");
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_records: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft_records: K=%d outside 1..%d", K, kMaxK);
+  SLG_REQUIRE(N > 0 && N < (1LL << 20) && C > 0 && C < (1LL << 20) && H > 0 && H < 4096 &&
+                  W > 0 && W < 4096 && pad >= 0 && pad <= 4,
+              SLG_E_SHAPE, "conv_soft_records: bad sizes");
+  const int64_t RS = W + pad, plane = (H + 2 * pad) * RS + pad;
+  SLG_REQUIRE(C * plane < (1LL << 31), SLG_E_SHAPE, "conv_soft_records: image too large");
+  const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K);
+  const int km = K <= 4 ? 4 : kMaxK;
+  hipLaunchKernelGGL(conv_soft_records_kernel, dim3((unsigned)cdiv(N * R, 256)), dim3(256), 0,
+                     as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km, node_kind, arity,
+                     raw, (int)C, 2 * pad + 1, (int)plane, (int)RS, R, rec);
+  SLG_LAUNCH_CHECK("conv_soft_records");
+  return 0;
+}
+
+int slg_conv_soft_fwd_records(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                              int64_t N, int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                              const float* rec, int32_t pad, int32_t pool, float* out,
+                              slg_stream_t stream) {
+  SLG_REQUIRE(rec && ((x && out) || B == 0), SLG_E_ARG, "conv_soft_records: null pointer");
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
+              "conv_soft: node_kind %d", node_kind);
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft: K=%d outside 1..%d", K, kMaxK);
+  SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && N > 0 && pad >= 0 && pad <= 4 &&
+                  B < (1LL << 31) && N < (1LL << 20) && C < (1LL << 20) && H < 4096 && W < 4096,
+              SLG_E_SHAPE, "conv_soft: bad sizes");
+  const int kernel = 2 * pad + 1;
+  const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
+  const int64_t Ho = pool ? Hf / 2 : Hf, Wo = pool ? Wf / 2 : Wf;
+  if (B == 0 || Ho == 0 || Wo == 0) return 0;
+  ConvSoftArgs a{x, B, C, H, W, N, K, kernel, pad, nullptr, nullptr, nullptr, nullptr, nullptr,
+                 out, Ho, Wo, rec};
   return pool ? conv_soft_dispatch<true>(a, node_kind, nleaf, as_stream(stream))
               : conv_soft_dispatch<false>(a, node_kind, nleaf, as_stream(stream));
 }

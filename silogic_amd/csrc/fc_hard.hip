@@ -218,8 +218,6 @@ struct NetDesc {
   int maxw;  // words per activation buffer: the widest layer + kGuard
 };
 
-constexpr int kBufferWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit data format
-
 // Codes of this thread's outputs o = tid + j*1024 of a W-wide layer, read
 // through a raw buffer resource of W codes: offsets past it read 0 (a valid
 // code), so the loads need no clamp.

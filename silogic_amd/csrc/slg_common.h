@@ -50,4 +50,18 @@ __device__ inline uint32_t xcd_logical_id(uint32_t i, uint32_t grid) {
   return (i & 7u) * (grid >> 3) + (i >> 3);
 }
 
+// Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format).
+// Loads through such a resource at offsets past its byte size return 0.
+constexpr int kBufferWord3 = 0x00020000;
+
+// q = e / d for 0 <= e < 2^24 and 0 < d < 2^24, with inv = 1.0f / d: the
+// float quotient is within one of the true one, and the remainder test
+// corrects it.
+__device__ inline int div_small(int e, int d, float inv) {
+  int q = (int)((float)e * inv);
+  const int r = e - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
+}
+
 }  // namespace slg

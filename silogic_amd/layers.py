@@ -319,9 +319,7 @@ class ConvLogicTree(nn.Module):
 
     def soft_params(self, grad):
         K = 1 if self.connect == "fixed" else self.k
-        plain = self.gate_select == "softmax" or (
-            not self.training and self.gate_select != "hard")
-        if grad or not plain:
+        if grad or not self._plain_soft():
             w = (torch.ones(self.n, self.leaves, 1, device=self.cm_idx.device)
                  if self.connect == "fixed" else self._topk_w())
             npar = (self._basis_coef() if self.node_name == "gate16"
@@ -331,11 +329,28 @@ class ConvLogicTree(nn.Module):
         return ops.conv_soft_prep(conn, self._raw(), self._kind(), self.n, self.leaves, K,
                                   self.d, self.node_arity)
 
+    def _plain_soft(self):
+        return self.gate_select == "softmax" or (
+            not self.training and self.gate_select != "hard")
+
+    def soft_records(self, in_shape):
+        """Per-channel records for input (C, H, W): resolved taps, softmax
+        leaf weights and node parameters (forward only, plain softmax)."""
+        cm, ch, cw = self._taps()
+        conn = None if self.connect == "fixed" else self.conn
+        return ops.conv_soft_records(conn, cm, ch, cw, self._raw(), self._kind(), self.d,
+                                     self.node_arity, cm.shape[-1], tuple(in_shape),
+                                     self.padding)
+
     def _soft(self, x, pool):
         ops.require_gpu(x)
-        w, npar = self.soft_params(_needs_grad(self, x))
         cm, ch, cw = self._taps()
         K = cm.shape[-1]
+        if not _needs_grad(self, x) and self._plain_soft():
+            rec = self.soft_records(x.shape[1:])
+            return ops.conv_soft_rec(x, rec, self.n, self._kind(), self.d, self.node_arity, K,
+                                     self.padding, pool)
+        w, npar = self.soft_params(_needs_grad(self, x))
         return ops.conv_soft(x, npar, w, cm, ch, cw, self._kind(), self.d, self.node_arity, K,
                              self.padding, pool)
 

@@ -429,6 +429,45 @@ def test_conv_multilinear_lut(arity):
     assert torch.equal(conv.forward_hard(xb.to(DEV)).cpu(), torch_ref.conv_hard(blk, sd, xb))
 
 
+@pytest.mark.parametrize("kernel,hw,cin,B,k,node", [
+    (1, (5, 6), 3, 9, 1, "gate16"),          # no padding
+    (3, (7, 7), 40, 300, 4, "gate16"),       # many narrow planes
+    (5, (12, 9), 4, 17, 8, "gate16"),        # pad 2, 8 taps per leaf
+    (3, (4, 4), 3, 2101, 4, "gate16"),       # several samples per workgroup, ragged last
+    (3, (9, 10), 6, 33, 8, "multilinear"),   # LUT with 8 taps per leaf
+])
+def test_conv_staging_and_records(kernel, hw, cin, B, k, node):
+    """The records path (no grad) against the oracle and, bit for bit, against
+    the separate-array entry point on the same parameters."""
+    depth, arity = (2, 2) if node == "gate16" else (1, 4)
+    conv = sl.ConvLogicTree(cin, 24, kernel=kernel, padding=kernel // 2, tree_depth=depth,
+                            connect="topk", k=k, n_chan=2, node=node, arity=arity,
+                            residual_init=False, seed=3)
+    sd = {kk: v.clone() for kk, v in conv.state_dict().items()}
+    leaves = 2 ** depth if node == "gate16" else arity
+    blk = dict(prefix="", cin=cin, n=24, kernel=kernel, depth=depth, stride=1,
+               padding=kernel // 2, connect="topk", k=conv.k, node=node,
+               node_arity=conv.node_arity, leaves=leaves)
+    conv = conv.to(DEV).eval()
+    x = torch.rand(B, cin, *hw)
+    xd = x.to(DEV)
+    with torch.no_grad():
+        y, yp = conv(xd), conv.forward_pooled(xd)
+        ref = torch_ref.conv_soft(blk, sd, x)
+        assert_soft_close(y, ref, "conv")
+        assert_soft_close(yp, torch_ref.orpool_soft(ref), "pooled")
+        w, npar = conv.soft_params(False)
+        cm, ch, cw = conv._taps()
+        rec = conv.soft_records(x.shape[1:])
+        for pool, got in ((False, y), (True, yp)):
+            arr = ops.conv_soft(xd, npar, w, cm, ch, cw, conv._kind(), conv.d, conv.node_arity,
+                                cm.shape[-1], conv.padding, pool)
+            assert torch.equal(got, arr)
+            r = ops.conv_soft_rec(xd, rec, 24, conv._kind(), conv.d, conv.node_arity,
+                                  cm.shape[-1], conv.padding, pool)
+            assert torch.equal(got, r)
+
+
 def test_kernels_module_drop_ins():
     """silogic.kernels-compatible entry points (tests/test_triton.py analogues)."""
     layer = sl.LogicLayer(256, 512, connectome="TopK", k=8, seed=0)
