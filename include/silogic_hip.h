@@ -268,23 +268,24 @@ int slg_conv_soft_prep(const float* conn, int64_t N, int32_t leaves, int32_t K,
 
 /* Per-channel records for slg_conv_soft_fwd_records: the soft conv
  * parameters of slg_conv_soft_prep together with the tap positions,
- * resolved for one input geometry (C, H, W, pad). conn [N,leaves,K] (NULL:
- * w = 1), taps cm/ch/cw [N,leaves,K] as for slg_conv_soft_fwd, raw as for
+ * resolved for one input geometry (C, H, W, pad) and pooling flag (the LDS
+ * layout of the pooled kernel differs). conn [N,leaves,K] (NULL: w = 1),
+ * taps cm/ch/cw [N,leaves,K] as for slg_conv_soft_fwd, raw as for
  * slg_conv_soft_prep. rec holds N * slg_conv_soft_record_floats(...)
  * floats; the layout is internal to the library. The reference computes
  * these parameters inside every forward (layers.py:487-497, 408-417,
  * nodes.py:178); a caller keeps the records while the parameters and the
  * geometry stay the same. */
 int64_t slg_conv_soft_record_floats(int32_t node_kind, int32_t depth, int32_t arity,
-                                    int32_t K);
+                                    int32_t K, int32_t pool);
 int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* ch,
                           const int32_t* cw, int64_t N, int32_t K, int32_t node_kind,
                           int32_t depth, int32_t arity, const float* raw, int64_t C,
-                          int64_t H, int64_t W, int32_t pad, float* rec,
+                          int64_t H, int64_t W, int32_t pad, int32_t pool, float* rec,
                           slg_stream_t stream);
 
 /* slg_conv_soft_fwd with the channel parameters taken from records built for
- * the same (C, H, W, pad, K, node_kind, depth, arity); same output. */
+ * the same (C, H, W, pad, pool, K, node_kind, depth, arity); same output. */
 int slg_conv_soft_fwd_records(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
                               int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
                               int32_t K, const float* rec, int32_t pad, int32_t pool,

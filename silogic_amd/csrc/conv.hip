@@ -1,15 +1,27 @@
 // ConvLogicTree + OrPool for gfx950: soft (fp32) and hard (bit-packed), each
 // with the 2x2 OR-pool fused so only the pooled map is written.
 //
-// Soft design: a workgroup owns S samples and every output channel. It stages
-// the S input images in LDS in a zero-padded layout whose right padding is
-// shared with the next row's left padding (row stride W+pad, plane
-// (H+2pad)(W+pad)+pad floats), so every tap of every output position is one
-// LDS read at base(position) + off(tap) with no bounds test. Waves take
-// tasks = (output channel, 64 consecutive (sample, position) pairs); the
-// channel is wave-uniform, so tap offsets, leaf weights and node
-// coefficients come from scalar loads. Each lane evaluates the tree at the
-// 2x2 positions of its pooled output and keeps the max.
+// Soft design: a workgroup owns S samples and every output channel. It
+// stages the S input images in LDS with their zero padding, so every tap read
+// is unconditional, and its waves take output channels in turn; the channel
+// is wave-uniform, so tap offsets, leaf weights and node parameters sit in
+// registers while the wave walks every 64-lane chunk of the workgroup's
+// output positions. Two LDS layouts:
+//  * row-major: plane (s, c) holds padded row r at r*RS with RS = W + pad
+//    (the right padding of a row is the next row's left padding), plane size
+//    (H+2pad)*RS + pad. Unpooled, lanes walk (row, column < RS) of each
+//    sample and a chunk reads 64 consecutive floats; pooled, lanes walk
+//    (pooled row, pooled column) and read each tap's 2x2 window as two pairs.
+//  * phase-split (pooled, at most 16 taps per output): plane (s, c) is split
+//    by (row parity, column parity) of the padded image into four sub-planes
+//    of (Ho+pad) x (Wo+pad). Window position (dy, dx) of pooled output
+//    (py, px) under tap (h, w) is sub-plane ((dy+h)&1, (dx+w)&1) at
+//    (py + (dy+h)/2, px + (dx+w)/2), so lanes that walk (py, px < Wo+pad)
+//    read consecutive floats of one sub-plane: four reads per tap at four
+//    offsets held in registers.
+// Where lanes read consecutive floats, the sample stride is padded to equal
+// the lanes per sample modulo 64, so that a chunk that spans two samples
+// still hits 64 distinct LDS banks.
 //
 // Hard design: B-packed activations [C,H,W,nw] (64 samples per word).
 // Threads walk (pooled position, word) with the word index fastest, so
@@ -36,29 +48,58 @@ struct ConvNode {
   static constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);  // raw params
 };
 
+// Layout choice and register budget of one kernel variant (host and device).
+__host__ __device__ constexpr bool conv_phase_layout(bool pool, int nleaf, int km) {
+  return pool && nleaf * km <= 16;
+}
+
+template <int NODE, int NLEAF, int KM, bool POOL>
+struct ConvCfg {
+  static constexpr bool PHASE = conv_phase_layout(POOL, NLEAF, KM);
+  static constexpr int NW = PHASE ? 4 : 1;  // LDS offsets per tap
+  static constexpr int NPR = ConvNode<NODE, NLEAF>::NPR;
+  static constexpr int PARAMS = NLEAF * KM * (NW + 1) + NPR;  // per-channel registers
+  static constexpr int REC = (PARAMS + 3) & ~3;               // record floats
+  // eight waves per workgroup where the parameters leave room for two waves
+  // per SIMD, else four
+  static constexpr int THREADS = PARAMS <= 128 ? 512 : 256;
+};
+
+// LDS geometry of one launch (see the layouts above).
+struct ConvGeom {
+  int RS;     // row stride: W + pad (row-major) or Wo + pad (sub-plane rows)
+  int PR;     // sub-plane rows Ho + pad (phase-split), 0 otherwise
+  int PP;     // sub-plane size PR * RS (phase-split), 0 otherwise
+  int plane;  // channel stride
+  int SST;    // sample stride
+  int LPS;    // lanes per sample
+};
+
 // One output channel's parameters in registers: LDS tap offsets, leaf
 // weights and node parameters.
-template <int NODE, int NLEAF, int KM>
+template <int NODE, int NLEAF, int KM, int NW>
 struct ConvParams {
-  int off[NLEAF][KM];
+  int off[NLEAF][KM][NW];
   float wt[NLEAF][KM];
   float par[ConvNode<NODE, NLEAF>::NPR];
 };
 
-// Record of one channel (slg_conv_soft_records): the fields of ConvParams in
-// order, padded to a multiple of 4 floats.
-template <int NODE, int NLEAF, int KM>
-constexpr int conv_rec_floats() {
-  return (2 * NLEAF * KM + ConvNode<NODE, NLEAF>::NPR + 3) & ~3;
+// LDS offset of tap (c, h, w) for window position q = 2*dy + dx (NW = 4,
+// phase-split) or the tap itself (NW = 1, row-major).
+__host__ __device__ inline int conv_tap_offset(const ConvGeom& g, int NW, int c, int h, int w,
+                                               int q) {
+  if (NW == 1) return c * g.plane + h * g.RS + w;
+  const int Y = (q >> 1) + h, X = (q & 1) + w;
+  return c * g.plane + (Y & 1) * 2 * g.PP + (X & 1) * g.PP + (Y >> 1) * g.RS + (X >> 1);
 }
 
 // Channel parameters from separate arrays (slg_conv_soft_fwd). The index nv
 // is a vector register (the same value in every lane), so the loads are
 // vector loads and the parameters stay in VGPRs: there are too many for the
 // scalar file, and an FMA takes one scalar operand on gfx9.
-template <int NODE, int NLEAF, int KM>
-__device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM>& P, int nv, int K, int C,
-                                          int kernel, int plane, int RS, const float* np,
+template <int NODE, int NLEAF, int KM, int NW>
+__device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM, NW>& P, int nv, int K,
+                                          int C, int kernel, const ConvGeom& g, const float* np,
                                           const float* wts, const int* cm, const int* ch,
                                           const int* cw) {
 #pragma unroll
@@ -70,10 +111,12 @@ __device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM>& P, int nv
         const int c_ = min(max(cm[idx], 0), C - 1);
         const int h_ = min(max(ch[idx], 0), kernel - 1);
         const int w_ = min(max(cw[idx], 0), kernel - 1);
-        P.off[l][k] = c_ * plane + h_ * RS + w_;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) P.off[l][k][q] = conv_tap_offset(g, NW, c_, h_, w_, q);
         P.wt[l][k] = wts ? wts[idx] : 1.0f;
       } else {
-        P.off[l][k] = 0;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) P.off[l][k][q] = 0;
         P.wt[l][k] = 0.0f;
       }
     }
@@ -93,10 +136,12 @@ __device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM>& P, int nv
   }
 }
 
-// Channel parameters from a record: contiguous 16-byte vector loads.
-template <int NODE, int NLEAF, int KM>
-__device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM>& P, const float* rec, int nv) {
-  constexpr int R = conv_rec_floats<NODE, NLEAF, KM>();
+// Channel parameters from a record (slg_conv_soft_records): R floats laid
+// out as ConvParams (offsets, weights, node parameters), read with 16-byte
+// vector loads.
+template <int NODE, int NLEAF, int KM, int NW, int R>
+__device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM, NW>& P, const float* rec,
+                                          int nv) {
   float v[R];
   const float4* r4 = reinterpret_cast<const float4*>(rec + (int64_t)nv * R);
 #pragma unroll
@@ -104,51 +149,47 @@ __device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM>& P, const 
     const float4 t = r4[q];
     v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
   }
+  constexpr int LK = NLEAF * KM;
 #pragma unroll
   for (int l = 0; l < NLEAF; ++l)
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
-      P.off[l][k] = __float_as_int(v[l * KM + k]);
-      P.wt[l][k] = v[NLEAF * KM + l * KM + k];
+#pragma unroll
+      for (int q = 0; q < NW; ++q) P.off[l][k][q] = __float_as_int(v[(l * KM + k) * NW + q]);
+      P.wt[l][k] = v[LK * NW + l * KM + k];
     }
 #pragma unroll
-  for (int i = 0; i < ConvNode<NODE, NLEAF>::NPR; ++i) P.par[i] = v[2 * NLEAF * KM + i];
+  for (int i = 0; i < ConvNode<NODE, NLEAF>::NPR; ++i) P.par[i] = v[LK * (NW + 1) + i];
 }
 
-// Work split: wave w takes output channels n = w, w + nwaves, ...; for each
-// channel it holds the channel's parameters in registers and walks every chunk
-// of 64 (sample, pooled position) pairs of the workgroup's S samples. A lane
-// evaluates the 2x2 window of its pooled position: for each tap, two LDS
-// reads of adjacent pairs (rows y and y+1), four FMAs.
 template <int NODE, int NLEAF, bool POOL, int KM, bool REC>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__((ConvCfg<NODE, NLEAF, KM, POOL>::THREADS))
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
-                 int pad, const float* __restrict__ np, const float* __restrict__ wts,
+                 int pad, ConvGeom g, const float* __restrict__ np, const float* __restrict__ wts,
                  const int* __restrict__ cm, const int* __restrict__ ch, const int* __restrict__ cw,
                  const float* __restrict__ rec, int S, float* __restrict__ out, int Ho, int Wo) {
+  using Cfg = ConvCfg<NODE, NLEAF, KM, POOL>;
+  constexpr bool PHASE = Cfg::PHASE;
+  constexpr int NW = Cfg::NW;
   extern __shared__ float lds[];
-  const int RS = W + pad;
-  const int rows = H + 2 * pad;
-  const int plane = rows * RS + pad;
-  const int SST = C * plane;
   const int b0 = blockIdx.x * S;
   const int ns = min(S, B - b0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
 
-  // Stage the images. Plane (s, c) holds row r - pad of the input in row r
-  // at columns pad..pad+W-1; columns 0..pad-1 are the shared zero padding
-  // (also the right padding of the previous row), rows 0..pad-1 and
-  // H+pad..rows-1 are zero, and each plane ends with pad zeros. The ns*C*H*W
-  // input floats are contiguous: every thread issues kStage loads before it
-  // writes them, so that the copy is not one load latency per row.
+  // Stage the images: clear the region, then scatter the ns*C*H*W input
+  // floats (contiguous in memory) to their padded positions. Every thread
+  // issues kStage loads before it writes them, so that the copy is not one
+  // load latency per row.
+  for (int i = threadIdx.x; i < ns * g.SST; i += blockDim.x) lds[i] = 0.0f;
+  __syncthreads();
   {
     const int HW = H * W;
     const int total = ns * C * HW;
     const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(x + (int64_t)b0 * C * HW), (short)0, total * 4, kBufferWord3);
-    const float inv_hw = 1.0f / (float)HW, inv_w = 1.0f / (float)W;
+    const float inv_hw = 1.0f / (float)HW, inv_w = 1.0f / (float)W, inv_c = 1.0f / (float)C;
     constexpr int kStage = 8;
     for (int e0 = threadIdx.x; e0 < total; e0 += kStage * blockDim.x) {
       float v[kStage];
@@ -161,54 +202,56 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
         const int e = e0 + u * (int)blockDim.x;
         const int sc = div_small(e, HW, inv_hw);
         const int rem = e - sc * HW;
-        const int r = div_small(rem, W, inv_w);
-        if (e < total) lds[sc * plane + (r + pad) * RS + pad + (rem - r * W)] = v[u];
+        const int y = div_small(rem, W, inv_w);
+        const int xx = rem - y * W;
+        const int s = div_small(sc, C, inv_c);
+        const int c = sc - s * C;
+        int at;
+        bool keep = e < total;
+        if constexpr (PHASE) {
+          const int Y = y + pad, X = xx + pad;
+          keep = keep && (Y >> 1) < g.PR && (X >> 1) < g.RS;  // rows/columns no window reads
+          at = (Y & 1) * 2 * g.PP + (X & 1) * g.PP + (Y >> 1) * g.RS + (X >> 1);
+        } else {
+          at = (y + pad) * g.RS + pad + xx;
+        }
+        if (keep) lds[s * g.SST + c * g.plane + at] = v[u];
       }
-    }
-    // zero slots of one plane: top rows, bottom rows, left pads, tail
-    const int ztop = pad * RS, zleft = H * pad;
-    const int Z = 2 * ztop + zleft + pad;
-    const float inv_z = 1.0f / (float)max(Z, 1), inv_pad = 1.0f / (float)max(pad, 1);
-    for (int z = threadIdx.x; z < ns * C * Z; z += blockDim.x) {
-      const int sc = div_small(z, Z, inv_z);
-      int k = z - sc * Z, at;
-      if (k < 2 * ztop) {
-        at = k < ztop ? k : (H + pad) * RS + (k - ztop);
-      } else if ((k -= 2 * ztop) < zleft) {
-        const int r = div_small(k, pad, inv_pad);
-        at = (r + pad) * RS + (k - r * pad);
-      } else {
-        at = rows * RS + (k - zleft);
-      }
-      lds[sc * plane + at] = 0.0f;
     }
   }
   __syncthreads();
 
   const int P = Ho * Wo;
-  const int nchunks = (ns * P + 63) / 64;
+  const int nchunks = (ns * g.LPS + 63) / 64;
+  const float inv_lps = 1.0f / (float)g.LPS;
+  const float inv_col = 1.0f / (float)(PHASE || !POOL ? g.RS : Wo);
   constexpr int H2 = (NODE == SLG_NODE_GATE16) ? 1 : (1 << (NLEAF - 1));
 
-  auto load = [&](ConvParams<NODE, NLEAF, KM>& Pr, int n) {
+  auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int n) {
     int nv;  // the channel in a vector register: vector loads, VGPR parameters
     asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
-    if constexpr (REC) conv_params_record<NODE, NLEAF, KM>(Pr, rec, nv);
-    else conv_params_arrays<NODE, NLEAF, KM>(Pr, nv, K, C, kernel, plane, RS, np, wts, cm, ch, cw);
+    if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
+    else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, nv, K, C, kernel, g, np, wts, cm, ch, cw);
   };
 
-  ConvParams<NODE, NLEAF, KM> Pc;
+  ConvParams<NODE, NLEAF, KM, NW> Pc;
   if (wave < N) load(Pc, wave);
   for (int n = wave; n < N; n += nwaves) {
-
     for (int chunk = 0; chunk < nchunks; ++chunk) {
-      const int sp = chunk * 64 + lane;
-      const bool active = sp < ns * P;
-      const int s = active ? sp / P : 0;
-      const int p = active ? sp - s * P : 0;
-      const int py = p / Wo;
-      const int oy = py * (POOL ? 2 : 1);
-      const int ox = (p - py * Wo) * (POOL ? 2 : 1);
-      const float* base = lds + s * SST + oy * RS + ox;
+      const int q = chunk * 64 + lane;
+      bool active = q < ns * g.LPS;
+      const int s = active ? div_small(q, g.LPS, inv_lps) : 0;
+      const int rem = active ? q - s * g.LPS : 0;
+      // (row, column) of the lane within its sample: pooled row-major lanes
+      // walk Wo columns, the others RS columns (those >= Wo idle)
+      const int row = div_small(rem, PHASE || !POOL ? g.RS : Wo, inv_col);
+      const int col = rem - row * (PHASE || !POOL ? g.RS : Wo);
+      active = active && col < Wo;
+      const int p = row * Wo + col;
+      int bofs;
+      if constexpr (PHASE || !POOL) bofs = rem;                 // row * RS + col
+      else bofs = 2 * row * g.RS + 2 * col;
+      const float* base = lds + s * g.SST + (active ? bofs : 0);
 
       constexpr int NQ = POOL ? 4 : 1;
       float v[NQ][NLEAF];
@@ -216,33 +259,39 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       for (int l = 0; l < NLEAF; ++l) {
         float acc[NQ];
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) acc[q] = 0.0f;
+        for (int qq = 0; qq < NQ; ++qq) acc[qq] = 0.0f;
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
           if (k < K) {
-            const float* t0 = base + Pc.off[l][k];
-            acc[0] = fmaf(Pc.wt[l][k], t0[0], acc[0]);
-            if constexpr (POOL) {
-              const float* t1 = t0 + RS;
-              acc[1] = fmaf(Pc.wt[l][k], t0[1], acc[1]);
-              acc[2] = fmaf(Pc.wt[l][k], t1[0], acc[2]);
-              acc[3] = fmaf(Pc.wt[l][k], t1[1], acc[3]);
+            if constexpr (PHASE) {
+#pragma unroll
+              for (int qq = 0; qq < 4; ++qq)
+                acc[qq] = fmaf(Pc.wt[l][k], base[Pc.off[l][k][qq]], acc[qq]);
+            } else {
+              const float* t0 = base + Pc.off[l][k][0];
+              acc[0] = fmaf(Pc.wt[l][k], t0[0], acc[0]);
+              if constexpr (POOL) {
+                const float* t1 = t0 + g.RS;
+                acc[1] = fmaf(Pc.wt[l][k], t0[1], acc[1]);
+                acc[2] = fmaf(Pc.wt[l][k], t1[0], acc[2]);
+                acc[3] = fmaf(Pc.wt[l][k], t1[1], acc[3]);
+              }
             }
           }
         }
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) v[q][l] = acc[q];
+        for (int qq = 0; qq < NQ; ++qq) v[qq][l] = acc[qq];
       }
       float best = -INFINITY;
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
+      for (int qq = 0; qq < NQ; ++qq) {
         float val;
         if constexpr (NODE == SLG_NODE_GATE16) {
           // level i combines children 2m (a) and 2m+1 (b), node ids level-major
           // (silogic/layers.py:388-401, 408-417)
           float u[NLEAF];
 #pragma unroll
-          for (int l = 0; l < NLEAF; ++l) u[l] = v[q][l];
+          for (int l = 0; l < NLEAF; ++l) u[l] = v[qq][l];
           int nb = 0;
 #pragma unroll
           for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
@@ -260,12 +309,12 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
           // leaf j), silogic/nodes.py:174-178, as a lerp tree
           float t[H2];
 #pragma unroll
-          for (int m = 0; m < H2; ++m) t[m] = fmaf(v[q][0], Pc.par[H2 + m], Pc.par[m]);
+          for (int m = 0; m < H2; ++m) t[m] = fmaf(v[qq][0], Pc.par[H2 + m], Pc.par[m]);
 #pragma unroll
           for (int j = 1; j < NLEAF; ++j) {
 #pragma unroll
             for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
-              t[m] = fmaf(v[q][j], t[2 * m + 1] - t[2 * m], t[2 * m]);
+              t[m] = fmaf(v[qq][j], t[2 * m + 1] - t[2 * m], t[2 * m]);
           }
           val = t[0];
         }
@@ -397,32 +446,33 @@ __global__ void conv_soft_prep_kernel(const float* __restrict__ conn, int N, int
 }
 
 // Per-channel records for conv_soft_kernel<..., REC = true>, R floats per
-// channel: [0, L*KM) LDS offsets of the KM taps of every leaf (clamped taps;
-// taps k >= K get offset 0 and weight 0), [L*KM, 2*L*KM) softmax leaf
-// weights, then the node parameters (gate16: softmax(logits) @ BASIS per
-// node; LUT: sigmoid(s) of the even corners, then odd - even differences),
-// zeros to R. One thread per record word, so that the loads of different
-// words overlap.
+// channel: [0, L*KM*NW) LDS offsets of the KM taps of every leaf, NW per tap
+// (ConvParams order; clamped taps; taps k >= K get offset 0 and weight 0),
+// then L*KM softmax leaf weights, then the node parameters (gate16:
+// softmax(logits) @ BASIS per node; LUT: sigmoid(s) of the even corners,
+// then odd - even differences), zeros to R. One thread per record word, so
+// that the loads of different words overlap.
 __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const int* __restrict__ cm,
                                          const int* __restrict__ ch, const int* __restrict__ cw,
-                                         int N, int leaves, int K, int KM, int node, int arity,
-                                         const float* __restrict__ raw, int C, int kernel,
-                                         int plane, int RS, int R, float* __restrict__ rec) {
+                                         int N, int leaves, int K, int KM, int NW, int node,
+                                         int arity, const float* __restrict__ raw, int C,
+                                         int kernel, ConvGeom g, int R, float* __restrict__ rec) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (int64_t)N * R) return;
   const int n = (int)(t / R), slot = (int)(t - (int64_t)n * R);
   const int LK = leaves * KM;
   float v = 0.0f;
-  if (slot < 2 * LK) {
-    const int lk = slot < LK ? slot : slot - LK;
+  if (slot < LK * (NW + 1)) {
+    const bool is_off = slot < LK * NW;
+    const int lk = is_off ? slot / NW : slot - LK * NW;
     const int l = lk / KM, k = lk - l * KM;
     const int64_t base = ((int64_t)n * leaves + l) * K;
     if (k < K) {
-      if (slot < LK) {
+      if (is_off) {
         const int c_ = min(max(cm[base + k], 0), C - 1);
         const int h_ = min(max(ch[base + k], 0), kernel - 1);
         const int w_ = min(max(cw[base + k], 0), kernel - 1);
-        v = __int_as_float(c_ * plane + h_ * RS + w_);
+        v = __int_as_float(conv_tap_offset(g, NW, c_, h_, w_, slot - lk * NW));
       } else if (!conn) {
         v = 1.0f;
       } else {
@@ -439,12 +489,12 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
       }
     }
   } else if (node == SLG_NODE_GATE16) {
-    const int q = slot - 2 * LK, j = q >> 2;
+    const int q = slot - LK * (NW + 1), j = q >> 2;
     if (j < leaves - 1) {
-      const float* g = raw + ((int64_t)n * (leaves - 1) + j) * 16;
+      const float* gl = raw + ((int64_t)n * (leaves - 1) + j) * 16;
       float e[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) e[i] = g[i];
+      for (int i = 0; i < 16; ++i) e[i] = gl[i];
       float m = e[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) m = fmaxf(m, e[i]);
@@ -457,7 +507,7 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
       v = acc;
     }
   } else {
-    const int H2 = 1 << (arity - 1), q = slot - 2 * LK;
+    const int H2 = 1 << (arity - 1), q = slot - LK * (NW + 1);
     const float* s_ = raw + (int64_t)n * 2 * H2;
     if (q < H2) {
       v = sigmoidc(s_[2 * q]);
@@ -529,10 +579,46 @@ struct ConvSoftArgs {
   const float* rec;  // records (REC kernels) or null
 };
 
+// LDS geometry for images (C, H, W) with 'same' padding pad, pooled to
+// (Ho, Wo) or not (Ho = H, Wo = W).
+static ConvGeom conv_geom(int64_t C, int64_t H, int64_t W, int pad, bool pool, bool phase,
+                          int64_t Ho, int64_t Wo) {
+  ConvGeom g{};
+  if (phase) {
+    g.RS = (int)(Wo + pad);
+    g.PR = (int)(Ho + pad);
+    g.PP = g.PR * g.RS;
+    g.plane = 4 * g.PP;
+    g.LPS = (int)Ho * g.RS;
+  } else {
+    g.RS = (int)(W + pad);
+    g.plane = (int)((H + 2 * pad) * g.RS + pad);
+    g.LPS = pool ? (int)(Ho * Wo) : (int)H * g.RS;
+  }
+  int64_t sst = C * g.plane;
+  if (phase || !pool) sst += (((int64_t)g.LPS - sst) % 64 + 64) % 64;  // sst = LPS (mod 64)
+  g.SST = (int)sst;
+  return g;
+}
+
 template <int NODE, int NLEAF, bool POOL, int KM, bool REC>
-static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st, int64_t S) {
-  const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
-  const int64_t per_sample = a.C * plane * 4;
+static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
+  using Cfg = ConvCfg<NODE, NLEAF, KM, POOL>;
+  const ConvGeom g = conv_geom(a.C, a.H, a.W, a.pad, POOL, Cfg::PHASE, a.Ho, a.Wo);
+  const int64_t per_sample = (int64_t)g.SST * 4;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  SLG_REQUIRE(per_sample <= cap && (int64_t)a.C * a.H * a.W * 4 < (1LL << 31), SLG_E_UNSUPPORTED,
+              "conv_soft: one image (%lld B) exceeds LDS", (long long)per_sample);
+  // Samples per workgroup: two chunks per channel where the images are
+  // small; up to half the LDS so that two workgroups share a CU, or all of it
+  // when half would leave most lanes of a chunk idle; at least one workgroup
+  // per CU.
+  int64_t S = std::max<int64_t>(1, cdiv(128, g.LPS));
+  const int64_t s_half = cap / 2 / per_sample;
+  if (s_half >= 1 && s_half * g.LPS >= 64) S = std::min(S, s_half);
+  else S = std::min(S, std::max<int64_t>(1, std::min(cap / per_sample, cdiv(64, g.LPS))));
+  S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / device_cus()));
+  S = std::min<int64_t>(S, a.B);
   const size_t lds = (size_t)(S * per_sample);
   auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC>;
   if (lds > 65536) {
@@ -543,44 +629,21 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st, int64_t S) 
       return (int)e;
     }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(256), lds, st, a.x, (int)a.B,
-                     (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, a.np, a.w, a.cm,
-                     a.ch, a.cw, a.rec, (int)S, a.out, (int)a.Ho, (int)a.Wo);
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(Cfg::THREADS), lds, st, a.x,
+                     (int)a.B, (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, g,
+                     a.np, a.w, a.cm, a.ch, a.cw, a.rec, (int)S, a.out, (int)a.Ho, (int)a.Wo);
   SLG_LAUNCH_CHECK("conv_soft");
   return 0;
-}
-
-// Samples per workgroup: whole 64-lane chunks of (sample, position) pairs
-// where the images are small, up to half the LDS so that two workgroups
-// share a CU, and enough workgroups to fill the chip.
-static int64_t conv_soft_samples(const ConvSoftArgs& a) {
-  const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
-  const int64_t per_sample = a.C * plane * 4;
-  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
-  const int64_t P = a.Ho * a.Wo;
-  int64_t S = std::max<int64_t>(1, cdiv(128, P));
-  S = std::min<int64_t>(S, std::max<int64_t>(1, cap / 2 / per_sample));
-  S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / (2 * device_cus())));
-  return std::min<int64_t>(S, a.B);
-}
-
-template <int NODE, int NLEAF, bool POOL, int KM>
-static int launch_conv_soft_km(const ConvSoftArgs& a, hipStream_t st) {
-  const int64_t plane = (a.H + 2 * a.pad) * (a.W + a.pad) + a.pad;
-  const int64_t per_sample = a.C * plane * 4;
-  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
-  SLG_REQUIRE(per_sample <= cap, SLG_E_UNSUPPORTED, "conv_soft: one image (%lld B) exceeds LDS",
-              (long long)per_sample);
-  const int64_t S = conv_soft_samples(a);
-  return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, KM, true>(a, st, S)
-               : launch_conv_soft_k<NODE, NLEAF, POOL, KM, false>(a, st, S);
 }
 
 template <int NODE, int NLEAF, bool POOL>
 static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
   // taps per leaf: 4 registers when K <= 4 (TopK k=4, fixed wiring), else 8
-  return a.K <= 4 ? launch_conv_soft_km<NODE, NLEAF, POOL, 4>(a, st)
-                  : launch_conv_soft_km<NODE, NLEAF, POOL, kMaxK>(a, st);
+  if (a.K <= 4)
+    return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true>(a, st)
+                 : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false>(a, st);
+  return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true>(a, st)
+               : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false>(a, st);
 }
 
 template <bool POOL>
@@ -685,18 +748,20 @@ int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
               : conv_soft_dispatch<false>(a, node_kind, nleaf, as_stream(stream));
 }
 
-int64_t slg_conv_soft_record_floats(int32_t node_kind, int32_t depth, int32_t arity, int32_t K) {
+int64_t slg_conv_soft_record_floats(int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                                    int32_t pool) {
   const int nleaf = node_leaves(node_kind, depth, arity);
   if (nleaf <= 0 || K < 1 || K > kMaxK) return -1;
   const int km = K <= 4 ? 4 : kMaxK;
+  const int nw = conv_phase_layout(pool != 0, nleaf, km) ? 4 : 1;
   const int npr = node_kind == SLG_NODE_GATE16 ? 4 * (nleaf - 1) : (1 << nleaf);
-  return (2 * nleaf * km + npr + 3) & ~3;
+  return (nleaf * km * (nw + 1) + npr + 3) & ~3;
 }
 
 int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* ch,
                           const int32_t* cw, int64_t N, int32_t K, int32_t node_kind, int32_t depth,
                           int32_t arity, const float* raw, int64_t C, int64_t H, int64_t W,
-                          int32_t pad, float* rec, slg_stream_t stream) {
+                          int32_t pad, int32_t pool, float* rec, slg_stream_t stream) {
   SLG_REQUIRE(cm && ch && cw && raw && rec, SLG_E_ARG, "conv_soft_records: null pointer");
   const int nleaf = node_leaves(node_kind, depth, arity);
   SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_records: depth %d / arity %d", depth, arity);
@@ -704,13 +769,16 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
   SLG_REQUIRE(N > 0 && N < (1LL << 20) && C > 0 && C < (1LL << 20) && H > 0 && H < 4096 &&
                   W > 0 && W < 4096 && pad >= 0 && pad <= 4,
               SLG_E_SHAPE, "conv_soft_records: bad sizes");
-  const int64_t RS = W + pad, plane = (H + 2 * pad) * RS + pad;
-  SLG_REQUIRE(C * plane < (1LL << 31), SLG_E_SHAPE, "conv_soft_records: image too large");
-  const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K);
   const int km = K <= 4 ? 4 : kMaxK;
+  const bool phase = conv_phase_layout(pool != 0, nleaf, km);
+  const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
+  SLG_REQUIRE(C * ((H + 2 * pad) * (W + 2 * pad) + 64) < (1LL << 31), SLG_E_SHAPE,
+              "conv_soft_records: image too large");
+  const ConvGeom g = conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo);
+  const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K, pool);
   hipLaunchKernelGGL(conv_soft_records_kernel, dim3((unsigned)cdiv(N * R, 256)), dim3(256), 0,
-                     as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km, node_kind, arity,
-                     raw, (int)C, 2 * pad + 1, (int)plane, (int)RS, R, rec);
+                     as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km, phase ? 4 : 1,
+                     node_kind, arity, raw, (int)C, 2 * pad + 1, g, R, rec);
   SLG_LAUNCH_CHECK("conv_soft_records");
   return 0;
 }

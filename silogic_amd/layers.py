@@ -333,21 +333,22 @@ class ConvLogicTree(nn.Module):
         return self.gate_select == "softmax" or (
             not self.training and self.gate_select != "hard")
 
-    def soft_records(self, in_shape):
-        """Per-channel records for input (C, H, W): resolved taps, softmax
-        leaf weights and node parameters (forward only, plain softmax)."""
+    def soft_records(self, in_shape, pool):
+        """Per-channel records for input (C, H, W) and the pooled or plain
+        forward: resolved taps, softmax leaf weights and node parameters
+        (forward only, plain softmax)."""
         cm, ch, cw = self._taps()
         conn = None if self.connect == "fixed" else self.conn
         return ops.conv_soft_records(conn, cm, ch, cw, self._raw(), self._kind(), self.d,
                                      self.node_arity, cm.shape[-1], tuple(in_shape),
-                                     self.padding)
+                                     self.padding, pool)
 
     def _soft(self, x, pool):
         ops.require_gpu(x)
         cm, ch, cw = self._taps()
         K = cm.shape[-1]
         if not _needs_grad(self, x) and self._plain_soft():
-            rec = self.soft_records(x.shape[1:])
+            rec = self.soft_records(x.shape[1:], pool)
             return ops.conv_soft_rec(x, rec, self.n, self._kind(), self.d, self.node_arity, K,
                                      self.padding, pool)
         w, npar = self.soft_params(_needs_grad(self, x))

@@ -535,9 +535,10 @@ def conv_soft(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
                              cw, node_kind, depth, arity, K, pad, pool)
 
 
-def conv_soft_records(conn, cm, ch, cw, raw, node_kind, depth, arity, K, in_shape, pad):
-    """Per-channel records (taps resolved for in_shape = (C, H, W) and pad,
-    leaf weights, node parameters) for conv_soft_rec; [N, R] float32."""
+def conv_soft_records(conn, cm, ch, cw, raw, node_kind, depth, arity, K, in_shape, pad, pool):
+    """Per-channel records (taps resolved for in_shape = (C, H, W), pad and
+    the pooling flag, leaf weights, node parameters) for conv_soft_rec;
+    [N, R] float32."""
     require_gpu(raw, cm)
     cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
     N = cm.shape[0]
@@ -546,25 +547,25 @@ def conv_soft_records(conn, cm, ch, cw, raw, node_kind, depth, arity, K, in_shap
         raise ValueError("conv_soft_records: tap shapes are inconsistent")
     if conn is not None and tuple(conn.shape) != (N, leaves, K):
         raise ValueError("conv_soft_records: conn shape %s" % (tuple(conn.shape),))
-    R = _lib.lib().slg_conv_soft_record_floats(node_kind, depth, arity, K)
+    R = _lib.lib().slg_conv_soft_record_floats(node_kind, depth, arity, K, int(bool(pool)))
     if R <= 0:
         raise ValueError("conv_soft_records: unsupported node %d depth %d arity %d K %d"
                          % (node_kind, depth, arity, K))
     C, H, W = in_shape
     rec = torch.empty((N, R), device=raw.device, dtype=torch.float32)
     _lib.call("slg_conv_soft_records", _p(_c(conn, torch.float32)), _p(cm), _p(ch), _p(cw), N, K,
-              node_kind, depth, arity, _p(_c(raw, torch.float32)), C, H, W, pad, _p(rec),
-              _stream(raw))
+              node_kind, depth, arity, _p(_c(raw, torch.float32)), C, H, W, pad,
+              int(bool(pool)), _p(rec), _stream(raw))
     return rec
 
 
 def conv_soft_rec(x, rec, N, node_kind, depth, arity, K, pad, pool):
     """Fused soft conv (+ 2x2 max pool) from records built by conv_soft_records
-    for x's (C, H, W) and the same pad; forward only."""
+    for x's (C, H, W), the same pad and the same pooling flag; forward only."""
     require_gpu(x, rec)
     x = _as_f32(x)
     B, Cc, H, W = x.shape
-    R = _lib.lib().slg_conv_soft_record_floats(node_kind, depth, arity, K)
+    R = _lib.lib().slg_conv_soft_record_floats(node_kind, depth, arity, K, int(bool(pool)))
     if R <= 0 or tuple(rec.shape) != (N, R) or rec.dtype != torch.float32 or not rec.is_contiguous():
         raise ValueError("conv_soft_rec: records do not match node %d depth %d arity %d K %d"
                          % (node_kind, depth, arity, K))

@@ -458,11 +458,11 @@ def test_conv_staging_and_records(kernel, hw, cin, B, k, node):
         assert_soft_close(yp, torch_ref.orpool_soft(ref), "pooled")
         w, npar = conv.soft_params(False)
         cm, ch, cw = conv._taps()
-        rec = conv.soft_records(x.shape[1:])
         for pool, got in ((False, y), (True, yp)):
             arr = ops.conv_soft(xd, npar, w, cm, ch, cw, conv._kind(), conv.d, conv.node_arity,
                                 cm.shape[-1], conv.padding, pool)
             assert torch.equal(got, arr)
+            rec = conv.soft_records(x.shape[1:], pool)
             r = ops.conv_soft_rec(xd, rec, 24, conv._kind(), conv.d, conv.node_arity,
                                   cm.shape[-1], conv.padding, pool)
             assert torch.equal(got, r)
