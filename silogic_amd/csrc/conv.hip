@@ -65,6 +65,10 @@ struct ConvCfg {
   static constexpr int THREADS = PARAMS <= 128 ? 512 : 256;
 };
 
+// LDS floats after the S staged samples: 64 dump slots, one per lane, that
+// take the staged floats no window reads.
+constexpr int kConvExtra = 64;
+
 // LDS geometry of one launch (see the layouts above).
 struct ConvGeom {
   int RS;     // row stride: W + pad (row-major) or Wo + pad (sub-plane rows)
@@ -185,37 +189,47 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   for (int i = threadIdx.x; i < ns * g.SST; i += blockDim.x) lds[i] = 0.0f;
   __syncthreads();
   {
+    // Thread t takes elements e = t + i*T (T = blockDim.x) and steps its
+    // (sample, channel, row, column) by T's decomposition with carries, so
+    // that no element needs a division.
     const int HW = H * W;
     const int total = ns * C * HW;
+    const int T = blockDim.x;
     const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(x + (int64_t)b0 * C * HW), (short)0, total * 4, kBufferWord3);
-    const float inv_hw = 1.0f / (float)HW, inv_w = 1.0f / (float)W, inv_c = 1.0f / (float)C;
+    const int tx = T % W, ty = (T / W) % H, tc = (T / HW) % C, ts = T / (HW * C);
+    int px = threadIdx.x % W, py = (threadIdx.x / W) % H, pc = (threadIdx.x / HW) % C,
+        ps = threadIdx.x / (HW * C);
+    const int dump = S * g.SST + lane;
     constexpr int kStage = 8;
-    for (int e0 = threadIdx.x; e0 < total; e0 += kStage * blockDim.x) {
+    for (int e0 = threadIdx.x; e0 < total; e0 += kStage * T) {
       float v[kStage];
 #pragma unroll
       for (int u = 0; u < kStage; ++u)  // offsets past the images read 0
-        v[u] = __uint_as_float(
-            __builtin_amdgcn_raw_buffer_load_b32(src, (e0 + u * (int)blockDim.x) * 4, 0, 0));
+        v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(src, (e0 + u * T) * 4, 0, 0));
 #pragma unroll
       for (int u = 0; u < kStage; ++u) {
-        const int e = e0 + u * (int)blockDim.x;
-        const int sc = div_small(e, HW, inv_hw);
-        const int rem = e - sc * HW;
-        const int y = div_small(rem, W, inv_w);
-        const int xx = rem - y * W;
-        const int s = div_small(sc, C, inv_c);
-        const int c = sc - s * C;
         int at;
-        bool keep = e < total;
+        bool keep = ps < ns;
         if constexpr (PHASE) {
-          const int Y = y + pad, X = xx + pad;
+          const int Y = py + pad, X = px + pad;
           keep = keep && (Y >> 1) < g.PR && (X >> 1) < g.RS;  // rows/columns no window reads
-          at = (Y & 1) * 2 * g.PP + (X & 1) * g.PP + (Y >> 1) * g.RS + (X >> 1);
+          at = ((Y & 1) ? 2 * g.PP : 0) + ((X & 1) ? g.PP : 0) + __umul24(Y >> 1, g.RS) + (X >> 1);
         } else {
-          at = (y + pad) * g.RS + pad + xx;
+          at = __umul24(py + pad, g.RS) + pad + px;
         }
-        if (keep) lds[s * g.SST + c * g.plane + at] = v[u];
+        // elements that are not kept go to this lane's dump slot
+        lds[keep ? __umul24(ps, g.SST) + __umul24(pc, g.plane) + at : dump] = v[u];
+        px += tx;
+        const int cy = px >= W;
+        px -= cy ? W : 0;
+        py += ty + cy;
+        const int cc = py >= H;
+        py -= cc ? H : 0;
+        pc += tc + cc;
+        const int cs = pc >= C;
+        pc -= cs ? C : 0;
+        ps += ts + cs;
       }
     }
   }
@@ -240,47 +254,52 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
     for (int chunk = 0; chunk < nchunks; ++chunk) {
       const int q = chunk * 64 + lane;
       bool active = q < ns * g.LPS;
+      // (sample, row, column) of the lane: pooled row-major lanes walk Wo
+      // columns, the others RS columns (those >= Wo idle). Idle lanes read
+      // at the start of the staged region.
+      constexpr bool LINEAR = PHASE || !POOL;
       const int s = active ? div_small(q, g.LPS, inv_lps) : 0;
-      const int rem = active ? q - s * g.LPS : 0;
-      // (row, column) of the lane within its sample: pooled row-major lanes
-      // walk Wo columns, the others RS columns (those >= Wo idle)
-      const int row = div_small(rem, PHASE || !POOL ? g.RS : Wo, inv_col);
-      const int col = rem - row * (PHASE || !POOL ? g.RS : Wo);
+      const int rem = active ? q - (int)__umul24(s, g.LPS) : 0;
+      const int row = div_small(rem, LINEAR ? g.RS : Wo, inv_col);
+      const int col = rem - (int)__umul24(row, LINEAR ? g.RS : Wo);
       active = active && col < Wo;
-      const int p = row * Wo + col;
-      int bofs;
-      if constexpr (PHASE || !POOL) bofs = rem;                 // row * RS + col
-      else bofs = 2 * row * g.RS + 2 * col;
-      const float* base = lds + s * g.SST + (active ? bofs : 0);
+      const int p = (int)__umul24(row, Wo) + col;
+      const int bofs = LINEAR ? rem : 2 * (int)__umul24(row, g.RS) + 2 * col;
+      const float* base = lds + (active ? __umul24(s, g.SST) + bofs : 0);
 
+      // Tap k of every leaf per step: the guard k < K is uniform, and one
+      // step issues all NLEAF * NQ LDS reads before its first wait.
       constexpr int NQ = POOL ? 4 : 1;
       float v[NQ][NLEAF];
 #pragma unroll
-      for (int l = 0; l < NLEAF; ++l) {
-        float acc[NQ];
+      for (int l = 0; l < NLEAF; ++l)
 #pragma unroll
-        for (int qq = 0; qq < NQ; ++qq) acc[qq] = 0.0f;
+        for (int qq = 0; qq < NQ; ++qq) v[qq][l] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < KM; ++k) {
-          if (k < K) {
+      for (int k = 0; k < KM; ++k) {
+        if (k < K) {
+          float t[NLEAF][NQ];
+#pragma unroll
+          for (int l = 0; l < NLEAF; ++l) {
             if constexpr (PHASE) {
 #pragma unroll
-              for (int qq = 0; qq < 4; ++qq)
-                acc[qq] = fmaf(Pc.wt[l][k], base[Pc.off[l][k][qq]], acc[qq]);
+              for (int qq = 0; qq < 4; ++qq) t[l][qq] = base[Pc.off[l][k][qq]];
             } else {
               const float* t0 = base + Pc.off[l][k][0];
-              acc[0] = fmaf(Pc.wt[l][k], t0[0], acc[0]);
+              t[l][0] = t0[0];
               if constexpr (POOL) {
-                const float* t1 = t0 + g.RS;
-                acc[1] = fmaf(Pc.wt[l][k], t0[1], acc[1]);
-                acc[2] = fmaf(Pc.wt[l][k], t1[0], acc[2]);
-                acc[3] = fmaf(Pc.wt[l][k], t1[1], acc[3]);
+                t[l][1] = t0[1];
+                t[l][2] = t0[g.RS];
+                t[l][3] = t0[g.RS + 1];
               }
             }
           }
-        }
+          __builtin_amdgcn_sched_barrier(0);  // all reads of the step, then the FMAs
 #pragma unroll
-        for (int qq = 0; qq < NQ; ++qq) v[qq][l] = acc[qq];
+          for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+            for (int qq = 0; qq < NQ; ++qq) v[qq][l] = fmaf(Pc.wt[l][k], t[l][qq], v[qq][l]);
+        }
       }
       float best = -INFINITY;
 #pragma unroll
@@ -607,19 +626,21 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   const ConvGeom g = conv_geom(a.C, a.H, a.W, a.pad, POOL, Cfg::PHASE, a.Ho, a.Wo);
   const int64_t per_sample = (int64_t)g.SST * 4;
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
-  SLG_REQUIRE(per_sample <= cap && (int64_t)a.C * a.H * a.W * 4 < (1LL << 31), SLG_E_UNSUPPORTED,
-              "conv_soft: one image (%lld B) exceeds LDS", (long long)per_sample);
+  SLG_REQUIRE(per_sample + kConvExtra * 4 <= cap && (int64_t)a.C * a.H * a.W * 4 < (1LL << 31),
+              SLG_E_UNSUPPORTED, "conv_soft: one image (%lld B) exceeds LDS",
+              (long long)per_sample);
   // Samples per workgroup: two chunks per channel where the images are
   // small; up to half the LDS so that two workgroups share a CU, or all of it
   // when half would leave most lanes of a chunk idle; at least one workgroup
   // per CU.
+  const int64_t room = cap - kConvExtra * 4;
   int64_t S = std::max<int64_t>(1, cdiv(128, g.LPS));
-  const int64_t s_half = cap / 2 / per_sample;
+  const int64_t s_half = (cap / 2 - kConvExtra * 4) / per_sample;
   if (s_half >= 1 && s_half * g.LPS >= 64) S = std::min(S, s_half);
-  else S = std::min(S, std::max<int64_t>(1, std::min(cap / per_sample, cdiv(64, g.LPS))));
+  else S = std::min(S, std::max<int64_t>(1, std::min(room / per_sample, cdiv(64, g.LPS))));
   S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / device_cus()));
   S = std::min<int64_t>(S, a.B);
-  const size_t lds = (size_t)(S * per_sample);
+  const size_t lds = (size_t)(S * per_sample + kConvExtra * 4);
   auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,

@@ -59,7 +59,7 @@ constexpr int kBufferWord3 = 0x00020000;
 // corrects it.
 __device__ inline int div_small(int e, int d, float inv) {
   int q = (int)((float)e * inv);
-  const int r = e - q * d;
+  const int r = e - (int)__umul24(q, d);  // full-rate 24-bit multiply
   q += (r >= d) - (r < 0);
   return q;
 }
