@@ -313,6 +313,41 @@ int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64
                       const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
                       int32_t pool, uint64_t* out, slg_stream_t stream);
 
+/* ---------------------------------------------------------------------- */
+/* Packed building blocks of the silogic.bitpacking API                      */
+/* ---------------------------------------------------------------------- */
+
+/* BitpackedLUTLayer.forward (bitpacking/packed_layer.py:121-178): x [IN,nw]
+ * packed -> out [OUT,nw]; output o reads inputs idx[o][0..arity) (clamped)
+ * and its truth table tt[o], entry e = sum_j x_j << j at bit e
+ * (arity <= 6). */
+int slg_fc_lut_hard(const uint64_t* x, int64_t IN, int64_t nw, const int32_t* idx,
+                    int32_t arity, const uint64_t* tt, int64_t OUT, uint64_t* out,
+                    slg_stream_t stream);
+
+/* packed_unfold (bitpacking/packed_layer.py:224-283): x [C,H*W,nw] ->
+ * out [C*kh*kw, Ho*Wo, nw], row c*kh*kw + dy*kw + dx, zero padding. */
+int slg_packed_unfold(const uint64_t* x, int64_t C, int64_t H, int64_t W, int64_t nw,
+                      int32_t kh, int32_t kw, int32_t stride, int32_t pad, uint64_t* out,
+                      slg_stream_t stream);
+
+/* packed_or_pool (bitpacking/packed_layer.py:286-319): x [C,H*W,nw] ->
+ * out [C,(H/ps)*(W/ps),nw], OR over ps x ps windows (floor sizes). */
+int slg_packed_or_pool(const uint64_t* x, int64_t C, int64_t H, int64_t W, int64_t nw,
+                       int32_t ps, uint64_t* out, slg_stream_t stream);
+
+/* BitpackedConvTreeLayer / BitpackedConvLUTLayer.forward_packed
+ * (bitpacking/packed_layer.py:324-540) on unfolded input xu [P,L,nw]:
+ * output n gathers leaves leaf[n][0..arity^depth) (flat P indices), then
+ * evaluates a tree of arity-input LUT nodes; tables [N][nodes] hold the
+ * nodes level-major (leaves' level first), node m of a level combining
+ * values arity*m .. arity*m+arity-1 of the level below; LUT addressing as
+ * slg_fc_lut_hard (a gate16 node is an arity-2 LUT with entry
+ * (first child) | (second child) << 1). out [N,L,nw]. */
+int slg_lut_tree_hard(const uint64_t* xu, int64_t P, int64_t L, int64_t nw, int64_t N,
+                      const int32_t* leaf, int32_t arity, int32_t depth,
+                      const uint64_t* tables, uint64_t* out, slg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -229,13 +229,22 @@ def forward_hard(spec, sd, x):
     xb = (x.astype(np.float32) >= 1.0).astype(np.uint8) if x.dtype != np.uint8 else x
     if st["kind"] == "fc":
         xp = pack_bits(xb)
+        wire_r = st.get("wire_r", 0)
         for L in st["layers"]:
+            prev = xp
             xp = _fc_any(L, sd, xp)
+            if wire_r and prev.shape[0] == xp.shape[0]:   # packed_model.py:104-108
+                xp[:wire_r] = prev[:wire_r]
     else:
         _, C, H, W = xb.shape
         x3 = pack_conv_input(xb)
+        wr = st.get("wire_residual", 0.0)
         for blk in st["blocks"]:
             y = conv_block(blk, sd, x3, H, W)
+            if wr > 0:   # same-size conv: copy input channels before the pool (221-227)
+                r = min(int(blk["n"] * wr), x3.shape[0])
+                if r > 0:
+                    y[:r] = x3[:r, :H * W]
             x3 = packed_or_pool(y, H, W)
             H, W = H // 2, W // 2
         xp = x3.reshape(-1, x3.shape[2])

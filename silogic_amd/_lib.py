@@ -41,6 +41,10 @@ SIGNATURES = {
     "slg_fc_hard_net": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _I32, _I64, _P, _P]),
     "slg_fc_hard_net_supported": (C.c_int, [_I64, _I32, _P, _I32]),
     "slg_groupsum_packed": (C.c_int, [_P, _I64, _I64, _I32, _P, _P]),
+    "slg_fc_lut_hard": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _I64, _P, _P]),
+    "slg_packed_unfold": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P]),
+    "slg_packed_or_pool": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I32, _P, _P]),
+    "slg_lut_tree_hard": (C.c_int, [_P, _I64, _I64, _I64, _I64, _P, _I32, _I32, _P, _P, _P]),
     "slg_tree_conv_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P,
                                     _P, _I32, _I32, _I64, _I64, _P, _P]),
     "slg_conv_soft_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P,

@@ -218,13 +218,20 @@ class LogicConvNet(nn.Module):
     @torch.no_grad()
     def forward_hard(self, x):
         ops.require_gpu(x)
-        if self.wire_residual > 0:
-            raise NotImplementedError("wire_residual conv nets are not on the packed MI355X path")
         B, C, H, W = x.shape
         xp = ops.pack_bits(x.reshape(B, -1))                  # [C*H*W, nw] = [C,H,W,nw]
         for conv in self._convs():
+            x_in = xp
             xp = conv.packed_forward(xp, (C, H, W), pool=True)
             Ho, Wo = conv._hw_out(H, W)
+            if self.wire_residual > 0:
+                # the first r channels copy the input before the OR-pool
+                # (models.py:252-261); pooling is channel-wise, so pool them
+                r = min(int(conv.n * self.wire_residual), C)
+                if r > 0:
+                    nw = xp.shape[-1]
+                    res = ops.packed_or_pool(x_in.reshape(C, H * W, nw)[:r].contiguous(), Ho, Wo)
+                    xp.view(conv.n, -1, nw)[:r] = res
             C, H, W = conv.n, Ho // 2, Wo // 2
         xp = xp.view(-1, xp.shape[-1])                        # flatten (n, h, w)
         return _hard_fc_stack(self.head_layers, xp, ops.PACKED, B, xp.shape[0],

@@ -329,8 +329,18 @@ def pack_bits(x, word_major=False):
     return xp
 
 
+def _words_for(xp, B, what):
+    """``xp`` [rows, >= ceil(B/64)] cut to exactly ceil(B/64) words per row
+    (the kernels take that as the row stride)."""
+    nw = n_words(B)
+    if xp.dim() != 2 or xp.shape[1] < nw:
+        raise ValueError("%s: packed input must be [rows, >= %d] for B = %d" % (what, nw, B))
+    return xp if xp.shape[1] == nw and xp.is_contiguous() else xp[:, :nw].contiguous()
+
+
 def unpack_bits(xp, B):
     require_gpu(xp)
+    xp = _words_for(xp, B, "unpack_bits")
     D = xp.shape[0]
     out = torch.empty((B, D), device=xp.device, dtype=torch.uint8)
     _lib.call("slg_unpack_bits", _p(xp), B, D, _p(out), _stream(xp))
@@ -431,9 +441,72 @@ def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
 
 def groupsum_packed(xp, B, C):
     require_gpu(xp)
+    xp = _words_for(xp, B, "groupsum_packed")
     W = xp.shape[0]
+    if W % C:
+        raise ValueError("groupsum_packed: %d rows not divisible by %d classes" % (W, C))
     out = torch.empty((B, C), device=xp.device, dtype=torch.float32)
     _lib.call("slg_groupsum_packed", _p(xp), W, B, C, _p(out), _stream(xp))
+    return out
+
+
+def fc_lut_hard(xp, idx, tt):
+    """Packed LUT layer: ``xp`` [IN, nw], ``idx`` [OUT, arity] int32, ``tt``
+    [OUT] int64 truth tables (entry sum_j x_j << j at that bit) -> [OUT, nw]."""
+    require_gpu(xp, idx, tt)
+    IN, nw = xp.shape
+    idx, tt = _c(idx, torch.int32), _c(tt, torch.int64)
+    OUT, arity = idx.shape
+    if tt.shape != (OUT,):
+        raise ValueError("fc_lut_hard: tt must be [OUT] int64")
+    out = torch.empty((OUT, nw), device=xp.device, dtype=torch.int64)
+    _lib.call("slg_fc_lut_hard", _p(_c(xp)), IN, nw, _p(idx), arity, _p(tt), OUT, _p(out),
+              _stream(xp))
+    return out
+
+
+def packed_unfold(x3, kh, kw, stride, padding, H, W):
+    """``x3`` [C, H*W, nw] -> [C*kh*kw, Ho*Wo, nw] (zero padding)."""
+    require_gpu(x3)
+    C, L, nw = x3.shape
+    if L != H * W:
+        raise ValueError("packed_unfold: L = %d is not H*W = %d" % (L, H * W))
+    Ho = (H + 2 * padding - kh) // stride + 1
+    Wo = (W + 2 * padding - kw) // stride + 1
+    if Ho <= 0 or Wo <= 0:
+        raise ValueError("packed_unfold: empty output")
+    out = torch.empty((C * kh * kw, Ho * Wo, nw), device=x3.device, dtype=torch.int64)
+    _lib.call("slg_packed_unfold", _p(_c(x3)), C, H, W, nw, kh, kw, stride, padding, _p(out),
+              _stream(x3))
+    return out
+
+
+def packed_or_pool(x3, H, W, ps=2):
+    """``x3`` [C, H*W, nw] -> [C, (H//ps)*(W//ps), nw], OR over windows."""
+    require_gpu(x3)
+    C, L, nw = x3.shape
+    if L != H * W:
+        raise ValueError("packed_or_pool: L = %d is not H*W = %d" % (L, H * W))
+    out = torch.empty((C, (H // ps) * (W // ps), nw), device=x3.device, dtype=torch.int64)
+    if out.numel():
+        _lib.call("slg_packed_or_pool", _p(_c(x3)), C, H, W, nw, ps, _p(out), _stream(x3))
+    return out
+
+
+def lut_tree_hard(xu, leaf, arity, depth, tables):
+    """LUT tree on unfolded input ``xu`` [P, L, nw]: ``leaf`` [N, arity**depth]
+    int32 flat P indices, ``tables`` [N, nodes] int64 level-major -> [N, L, nw]."""
+    require_gpu(xu, leaf, tables)
+    P, L, nw = xu.shape
+    leaf, tables = _c(leaf, torch.int32), _c(tables, torch.int64)
+    N = leaf.shape[0]
+    nodes = sum(arity ** i for i in range(depth))
+    if leaf.shape != (N, arity ** depth) or tables.shape != (N, nodes):
+        raise ValueError("lut_tree_hard: leaf / table shapes do not match arity %d depth %d"
+                         % (arity, depth))
+    out = torch.empty((N, L, nw), device=xu.device, dtype=torch.int64)
+    _lib.call("slg_lut_tree_hard", _p(_c(xu)), P, L, nw, N, _p(leaf), arity, depth, _p(tables),
+              _p(out), _stream(xu))
     return out
 
 

@@ -115,3 +115,39 @@ def test_public_api_names_mirror_the_reference():
     for name in ["dense_logic", "warp_logic", "tree_conv", "tree_conv_topk", "HAS_DENSE",
                  "HAS_WARP", "HAS_CONV", "HAS_CONV_TOPK"]:
         assert hasattr(silogic_amd.kernels, name), name
+
+
+def test_bitpacking_api_names_and_host_tables():
+    from silogic_amd import bitpacking as bp
+    from silogic_amd.bitpacking.ops import layer_codes
+    from silogic_amd.bitpacking.packed_layer import _tt_word, gate16_lut_word
+    from oracle import packed_ref
+    for name in ["convert_logic_net", "convert_logic_conv_net", "convert_layer", "convert_head",
+                 "BitpackedNet", "BitpackedConvNet", "BitpackedConvGPUNet", "packed_unfold_gpu",
+                 "packed_or_pool_gpu", "pack_bits", "unpack_bits", "n_words", "HAS_TRITON"]:
+        assert hasattr(bp, name), name
+    assert np.array_equal(bp.code_to_gate16(), packed_ref.code_to_gate16())
+    # gate16 as a LUT: entry c0 | c1 << 1 is the gate at address (c0 << 1) | c1
+    for g in range(16):
+        word = gate16_lut_word(g)
+        for c0 in (0, 1):
+            for c1 in (0, 1):
+                a = np.array([-1 if c0 else 0], dtype=np.int64)
+                b = np.array([-1 if c1 else 0], dtype=np.int64)
+                want = int(packed_ref.GATE_OPS[g](a, b)[0] & 1)
+                assert (word >> (c0 | c1 << 1)) & 1 == want, (g, c0, c1)
+    assert _tt_word([0] * 63 + [1]) == -(1 << 63) and _tt_word([1, 0, 1]) == 5
+    codes = layer_codes([1, 15], [3, 7], [5, (1 << 28) - 1], torch.device("cpu")).numpy()
+    code_and = packed_ref.code_to_gate16().tolist().index(1)          # AND's truth-table code
+    assert codes[0, 0] == 3 and (int(codes[0, 1]) & 0xFFFFFFFF) == 5 | (code_and << 28)
+    assert (codes[1, 1].astype(np.int64) & 0xFFFFFFFF) >> 28 == 15
+    with pytest.raises(ValueError):
+        layer_codes([0], [0], [1 << 28], torch.device("cpu"))
+
+
+def test_bitpacking_without_a_gpu_raises():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from silogic_amd import bitpacking as bp
+    with pytest.raises((RuntimeError, AssertionError)):
+        bp.pack_bits(np.zeros((4, 3), dtype=np.uint8))

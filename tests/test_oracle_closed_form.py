@@ -142,6 +142,52 @@ def test_exhaustive_brute_force_small_net():
     assert counts == a[777].astype(int).tolist()
 
 
+def test_wire_residual_fc_three_ways():
+    """Wire residual (models.py:88-94; packed_model.py:104-108): the torch
+    oracle, the packed oracle and a plain loop over all 2^8 inputs agree."""
+    spec = ("LogicNet", dict(in_dim=8, width=12, depth=3, num_classes=4, k=4,
+                             wire_residual=0.25))
+    torch.manual_seed(0)
+    model = silogic_amd.LogicNet(seed=0, **spec[1])
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    x = torch.tensor(list(itertools.product([0, 1], repeat=8)), dtype=torch.float32)
+    a = torch_ref.forward_hard(spec, sd, x).numpy()
+    b = packed_ref.forward_hard(spec, sd, x.numpy())
+    np.testing.assert_array_equal(a, b)
+    wire_r = 3
+    for s_i in (0, 77, 255):
+        cur = x[s_i].long().tolist()
+        for i in range(3):
+            cand, conn = sd[f"layers.{i}._conn.cand"], sd[f"layers.{i}._conn.conn"]
+            gate = sd[f"layers.{i}.node.gate_logits"].argmax(1)
+            nxt = []
+            for o in range(12):
+                ia = int(cand[o, 0, int(conn[o, 0].argmax())])
+                ib = int(cand[o, 1, int(conn[o, 1].argmax())])
+                nxt.append(int(torch_ref.TRUTH[gate[o], (cur[ia] << 1) | cur[ib]]))
+            if len(cur) == len(nxt):          # the first wire_r outputs copy the inputs
+                nxt[:wire_r] = cur[:wire_r]
+            cur = nxt
+        assert [sum(cur[c * 3:(c + 1) * 3]) for c in range(4)] == a[s_i].astype(int).tolist()
+    # the residual changes the result (the check is not vacuous)
+    st_off = dict(spec[1], wire_residual=0.0)
+    assert not np.array_equal(a, torch_ref.forward_hard(("LogicNet", st_off), sd, x).numpy())
+
+
+def test_wire_residual_conv_packed_equals_torch():
+    spec = ("LogicConvNet", dict(in_channels=4, in_hw=6, channels=[4, 4], head_widths=[20],
+                                 num_classes=4, connect="topk", k=4, kernel=3, tree_depth=2,
+                                 n_chan=2, wire_residual=0.5))
+    torch.manual_seed(0)
+    model = silogic_amd.LogicConvNet(seed=0, **spec[1])
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    x = (torch.rand(70, 4, 6, 6, generator=torch.Generator().manual_seed(3)) > 0.5).float()
+    a = torch_ref.forward_hard(spec, sd, x).numpy()
+    np.testing.assert_array_equal(a, packed_ref.forward_hard(spec, sd, x.numpy()))
+    off = ("LogicConvNet", dict(spec[1], wire_residual=0.0))
+    assert not np.array_equal(a, torch_ref.forward_hard(off, sd, x).numpy())
+
+
 @pytest.mark.parametrize("B,dim", [(1, 1), (63, 8), (64, 64), (65, 256), (200, 784)])
 def test_pack_roundtrip_and_layout(B, dim):
     rng = np.random.default_rng(0)
