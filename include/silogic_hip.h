@@ -10,9 +10,9 @@
  *   - Return 0 on success, a negative SLG_E_* code for a rejected argument or
  *     shape (nothing is launched), or a positive hipError_t from the launch.
  *     slg_last_error() returns a thread-local message for the last failure.
- *   - No entry point allocates device memory or needs a workspace: every
- *     intermediate lives in registers or LDS, or in an output array the
- *     caller passes.
+ *   - No entry point allocates device memory. Intermediates live in
+ *     registers or LDS, or in arrays the caller passes: outputs, and for the
+ *     soft backward a workspace whose size slg_fc_soft_bwd_workspace gives.
  *   - Floating-point math is IEEE fp32 (no fast-math); hard paths are exact.
  *
  * Bit-packed layout ("packed"): a [D, nw] array of uint64 words,
@@ -143,6 +143,24 @@ int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT,
 /* 1 if slg_fc_soft_fwd_groupsum runs this shape (one workgroup holds every
  * output of its sample tile), else 0. */
 int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C);
+
+/* Soft FC backward (replaces DenseLogicFn.backward and WarpLogicFn.backward,
+ * kernels/dense.py:46-75, 107-120 and warp.py:33-64, plus the arity-2
+ * multilinear node of nodes.py:174-178): for the layer of slg_fc_soft_fwd
+ * (cand [OUT,2,K] int32, w [OUT,2,K], node_param [OUT,4]) and dL/dy = gy
+ * [B,OUT], writes dL/dx into gx [B,IN], dL/dw into gw [OUT,2,K] and
+ * dL/dnode_param into gnp [OUT,4]; any of the three may be NULL (not
+ * computed). gx is accumulated in LDS with float atomics (the fp32 summation
+ * order varies between runs); gw and gnp are reduced in a fixed order.
+ * workspace: caller-owned device memory of at least
+ * slg_fc_soft_bwd_workspace(B, IN, OUT, K) floats; that function returns
+ * -1 for shapes the kernels do not take (IN beyond what LDS holds). */
+int64_t slg_fc_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t K);
+int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
+                    const int32_t* cand, const float* w, int32_t node_kind,
+                    const float* node_param, float inv_tau, const float* gy, float* gx,
+                    float* gw, float* gnp, float* workspace, int64_t workspace_floats,
+                    slg_stream_t stream);
 
 /* GroupSum.forward (silogic/heads.py:34-39): x [B,W] -> logits [B,C] =
  * sum over class block of (ste ? (x > 0.5) : x), divided by tau. */

@@ -93,6 +93,28 @@ def fc_soft_torch(x, cand, w, npar, node_kind, inv_tau):
     return torch.sigmoid(z * inv_tau) if node_kind == WALSH else z
 
 
+def fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need_x=True, need_w=True,
+                need_np=True):
+    """HIP backward of the FC soft op: ``(gx, gw, gnp)`` (None where not
+    needed), or None when the kernels do not take the shape."""
+    require_gpu(x, cand, w, npar, gy)
+    x, cand = _as_f32(x.detach()), _c(cand, torch.int32)
+    w, npar = _c(w.detach(), torch.float32), _c(npar.detach(), torch.float32)
+    B, IN = x.shape
+    OUT, _, K = cand.shape
+    ws = _lib.lib().slg_fc_soft_bwd_workspace(B, IN, OUT, K)
+    if ws < 0:
+        return None
+    gy = _c(gy, torch.float32)
+    gx = torch.empty_like(x) if need_x else None
+    gw = torch.empty((OUT, 2, K), device=x.device, dtype=torch.float32) if need_w else None
+    gn = torch.empty((OUT, 4), device=x.device, dtype=torch.float32) if need_np else None
+    work = torch.empty(max(ws, 1), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_soft_bwd", _p(x), B, IN, OUT, K, _p(cand), _p(w), node_kind, _p(npar),
+              float(inv_tau), _p(gy), _p(gx), _p(gw), _p(gn), _p(work), ws, _stream(x))
+    return gx, gw, gn
+
+
 class FCSoftFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, cand, w, npar, node_kind, inv_tau):
@@ -107,6 +129,11 @@ class FCSoftFn(torch.autograd.Function):
         x, cand, w, npar = ctx.saved_tensors
         node_kind, inv_tau = ctx.meta
         need = ctx.needs_input_grad
+        got = fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need[0], need[2], need[3])
+        if got is not None:
+            gx, gw, gn = got
+            return gx, None, gw, gn, None, None
+        # shapes the HIP backward does not take: the composite torch backward
         with torch.enable_grad():
             xs = x.detach().requires_grad_(need[0])
             ws = w.detach().requires_grad_(need[2])

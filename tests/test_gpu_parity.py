@@ -553,3 +553,46 @@ def test_gradients_match_the_oracle():
     assert (xg.grad.cpu() - xr.grad).abs().max() < 1e-4
     for name, p in model.named_parameters():
         assert (p.grad.cpu() - params[name].grad).abs().max() < 1e-4, name
+
+
+@pytest.mark.parametrize("node,conn,k,IN,OUT,B", [
+    ("gate16", "topk", 8, 100, 300, 37),       # 4-sample tiles
+    ("gate16", "topk", 8, 7000, 2000, 70),     # 2-sample input-gradient tiles
+    ("gate16", "topk", 8, 15000, 600, 33),     # 1-sample input-gradient tiles
+    ("walsh", "topk", 8, 500, 400, 65),
+    ("multilinear", "topk", 4, 300, 200, 50),
+    ("gate16", "fixed", 1, 200, 150, 40),
+    ("gate16", "topk", 3, 120, 90, 21),        # candidate count known only at run time
+])
+def test_fc_soft_backward_kernels(node, conn, k, IN, OUT, B):
+    """The HIP backward (input, connection and node gradients) against fp32
+    autograd through the oracle's layer (silogic layers.py / connectomes.py /
+    nodes.py semantics) with a random upstream gradient."""
+    if node == "walsh":
+        layer = sl.WARPLayer(IN, OUT, k=k, tau=0.5, seed=4)
+        L = dict(prefix="", node="walsh", arity=2, conn=conn, node_tau=0.5)
+    else:
+        layer = sl.LogicLayer(IN, OUT, node=node, connectome=conn, k=k, seed=4)
+        L = dict(prefix="", node=node, arity=2, conn=conn)
+    params = {kk: v.clone().requires_grad_(v.is_floating_point())
+              for kk, v in layer.state_dict().items()}
+    gen = torch.Generator().manual_seed(5)
+    x = torch.rand(B, IN, generator=gen)
+    gy = torch.randn(B, OUT, generator=gen)
+    xr = x.clone().requires_grad_(True)
+    (torch_ref.fc_layer_soft(L, params, xr) * gy).sum().backward()
+    layer = layer.to(DEV).train()
+    xg = x.to(DEV).requires_grad_(True)
+    (layer(xg) * gy.to(DEV)).sum().backward()
+
+    def close(got, ref, what):
+        got = got.cpu()
+        scale = ref.abs().max().item()
+        err = (got - ref).abs().max().item()
+        assert err <= 1e-4 * scale + 1e-6, f"{what}: max err {err:.3e} (scale {scale:.3e})"
+
+    close(xg.grad, xr.grad, "dL/dx")
+    for name, p in layer.named_parameters():
+        close(p.grad, params[name].grad, name)
+    assert sl.ops.fc_soft_bwd(xg.detach(), *layer.soft_params(True), layer.node.kind,
+                              layer._inv_tau(), gy.to(DEV)) is not None   # the HIP kernels ran
