@@ -61,53 +61,8 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, Para
   }
 
   // Stage S rows transposed: lds[g * IN + i] holds samples b0+gV .. b0+gV+V-1
-  // of input i. Threads load float4 runs of 4 inputs from each of the V rows
-  // of a group (NBAT batches in flight), then scatter them to 4 input slots.
-  const bool vec_rows = (IN & 3) == 0;
-  for (int g = 0; g < G; ++g) {
-    vt* dst = lds + g * IN;
-    if (vec_rows) {
-      const int n4 = IN >> 2;
-      constexpr int NBAT = V == 4 ? 2 : 4;  // float4 batches in flight per thread
-      for (int q0 = threadIdx.x; q0 < n4; q0 += NBAT * blockDim.x) {
-        float4 t[NBAT][V];
-#pragma unroll
-        for (int u = 0; u < NBAT; ++u) {
-          const int q = q0 + u * blockDim.x;
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const int b = b0 + g * V + v;
-            t[u][v] = (b < B && q < n4)
-                          ? ld_stream4(x + (int64_t)b * IN + 4 * q)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < NBAT; ++u) {
-          const int q = q0 + u * blockDim.x;
-          if (q < n4) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              float e[V];
-#pragma unroll
-              for (int v = 0; v < V; ++v) e[v] = lanev(t[u][v], c);
-              dst[4 * q + c] = make_vec<V>(e);
-            }
-          }
-        }
-      }
-    } else {
-      for (int i = threadIdx.x; i < IN; i += blockDim.x) {
-        float e[V];
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          const int b = b0 + g * V + v;
-          e[v] = (b < B) ? __builtin_nontemporal_load(x + (int64_t)b * IN + i) : 0.0f;
-        }
-        dst[i] = make_vec<V>(e);
-      }
-    }
-  }
+  // of input i.
+  for (int g = 0; g < G; ++g) stage_rows<V, true>(lds + g * IN, x, B, IN, b0 + g * V);
   __syncthreads();
 
   const uint32_t lim = (uint32_t)IN - 1u;

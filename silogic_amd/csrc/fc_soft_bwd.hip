@@ -5,23 +5,24 @@
 //                     (and the b side),
 //   gw  [OUT,2,K]   = sum over b of ga[b,o] * x[b, cand_a[o,k]] (and b),
 //   gnp [OUT,4]     = sum over b of dL/dparam,
-// where ga, gb are the node's input gradients at the recomputed operands.
+// where ga, gb are the node's operand gradients at the recomputed operands.
 //
-// Three launches, each shaped for one reduction:
+// No atomics on values, and every sum runs in a fixed order (the gradients
+// are the same bits on every call):
 //   * records: the parameters repacked into the forward's chunk-major
-//     records (natural candidate order), so every parameter load of a wave
-//     is one coalesced 16-byte load per quad.
-//   * fc_soft_bwd_x_kernel: a workgroup owns S samples and every output. It
-//     stages the S rows in LDS next to an S-row gradient accumulator,
-//     recomputes each output's operands, and adds its input gradients with
-//     LDS float atomics; the finished rows are written once. No global
-//     atomics: every contribution to a row of gx comes from this workgroup.
+//     records, so every parameter load of a wave is one 16-byte load per lane.
 //   * fc_soft_bwd_w_kernel: a workgroup owns 1024 outputs (one per thread)
 //     and a range of samples; it streams that range through LDS in S-sample
-//     tiles and keeps its output's 2K + 4 gradient sums in registers, then
-//     writes them once as one partial per sample range.
-//   * fc_soft_bwd_reduce_kernel: sums the partials over sample ranges in a
-//     fixed order (deterministic weight gradients).
+//     tiles, keeps its outputs' 2K + 4 weight / parameter gradient sums in
+//     registers (one partial per sample range), and writes every (sample,
+//     output) operand gradient ga, gb to gbr [B][2*OUT] (coalesced rows).
+//   * fc_soft_bwd_reduce_kernel: sums the partials over sample ranges in
+//     ascending order.
+//   * the input gradient is the transposed problem: a table lists, for every
+//     input, the (row = side*OUT + o, weight) of the references to it in
+//     ascending reference order (count, scan, place, rank kernels); gbr is
+//     transposed to sample-minor rows gab [2*OUT][LB]; the gather kernel
+//     walks each input's entries with its lanes along samples.
 #include "fc_soft_common.h"
 
 namespace slg {
@@ -89,87 +90,262 @@ __global__ void __launch_bounds__(256) fc_soft_pack_records_kernel(const int* __
 template <int KC>
 constexpr int bwd_threads() { return KC > 0 && KC <= 8 ? 1024 : 512; }
 
-// Input gradient of S samples (see the file comment).
-template <int NODE, int KC, int S>
-__global__ void __launch_bounds__((bwd_threads<KC>()))
-fc_soft_bwd_x_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, ParamView pv,
-                     float inv_tau, const float* __restrict__ gy, float* __restrict__ gx) {
-  constexpr int KM = KC > 0 ? KC : 16;
-  using vt = typename vecf<S>::t;
-  extern __shared__ __align__(16) unsigned char smem[];
-  vt* xs = reinterpret_cast<vt*>(smem);                                   // [IN] x S samples
-  float* gs = reinterpret_cast<float*>(smem + (size_t)IN * S * sizeof(float));  // [IN][S]
-  const int K = KC > 0 ? KC : Kr;
-  const int b0 = blockIdx.x * S;
+// ---------------------------------------------------------------------------
+// Transposed reference table: for every input i, the references (o, side, k)
+// whose candidate is i, in ascending r = o*2K + side*K + k (a fixed order, so
+// the input gradient sums in the same order on every call). Built as
+//   cnt = 0; cnt[i] = #refs of i; start = exclusive scan; refs placed by
+//   atomic cursors; each bucket heap-sorted by r; entries (row, weight)
+// where row = side*OUT + o indexes the node-gradient rows.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) fc_soft_bwd_zero_kernel(int* __restrict__ p, int n) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) p[t] = 0;
+}
 
-  for (int i = threadIdx.x; i < IN; i += blockDim.x) {
-    float e[S];
+__global__ void __launch_bounds__(256) fc_soft_bwd_count_kernel(const int* __restrict__ cand, int R,
+                                                                int IN, int* __restrict__ cnt) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  const int i = min(max(cand[r], 0), IN - 1);
+  atomicAdd(&cnt[i], 1);
+}
+
+// One workgroup: start[0..IN] = exclusive scan of cnt, cursor = start.
+__global__ void __launch_bounds__(1024) fc_soft_bwd_scan_kernel(const int* __restrict__ cnt, int IN,
+                                                                int* __restrict__ start,
+                                                                int* __restrict__ cursor) {
+  __shared__ int part[1024];
+  const int t = threadIdx.x;
+  const int per = (IN + 1023) / 1024;
+  const int lo = min(t * per, IN), hi = min(lo + per, IN);
+  int sum = 0;
+  for (int i = lo; i < hi; ++i) sum += cnt[i];
+  part[t] = sum;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = t >= d ? part[t - d] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int run = part[t] - sum;
+  for (int i = lo; i < hi; ++i) {
+    start[i] = run;
+    cursor[i] = run;
+    run += cnt[i];
+  }
+  if (t == 1023) start[IN] = part[1023];
+}
+
+__global__ void __launch_bounds__(256) fc_soft_bwd_fill_kernel(const int* __restrict__ cand, int R,
+                                                               int IN, int* __restrict__ cursor,
+                                                               int* __restrict__ refs) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  const int i = min(max(cand[r], 0), IN - 1);
+  refs[atomicAdd(&cursor[i], 1)] = r;
+}
+
+__device__ inline void sift_down(int* a, int root, int n) {
+  const int v = a[root];
+  for (;;) {
+    int c = 2 * root + 1;
+    if (c >= n) break;
+    if (c + 1 < n && a[c + 1] > a[c]) ++c;
+    if (a[c] <= v) break;
+    a[root] = a[c];
+    root = c;
+  }
+  a[root] = v;
+}
+
+// One wave per input: order its bucket ascending and write (row, weight).
+// Buckets of up to kRankCap references are copied to LDS and each element
+// is placed at its rank (the count of smaller references: all distinct), so
+// the wave's reads are independent broadcasts; larger buckets are
+// heap-sorted in place by one lane.
+constexpr int kRankCap = 512;
+
+__global__ void __launch_bounds__(256) fc_soft_bwd_sort_kernel(const int* __restrict__ start, int IN,
+                                                               int OUT, int K,
+                                                               const float* __restrict__ w,
+                                                               int* __restrict__ refs,
+                                                               int2* __restrict__ ent) {
+  __shared__ int buf[4][kRankCap];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + wave;
+  const int s = i < IN ? start[i] : 0;
+  const int n = i < IN ? start[i + 1] - s : 0;
+  int* a = refs + s;
+  int* bw = buf[wave];
+  const bool small = n <= kRankCap;
+  if (small) {
+    for (int j = lane; j < n; j += 64) bw[j] = a[j];
+  } else if (lane == 0) {
+    for (int r = n / 2 - 1; r >= 0; --r) sift_down(a, r, n);
+    for (int e = n - 1; e > 0; --e) {
+      const int t = a[0];
+      a[0] = a[e];
+      a[e] = t;
+      sift_down(a, 0, e);
+    }
+  }
+  __syncthreads();  // LDS copies and the in-place sorts are visible to the workgroup
+  const int K2 = 2 * K;
+  for (int j = lane; j < n; j += 64) {
+    int r, pos;
+    if (small) {
+      r = bw[j];
+      pos = 0;
+      for (int t = 0; t < n; ++t) pos += bw[t] < r;
+    } else {
+      r = a[j];
+      pos = j;
+    }
+    const int o = r / K2, side = (r - o * K2) / K;
+    ent[s + pos] = make_int2(side * OUT + o, __float_as_int(w[r]));
+  }
+}
+
+// gab [R2][LB] = transpose of gbr [B][R2] (rows b >= B of gab's columns are
+// zero), through a 64 x 64 LDS tile; float4 loads along gbr rows when R2 is
+// a multiple of 4, float4 stores along gab rows (LB is a multiple of 64).
+__global__ void __launch_bounds__(256) fc_soft_bwd_transpose_kernel(const float* __restrict__ gbr,
+                                                                    int B, int R2, int64_t LB,
+                                                                    int n_rtiles,
+                                                                    float* __restrict__ gab) {
+  __shared__ float t[64][65];  // [b][r]
+  const int rt = blockIdx.x % n_rtiles, bt = blockIdx.x / n_rtiles;
+  const int r0 = rt * 64, b0 = bt * 64;
+  const int c4 = threadIdx.x & 15, q = threadIdx.x >> 4;  // 16 float4 columns x 16 rows
+  if ((R2 & 3) == 0) {
 #pragma unroll
-    for (int s = 0; s < S; ++s) e[s] = (b0 + s < B) ? x[(int64_t)(b0 + s) * IN + i] : 0.0f;
-    xs[i] = make_vec<S>(e);
+    for (int k = 0; k < 4; ++k) {
+      const int bl = q + 16 * k, b = b0 + bl, r = r0 + 4 * c4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (b < B && r < R2) v = *reinterpret_cast<const float4*>(gbr + (int64_t)b * R2 + r);
+      t[bl][4 * c4] = v.x;
+      t[bl][4 * c4 + 1] = v.y;
+      t[bl][4 * c4 + 2] = v.z;
+      t[bl][4 * c4 + 3] = v.w;
+    }
+  } else {
+    const int c = threadIdx.x & 63, qq = threadIdx.x >> 6;
 #pragma unroll
-    for (int s = 0; s < S; ++s) gs[i * S + s] = 0.0f;
+    for (int k = 0; k < 16; ++k) {
+      const int bl = qq + 4 * k, b = b0 + bl, r = r0 + c;
+      t[bl][c] = (b < B && r < R2) ? gbr[(int64_t)b * R2 + r] : 0.0f;
+    }
   }
   __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int rl = q + 16 * k, r = r0 + rl;
+    if (r < R2) {
+      const float4 v = make_float4(t[4 * c4][rl], t[4 * c4 + 1][rl], t[4 * c4 + 2][rl],
+                                   t[4 * c4 + 3][rl]);
+      *reinterpret_cast<float4*>(gab + (int64_t)r * LB + b0 + 4 * c4) = v;
+    }
+  }
+}
 
-  const uint32_t lim = (uint32_t)IN - 1u;
-  const int lane = threadIdx.x & 63;
+// Input gradient from the node-gradient rows gab [2*OUT][LB] (row side*OUT+o,
+// sample-minor): gx[b][i] = sum over the entries e of input i, in table
+// order, of weight(e) * gab[row(e)][b]. A workgroup owns 4*IW inputs x 64*V
+// samples. Each wave walks the entries of its IW consecutive inputs as one
+// flat range (contiguous in the table) with its lanes along samples: the
+// entries are wave-uniform (scalar loads, the next 8 prefetched), each costs
+// one coalesced 64V-sample row-segment load, and 8 such loads are in flight.
+// An input's sum is complete when the walk reaches the next input's start.
+// The results go through LDS so gx rows are written contiguously.
+template <int V, int IW>
+__global__ void __launch_bounds__(256) fc_soft_bwd_gather_kernel(const float* __restrict__ gab,
+                                                                 int64_t LB, int B, int IN,
+                                                                 const int* __restrict__ start,
+                                                                 const int2* __restrict__ ent,
+                                                                 int n_itiles, int n_blocks,
+                                                                 float* __restrict__ gx) {
+  using vt = typename vecf<V>::t;
+  constexpr int NI = 4 * IW;       // inputs per workgroup
+  constexpr int NS = 64 * V;       // samples per workgroup
+  constexpr int G = 8;             // entries per step
+  __shared__ float T[NI][NS + 1];  // [input][sample]
+  const int L = (int)xcd_logical_id(blockIdx.x, gridDim.x);
+  if (L >= n_blocks) return;
+  const int it = L % n_itiles, sc = L / n_itiles;
+  const int i0 = it * NI;
+  const int b0 = sc * NS;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwaves = blockDim.x >> 6;
-  const int n64 = (OUT + 63) >> 6;
-  for (int j = wave; j < n64; j += nwaves) {
-    const int o = j * 64 + lane;
-    const bool valid = o < OUT;
-    FcParams<KM> P;
-    load_params<KC, KM, true>(P, min(o, OUT - 1), K, pv);
-    uint32_t ia[KM], ib[KM];
+  const int lane = threadIdx.x & 63;
+  const float* col = gab + b0 + lane * V;
+  const int ia = i0 + wave * IW;
+  const int iend = min(ia + IW, IN);
+  int cur = ia;  // input whose sum is being accumulated
+  float acc[V];
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      ia[k] = min((uint32_t)P.ia[k], lim);
-      ib[k] = min((uint32_t)P.ib[k], lim);
-    }
-    vt A = zero_vec<vt>(), Bv = zero_vec<vt>();
+  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+  if (ia < iend) {
+    int e = start[ia];
+    const int e_end = start[iend];
+    int nb = start[ia + 1];  // first entry of input cur + 1
+    int2 qn[G];
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      if (KC > 0 || k < K) {
-        fma_acc(A, P.fa[k], xs[ia[k]]);
-        fma_acc(Bv, P.fb[k], xs[ib[k]]);
-      }
-    }
-    float ga[S], gb[S];
+    for (int u = 0; u < G; ++u) qn[u] = ent[min(e + u, max(e_end - 1, 0))];
+    while (e < e_end) {
+      int2 q[G];
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const float g = (valid && b0 + s < B) ? gy[(int64_t)(b0 + s) * OUT + o] : 0.0f;
-      float gp[4];
-      node_grad<NODE>(lanev(A, s), lanev(Bv, s), g, P.p, inv_tau, ga[s], gb[s], gp);
-    }
+      for (int u = 0; u < G; ++u) q[u] = qn[u];
+      vt g[G];
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      if (KC > 0 || k < K) {
+      for (int u = 0; u < G; ++u) g[u] = *reinterpret_cast<const vt*>(col + (int64_t)q[u].x * LB);
+      const int en = e + G;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          atomicAdd(&gs[ia[k] * S + s], ga[s] * P.fa[k]);
-          atomicAdd(&gs[ib[k] * S + s], gb[s] * P.fb[k]);
+      for (int u = 0; u < G; ++u) qn[u] = ent[min(en + u, e_end - 1)];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        if (e + u < e_end) {
+          while (e + u == nb) {  // input cur is complete (inputs without entries: zero)
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              T[cur - i0][lane * V + v] = acc[v];
+              acc[v] = 0.0f;
+            }
+            ++cur;
+            nb = start[cur + 1];
+          }
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[v] = fmaf(__int_as_float(q[u].y), lanev(g[u], v), acc[v]);
         }
       }
+      e = en;
+    }
+  }
+  for (; cur < ia + IW; ++cur) {  // the last input with entries, then empty ones
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      T[cur - i0][lane * V + v] = acc[v];
+      acc[v] = 0.0f;
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < IN; i += blockDim.x) {
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-      if (b0 + s < B) gx[(int64_t)(b0 + s) * IN + i] = gs[i * S + s];
+  const int c = threadIdx.x % NI;
+#pragma unroll 4
+  for (int s = threadIdx.x / NI; s < NS; s += 256 / NI) {
+    if (b0 + s < B && i0 + c < IN) gx[(int64_t)(b0 + s) * IN + i0 + c] = T[c][s];
   }
 }
 
 // Weight / node-parameter gradient partials of one output per thread over a
 // range of sample tiles: part [NR][2K+4][OUT] (components w_a[0..K),
-// w_b[0..K), param[0..4)).
+// w_b[0..K), param[0..4)); with gbr, also the node's operand gradients
+// ga, gb of every (sample, output) at gbr[b][o], gbr[b][OUT+o] (rows of
+// 2*OUT, coalesced along the outputs), transposed for the gather kernel.
 template <int NODE, int KC, int S>
 __global__ void __launch_bounds__((bwd_threads<KC>()))
 fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, ParamView pv,
                      float inv_tau, const float* __restrict__ gy, int n_orange, int tiles_per_range,
-                     float* __restrict__ part) {
+                     float* __restrict__ part, float* __restrict__ gbr) {
   constexpr int KM = KC > 0 ? KC : 16;
   using vt = typename vecf<S>::t;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -198,12 +374,7 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
   for (int t = r_b * tiles_per_range; t < t_end; ++t) {
     const int b0 = t * S;
     __syncthreads();  // the previous tile's reads are done
-    for (int i = threadIdx.x; i < IN; i += blockDim.x) {
-      float e[S];
-#pragma unroll
-      for (int s = 0; s < S; ++s) e[s] = (b0 + s < B) ? x[(int64_t)(b0 + s) * IN + i] : 0.0f;
-      xs[i] = make_vec<S>(e);
-    }
+    stage_rows<S, false>(xs, x, B, IN, b0);  // the other output ranges re-read these rows
     __syncthreads();
     vt A = zero_vec<vt>(), Bv = zero_vec<vt>();
 #pragma unroll
@@ -222,6 +393,13 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
 #pragma unroll
       for (int q = 0; q < 4; ++q) sp[q] += gp[q];
     }
+    if (gbr != nullptr && valid) {  // sample rows of 2*OUT; tiles end at or before LB
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        gbr[(int64_t)(b0 + s) * (2 * OUT) + o] = ga[s];
+        gbr[(int64_t)(b0 + s) * (2 * OUT) + OUT + o] = gb[s];
+      }
+    }
     // second pass over the candidates: sum_s ga[s] * x[s][cand]
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
@@ -235,7 +413,7 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
       }
     }
   }
-  if (valid) {
+  if (part != nullptr && valid) {
     float* base = part + (int64_t)r_b * (2 * K + 4) * OUT + o;
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
@@ -277,52 +455,60 @@ static int bwd_tile(int64_t IN, int64_t per_float_bytes_per_sample) {
   return 0;
 }
 
+constexpr int kGatherV = 4;              // samples per lane in the gather kernel
+constexpr int kGatherIW = 8;             // inputs per wave in the gather kernel
+constexpr int kGatherSamples = 64 * kGatherV;
+constexpr int kGatherInputs = 4 * kGatherIW;
+
+inline int64_t round4(int64_t n) { return (n + 3) & ~int64_t(3); }
+
+// Workspace (in 4-byte words): records | partials | gbr | gab | start | cursor | refs | ent.
 struct BwdPlan {
-  int Sx, Sw;          // samples per LDS tile of the two kernels (0 = unsupported)
+  int Sw;              // samples per LDS tile of the weight kernel (0 = unsupported)
   int n_orange, NR, tiles_per_range;
-  int64_t rec_floats, part_floats;
+  int64_t LB;          // gab row stride (samples, padded to the gather tile)
+  int64_t R;           // references = 2 * OUT * K
+  int64_t rec_floats, part_floats, gbr_floats, gab_floats, start_ints, cursor_ints, refs_ints,
+      ent_ints;
+  int64_t total() const {
+    return rec_floats + part_floats + gbr_floats + gab_floats + start_ints + cursor_ints +
+           refs_ints + ent_ints;
+  }
 };
 
 static BwdPlan bwd_plan(int64_t B, int64_t IN, int64_t OUT, int K) {
   BwdPlan p{};
-  p.Sx = bwd_tile(IN, 8);   // x tile + gradient accumulator
   p.Sw = bwd_tile(IN, 4);   // x tile
   if (K == 8) p.Sw = std::min(p.Sw, 2);  // 4-sample tiles overflow 128 VGPRs at 1024 threads
   const int threads = K == 8 || K == 4 ? 1024 : 512;
   p.n_orange = (int)cdiv(OUT, threads);
   const int64_t n_tiles = p.Sw ? cdiv(std::max<int64_t>(B, 1), p.Sw) : 1;
-  p.NR = (int)std::max<int64_t>(1, std::min<int64_t>(n_tiles, cdiv(2 * device_cus(), p.n_orange)));
+  // one round of workgroups: as many sample ranges as resident slots allow
+  // (2048 threads and 160 KB of LDS per CU); a partial second round would
+  // double the kernel's time
+  const int64_t lds = std::max<int64_t>(IN * std::max(p.Sw, 1) * 4, 1);
+  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(2048 / threads, (160 * 1024) / lds));
+  const int64_t slots = per_cu * device_cus();
+  p.NR = (int)std::max<int64_t>(1, std::min<int64_t>(n_tiles, slots / p.n_orange));
   p.tiles_per_range = (int)cdiv(n_tiles, p.NR);
   p.NR = (int)cdiv(n_tiles, p.tiles_per_range);
+  p.LB = cdiv(std::max<int64_t>(B, 1), kGatherSamples) * kGatherSamples;
+  p.R = 2 * OUT * (int64_t)K;
   p.rec_floats = cdiv(OUT, 64) * 64 * (int64_t)(K + 1) * 4;
-  p.part_floats = (int64_t)p.NR * (2 * K + 4) * OUT;
+  p.part_floats = round4((int64_t)p.NR * (2 * K + 4) * OUT);
+  p.gbr_floats = 2 * OUT * p.LB;  // rows b < n_tiles * Sw <= LB
+  p.gab_floats = 2 * OUT * p.LB;
+  p.start_ints = round4(IN + 1);
+  p.cursor_ints = round4(IN);
+  p.refs_ints = round4(p.R);
+  p.ent_ints = 2 * p.R;
   return p;
-}
-
-template <int NODE, int KC, int S>
-static int launch_bwd_x(const float* x, int64_t B, int64_t IN, int64_t OUT, int K,
-                        const ParamView& pv, float inv_tau, const float* gy, float* gx,
-                        hipStream_t st) {
-  auto kern = fc_soft_bwd_x_kernel<NODE, KC, S>;
-  const size_t lds = (size_t)IN * S * 8;
-  if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) {
-      set_error("fc_soft_bwd: LDS %zu: %s", lds, hipGetErrorString(e));
-      return (int)e;
-    }
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(B, S)), dim3(bwd_threads<KC>()), lds, st, x,
-                     (int)B, (int)IN, (int)OUT, K, pv, inv_tau, gy, gx);
-  SLG_LAUNCH_CHECK("fc_soft_bwd_x");
-  return 0;
 }
 
 template <int NODE, int KC, int S>
 static int launch_bwd_w(const float* x, int64_t B, int64_t IN, int64_t OUT, int K,
                         const ParamView& pv, float inv_tau, const float* gy, const BwdPlan& p,
-                        float* part, hipStream_t st) {
+                        float* part, float* gbr, hipStream_t st) {
   auto kern = fc_soft_bwd_w_kernel<NODE, KC, S>;
   const size_t lds = (size_t)IN * S * 4;
   if (lds > 65536) {
@@ -335,36 +521,49 @@ static int launch_bwd_w(const float* x, int64_t B, int64_t IN, int64_t OUT, int 
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)(p.n_orange * p.NR)), dim3(bwd_threads<KC>()), lds, st,
                      x, (int)B, (int)IN, (int)OUT, K, pv, inv_tau, gy, p.n_orange,
-                     p.tiles_per_range, part);
+                     p.tiles_per_range, part, gbr);
   SLG_LAUNCH_CHECK("fc_soft_bwd_w");
   return 0;
 }
 
 template <int NODE, int KC>
 static int bwd_node_k(const float* x, int64_t B, int64_t IN, int64_t OUT, int K,
-                      const ParamView& pv, float inv_tau, const float* gy, float* gx,
-                      float* part, const BwdPlan& p, hipStream_t st) {
-  if (gx) {
-    int rc = p.Sx == 4 ? launch_bwd_x<NODE, KC, 4>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, st)
-           : p.Sx == 2 ? launch_bwd_x<NODE, KC, 2>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, st)
-                       : launch_bwd_x<NODE, KC, 1>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, st);
-    if (rc) return rc;
+                      const ParamView& pv, float inv_tau, const float* gy, float* part, float* gbr,
+                      const BwdPlan& p, hipStream_t st) {
+  if constexpr (KC != 8) {  // K = 8 tiles stop at 2 samples (the plan caps them)
+    if (p.Sw == 4)
+      return launch_bwd_w<NODE, KC, 4>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, gbr, st);
   }
-  if (part) {
-    return p.Sw == 4 ? launch_bwd_w<NODE, KC, 4>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, st)
-         : p.Sw == 2 ? launch_bwd_w<NODE, KC, 2>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, st)
-                     : launch_bwd_w<NODE, KC, 1>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, st);
-  }
-  return 0;
+  return p.Sw >= 2 ? launch_bwd_w<NODE, KC, 2>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, gbr, st)
+                   : launch_bwd_w<NODE, KC, 1>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, gbr, st);
 }
 
 template <int NODE>
 static int bwd_node(const float* x, int64_t B, int64_t IN, int64_t OUT, int K, const ParamView& pv,
-                    float inv_tau, const float* gy, float* gx, float* part, const BwdPlan& p,
+                    float inv_tau, const float* gy, float* part, float* gbr, const BwdPlan& p,
                     hipStream_t st) {
-  if (K == 8) return bwd_node_k<NODE, 8>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, part, p, st);
-  if (K == 4) return bwd_node_k<NODE, 4>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, part, p, st);
-  return bwd_node_k<NODE, 0>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, part, p, st);
+  if (K == 8) return bwd_node_k<NODE, 8>(x, B, IN, OUT, K, pv, inv_tau, gy, part, gbr, p, st);
+  if (K == 4) return bwd_node_k<NODE, 4>(x, B, IN, OUT, K, pv, inv_tau, gy, part, gbr, p, st);
+  return bwd_node_k<NODE, 0>(x, B, IN, OUT, K, pv, inv_tau, gy, part, gbr, p, st);
+}
+
+// The transposed reference table of cand into start / refs / ent.
+static int build_ref_table(const int32_t* cand, const float* w, int64_t IN, int64_t OUT, int K,
+                           const BwdPlan& p, int* start, int* cursor, int* refs, int2* ent,
+                           hipStream_t st) {
+  const int R = (int)p.R;
+  hipLaunchKernelGGL(fc_soft_bwd_zero_kernel, dim3((unsigned)cdiv(IN, 256)), dim3(256), 0, st,
+                     cursor, (int)IN);
+  hipLaunchKernelGGL(fc_soft_bwd_count_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                     cand, R, (int)IN, cursor);
+  hipLaunchKernelGGL(fc_soft_bwd_scan_kernel, dim3(1), dim3(1024), 0, st, cursor, (int)IN, start,
+                     cursor);
+  hipLaunchKernelGGL(fc_soft_bwd_fill_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                     cand, R, (int)IN, cursor, refs);
+  hipLaunchKernelGGL(fc_soft_bwd_sort_kernel, dim3((unsigned)cdiv(IN, 4)), dim3(256), 0, st,
+                     start, (int)IN, (int)OUT, K, w, refs, ent);
+  SLG_LAUNCH_CHECK("fc_soft_bwd table");
+  return 0;
 }
 
 }  // namespace slg
@@ -374,10 +573,10 @@ using namespace slg;
 extern "C" {
 
 int64_t slg_fc_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t K) {
-  if (B < 0 || IN <= 0 || OUT <= 0 || K < 1 || K > 16) return -1;
+  if (B < 0 || IN <= 0 || OUT <= 0 || K < 1 || K > 16 || 2 * OUT * K >= (1LL << 31)) return -1;
   const BwdPlan p = bwd_plan(B, IN, OUT, K);
-  if (!p.Sx || !p.Sw) return -1;
-  return p.rec_floats + p.part_floats;
+  if (!p.Sw) return -1;
+  return p.total();
 }
 
 int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
@@ -391,36 +590,63 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
                   node_kind == SLG_NODE_MULTILINEAR2,
               SLG_E_ARG, "fc_soft_bwd: node_kind %d", node_kind);
   SLG_REQUIRE(B >= 0 && IN > 0 && OUT > 0 && K >= 1 && K <= 16 && B < (1LL << 31) &&
-                  IN < (1LL << 28) && OUT < (1LL << 28) && (int64_t)B * IN < (1LL << 40),
+                  IN < (1LL << 28) && OUT < (1LL << 28) && 2 * OUT * K < (1LL << 31) &&
+                  (int64_t)B * IN < (1LL << 40),
               SLG_E_SHAPE, "fc_soft_bwd: bad sizes");
   const BwdPlan p = bwd_plan(B, IN, OUT, K);
-  SLG_REQUIRE(p.Sx && p.Sw, SLG_E_UNSUPPORTED, "fc_soft_bwd: IN=%lld does not fit LDS",
-              (long long)IN);
-  SLG_REQUIRE(workspace_floats >= p.rec_floats + p.part_floats, SLG_E_ARG,
+  SLG_REQUIRE(p.Sw, SLG_E_UNSUPPORTED, "fc_soft_bwd: IN=%lld does not fit LDS", (long long)IN);
+  SLG_REQUIRE(workspace_floats >= p.total(), SLG_E_ARG,
               "fc_soft_bwd: workspace of %lld floats, %lld needed", (long long)workspace_floats,
-              (long long)(p.rec_floats + p.part_floats));
+              (long long)p.total());
   hipStream_t st = as_stream(stream);
   float* rec = workspace;
-  float* part = workspace + p.rec_floats;
+  float* part = rec + p.rec_floats;
+  float* gbr = part + p.part_floats;
+  float* gab = gbr + p.gbr_floats;
+  int* start = reinterpret_cast<int*>(gab + p.gab_floats);
+  int* cursor = start + p.start_ints;
+  int* refs = cursor + p.cursor_ints;
+  int2* ent = reinterpret_cast<int2*>(refs + p.refs_ints);  // 8-byte aligned: offsets are even
   hipLaunchKernelGGL(fc_soft_pack_records_kernel, dim3((unsigned)cdiv(p.rec_floats, 256)),
                      dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN, rec);
   SLG_LAUNCH_CHECK("fc_soft_pack_records");
   const bool want_w = gw || gnp;
-  if (B > 0) {
+  const bool want_x = gx != nullptr && B > 0;
+  if (B > 0 && (want_w || want_x)) {
     ParamView pv{};
     pv.rec = rec;
     float* pp = want_w ? part : nullptr;
+    float* pg = want_x ? gbr : nullptr;
     int rc = 0;
     switch (node_kind) {
       case SLG_NODE_GATE16:
-        rc = bwd_node<SLG_NODE_GATE16>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, pp, p, st); break;
+        rc = bwd_node<SLG_NODE_GATE16>(x, B, IN, OUT, K, pv, inv_tau, gy, pp, pg, p, st); break;
       case SLG_NODE_WALSH:
-        rc = bwd_node<SLG_NODE_WALSH>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, pp, p, st); break;
+        rc = bwd_node<SLG_NODE_WALSH>(x, B, IN, OUT, K, pv, inv_tau, gy, pp, pg, p, st); break;
       default:
-        rc = bwd_node<SLG_NODE_MULTILINEAR2>(x, B, IN, OUT, K, pv, inv_tau, gy, gx, pp, p, st);
+        rc = bwd_node<SLG_NODE_MULTILINEAR2>(x, B, IN, OUT, K, pv, inv_tau, gy, pp, pg, p, st);
         break;
     }
     if (rc) return rc;
+  }
+  if (want_x) {
+    int rc = build_ref_table(cand, w, IN, OUT, K, p, start, cursor, refs, ent, st);
+    if (rc) return rc;
+    const int R2 = (int)(2 * OUT);
+    const int n_rtiles = (int)cdiv(R2, 64);
+    const int64_t n_tr = n_rtiles * (p.LB / 64);
+    SLG_REQUIRE(n_tr < (1LL << 31), SLG_E_SHAPE, "fc_soft_bwd: grid too large");
+    hipLaunchKernelGGL(fc_soft_bwd_transpose_kernel, dim3((unsigned)n_tr), dim3(256), 0, st, gbr,
+                       (int)B, R2, p.LB, n_rtiles, gab);
+    SLG_LAUNCH_CHECK("fc_soft_bwd_transpose");
+    const int n_itiles = (int)cdiv(IN, kGatherInputs);
+    const int64_t n_blocks = n_itiles * (p.LB / kGatherSamples);
+    SLG_REQUIRE(n_blocks < (1LL << 31) - 8, SLG_E_SHAPE, "fc_soft_bwd: grid too large");
+    const int64_t grid = cdiv(n_blocks, 8) * 8;  // a multiple of 8 for the XCD remap
+    auto gather = fc_soft_bwd_gather_kernel<kGatherV, kGatherIW>;
+    hipLaunchKernelGGL(gather, dim3((unsigned)grid), dim3(256), 0, st,
+                       gab, p.LB, (int)B, (int)IN, start, ent, n_itiles, (int)n_blocks, gx);
+    SLG_LAUNCH_CHECK("fc_soft_bwd_gather");
   }
   if (want_w) {
     const int NR = B > 0 ? p.NR : 0;  // no samples: zero gradients

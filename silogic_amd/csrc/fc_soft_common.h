@@ -45,6 +45,60 @@ __device__ inline float4 ld_stream4(const float* p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Stage V rows of x (samples b0 .. b0+V-1, zeros past B) into LDS
+// transposed: dst[i] holds the V samples of input i. Threads load float4 runs
+// of 4 inputs from each row (NBAT batches in flight per thread), then scatter
+// them to 4 input slots; rows whose length is not a multiple of 4 go one
+// input at a time. STREAM: non-temporal loads (rows read once).
+template <int V, bool STREAM>
+__device__ inline void stage_rows(typename vecf<V>::t* __restrict__ dst,
+                                  const float* __restrict__ x, int B, int IN, int b0) {
+  using vt = typename vecf<V>::t;
+  if ((IN & 3) == 0) {
+    const int n4 = IN >> 2;
+    constexpr int NBAT = V == 4 ? 2 : 4;
+    for (int q0 = threadIdx.x; q0 < n4; q0 += NBAT * blockDim.x) {
+      float4 t[NBAT][V];
+#pragma unroll
+      for (int u = 0; u < NBAT; ++u) {
+        const int q = q0 + u * blockDim.x;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const int b = b0 + v;
+          const float* p = x + (int64_t)b * IN + 4 * q;
+          t[u][v] = (b < B && q < n4)
+                        ? (STREAM ? ld_stream4(p) : *reinterpret_cast<const float4*>(p))
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NBAT; ++u) {
+        const int q = q0 + u * blockDim.x;
+        if (q < n4) {
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) {
+            float e[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) e[v] = lanev(t[u][v], cc);
+            dst[4 * q + cc] = make_vec<V>(e);
+          }
+        }
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < IN; i += blockDim.x) {
+      float e[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int b = b0 + v;
+        const float* p = x + (int64_t)b * IN + i;
+        e[v] = (b < B) ? (STREAM ? __builtin_nontemporal_load(p) : *p) : 0.0f;
+      }
+      dst[i] = make_vec<V>(e);
+    }
+  }
+}
+
 // Node evaluation on the two gathered operands (silogic/nodes.py:86-91 for
 // gate16, the warp_logic form of kernels/warp.py:14-31 for walsh,
 // nodes.py:174-178 with n = 2 for multilinear).
