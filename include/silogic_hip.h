@@ -150,9 +150,9 @@ int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C
  * (cand [OUT,2,K] int32, w [OUT,2,K], node_param [OUT,4]) and dL/dy = gy
  * [B,OUT], writes dL/dx into gx [B,IN], dL/dw into gw [OUT,2,K] and
  * dL/dnode_param into gnp [OUT,4]; any of the three may be NULL (not
- * computed). gx is accumulated in LDS with float atomics (the fp32 summation
- * order varies between runs); gw and gnp are reduced in a fixed order.
- * workspace: caller-owned device memory of at least
+ * computed). No atomics on values: every sum runs in a fixed order, so the
+ * three gradients are the same bits on every call (the reference adds gx
+ * with atomics). workspace: caller-owned device memory of at least
  * slg_fc_soft_bwd_workspace(B, IN, OUT, K) floats; that function returns
  * -1 for shapes the kernels do not take (IN beyond what LDS holds). */
 int64_t slg_fc_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t K);
@@ -308,6 +308,29 @@ int slg_conv_soft_fwd_records(const float* x, int64_t B, int64_t C, int64_t H, i
                               int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
                               int32_t K, const float* rec, int32_t pad, int32_t pool,
                               float* out, slg_stream_t stream);
+
+/* Soft conv backward (replaces the backward of the reference's tree-conv
+ * ops, kernels/conv.py:94-145 and kernels/conv_topk.py:84-121, with the
+ * following OrPool's F.max_pool2d routing, layers.py:558-559, when pool): for
+ * the op of slg_conv_soft_fwd (same arguments; node_param as there: gate16
+ * coefficients [N, 2^depth-1, 4] or LUT values [N, 2^arity]) and dL/dout =
+ * gy [B,N,Ho,Wo], writes dL/dx into gx [B,C,H,W], dL/dw into gw [N,leaves,K]
+ * and dL/dnode_param into gnp; any of the three may be NULL (not computed).
+ * A pooled output's gradient goes to the first window position (row-major)
+ * that holds the window's maximum. No atomics on values: every sum runs in
+ * a fixed order. Supports gate16 trees of depth 1-3 and LUTs of arity 2-6,
+ * K <= 8, and images whose C*H*W floats fit LDS next to the per-tree state;
+ * slg_conv_soft_bwd_workspace returns the workspace floats, or -1 for
+ * shapes the kernel does not take. */
+int64_t slg_conv_soft_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                                    int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                                    int32_t pad, int32_t pool);
+int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                      int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                      const float* node_param, const float* w, const int32_t* cm,
+                      const int32_t* ch, const int32_t* cw, int32_t pad, int32_t pool,
+                      const float* gy, float* gx, float* gw, float* gnp, float* workspace,
+                      int64_t workspace_floats, slg_stream_t stream);
 
 /* Hard conv parameters (layers.py:505-527 + nodes.py:183-189 semantics):
  * leaf (cm,ch,cw) by argmax over conn [N,leaves,K] (conn == NULL: K = 1,

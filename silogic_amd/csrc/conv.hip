@@ -29,7 +29,7 @@
 // channel is the grid's y index, so leaf taps and truth tables are uniform.
 #include <math.h>
 
-#include "slg_common.h"
+#include "conv_tree.h"
 
 namespace slg {
 
@@ -37,16 +37,6 @@ __device__ inline float sigmoidc(float z) { return 1.0f / (1.0f + expf(-z)); }
 
 constexpr int kMaxK = 8;
 
-// NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree) or
-// SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1).
-template <int NODE, int NLEAF>
-struct ConvNode {
-  static constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
-  // parameters kept per channel: gate16 coefficients [NN][4], or for the LUT
-  // the even corner values s[2m] and the differences s[2m+1] - s[2m]
-  static constexpr int NPR = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
-  static constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);  // raw params
-};
 
 // Layout choice and register budget of one kernel variant (host and device).
 __host__ __device__ constexpr bool conv_phase_layout(bool pool, int nleaf, int km) {
@@ -239,8 +229,6 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   const int nchunks = (ns * g.LPS + 63) / 64;
   const float inv_lps = 1.0f / (float)g.LPS;
   const float inv_col = 1.0f / (float)(PHASE || !POOL ? g.RS : Wo);
-  constexpr int H2 = (NODE == SLG_NODE_GATE16) ? 1 : (1 << (NLEAF - 1));
-
   auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int n) {
     int nv;  // the channel in a vector register: vector loads, VGPR parameters
     asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
@@ -304,39 +292,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       float best = -INFINITY;
 #pragma unroll
       for (int qq = 0; qq < NQ; ++qq) {
-        float val;
-        if constexpr (NODE == SLG_NODE_GATE16) {
-          // level i combines children 2m (a) and 2m+1 (b), node ids level-major
-          // (silogic/layers.py:388-401, 408-417)
-          float u[NLEAF];
-#pragma unroll
-          for (int l = 0; l < NLEAF; ++l) u[l] = v[qq][l];
-          int nb = 0;
-#pragma unroll
-          for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
-#pragma unroll
-            for (int m = 0; m < cnt / 2; ++m) {
-              const float a = u[2 * m], b = u[2 * m + 1];
-              const float* c = Pc.par + 4 * (nb + m);
-              u[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
-            }
-            nb += cnt / 2;
-          }
-          val = u[0];
-        } else {
-          // multilinear interpolation of s over the leaves (corner bit j =
-          // leaf j), silogic/nodes.py:174-178, as a lerp tree
-          float t[H2];
-#pragma unroll
-          for (int m = 0; m < H2; ++m) t[m] = fmaf(v[qq][0], Pc.par[H2 + m], Pc.par[m]);
-#pragma unroll
-          for (int j = 1; j < NLEAF; ++j) {
-#pragma unroll
-            for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
-              t[m] = fmaf(v[qq][j], t[2 * m + 1] - t[2 * m], t[2 * m]);
-          }
-          val = t[0];
-        }
+        const float val = conv_tree_eval<NODE, NLEAF>(v[qq], Pc.par);
         best = fmaxf(best, val);
       }
       if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;

@@ -1,0 +1,747 @@
+// ConvLogicTree soft backward for gfx950, with the fused 2x2 OR-pool (the
+// gradients the reference's tree-conv ops return: kernels/conv.py:94-145,
+// kernels/conv_topk.py:84-121, with F.max_pool2d's routing, layers.py:558-559).
+// Given x [B,C,H,W], the trees' taps (cm, ch, cw), leaf weights w and node
+// parameters, and gy [B,N,Ho,Wo] on the (pooled) output, write
+//   gx  [B,C,H,W]   = sum over taps of w * (leaf gradient at the tap's output),
+//   gw  [N,L,K]     = sum over samples and outputs of leaf gradient * tap value,
+//   gnp             = sum over samples and outputs of dL/dparam.
+// With pooling, each pooled output sends its gradient to the first window
+// position (row-major) holding the window's maximum, as F.max_pool2d does.
+//
+// One kernel does the work; no value atomics, and every sum has a fixed
+// order. A workgroup owns a group of TG trees and a range of samples; per
+// sample (the image staged in LDS when it is small, else read through the
+// caches) it
+//   A. for each (tree, routed output): recomputes the leaf values at the
+//      window positions with the forward's tap order, evaluates the tree
+//      (conv_tree_eval: the forward's operations, so the routing compares
+//      the forward's values), routes, and back-propagates to the leaves;
+//      keeps the leaf gradients and the route in LDS, and adds leaf gradient
+//      * tap value (and, for gate16 trees, each node's parameter gradient)
+//      to per-thread sums;
+//   B. gathers the input gradient of every pixel from its channel's taps in
+//      the group (a table of (tree, leaf, dh, dw, weight) per (group,
+//      channel), built once per call and staged in LDS); for LUT trees, adds
+//      each corner's gradient over the sample's outputs (from the leaf
+//      values and upstream gradients kept in LDS) to per-thread sums.
+// At the end of its range the workgroup reduces the per-thread sums over
+// each tree's threads in LDS and writes them as one partial per range; small
+// kernels then add the partials over ranges and, with several groups, the
+// input-gradient partials over groups.
+#include <math.h>
+
+#include <type_traits>
+
+#include "conv_tree.h"
+#include "ref_table.h"
+
+namespace slg {
+
+constexpr int kBwdMaxK = 8;
+constexpr int kBwdThreads = 1024;  // largest workgroup (LDS reduction buffer size)
+constexpr int kBwdNodeAcc = 16;    // node-parameter sums per thread
+
+// Workgroup size cap of a variant: the large trees (LUT arity >= 5, gate16
+// depth 3) need more than the 128 VGPRs of 1024-thread workgroups.
+template <int NODE, int NLEAF>
+__host__ __device__ constexpr int conv_bwd_threads() {
+  return (NODE == SLG_NODE_GATE16 ? NLEAF >= 8 : NLEAF >= 5) ? 512 : 1024;
+}
+
+// Per-thread node-parameter sums: gate16 trees sum every node's four
+// coefficients in phase A; LUT trees take up to 16 corners in phase B.
+template <int NODE, int NLEAF>
+__host__ __device__ constexpr int conv_bwd_nacc() {
+  return NODE == SLG_NODE_GATE16 ? 4 * (NLEAF - 1) : kBwdNodeAcc;
+}
+
+struct ConvBwdArgs {
+  int C, H, W, pad, kernel;
+  int Ho, Wo, P;  // routed map (pooled or the full map) and its size
+  int N, K, TG, TPT, NG, SPR, B;
+};
+
+// LDS layout of one workgroup (offsets in floats).
+struct ConvBwdLds {
+  int xs, tab_start, tab_ent, taps, par, raw, vq, gv, gq, route, red, total;
+};
+
+// XS: the image is staged (C*H*W floats). The table part holds the group's
+// C + 1 bucket starts and its TG * NLEAF * K entries. vq / gq (leaf values
+// and upstream gradients at the routed positions) exist for LUT trees only.
+template <int NODE, int NLEAF, bool POOL>
+__host__ __device__ inline ConvBwdLds conv_bwd_lds(bool XS, int C, int CHW, int TG, int K, int P) {
+  using Nd = ConvNode<NODE, NLEAF>;
+  constexpr bool LUT = NODE != SLG_NODE_GATE16;
+  ConvBwdLds L{};
+  int o = 0;
+  L.xs = o; o += XS ? (CHW + 3) & ~3 : 0;
+  L.tab_start = o; o += (C + 1 + 3) & ~3;
+  L.tab_ent = o; o += TG * NLEAF * K * 4;  // int4 per entry
+  L.taps = o; o += TG * NLEAF * K * 4;     // int4 per tap
+  L.par = o; o += (TG * Nd::NPR + 3) & ~3;
+  L.raw = o; o += LUT ? ((TG * NLEAF * (Nd::NP / 2) + 3) & ~3) : 0;
+  L.vq = o; o += LUT ? ((TG * NLEAF * P + 3) & ~3) : 0;
+  L.gv = o; o += (TG * NLEAF * P + 3) & ~3;
+  L.gq = o; o += LUT ? ((TG * P + 3) & ~3) : 0;
+  L.route = o; o += POOL ? ((TG * P + 3) / 4 + 3) & ~3 : 0;  // bytes
+  L.red = o; o += kBwdThreads;
+  L.total = o;
+  return L;
+}
+
+// Leaf gradients g * dy/dv_l of the tree at leaf values v.
+// Gate16: also adds each node's parameter gradient U * (1, a, b, ab) to
+// accn[4 * node ...].
+template <int NODE, int NLEAF>
+__device__ inline void conv_tree_leaf_grad(const float (&v)[NLEAF], const float* par,
+                                           const float* raw, float g, float (&gl)[NLEAF],
+                                           float* accn) {
+  if constexpr (NODE == SLG_NODE_GATE16) {
+    // node outputs level by level (ids level-major), then U from the root
+    constexpr int NN = NLEAF - 1;
+    float nv[NN], na[NN], nb_[NN];
+    {
+      int nb = 0, prev = -1;  // prev: first id of the previous level (-1: leaves)
+#pragma unroll
+      for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
+#pragma unroll
+        for (int m = 0; m < cnt / 2; ++m) {
+          const float a = prev < 0 ? v[2 * m] : nv[prev + 2 * m];
+          const float b = prev < 0 ? v[2 * m + 1] : nv[prev + 2 * m + 1];
+          const float* c = par + 4 * (nb + m);
+          na[nb + m] = a;
+          nb_[nb + m] = b;
+          nv[nb + m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+        }
+        prev = nb;
+        nb += cnt / 2;
+      }
+    }
+    float U[NN];
+    U[NN - 1] = g;
+    // levels from the root down: level with cnt children starts at id base
+    int base = NN - 1, cnt = 2;
+#pragma unroll
+    for (int lvl = 0; (1 << lvl) < NLEAF; ++lvl) {
+      // nodes of this level: ids base .. base + cnt/2 - 1; children at the
+      // previous level (ids base - cnt .. base - 1) or the leaves
+      const int nodes = cnt / 2;
+#pragma unroll
+      for (int m = 0; m < nodes; ++m) {
+        const int id = base + m;
+        const float* c = par + 4 * id;
+        accn[4 * id] += U[id];
+        accn[4 * id + 1] += U[id] * na[id];
+        accn[4 * id + 2] += U[id] * nb_[id];
+        accn[4 * id + 3] += U[id] * (na[id] * nb_[id]);
+        const float ua = U[id] * (c[1] + c[3] * nb_[id]);
+        const float ub = U[id] * (c[2] + c[3] * na[id]);
+        if (base - cnt < 0) {  // children are leaves
+          gl[2 * m] = ua;
+          gl[2 * m + 1] = ub;
+        } else {
+          U[base - cnt + 2 * m] = ua;
+          U[base - cnt + 2 * m + 1] = ub;
+        }
+      }
+      base -= cnt;
+      cnt *= 2;
+    }
+  } else {
+    // dy/dv_j = multilinear interpolation over the other leaves (in
+    // increasing order) of the differences D[j][q] = s[p | bit j] - s[p],
+    // p = q with a 0 inserted at bit j (raw holds D [NLEAF][2^(NLEAF-1)]).
+    // The lerp tree is reduced as a stream: leaf q is combined with the
+    // pending left siblings of the levels where q has a 1 bit.
+    constexpr int H2 = 1 << (NLEAF - 1);
+#pragma unroll
+    for (int j = 0; j < NLEAF; ++j) {
+      float vo[NLEAF];  // the other leaves, in increasing order
+#pragma unroll
+      for (int i = 0, m = 0; i < NLEAF; ++i)
+        if (i != j) vo[m++] = v[i];
+      float st[NLEAF];
+      const float4* d4 = reinterpret_cast<const float4*>(raw + j * H2);
+#pragma unroll
+      for (int q4 = 0; q4 < (H2 + 3) / 4; ++q4) {
+        float dq[4];
+        if constexpr (H2 >= 4) {
+          const float4 t = d4[q4];
+          dq[0] = t.x; dq[1] = t.y; dq[2] = t.z; dq[3] = t.w;
+        } else {
+#pragma unroll
+          for (int u = 0; u < H2; ++u) dq[u] = raw[j * H2 + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4 && 4 * q4 + u < H2; ++u) {
+          const int q = 4 * q4 + u;
+          float val = dq[u];
+          int lvl = 0;
+#pragma unroll
+          for (; lvl < NLEAF - 1 && ((q >> lvl) & 1); ++lvl)
+            val = fmaf(vo[lvl], val - st[lvl], st[lvl]);
+          st[lvl] = val;
+        }
+      }
+      gl[j] = g * st[NLEAF - 1];
+    }
+    (void)par;
+    (void)accn;
+  }
+}
+
+template <int NODE, int NLEAF, bool POOL, int KM, bool XS>
+__global__ void __launch_bounds__((conv_bwd_threads<NODE, NLEAF>()))
+conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, ConvBwdArgs a,
+                     const float* __restrict__ np, const float* __restrict__ wts,
+                     const int* __restrict__ cm, const int* __restrict__ ch,
+                     const int* __restrict__ cw, const int* __restrict__ tstart,
+                     const int4* __restrict__ tent, float* __restrict__ gx_out,
+                     float* __restrict__ part_w, float* __restrict__ part_np) {
+  using Nd = ConvNode<NODE, NLEAF>;
+  constexpr int NPR = Nd::NPR, NP = Nd::NP;
+  constexpr bool LUT = NODE != SLG_NODE_GATE16;
+  constexpr int NQ = POOL ? 4 : 1;
+  constexpr int NACC = conv_bwd_nacc<NODE, NLEAF>();
+  extern __shared__ __align__(16) float lds[];
+  const int HW = a.H * a.W, CHW = a.C * HW;
+  const ConvBwdLds L = conv_bwd_lds<NODE, NLEAF, POOL>(XS, a.C, CHW, a.TG, a.K, a.P);
+  float* xs = lds + L.xs;
+  int* tab_start = reinterpret_cast<int*>(lds + L.tab_start);
+  int4* tab_ent = reinterpret_cast<int4*>(lds + L.tab_ent);
+  int4* taps = reinterpret_cast<int4*>(lds + L.taps);
+  float* par = lds + L.par;
+  float* raw = lds + L.raw;
+  float* vq = lds + L.vq;
+  float* gv = lds + L.gv;
+  float* gq = lds + L.gq;
+  unsigned char* route = reinterpret_cast<unsigned char*>(lds + L.route);
+  float* red = lds + L.red;
+
+  const int g = (int)(blockIdx.x % (unsigned)a.NG);
+  const int r = (int)(blockIdx.x / (unsigned)a.NG);
+  const int n0 = g * a.TG;
+  const int TG = a.TG, K = a.K, P = a.P;
+  const int tid = threadIdx.x, T = blockDim.x;
+
+  // the group's table (bucket starts relative to the group's first entry)
+  const int e0 = tstart[g * a.C];
+  for (int i = tid; i <= a.C; i += T) tab_start[i] = tstart[g * a.C + i] - e0;
+  for (int i = tid; i < tstart[g * a.C + a.C] - e0; i += T) tab_ent[i] = tent[e0 + i];
+  // taps and parameters of the group's trees (trees past N: zero weight)
+  for (int i = tid; i < TG * NLEAF * K; i += T) {
+    const int t = i / (NLEAF * K), lk = i - t * NLEAF * K;
+    const int n = n0 + t;
+    int4 e = make_int4(0, 0, 0, 0);
+    if (n < a.N) {
+      const int idx = n * NLEAF * K + lk;
+      const int c_ = min(max(cm[idx], 0), a.C - 1);
+      const int dh = min(max(ch[idx], 0), a.kernel - 1) - a.pad;
+      const int dw = min(max(cw[idx], 0), a.kernel - 1) - a.pad;
+      e = make_int4(c_ * HW + dh * a.W + dw, dh, dw, __float_as_int(wts ? wts[idx] : 1.0f));
+    }
+    taps[i] = e;
+  }
+  for (int i = tid; i < TG * NP; i += T) {
+    const int t = i / NP, q = i - t * NP;
+    const int n = min(n0 + t, a.N - 1);
+    const float v = np[(int64_t)n * NP + q];
+    if constexpr (!LUT) {
+      par[i] = v;
+    } else {
+      constexpr int H2 = NP / 2;
+      // kept form: even corners, then odd - even (as the forward keeps them)
+      if ((q & 1) == 0) par[t * NPR + q / 2] = v;
+      else par[t * NPR + H2 + q / 2] = v - np[(int64_t)n * NP + q - 1];
+      // leaf differences D[j][qq] = s[p | bit j] - s[p] at the p with bit j set
+#pragma unroll
+      for (int j = 0; j < NLEAF; ++j) {
+        if ((q >> j) & 1) {
+          const int p0 = q & ~(1 << j);
+          const int qq = ((p0 >> (j + 1)) << j) | (p0 & ((1 << j) - 1));
+          raw[(t * NLEAF + j) * H2 + qq] = v - np[(int64_t)n * NP + p0];
+        }
+      }
+    }
+  }
+
+  // this thread's tree and position slot in phase A
+  const int ta = tid / a.TPT, ja = tid - ta * a.TPT;
+  const bool tree_on = ta < TG && n0 + ta < a.N;
+  float accw[NLEAF][KM];
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+    for (int k = 0; k < KM; ++k) accw[l][k] = 0.0f;
+  float accn[NACC];
+#pragma unroll
+  for (int i = 0; i < NACC; ++i) accn[i] = 0.0f;
+
+  const int b_begin = r * a.SPR, b_end = min(a.B, b_begin + a.SPR);
+  for (int b = b_begin; b < b_end; ++b) {
+    __syncthreads();  // the previous sample's reads are done (and the tables are staged)
+    const float* xb = x + (int64_t)b * CHW;
+    if constexpr (XS) {
+      for (int i0 = tid; i0 < CHW; i0 += 4 * T) {  // four loads in flight per thread
+        float t4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t4[u] = i0 + u * T < CHW ? xb[i0 + u * T] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i0 + u * T < CHW) xs[i0 + u * T] = t4[u];
+      }
+      __syncthreads();
+    }
+    const float* xr = XS ? xs : xb;
+
+    // ---- A: per (tree, routed output) ----
+    if (tree_on) {
+      const int n = n0 + ta;
+      const int4* tp = taps + ta * NLEAF * K;
+      const float* pr = par + ta * NPR;
+      const float* rw = raw + ta * NLEAF * (NP / 2);
+      for (int p = ja; p < P; p += a.TPT) {
+        const int py = p / a.Wo, px = p - py * a.Wo;
+        const int oy = POOL ? 2 * py : py, ox = POOL ? 2 * px : px;
+        float v[NQ][NLEAF];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+          for (int l = 0; l < NLEAF; ++l) v[q][l] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (k < K) {
+#pragma unroll
+            for (int l = 0; l < NLEAF; ++l) {
+              const int4 e = tp[l * K + k];
+#pragma unroll
+              for (int q = 0; q < NQ; ++q) {
+                const int y = oy + (q >> 1), xx = ox + (q & 1);
+                const bool ok = (unsigned)(y + e.y) < (unsigned)a.H &&
+                                (unsigned)(xx + e.z) < (unsigned)a.W;
+                const float xv = ok ? xr[e.x + y * a.W + xx] : 0.0f;
+                v[q][l] = fmaf(__int_as_float(e.w), xv, v[q][l]);
+              }
+            }
+          }
+        }
+        int qs = 0;
+        if constexpr (POOL) {
+          float best = conv_tree_eval<NODE, NLEAF>(v[0], pr);
+#pragma unroll
+          for (int q = 1; q < 4; ++q) {
+            const float val = conv_tree_eval<NODE, NLEAF>(v[q], pr);
+            if (val > best) {
+              best = val;
+              qs = q;
+            }
+          }
+        }
+        float vs[NLEAF];
+#pragma unroll
+        for (int l = 0; l < NLEAF; ++l) {
+          float sv = v[0][l];
+#pragma unroll
+          for (int q = 1; q < NQ; ++q) sv = qs == q ? v[q][l] : sv;
+          vs[l] = sv;
+        }
+        const float gup = gy[((int64_t)b * a.N + n) * P + p];
+        float gl[NLEAF];
+        conv_tree_leaf_grad<NODE, NLEAF>(vs, pr, rw, gup, gl, accn);
+        const int y = oy + (qs >> 1), xx = ox + (qs & 1);
+#pragma unroll
+        for (int l = 0; l < NLEAF; ++l) {
+          if constexpr (LUT) vq[(ta * NLEAF + l) * P + p] = vs[l];
+          gv[(ta * NLEAF + l) * P + p] = gl[l];
+#pragma unroll
+          for (int k = 0; k < KM; ++k) {
+            if (k < K) {
+              const int4 e = tp[l * K + k];
+              const bool ok = (unsigned)(y + e.y) < (unsigned)a.H &&
+                              (unsigned)(xx + e.z) < (unsigned)a.W;
+              const float xv = ok ? xr[e.x + y * a.W + xx] : 0.0f;
+              accw[l][k] = fmaf(gl[l], xv, accw[l][k]);
+            }
+          }
+        }
+        if constexpr (LUT) gq[ta * P + p] = gup;
+        if constexpr (POOL) route[ta * P + p] = (unsigned char)qs;
+      }
+    }
+    __syncthreads();
+
+    // ---- B1: input gradient of every pixel from the group's taps ----
+    for (int e = tid; gx_out != nullptr && e < CHW; e += T) {
+      const int c = e / HW, hw = e - c * HW;
+      const int h = hw / a.W, w = hw - h * a.W;
+      const int j1 = tab_start[c + 1];
+      float acc = 0.0f;
+#pragma unroll 4
+      for (int j = tab_start[c]; j < j1; ++j) {
+        const int4 en = tab_ent[j];  // (t * NLEAF + l, dh, dw, weight)
+        const int y = h - en.y, xx = w - en.z;  // the tap's output position
+        float gval = 0.0f;
+        if constexpr (POOL) {
+          const int py = y >> 1, px = xx >> 1;
+          if (y >= 0 && xx >= 0 && py < a.Ho && px < a.Wo) {
+            const int pp = py * a.Wo + px;
+            const int t = en.x / NLEAF;
+            if (route[t * P + pp] == (unsigned char)(((y & 1) << 1) | (xx & 1)))
+              gval = gv[en.x * P + pp];
+          }
+        } else {
+          if ((unsigned)y < (unsigned)a.Ho && (unsigned)xx < (unsigned)a.Wo)
+            gval = gv[en.x * P + y * a.Wo + xx];
+        }
+        acc = fmaf(__int_as_float(en.w), gval, acc);
+      }
+      gx_out[((int64_t)g * a.B + b) * CHW + e] = acc;
+    }
+
+    // ---- B2 (LUT trees): corner gradients over the sample's outputs ----
+    if constexpr (LUT) {
+      int slot = 0;
+      for (int it = tid; it < TG * NP; it += T, ++slot) {
+        const int t = it / NP, item = it - t * NP;
+        if (n0 + t >= a.N) continue;
+        float sum = 0.0f;
+        for (int p = 0; p < P; ++p) {
+          // corner weight of corner `item`: prod over leaves of v or 1 - v
+          float wgt = gq[t * P + p];
+#pragma unroll
+          for (int l = 0; l < NLEAF; ++l) {
+            const float lv = vq[(t * NLEAF + l) * P + p];
+            wgt *= ((item >> l) & 1) ? lv : 1.0f - lv;
+          }
+          sum += wgt;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < NACC; ++s2)
+          if (s2 == slot) accn[s2] += sum;
+      }
+    }
+  }
+
+  // ---- range sums, reduced over each tree's phase-A threads in LDS ----
+  auto reduce_tree = [&](float val, float* dst, int stride, int col) {
+    __syncthreads();
+    red[tid] = tree_on ? val : 0.0f;
+    __syncthreads();
+    if (tid < TG && n0 + tid < a.N) {
+      float sum = 0.0f;
+      for (int j = 0; j < a.TPT; ++j) sum += red[tid * a.TPT + j];
+      dst[(int64_t)(n0 + tid) * stride + col] = sum;
+    }
+  };
+  float* pw = part_w + (int64_t)r * a.N * (NLEAF * K);
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+      if (k < K) reduce_tree(accw[l][k], pw, NLEAF * K, l * K + k);
+  float* pn = part_np + (int64_t)r * a.N * NP;
+  if constexpr (!LUT) {
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) reduce_tree(accn[i], pn, NP, i);
+  } else {
+    int slot = 0;
+    for (int it = tid; it < TG * NP; it += T, ++slot) {
+      const int t = it / NP, item = it - t * NP;
+      if (n0 + t >= a.N) continue;
+#pragma unroll
+      for (int s2 = 0; s2 < NACC; ++s2)
+        if (s2 == slot) pn[(int64_t)(n0 + t) * NP + item] = accn[s2];
+    }
+  }
+}
+
+// gx[b][e] = sum over groups of part[g][b][e], groups ascending.
+__global__ void __launch_bounds__(256) conv_bwd_sum_groups_kernel(const float* __restrict__ part,
+                                                                  int NG, int64_t n,
+                                                                  float* __restrict__ gx) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.0f;
+  for (int g = 0; g < NG; ++g) s += part[(int64_t)g * n + i];
+  gx[i] = s;
+}
+
+// out[i] = sum over ranges of part[r][i], ranges ascending.
+__global__ void __launch_bounds__(256) conv_bwd_sum_ranges_kernel(const float* __restrict__ part,
+                                                                  int NR, int64_t n,
+                                                                  float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.0f;
+  for (int r = 0; r < NR; ++r) s += part[(int64_t)r * n + i];
+  out[i] = s;
+}
+
+// Table keys: tap (n, l, k) -> group * C + channel.
+__global__ void __launch_bounds__(256) conv_bwd_keys_kernel(const int* __restrict__ cm, int R,
+                                                            int LK, int TG, int C,
+                                                            int* __restrict__ keys) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  const int n = r / LK;
+  keys[r] = (n / TG) * C + min(max(cm[r], 0), C - 1);
+}
+
+// Table entries: sorted tap r -> (tree in group * NLEAF + leaf, dh, dw, weight).
+__global__ void __launch_bounds__(256) conv_bwd_entries_kernel(const int* __restrict__ sorted,
+                                                               int R, int NLEAF, int K, int TG,
+                                                               int kernel, int pad,
+                                                               const int* __restrict__ ch,
+                                                               const int* __restrict__ cw,
+                                                               const float* __restrict__ wts,
+                                                               int4* __restrict__ ent) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= R) return;
+  const int r = sorted[j];
+  const int n = r / (NLEAF * K), l = (r / K) % NLEAF;
+  const int dh = min(max(ch[r], 0), kernel - 1) - pad;
+  const int dw = min(max(cw[r], 0), kernel - 1) - pad;
+  ent[j] = make_int4((n % TG) * NLEAF + l, dh, dw, __float_as_int(wts ? wts[r] : 1.0f));
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct ConvBwdPlan {
+  bool XS;  // image staged in LDS
+  int TG, TPT, threads, NG, NR, SPR;
+  size_t lds;
+  int64_t R;  // taps N * NLEAF * K
+  // workspace (4-byte words): keys | table | entries (int4) | part_x | part_w | part_np
+  int64_t keys_ints, table_ints, ent_ints, partx_floats, partw_floats, partn_floats;
+  int64_t total() const {
+    return keys_ints + table_ints + ent_ints + partx_floats + partw_floats + partn_floats;
+  }
+};
+
+static int next_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+template <int NODE, int NLEAF, bool POOL>
+static bool conv_bwd_plan_t(int64_t B, int64_t C, int64_t H, int64_t W, int64_t N, int K,
+                            int64_t Ho, int64_t Wo, ConvBwdPlan& p) {
+  using Nd = ConvNode<NODE, NLEAF>;
+  const int64_t CHW = C * H * W, P = Ho * Wo;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  if (CHW >= (1LL << 26) || P >= (1LL << 20) || P < 1 || C >= (1LL << 16)) return false;
+  constexpr bool LUT = NODE != SLG_NODE_GATE16;
+  constexpr int TMAX = conv_bwd_threads<NODE, NLEAF>();
+  // largest tree group (a power of two) whose state fits LDS, with the image
+  // staged or read through the caches
+  auto best_tg = [&](bool xs, int& tpt, int& threads, size_t& lds) {
+    for (int TG = std::min(TMAX, next_pow2((int)std::min<int64_t>(N, TMAX))); TG >= 1;
+         TG >>= 1) {
+      const ConvBwdLds L = conv_bwd_lds<NODE, NLEAF, POOL>(xs, (int)C, (int)CHW, TG, K, (int)P);
+      const int TPT = std::min(TMAX / TG, next_pow2((int)P));
+      const int th = std::max(64, TG * TPT);
+      const int slots = LUT ? (TG * Nd::NP + th - 1) / th : 0;  // corners per thread
+      if ((int64_t)L.total * 4 <= cap && slots <= kBwdNodeAcc) {
+        tpt = TPT;
+        threads = (th + 63) & ~63;
+        lds = (size_t)L.total * 4;
+        return TG;
+      }
+    }
+    return 0;
+  };
+  int tpt_s = 0, th_s = 0, tpt_g = 0, th_g = 0;
+  size_t lds_s = 0, lds_g = 0;
+  const int tg_s = best_tg(true, tpt_s, th_s, lds_s);
+  const int tg_g = best_tg(false, tpt_g, th_g, lds_g);
+  // stage the image unless that leaves room for fewer than 16 trees (or all
+  // of them) while reading it through the caches fits more
+  const bool xs = tg_s > 0 && (tg_s >= std::min<int64_t>(N, 16) || tg_g <= tg_s);
+  p.XS = xs;
+  p.TG = xs ? tg_s : tg_g;
+  if (p.TG < 1) return false;
+  p.TPT = xs ? tpt_s : tpt_g;
+  p.threads = xs ? th_s : th_g;
+  p.lds = xs ? lds_s : lds_g;
+  p.NG = (int)cdiv(N, p.TG);
+  const int64_t per_cu = std::max<int64_t>(
+      1, std::min<int64_t>(2048 / p.threads, (int64_t)(160 * 1024) / (int64_t)p.lds));
+  const int64_t slots = per_cu * device_cus();
+  int64_t NR = std::max<int64_t>(1, std::min<int64_t>(B, slots / p.NG));
+  p.SPR = (int)cdiv(B, NR);
+  p.NR = (int)cdiv(B, p.SPR);
+  p.R = N * NLEAF * (int64_t)K;
+  const int64_t nkeys = (int64_t)p.NG * C;
+  p.keys_ints = (p.R + 3) & ~3LL;
+  p.table_ints = ref_table_ints(p.R, nkeys);
+  p.ent_ints = 4 * p.R;
+  p.partx_floats = p.NG > 1 ? (((int64_t)p.NG * B * CHW + 3) & ~3LL) : 0;
+  p.partw_floats = ((int64_t)p.NR * N * NLEAF * K + 3) & ~3LL;
+  p.partn_floats = ((int64_t)p.NR * N * Nd::NP + 3) & ~3LL;
+  return true;
+}
+
+static int conv_bwd_leaves(int node, int depth, int arity) {
+  if (node == SLG_NODE_GATE16) return (depth >= 1 && depth <= 3) ? (1 << depth) : -1;
+  if (node == SLG_NODE_MULTILINEAR2) return (depth == 1 && arity >= 2 && arity <= 6) ? arity : -1;
+  return -1;
+}
+
+// Dispatch over (node, leaves, pool) with a callable taking the template
+// arguments as integral constants.
+template <typename F>
+static int conv_bwd_dispatch(int node, int nleaf, bool pool, F&& f) {
+#define SLG_CB(NODE_, NL_)                                                           \
+  if (node == NODE_ && nleaf == NL_)                                                 \
+    return pool ? f(std::integral_constant<int, NODE_>{}, std::integral_constant<int, NL_>{}, \
+                    std::true_type{})                                                \
+                : f(std::integral_constant<int, NODE_>{}, std::integral_constant<int, NL_>{}, \
+                    std::false_type{});
+  SLG_CB(SLG_NODE_GATE16, 2)
+  SLG_CB(SLG_NODE_GATE16, 4)
+  SLG_CB(SLG_NODE_GATE16, 8)
+  SLG_CB(SLG_NODE_MULTILINEAR2, 2)
+  SLG_CB(SLG_NODE_MULTILINEAR2, 3)
+  SLG_CB(SLG_NODE_MULTILINEAR2, 4)
+  SLG_CB(SLG_NODE_MULTILINEAR2, 5)
+  SLG_CB(SLG_NODE_MULTILINEAR2, 6)
+#undef SLG_CB
+  set_error("conv_soft_bwd: unsupported leaves %d", nleaf);
+  return SLG_E_UNSUPPORTED;
+}
+
+}  // namespace slg
+
+using namespace slg;
+
+extern "C" {
+
+int64_t slg_conv_soft_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                                    int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                                    int32_t pad, int32_t pool) {
+  const int nleaf = conv_bwd_leaves(node_kind, depth, arity);
+  if (nleaf <= 0 || K < 1 || K > kBwdMaxK || B < 0 || C <= 0 || H <= 0 || W <= 0 || N <= 0 ||
+      pad < 0 || pad > 4 || B >= (1LL << 31) || N >= (1LL << 20) || C >= (1LL << 20) ||
+      H >= 4096 || W >= 4096 || N * nleaf * K >= (1LL << 31))
+    return -1;
+  const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
+  if (Ho == 0 || Wo == 0) return 0;
+  ConvBwdPlan p{};
+  bool ok = false;
+  conv_bwd_dispatch(node_kind, nleaf, pool != 0, [&](auto nd, auto nl, auto pl) {
+    ok = conv_bwd_plan_t<decltype(nd)::value, decltype(nl)::value, decltype(pl)::value>(
+        std::max<int64_t>(B, 1), C, H, W, N, K, Ho, Wo, p);
+    return 0;
+  });
+  return ok ? p.total() : -1;
+}
+
+int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                      int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
+                      const float* node_param, const float* w, const int32_t* cm,
+                      const int32_t* ch, const int32_t* cw, int32_t pad, int32_t pool,
+                      const float* gy, float* gx, float* gw, float* gnp, float* workspace,
+                      int64_t workspace_floats, slg_stream_t stream) {
+  SLG_REQUIRE(node_param && cm && ch && cw && workspace && ((x && gy) || B == 0), SLG_E_ARG,
+              "conv_soft_bwd: null pointer");
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
+              "conv_soft_bwd: node_kind %d", node_kind);
+  const int nleaf = conv_bwd_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_bwd: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(K >= 1 && K <= kBwdMaxK, SLG_E_SHAPE, "conv_soft_bwd: K=%d outside 1..%d", K,
+              kBwdMaxK);
+  SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && N > 0 && pad >= 0 && pad <= 4 &&
+                  B < (1LL << 31) && N < (1LL << 20) && C < (1LL << 20) && H < 4096 &&
+                  W < 4096 && N * nleaf * K < (1LL << 31),
+              SLG_E_SHAPE, "conv_soft_bwd: bad sizes");
+  const int kernel = 2 * pad + 1;  // 'same' convolution, stride 1 (models.py:222)
+  const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
+  hipStream_t st = as_stream(stream);
+  const int64_t CHW = C * H * W;
+  if (B == 0) {
+    // no samples: zero weight / parameter gradients (a sum over no ranges)
+    const int64_t NP = node_kind == SLG_NODE_GATE16 ? 4 * (nleaf - 1) : (1 << nleaf);
+    const int64_t nw = N * nleaf * K;
+    if (gw)
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(nw, 256)), dim3(256), 0,
+                         st, workspace, 0, nw, gw);
+    if (gnp)
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(N * NP, 256)),
+                         dim3(256), 0, st, workspace, 0, N * NP, gnp);
+    SLG_LAUNCH_CHECK("conv_soft_bwd zero");
+    return 0;
+  }
+  SLG_REQUIRE(Ho > 0 && Wo > 0, SLG_E_SHAPE, "conv_soft_bwd: empty output map");
+  return conv_bwd_dispatch(node_kind, nleaf, pool != 0, [&](auto nd, auto nl, auto pl) -> int {
+    constexpr int NODE = decltype(nd)::value, NL = decltype(nl)::value;
+    constexpr bool POOL = decltype(pl)::value;
+    using Nd = ConvNode<NODE, NL>;
+    ConvBwdPlan p{};
+    SLG_REQUIRE((conv_bwd_plan_t<NODE, NL, POOL>(B, C, H, W, N, K, Ho, Wo, p)),
+                SLG_E_UNSUPPORTED, "conv_soft_bwd: image of %lld floats does not fit LDS",
+                (long long)CHW);
+    SLG_REQUIRE(workspace_floats >= p.total(), SLG_E_ARG,
+                "conv_soft_bwd: workspace of %lld floats, %lld needed",
+                (long long)workspace_floats, (long long)p.total());
+    int* keys = reinterpret_cast<int*>(workspace);
+    int* table = keys + p.keys_ints;
+    int4* ent = reinterpret_cast<int4*>(table + p.table_ints);  // 16-byte aligned offsets
+    float* partx = reinterpret_cast<float*>(ent) + p.ent_ints;
+    float* partw = partx + p.partx_floats;
+    float* partn = partw + p.partw_floats;
+    const int R = (int)p.R;
+    hipLaunchKernelGGL(conv_bwd_keys_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st, cm,
+                       R, NL * K, p.TG, (int)C, keys);
+    RefTable tb{};
+    int rc = build_ref_table(keys, R, (int64_t)p.NG * C, table, st, &tb);
+    if (rc) return rc;
+    hipLaunchKernelGGL(conv_bwd_entries_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                       tb.sorted, R, NL, K, p.TG, kernel, (int)pad, ch, cw, w, ent);
+    SLG_LAUNCH_CHECK("conv_soft_bwd entries");
+
+    ConvBwdArgs a{};
+    a.C = (int)C; a.H = (int)H; a.W = (int)W; a.pad = pad; a.kernel = kernel;
+    a.Ho = (int)Ho; a.Wo = (int)Wo; a.P = (int)(Ho * Wo);
+    a.N = (int)N; a.K = K; a.TG = p.TG; a.TPT = p.TPT; a.NG = p.NG; a.SPR = p.SPR; a.B = (int)B;
+    // gx written directly when one group holds every tree; none when not wanted
+    float* gxo = gx == nullptr ? nullptr : (p.NG > 1 ? partx : gx);
+    auto kern = (K <= 4) ? (p.XS ? conv_soft_bwd_kernel<NODE, NL, POOL, 4, true>
+                                 : conv_soft_bwd_kernel<NODE, NL, POOL, 4, false>)
+                         : (p.XS ? conv_soft_bwd_kernel<NODE, NL, POOL, kBwdMaxK, true>
+                                 : conv_soft_bwd_kernel<NODE, NL, POOL, kBwdMaxK, false>);
+    if (p.lds > 65536) {
+      hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
+      if (e != hipSuccess) {
+        set_error("conv_soft_bwd: LDS %zu: %s", p.lds, hipGetErrorString(e));
+        return (int)e;
+      }
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)(p.NG * p.NR)), dim3(p.threads), p.lds, st, x, gy, a,
+                       node_param, w, cm, ch, cw, tb.start, ent, gxo, partw, partn);
+    SLG_LAUNCH_CHECK("conv_soft_bwd");
+    if (gx != nullptr && p.NG > 1) {
+      const int64_t n = B * CHW;
+      hipLaunchKernelGGL(conv_bwd_sum_groups_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                         st, partx, p.NG, n, gx);
+    }
+    if (gw) {
+      const int64_t n = N * NL * K;
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                         st, partw, p.NR, n, gw);
+    }
+    if (gnp) {
+      const int64_t n = N * Nd::NP;
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                         st, partn, p.NR, n, gnp);
+    }
+    SLG_LAUNCH_CHECK("conv_soft_bwd sums");
+    return 0;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+// The tree of one ConvLogicTree output channel, shared by the soft forward
+// and backward kernels so that both evaluate it with the same operations
+// (the backward's max-pool routing compares the forward's exact values).
+#pragma once
+
+#include "slg_common.h"
+
+namespace slg {
+
+// NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree) or
+// SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1).
+template <int NODE, int NLEAF>
+struct ConvNode {
+  static constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
+  // parameters kept per channel: gate16 coefficients [NN][4], or for the LUT
+  // the even corner values s[2m] and the differences s[2m+1] - s[2m]
+  static constexpr int NPR = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
+  static constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);  // raw params
+};
+
+// Tree value at leaf values v with kept parameters par (ConvNode::NPR).
+template <int NODE, int NLEAF>
+__device__ inline float conv_tree_eval(const float (&v)[NLEAF], const float* par) {
+  if constexpr (NODE == SLG_NODE_GATE16) {
+    // level i combines children 2m (a) and 2m+1 (b), node ids level-major
+    // (silogic/layers.py:388-401, 408-417)
+    float u[NLEAF];
+#pragma unroll
+    for (int l = 0; l < NLEAF; ++l) u[l] = v[l];
+    int nb = 0;
+#pragma unroll
+    for (int cnt = NLEAF; cnt > 1; cnt >>= 1) {
+#pragma unroll
+      for (int m = 0; m < cnt / 2; ++m) {
+        const float a = u[2 * m], b = u[2 * m + 1];
+        const float* c = par + 4 * (nb + m);
+        u[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+      }
+      nb += cnt / 2;
+    }
+    return u[0];
+  } else {
+    // multilinear interpolation of s over the leaves (corner bit j = leaf
+    // j), silogic/nodes.py:174-178, as a lerp tree
+    constexpr int H2 = 1 << (NLEAF - 1);
+    float t[H2];
+#pragma unroll
+    for (int m = 0; m < H2; ++m) t[m] = fmaf(v[0], par[H2 + m], par[m]);
+#pragma unroll
+    for (int j = 1; j < NLEAF; ++j) {
+#pragma unroll
+      for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
+        t[m] = fmaf(v[j], t[2 * m + 1] - t[2 * m], t[2 * m]);
+    }
+    return t[0];
+  }
+}
+
+}  // namespace slg

@@ -24,6 +24,7 @@
 //     transposed to sample-minor rows gab [2*OUT][LB]; the gather kernel
 //     walks each input's entries with its lanes along samples.
 #include "fc_soft_common.h"
+#include "ref_table.h"
 
 namespace slg {
 
@@ -93,119 +94,24 @@ constexpr int bwd_threads() { return KC > 0 && KC <= 8 ? 1024 : 512; }
 // ---------------------------------------------------------------------------
 // Transposed reference table: for every input i, the references (o, side, k)
 // whose candidate is i, in ascending r = o*2K + side*K + k (a fixed order, so
-// the input gradient sums in the same order on every call). Built as
-//   cnt = 0; cnt[i] = #refs of i; start = exclusive scan; refs placed by
-//   atomic cursors; each bucket heap-sorted by r; entries (row, weight)
-// where row = side*OUT + o indexes the node-gradient rows.
+// the input gradient sums in the same order on every call), as entries
+// (row, weight) with row = side*OUT + o indexing the operand-gradient rows.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) fc_soft_bwd_zero_kernel(int* __restrict__ p, int n) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) p[t] = 0;
-}
-
-__global__ void __launch_bounds__(256) fc_soft_bwd_count_kernel(const int* __restrict__ cand, int R,
-                                                                int IN, int* __restrict__ cnt) {
+__global__ void __launch_bounds__(256) fc_soft_bwd_keys_kernel(const int* __restrict__ cand, int R,
+                                                               int IN, int* __restrict__ keys) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= R) return;
-  const int i = min(max(cand[r], 0), IN - 1);
-  atomicAdd(&cnt[i], 1);
+  if (r < R) keys[r] = min(max(cand[r], 0), IN - 1);
 }
 
-// One workgroup: start[0..IN] = exclusive scan of cnt, cursor = start.
-__global__ void __launch_bounds__(1024) fc_soft_bwd_scan_kernel(const int* __restrict__ cnt, int IN,
-                                                                int* __restrict__ start,
-                                                                int* __restrict__ cursor) {
-  __shared__ int part[1024];
-  const int t = threadIdx.x;
-  const int per = (IN + 1023) / 1024;
-  const int lo = min(t * per, IN), hi = min(lo + per, IN);
-  int sum = 0;
-  for (int i = lo; i < hi; ++i) sum += cnt[i];
-  part[t] = sum;
-  __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = t >= d ? part[t - d] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  int run = part[t] - sum;
-  for (int i = lo; i < hi; ++i) {
-    start[i] = run;
-    cursor[i] = run;
-    run += cnt[i];
-  }
-  if (t == 1023) start[IN] = part[1023];
-}
-
-__global__ void __launch_bounds__(256) fc_soft_bwd_fill_kernel(const int* __restrict__ cand, int R,
-                                                               int IN, int* __restrict__ cursor,
-                                                               int* __restrict__ refs) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= R) return;
-  const int i = min(max(cand[r], 0), IN - 1);
-  refs[atomicAdd(&cursor[i], 1)] = r;
-}
-
-__device__ inline void sift_down(int* a, int root, int n) {
-  const int v = a[root];
-  for (;;) {
-    int c = 2 * root + 1;
-    if (c >= n) break;
-    if (c + 1 < n && a[c + 1] > a[c]) ++c;
-    if (a[c] <= v) break;
-    a[root] = a[c];
-    root = c;
-  }
-  a[root] = v;
-}
-
-// One wave per input: order its bucket ascending and write (row, weight).
-// Buckets of up to kRankCap references are copied to LDS and each element
-// is placed at its rank (the count of smaller references: all distinct), so
-// the wave's reads are independent broadcasts; larger buckets are
-// heap-sorted in place by one lane.
-constexpr int kRankCap = 512;
-
-__global__ void __launch_bounds__(256) fc_soft_bwd_sort_kernel(const int* __restrict__ start, int IN,
-                                                               int OUT, int K,
-                                                               const float* __restrict__ w,
-                                                               int* __restrict__ refs,
-                                                               int2* __restrict__ ent) {
-  __shared__ int buf[4][kRankCap];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i = blockIdx.x * 4 + wave;
-  const int s = i < IN ? start[i] : 0;
-  const int n = i < IN ? start[i + 1] - s : 0;
-  int* a = refs + s;
-  int* bw = buf[wave];
-  const bool small = n <= kRankCap;
-  if (small) {
-    for (int j = lane; j < n; j += 64) bw[j] = a[j];
-  } else if (lane == 0) {
-    for (int r = n / 2 - 1; r >= 0; --r) sift_down(a, r, n);
-    for (int e = n - 1; e > 0; --e) {
-      const int t = a[0];
-      a[0] = a[e];
-      a[e] = t;
-      sift_down(a, 0, e);
-    }
-  }
-  __syncthreads();  // LDS copies and the in-place sorts are visible to the workgroup
-  const int K2 = 2 * K;
-  for (int j = lane; j < n; j += 64) {
-    int r, pos;
-    if (small) {
-      r = bw[j];
-      pos = 0;
-      for (int t = 0; t < n; ++t) pos += bw[t] < r;
-    } else {
-      r = a[j];
-      pos = j;
-    }
-    const int o = r / K2, side = (r - o * K2) / K;
-    ent[s + pos] = make_int2(side * OUT + o, __float_as_int(w[r]));
-  }
+__global__ void __launch_bounds__(256) fc_soft_bwd_entries_kernel(const int* __restrict__ sorted,
+                                                                  int R, int OUT, int K,
+                                                                  const float* __restrict__ w,
+                                                                  int2* __restrict__ ent) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= R) return;
+  const int r = sorted[j], K2 = 2 * K;
+  const int o = r / K2, side = (r - o * K2) / K;
+  ent[j] = make_int2(side * OUT + o, __float_as_int(w[r]));
 }
 
 // gab [R2][LB] = transpose of gbr [B][R2] (rows b >= B of gab's columns are
@@ -462,17 +368,15 @@ constexpr int kGatherInputs = 4 * kGatherIW;
 
 inline int64_t round4(int64_t n) { return (n + 3) & ~int64_t(3); }
 
-// Workspace (in 4-byte words): records | partials | gbr | gab | start | cursor | refs | ent.
+// Workspace (in 4-byte words): records | partials | gbr | gab | keys | table | ent.
 struct BwdPlan {
   int Sw;              // samples per LDS tile of the weight kernel (0 = unsupported)
   int n_orange, NR, tiles_per_range;
   int64_t LB;          // gab row stride (samples, padded to the gather tile)
   int64_t R;           // references = 2 * OUT * K
-  int64_t rec_floats, part_floats, gbr_floats, gab_floats, start_ints, cursor_ints, refs_ints,
-      ent_ints;
+  int64_t rec_floats, part_floats, gbr_floats, gab_floats, keys_ints, table_ints, ent_ints;
   int64_t total() const {
-    return rec_floats + part_floats + gbr_floats + gab_floats + start_ints + cursor_ints +
-           refs_ints + ent_ints;
+    return rec_floats + part_floats + gbr_floats + gab_floats + keys_ints + table_ints + ent_ints;
   }
 };
 
@@ -498,9 +402,8 @@ static BwdPlan bwd_plan(int64_t B, int64_t IN, int64_t OUT, int K) {
   p.part_floats = round4((int64_t)p.NR * (2 * K + 4) * OUT);
   p.gbr_floats = 2 * OUT * p.LB;  // rows b < n_tiles * Sw <= LB
   p.gab_floats = 2 * OUT * p.LB;
-  p.start_ints = round4(IN + 1);
-  p.cursor_ints = round4(IN);
-  p.refs_ints = round4(p.R);
+  p.keys_ints = round4(p.R);
+  p.table_ints = ref_table_ints(p.R, IN);
   p.ent_ints = 2 * p.R;
   return p;
 }
@@ -547,25 +450,6 @@ static int bwd_node(const float* x, int64_t B, int64_t IN, int64_t OUT, int K, c
   return bwd_node_k<NODE, 0>(x, B, IN, OUT, K, pv, inv_tau, gy, part, gbr, p, st);
 }
 
-// The transposed reference table of cand into start / refs / ent.
-static int build_ref_table(const int32_t* cand, const float* w, int64_t IN, int64_t OUT, int K,
-                           const BwdPlan& p, int* start, int* cursor, int* refs, int2* ent,
-                           hipStream_t st) {
-  const int R = (int)p.R;
-  hipLaunchKernelGGL(fc_soft_bwd_zero_kernel, dim3((unsigned)cdiv(IN, 256)), dim3(256), 0, st,
-                     cursor, (int)IN);
-  hipLaunchKernelGGL(fc_soft_bwd_count_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
-                     cand, R, (int)IN, cursor);
-  hipLaunchKernelGGL(fc_soft_bwd_scan_kernel, dim3(1), dim3(1024), 0, st, cursor, (int)IN, start,
-                     cursor);
-  hipLaunchKernelGGL(fc_soft_bwd_fill_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
-                     cand, R, (int)IN, cursor, refs);
-  hipLaunchKernelGGL(fc_soft_bwd_sort_kernel, dim3((unsigned)cdiv(IN, 4)), dim3(256), 0, st,
-                     start, (int)IN, (int)OUT, K, w, refs, ent);
-  SLG_LAUNCH_CHECK("fc_soft_bwd table");
-  return 0;
-}
-
 }  // namespace slg
 
 using namespace slg;
@@ -603,10 +487,9 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
   float* part = rec + p.rec_floats;
   float* gbr = part + p.part_floats;
   float* gab = gbr + p.gbr_floats;
-  int* start = reinterpret_cast<int*>(gab + p.gab_floats);
-  int* cursor = start + p.start_ints;
-  int* refs = cursor + p.cursor_ints;
-  int2* ent = reinterpret_cast<int2*>(refs + p.refs_ints);  // 8-byte aligned: offsets are even
+  int* keys = reinterpret_cast<int*>(gab + p.gab_floats);
+  int* table = keys + p.keys_ints;
+  int2* ent = reinterpret_cast<int2*>(table + p.table_ints);  // 8-byte aligned: offsets are even
   hipLaunchKernelGGL(fc_soft_pack_records_kernel, dim3((unsigned)cdiv(p.rec_floats, 256)),
                      dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN, rec);
   SLG_LAUNCH_CHECK("fc_soft_pack_records");
@@ -630,8 +513,15 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
     if (rc) return rc;
   }
   if (want_x) {
-    int rc = build_ref_table(cand, w, IN, OUT, K, p, start, cursor, refs, ent, st);
+    const int R = (int)p.R;
+    hipLaunchKernelGGL(fc_soft_bwd_keys_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                       cand, R, (int)IN, keys);
+    RefTable tb{};
+    int rc = build_ref_table(keys, R, IN, table, st, &tb);
     if (rc) return rc;
+    hipLaunchKernelGGL(fc_soft_bwd_entries_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                       tb.sorted, R, (int)OUT, K, w, ent);
+    SLG_LAUNCH_CHECK("fc_soft_bwd entries");
     const int R2 = (int)(2 * OUT);
     const int n_rtiles = (int)cdiv(R2, 64);
     const int64_t n_tr = n_rtiles * (p.LB / 64);
@@ -645,7 +535,7 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
     const int64_t grid = cdiv(n_blocks, 8) * 8;  // a multiple of 8 for the XCD remap
     auto gather = fc_soft_bwd_gather_kernel<kGatherV, kGatherIW>;
     hipLaunchKernelGGL(gather, dim3((unsigned)grid), dim3(256), 0, st,
-                       gab, p.LB, (int)B, (int)IN, start, ent, n_itiles, (int)n_blocks, gx);
+                       gab, p.LB, (int)B, (int)IN, tb.start, ent, n_itiles, (int)n_blocks, gx);
     SLG_LAUNCH_CHECK("fc_soft_bwd_gather");
   }
   if (want_w) {

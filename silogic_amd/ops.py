@@ -599,6 +599,31 @@ def conv_soft_torch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, poo
     return F.max_pool2d(out, 2, 2) if pool else out
 
 
+def conv_soft_bwd(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool, gy,
+                  need_x=True, need_np=True, need_w=True):
+    """HIP backward of the conv soft op: ``(gx, gnp, gw)`` (None where not
+    needed), or None when the kernel does not take the shape."""
+    require_gpu(x, npar, w, cm, gy)
+    x = _as_f32(x.detach())
+    npar, w = _c(npar.detach(), torch.float32), _c(w.detach(), torch.float32)
+    cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
+    B, Cc, H, W = x.shape
+    N = cm.shape[0]
+    ws = _lib.lib().slg_conv_soft_bwd_workspace(B, Cc, H, W, N, node_kind, depth, arity, K, pad,
+                                                int(bool(pool)))
+    if ws < 0:
+        return None
+    gy = _c(gy, torch.float32)
+    gx = torch.empty_like(x) if need_x else None
+    gn = torch.empty_like(npar) if need_np else None
+    gw = torch.empty_like(w) if need_w else None
+    work = torch.empty(max(ws, 1), device=x.device, dtype=torch.float32)
+    _lib.call("slg_conv_soft_bwd", _p(x), B, Cc, H, W, N, node_kind, depth, arity, K, _p(npar),
+              _p(w), _p(cm), _p(ch), _p(cw), pad, int(bool(pool)), _p(gy), _p(gx), _p(gw),
+              _p(gn), _p(work), ws, _stream(x))
+    return gx, gn, gw
+
+
 class ConvSoftFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
@@ -613,6 +638,10 @@ class ConvSoftFn(torch.autograd.Function):
         x, npar, w, cm, ch, cw = ctx.saved_tensors
         meta = ctx.meta
         need = ctx.needs_input_grad
+        got = conv_soft_bwd(x, npar, w, cm, ch, cw, *meta, gy, need[0], need[1], need[2])
+        if got is not None:
+            return got + (None,) * 9
+        # shapes the HIP backward does not take: the composite torch backward
         with torch.enable_grad():
             xs = x.detach().requires_grad_(need[0])
             ns = npar.detach().requires_grad_(need[1])

@@ -598,6 +598,67 @@ def test_fc_soft_backward_kernels(node, conn, k, IN, OUT, B):
                               layer._inv_tau(), gy.to(DEV)) is not None   # the HIP kernels ran
 
 
+@pytest.mark.parametrize("node,depth,arity,connect,k,C,H,N,B,pool,binary", [
+    ("gate16", 2, 2, "topk", 4, 7, 12, 24, 5, True, True),      # exact pooling ties
+    ("gate16", 2, 2, "topk", 4, 7, 12, 24, 5, False, False),
+    ("gate16", 2, 2, "topk", 4, 3, 28, 40, 4, True, True),      # 3 tree groups, last partial
+    ("gate16", 3, 2, "topk", 8, 4, 9, 12, 3, True, False),      # odd map: floor pooling
+    ("gate16", 1, 2, "fixed", 1, 5, 8, 16, 6, True, True),
+    ("multilinear", 1, 6, "topk", 4, 9, 10, 16, 3, True, False),
+    ("multilinear", 1, 3, "fixed", 1, 4, 7, 10, 4, False, True),
+    ("multilinear", 1, 6, "topk", 4, 9, 32, 20, 2, True, True),  # the 32x32 LUT block
+    ("gate16", 2, 2, "topk", 4, 2, 6, 8, 600, True, True),      # several samples per range
+])
+def test_conv_soft_backward_kernel(node, depth, arity, connect, k, C, H, N, B, pool, binary):
+    """The HIP conv backward (fused pooling or not) against fp32 autograd
+    through the oracle's ConvLogicTree (+ F.max_pool2d) on the CPU: input,
+    connection and node-logit gradients."""
+    layer = sl.ConvLogicTree(C, N, kernel=3, tree_depth=depth, connect=connect, k=k, seed=3,
+                             node=node, arity=arity)
+    blk = dict(prefix="", cin=C, n=N, kernel=3, depth=depth, stride=1, padding=1,
+               connect=connect, k=layer.k if connect != "fixed" else 1, node=node,
+               node_arity=2 if node == "gate16" else arity,
+               leaves=(2 if node == "gate16" else arity) ** depth, tau=1.0, hw=H)
+    params = {kk: v.clone().requires_grad_(v.is_floating_point())
+              for kk, v in layer.state_dict().items()}
+    gen = torch.Generator().manual_seed(11)
+    x = torch.rand(B, C, H, H, generator=gen)
+    if binary:
+        x = (x > 0.5).float()
+    xr = x.clone().requires_grad_(True)
+    ref = torch_ref.conv_soft(blk, params, xr)
+    if pool:
+        ref = torch_ref.orpool_soft(ref)
+    gy = torch.randn(ref.shape, generator=gen)
+    (ref * gy).sum().backward()
+    layer = layer.to(DEV).train()
+    xg = x.to(DEV).requires_grad_(True)
+    out = layer.forward_pooled(xg) if pool else layer(xg)
+    (out * gy.to(DEV)).sum().backward()
+
+    def close(got, ref_, what):
+        got = got.cpu()
+        scale = ref_.abs().max().item()
+        err = (got - ref_).abs().max().item()
+        assert err <= 1e-4 * scale + 1e-6, f"{what}: max err {err:.3e} (scale {scale:.3e})"
+
+    close(xg.grad, xr.grad, "dL/dx")
+    for name, prm in layer.named_parameters():
+        close(prm.grad, params[name].grad, name)
+    # the HIP kernel takes this shape (the gradients above came from it)
+    cm, ch, cw = layer._taps()
+    w, npar = layer.soft_params(True)
+    got = ops.conv_soft_bwd(xg.detach(), npar, w, cm, ch, cw, layer._kind(), layer.d,
+                            layer.node_arity, cm.shape[-1], layer.padding, pool, gy.to(DEV))
+    assert got is not None
+    # only the parameter gradients (gx not wanted): same values
+    got2 = ops.conv_soft_bwd(xg.detach(), npar, w, cm, ch, cw, layer._kind(), layer.d,
+                             layer.node_arity, cm.shape[-1], layer.padding, pool, gy.to(DEV),
+                             need_x=False)
+    assert got2[0] is None
+    assert torch.equal(got2[1], got[1]) and torch.equal(got2[2], got[2])
+
+
 def test_fc_soft_backward_skewed_references_and_determinism():
     """Input gradient when references pile onto a few inputs (half of all
     candidates name input 3, some twice on one side): against fp32 autograd
