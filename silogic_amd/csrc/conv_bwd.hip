@@ -22,7 +22,7 @@
 //      to per-thread sums;
 //   B. gathers the input gradient of every pixel from its channel's taps in
 //      the group (a table of (tree, leaf, dh, dw, weight) per (group,
-//      channel), built once per call and staged in LDS); for LUT trees, adds
+//      channel), built once per call); for LUT trees, adds
 //      each corner's gradient over the sample's outputs (from the leaf
 //      values and upstream gradients kept in LDS) to per-thread sums.
 // At the end of its range the workgroup reduces the per-thread sums over
@@ -42,11 +42,11 @@ constexpr int kBwdMaxK = 8;
 constexpr int kBwdThreads = 1024;  // largest workgroup (LDS reduction buffer size)
 constexpr int kBwdNodeAcc = 16;    // node-parameter sums per thread
 
-// Workgroup size cap of a variant: the large trees (LUT arity >= 5, gate16
-// depth 3) need more than the 128 VGPRs of 1024-thread workgroups.
+// Workgroup size cap of a variant: LUT trees (their corner sums) and gate16
+// trees of depth 3 need more than the 128 VGPRs of 1024-thread workgroups.
 template <int NODE, int NLEAF>
 __host__ __device__ constexpr int conv_bwd_threads() {
-  return (NODE == SLG_NODE_GATE16 ? NLEAF >= 8 : NLEAF >= 5) ? 512 : 1024;
+  return (NODE == SLG_NODE_GATE16 ? NLEAF >= 8 : true) ? 512 : 1024;
 }
 
 // Per-thread node-parameter sums: gate16 trees sum every node's four
@@ -60,16 +60,17 @@ struct ConvBwdArgs {
   int C, H, W, pad, kernel;
   int Ho, Wo, P;  // routed map (pooled or the full map) and its size
   int N, K, TG, TPT, NG, SPR, B;
+  int J2;  // LUT trees: position slots per (tree, low-corner) item
+  int KB;  // table buckets per (group, channel): kernel^2 (by tap offset) or 1
 };
 
 // LDS layout of one workgroup (offsets in floats).
 struct ConvBwdLds {
-  int xs, tab_start, tab_ent, taps, par, raw, vq, gv, gq, route, red, total;
+  int xs, taps, par, raw, vq, gv, gq, route, red, total;
 };
 
-// XS: the image is staged (C*H*W floats). The table part holds the group's
-// C + 1 bucket starts and its TG * NLEAF * K entries. vq / gq (leaf values
-// and upstream gradients at the routed positions) exist for LUT trees only.
+// XS: the image is staged (C*H*W floats). vq / gq (leaf values and upstream
+// gradients at the routed positions) exist for LUT trees only.
 template <int NODE, int NLEAF, bool POOL>
 __host__ __device__ inline ConvBwdLds conv_bwd_lds(bool XS, int C, int CHW, int TG, int K, int P) {
   using Nd = ConvNode<NODE, NLEAF>;
@@ -77,8 +78,6 @@ __host__ __device__ inline ConvBwdLds conv_bwd_lds(bool XS, int C, int CHW, int 
   ConvBwdLds L{};
   int o = 0;
   L.xs = o; o += XS ? (CHW + 3) & ~3 : 0;
-  L.tab_start = o; o += (C + 1 + 3) & ~3;
-  L.tab_ent = o; o += TG * NLEAF * K * 4;  // int4 per entry
   L.taps = o; o += TG * NLEAF * K * 4;     // int4 per tap
   L.par = o; o += (TG * Nd::NPR + 3) & ~3;
   L.raw = o; o += LUT ? ((TG * NLEAF * (Nd::NP / 2) + 3) & ~3) : 0;
@@ -209,8 +208,6 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
   const int HW = a.H * a.W, CHW = a.C * HW;
   const ConvBwdLds L = conv_bwd_lds<NODE, NLEAF, POOL>(XS, a.C, CHW, a.TG, a.K, a.P);
   float* xs = lds + L.xs;
-  int* tab_start = reinterpret_cast<int*>(lds + L.tab_start);
-  int4* tab_ent = reinterpret_cast<int4*>(lds + L.tab_ent);
   int4* taps = reinterpret_cast<int4*>(lds + L.taps);
   float* par = lds + L.par;
   float* raw = lds + L.raw;
@@ -226,10 +223,6 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
   const int TG = a.TG, K = a.K, P = a.P;
   const int tid = threadIdx.x, T = blockDim.x;
 
-  // the group's table (bucket starts relative to the group's first entry)
-  const int e0 = tstart[g * a.C];
-  for (int i = tid; i <= a.C; i += T) tab_start[i] = tstart[g * a.C + i] - e0;
-  for (int i = tid; i < tstart[g * a.C + a.C] - e0; i += T) tab_ent[i] = tent[e0 + i];
   // taps and parameters of the group's trees (trees past N: zero weight)
   for (int i = tid; i < TG * NLEAF * K; i += T) {
     const int t = i / (NLEAF * K), lk = i - t * NLEAF * K;
@@ -373,53 +366,113 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
     __syncthreads();
 
     // ---- B1: input gradient of every pixel from the group's taps ----
-    for (int e = tid; gx_out != nullptr && e < CHW; e += T) {
-      const int c = e / HW, hw = e - c * HW;
-      const int h = hw / a.W, w = hw - h * a.W;
-      const int j1 = tab_start[c + 1];
-      float acc = 0.0f;
-#pragma unroll 4
-      for (int j = tab_start[c]; j < j1; ++j) {
-        const int4 en = tab_ent[j];  // (t * NLEAF + l, dh, dw, weight)
-        const int y = h - en.y, xx = w - en.z;  // the tap's output position
-        float gval = 0.0f;
-        if constexpr (POOL) {
-          const int py = y >> 1, px = xx >> 1;
-          if (y >= 0 && xx >= 0 && py < a.Ho && px < a.Wo) {
-            const int pp = py * a.Wo + px;
-            const int t = en.x / NLEAF;
-            if (route[t * P + pp] == (unsigned char)(((y & 1) << 1) | (xx & 1)))
-              gval = gv[en.x * P + pp];
-          }
-        } else {
-          if ((unsigned)y < (unsigned)a.Ho && (unsigned)xx < (unsigned)a.Wo)
-            gval = gv[en.x * P + y * a.Wo + xx];
+    // A wave takes 64 * ppl pixels of one channel (ppl = 1..PPL per lane) and
+    // walks the channel's taps, bucketed by offset (dh, dw) where channels
+    // hold enough taps: the output position, bounds and window slot are then
+    // computed once per offset, and each tap costs two independent LDS reads
+    // (route, leaf gradient) and an FMA. Taps are wave-uniform (scalar loads
+    // from the table).
+    if (gx_out != nullptr) {
+      const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+      const int lane = tid & 63;
+      constexpr int PPL = (LUT && NLEAF >= 5) ? 2 : 4;  // register budget of the big LUTs
+      const int ppl = min(PPL, (HW + 63) >> 6);
+      const int span = 64 * ppl;
+      const int n_chunks = (HW + span - 1) / span;
+      for (int ci = wave; ci < a.C * n_chunks; ci += (T >> 6)) {
+        const int c = ci / n_chunks, chunk = ci - c * n_chunks;
+        int hh[PPL], ww[PPL];
+#pragma unroll
+        for (int u = 0; u < PPL; ++u) {
+          const int hw = chunk * span + u * 64 + lane;
+          hh[u] = hw / a.W;
+          ww[u] = hw - hh[u] * a.W;
         }
-        acc = fmaf(__int_as_float(en.w), gval, acc);
+        float acc[PPL];
+#pragma unroll
+        for (int u = 0; u < PPL; ++u) acc[u] = 0.0f;
+        const int kbase = (g * a.C + c) * a.KB;
+        // KB == KK: one bucket per offset; KB == 1: the channel's taps in one
+        // bucket, each with its own offset (for sparse channels)
+        for (int kk = 0; kk < a.KB; ++kk) {
+          const int j0 = tstart[kbase + kk], j1 = tstart[kbase + kk + 1];
+          if (j0 == j1) continue;  // uniform
+          int pp[PPL], qq[PPL];
+          bool inb[PPL];
+          auto place = [&](int dh, int dw) {
+#pragma unroll
+            for (int u = 0; u < PPL; ++u) {
+              const int y = hh[u] - dh, xx = ww[u] - dw;  // the taps' output position
+              if constexpr (POOL) {
+                const int py = y >> 1, px = xx >> 1;
+                inb[u] = u < ppl && y >= 0 && xx >= 0 && py < a.Ho && px < a.Wo;
+                pp[u] = inb[u] ? py * a.Wo + px : 0;
+                qq[u] = ((y & 1) << 1) | (xx & 1);
+              } else {
+                inb[u] = u < ppl && (unsigned)y < (unsigned)a.Ho && (unsigned)xx < (unsigned)a.Wo;
+                pp[u] = inb[u] ? y * a.Wo + xx : 0;
+                qq[u] = 0;
+              }
+            }
+          };
+          if (a.KB > 1) place(kk / a.kernel - a.pad, kk - (kk / a.kernel) * a.kernel - a.pad);
+          for (int j = j0; j < j1; ++j) {
+            const int4 en = tent[j];  // (leaf-gradient row base, route row base, offset, weight)
+            if (a.KB == 1) place((en.z >> 8) - a.pad, (en.z & 255) - a.pad);
+#pragma unroll
+            for (int u = 0; u < PPL; ++u) {
+              const float gg = gv[en.x + pp[u]];
+              bool ok = inb[u];
+              if constexpr (POOL) ok = ok && route[en.y + pp[u]] == (unsigned char)qq[u];
+              acc[u] = fmaf(__int_as_float(en.w), ok ? gg : 0.0f, acc[u]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < PPL; ++u) {
+          const int hw = chunk * span + u * 64 + lane;
+          if (u < ppl && hw < HW) gx_out[((int64_t)g * a.B + b) * CHW + c * HW + hw] = acc[u];
+        }
       }
-      gx_out[((int64_t)g * a.B + b) * CHW + e] = acc;
     }
 
     // ---- B2 (LUT trees): corner gradients over the sample's outputs ----
+    // corner = c1 + (c2 << H1): its weight is A(c1) * B(c2) with A the
+    // product over the low H1 leaves (times the upstream gradient) and B
+    // over the others. Item (tree, c1, position slot j) reads the leaf
+    // values of positions p = j (mod J2) once and adds to all NC2 sums.
     if constexpr (LUT) {
-      int slot = 0;
-      for (int it = tid; it < TG * NP; it += T, ++slot) {
-        const int t = it / NP, item = it - t * NP;
-        if (n0 + t >= a.N) continue;
-        float sum = 0.0f;
-        for (int p = 0; p < P; ++p) {
-          // corner weight of corner `item`: prod over leaves of v or 1 - v
-          float wgt = gq[t * P + p];
+      constexpr int H1 = NLEAF / 2, NC1 = 1 << H1, NC2 = 1 << (NLEAF - H1);
+      const int J2 = a.J2, items = TG * NC1 * J2;
 #pragma unroll
-          for (int l = 0; l < NLEAF; ++l) {
-            const float lv = vq[(t * NLEAF + l) * P + p];
-            wgt *= ((item >> l) & 1) ? lv : 1.0f - lv;
+      for (int s2 = 0; s2 < NACC / NC2; ++s2) {
+        const int it = tid + s2 * T;
+        if (it < items) {
+          const int t = it / (NC1 * J2), c1 = (it / J2) % NC1, j = it % J2;
+          if (n0 + t < a.N) {
+            for (int p = j; p < P; p += J2) {
+              float lv[NLEAF];
+#pragma unroll
+              for (int l = 0; l < NLEAF; ++l) lv[l] = vq[(t * NLEAF + l) * P + p];
+              float A = gq[t * P + p];
+#pragma unroll
+              for (int l = 0; l < H1; ++l) A *= ((c1 >> l) & 1) ? lv[l] : 1.0f - lv[l];
+              float bw[NC2];
+              bw[0] = A;
+#pragma unroll
+              for (int l = H1; l < NLEAF; ++l) {
+                const int sz = 1 << (l - H1);
+#pragma unroll
+                for (int i = 0; i < sz; ++i) {
+                  bw[i + sz] = bw[i] * lv[l];
+                  bw[i] = bw[i] * (1.0f - lv[l]);
+                }
+              }
+#pragma unroll
+              for (int c2 = 0; c2 < NC2; ++c2) accn[s2 * NC2 + c2] += bw[c2];
+            }
           }
-          sum += wgt;
         }
-#pragma unroll
-        for (int s2 = 0; s2 < NACC; ++s2)
-          if (s2 == slot) accn[s2] += sum;
       }
     }
   }
@@ -446,13 +499,27 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
 #pragma unroll
     for (int i = 0; i < NACC; ++i) reduce_tree(accn[i], pn, NP, i);
   } else {
-    int slot = 0;
-    for (int it = tid; it < TG * NP; it += T, ++slot) {
-      const int t = it / NP, item = it - t * NP;
-      if (n0 + t >= a.N) continue;
+    // corner sums reduced over the J2 position slots of each (tree, c1)
+    constexpr int H1 = NLEAF / 2, NC1 = 1 << H1, NC2 = 1 << (NLEAF - H1);
+    const int J2 = a.J2, items = TG * NC1 * J2;
 #pragma unroll
-      for (int s2 = 0; s2 < NACC; ++s2)
-        if (s2 == slot) pn[(int64_t)(n0 + t) * NP + item] = accn[s2];
+    for (int s2 = 0; s2 < NACC / NC2; ++s2) {
+      if (s2 * T >= items) break;  // uniform
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        __syncthreads();
+        red[tid] = accn[s2 * NC2 + c2];
+        __syncthreads();
+        const int grp = tid, first = s2 * T + grp * J2;  // item group (t, c1)
+        if (grp * J2 < T && first < items) {
+          const int t = first / (NC1 * J2), c1 = (first / J2) % NC1;
+          if (n0 + t < a.N) {
+            float sum = 0.0f;
+            for (int j = 0; j < J2; ++j) sum += red[grp * J2 + j];
+            pn[(int64_t)(n0 + t) * NP + c1 + (c2 << H1)] = sum;
+          }
+        }
+      }
     }
   }
 }
@@ -479,20 +546,26 @@ __global__ void __launch_bounds__(256) conv_bwd_sum_ranges_kernel(const float* _
   out[i] = s;
 }
 
-// Table keys: tap (n, l, k) -> group * C + channel.
-__global__ void __launch_bounds__(256) conv_bwd_keys_kernel(const int* __restrict__ cm, int R,
-                                                            int LK, int TG, int C,
-                                                            int* __restrict__ keys) {
+// Table keys: tap (n, l, k) -> (group * C + channel) * KB + offset (KB =
+// kernel^2, offset = ch * kernel + cw), or group * C + channel (KB = 1).
+__global__ void __launch_bounds__(256) conv_bwd_keys_kernel(const int* __restrict__ cm,
+                                                            const int* __restrict__ ch,
+                                                            const int* __restrict__ cw, int R,
+                                                            int LK, int TG, int C, int kernel,
+                                                            int KB, int* __restrict__ keys) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= R) return;
   const int n = r / LK;
-  keys[r] = (n / TG) * C + min(max(cm[r], 0), C - 1);
+  const int c = min(max(cm[r], 0), C - 1);
+  const int off = min(max(ch[r], 0), kernel - 1) * kernel + min(max(cw[r], 0), kernel - 1);
+  keys[r] = KB == 1 ? (n / TG) * C + c : ((n / TG) * C + c) * KB + off;
 }
 
-// Table entries: sorted tap r -> (tree in group * NLEAF + leaf, dh, dw, weight).
+// Table entries: sorted tap r -> (leaf-gradient row base (t * NLEAF + l) * P,
+// route row base t * P, (ch << 8) | cw, weight), t = tree within its group.
 __global__ void __launch_bounds__(256) conv_bwd_entries_kernel(const int* __restrict__ sorted,
                                                                int R, int NLEAF, int K, int TG,
-                                                               int kernel, int pad,
+                                                               int P, int kernel,
                                                                const int* __restrict__ ch,
                                                                const int* __restrict__ cw,
                                                                const float* __restrict__ wts,
@@ -501,9 +574,9 @@ __global__ void __launch_bounds__(256) conv_bwd_entries_kernel(const int* __rest
   if (j >= R) return;
   const int r = sorted[j];
   const int n = r / (NLEAF * K), l = (r / K) % NLEAF;
-  const int dh = min(max(ch[r], 0), kernel - 1) - pad;
-  const int dw = min(max(cw[r], 0), kernel - 1) - pad;
-  ent[j] = make_int4((n % TG) * NLEAF + l, dh, dw, __float_as_int(wts ? wts[r] : 1.0f));
+  const int t = n % TG;
+  const int off = (min(max(ch[r], 0), kernel - 1) << 8) | min(max(cw[r], 0), kernel - 1);
+  ent[j] = make_int4((t * NLEAF + l) * P, t * P, off, __float_as_int(wts ? wts[r] : 1.0f));
 }
 
 // ---------------------------------------------------------------------------
@@ -511,7 +584,7 @@ __global__ void __launch_bounds__(256) conv_bwd_entries_kernel(const int* __rest
 // ---------------------------------------------------------------------------
 struct ConvBwdPlan {
   bool XS;  // image staged in LDS
-  int TG, TPT, threads, NG, NR, SPR;
+  int TG, TPT, threads, NG, NR, SPR, J2, KB;
   size_t lds;
   int64_t R;  // taps N * NLEAF * K
   // workspace (4-byte words): keys | table | entries (int4) | part_x | part_w | part_np
@@ -529,7 +602,7 @@ static int next_pow2(int v) {
 
 template <int NODE, int NLEAF, bool POOL>
 static bool conv_bwd_plan_t(int64_t B, int64_t C, int64_t H, int64_t W, int64_t N, int K,
-                            int64_t Ho, int64_t Wo, ConvBwdPlan& p) {
+                            int pad, int64_t Ho, int64_t Wo, ConvBwdPlan& p) {
   using Nd = ConvNode<NODE, NLEAF>;
   const int64_t CHW = C * H * W, P = Ho * Wo;
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
@@ -543,11 +616,12 @@ static bool conv_bwd_plan_t(int64_t B, int64_t C, int64_t H, int64_t W, int64_t 
          TG >>= 1) {
       const ConvBwdLds L = conv_bwd_lds<NODE, NLEAF, POOL>(xs, (int)C, (int)CHW, TG, K, (int)P);
       const int TPT = std::min(TMAX / TG, next_pow2((int)P));
-      const int th = std::max(64, TG * TPT);
-      const int slots = LUT ? (TG * Nd::NP + th - 1) / th : 0;  // corners per thread
-      if ((int64_t)L.total * 4 <= cap && slots <= kBwdNodeAcc) {
+      const int th = (std::max(64, TG * TPT) + 63) & ~63;
+      constexpr int H1 = NLEAF / 2, NC1 = 1 << H1, NC2 = 1 << (NLEAF - H1);
+      const int slots = LUT ? (TG * NC1 + th - 1) / th : 0;  // (tree, c1) items per thread
+      if ((int64_t)L.total * 4 <= cap && slots * NC2 <= kBwdNodeAcc) {
         tpt = TPT;
-        threads = (th + 63) & ~63;
+        threads = th;
         lds = (size_t)L.total * 4;
         return TG;
       }
@@ -568,6 +642,11 @@ static bool conv_bwd_plan_t(int64_t B, int64_t C, int64_t H, int64_t W, int64_t 
   p.threads = xs ? th_s : th_g;
   p.lds = xs ? lds_s : lds_g;
   p.NG = (int)cdiv(N, p.TG);
+  p.J2 = 1;
+  if (LUT) {  // position slots: fill the workgroup with (tree, c1, slot) items
+    constexpr int NC1 = 1 << (NLEAF / 2);
+    while (2 * p.J2 <= (int)P && (int64_t)p.TG * NC1 * 2 * p.J2 <= p.threads) p.J2 *= 2;
+  }
   const int64_t per_cu = std::max<int64_t>(
       1, std::min<int64_t>(2048 / p.threads, (int64_t)(160 * 1024) / (int64_t)p.lds));
   const int64_t slots = per_cu * device_cus();
@@ -575,7 +654,10 @@ static bool conv_bwd_plan_t(int64_t B, int64_t C, int64_t H, int64_t W, int64_t 
   p.SPR = (int)cdiv(B, NR);
   p.NR = (int)cdiv(B, p.SPR);
   p.R = N * NLEAF * (int64_t)K;
-  const int64_t nkeys = (int64_t)p.NG * C;
+  // bucket the taps by offset where a channel holds at least two per offset
+  const int64_t kern = 2 * (int64_t)pad + 1;
+  p.KB = (int64_t)p.TG * NLEAF * K >= 2 * kern * kern * C ? (int)(kern * kern) : 1;
+  const int64_t nkeys = (int64_t)p.NG * C * p.KB;
   p.keys_ints = (p.R + 3) & ~3LL;
   p.table_ints = ref_table_ints(p.R, nkeys);
   p.ent_ints = 4 * p.R;
@@ -634,7 +716,7 @@ int64_t slg_conv_soft_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, 
   bool ok = false;
   conv_bwd_dispatch(node_kind, nleaf, pool != 0, [&](auto nd, auto nl, auto pl) {
     ok = conv_bwd_plan_t<decltype(nd)::value, decltype(nl)::value, decltype(pl)::value>(
-        std::max<int64_t>(B, 1), C, H, W, N, K, Ho, Wo, p);
+        std::max<int64_t>(B, 1), C, H, W, N, K, pad, Ho, Wo, p);
     return 0;
   });
   return ok ? p.total() : -1;
@@ -681,7 +763,7 @@ int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
     constexpr bool POOL = decltype(pl)::value;
     using Nd = ConvNode<NODE, NL>;
     ConvBwdPlan p{};
-    SLG_REQUIRE((conv_bwd_plan_t<NODE, NL, POOL>(B, C, H, W, N, K, Ho, Wo, p)),
+    SLG_REQUIRE((conv_bwd_plan_t<NODE, NL, POOL>(B, C, H, W, N, K, pad, Ho, Wo, p)),
                 SLG_E_UNSUPPORTED, "conv_soft_bwd: image of %lld floats does not fit LDS",
                 (long long)CHW);
     SLG_REQUIRE(workspace_floats >= p.total(), SLG_E_ARG,
@@ -695,18 +777,20 @@ int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
     float* partn = partw + p.partw_floats;
     const int R = (int)p.R;
     hipLaunchKernelGGL(conv_bwd_keys_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st, cm,
-                       R, NL * K, p.TG, (int)C, keys);
+                       ch, cw, R, NL * K, p.TG, (int)C, kernel, p.KB, keys);
     RefTable tb{};
-    int rc = build_ref_table(keys, R, (int64_t)p.NG * C, table, st, &tb);
+    int rc = build_ref_table(keys, R, (int64_t)p.NG * C * p.KB, table, st, &tb);
     if (rc) return rc;
     hipLaunchKernelGGL(conv_bwd_entries_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
-                       tb.sorted, R, NL, K, p.TG, kernel, (int)pad, ch, cw, w, ent);
+                       tb.sorted, R, NL, K, p.TG, (int)(Ho * Wo), kernel, ch, cw, w, ent);
     SLG_LAUNCH_CHECK("conv_soft_bwd entries");
 
     ConvBwdArgs a{};
     a.C = (int)C; a.H = (int)H; a.W = (int)W; a.pad = pad; a.kernel = kernel;
     a.Ho = (int)Ho; a.Wo = (int)Wo; a.P = (int)(Ho * Wo);
     a.N = (int)N; a.K = K; a.TG = p.TG; a.TPT = p.TPT; a.NG = p.NG; a.SPR = p.SPR; a.B = (int)B;
+    a.J2 = p.J2;
+    a.KB = p.KB;
     // gx written directly when one group holds every tree; none when not wanted
     float* gxo = gx == nullptr ? nullptr : (p.NG > 1 ? partx : gx);
     auto kern = (K <= 4) ? (p.XS ? conv_soft_bwd_kernel<NODE, NL, POOL, 4, true>
