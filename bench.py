@@ -139,6 +139,41 @@ def kernels_only(reps=3):
     log("kernels-only done")
 
 
+def train_step(cfg, steps, warmup):
+    """One training step of config ``cfg`` at its soft batch: soft forward,
+    cross-entropy on synthetic labels, backward through the HIP kernels
+    (FC and conv soft backward, GroupSum), Adam update. Prints one JSON line
+    (samples per second); not the headline metric."""
+    import silogic_amd as sl
+    from silogic_amd.synthetic import BATCHES, build_config, config_inputs
+    dev = torch.device("cuda:0")
+    B = BATCHES[cfg][0]
+    model = build_config(cfg, sl).train().to(dev)
+    x = config_inputs(cfg, B).to(dev)
+    labels = torch.randint(0, 10, (B,), generator=torch.Generator().manual_seed(2)).to(dev)
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = torch.nn.functional.cross_entropy(model(x), labels)
+        loss.backward()
+        opt.step()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    print(json.dumps({"metric": "train_samples_per_s", "value": B * 1e3 / ms,
+                      "unit": "samples/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+                      "ms_per_step": ms, "higher_is_better": True, "dtype": "fp32",
+                      "data": "synthetic", "config": {"workload": WORKLOADS[cfg],
+                                                      "global_batch": B}}), flush=True)
+
+
 WORKLOADS = {
     1: "cfg1: LogicNet(784, 2000, 4, gate16, TopK k=8, GroupSum 10, tau=10); forward_hard + "
        "soft forward, B=256 Bernoulli(0.5)",
@@ -309,9 +344,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the copy calibration and the dominant kernels (for --pmc)")
+    ap.add_argument("--train-step", action="store_true",
+                    help="time a training step (soft forward + backward + Adam) instead")
     args = ap.parse_args()
     if args.kernels_only:
         kernels_only()
+        return
+    if args.train_step:
+        train_step(args.config, args.steps, args.warmup)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

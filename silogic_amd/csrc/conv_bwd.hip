@@ -535,15 +535,25 @@ __global__ void __launch_bounds__(256) conv_bwd_sum_groups_kernel(const float* _
   gx[i] = s;
 }
 
-// out[i] = sum over ranges of part[r][i], ranges ascending.
+// out[i] = sum over ranges r of part[r][i]: a workgroup takes 16 columns;
+// its 16 thread rows sum the ranges r = row (mod 16) in ascending order, and
+// the 16 row sums are added in row order (a fixed order on every call).
 __global__ void __launch_bounds__(256) conv_bwd_sum_ranges_kernel(const float* __restrict__ part,
                                                                   int NR, int64_t n,
                                                                   float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+  __shared__ float rs[16][17];
+  const int col = threadIdx.x & 15, row = threadIdx.x >> 4;
+  const int64_t i = (int64_t)blockIdx.x * 16 + col;
   float s = 0.0f;
-  for (int r = 0; r < NR; ++r) s += part[(int64_t)r * n + i];
-  out[i] = s;
+  if (i < n)
+    for (int r = row; r < NR; r += 16) s += part[(int64_t)r * n + i];
+  rs[row][col] = s;
+  __syncthreads();
+  if (row == 0 && i < n) {
+    float t = 0.0f;
+    for (int q = 0; q < 16; ++q) t += rs[q][col];
+    out[i] = t;
+  }
 }
 
 // Table keys: tap (n, l, k) -> (group * C + channel) * KB + offset (KB =
@@ -749,10 +759,10 @@ int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
     const int64_t NP = node_kind == SLG_NODE_GATE16 ? 4 * (nleaf - 1) : (1 << nleaf);
     const int64_t nw = N * nleaf * K;
     if (gw)
-      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(nw, 256)), dim3(256), 0,
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(nw, 16)), dim3(256), 0,
                          st, workspace, 0, nw, gw);
     if (gnp)
-      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(N * NP, 256)),
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(N * NP, 16)),
                          dim3(256), 0, st, workspace, 0, N * NP, gnp);
     SLG_LAUNCH_CHECK("conv_soft_bwd zero");
     return 0;
@@ -815,12 +825,12 @@ int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
     }
     if (gw) {
       const int64_t n = N * NL * K;
-      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(n, 16)), dim3(256), 0,
                          st, partw, p.NR, n, gw);
     }
     if (gnp) {
       const int64_t n = N * Nd::NP;
-      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+      hipLaunchKernelGGL(conv_bwd_sum_ranges_kernel, dim3((unsigned)cdiv(n, 16)), dim3(256), 0,
                          st, partn, p.NR, n, gnp);
     }
     SLG_LAUNCH_CHECK("conv_soft_bwd sums");

@@ -333,21 +333,32 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
   }
 }
 
-// gw [OUT,2,K], gnp [OUT,4] = sum over r of part[r] (r ascending).
+// gw [OUT,2,K], gnp [OUT,4] = sum over ranges r of part[r]: a workgroup
+// takes 16 columns (component, output); its 16 thread rows sum the ranges
+// r = row (mod 16) in ascending order, and the 16 row sums are added in row
+// order (a fixed order on every call).
 __global__ void __launch_bounds__(256) fc_soft_bwd_reduce_kernel(const float* __restrict__ part,
                                                                  int NR, int OUT, int K,
                                                                  float* __restrict__ gw,
                                                                  float* __restrict__ gnp) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ float rs[16][17];
+  const int col = threadIdx.x & 15, row = threadIdx.x >> 4;
+  const int64_t t = (int64_t)blockIdx.x * 16 + col;
   const int NC = 2 * K + 4;
-  if (t >= (int64_t)NC * OUT) return;
-  const int c = (int)(t / OUT), o = (int)(t - (int64_t)c * OUT);
+  const int64_t n = (int64_t)NC * OUT;
   float s = 0.0f;
-  for (int r = 0; r < NR; ++r) s += part[((int64_t)r * NC + c) * OUT + o];
+  if (t < n)
+    for (int r = row; r < NR; r += 16) s += part[(int64_t)r * n + t];
+  rs[row][col] = s;
+  __syncthreads();
+  if (row != 0 || t >= n) return;
+  float sum = 0.0f;
+  for (int q = 0; q < 16; ++q) sum += rs[q][col];
+  const int c = (int)(t / OUT), o = (int)(t - (int64_t)c * OUT);
   if (c < 2 * K) {
-    if (gw) gw[(int64_t)o * 2 * K + c] = s;  // c = side * K + k
+    if (gw) gw[(int64_t)o * 2 * K + c] = sum;  // c = side * K + k
   } else if (gnp) {
-    gnp[(int64_t)o * 4 + (c - 2 * K)] = s;
+    gnp[(int64_t)o * 4 + (c - 2 * K)] = sum;
   }
 }
 
@@ -541,7 +552,7 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
   if (want_w) {
     const int NR = B > 0 ? p.NR : 0;  // no samples: zero gradients
     const int64_t n = (int64_t)(2 * K + 4) * OUT;
-    hipLaunchKernelGGL(fc_soft_bwd_reduce_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
+    hipLaunchKernelGGL(fc_soft_bwd_reduce_kernel, dim3((unsigned)cdiv(n, 16)), dim3(256), 0, st,
                        part, NR, (int)OUT, K, gw, gnp);
     SLG_LAUNCH_CHECK("fc_soft_bwd_reduce");
   }
