@@ -162,6 +162,39 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
                     float* gw, float* gnp, float* workspace, int64_t workspace_floats,
                     slg_stream_t stream);
 
+/* FC layers of n-input LUT nodes, arity 2..6, Top-K (K <= 8) or fixed (K = 1)
+ * wiring: the multilinear node (nodes.py:165-189, arity != 2 or any arity)
+ * and the DWN-style hybrid node (nodes.py:198-206; replaces the fused op
+ * multilinear_logic, kernels/multilinear.py:123-160). cand/w [OUT,n,K]
+ * (w: softmax of the connection logits; 1 for fixed wiring), s [OUT,2^n]
+ * (sigmoid of the node logits), leaf j = address bit j.
+ * Forward: y [B,OUT] = multilinear interpolation of s at the operands, or
+ * (hybrid) s at the address of the operands thresholded at 0.5. workspace:
+ * slg_fc_lut_soft_workspace(OUT, n, K) floats. */
+int64_t slg_fc_lut_soft_workspace(int64_t OUT, int32_t arity, int32_t K);
+int slg_fc_lut_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t arity,
+                        int32_t K, const int32_t* cand, const float* w, const float* s,
+                        int32_t hybrid, float* y, float* workspace, int64_t workspace_floats,
+                        slg_stream_t stream);
+/* Backward of both (the gradient of the multilinear form, the hybrid node's
+ * surrogate): gy [B,OUT] -> gx [B,IN], gw [OUT,n,K], gs [OUT,2^n]; any of the
+ * three may be NULL. Every sum runs in a fixed order (the reference adds gx
+ * with atomics). workspace: slg_fc_lut_soft_bwd_workspace(...) floats, -1 for
+ * shapes not taken (IN beyond what LDS holds). */
+int64_t slg_fc_lut_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t arity,
+                                      int32_t K);
+int slg_fc_lut_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t arity,
+                        int32_t K, const int32_t* cand, const float* w, const float* s,
+                        const float* gy, float* gx, float* gw, float* gs, float* workspace,
+                        int64_t workspace_floats, slg_stream_t stream);
+/* Hard codes of such a layer for slg_fc_lut_hard (LogicLayer.forward_hard,
+ * layers.py:131-135 with nodes.py:180-187): idx [OUT,n] = per slot the first
+ * candidate with the largest connection logit (conn NULL: K = 1), tt [OUT]
+ * bit p = (logits[o][p] > 0). */
+int slg_fc_lut_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, int32_t arity,
+                         int32_t K, int64_t IN, const float* logits, int32_t* idx, uint64_t* tt,
+                         slg_stream_t stream);
+
 /* GroupSum.forward (silogic/heads.py:34-39): x [B,W] -> logits [B,C] =
  * sum over class block of (ste ? (x > 0.5) : x), divided by tau. */
 int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau,

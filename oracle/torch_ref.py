@@ -53,7 +53,8 @@ def walsh_monomials(u):
 # structure: expand constructor defaults (silogic/models.py)
 # --------------------------------------------------------------------------
 _NODE_ALIAS = {"gate16": "gate16", "gate": "gate16", "walsh": "walsh",
-               "multilinear": "multilinear", "probabilistic": "multilinear"}
+               "multilinear": "multilinear", "probabilistic": "multilinear",
+               "hybrid": "hybrid"}
 _CONN_ALIAS = {"f": "fixed", "fixed": "fixed", "topk": "topk", "blocktopk": "topk"}
 
 
@@ -153,6 +154,11 @@ def node_soft(L, sd, ops):
         u = 2 * ops - 1
         z = (walsh_monomials(u) * sd[p + "node.theta"][None]).sum(2)
         return torch.sigmoid(z * (1.0 / L["node_tau"]))
+    if L["node"] == "hybrid":                                  # nodes.py:202-206
+        f_soft = multilinear_f(ops, sd[p + "node.logits"], L["arity"])
+        with torch.no_grad():
+            f_disc = multilinear_f((ops >= 0.5).float(), sd[p + "node.logits"], L["arity"])
+        return f_disc + f_soft - f_soft.detach()
     return multilinear_f(ops, sd[p + "node.logits"], L["arity"])
 
 

@@ -24,12 +24,23 @@ from .packed_layer import (
     BitpackedConvTreeLayer,
     BitpackedFCLayer,
     BitpackedGroupSumHead,
+    BitpackedLUTLayer,
 )
 from .packed_model import BitpackedConvNet, BitpackedNet
 
 
-def convert_layer(layer) -> BitpackedFCLayer:
-    """One LogicLayer -> :class:`BitpackedFCLayer` (convert.py:165-214)."""
+def convert_layer(layer):
+    """One LogicLayer -> :class:`BitpackedFCLayer` (gate16 / walsh / arity-2
+    multilinear, convert.py:165-214) or :class:`BitpackedLUTLayer` (hybrid
+    and multilinear LUT layers of any arity, convert.py:84-120)."""
+    if getattr(layer, "is_lut", False):
+        with torch.no_grad():
+            idx, tt = layer.lut_hard_codes()                            # HIP prep
+            idx = idx.cpu().numpy().astype(np.int32)
+            words = tt.cpu().numpy().astype(np.uint64)
+        n = idx.shape[1]
+        tables = ((words[:, None] >> np.arange(1 << n, dtype=np.uint64)[None, :]) & 1).astype(bool)
+        return BitpackedLUTLayer(tables, idx)
     with torch.no_grad():
         codes = layer.hard_codes().cpu().numpy().astype(np.int64)      # [OUT, 2]
     a_idx = codes[:, 0].astype(np.int32)

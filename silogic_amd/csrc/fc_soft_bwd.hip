@@ -24,6 +24,7 @@
 //     transposed to sample-minor rows gab [2*OUT][LB]; the gather kernel
 //     walks each input's entries with its lanes along samples.
 #include "fc_soft_common.h"
+#include "fc_bwd_input.h"
 #include "ref_table.h"
 
 namespace slg {
@@ -104,13 +105,13 @@ __global__ void __launch_bounds__(256) fc_soft_bwd_keys_kernel(const int* __rest
 }
 
 __global__ void __launch_bounds__(256) fc_soft_bwd_entries_kernel(const int* __restrict__ sorted,
-                                                                  int R, int OUT, int K,
+                                                                  int R, int OUT, int NS, int K,
                                                                   const float* __restrict__ w,
                                                                   int2* __restrict__ ent) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= R) return;
-  const int r = sorted[j], K2 = 2 * K;
-  const int o = r / K2, side = (r - o * K2) / K;
+  const int r = sorted[j], SK = NS * K;  // r = (o * NS + side) * K + k
+  const int o = r / SK, side = (r - o * SK) / K;
   ent[j] = make_int2(side * OUT + o, __float_as_int(w[r]));
 }
 
@@ -379,17 +380,70 @@ constexpr int kGatherInputs = 4 * kGatherIW;
 
 inline int64_t round4(int64_t n) { return (n + 3) & ~int64_t(3); }
 
-// Workspace (in 4-byte words): records | partials | gbr | gab | keys | table | ent.
+// Workspace (in 4-byte words): records | partials | gbr | input-gradient part.
 struct BwdPlan {
   int Sw;              // samples per LDS tile of the weight kernel (0 = unsupported)
   int n_orange, NR, tiles_per_range;
-  int64_t LB;          // gab row stride (samples, padded to the gather tile)
-  int64_t R;           // references = 2 * OUT * K
-  int64_t rec_floats, part_floats, gbr_floats, gab_floats, keys_ints, table_ints, ent_ints;
-  int64_t total() const {
-    return rec_floats + part_floats + gbr_floats + gab_floats + keys_ints + table_ints + ent_ints;
-  }
+  int64_t rec_floats, part_floats, gbr_floats, in_floats;
+  int64_t total() const { return rec_floats + part_floats + gbr_floats + in_floats; }
 };
+
+// Input-gradient workspace: gab [nsides*OUT][LB] | keys | table | entries.
+struct InPlan {
+  int64_t LB, R, gab_floats, keys_ints, table_ints, ent_ints;
+  int64_t total() const { return gab_floats + keys_ints + table_ints + ent_ints; }
+};
+
+static InPlan in_plan(int64_t B, int64_t IN, int64_t OUT, int nsides, int K) {
+  InPlan q{};
+  q.LB = cdiv(std::max<int64_t>(B, 1), kGatherSamples) * kGatherSamples;
+  q.R = nsides * OUT * (int64_t)K;
+  q.gab_floats = nsides * OUT * q.LB;
+  q.keys_ints = round4(q.R);
+  q.table_ints = ref_table_ints(q.R, IN);
+  q.ent_ints = 2 * q.R;
+  return q;
+}
+
+int64_t fc_input_grad_floats(int64_t B, int64_t IN, int64_t OUT, int nsides, int K) {
+  return in_plan(B, IN, OUT, nsides, K).total();
+}
+
+int fc_input_grad(const float* gbr, int64_t B, int64_t IN, int64_t OUT, int nsides, int K,
+                  const int32_t* cand, const float* w, float* ws, float* gx, hipStream_t st) {
+  const InPlan q = in_plan(B, IN, OUT, nsides, K);
+  SLG_REQUIRE(q.R < (1LL << 31) && nsides * OUT < (1LL << 31), SLG_E_SHAPE,
+              "fc input gradient: too many references");
+  float* gab = ws;
+  int* keys = reinterpret_cast<int*>(gab + q.gab_floats);
+  int* table = keys + q.keys_ints;
+  int2* ent = reinterpret_cast<int2*>(table + q.table_ints);  // 8-byte aligned: offsets are even
+  const int R = (int)q.R;
+  hipLaunchKernelGGL(fc_soft_bwd_keys_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                     cand, R, (int)IN, keys);
+  RefTable tb{};
+  int rc = build_ref_table(keys, R, IN, table, st, &tb);
+  if (rc) return rc;
+  hipLaunchKernelGGL(fc_soft_bwd_entries_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
+                     tb.sorted, R, (int)OUT, nsides, K, w, ent);
+  SLG_LAUNCH_CHECK("fc input gradient entries");
+  const int R2 = (int)(nsides * OUT);
+  const int n_rtiles = (int)cdiv(R2, 64);
+  const int64_t n_tr = n_rtiles * (q.LB / 64);
+  SLG_REQUIRE(n_tr < (1LL << 31), SLG_E_SHAPE, "fc input gradient: grid too large");
+  hipLaunchKernelGGL(fc_soft_bwd_transpose_kernel, dim3((unsigned)n_tr), dim3(256), 0, st, gbr,
+                     (int)B, R2, q.LB, n_rtiles, gab);
+  SLG_LAUNCH_CHECK("fc input gradient transpose");
+  const int n_itiles = (int)cdiv(IN, kGatherInputs);
+  const int64_t n_blocks = n_itiles * (q.LB / kGatherSamples);
+  SLG_REQUIRE(n_blocks < (1LL << 31) - 8, SLG_E_SHAPE, "fc input gradient: grid too large");
+  const int64_t grid = cdiv(n_blocks, 8) * 8;  // a multiple of 8 for the XCD remap
+  auto gather = fc_soft_bwd_gather_kernel<kGatherV, kGatherIW>;
+  hipLaunchKernelGGL(gather, dim3((unsigned)grid), dim3(256), 0, st, gab, q.LB, (int)B, (int)IN,
+                     tb.start, ent, n_itiles, (int)n_blocks, gx);
+  SLG_LAUNCH_CHECK("fc input gradient gather");
+  return 0;
+}
 
 static BwdPlan bwd_plan(int64_t B, int64_t IN, int64_t OUT, int K) {
   BwdPlan p{};
@@ -407,15 +461,11 @@ static BwdPlan bwd_plan(int64_t B, int64_t IN, int64_t OUT, int K) {
   p.NR = (int)std::max<int64_t>(1, std::min<int64_t>(n_tiles, slots / p.n_orange));
   p.tiles_per_range = (int)cdiv(n_tiles, p.NR);
   p.NR = (int)cdiv(n_tiles, p.tiles_per_range);
-  p.LB = cdiv(std::max<int64_t>(B, 1), kGatherSamples) * kGatherSamples;
-  p.R = 2 * OUT * (int64_t)K;
+  const int64_t LB = cdiv(std::max<int64_t>(B, 1), kGatherSamples) * kGatherSamples;
   p.rec_floats = cdiv(OUT, 64) * 64 * (int64_t)(K + 1) * 4;
   p.part_floats = round4((int64_t)p.NR * (2 * K + 4) * OUT);
-  p.gbr_floats = 2 * OUT * p.LB;  // rows b < n_tiles * Sw <= LB
-  p.gab_floats = 2 * OUT * p.LB;
-  p.keys_ints = round4(p.R);
-  p.table_ints = ref_table_ints(p.R, IN);
-  p.ent_ints = 2 * p.R;
+  p.gbr_floats = 2 * OUT * LB;  // rows b < n_tiles * Sw <= LB
+  p.in_floats = fc_input_grad_floats(B, IN, OUT, 2, K);
   return p;
 }
 
@@ -497,10 +547,7 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
   float* rec = workspace;
   float* part = rec + p.rec_floats;
   float* gbr = part + p.part_floats;
-  float* gab = gbr + p.gbr_floats;
-  int* keys = reinterpret_cast<int*>(gab + p.gab_floats);
-  int* table = keys + p.keys_ints;
-  int2* ent = reinterpret_cast<int2*>(table + p.table_ints);  // 8-byte aligned: offsets are even
+  float* in_ws = gbr + p.gbr_floats;
   hipLaunchKernelGGL(fc_soft_pack_records_kernel, dim3((unsigned)cdiv(p.rec_floats, 256)),
                      dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN, rec);
   SLG_LAUNCH_CHECK("fc_soft_pack_records");
@@ -524,30 +571,8 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
     if (rc) return rc;
   }
   if (want_x) {
-    const int R = (int)p.R;
-    hipLaunchKernelGGL(fc_soft_bwd_keys_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
-                       cand, R, (int)IN, keys);
-    RefTable tb{};
-    int rc = build_ref_table(keys, R, IN, table, st, &tb);
+    int rc = fc_input_grad(gbr, B, IN, OUT, 2, K, cand, w, in_ws, gx, st);
     if (rc) return rc;
-    hipLaunchKernelGGL(fc_soft_bwd_entries_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, st,
-                       tb.sorted, R, (int)OUT, K, w, ent);
-    SLG_LAUNCH_CHECK("fc_soft_bwd entries");
-    const int R2 = (int)(2 * OUT);
-    const int n_rtiles = (int)cdiv(R2, 64);
-    const int64_t n_tr = n_rtiles * (p.LB / 64);
-    SLG_REQUIRE(n_tr < (1LL << 31), SLG_E_SHAPE, "fc_soft_bwd: grid too large");
-    hipLaunchKernelGGL(fc_soft_bwd_transpose_kernel, dim3((unsigned)n_tr), dim3(256), 0, st, gbr,
-                       (int)B, R2, p.LB, n_rtiles, gab);
-    SLG_LAUNCH_CHECK("fc_soft_bwd_transpose");
-    const int n_itiles = (int)cdiv(IN, kGatherInputs);
-    const int64_t n_blocks = n_itiles * (p.LB / kGatherSamples);
-    SLG_REQUIRE(n_blocks < (1LL << 31) - 8, SLG_E_SHAPE, "fc_soft_bwd: grid too large");
-    const int64_t grid = cdiv(n_blocks, 8) * 8;  // a multiple of 8 for the XCD remap
-    auto gather = fc_soft_bwd_gather_kernel<kGatherV, kGatherIW>;
-    hipLaunchKernelGGL(gather, dim3((unsigned)grid), dim3(256), 0, st,
-                       gab, p.LB, (int)B, (int)IN, tb.start, ent, n_itiles, (int)n_blocks, gx);
-    SLG_LAUNCH_CHECK("fc_soft_bwd_gather");
   }
   if (want_w) {
     const int NR = B > 0 ? p.NR : 0;  // no samples: zero gradients

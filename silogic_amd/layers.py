@@ -83,10 +83,24 @@ class LogicLayer(nn.Module):
         return self._conn.conn[:, 1]
 
     # -- HIP dispatch ----------------------------------------------------------
+    @property
+    def is_lut(self):
+        """An n-input LUT layer (the hybrid node, or a multilinear node of
+        arity other than 2): ``slg_fc_lut_*`` instead of the gate kernels."""
+        return getattr(self.node, "hybrid", False) or (
+            self._node_name == "multilinear" and self.arity != 2)
+
     def _check_supported(self):
-        if self.arity != 2:
+        if self.arity != 2 or self.is_lut:
             raise NotImplementedError(
-                f"LogicLayer arity {self.arity}: the MI355X FC kernels take arity-2 nodes")
+                f"LogicLayer arity {self.arity} / node {self._node_name}: the gate kernels "
+                "take arity-2 gate16 / walsh / multilinear nodes (LUT layers run slg_fc_lut_*)")
+
+    def lut_hard_codes(self):
+        """``(idx [out, n] int32, tt [out] int64)`` of a LUT layer (HIP prep)."""
+        conn = None if isinstance(self._conn, FixedConnectome) else self._conn.conn
+        return ops.fc_lut_hard_codes(self._conn.candidates_i32(), conn, self.node.logits,
+                                     self.in_dim)
 
     def _inv_tau(self):
         return self.node.inv_tau if self._node_name == "walsh" else 1.0
@@ -109,7 +123,9 @@ class LogicLayer(nn.Module):
     def record_spec(self):
         """``(cand, conn, raw, in_dim, node_kind, order)`` for
         ``ops.fc_soft_records`` when the forward without gradients is a plain
-        softmax selection, else ``None``."""
+        softmax selection, else ``None`` (also for LUT layers)."""
+        if self.is_lut:
+            return None
         self._check_supported()
         conn = self._conn
         if not self.node.plain_softmax() or getattr(conn, "ste", False):
@@ -138,8 +154,12 @@ class LogicLayer(nn.Module):
         return self._order_cache[1]
 
     def forward(self, x):
-        self._check_supported()
         ops.require_gpu(x)
+        if self.is_lut:
+            conn = self._conn
+            return ops.fc_lut_soft(x, conn.candidates_i32(), conn.weights(),
+                                   torch.sigmoid(self.node.logits), self.node.hybrid)
+        self._check_supported()
         grad = _needs_grad(self, x)
         spec = None if grad else self.record_spec()
         if spec is not None:
@@ -159,12 +179,17 @@ class LogicLayer(nn.Module):
         """Per-output ``(a, b | tt << 28)`` codes [out, 2] int32 (HIP prep)."""
         return ops.fc_hard_codes(*self.hard_spec())
 
+    def packed_forward(self, xp):
+        """Packed ``[in, nw]`` -> ``[out, nw]`` words."""
+        if self.is_lut:
+            return ops.fc_lut_hard(xp, *self.lut_hard_codes())
+        return ops.fc_hard_layer(xp, self.hard_codes())
+
     @torch.no_grad()
     def forward_hard(self, x):
         ops.require_gpu(x)
         B = x.shape[0]
-        xp = ops.pack_bits(x)
-        return ops.unpack_bits(ops.fc_hard_layer(xp, self.hard_codes()), B)
+        return ops.unpack_bits(self.packed_forward(ops.pack_bits(x)), B)
 
 
 class WARPLayer(LogicLayer):

@@ -59,6 +59,15 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
     fused into it when the input is at most 1024 features wide; otherwise one
     packed kernel per layer."""
+    if any(layer.is_lut for layer in layers):
+        # LUT layers: one packed kernel per layer (gate or LUT)
+        xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
+        for layer in layers:
+            yp = layer.packed_forward(xp)
+            if wire_r and yp.shape[0] == xp.shape[0]:
+                yp[:wire_r] = xp[:wire_r]
+            xp = yp
+        return ops.groupsum_packed(xp, B, C)
     specs = [layer.hard_spec() for layer in layers]
     widths = [layer.out_dim for layer in layers]
     spw = ops.fc_hard_net_supported(in_dim, widths, C)

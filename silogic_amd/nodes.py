@@ -22,7 +22,7 @@ from .functional import (BASIS_COEFFS, TRUTH_TABLES, GATE_A, gate_probs, residua
 
 NODES = ("gate16", "walsh", "multilinear", "hybrid", "linear", "polynomial")
 RELAXATIONS = ("probabilistic", "hybrid", "linear", "polynomial")
-SUPPORTED = ("gate16", "walsh", "multilinear")
+SUPPORTED = ("gate16", "walsh", "multilinear", "hybrid")
 _NODE_ALIASES = {
     "gate16": "gate16", "gate": "gate16",
     "walsh": "walsh",
@@ -159,7 +159,19 @@ class MultilinearNode(Node):
         self.logits.copy_((2 * bit0 - 1) * c + 0.1 * torch.randn_like(self.logits))
 
 
-_BUILDERS = {"gate16": Gate16Node, "walsh": WalshNode, "multilinear": MultilinearNode}
+class HybridNode(MultilinearNode):
+    """DWN-style: the forward reads the LUT at the address of the operands
+    thresholded at 0.5; the gradient is the multilinear node's (straight
+    through), silogic/nodes.py:198-206. Same parameters as the multilinear
+    node (``logits`` [out, 2^arity])."""
+
+    hybrid = True
+
+
+MultilinearNode.hybrid = False
+
+_BUILDERS = {"gate16": Gate16Node, "walsh": WalshNode, "multilinear": MultilinearNode,
+             "hybrid": HybridNode}
 
 
 def build_node(name, out_dim, arity=2, **kw):
@@ -177,4 +189,6 @@ def build_node(name, out_dim, arity=2, **kw):
     if key == "walsh":
         return WalshNode(out_dim, arity, tau=kw.get("tau", 1.0),
                          gate_select=kw.get("gate_select", "softmax"))
+    if key == "hybrid":
+        return HybridNode(out_dim, arity)
     return MultilinearNode(out_dim, arity)

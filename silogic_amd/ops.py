@@ -156,6 +156,89 @@ def fc_soft(x, cand, w, npar, node_kind, inv_tau=1.0):
                            _c(npar, torch.float32), node_kind, inv_tau)
 
 
+# ---------------------------------------------------------------------------
+# FC layers of n-input LUT nodes (multilinear of any arity, hybrid)
+# ---------------------------------------------------------------------------
+def _fc_lut_launch(x, cand, w, s, hybrid):
+    B, IN = x.shape
+    OUT, n, K = cand.shape
+    if w.shape != cand.shape or tuple(s.shape) != (OUT, 2 ** n):
+        raise ValueError("fc_lut_soft: cand/w [OUT,n,K] and s [OUT,2^n] expected")
+    ws = _lib.lib().slg_fc_lut_soft_workspace(OUT, n, K)
+    if ws < 0:
+        raise NotImplementedError(f"fc_lut_soft: arity {n} / K {K} (arity 2..6, K 1..8)")
+    work = torch.empty(ws, device=x.device, dtype=torch.float32)
+    y = torch.empty((B, OUT), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_lut_soft_fwd", _p(x), B, IN, OUT, n, K, _p(cand), _p(w), _p(s),
+              int(bool(hybrid)), _p(y), _p(work), ws, _stream(x))
+    return y
+
+
+def fc_lut_soft_bwd(x, cand, w, s, gy, need_x=True, need_w=True, need_s=True):
+    """HIP backward of the LUT layer: ``(gx, gw, gs)`` (None where not
+    needed), or None when the kernels do not take the shape."""
+    require_gpu(x, cand, w, s, gy)
+    x, cand = _as_f32(x.detach()), _c(cand, torch.int32)
+    w, s = _c(w.detach(), torch.float32), _c(s.detach(), torch.float32)
+    B, IN = x.shape
+    OUT, n, K = cand.shape
+    ws = _lib.lib().slg_fc_lut_soft_bwd_workspace(B, IN, OUT, n, K)
+    if ws < 0:
+        return None
+    gy = _c(gy, torch.float32)
+    gx = torch.empty_like(x) if need_x else None
+    gw = torch.empty_like(w) if need_w else None
+    gs = torch.empty_like(s) if need_s else None
+    work = torch.empty(max(ws, 1), device=x.device, dtype=torch.float32)
+    _lib.call("slg_fc_lut_soft_bwd", _p(x), B, IN, OUT, n, K, _p(cand), _p(w), _p(s), _p(gy),
+              _p(gx), _p(gw), _p(gs), _p(work), ws, _stream(x))
+    return gx, gw, gs
+
+
+class FCLutFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, cand, w, s, hybrid):
+        x = _as_f32(x)
+        cand, w, s = _c(cand, torch.int32), _c(w, torch.float32), _c(s, torch.float32)
+        ctx.save_for_backward(x, cand, w, s)
+        return _fc_lut_launch(x, cand, w, s, hybrid)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, cand, w, s = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        got = fc_lut_soft_bwd(x, cand, w, s, gy, need[0], need[2], need[3])
+        if got is None:
+            raise NotImplementedError("fc_lut_soft backward: the input width exceeds what the "
+                                      "kernels stage in LDS")
+        gx, gw, gs = got
+        return gx, None, gw, gs, None
+
+
+def fc_lut_soft(x, cand, w, s, hybrid):
+    """``[B,IN] -> [B,OUT]`` LUT layer (multilinear interpolation of ``s``, or
+    the hybrid lookup), autograd-aware (the multilinear gradient)."""
+    require_gpu(x, cand, w, s)
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or s.requires_grad):
+        return FCLutFn.apply(x, cand, w, s, hybrid)
+    return _fc_lut_launch(_as_f32(x), _c(cand, torch.int32), _c(w, torch.float32),
+                          _c(s, torch.float32), hybrid)
+
+
+def fc_lut_hard_codes(cand, conn, logits, in_dim):
+    """``(idx [OUT,n] int32, tt [OUT] int64)`` for ``fc_lut_hard``."""
+    require_gpu(cand, logits)
+    cand = _c(cand, torch.int32)
+    OUT, n, K = cand.shape
+    idx = torch.empty((OUT, n), device=cand.device, dtype=torch.int32)
+    tt = torch.empty((OUT,), device=cand.device, dtype=torch.int64)
+    _lib.call("slg_fc_lut_hard_prep", _p(cand), _p(None if conn is None else
+                                                   _c(conn.detach(), torch.float32)),
+              OUT, n, K, in_dim, _p(_c(logits.detach(), torch.float32)), _p(idx), _p(tt),
+              _stream(cand))
+    return idx, tt
+
+
 MAX_RECORD_LAYERS = 16
 
 

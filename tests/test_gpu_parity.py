@@ -692,3 +692,92 @@ def test_fc_soft_backward_skewed_references_and_determinism():
         assert err <= 1e-4 * scale + 1e-6, f"{what}: max err {err:.3e} (scale {scale:.3e})"
     assert torch.equal(gx, gx2) and torch.equal(gw, gw2) and torch.equal(gn, gn2)
     assert torch.equal(gx, gx3)
+
+
+# --------------------------------------------------------------------------
+# FC layers of n-input LUT nodes (multilinear of any arity, hybrid)
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("node,arity,conn,k,IN,OUT,B", [
+    ("multilinear", 3, "topk", 8, 300, 200, 37),
+    ("hybrid", 4, "topk", 8, 500, 300, 70),
+    ("hybrid", 6, "topk", 8, 2000, 1100, 300),     # two output groups, several tiles
+    ("multilinear", 6, "topk", 4, 100, 64, 9),
+    ("hybrid", 2, "fixed", 1, 64, 50, 20),
+    ("multilinear", 5, "fixed", 1, 40, 30, 5),
+    ("hybrid", 6, "topk", 8, 20000, 300, 16),       # 2-sample tiles
+    ("hybrid", 4, "topk", 3, 90, 70, 11),           # K padded to 4
+])
+def test_fc_lut_layer_forward_backward_hard(node, arity, conn, k, IN, OUT, B):
+    """LUT layers (nodes.py:165-206, the fused op kernels/multilinear.py)
+    against the oracle: soft values (hybrid: equal except where an operand is
+    within rounding of the 0.5 threshold), gradients of x, the connection and
+    node logits against fp32 autograd on the CPU, hard outputs bit for bit."""
+    layer = sl.LogicLayer(IN, OUT, node=node, connectome=conn, arity=arity, k=k, seed=7)
+    L = dict(prefix="", node=node, arity=arity, conn=conn)
+    params = {kk: v.clone().requires_grad_(v.is_floating_point())
+              for kk, v in layer.state_dict().items()}
+    gen = torch.Generator().manual_seed(13)
+    x = torch.rand(B, IN, generator=gen)
+    gy = torch.randn(B, OUT, generator=gen)
+    xr = x.clone().requires_grad_(True)
+    ref = torch_ref.fc_layer_soft(L, params, xr)
+    (ref * gy).sum().backward()
+    layer = layer.to(DEV).train()
+    xg = x.to(DEV).requires_grad_(True)
+    out = layer(xg)
+    (out * gy.to(DEV)).sum().backward()
+    got, want = out.detach().cpu(), ref.detach()
+    if node == "hybrid":
+        with torch.no_grad():
+            a = torch_ref.select_soft(L, params, x)
+        near = ((a - 0.5).abs() <= 1e-5).any(2)            # operands at the threshold
+        bad = (got - want).abs() > 1e-6
+        assert not (bad & ~near).any(), int((bad & ~near).sum())
+    else:
+        assert_soft_close(got, want, "lut soft")
+
+    def close(g, r, what):
+        g = g.cpu()
+        scale = r.abs().max().item()
+        err = (g - r).abs().max().item()
+        assert err <= 1e-4 * scale + 1e-6, f"{what}: max err {err:.3e} (scale {scale:.3e})"
+
+    close(xg.grad, xr.grad, "dL/dx")
+    for name, p in layer.named_parameters():
+        close(p.grad, params[name].grad, name)
+    xb = random_bits(B, IN)
+    hard = layer.forward_hard(xb.to(DEV)).cpu()
+    assert torch.equal(hard, torch_ref.fc_layer_hard(L, {k2: v.detach() for k2, v in
+                                                         params.items()}, xb))
+
+
+def test_hybrid_logicnet_soft_hard_and_packed():
+    """A hybrid LogicNet (the MNIST recipe's node, examples/train_mnist.py:51-52,
+    at small size): soft logits and gradients against the oracle, hard counts
+    bit for bit, and the bit-packed conversion's logits equal counts / tau."""
+    from silogic_amd import bitpacking as bp
+    spec = ("LogicNet", dict(in_dim=100, width=200, depth=2, node="hybrid", arity=4, k=8,
+                             tau=4.0, decoder_ste=False))
+    model = build_product(spec)
+    st = torch_ref.structure(spec)
+    params = {k: v.clone().requires_grad_(v.is_floating_point())
+              for k, v in model.state_dict().items()}
+    gen = torch.Generator().manual_seed(21)
+    x = (torch.rand(50, 100, generator=gen) > 0.5).float()
+    xr = x.clone().requires_grad_(True)
+    ref = torch_ref.groupsum_soft(st["head"], torch_ref.forward_features(st, params, xr, hard=False))
+    ref.pow(2).sum().backward()
+    model = model.to(DEV).train()
+    xg = x.to(DEV).requires_grad_(True)
+    out = model(xg)
+    out.pow(2).sum().backward()
+    assert (out.detach().cpu() - ref.detach()).abs().max() < 1e-4
+    assert (xg.grad.cpu() - xr.grad).abs().max() < 1e-4
+    for name, p in model.named_parameters():
+        assert (p.grad.cpu() - params[name].grad).abs().max() < 1e-4, name
+    model.eval()
+    counts = torch_ref.forward_hard(spec, {k: v.detach() for k, v in params.items()}, x)
+    assert torch.equal(model.forward_hard(x.to(DEV)).cpu(), counts)
+    packed = bp.convert_logic_net(model)
+    logits = packed(x.to(torch.uint8).to(DEV))
+    assert torch.equal(logits.cpu(), counts / torch.tensor(4.0))

@@ -101,7 +101,11 @@ def test_unsupported_components_are_rejected_at_construction():
     with pytest.raises(NotImplementedError):
         silogic_amd.LogicLayer(8, 8, connectome="dense")
     with pytest.raises(NotImplementedError):
-        silogic_amd.LogicLayer(8, 8, node="hybrid")
+        silogic_amd.LogicLayer(8, 8, node="linear")
+    # hybrid and n-input multilinear layers construct (the LUT kernels)
+    assert silogic_amd.LogicLayer(8, 8, node="hybrid", arity=4).is_lut
+    assert silogic_amd.LogicLayer(8, 8, node="multilinear", arity=3).is_lut
+    assert not silogic_amd.LogicLayer(8, 8, node="multilinear", arity=2).is_lut
     with pytest.raises(NotImplementedError):
         silogic_amd.LogicNet(8, 20, 2, decoder="linear")
 

@@ -82,6 +82,34 @@ def test_multilinear_interpolates_its_truth_table():
         assert torch.allclose(torch_ref.multilinear_f(a, logits, n), lin, atol=1e-6)
 
 
+def test_hybrid_is_the_lut_at_the_thresholded_address_with_multilinear_gradient():
+    """Hybrid node (nodes.py:198-206): its value is sigmoid(logit) of the
+    corner the operands round to (a LUT lookup, written here as a plain index
+    computation; the reference's PyTorch form adds and subtracts the soft
+    value, so equal up to fp32 rounding), and its gradient is the
+    multilinear node's."""
+    n = 5
+    L = dict(prefix="", node="hybrid", arity=n)
+    Lm = dict(prefix="", node="multilinear", arity=n)
+    logits = torch.randn(4, 2 ** n)
+    ops = torch.rand(7, 4, n)
+    ops[0, 0, 0] = 0.5                                       # the threshold itself rounds up
+    addr = ((ops >= 0.5).long() * (2 ** torch.arange(n))).sum(2)        # [B, out]
+    want = torch.sigmoid(logits)[torch.arange(4)[None, :].expand(7, 4), addr]
+    sd = {"node.logits": logits.clone().requires_grad_(True)}
+    a = ops.clone().requires_grad_(True)
+    y = torch_ref.node_soft(L, sd, a)
+    # f_disc + f_soft - f_soft.detach() in fp32: f_disc up to rounding
+    assert torch.allclose(y.detach(), want, rtol=0, atol=1e-6)
+    g = torch.randn(7, 4)
+    (y * g).sum().backward()
+    sdm = {"node.logits": logits.clone().requires_grad_(True)}
+    am = ops.clone().requires_grad_(True)
+    (torch_ref.node_soft(Lm, sdm, am) * g).sum().backward()
+    assert torch.equal(a.grad, am.grad)
+    assert torch.equal(sd["node.logits"].grad, sdm["node.logits"].grad)
+
+
 def _hardened_fc(spec):
     torch.manual_seed(0)
     model = getattr(silogic_amd, spec[0])(seed=0, **spec[1])
