@@ -47,7 +47,9 @@ enum {
 enum {
   SLG_NODE_GATE16 = 0,      /* y = c0 + c1 a + c2 b + c3 ab, param = coef [OUT,4] */
   SLG_NODE_WALSH = 1,       /* y = sigmoid((c0 + c1 a + c2 b + c3 ab) * inv_tau)  */
-  SLG_NODE_MULTILINEAR2 = 2 /* y = sum_P s_P prod_j(...), param = sigmoid(l) [OUT,4] */
+  SLG_NODE_MULTILINEAR2 = 2, /* y = sum_P s_P prod_j(...), param = sigmoid(l) [OUT,4] */
+  SLG_NODE_HYBRID = 3        /* conv LUT trees: y = s[addr of leaves >= 0.5], gradient of the
+                                multilinear form (nodes.py:198-206) */
 };
 
 const char* slg_last_error(void);

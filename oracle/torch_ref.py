@@ -155,11 +155,30 @@ def node_soft(L, sd, ops):
         z = (walsh_monomials(u) * sd[p + "node.theta"][None]).sum(2)
         return torch.sigmoid(z * (1.0 / L["node_tau"]))
     if L["node"] == "hybrid":                                  # nodes.py:202-206
-        f_soft = multilinear_f(ops, sd[p + "node.logits"], L["arity"])
-        with torch.no_grad():
-            f_disc = multilinear_f((ops >= 0.5).float(), sd[p + "node.logits"], L["arity"])
-        return f_disc + f_soft - f_soft.detach()
+        return hybrid_f(ops, sd[p + "node.logits"], L["arity"])
     return multilinear_f(ops, sd[p + "node.logits"], L["arity"])
+
+
+class _Straight(torch.autograd.Function):
+    """Value of ``disc``, gradient into ``soft``: the hybrid node's
+    ``f_disc + f_soft - f_soft.detach()`` (nodes.py:202-206) without the
+    fp32 rounding of that sum, i.e. the LUT value exactly, as the reference's
+    fused kernels return it (kernels/multilinear.py:40-61)."""
+
+    @staticmethod
+    def forward(ctx, disc, soft):
+        return disc.clone()
+
+    @staticmethod
+    def backward(ctx, g):
+        return None, g
+
+
+def hybrid_f(ops, logits, n):
+    f_soft = multilinear_f(ops, logits, n)
+    with torch.no_grad():
+        f_disc = multilinear_f((ops >= 0.5).float(), logits, n)
+    return _Straight.apply(f_disc, f_soft)
 
 
 def multilinear_f(ops, logits, n):
@@ -268,9 +287,14 @@ def _node_tree(blk, sd, vals, hard):
         m = km // k
         ops = vals.view(B, n, m, k, L).permute(0, 4, 1, 2, 3).reshape(B * L, n * m, k)
         logits = sd[f"{blk['prefix']}tree_nodes.{i}.logits"]
-        if blk["node"] != "multilinear":
+        if blk["node"] not in ("multilinear", "hybrid"):
             raise NotImplementedError(blk["node"])
-        out = multilinear_hard(ops, logits, k) if hard else multilinear_f(ops, logits, k)
+        if hard:
+            out = multilinear_hard(ops, logits, k)
+        elif blk["node"] == "hybrid":                          # nodes.py:202-206
+            out = hybrid_f(ops, logits, k)
+        else:
+            out = multilinear_f(ops, logits, k)
         vals = out.view(B, L, n, m).permute(0, 2, 3, 1)
     return vals[:, :, 0, :]
 

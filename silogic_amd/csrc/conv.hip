@@ -116,7 +116,7 @@ __device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM, NW>& P, in
     }
   }
   constexpr int NP = ConvNode<NODE, NLEAF>::NP;
-  if constexpr (NODE == SLG_NODE_GATE16) {
+  if constexpr (NODE != SLG_NODE_MULTILINEAR2) {  // gate16 coefficients, hybrid values
 #pragma unroll
     for (int i = 0; i < NP; ++i) P.par[i] = np[(int64_t)nv * NP + i];
   } else {
@@ -481,6 +481,9 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
       for (int i = 0; i < 16; ++i) acc += (e[i] / sum) * c_basis_conv[i][q & 3];
       v = acc;
     }
+  } else if (node == SLG_NODE_HYBRID) {
+    const int P = 1 << arity, q = slot - LK * (NW + 1);
+    if (q < P) v = sigmoidc(raw[(int64_t)n * P + q]);
   } else {
     const int H2 = 1 << (arity - 1), q = slot - LK * (NW + 1);
     const float* s_ = raw + (int64_t)n * 2 * H2;
@@ -633,13 +636,23 @@ static int conv_soft_dispatch(const ConvSoftArgs& a, int node, int nleaf, hipStr
       case 16: return launch_conv_soft<SLG_NODE_GATE16, 16, POOL>(a, st);
       default: break;
     }
-  } else {
+  } else if (node == SLG_NODE_MULTILINEAR2) {
     switch (nleaf) {
       case 2: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 2, POOL>(a, st);
       case 3: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 3, POOL>(a, st);
       case 4: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 4, POOL>(a, st);
       case 5: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 5, POOL>(a, st);
       case 6: return launch_conv_soft<SLG_NODE_MULTILINEAR2, 6, POOL>(a, st);
+      default: break;
+    }
+  }
+  if (node == SLG_NODE_HYBRID) {
+    switch (nleaf) {
+      case 2: return launch_conv_soft<SLG_NODE_HYBRID, 2, POOL>(a, st);
+      case 3: return launch_conv_soft<SLG_NODE_HYBRID, 3, POOL>(a, st);
+      case 4: return launch_conv_soft<SLG_NODE_HYBRID, 4, POOL>(a, st);
+      case 5: return launch_conv_soft<SLG_NODE_HYBRID, 5, POOL>(a, st);
+      case 6: return launch_conv_soft<SLG_NODE_HYBRID, 6, POOL>(a, st);
       default: break;
     }
   }
@@ -692,7 +705,8 @@ static int conv_hard_dispatch(int node, int nleaf, const uint64_t* xp, int64_t C
 
 static int node_leaves(int node, int depth, int arity) {
   if (node == SLG_NODE_GATE16) return (depth >= 1 && depth <= 4) ? (1 << depth) : -1;
-  if (node == SLG_NODE_MULTILINEAR2) return (depth == 1 && arity >= 2 && arity <= 6) ? arity : -1;
+  if (node == SLG_NODE_MULTILINEAR2 || node == SLG_NODE_HYBRID)
+    return (depth == 1 && arity >= 2 && arity <= 6) ? arity : -1;
   return -1;
 }
 
@@ -708,8 +722,9 @@ int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
                       const int32_t* cw, int32_t pad, int32_t pool, float* out, slg_stream_t stream) {
   SLG_REQUIRE(node_param && cm && ch && cw && ((x && out) || B == 0), SLG_E_ARG,
               "conv_soft: null pointer");
-  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
-              "conv_soft: node_kind %d", node_kind);
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2 ||
+                  node_kind == SLG_NODE_HYBRID,
+              SLG_E_ARG, "conv_soft: node_kind %d", node_kind);
   const int nleaf = node_leaves(node_kind, depth, arity);
   SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft: depth %d / arity %d", depth, arity);
   SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft: K=%d outside 1..%d", K, kMaxK);
@@ -765,8 +780,9 @@ int slg_conv_soft_fwd_records(const float* x, int64_t B, int64_t C, int64_t H, i
                               const float* rec, int32_t pad, int32_t pool, float* out,
                               slg_stream_t stream) {
   SLG_REQUIRE(rec && ((x && out) || B == 0), SLG_E_ARG, "conv_soft_records: null pointer");
-  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
-              "conv_soft: node_kind %d", node_kind);
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2 ||
+                  node_kind == SLG_NODE_HYBRID,
+              SLG_E_ARG, "conv_soft: node_kind %d", node_kind);
   const int nleaf = node_leaves(node_kind, depth, arity);
   SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft: depth %d / arity %d", depth, arity);
   SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft: K=%d outside 1..%d", K, kMaxK);

@@ -245,9 +245,13 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
       par[i] = v;
     } else {
       constexpr int H2 = NP / 2;
-      // kept form: even corners, then odd - even (as the forward keeps them)
-      if ((q & 1) == 0) par[t * NPR + q / 2] = v;
-      else par[t * NPR + H2 + q / 2] = v - np[(int64_t)n * NP + q - 1];
+      if constexpr (NODE == SLG_NODE_HYBRID) {
+        par[i] = v;  // the values as they are (the forward's lookup)
+      } else {
+        // kept form: even corners, then odd - even (as the forward keeps them)
+        if ((q & 1) == 0) par[t * NPR + q / 2] = v;
+        else par[t * NPR + H2 + q / 2] = v - np[(int64_t)n * NP + q - 1];
+      }
       // leaf differences D[j][qq] = s[p | bit j] - s[p] at the p with bit j set
 #pragma unroll
       for (int j = 0; j < NLEAF; ++j) {
@@ -679,7 +683,8 @@ static bool conv_bwd_plan_t(int64_t B, int64_t C, int64_t H, int64_t W, int64_t 
 
 static int conv_bwd_leaves(int node, int depth, int arity) {
   if (node == SLG_NODE_GATE16) return (depth >= 1 && depth <= 3) ? (1 << depth) : -1;
-  if (node == SLG_NODE_MULTILINEAR2) return (depth == 1 && arity >= 2 && arity <= 6) ? arity : -1;
+  if (node == SLG_NODE_MULTILINEAR2 || node == SLG_NODE_HYBRID)
+    return (depth == 1 && arity >= 2 && arity <= 6) ? arity : -1;
   return -1;
 }
 
@@ -701,6 +706,11 @@ static int conv_bwd_dispatch(int node, int nleaf, bool pool, F&& f) {
   SLG_CB(SLG_NODE_MULTILINEAR2, 4)
   SLG_CB(SLG_NODE_MULTILINEAR2, 5)
   SLG_CB(SLG_NODE_MULTILINEAR2, 6)
+  SLG_CB(SLG_NODE_HYBRID, 2)
+  SLG_CB(SLG_NODE_HYBRID, 3)
+  SLG_CB(SLG_NODE_HYBRID, 4)
+  SLG_CB(SLG_NODE_HYBRID, 5)
+  SLG_CB(SLG_NODE_HYBRID, 6)
 #undef SLG_CB
   set_error("conv_soft_bwd: unsupported leaves %d", nleaf);
   return SLG_E_UNSUPPORTED;
@@ -740,8 +750,9 @@ int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
                       int64_t workspace_floats, slg_stream_t stream) {
   SLG_REQUIRE(node_param && cm && ch && cw && workspace && ((x && gy) || B == 0), SLG_E_ARG,
               "conv_soft_bwd: null pointer");
-  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2, SLG_E_ARG,
-              "conv_soft_bwd: node_kind %d", node_kind);
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2 ||
+                  node_kind == SLG_NODE_HYBRID,
+              SLG_E_ARG, "conv_soft_bwd: node_kind %d", node_kind);
   const int nleaf = conv_bwd_leaves(node_kind, depth, arity);
   SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_bwd: depth %d / arity %d", depth, arity);
   SLG_REQUIRE(K >= 1 && K <= kBwdMaxK, SLG_E_SHAPE, "conv_soft_bwd: K=%d outside 1..%d", K,

@@ -7,13 +7,16 @@
 
 namespace slg {
 
-// NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree) or
-// SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1).
+// NODE: SLG_NODE_GATE16 (NLEAF = 2^depth leaves, binary BasisProj tree),
+// SLG_NODE_MULTILINEAR2 used as "LUT" (NLEAF = arity, depth 1), or
+// SLG_NODE_HYBRID (the same LUT read at the address of the leaves
+// thresholded at 0.5, nodes.py:198-206).
 template <int NODE, int NLEAF>
 struct ConvNode {
   static constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
-  // parameters kept per channel: gate16 coefficients [NN][4], or for the LUT
-  // the even corner values s[2m] and the differences s[2m+1] - s[2m]
+  // parameters kept per channel: gate16 coefficients [NN][4]; for the
+  // multilinear LUT the even corner values s[2m] and the differences
+  // s[2m+1] - s[2m]; for the hybrid LUT the values s[p] as they are
   static constexpr int NPR = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
   static constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);  // raw params
 };
@@ -39,6 +42,11 @@ __device__ inline float conv_tree_eval(const float (&v)[NLEAF], const float* par
       nb += cnt / 2;
     }
     return u[0];
+  } else if constexpr (NODE == SLG_NODE_HYBRID) {
+    int addr = 0;
+#pragma unroll
+    for (int l = 0; l < NLEAF; ++l) addr |= (v[l] >= 0.5f ? 1 : 0) << l;
+    return par[addr];
   } else {
     // multilinear interpolation of s over the leaves (corner bit j = leaf
     // j), silogic/nodes.py:174-178, as a lerp tree

@@ -333,17 +333,18 @@ __global__ void __launch_bounds__(512) fc_lut_bwd_w_kernel(const float* __restri
   }
 }
 
-// Corner sums: thread (output o, low corner c1 = blockIdx.y) over samples
-// [r*spr, (r+1)*spr): for every high corner c2, sum of g * A(c1) * B(c2);
-// part [NR][2^NA][OUT] (corner c1 + (c2 << H1)).
+// Corner sums: thread (output o, low corner c1) over samples [r*spr,
+// (r+1)*spr): for every high corner c2, sum of g * A(c1) * B(c2); part
+// [NR][2^NA][OUT] (corner c1 + (c2 << H1)). The NC1 threads of an output are
+// adjacent lanes, so one wave load of an operand row serves all of them.
 template <int NA>
 __global__ void __launch_bounds__(256) fc_lut_bwd_c_kernel(const float* __restrict__ arows,
                                                            const float* __restrict__ gy, int B,
                                                            int OUT, int spr,
                                                            float* __restrict__ part) {
-  constexpr int H1 = NA / 2, NC2 = 1 << (NA - H1), NP = 1 << NA;
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  const int c1 = blockIdx.y, r = blockIdx.z;
+  constexpr int H1 = NA / 2, NC1 = 1 << H1, NC2 = 1 << (NA - H1), NP = 1 << NA;
+  const int o = blockIdx.x * (256 / NC1) + threadIdx.x / NC1;
+  const int c1 = threadIdx.x % NC1, r = blockIdx.y;
   if (o >= OUT) return;
   float acc[NC2];
 #pragma unroll
@@ -563,8 +564,8 @@ static int lut_bwd_t(const float* x, int64_t B, int64_t IN, int64_t OUT, const f
   }
   if (partc) {
     hipLaunchKernelGGL(fc_lut_bwd_c_kernel<NA>,
-                       dim3((unsigned)cdiv(OUT, 256), (unsigned)(1 << (NA / 2)), (unsigned)p.NRc),
-                       dim3(256), 0, st, arows, gy, (int)B, (int)OUT, p.spr, partc);
+                       dim3((unsigned)cdiv(OUT, 256 >> (NA / 2)), (unsigned)p.NRc), dim3(256), 0,
+                       st, arows, gy, (int)B, (int)OUT, p.spr, partc);
     SLG_LAUNCH_CHECK("fc_lut_bwd_c");
   }
   return 0;

@@ -6,9 +6,10 @@ meaning and ``HAS_*`` capability flags, implemented by the HIP library.
 * :func:`warp_logic`  — silogic/kernels/warp.py:104-105
 * :func:`tree_conv`   — silogic/kernels/conv.py:399-400 (stride 1, 'same')
 * :func:`tree_conv_topk` — silogic/kernels/conv_topk.py:175-189
+* :func:`multilinear_logic` — silogic/kernels/multilinear.py:160-174 (hybrid LUT layer)
+* :func:`conv_hybrid` — silogic/kernels/conv_hybrid.py:196 (hybrid LUT trees of depth 1)
 
-The flags are True when ``libsilogic_hip.so`` loads; the hybrid-node kernels
-(``multilinear_logic``, ``conv_hybrid``) are not provided.
+The flags are True when ``libsilogic_hip.so`` loads.
 """
 import torch
 
@@ -16,7 +17,7 @@ from . import _lib, ops
 
 _OK = _lib.available()
 HAS_DENSE = HAS_WARP = HAS_CONV = HAS_CONV_TOPK = _OK
-HAS_MULTILINEAR = HAS_CONV_HYBRID = False
+HAS_MULTILINEAR = HAS_CONV_HYBRID = _OK
 
 
 def _pack_ab(ca, cb, wa, wb):
@@ -55,3 +56,23 @@ def tree_conv_topk(x, coef, w, cm, ch, cw, depth, K, stride, pad, Ho, Wo):
     """Top-K gate tree conv: w/cm/ch/cw [N,2^d,K]."""
     _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
     return ops.conv_soft(x, coef, w, cm, ch, cw, ops.GATE16, depth, 2, K, pad, False)
+
+
+def multilinear_logic(x, cand, w, s, arity):
+    """Hybrid (DWN-STE) LUT layer: x [B,IN], cand/w [OUT,arity,K], s
+    [OUT,2^arity] = sigmoid(logits) -> [B,OUT] = s at the address of the
+    operands thresholded at 0.5, with the multilinear gradient."""
+    if cand.shape[1] != arity:
+        raise ValueError("multilinear_logic: cand must be [OUT, arity, K]")
+    return ops.fc_lut_soft(x, cand, w, s, True)
+
+
+def conv_hybrid(x, s, w, cm, ch, cw, depth, node_arity, K, stride, pad, Ho, Wo):
+    """Hybrid LUT tree conv: s [N, nodes, 2^arity], w/cm/ch/cw [N, leaves, K];
+    trees of depth 1 (the reference's recipes), stride 1, 'same' padding."""
+    _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
+    if depth != 1:
+        raise NotImplementedError("conv_hybrid on MI355X: trees of depth 1")
+    N = cm.shape[0]
+    return ops.conv_soft(x, s.reshape(N, 2 ** node_arity), w, cm, ch, cw, ops.HYBRID, 1,
+                         node_arity, K, pad, False)

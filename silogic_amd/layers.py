@@ -211,8 +211,8 @@ class WARPLayer(LogicLayer):
 class ConvLogicTree(nn.Module):
     """Logic-gate-tree convolution (arguments as silogic.layers.ConvLogicTree).
 
-    The HIP path covers gate16 trees of depth 1-4 and depth-1 multilinear LUT
-    nodes of arity 2-6, stride 1 with ``padding = kernel // 2``."""
+    The HIP path covers gate16 trees of depth 1-4 and depth-1 multilinear or
+    hybrid LUT nodes of arity 2-6, stride 1 with ``padding = kernel // 2``."""
 
     def __init__(self, in_channels, out_channels, kernel=3, tree_depth=None,
                  stride=1, padding=1, connect="topk", k=4, n_chan=2,
@@ -237,10 +237,11 @@ class ConvLogicTree(nn.Module):
         self.k = k
         self.tau = tau
         self.use_triton = use_triton
-        if self.node_name not in ("gate16", "multilinear"):
+        if self.node_name not in ("gate16", "multilinear", "hybrid"):
             raise NotImplementedError(f"conv node {node!r} is not on the MI355X path")
-        if self.node_name == "multilinear" and (tree_depth != 1 or not 2 <= arity <= 6):
-            raise NotImplementedError("multilinear conv trees: depth 1, arity 2..6")
+        if self.node_name in ("multilinear", "hybrid") and (
+                tree_depth != 1 or not 2 <= arity <= 6):
+            raise NotImplementedError(f"{self.node_name} conv trees: depth 1, arity 2..6")
         if stride != 1 or 2 * padding + 1 != kernel:
             raise NotImplementedError("conv trees: stride 1 with padding = kernel // 2")
         gen = torch.Generator().manual_seed(seed)
@@ -322,7 +323,9 @@ class ConvLogicTree(nn.Module):
         return self.lc_cm, self.lc_ch, self.lc_cw
 
     def _kind(self):
-        return ops.GATE16 if self.node_name == "gate16" else ops.MULTILINEAR2
+        if self.node_name == "gate16":
+            return ops.GATE16
+        return ops.HYBRID if self.node_name == "hybrid" else ops.MULTILINEAR2
 
     def _raw(self):
         if self.node_name == "gate16":

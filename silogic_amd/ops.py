@@ -18,7 +18,7 @@ import torch.nn.functional as F
 
 from . import _lib
 
-GATE16, WALSH, MULTILINEAR2 = 0, 1, 2
+GATE16, WALSH, MULTILINEAR2, HYBRID = 0, 1, 2, 3
 NODE_KINDS = {"gate16": GATE16, "walsh": WALSH, "multilinear": MULTILINEAR2}
 
 
@@ -652,6 +652,18 @@ def _conv_soft_launch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, p
     return out
 
 
+class _StraightThrough(torch.autograd.Function):
+    """Value of ``disc`` exactly, gradient into ``soft`` (the hybrid node)."""
+
+    @staticmethod
+    def forward(ctx, disc, soft):
+        return disc.clone()
+
+    @staticmethod
+    def backward(ctx, g):
+        return None, g
+
+
 def conv_soft_torch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
     """Differentiable torch expression of the fused conv op (backward only)."""
     B, Cc, H, W = x.shape
@@ -673,10 +685,17 @@ def conv_soft_torch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, poo
     else:
         corners = torch.tensor([[(p >> j) & 1 for j in range(arity)] for p in range(2 ** arity)],
                                dtype=x.dtype, device=x.device)
-        a = vals.permute(0, 1, 3, 2).unsqueeze(3)                    # [B, N, L, 1, A]
         c = corners.view(1, 1, 1, -1, arity)
-        prod = (c * a + (1 - c) * (1 - a)).prod(-1)                   # [B, N, L, P]
-        out = (prod * npar.view(1, N, 1, -1)).sum(-1)
+
+        def lut(v):
+            a = v.permute(0, 1, 3, 2).unsqueeze(3)                   # [B, N, L, 1, A]
+            prod = (c * a + (1 - c) * (1 - a)).prod(-1)               # [B, N, L, P]
+            return (prod * npar.view(1, N, 1, -1)).sum(-1)
+        out = lut(vals)
+        if node_kind == HYBRID:  # discrete value, multilinear gradient (nodes.py:202-206)
+            with torch.no_grad():
+                disc = lut((vals >= 0.5).to(vals.dtype))
+            out = _StraightThrough.apply(disc, out)
     Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
     out = out.view(B, N, Hf, Wf)
     return F.max_pool2d(out, 2, 2) if pool else out

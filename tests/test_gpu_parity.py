@@ -414,17 +414,36 @@ def test_conv_gate16_depths(depth, connect):
     assert torch.equal(conv.forward_hard(xb.to(DEV)).cpu(), torch_ref.conv_hard(blk, sd, xb))
 
 
+@pytest.mark.parametrize("node", ["multilinear", "hybrid"])
 @pytest.mark.parametrize("arity", [2, 3, 4, 5, 6])
-def test_conv_multilinear_lut(arity):
+def test_conv_multilinear_lut(arity, node):
+    """LUT conv trees (multilinear; hybrid, kernels/conv_hybrid.py at depth 1):
+    soft values against the oracle (hybrid: within 1e-6 where no leaf is
+    within rounding of 0.5), both the records and the separate-array entry points,
+    pooled; hard outputs bit for bit."""
     conv = sl.ConvLogicTree(5, 10, kernel=3, tree_depth=1, connect="topk", k=4, n_chan=2,
-                            node="multilinear", arity=arity, residual_init=False, seed=2)
+                            node=node, arity=arity, residual_init=False, seed=2)
     sd = {k: v.clone() for k, v in conv.state_dict().items()}
     blk = dict(prefix="", cin=5, n=10, kernel=3, depth=1, stride=1, padding=1, connect="topk",
-               k=conv.k, node="multilinear", node_arity=arity, leaves=arity)
+               k=conv.k, node=node, node_arity=arity, leaves=arity)
     conv = conv.to(DEV).eval()
     x = torch.rand(3, 5, 8, 7)
     with torch.no_grad():
-        assert_soft_close(conv(x.to(DEV)), torch_ref.conv_soft(blk, sd, x), "conv")
+        ref = torch_ref.conv_soft(blk, sd, x)
+        outs = [conv(x.to(DEV)), conv.forward_pooled(x.to(DEV))]
+        with torch.enable_grad():   # the separate-array entry point (autograd path)
+            outs.append(conv(x.to(DEV).requires_grad_(True)).detach())
+    if node == "multilinear":
+        assert_soft_close(outs[0], ref, "conv")
+        assert_soft_close(outs[1], F.max_pool2d(ref, 2, 2), "conv pooled")
+        assert_soft_close(outs[2], ref, "conv (arrays)")
+    else:
+        patches = F.unfold(x, (3, 3), padding=1)
+        leaves = torch_ref.conv_leaves_soft(blk, sd, patches)           # [B, n, L, HW]
+        near = ((leaves - 0.5).abs() <= 1e-5).any(2).view(ref.shape)
+        for got in (outs[0], outs[2]):   # LUT values: sigmoid on the GPU vs torch's, ~1 ulp
+            bad = (got.cpu() - ref).abs() > 1e-6
+            assert not (bad & ~near).any(), int((bad & ~near).sum())
     xb = random_bits(66, 5, 8, 7)
     assert torch.equal(conv.forward_hard(xb.to(DEV)).cpu(), torch_ref.conv_hard(blk, sd, xb))
 
@@ -608,6 +627,8 @@ def test_fc_soft_backward_kernels(node, conn, k, IN, OUT, B):
     ("multilinear", 1, 3, "fixed", 1, 4, 7, 10, 4, False, True),
     ("multilinear", 1, 6, "topk", 4, 9, 32, 20, 2, True, True),  # the 32x32 LUT block
     ("gate16", 2, 2, "topk", 4, 2, 6, 8, 600, True, True),      # several samples per range
+    ("hybrid", 1, 6, "topk", 8, 9, 10, 16, 3, True, True),      # the CIFAR recipe's trees
+    ("hybrid", 1, 4, "fixed", 1, 4, 8, 10, 4, False, False),
 ])
 def test_conv_soft_backward_kernel(node, depth, arity, connect, k, C, H, N, B, pool, binary):
     """The HIP conv backward (fused pooling or not) against fp32 autograd
@@ -781,3 +802,38 @@ def test_hybrid_logicnet_soft_hard_and_packed():
     packed = bp.convert_logic_net(model)
     logits = packed(x.to(torch.uint8).to(DEV))
     assert torch.equal(logits.cpu(), counts / torch.tensor(4.0))
+
+
+def test_kernels_dropin_hybrid_ops():
+    """silogic.kernels' hybrid ops through the drop-in module, with the
+    reference's argument layout (kernels/multilinear.py:160-174,
+    kernels/conv_hybrid.py:196), against the oracle."""
+    from silogic_amd import kernels
+    assert kernels.HAS_MULTILINEAR and kernels.HAS_CONV_HYBRID
+    layer = sl.LogicLayer(60, 40, node="hybrid", arity=3, k=4, seed=5)
+    L = dict(prefix="", node="hybrid", arity=3, conn="topk")
+    sd = layer.state_dict()
+    x = torch.rand(9, 60)
+    ref = torch_ref.fc_layer_soft(L, sd, x)
+    cand = layer._conn.candidates_i32()
+    w = torch.softmax(sd["_conn.conn"], dim=2)
+    s = torch.sigmoid(sd["node.logits"])
+    got = kernels.multilinear_logic(x.to(DEV), cand.to(DEV), w.to(DEV), s.to(DEV), 3).cpu()
+    with torch.no_grad():
+        a = torch_ref.select_soft(L, sd, x)
+    near = ((a - 0.5).abs() <= 1e-5).any(2)
+    assert not (((got - ref).abs() > 1e-6) & ~near).any()
+    conv = sl.ConvLogicTree(4, 6, kernel=3, tree_depth=1, k=4, node="hybrid", arity=4, seed=4)
+    blk = dict(prefix="", cin=4, n=6, kernel=3, depth=1, stride=1, padding=1, connect="topk",
+               k=conv.k, node="hybrid", node_arity=4, leaves=4)
+    csd = conv.state_dict()
+    xc = torch.rand(2, 4, 7, 7)
+    cref = torch_ref.conv_soft(blk, csd, xc)
+    sc = torch.sigmoid(csd["tree_nodes.0.logits"]).view(6, 1, 16)       # [N, nodes, 2^arity]
+    wc = torch.softmax(csd["conn"], dim=2)
+    cgot = kernels.conv_hybrid(xc.to(DEV), sc.to(DEV), wc.to(DEV), conv.lc_cm.to(DEV),
+                               conv.lc_ch.to(DEV), conv.lc_cw.to(DEV), 1, 4, conv.k, 1, 1, 7,
+                               7).cpu()
+    leaves = torch_ref.conv_leaves_soft(blk, csd, F.unfold(xc, (3, 3), padding=1))
+    cnear = ((leaves - 0.5).abs() <= 1e-5).any(2).view(cref.shape)
+    assert not (((cgot - cref).abs() > 1e-6) & ~cnear).any()

@@ -85,8 +85,8 @@ def test_multilinear_interpolates_its_truth_table():
 def test_hybrid_is_the_lut_at_the_thresholded_address_with_multilinear_gradient():
     """Hybrid node (nodes.py:198-206): its value is sigmoid(logit) of the
     corner the operands round to (a LUT lookup, written here as a plain index
-    computation; the reference's PyTorch form adds and subtracts the soft
-    value, so equal up to fp32 rounding), and its gradient is the
+    computation; exact, as the reference's fused kernels return it, where its
+    PyTorch form adds and subtracts the soft value), and its gradient is the
     multilinear node's."""
     n = 5
     L = dict(prefix="", node="hybrid", arity=n)
@@ -99,8 +99,10 @@ def test_hybrid_is_the_lut_at_the_thresholded_address_with_multilinear_gradient(
     sd = {"node.logits": logits.clone().requires_grad_(True)}
     a = ops.clone().requires_grad_(True)
     y = torch_ref.node_soft(L, sd, a)
-    # f_disc + f_soft - f_soft.detach() in fp32: f_disc up to rounding
-    assert torch.allclose(y.detach(), want, rtol=0, atol=1e-6)
+    assert torch.equal(y.detach(), want)
+    # the reference's PyTorch form equals it up to fp32 rounding
+    f_soft = torch_ref.multilinear_f(ops, logits, n)
+    assert torch.allclose(want + f_soft - f_soft, want, rtol=0, atol=1e-6)
     g = torch.randn(7, 4)
     (y * g).sum().backward()
     sdm = {"node.logits": logits.clone().requires_grad_(True)}
