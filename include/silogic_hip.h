@@ -197,6 +197,29 @@ int slg_fc_lut_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, in
                          int32_t K, int64_t IN, const float* logits, int32_t* idx, uint64_t* tt,
                          slg_stream_t stream);
 
+/* Input encoders (the step before the gate layers). Thermometer codes of
+ * x [B,D] fp32 with T thresholds: learned = 0 is binarize / binarize_spatial
+ * (silogic/data.py:23-40, 75-89): feature t*D + d = (x[b][d] >= thr[t]);
+ * learned = 1 is LearnedThermometerEncoder.forward_hard (encoders.py:46-49):
+ * feature f*T + i = (x[b][f] - thr[f*T + i] > 0). layout 2: uint8 [B, D*T]
+ * (the reference's output); 0: packed [D*T, nw] (for images also the conv
+ * layout [C*T, H*W, nw]); 1: packed word-major [nw, D*T]. */
+int slg_encode_thermometer(const float* x, int64_t B, int64_t D, const float* thr, int32_t T,
+                           int32_t learned, int32_t layout, void* out, slg_stream_t stream);
+/* edge_bits (data.py:102-131): x [N,C,H,W] -> uint8 [N, C*3*2*T, H, W], per
+ * colour the 3x3 Sobel-x, Sobel-y and Laplacian responses (zero padding),
+ * each thresholded at > t and < -t; channel (ti*2 + s)*3C + c*3 + det. */
+int slg_edge_bits(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const float* thr,
+                  int32_t T, uint8_t* out, slg_stream_t stream);
+/* Gradient of the learnable thermometer's soft pass (encoders.py:40-44: the
+ * hard bits carry the gradient of sigmoid((x - t) * scale)): g [B, F*T] ->
+ * gx [B,F], gt [F,T] (either may be NULL; gt summed over samples in a fixed
+ * order, workspace slg_learned_thermo_bwd_workspace(B, F, T) floats). */
+int64_t slg_learned_thermo_bwd_workspace(int64_t B, int64_t F, int32_t T);
+int slg_learned_thermo_bwd(const float* x, int64_t B, int64_t F, int32_t T, const float* thr,
+                           float scale, const float* g, float* gx, float* gt, float* workspace,
+                           int64_t workspace_floats, slg_stream_t stream);
+
 /* GroupSum.forward (silogic/heads.py:34-39): x [B,W] -> logits [B,C] =
  * sum over class block of (ste ? (x > 0.5) : x), divided by tau. */
 int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau,

@@ -29,6 +29,9 @@ from .nodes import build_node, NODES, RELAXATIONS
 from .heads import GroupSum, build_decoder
 from .layers import LogicLayer, WARPLayer, ConvLogicTree, ConvLogicLayer, OrPool
 from .models import LogicNet, WARPNet, LogicConvNet, LogicTreeNet
+from .encoders import LearnedThermometerEncoder
+from .data import (binarize, binarize_spatial, binarize_packed, edge_bits, MNIST_THRESH,
+                   SEVEN_THRESH, FOUR_THRESH, FIVE_THRESH, CIFAR3_THRESH, EDGE_THRESH)
 from . import kernels, ops
 
 __all__ = [
@@ -37,4 +40,6 @@ __all__ = [
     "build_connectome", "build_node", "NODES", "RELAXATIONS", "GroupSum", "build_decoder",
     "LogicLayer", "WARPLayer", "ConvLogicTree", "ConvLogicLayer", "OrPool",
     "LogicNet", "WARPNet", "LogicConvNet", "LogicTreeNet", "kernels", "ops",
+    "LearnedThermometerEncoder", "binarize", "binarize_spatial", "binarize_packed", "edge_bits",
+    "MNIST_THRESH", "SEVEN_THRESH", "FOUR_THRESH", "FIVE_THRESH", "CIFAR3_THRESH", "EDGE_THRESH",
 ]

@@ -1,0 +1,264 @@
+// Input encoders on the GPU (the step before the gate layers): fixed
+// thermometer codes (silogic/data.py:23-40 binarize, 75-89 binarize_spatial),
+// edge-detector bits (data.py:102-131 edge_bits) and the learnable
+// thermometer (silogic/encoders.py:12-49). Each writes the reference's uint8
+// layout, and the thermometers also write the packed layouts the hard kernels
+// read ([F, nw] rows, which is also the conv [C, H*W, nw] layout, or [nw, F]
+// word-major for the fused FC network), so a batch goes from pixels to
+// packed bits in one pass.
+//
+// binarize / binarize_spatial share one memory order: feature t*D + d is
+// (x[b][d] >= thr[t]) for D = C*H*W (the spatial form's channel t*C + c).
+// The learnable thermometer orders f*bits + i: (x[b][f] - thr[f][i] > 0).
+#include <math.h>
+
+#include "slg_common.h"
+
+namespace slg {
+
+// Bit of feature j of sample b. FIXED: j = t*D + d, x >= thr[t]; else
+// (learned): j = f*T + i, x[f] - thr[f*T + i] > 0.
+template <bool FIXED>
+__device__ inline bool encode_bit(const float* __restrict__ x, int64_t b, int D, int T,
+                                  const float* __restrict__ thr, int j) {
+  if constexpr (FIXED) {
+    const int t = j / D, d = j - t * D;
+    return x[b * D + d] >= thr[t];
+  } else {
+    const int f = j / T;
+    return x[b * D + f] - thr[j] > 0.0f;
+  }
+}
+
+__global__ void __launch_bounds__(256) encode_u8_kernel(const float* __restrict__ x, int B, int D,
+                                                        int T, const float* __restrict__ thr,
+                                                        int fixed, uint8_t* __restrict__ out) {
+  const int64_t F = (int64_t)D * T;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * F) return;
+  const int64_t b = i / F;
+  const int j = (int)(i - b * F);
+  out[i] = (fixed ? encode_bit<true>(x, b, D, T, thr, j) : encode_bit<false>(x, b, D, T, thr, j))
+               ? 1 : 0;
+}
+
+// Packed: a workgroup takes 64 samples (one word) x 64 features; the bits go
+// through an LDS tile and each feature's word is one ballot over the samples.
+// LAYOUT 0: xp [F, nw]; 1: xp [nw, F].
+template <bool FIXED, int LAYOUT>
+__global__ void __launch_bounds__(256) encode_pack_kernel(const float* __restrict__ x, int B, int D,
+                                                          int T, const float* __restrict__ thr,
+                                                          int nw, int ftiles,
+                                                          uint64_t* __restrict__ xp) {
+  __shared__ uint8_t tile[64][68];
+  const int F = D * T;
+  const int w = (int)(blockIdx.x / (uint32_t)ftiles);
+  const int j0 = (int)(blockIdx.x % (uint32_t)ftiles) * 64;
+  const int c = threadIdx.x & 63;
+  for (int r = threadIdx.x >> 6; r < 64; r += 4) {
+    const int b = w * 64 + r, j = j0 + c;
+    tile[r][c] = (b < B && j < F) ? (encode_bit<FIXED>(x, b, D, T, thr, j) ? 1 : 0) : 0;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int q = 0; q < 16; ++q) {
+    const int cc = wave * 16 + q;
+    const uint64_t m = __ballot(tile[lane][cc] != 0);
+    if (lane == 0 && j0 + cc < F) {
+      if constexpr (LAYOUT == 0) xp[(int64_t)(j0 + cc) * nw + w] = m;
+      else xp[(int64_t)w * F + j0 + cc] = m;
+    }
+  }
+}
+
+// Edge bits: per colour channel c the 3x3 responses Sobel-x, Sobel-y,
+// Laplacian (zero padding), channel-major as the grouped convolution
+// (data.py:123-126), then per level t two planes (> t, < -t); output channel
+// (ti*2 + s) * 3C + c*3 + det (data.py:127-131). One thread per pixel of
+// one (sample, colour); the three responses are sums of the nine taps in
+// row-major order.
+__constant__ float c_edge_k[3][9] = {
+    {-1.f, 0.f, 1.f, -2.f, 0.f, 2.f, -1.f, 0.f, 1.f},   // Sobel-x
+    {-1.f, -2.f, -1.f, 0.f, 0.f, 0.f, 1.f, 2.f, 1.f},   // Sobel-y (its transpose)
+    {0.f, 1.f, 0.f, 1.f, -4.f, 1.f, 0.f, 1.f, 0.f}};    // Laplacian
+
+__global__ void __launch_bounds__(256) edge_bits_kernel(const float* __restrict__ x, int N, int C,
+                                                        int H, int W, const float* __restrict__ thr,
+                                                        int T, uint8_t* __restrict__ out) {
+  const int64_t HW = (int64_t)H * W;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)N * C * HW) return;
+  const int64_t nc = i / HW;
+  const int hw = (int)(i - nc * HW);
+  const int n = (int)(nc / C), c = (int)(nc - (int64_t)n * C);
+  const int h = hw / W, w = hw - h * W;
+  const float* xc = x + nc * HW;
+  float v[9];
+#pragma unroll
+  for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+    for (int dx = 0; dx < 3; ++dx) {
+      const int y = h + dy - 1, xx = w + dx - 1;
+      v[dy * 3 + dx] = (y >= 0 && y < H && xx >= 0 && xx < W) ? xc[(int64_t)y * W + xx] : 0.0f;
+    }
+  float r[3];
+#pragma unroll
+  for (int det = 0; det < 3; ++det) {
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 9; ++q) s = fmaf(c_edge_k[det][q], v[q], s);
+    r[det] = s;
+  }
+  const int64_t planes = (int64_t)2 * T * 3 * C;
+  uint8_t* on = out + (int64_t)n * planes * HW + hw;
+  for (int ti = 0; ti < T; ++ti) {
+    const float t = thr[ti];
+#pragma unroll
+    for (int det = 0; det < 3; ++det) {
+      on[((int64_t)(ti * 2) * 3 * C + c * 3 + det) * HW] = r[det] > t ? 1 : 0;
+      on[((int64_t)(ti * 2 + 1) * 3 * C + c * 3 + det) * HW] = r[det] < -t ? 1 : 0;
+    }
+  }
+}
+
+// Learnable thermometer, soft path: the value is the hard bit (the
+// reference's hard + soft - soft.detach(), encoders.py:40-44, without its
+// fp32 rounding); the gradient is that of sigmoid((x - t) * scale).
+// gx [B,F] = sum_i g[b][f*T+i] * ds; gt partials over sample ranges.
+__global__ void __launch_bounds__(256) learned_thermo_bwd_x_kernel(
+    const float* __restrict__ x, int B, int F, int T, const float* __restrict__ thr, float scale,
+    const float* __restrict__ g, float* __restrict__ gx) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * F) return;
+  const int64_t b = i / F;
+  const int f = (int)(i - b * F);
+  const float xv = x[i];
+  float acc = 0.0f;
+  for (int k = 0; k < T; ++k) {
+    const float s = 1.0f / (1.0f + expf(-(xv - thr[f * T + k]) * scale));
+    acc = fmaf(g[b * (int64_t)F * T + f * T + k], s * (1.0f - s) * scale, acc);
+  }
+  gx[i] = acc;
+}
+
+// part [NR][F*T]: range r sums samples [r*spr, (r+1)*spr) in order.
+__global__ void __launch_bounds__(256) learned_thermo_bwd_t_kernel(
+    const float* __restrict__ x, int B, int F, int T, const float* __restrict__ thr, float scale,
+    const float* __restrict__ g, int spr, float* __restrict__ part) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.y;
+  if (j >= F * T) return;
+  const int f = j / T;
+  const float t = thr[j];
+  float acc = 0.0f;
+  const int b1 = min(B, (r + 1) * spr);
+  for (int b = r * spr; b < b1; ++b) {
+    const float s = 1.0f / (1.0f + expf(-(x[(int64_t)b * F + f] - t) * scale));
+    acc = fmaf(g[(int64_t)b * F * T + j], -(s * (1.0f - s) * scale), acc);
+  }
+  part[(int64_t)r * F * T + j] = acc;
+}
+
+__global__ void __launch_bounds__(256) learned_thermo_sum_kernel(const float* __restrict__ part,
+                                                                 int NR, int n,
+                                                                 float* __restrict__ gt) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  float s = 0.0f;
+  for (int r = 0; r < NR; ++r) s += part[(int64_t)r * n + j];
+  gt[j] = s;
+}
+
+static int learned_ranges(int64_t B, int64_t FT) {
+  const int64_t tiles = cdiv(FT, 256);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(B, 1024),
+                                                     cdiv(8 * device_cus(), tiles)));
+}
+
+}  // namespace slg
+
+using namespace slg;
+
+extern "C" {
+
+int slg_encode_thermometer(const float* x, int64_t B, int64_t D, const float* thr, int32_t T,
+                           int32_t learned, int32_t layout, void* out, slg_stream_t stream) {
+  SLG_REQUIRE(thr && out && (x || B == 0), SLG_E_ARG, "encode_thermometer: null pointer");
+  SLG_REQUIRE(B >= 0 && D > 0 && T >= 1 && layout >= 0 && layout <= 2 && D * T < (1LL << 31) &&
+                  B < (1LL << 31) && B * D * T < (1LL << 46),
+              SLG_E_SHAPE, "encode_thermometer: bad sizes");
+  if (B == 0) return 0;
+  hipStream_t st = as_stream(stream);
+  const int64_t F = D * T;
+  if (layout == 2) {
+    hipLaunchKernelGGL(encode_u8_kernel, dim3((unsigned)cdiv(B * F, 256)), dim3(256), 0, st, x,
+                       (int)B, (int)D, T, thr, learned ? 0 : 1, (uint8_t*)out);
+    SLG_LAUNCH_CHECK("encode_thermometer");
+    return 0;
+  }
+  const int64_t nw = cdiv(B, 64), ftiles = cdiv(F, 64);
+  SLG_REQUIRE(nw * ftiles < (1LL << 31), SLG_E_SHAPE, "encode_thermometer: grid too large");
+  const dim3 grid((unsigned)(nw * ftiles));
+  uint64_t* xp = (uint64_t*)out;
+#define SLG_ENC(FX, LY)                                                                      \
+  hipLaunchKernelGGL((encode_pack_kernel<FX, LY>), grid, dim3(256), 0, st, x, (int)B, (int)D, T, \
+                     thr, (int)nw, (int)ftiles, xp)
+  if (!learned) {
+    if (layout == 0) SLG_ENC(true, 0); else SLG_ENC(true, 1);
+  } else {
+    if (layout == 0) SLG_ENC(false, 0); else SLG_ENC(false, 1);
+  }
+#undef SLG_ENC
+  SLG_LAUNCH_CHECK("encode_thermometer");
+  return 0;
+}
+
+int slg_edge_bits(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const float* thr,
+                  int32_t T, uint8_t* out, slg_stream_t stream) {
+  SLG_REQUIRE(thr && ((x && out) || N == 0), SLG_E_ARG, "edge_bits: null pointer");
+  SLG_REQUIRE(N >= 0 && C > 0 && H > 0 && W > 0 && T >= 1 && N * C * H * W < (1LL << 40) &&
+                  H * W < (1LL << 31),
+              SLG_E_SHAPE, "edge_bits: bad sizes");
+  if (N == 0) return 0;
+  const int64_t n = N * C * H * W;
+  hipLaunchKernelGGL(edge_bits_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+                     as_stream(stream), x, (int)N, (int)C, (int)H, (int)W, thr, T, out);
+  SLG_LAUNCH_CHECK("edge_bits");
+  return 0;
+}
+
+int64_t slg_learned_thermo_bwd_workspace(int64_t B, int64_t F, int32_t T) {
+  if (B < 0 || F <= 0 || T < 1) return -1;
+  return (int64_t)learned_ranges(std::max<int64_t>(B, 1), F * T) * F * T;
+}
+
+int slg_learned_thermo_bwd(const float* x, int64_t B, int64_t F, int32_t T, const float* thr,
+                           float scale, const float* g, float* gx, float* gt, float* workspace,
+                           int64_t workspace_floats, slg_stream_t stream) {
+  SLG_REQUIRE(thr && ((x && g) || B == 0) && (workspace || !gt), SLG_E_ARG,
+              "learned_thermo_bwd: null pointer");
+  SLG_REQUIRE(B >= 0 && F > 0 && T >= 1 && F * T < (1LL << 31) && B < (1LL << 31), SLG_E_SHAPE,
+              "learned_thermo_bwd: bad sizes");
+  hipStream_t st = as_stream(stream);
+  const int64_t FT = F * T;
+  if (gx && B > 0) {
+    hipLaunchKernelGGL(learned_thermo_bwd_x_kernel, dim3((unsigned)cdiv(B * F, 256)), dim3(256),
+                       0, st, x, (int)B, (int)F, T, thr, scale, g, gx);
+  }
+  if (gt) {
+    const int NR = learned_ranges(std::max<int64_t>(B, 1), FT);
+    SLG_REQUIRE(workspace_floats >= (int64_t)NR * FT, SLG_E_ARG,
+                "learned_thermo_bwd: workspace of %lld floats, %lld needed",
+                (long long)workspace_floats, (long long)NR * FT);
+    const int spr = (int)cdiv(std::max<int64_t>(B, 1), NR);
+    if (B > 0)
+      hipLaunchKernelGGL(learned_thermo_bwd_t_kernel, dim3((unsigned)cdiv(FT, 256), (unsigned)NR),
+                         dim3(256), 0, st, x, (int)B, (int)F, T, thr, scale, g, spr, workspace);
+    hipLaunchKernelGGL(learned_thermo_sum_kernel, dim3((unsigned)cdiv(FT, 256)), dim3(256), 0, st,
+                       workspace, B > 0 ? NR : 0, (int)FT, gt);
+  }
+  SLG_LAUNCH_CHECK("learned_thermo_bwd");
+  return 0;
+}
+
+}  // extern "C"

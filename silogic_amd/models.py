@@ -141,6 +141,27 @@ class LogicNet(nn.Module):
         return _hard_fc_stack(self.layers, x, kind, x.shape[0], x.shape[1],
                               self.head.num_classes, self.wire_r)
 
+    @torch.no_grad()
+    def forward_hard_packed(self, xp, B, word_major=False):
+        """``forward_hard`` on packed input for ``B`` samples: ``[in_dim, nw]``
+        rows, or ``[nw, in_dim]`` words with ``word_major`` (the layouts of
+        ``ops.pack_bits`` and ``data.binarize_packed``): class counts."""
+        ops.require_gpu(xp)
+        if word_major:
+            if xp.dim() != 2 or xp.shape[0] != ops.n_words(B):
+                raise ValueError("forward_hard_packed: word-major input must be [nw, in_dim]")
+            in_dim = xp.shape[1]
+            if any(layer.is_lut for layer in self.layers) or not ops.fc_hard_net_supported(
+                    in_dim, [l.out_dim for l in self.layers], self.head.num_classes):
+                xp, kind = xp.t().contiguous(), ops.PACKED     # the per-layer kernels take rows
+            else:
+                xp, kind = xp.contiguous(), ops.PACKED_WORD_MAJOR
+        else:
+            xp, kind = ops._words_for(xp, B, "forward_hard_packed"), ops.PACKED
+            in_dim = xp.shape[0]
+        return _hard_fc_stack(self.layers, xp, kind, B, in_dim, self.head.num_classes,
+                              self.wire_r)
+
     def num_gates(self):
         return self.width * self.depth
 
@@ -229,6 +250,18 @@ class LogicConvNet(nn.Module):
         ops.require_gpu(x)
         B, C, H, W = x.shape
         xp = ops.pack_bits(x.reshape(B, -1))                  # [C*H*W, nw] = [C,H,W,nw]
+        return self.forward_hard_packed(xp, B, (C, H, W))
+
+    @torch.no_grad()
+    def forward_hard_packed(self, xp, B, chw):
+        """``forward_hard`` on packed input ``[C*H*W, nw]`` (the layout of
+        ``ops.pack_bits`` and ``data.binarize_packed`` for images, channel-
+        major) for ``B`` samples of shape ``chw``: class counts ``[B, C]``."""
+        ops.require_gpu(xp)
+        C, H, W = chw
+        xp = ops._words_for(xp, B, "forward_hard_packed")
+        if xp.shape[0] != C * H * W:
+            raise ValueError("forward_hard_packed: %d rows for C*H*W = %d" % (xp.shape[0], C * H * W))
         for conv in self._convs():
             x_in = xp
             xp = conv.packed_forward(xp, (C, H, W), pool=True)
