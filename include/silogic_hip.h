@@ -198,14 +198,17 @@ int slg_fc_lut_hard_prep(const int32_t* cand, const float* conn, int64_t OUT, in
                          slg_stream_t stream);
 
 /* Input encoders (the step before the gate layers). Thermometer codes of
- * x [B,D] fp32 with T thresholds: learned = 0 is binarize / binarize_spatial
+ * x [B,D] (dtype 0: fp32; 1: uint8 pixel bytes taken as x / 255 in fp32, the
+ * value the reference's loaders compute, data.py:49-57) with T thresholds:
+ * learned = 0 is binarize / binarize_spatial
  * (silogic/data.py:23-40, 75-89): feature t*D + d = (x[b][d] >= thr[t]);
  * learned = 1 is LearnedThermometerEncoder.forward_hard (encoders.py:46-49):
  * feature f*T + i = (x[b][f] - thr[f*T + i] > 0). layout 2: uint8 [B, D*T]
  * (the reference's output); 0: packed [D*T, nw] (for images also the conv
  * layout [C*T, H*W, nw]); 1: packed word-major [nw, D*T]. */
-int slg_encode_thermometer(const float* x, int64_t B, int64_t D, const float* thr, int32_t T,
-                           int32_t learned, int32_t layout, void* out, slg_stream_t stream);
+int slg_encode_thermometer(const void* x, int32_t dtype, int64_t B, int64_t D, const float* thr,
+                           int32_t T, int32_t learned, int32_t layout, void* out,
+                           slg_stream_t stream);
 /* edge_bits (data.py:102-131): x [N,C,H,W] -> uint8 [N, C*3*2*T, H, W], per
  * colour the 3x3 Sobel-x, Sobel-y and Laplacian responses (zero padding),
  * each thresholded at > t and < -t; channel (ti*2 + s)*3C + c*3 + det. */

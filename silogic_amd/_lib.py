@@ -55,7 +55,7 @@ SIGNATURES = {
     "slg_fc_lut_soft_bwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P,
                                       _P, _P, _I64, _P]),
     "slg_fc_lut_hard_prep": (C.c_int, [_P, _P, _I64, _I32, _I32, _I64, _P, _P, _P, _P]),
-    "slg_encode_thermometer": (C.c_int, [_P, _I64, _I64, _P, _I32, _I32, _I32, _P, _P]),
+    "slg_encode_thermometer": (C.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I32, _I32, _P, _P]),
     "slg_edge_bits": (C.c_int, [_P, _I64, _I64, _I64, _I64, _P, _I32, _P, _P]),
     "slg_learned_thermo_bwd_workspace": (C.c_int64, [_I64, _I64, _I32]),
     "slg_learned_thermo_bwd": (C.c_int, [_P, _I64, _I64, _I32, _P, _F32, _P, _P, _P, _P, _I64,

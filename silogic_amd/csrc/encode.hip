@@ -16,21 +16,30 @@
 
 namespace slg {
 
+// Input value: fp32, or a pixel byte taken as x / 255 in fp32 (the value
+// the reference's loaders compute, data.py:49-57, before encoding).
+template <typename TX>
+__device__ inline float in_val(const TX* __restrict__ x, int64_t i) {
+  if constexpr (sizeof(TX) == 1) return (float)x[i] / 255.0f;
+  else return x[i];
+}
+
 // Bit of feature j of sample b. FIXED: j = t*D + d, x >= thr[t]; else
 // (learned): j = f*T + i, x[f] - thr[f*T + i] > 0.
-template <bool FIXED>
-__device__ inline bool encode_bit(const float* __restrict__ x, int64_t b, int D, int T,
+template <bool FIXED, typename TX>
+__device__ inline bool encode_bit(const TX* __restrict__ x, int64_t b, int D, int T,
                                   const float* __restrict__ thr, int j) {
   if constexpr (FIXED) {
     const int t = j / D, d = j - t * D;
-    return x[b * D + d] >= thr[t];
+    return in_val(x, b * D + d) >= thr[t];
   } else {
     const int f = j / T;
-    return x[b * D + f] - thr[j] > 0.0f;
+    return in_val(x, b * D + f) - thr[j] > 0.0f;
   }
 }
 
-__global__ void __launch_bounds__(256) encode_u8_kernel(const float* __restrict__ x, int B, int D,
+template <typename TX>
+__global__ void __launch_bounds__(256) encode_u8_kernel(const TX* __restrict__ x, int B, int D,
                                                         int T, const float* __restrict__ thr,
                                                         int fixed, uint8_t* __restrict__ out) {
   const int64_t F = (int64_t)D * T;
@@ -45,8 +54,8 @@ __global__ void __launch_bounds__(256) encode_u8_kernel(const float* __restrict_
 // Packed: a workgroup takes 64 samples (one word) x 64 features; the bits go
 // through an LDS tile and each feature's word is one ballot over the samples.
 // LAYOUT 0: xp [F, nw]; 1: xp [nw, F].
-template <bool FIXED, int LAYOUT>
-__global__ void __launch_bounds__(256) encode_pack_kernel(const float* __restrict__ x, int B, int D,
+template <bool FIXED, int LAYOUT, typename TX>
+__global__ void __launch_bounds__(256) encode_pack_kernel(const TX* __restrict__ x, int B, int D,
                                                           int T, const float* __restrict__ thr,
                                                           int nw, int ftiles,
                                                           uint64_t* __restrict__ xp) {
@@ -175,24 +184,13 @@ static int learned_ranges(int64_t B, int64_t FT) {
                                                      cdiv(8 * device_cus(), tiles)));
 }
 
-}  // namespace slg
-
-using namespace slg;
-
-extern "C" {
-
-int slg_encode_thermometer(const float* x, int64_t B, int64_t D, const float* thr, int32_t T,
-                           int32_t learned, int32_t layout, void* out, slg_stream_t stream) {
-  SLG_REQUIRE(thr && out && (x || B == 0), SLG_E_ARG, "encode_thermometer: null pointer");
-  SLG_REQUIRE(B >= 0 && D > 0 && T >= 1 && layout >= 0 && layout <= 2 && D * T < (1LL << 31) &&
-                  B < (1LL << 31) && B * D * T < (1LL << 46),
-              SLG_E_SHAPE, "encode_thermometer: bad sizes");
-  if (B == 0) return 0;
-  hipStream_t st = as_stream(stream);
+template <typename TX>
+static int encode_thermo_t(const TX* x, int64_t B, int64_t D, const float* thr, int T,
+                           int learned, int layout, void* out, hipStream_t st) {
   const int64_t F = D * T;
   if (layout == 2) {
-    hipLaunchKernelGGL(encode_u8_kernel, dim3((unsigned)cdiv(B * F, 256)), dim3(256), 0, st, x,
-                       (int)B, (int)D, T, thr, learned ? 0 : 1, (uint8_t*)out);
+    hipLaunchKernelGGL(encode_u8_kernel<TX>, dim3((unsigned)cdiv(B * F, 256)), dim3(256), 0, st,
+                       x, (int)B, (int)D, T, thr, learned ? 0 : 1, (uint8_t*)out);
     SLG_LAUNCH_CHECK("encode_thermometer");
     return 0;
   }
@@ -200,9 +198,9 @@ int slg_encode_thermometer(const float* x, int64_t B, int64_t D, const float* th
   SLG_REQUIRE(nw * ftiles < (1LL << 31), SLG_E_SHAPE, "encode_thermometer: grid too large");
   const dim3 grid((unsigned)(nw * ftiles));
   uint64_t* xp = (uint64_t*)out;
-#define SLG_ENC(FX, LY)                                                                      \
-  hipLaunchKernelGGL((encode_pack_kernel<FX, LY>), grid, dim3(256), 0, st, x, (int)B, (int)D, T, \
-                     thr, (int)nw, (int)ftiles, xp)
+#define SLG_ENC(FX, LY)                                                                    \
+  hipLaunchKernelGGL((encode_pack_kernel<FX, LY, TX>), grid, dim3(256), 0, st, x, (int)B,    \
+                     (int)D, T, thr, (int)nw, (int)ftiles, xp)
   if (!learned) {
     if (layout == 0) SLG_ENC(true, 0); else SLG_ENC(true, 1);
   } else {
@@ -211,6 +209,25 @@ int slg_encode_thermometer(const float* x, int64_t B, int64_t D, const float* th
 #undef SLG_ENC
   SLG_LAUNCH_CHECK("encode_thermometer");
   return 0;
+}
+
+}  // namespace slg
+
+using namespace slg;
+
+extern "C" {
+
+int slg_encode_thermometer(const void* x, int32_t dtype, int64_t B, int64_t D, const float* thr,
+                           int32_t T, int32_t learned, int32_t layout, void* out,
+                           slg_stream_t stream) {
+  SLG_REQUIRE(thr && out && (x || B == 0), SLG_E_ARG, "encode_thermometer: null pointer");
+  SLG_REQUIRE(B >= 0 && D > 0 && T >= 1 && layout >= 0 && layout <= 2 && (dtype == 0 || dtype == 1) &&
+                  D * T < (1LL << 31) && B < (1LL << 31) && B * D * T < (1LL << 46),
+              SLG_E_SHAPE, "encode_thermometer: bad sizes");
+  if (B == 0) return 0;
+  hipStream_t st = as_stream(stream);
+  return dtype == 1 ? encode_thermo_t((const uint8_t*)x, B, D, thr, T, learned, layout, out, st)
+                    : encode_thermo_t((const float*)x, B, D, thr, T, learned, layout, out, st);
 }
 
 int slg_edge_bits(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const float* thr,

@@ -25,15 +25,17 @@ def _thr(thresholds, device):
 
 
 def _encode(x, thr, learned, layout, T):
+    """x [B, D] fp32, or uint8 pixel bytes (value x / 255)."""
     B, D = x.shape
+    dtype = 1 if x.dtype == torch.uint8 else 0
     if layout == 2:
         out = torch.empty((B, D * T), device=x.device, dtype=torch.uint8)
     else:
         nw = ops.n_words(B)
         shape = (D * T, nw) if layout == 0 else (nw, D * T)
         out = torch.empty(shape, device=x.device, dtype=torch.int64)
-    _lib.call("slg_encode_thermometer", ops._p(x), B, D, ops._p(thr), T, int(learned), layout,
-              ops._p(out), ops._stream(x))
+    _lib.call("slg_encode_thermometer", ops._p(x), dtype, B, D, ops._p(thr), T, int(learned),
+              layout, ops._p(out), ops._stream(x))
     return out
 
 
@@ -61,9 +63,12 @@ def binarize_packed(x, thresholds, word_major=False):
     """The bits of :func:`binarize` packed 64 samples per word: ``[T*D, nw]``
     (``word_major``: ``[nw, T*D]``, the fused FC network's input). For image
     input the rows are the conv layout ``[C*T, H*W, nw]`` of
-    :func:`binarize_spatial`."""
+    :func:`binarize_spatial`. ``x`` may be fp32 in [0, 1] or the uint8 pixel
+    bytes of a dataset (value ``x / 255`` as the reference's loaders compute
+    it, data.py:49-57), read directly."""
     ops.require_gpu(x)
-    xf = ops._as_f32(x.reshape(x.shape[0], -1))
+    x2 = x.reshape(x.shape[0], -1)
+    xf = x2.contiguous() if x2.dtype == torch.uint8 else ops._as_f32(x2)
     thr = _thr(thresholds, x.device)
     return _encode(xf, thr, False, 1 if word_major else 0, thr.numel())
 

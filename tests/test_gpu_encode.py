@@ -91,3 +91,17 @@ def test_packed_encoding_feeds_the_hard_networks():
     want_c = conv.forward_hard(sl.binarize_spatial(pix, sl.CIFAR3_THRESH))
     got_c = conv.forward_hard_packed(sl.binarize_packed(pix, sl.CIFAR3_THRESH), 70, (9, 16, 16))
     assert torch.equal(got_c, want_c)
+
+
+def test_pixel_bytes_encode_as_the_reference_loaders_scale_them():
+    """uint8 pixel input is taken as x / 255 in fp32 (data.py:49-57) and
+    packed directly: same words as encoding the scaled floats."""
+    g = torch.Generator().manual_seed(6)
+    pix = torch.randint(0, 256, (130, 784), generator=g, dtype=torch.uint8)
+    pix[0, :256] = torch.arange(256, dtype=torch.uint8)            # every byte value
+    thr = sl.SEVEN_THRESH
+    ref = encode_ref.binarize(pix.float() / 255.0, thr)
+    want = packed_ref.pack_bits(ref.numpy())
+    np.testing.assert_array_equal(sl.binarize_packed(pix.to(DEV), thr).cpu().numpy(), want)
+    np.testing.assert_array_equal(
+        sl.binarize_packed(pix.to(DEV), thr, word_major=True).cpu().numpy(), want.T)
