@@ -51,31 +51,110 @@ __global__ void __launch_bounds__(256) encode_u8_kernel(const TX* __restrict__ x
                ? 1 : 0;
 }
 
-// Packed: a workgroup takes 64 samples (one word) x 64 features; the bits go
-// through an LDS tile and each feature's word is one ballot over the samples.
-// LAYOUT 0: xp [F, nw]; 1: xp [nw, F].
-template <bool FIXED, int LAYOUT, typename TX>
+// Smallest byte k in [0, 256] whose value k / 255 passes the test against
+// threshold t (256: none). The test is monotone in the byte (a correctly
+// rounded k / 255 does not decrease with k), so byte >= k is the same bit
+// as the fp32 test on byte / 255.
+template <bool FIXED>
+__device__ inline int byte_cut(float t) {
+  int lo = 0, hi = 256;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const float v = (float)mid / 255.0f;
+    const bool pass = FIXED ? (v >= t) : (v - t > 0.0f);
+    if (pass) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+template <bool FIXED, typename TX>
+__device__ inline bool pass_bit(TX v, float th, int cut) {
+  if constexpr (sizeof(TX) == 1) return (int)v >= cut;
+  else return FIXED ? (v >= th) : (v - th > 0.0f);
+}
+
+// Packed: a lane takes V consecutive features and builds their words over
+// the 64 samples of one word in registers (no LDS, no ballot); the four
+// waves of a workgroup take four consecutive words. V = 4 reads the four
+// features of a row as one vector (fixed thresholds, D % 4 == 0, aligned
+// input). LAYOUT 0: xp [F, nw]; 1: xp [nw, F].
+template <bool FIXED, int LAYOUT, typename TX, int V>
 __global__ void __launch_bounds__(256) encode_pack_kernel(const TX* __restrict__ x, int B, int D,
                                                           int T, const float* __restrict__ thr,
                                                           int nw, int ftiles,
                                                           uint64_t* __restrict__ xp) {
-  __shared__ uint8_t tile[64][68];
+  const int lane = threadIdx.x & 63;
+  const int w = (int)(blockIdx.x / (uint32_t)ftiles) * 4 + (int)(threadIdx.x >> 6);
   const int F = D * T;
-  const int w = (int)(blockIdx.x / (uint32_t)ftiles);
-  const int j0 = (int)(blockIdx.x % (uint32_t)ftiles) * 64;
-  const int c = threadIdx.x & 63;
-  for (int r = threadIdx.x >> 6; r < 64; r += 4) {
-    const int b = w * 64 + r, j = j0 + c;
-    tile[r][c] = (b < B && j < F) ? (encode_bit<FIXED>(x, b, D, T, thr, j) ? 1 : 0) : 0;
+  const int j0 = (int)(blockIdx.x % (uint32_t)ftiles) * 64 * V + lane * V;
+  if (w >= nw || j0 >= F) return;                       // no barriers below
+  int src[V], cut[V];
+  float th[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int j = min(j0 + v, F - 1);                    // tail lanes: stores are guarded
+    if constexpr (FIXED) {
+      const int t = j / D;
+      src[v] = j - t * D;
+      th[v] = thr[t];
+    } else {
+      src[v] = j / T;
+      th[v] = thr[j];
+    }
+    cut[v] = sizeof(TX) == 1 ? byte_cut<FIXED>(th[v]) : 0;
   }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int q = 0; q < 16; ++q) {
-    const int cc = wave * 16 + q;
-    const uint64_t m = __ballot(tile[lane][cc] != 0);
-    if (lane == 0 && j0 + cc < F) {
-      if constexpr (LAYOUT == 0) xp[(int64_t)(j0 + cc) * nw + w] = m;
-      else xp[(int64_t)w * F + j0 + cc] = m;
+  const int nr = min(64, B - w * 64);                    // samples in this word (wave-uniform)
+  const TX* xr = x + (int64_t)w * 64 * D;
+  uint64_t word[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) word[v] = 0;
+  auto chunk = [&](int c) {
+    uint32_t m[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) m[v] = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      {
+        // rows past the batch read the last row (no branch, so every load
+        // can be in flight at once); their bits are cleared below
+        const TX* row = xr + (int64_t)min(c + i, nr - 1) * D;
+        if constexpr (V == 4) {
+          if constexpr (sizeof(TX) == 1) {
+            const uint32_t q = *(const uint32_t*)(row + src[0]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              m[v] |= (pass_bit<FIXED>((uint8_t)(q >> (8 * v)), th[v], cut[v]) ? 1u : 0u) << i;
+          } else {
+            const float4 q = *(const float4*)(row + src[0]);
+            const float qv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              m[v] |= (pass_bit<FIXED>(qv[v], th[v], cut[v]) ? 1u : 0u) << i;
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            m[v] |= (pass_bit<FIXED>(row[src[v]], th[v], cut[v]) ? 1u : 0u) << i;
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) word[v] |= (uint64_t)m[v] << c;
+  };
+  if constexpr (sizeof(TX) == 1) {
+    // bytes: all 64 rows' loads in flight at once (one register per load)
+    chunk(0); chunk(16); chunk(32); chunk(48);
+  } else {
+#pragma unroll 1
+    for (int c = 0; c < 64; c += 16) chunk(c);
+  }
+  const uint64_t valid = nr == 64 ? ~0ull : (1ull << nr) - 1;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    word[v] &= valid;
+    if (j0 + v < F) {
+      if constexpr (LAYOUT == 0) xp[(int64_t)(j0 + v) * nw + w] = word[v];
+      else xp[(int64_t)w * F + j0 + v] = word[v];
     }
   }
 }
@@ -194,17 +273,21 @@ static int encode_thermo_t(const TX* x, int64_t B, int64_t D, const float* thr, 
     SLG_LAUNCH_CHECK("encode_thermometer");
     return 0;
   }
-  const int64_t nw = cdiv(B, 64), ftiles = cdiv(F, 64);
-  SLG_REQUIRE(nw * ftiles < (1LL << 31), SLG_E_SHAPE, "encode_thermometer: grid too large");
-  const dim3 grid((unsigned)(nw * ftiles));
+  const bool vec = !learned && D % 4 == 0 && (uintptr_t)x % (4 * sizeof(TX)) == 0;
+  const int64_t nw = cdiv(B, 64), ftiles = cdiv(F, vec ? 256 : 64);
+  SLG_REQUIRE(cdiv(nw, 4) * ftiles < (1LL << 31), SLG_E_SHAPE,
+              "encode_thermometer: grid too large");
+  const dim3 grid((unsigned)(cdiv(nw, 4) * ftiles));
   uint64_t* xp = (uint64_t*)out;
-#define SLG_ENC(FX, LY)                                                                    \
-  hipLaunchKernelGGL((encode_pack_kernel<FX, LY, TX>), grid, dim3(256), 0, st, x, (int)B,    \
+#define SLG_ENC(FX, LY, V)                                                                 \
+  hipLaunchKernelGGL((encode_pack_kernel<FX, LY, TX, V>), grid, dim3(256), 0, st, x, (int)B, \
                      (int)D, T, thr, (int)nw, (int)ftiles, xp)
-  if (!learned) {
-    if (layout == 0) SLG_ENC(true, 0); else SLG_ENC(true, 1);
+  if (vec) {
+    if (layout == 0) SLG_ENC(true, 0, 4); else SLG_ENC(true, 1, 4);
+  } else if (!learned) {
+    if (layout == 0) SLG_ENC(true, 0, 1); else SLG_ENC(true, 1, 1);
   } else {
-    if (layout == 0) SLG_ENC(false, 0); else SLG_ENC(false, 1);
+    if (layout == 0) SLG_ENC(false, 0, 1); else SLG_ENC(false, 1, 1);
   }
 #undef SLG_ENC
   SLG_LAUNCH_CHECK("encode_thermometer");

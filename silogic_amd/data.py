@@ -17,11 +17,25 @@ FIVE_THRESH = [1 / 6, 2 / 6, 3 / 6, 4 / 6, 5 / 6]
 EDGE_THRESH = [0.12, 0.25]
 
 
+_THR_CACHE = {}
+
+
 def _thr(thresholds, device):
-    t = torch.as_tensor(list(thresholds), dtype=torch.float32)
-    if t.dim() != 1 or t.numel() == 0:
-        raise ValueError("thresholds: a non-empty list of floats")
-    return t.to(device)
+    """Thresholds as an fp32 device tensor; a list's copy is kept per device
+    so repeated calls issue no host-to-device copy."""
+    if isinstance(thresholds, torch.Tensor):
+        t = thresholds.detach().reshape(-1).to(device=device, dtype=torch.float32)
+        if t.numel() == 0:
+            raise ValueError("thresholds: a non-empty list of floats")
+        return t.contiguous()
+    key = (tuple(float(v) for v in thresholds), str(device))
+    t = _THR_CACHE.get(key)
+    if t is None:
+        if not key[0]:
+            raise ValueError("thresholds: a non-empty list of floats")
+        t = torch.tensor(key[0], dtype=torch.float32).to(device)
+        _THR_CACHE[key] = t
+    return t
 
 
 def _encode(x, thr, learned, layout, T):

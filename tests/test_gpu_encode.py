@@ -105,3 +105,26 @@ def test_pixel_bytes_encode_as_the_reference_loaders_scale_them():
     np.testing.assert_array_equal(sl.binarize_packed(pix.to(DEV), thr).cpu().numpy(), want)
     np.testing.assert_array_equal(
         sl.binarize_packed(pix.to(DEV), thr, word_major=True).cpu().numpy(), want.T)
+
+
+def test_pixel_bytes_at_threshold_edges_and_unaligned_input():
+    """Thresholds at a byte's exact value (51 / 255 == 0.2 in fp32), at 0
+    and 1 and above 1; input whose address is not 4-byte aligned takes the
+    one-feature-per-lane path and gives the same words."""
+    g = torch.Generator().manual_seed(8)
+    pix = torch.randint(0, 256, (67, 784), generator=g, dtype=torch.uint8)
+    pix[0, :256] = torch.arange(256, dtype=torch.uint8)
+    thr = [0.0, 51 / 255, 1.0, 1.5]
+    want = packed_ref.pack_bits(encode_ref.binarize(pix.float() / 255.0, thr).numpy())
+    buf = torch.empty(pix.numel() + 1, dtype=torch.uint8, device=DEV)
+    buf[1:] = pix.reshape(-1).to(DEV)
+    shifted = buf[1:].view(67, 784)
+    assert shifted.data_ptr() % 4 != 0
+    for x in (pix.to(DEV), shifted):
+        np.testing.assert_array_equal(sl.binarize_packed(x, thr).cpu().numpy(), want)
+        np.testing.assert_array_equal(sl.binarize_packed(x, thr, word_major=True).cpu().numpy(),
+                                      want.T)
+    # the equality case: byte 51 passes 51 / 255, byte 50 does not
+    bits = encode_ref.binarize(pix[:1].float() / 255.0, thr)[0]
+    assert bits[784 + 51] == 1 and bits[784 + 50] == 0 and bits[2 * 784 + 255] == 1
+    assert bits[3 * 784:].sum() == 0 and bits[:784].sum() == 784
