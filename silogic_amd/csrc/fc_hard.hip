@@ -307,21 +307,143 @@ __device__ inline void keep_inputs(WT* lds, int cur, int nxt, int keep) {
   }
 }
 
+// Per-class sample counts without a bit transpose, one 32-sample half of
+// the words at a time (32-bit slices keep the register count low). A wave
+// takes 1024 words of one class (16 per lane, lane-contiguous LDS reads): a
+// carry-save adder tree (Harley-Seal) turns each lane's 16 half-words into
+// a bit-sliced 5-bit count per sample (slice k holds bit k of every
+// sample's count), then six butterfly rounds add the lanes' bit-sliced
+// counts (ripple-carry adders on the slices), after
+// which every lane holds the class total of the half's 32 samples in 11
+// slices (the exchanges are DPP moves and permlane swaps, no LDS). Words
+// past the class read 0; every lane of the wave must be active.
+__device__ inline uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) { return (a & b) | (c & (a | b)); }
+
+__device__ inline void csa(uint32_t& h, uint32_t& l, uint32_t a, uint32_t b, uint32_t c) {
+  h = maj3(a, b, c);
+  l = a ^ b ^ c;
+}
+
+constexpr int kGsWordsPerLane = 16, kGsChunk = 64 * kGsWordsPerLane;
+
+// Bit-sliced add x += y of NB-bit counts (x[NB] is 0 on entry and takes the
+// carry out): a ripple of full adders, slice by slice.
+template <int NB>
+__device__ __forceinline__ void add_slices(uint32_t (&x)[11], const uint32_t (&y)[11]) {
+  uint32_t carry = 0;
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const uint32_t t = x[k] ^ y[k] ^ carry;
+    carry = maj3(x[k], y[k], carry);
+    x[k] = t;
+  }
+  x[NB] = carry;
+}
+
+// Butterfly step within 16-lane rows by a DPP lane pattern: quad_perm
+// [1,0,3,2] (lane ^ 1), [2,3,0,1] (lane ^ 2), then row_half_mirror (lane i of
+// 8 with 7 - i: joins the two quads' totals) and row_mirror (i of 16 with
+// 15 - i: joins the two 8-lane totals).
+template <int NB, int CTRL>
+__device__ __forceinline__ void add_dpp(uint32_t (&x)[11]) {
+  uint32_t y[11];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) y[k] = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[k], CTRL, 0xF, 0xF, false);
+  add_slices<NB>(x, y);
+}
+
+// Butterfly step across 16- or 32-lane halves: v_permlane16/32_swap of a
+// value with itself returns, in every lane, the lane's own value and that of
+// lane ^ 16 (^ 32) as the pair (a, b), so the sum is a + b.
+template <int NB, bool P32>
+__device__ __forceinline__ void add_swap(uint32_t (&x)[11]) {
+  uint32_t a[11], b[11];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    if constexpr (P32) {
+      const auto r = __builtin_amdgcn_permlane32_swap(x[k], x[k], false, false);
+      a[k] = r[0];
+      b[k] = r[1];
+    } else {
+      const auto r = __builtin_amdgcn_permlane16_swap(x[k], x[k], false, false);
+      a[k] = r[0];
+      b[k] = r[1];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NB; ++k) x[k] = a[k];
+  x[NB] = 0;
+  add_slices<NB>(x, b);
+}
+
+// Count of sample `sh` of the half (0..31) over words [q*1024, q*1024 + 1024)
+// of the class; `cls32` are the class's words as 32-bit halves, `stride`
+// halves per word (2 for 64-bit words, 1 for 32-bit), `half` which one.
+__device__ __forceinline__ int class_chunk_count32(const uint32_t* cls32, int stride, int half, int G, int q,
+                                          int lane, int sh) {
+  uint32_t w[kGsWordsPerLane];
+#pragma unroll
+  for (int j = 0; j < kGsWordsPerLane; ++j) {
+    const int g = q * kGsChunk + j * 64 + lane;
+    w[j] = g < G ? cls32[g * stride + half] : 0u;
+  }
+  uint32_t x[11];
+#pragma unroll
+  for (int k = 0; k < 11; ++k) x[k] = 0;
+  {
+    uint32_t twosA, twosB, foursA, foursB, eightsA, eightsB;
+    uint32_t& ones = x[0];
+    uint32_t& twos = x[1];
+    uint32_t& fours = x[2];
+    uint32_t& eights = x[3];
+    csa(twosA, ones, ones, w[0], w[1]);
+    csa(twosB, ones, ones, w[2], w[3]);
+    csa(foursA, twos, twos, twosA, twosB);
+    csa(twosA, ones, ones, w[4], w[5]);
+    csa(twosB, ones, ones, w[6], w[7]);
+    csa(foursB, twos, twos, twosA, twosB);
+    csa(eightsA, fours, fours, foursA, foursB);
+    csa(twosA, ones, ones, w[8], w[9]);
+    csa(twosB, ones, ones, w[10], w[11]);
+    csa(foursA, twos, twos, twosA, twosB);
+    csa(twosA, ones, ones, w[12], w[13]);
+    csa(twosB, ones, ones, w[14], w[15]);
+    csa(foursB, twos, twos, twosA, twosB);
+    csa(eightsB, fours, fours, foursA, foursB);
+    csa(x[4], eights, eights, eightsA, eightsB);
+  }
+  // lanes' counts: 5 bits (<= 16) grow one bit per round to 11 (<= 1024)
+  add_dpp<5, 0xB1>(x);    // quad_perm [1,0,3,2]
+  add_dpp<6, 0x4E>(x);    // quad_perm [2,3,0,1]
+  add_dpp<7, 0x141>(x);   // row_half_mirror
+  add_dpp<8, 0x140>(x);   // row_mirror
+  add_swap<9, false>(x);  // lane ^ 16
+  add_swap<10, true>(x);  // lane ^ 32
+  int cnt = 0;
+#pragma unroll
+  for (int k = 0; k < 11; ++k) cnt |= (int)((x[k] >> sh) & 1u) << k;
+  return cnt;
+}
+
 // Per-class popcounts of a tile: cnt [C][64] must be zero on entry.
 template <typename WT>
-__device__ inline void groupsum_tile(const WT* cur, int W, int C, int* cnt, int b0, int B,
+__device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int* cnt, int b0, int B,
                                      float* __restrict__ logits) {
   constexpr int SPW = (int)sizeof(WT) * 8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nwaves = kNetThreads >> 6;
   const int G = W / C;
-  const int chunks = (G + 63) / 64;
+  const int chunks = (G + kGsChunk - 1) / kGsChunk;
   for (int task = wave; task < C * chunks; task += nwaves) {
-    const int c = task / chunks, j0 = (task % chunks) * 64;
-    uint64_t v = (j0 + lane < G) ? (uint64_t)cur[c * G + j0 + lane] : 0ull;
-    v = transpose64(v, lane);
-    const int pc = __popcll(v);
-    if (pc) atomicAdd(&cnt[c * 64 + lane], pc);
+    const int c = task / chunks, q = task % chunks;
+    const uint32_t* cls32 = reinterpret_cast<const uint32_t*>(cur + c * G);
+    int n = class_chunk_count32(cls32, SPW / 32, 0, G, q, lane, lane & 31);
+    if constexpr (SPW == 64) {
+      const int nh = class_chunk_count32(cls32, 2, 1, G, q, lane, lane & 31);
+      n = lane < 32 ? n : nh;
+    }
+    if (chunks == 1) cnt[c * 64 + lane] = n;
+    else if (n) atomicAdd(&cnt[c * 64 + lane], n);
   }
   __syncthreads();
   for (int i = threadIdx.x; i < SPW * C; i += kNetThreads) {
@@ -487,6 +609,11 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
       issue_chunk(val0, r, voff0, rowb, c);
       fold_chunk(nword, val0, c);
     }
+    // every chunk is folded: the chunk registers hold nothing the next tile
+    // reads before writing, but the layer loop's control flow does not show
+    // it; constants here let the GroupSum below have those registers
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) val0[j] = val1[j] = (IT)0;
     groupsum_tile<uint64_t>(lds + cur, cur_w, d.C, cnt, tile * 64, B, logits);
     __syncthreads();
     word = fv ? nword : 0ull;
