@@ -208,14 +208,15 @@ __global__ void __launch_bounds__(256) fc_hard_layer_kernel(const uint64_t* __re
 // layer each thread owns outputs tid, tid+1024, ...: it holds their codes in
 // registers (prefetched one layer ahead: codes do not depend on the data),
 // reads its two operand words from LDS and writes the result word. The
-// GroupSum counts come from 64x64 bit transposes + popcount per class.
+// GroupSum counts are bit-sliced sums (carry-save adders and lane
+// butterflies) per class.
 constexpr int kMaxLayers = 16;
 constexpr int kNetThreads = 1024;
 struct NetDesc {
   const uint32_t* codes[kMaxLayers];  // compact codes, one word per output
   int width[kMaxLayers];
   int n_layers, in0, C, wire_r;
-  int maxw;  // words per activation buffer: the widest layer + kGuard
+  int maxw;  // words per activation buffer: MAXO * 1024 (every row of every layer)
 };
 
 // Codes of this thread's outputs o = tid + j*1024 of a W-wide layer, read
@@ -253,47 +254,37 @@ __device__ inline WT gate_compact(WT a, WT b, uint32_t c) {
 
 // One layer on the LDS column: lds[nxt + o] = gate_o(lds[cur + a_o], lds[cur + b_o])
 // for this thread's outputs o = tid + j*1024, in groups of GRP outputs: all
-// operand reads of a group are issued before its results are computed
-// (operand indices are clamped to the layer's input width), so the LDS
-// latency of a thread's gates overlaps; the group's gate math runs between
-// its reads and its writes, with no LDS access in between. Lanes of the last,
-// partial row past W write to a per-lane guard word after the layer's
-// outputs (kGuard words follow each buffer) instead of being masked off.
-constexpr int kGuard = 64;
-
+// operand reads of a group are issued before its results are computed, so
+// the LDS latency of a thread's gates overlaps; the group's gate math runs
+// between its reads and its writes, with no LDS access in between. Each
+// buffer holds MAXO*1024 words, so every row of a group is computed and
+// written without a mask: rows past the layer have code 0 (read past the
+// codes' buffer resource) and write their word into the buffer's unused
+// tail. Operand indices are below the layer's input width by construction
+// (the prep kernel clamps them). Groups wholly past the layer are skipped.
 template <typename WT, int MAXO, int GRP>
-__device__ inline void layer_step(WT* lds, int cur, int nxt, int W, int in_w,
-                                  const uint32_t (&cb)[MAXO]) {
+__device__ __forceinline__ void layer_step(WT* lds, int cur, int nxt, int W,
+                                           const uint32_t (&cb)[MAXO]) {
   static_assert(MAXO % GRP == 0, "groups must tile MAXO");
   const int rows = (W + kNetThreads - 1) / kNetThreads;
-  const int nfull = W / kNetThreads;
-  const uint32_t lim = (uint32_t)in_w - 1u;
   const WT* src = lds + cur;
-  const int guard = W + (int)(threadIdx.x & 63);
+  WT* dst = lds + nxt + threadIdx.x;
 #pragma unroll
   for (int g0 = 0; g0 < MAXO; g0 += GRP) {
-    WT va[GRP] = {}, vb[GRP] = {};
+    if (g0 >= rows) break;                               // wave-uniform
+    WT va[GRP], vb[GRP];
 #pragma unroll
     for (int u = 0; u < GRP; ++u) {
-      if (g0 + u < rows) {
-        const uint32_t c = cb[g0 + u];
-        va[u] = src[min((c >> 14) & 0x3FFFu, lim)];
-        vb[u] = src[min(c & 0x3FFFu, lim)];
-      }
+      const uint32_t c = cb[g0 + u];
+      va[u] = src[(c >> 14) & 0x3FFFu];
+      vb[u] = src[c & 0x3FFFu];
     }
     // all gate math, then all writes: no LDS access between the computes
     WT r[GRP];
 #pragma unroll
     for (int u = 0; u < GRP; ++u) r[u] = gate_compact<WT>(va[u], vb[u], cb[g0 + u]);
 #pragma unroll
-    for (int u = 0; u < GRP; ++u) {
-      const int j = g0 + u;
-      if (j < rows) {
-        const int o = threadIdx.x + j * kNetThreads;
-        if (j < nfull) lds[nxt + o] = r[u];
-        else lds[nxt + (o < W ? o : guard)] = r[u];
-      }
-    }
+    for (int u = 0; u < GRP; ++u) dst[(g0 + u) * kNetThreads] = r[u];
   }
 }
 
@@ -307,24 +298,55 @@ __device__ inline void keep_inputs(WT* lds, int cur, int nxt, int keep) {
   }
 }
 
-// Per-class sample counts without a bit transpose, one 32-sample half of
-// the words at a time (32-bit slices keep the register count low). A wave
-// takes 1024 words of one class (16 per lane, lane-contiguous LDS reads): a
-// carry-save adder tree (Harley-Seal) turns each lane's 16 half-words into
-// a bit-sliced 5-bit count per sample (slice k holds bit k of every
-// sample's count), then six butterfly rounds add the lanes' bit-sliced
-// counts (ripple-carry adders on the slices), after
-// which every lane holds the class total of the half's 32 samples in 11
-// slices (the exchanges are DPP moves and permlane swaps, no LDS). Words
-// past the class read 0; every lane of the wave must be active.
-__device__ inline uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) { return (a & b) | (c & (a | b)); }
-
-__device__ inline void csa(uint32_t& h, uint32_t& l, uint32_t a, uint32_t b, uint32_t c) {
-  h = maj3(a, b, c);
-  l = a ^ b ^ c;
+// Per-class sample counts without a bit transpose. One wave takes a class:
+// for 64-bit words lanes 0..31 count the low 32 samples and lanes 32..63 the
+// high 32, each lane carry-save adding (Harley-Seal) the half-words of 32
+// words into a bit-sliced 6-bit count per sample (slice k holds bit k of
+// every sample's count); five butterfly rounds inside each 32-lane group
+// then add the lanes' bit-sliced counts (ripple-carry adders on the slices),
+// after which every lane of a group holds its 32 samples' class totals in
+// 11 slices and lane s reads its own bits. 32-bit words take 16 words per
+// lane over all 64 lanes and a sixth round across the two groups. The
+// exchanges are DPP moves and permlane swaps, no LDS; words past the class
+// read 0; every lane of the wave must be active.
+// Majority and 3-input xor as one v_bitop3 each (truth tables 0xE8 and
+// 0x96, both symmetric in their inputs).
+__device__ __forceinline__ uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0xE8);
+}
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
 }
 
-constexpr int kGsWordsPerLane = 16, kGsChunk = 64 * kGsWordsPerLane;
+__device__ __forceinline__ void csa(uint32_t& h, uint32_t& l, uint32_t a, uint32_t b, uint32_t c) {
+  h = maj3(a, b, c);
+  l = xor3(a, b, c);
+}
+
+constexpr int kGsChunk = 1024;  // words of a class per pass
+
+// Harley-Seal step over 16 words: ones..eights carry across calls, the
+// 16s word of this block is returned.
+__device__ __forceinline__ uint32_t hs16(uint32_t& ones, uint32_t& twos, uint32_t& fours,
+                                         uint32_t& eights, const uint32_t* w) {
+  uint32_t twosA, twosB, foursA, foursB, eightsA, eightsB, sixteens;
+  csa(twosA, ones, ones, w[0], w[1]);
+  csa(twosB, ones, ones, w[2], w[3]);
+  csa(foursA, twos, twos, twosA, twosB);
+  csa(twosA, ones, ones, w[4], w[5]);
+  csa(twosB, ones, ones, w[6], w[7]);
+  csa(foursB, twos, twos, twosA, twosB);
+  csa(eightsA, fours, fours, foursA, foursB);
+  csa(twosA, ones, ones, w[8], w[9]);
+  csa(twosB, ones, ones, w[10], w[11]);
+  csa(foursA, twos, twos, twosA, twosB);
+  csa(twosA, ones, ones, w[12], w[13]);
+  csa(twosB, ones, ones, w[14], w[15]);
+  csa(foursB, twos, twos, twosA, twosB);
+  csa(eightsB, fours, fours, foursA, foursB);
+  csa(sixteens, eights, eights, eightsA, eightsB);
+  return sixteens;
+}
 
 // Bit-sliced add x += y of NB-bit counts (x[NB] is 0 on entry and takes the
 // carry out): a ripple of full adders, slice by slice.
@@ -333,7 +355,7 @@ __device__ __forceinline__ void add_slices(uint32_t (&x)[11], const uint32_t (&y
   uint32_t carry = 0;
 #pragma unroll
   for (int k = 0; k < NB; ++k) {
-    const uint32_t t = x[k] ^ y[k] ^ carry;
+    const uint32_t t = xor3(x[k], y[k], carry);
     carry = maj3(x[k], y[k], carry);
     x[k] = t;
   }
@@ -376,80 +398,72 @@ __device__ __forceinline__ void add_swap(uint32_t (&x)[11]) {
   add_slices<NB>(x, b);
 }
 
-// Count of sample `sh` of the half (0..31) over words [q*1024, q*1024 + 1024)
-// of the class; `cls32` are the class's words as 32-bit halves, `stride`
-// halves per word (2 for 64-bit words, 1 for 32-bit), `half` which one.
-__device__ __forceinline__ int class_chunk_count32(const uint32_t* cls32, int stride, int half, int G, int q,
-                                          int lane, int sh) {
-  uint32_t w[kGsWordsPerLane];
+// Class total of this lane's sample over the class's G words `cls32`
+// (32-bit halves, NH per word): sample lane for NH == 2, lane & 31 for
+// NH == 1.
+template <int NH>
+__device__ __forceinline__ int class_count(const uint32_t* cls32, int G, int lane) {
+  constexpr int WPL = NH == 2 ? 32 : 16;                 // words per lane per chunk
+  constexpr int LSTRIDE = NH == 2 ? 32 : 64;             // word stride between them
+  const int l = NH == 2 ? (lane & 31) : lane;
+  const int h = NH == 2 ? (lane >> 5) : 0;
+  int total = 0;
+  for (int q0 = 0; q0 < G; q0 += kGsChunk) {
+    // rows of the pass wholly inside the class load without a lane guard
+    // (a wave-uniform test); only the class's last partial row is guarded
+    const int nvalid = G - q0;
+    const uint32_t* p = cls32 + (q0 + l) * NH + h;
+    uint32_t w[WPL];
 #pragma unroll
-  for (int j = 0; j < kGsWordsPerLane; ++j) {
-    const int g = q * kGsChunk + j * 64 + lane;
-    w[j] = g < G ? cls32[g * stride + half] : 0u;
+    for (int j = 0; j < WPL; ++j) {
+      if (j * LSTRIDE + LSTRIDE <= nvalid) w[j] = p[j * LSTRIDE * NH];
+      else w[j] = j * LSTRIDE + l < nvalid ? p[j * LSTRIDE * NH] : 0u;
+    }
+    uint32_t x[11];
+#pragma unroll
+    for (int k = 0; k < 11; ++k) x[k] = 0;
+    if constexpr (NH == 2) {
+      const uint32_t s16a = hs16(x[0], x[1], x[2], x[3], w);
+      const uint32_t s16b = hs16(x[0], x[1], x[2], x[3], w + 16);
+      x[4] = s16a ^ s16b;
+      x[5] = s16a & s16b;
+      // 6 bits (<= 32) grow one bit per round to 11 (<= 1024)
+      add_dpp<6, 0xB1>(x);    // quad_perm [1,0,3,2]
+      add_dpp<7, 0x4E>(x);    // quad_perm [2,3,0,1]
+      add_dpp<8, 0x141>(x);   // row_half_mirror
+      add_dpp<9, 0x140>(x);   // row_mirror
+      add_swap<10, false>(x);  // lane ^ 16
+    } else {
+      x[4] = hs16(x[0], x[1], x[2], x[3], w);
+      add_dpp<5, 0xB1>(x);
+      add_dpp<6, 0x4E>(x);
+      add_dpp<7, 0x141>(x);
+      add_dpp<8, 0x140>(x);
+      add_swap<9, false>(x);
+      add_swap<10, true>(x);  // lane ^ 32
+    }
+    const int sh = lane & 31;
+    int cnt = 0;
+#pragma unroll
+    for (int k = 0; k < 11; ++k) cnt |= (int)((x[k] >> sh) & 1u) << k;
+    total += cnt;
   }
-  uint32_t x[11];
-#pragma unroll
-  for (int k = 0; k < 11; ++k) x[k] = 0;
-  {
-    uint32_t twosA, twosB, foursA, foursB, eightsA, eightsB;
-    uint32_t& ones = x[0];
-    uint32_t& twos = x[1];
-    uint32_t& fours = x[2];
-    uint32_t& eights = x[3];
-    csa(twosA, ones, ones, w[0], w[1]);
-    csa(twosB, ones, ones, w[2], w[3]);
-    csa(foursA, twos, twos, twosA, twosB);
-    csa(twosA, ones, ones, w[4], w[5]);
-    csa(twosB, ones, ones, w[6], w[7]);
-    csa(foursB, twos, twos, twosA, twosB);
-    csa(eightsA, fours, fours, foursA, foursB);
-    csa(twosA, ones, ones, w[8], w[9]);
-    csa(twosB, ones, ones, w[10], w[11]);
-    csa(foursA, twos, twos, twosA, twosB);
-    csa(twosA, ones, ones, w[12], w[13]);
-    csa(twosB, ones, ones, w[14], w[15]);
-    csa(foursB, twos, twos, twosA, twosB);
-    csa(eightsB, fours, fours, foursA, foursB);
-    csa(x[4], eights, eights, eightsA, eightsB);
-  }
-  // lanes' counts: 5 bits (<= 16) grow one bit per round to 11 (<= 1024)
-  add_dpp<5, 0xB1>(x);    // quad_perm [1,0,3,2]
-  add_dpp<6, 0x4E>(x);    // quad_perm [2,3,0,1]
-  add_dpp<7, 0x141>(x);   // row_half_mirror
-  add_dpp<8, 0x140>(x);   // row_mirror
-  add_swap<9, false>(x);  // lane ^ 16
-  add_swap<10, true>(x);  // lane ^ 32
-  int cnt = 0;
-#pragma unroll
-  for (int k = 0; k < 11; ++k) cnt |= (int)((x[k] >> sh) & 1u) << k;
-  return cnt;
+  return total;
 }
 
-// Per-class popcounts of a tile: cnt [C][64] must be zero on entry.
+// Per-class popcounts of a tile written as logits: one wave per class.
 template <typename WT>
-__device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int* cnt, int b0, int B,
-                                     float* __restrict__ logits) {
-  constexpr int SPW = (int)sizeof(WT) * 8;
+__device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int b0, int B,
+                                              float* __restrict__ logits) {
+  constexpr int NH = (int)sizeof(WT) / 4;                // 32-sample halves per word
+  constexpr int SPW = NH * 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nwaves = kNetThreads >> 6;
   const int G = W / C;
-  const int chunks = (G + kGsChunk - 1) / kGsChunk;
-  for (int task = wave; task < C * chunks; task += nwaves) {
-    const int c = task / chunks, q = task % chunks;
-    const uint32_t* cls32 = reinterpret_cast<const uint32_t*>(cur + c * G);
-    int n = class_chunk_count32(cls32, SPW / 32, 0, G, q, lane, lane & 31);
-    if constexpr (SPW == 64) {
-      const int nh = class_chunk_count32(cls32, 2, 1, G, q, lane, lane & 31);
-      n = lane < 32 ? n : nh;
-    }
-    if (chunks == 1) cnt[c * 64 + lane] = n;
-    else if (n) atomicAdd(&cnt[c * 64 + lane], n);
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < SPW * C; i += kNetThreads) {
-    const int s = i / C, c = i % C;
-    const int b = b0 + s;
-    if (b < B) logits[(int64_t)b * C + c] = (float)cnt[c * 64 + s];
+  for (int c = wave; c < C; c += nwaves) {
+    const int n = class_count<NH>(reinterpret_cast<const uint32_t*>(cur + c * G), G, lane);
+    const int b = b0 + lane;
+    if (lane < SPW && b < B) logits[(int64_t)b * C + c] = (float)n;
   }
 }
 
@@ -461,11 +475,9 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
   constexpr int SPW = (int)sizeof(WT) * 8;
   extern __shared__ __align__(16) unsigned char smem[];
   WT* lds = reinterpret_cast<WT*>(smem);
-  int* cnt = reinterpret_cast<int*>(lds + 2 * d.maxw);
   const int tile = blockIdx.x;
   uint32_t cb[MAXO];
   load_codes(cb, d.codes[0], d.width[0]);
-  for (int i = threadIdx.x; i < d.C * 64; i += kNetThreads) cnt[i] = 0;
   const int w64 = tile / (64 / SPW);
   for (int i = threadIdx.x; i < d.in0; i += kNetThreads) {
     const uint64_t word = LAYOUT == 0 ? xp[(int64_t)i * nw + w64] : xp[(int64_t)w64 * d.in0 + i];
@@ -479,7 +491,7 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
     uint32_t nb[MAXO];
     const int ln = (l + 1 < d.n_layers) ? l + 1 : l;
     load_codes(nb, d.codes[ln], d.width[ln]);
-    layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cur_w, cb);
+    layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cb);
     if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
     __syncthreads();
     const int t = cur; cur = nxt; nxt = t;
@@ -487,7 +499,7 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
 #pragma unroll
     for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
   }
-  groupsum_tile<WT>(lds + cur, cur_w, d.C, cnt, tile * SPW, B, logits);
+  groupsum_tile<WT>(lds + cur, cur_w, d.C, tile * SPW, B, logits);
 }
 
 // Unpacked rows [B][in0] (fp32, or uint8) with the packing fused: thread f
@@ -554,7 +566,6 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
                         float* __restrict__ logits) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* lds = reinterpret_cast<uint64_t*>(smem);
-  int* cnt = reinterpret_cast<int*>(lds + 2 * d.maxw);
   const int f = threadIdx.x;
   const bool fv = f < d.in0;
   const int voff0 = f * (int)sizeof(IT);
@@ -564,41 +575,50 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
   int tile = blockIdx.x;
   uint64_t word = 0;
   {
+    // first tile: two chunks in flight at a time
+    static_assert(kChunks == 4, "the first tile's loads are written out for four chunks");
     const __amdgpu_buffer_rsrc_t r = tile_rows(x, B, d.in0, tile * 64);
-    for (int c = 0; c < kChunks; ++c) {  // first tile
-      issue_chunk(val0, r, voff0, rowb, c);
-      fold_chunk(word, val0, c);
-    }
+    issue_chunk(val0, r, voff0, rowb, 0);
+    issue_chunk(val1, r, voff0, rowb, 1);
+    fold_chunk(word, val0, 0);
+    issue_chunk(val0, r, voff0, rowb, 2);
+    fold_chunk(word, val1, 1);
+    issue_chunk(val1, r, voff0, rowb, 3);
+    fold_chunk(word, val0, 2);
+    fold_chunk(word, val1, 3);
   }
   uint32_t cb[MAXO];
   load_codes(cb, d.codes[0], d.width[0]);
 
   for (; tile < n_tiles; tile += gridDim.x) {
     if (fv) lds[f] = word;
-    for (int i = threadIdx.x; i < d.C * 64; i += kNetThreads) cnt[i] = 0;
     __syncthreads();
     const __amdgpu_buffer_rsrc_t r = tile_rows(x, B, d.in0, (tile + gridDim.x) * 64);
     uint64_t nword = 0;
     int cur = 0, nxt = d.maxw, cur_w = d.in0;
-    for (int l = 0; l < L; ++l) {
+    // Layer l streams chunk l into val(l & 1) and folds chunk l - 2 from it.
+    // Every layer issues its chunk (past the fourth the offsets are past the
+    // tile's resource and read 0 without memory traffic) and the loop is
+    // unrolled by two, so each layer issues the same loads into the same
+    // registers: the compiler then waits only for the loads a step needs.
+    auto layer = [&](int l, IT (&val)[kChunk]) {
       const int W = d.width[l];
       const int ln = (l + 1 < L) ? l + 1 : 0;  // after the last layer: layer 0 of the next tile
       uint32_t nb[MAXO];
       load_codes(nb, d.codes[ln], d.width[ln]);
-      if (l & 1) {
-        if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val1, l - 2);
-        if (l < kChunks) issue_chunk(val1, r, voff0, rowb, l);
-      } else {
-        if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val0, l - 2);
-        if (l < kChunks) issue_chunk(val0, r, voff0, rowb, l);
-      }
-      layer_step<uint64_t, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(lds, cur, nxt, W, cur_w, cb);
+      if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val, l - 2);
+      issue_chunk(val, r, voff0, rowb, l);
+      layer_step<uint64_t, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(lds, cur, nxt, W, cb);
       if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
       __syncthreads();
       const int t = cur; cur = nxt; nxt = t;
       cur_w = W;
 #pragma unroll
       for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
+    };
+    for (int l = 0; l < L; l += 2) {
+      layer(l, val0);
+      if (l + 1 < L) layer(l + 1, val1);
     }
     // chunks issued during the last two layers, then chunks no layer issued
     for (int c = max(0, L - 2); c < min(L, kChunks); ++c) {
@@ -614,7 +634,7 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
     // it; constants here let the GroupSum below have those registers
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) val0[j] = val1[j] = (IT)0;
-    groupsum_tile<uint64_t>(lds + cur, cur_w, d.C, cnt, tile * 64, B, logits);
+    groupsum_tile<uint64_t>(lds + cur, cur_w, d.C, tile * 64, B, logits);
     __syncthreads();
     word = fv ? nword : 0ull;
   }
@@ -649,24 +669,25 @@ __global__ void __launch_bounds__(256) groupsum_packed_kernel(const uint64_t* __
 }
 
 
-static int net_spw(int64_t IN0, int n_layers, const int64_t* widths, int C) {
-  if (!widths || n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
-  int64_t maxw = IN0;
-  for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
-  if (maxw > 16 * kNetThreads) return 0;
-  const int64_t words = ((maxw + 1) & ~1LL) + kGuard;  // per activation buffer
-  const int64_t lds = device_lds_bytes();
-  if (2 * words * 8 + (int64_t)C * 256 <= lds) return 64;
-  if (2 * words * 4 + (int64_t)C * 256 <= lds) return 32;
-  return 0;
-}
-
 static int pick_maxo(int64_t maxw) {
   const int64_t m = cdiv(maxw, kNetThreads);
   for (int c : {2, 4, 8, 10, 16})
     if (m <= c) return c;
   return 0;
 }
+
+static int net_spw(int64_t IN0, int n_layers, const int64_t* widths, int C) {
+  if (!widths || n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
+  int64_t maxw = IN0;
+  for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
+  if (maxw > 16 * kNetThreads) return 0;
+  const int64_t words = (int64_t)pick_maxo(maxw) * kNetThreads;  // per activation buffer
+  const int64_t lds = device_lds_bytes();
+  if (2 * words * 8 <= lds) return 64;
+  if (2 * words * 4 <= lds) return 32;
+  return 0;
+}
+
 
 template <typename K>
 static int set_lds(K kern, size_t lds, const char* what) {
@@ -866,10 +887,10 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
   d.n_layers = n_layers; d.in0 = (int)IN0; d.C = C; d.wire_r = (int)std::max<int64_t>(0, wire_r);
   int64_t maxw = IN0;
   for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
-  d.maxw = (int)(((maxw + 1) & ~1LL) + kGuard);
   const int maxo = pick_maxo(maxw);
   SLG_REQUIRE(maxo > 0, SLG_E_UNSUPPORTED, "fc_hard_net: width too large");
-  const size_t lds = (size_t)2 * d.maxw * (spw / 8) + (size_t)C * 256;
+  d.maxw = maxo * kNetThreads;
+  const size_t lds = (size_t)2 * d.maxw * (spw / 8);
   hipStream_t st = as_stream(stream);
   if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
   if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
