@@ -519,18 +519,11 @@ __device__ inline bool input_bit(IT v) {
   else return v >= (IT)1;
 }
 
-// The tile's rows as a buffer resource. Its words are read back with
-// readfirstlane: they are wave-uniform, and a resource the compiler cannot
-// prove uniform costs a waterfall loop around every load through it.
+// The tile's rows as a wave-uniform buffer resource.
 template <typename IT>
 __device__ inline __amdgpu_buffer_rsrc_t tile_rows(const IT* x, int B, int in0, int b0) {
   const int64_t rows = max(0, min(64, B - b0));
-  const uint64_t base = (uint64_t)(x + (int64_t)min(b0, B) * in0);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
-  const int bytes = __builtin_amdgcn_readfirstlane((int)(rows * in0 * (int64_t)sizeof(IT)));
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, bytes,
-                                           kBufferWord3);
+  return uniform_rsrc(x + (int64_t)min(b0, B) * in0, (int)(rows * in0 * (int64_t)sizeof(IT)));
 }
 
 template <typename IT>

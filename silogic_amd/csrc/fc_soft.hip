@@ -66,8 +66,12 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, Para
   __syncthreads();
 
   const uint32_t lim = (uint32_t)IN - 1u;
-  const bool full = b0 + S <= B;
   const int lane = threadIdx.x & 63;
+  // The tile's output rows as a buffer resource (S * OUT * 4 < 2^31 bytes,
+  // checked at launch): stores past its valid rows are dropped.
+  __amdgpu_buffer_rsrc_t yrows;
+  if constexpr (!HEAD)
+    yrows = uniform_rsrc(y + (int64_t)min(b0, B) * OUT, max(0, min(S, B - b0)) * OUT * 4);
 
   // Each wave owns a contiguous run of 64-output chunks; lane = output
   // within a chunk. The next chunk's parameters are loaded while this one
@@ -99,11 +103,12 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, Para
     const int o = oc0 + lane;
     const bool valid = o < o_end;
     // clamp into the staged rows (unsigned min also maps negatives to IN-1)
+    // (records hold indices the records kernel already clamped)
     uint32_t ia[KM], ib[KM];
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
-      ia[k] = min((uint32_t)P.ia[k], lim);
-      ib[k] = min((uint32_t)P.ib[k], lim);
+      ia[k] = REC ? (uint32_t)P.ia[k] : min((uint32_t)P.ia[k], lim);
+      ib[k] = REC ? (uint32_t)P.ib[k] : min((uint32_t)P.ib[k], lim);
     }
     float yv[S];
 #pragma unroll
@@ -147,17 +152,13 @@ fc_soft_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, Para
         hi_b = (cur_c + 1) * hd.per;
       }
     } else {
-      float* yo = y + (int64_t)b0 * OUT + o;
-      if (valid) {
-        if (full) {
+      // branch-free stores: lanes past the chunk and rows past the batch
+      // fall outside the tile's resource and are dropped by the hardware
+      const uint32_t vo = valid ? (uint32_t)o * 4u : 0x80000000u;
 #pragma unroll
-          for (int s = 0; s < S; ++s) yo[(int64_t)s * OUT] = yv[s];
-        } else {
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-            if (b0 + s < B) yo[(int64_t)s * OUT] = yv[s];
-        }
-      }
+      for (int s = 0; s < S; ++s)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv[s]), yrows,
+                                              (int)(vo + (uint32_t)(s * OUT) * 4u), 0, 0);
     }
   };
 
@@ -220,6 +221,8 @@ static int launch_soft_s(const SoftArgs& a, hipStream_t st) {
               "fc_soft: fused GroupSum needs one output chunk per tile");
   const int64_t grid = cdiv(a.B, S) * n_chunks;
   SLG_REQUIRE(grid < (1LL << 31), SLG_E_SHAPE, "fc_soft: grid too large");
+  SLG_REQUIRE(a.OUT * S * 4 < (1LL << 31), SLG_E_SHAPE, "fc_soft: OUT %lld too large",
+              (long long)a.OUT);
   auto kern = fc_soft_kernel<NODE, KC, S, HEAD, REC>;
   const int threads = std::min(a.threads, soft_max_threads<KC, S>());
   const size_t lds = (size_t)a.IN * S * sizeof(float) + (HEAD ? (size_t)S * a.hd.C * 4 : 0);

@@ -54,6 +54,21 @@ __device__ inline uint32_t xcd_logical_id(uint32_t i, uint32_t grid) {
 // Loads through such a resource at offsets past its byte size return 0.
 constexpr int kBufferWord3 = 0x00020000;
 
+// A raw buffer resource over `bytes` bytes at `p`, for a wave-uniform p and
+// size. The words are passed through readfirstlane so the compiler sees them
+// as uniform (a resource it cannot prove uniform costs a waterfall loop
+// around every access). readfirstlane returns a signed int: each half is
+// taken back as uint32_t before it is widened, or the sign of the low word
+// would spill into the high one.
+__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, int bytes) {
+  const uint64_t a = (uint64_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | (uint64_t)lo), (short)0,
+                                           n, kBufferWord3);
+}
+
 // q = e / d for 0 <= e < 2^24 and 0 < d < 2^24, with inv = 1.0f / d: the
 // float quotient is within one of the true one, and the remainder test
 // corrects it.
