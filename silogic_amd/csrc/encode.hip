@@ -12,6 +12,7 @@
 // The learnable thermometer orders f*bits + i: (x[b][f] - thr[f][i] > 0).
 #include <math.h>
 
+#include "pack_cols.h"
 #include "slg_common.h"
 
 namespace slg {
@@ -74,10 +75,10 @@ __device__ inline bool pass_bit(TX v, float th, int cut) {
 }
 
 // Packed: a lane takes V consecutive features and builds their words over
-// the 64 samples of one word in registers (no LDS, no ballot); the four
-// waves of a workgroup take four consecutive words. V = 4 reads the four
-// features of a row as one vector (fixed thresholds, D % 4 == 0, aligned
-// input). LAYOUT 0: xp [F, nw]; 1: xp [nw, F].
+// the 64 samples of one word in registers (pack_cols); the four waves of a
+// workgroup take four consecutive words. V = 4 reads the four features of a
+// row as one vector (fixed thresholds, D % 4 == 0, aligned input).
+// LAYOUT 0: xp [F, nw]; 1: xp [nw, F].
 template <bool FIXED, int LAYOUT, typename TX, int V>
 __global__ void __launch_bounds__(256) encode_pack_kernel(const TX* __restrict__ x, int B, int D,
                                                           int T, const float* __restrict__ thr,
@@ -103,55 +104,11 @@ __global__ void __launch_bounds__(256) encode_pack_kernel(const TX* __restrict__
     }
     cut[v] = sizeof(TX) == 1 ? byte_cut<FIXED>(th[v]) : 0;
   }
-  const int nr = min(64, B - w * 64);                    // samples in this word (wave-uniform)
-  const TX* xr = x + (int64_t)w * 64 * D;
   uint64_t word[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) word[v] = 0;
-  auto chunk = [&](int c) {
-    uint32_t m[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) m[v] = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      {
-        // rows past the batch read the last row (no branch, so every load
-        // can be in flight at once); their bits are cleared below
-        const TX* row = xr + (int64_t)min(c + i, nr - 1) * D;
-        if constexpr (V == 4) {
-          if constexpr (sizeof(TX) == 1) {
-            const uint32_t q = *(const uint32_t*)(row + src[0]);
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              m[v] |= (pass_bit<FIXED>((uint8_t)(q >> (8 * v)), th[v], cut[v]) ? 1u : 0u) << i;
-          } else {
-            const float4 q = *(const float4*)(row + src[0]);
-            const float qv[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              m[v] |= (pass_bit<FIXED>(qv[v], th[v], cut[v]) ? 1u : 0u) << i;
-          }
-        } else {
-#pragma unroll
-          for (int v = 0; v < V; ++v)
-            m[v] |= (pass_bit<FIXED>(row[src[v]], th[v], cut[v]) ? 1u : 0u) << i;
-        }
-      }
-    }
-#pragma unroll
-    for (int v = 0; v < V; ++v) word[v] |= (uint64_t)m[v] << c;
-  };
-  if constexpr (sizeof(TX) == 1) {
-    // bytes: all 64 rows' loads in flight at once (one register per load)
-    chunk(0); chunk(16); chunk(32); chunk(48);
-  } else {
-#pragma unroll 1
-    for (int c = 0; c < 64; c += 16) chunk(c);
-  }
-  const uint64_t valid = nr == 64 ? ~0ull : (1ull << nr) - 1;
+  pack_cols<V, V == 4>(x + (int64_t)w * 64 * D, D, min(64, B - w * 64), src,
+                       [&](TX v, int f) { return pass_bit<FIXED>(v, th[f], cut[f]); }, word);
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    word[v] &= valid;
     if (j0 + v < F) {
       if constexpr (LAYOUT == 0) xp[(int64_t)(j0 + v) * nw + w] = word[v];
       else xp[(int64_t)w * F + j0 + v] = word[v];

@@ -6,6 +6,7 @@
 // words is three bit-field-inserts per 32-bit half:
 //   out = bfi(a, bfi(b, T3, T2), bfi(b, T1, T0)),  T_g = tt bit g ? ~0 : 0,
 // so one output word costs the same whatever the gate, with no branching.
+#include "pack_cols.h"
 #include "slg_common.h"
 
 namespace slg {
@@ -46,35 +47,35 @@ __device__ inline uint64_t transpose64(uint64_t v, int lane) {
 // ---------------------------------------------------------------------------
 // pack / unpack
 // ---------------------------------------------------------------------------
-// Tile: 64 samples (one output word) x 64 features. Coalesced row reads into
-// LDS, then one ballot per feature. LAYOUT 0 writes the reference layout
-// [D][nw]; LAYOUT 1 writes word-major [nw][D], where one 64-sample column of
-// all features is contiguous (the fused network kernel's input).
-template <typename T, int LAYOUT>
+// A lane takes V consecutive features and builds their 64-sample words in
+// registers (pack_cols); the four waves of a workgroup take four consecutive
+// words. A feature's bit is (x >= 1) for fp32, (x != 0) for bytes. V = 4
+// reads four features of a row as one vector (D % 4 == 0, aligned input).
+// LAYOUT 0 writes the reference layout [D][nw]; LAYOUT 1 writes word-major
+// [nw][D], where one 64-sample column of all features is contiguous (the
+// fused network kernel's input).
+template <typename T, int LAYOUT, int V>
 __global__ void __launch_bounds__(256) pack_kernel(const T* __restrict__ x, int B, int D, int nw,
                                                    int dtiles, uint64_t* __restrict__ xp) {
-  __shared__ uint8_t tile[64][68];
-  const int w = (int)(blockIdx.x / (uint32_t)dtiles);
-  const int d0 = (int)(blockIdx.x % (uint32_t)dtiles) * 64;
-  const int c = threadIdx.x & 63;
-  for (int r = threadIdx.x >> 6; r < 64; r += 4) {
-    const int b = w * 64 + r, d = d0 + c;
-    uint8_t bit = 0;
-    if (b < B && d < D) {
-      const T v = x[(int64_t)b * D + d];
-      if constexpr (sizeof(T) == 1) bit = (v != 0);
-      else bit = (v >= (T)1);
-    }
-    tile[r][c] = bit;
-  }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int j = 0; j < 16; ++j) {
-    const int cc = wave * 16 + j;
-    const uint64_t m = __ballot(tile[lane][cc] != 0);
-    if (lane == 0 && d0 + cc < D) {
-      if constexpr (LAYOUT == 0) xp[(int64_t)(d0 + cc) * nw + w] = m;
-      else xp[(int64_t)w * D + d0 + cc] = m;
+  const int lane = threadIdx.x & 63;
+  const int w = (int)(blockIdx.x / (uint32_t)dtiles) * 4 + (int)(threadIdx.x >> 6);
+  const int d0 = (int)(blockIdx.x % (uint32_t)dtiles) * 64 * V + lane * V;
+  if (w >= nw || d0 >= D) return;                       // no barriers below
+  int src[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) src[v] = min(d0 + v, D - 1);  // tail lanes: stores are guarded
+  uint64_t word[V];
+  pack_cols<V, V == 4>(x + (int64_t)w * 64 * D, D, min(64, B - w * 64), src,
+                       [](T v, int) {
+                         if constexpr (sizeof(T) == 1) return v != 0;
+                         else return v >= (T)1;
+                       },
+                       word);
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if (d0 + v < D) {
+      if constexpr (LAYOUT == 0) xp[(int64_t)(d0 + v) * nw + w] = word[v];
+      else xp[(int64_t)w * D + d0 + v] = word[v];
     }
   }
 }
@@ -755,17 +756,22 @@ int slg_pack_bits(const void* x, int32_t dtype, int64_t B, int64_t D, int32_t la
               SLG_E_SHAPE, "pack_bits: bad sizes");
   if (B == 0) return 0;
   const int64_t nw = cdiv(B, 64);
-  const int64_t dtiles = cdiv(D, 64);
-  SLG_REQUIRE(nw * dtiles < (1LL << 31), SLG_E_SHAPE, "pack_bits: too many tiles");
-  dim3 grid((unsigned)(nw * dtiles));
+  const size_t esz = dtype == 0 ? 4 : 1;
+  const bool vec = D % 4 == 0 && (uintptr_t)x % (4 * esz) == 0;
+  const int64_t dtiles = cdiv(D, vec ? 256 : 64);
+  SLG_REQUIRE(cdiv(nw, 4) * dtiles < (1LL << 31), SLG_E_SHAPE, "pack_bits: too many tiles");
+  dim3 grid((unsigned)(cdiv(nw, 4) * dtiles));
   hipStream_t st = as_stream(stream);
-#define SLG_PACK(T, LY)                                                                    \
-  hipLaunchKernelGGL((pack_kernel<T, LY>), grid, dim3(256), 0, st, (const T*)x, (int)B, (int)D, \
-                     (int)nw, (int)dtiles, xp)
-  if (dtype == 0 && layout == 0) SLG_PACK(float, 0);
-  else if (dtype == 0) SLG_PACK(float, 1);
-  else if (layout == 0) SLG_PACK(uint8_t, 0);
-  else SLG_PACK(uint8_t, 1);
+#define SLG_PACK(T, LY, V)                                                                     \
+  hipLaunchKernelGGL((pack_kernel<T, LY, V>), grid, dim3(256), 0, st, (const T*)x, (int)B,     \
+                     (int)D, (int)nw, (int)dtiles, xp)
+#define SLG_PACK_V(T, LY) \
+  do { if (vec) SLG_PACK(T, LY, 4); else SLG_PACK(T, LY, 1); } while (0)
+  if (dtype == 0 && layout == 0) SLG_PACK_V(float, 0);
+  else if (dtype == 0) SLG_PACK_V(float, 1);
+  else if (layout == 0) SLG_PACK_V(uint8_t, 0);
+  else SLG_PACK_V(uint8_t, 1);
+#undef SLG_PACK_V
 #undef SLG_PACK
   SLG_LAUNCH_CHECK("pack_bits");
   return 0;
