@@ -367,6 +367,26 @@ def test_fused_net_equals_layerwise_path_and_wide_32bit_tiles():
             assert torch.equal(o.cpu(), ref)
 
 
+@pytest.mark.parametrize("width,C", [(2050, 2), (6300, 7), (640, 64), (10240, 5), (96, 3)])
+def test_fused_net_groupsum_class_shapes(width, C):
+    """The fused kernels' GroupSum (bit-sliced counts, one wave per class)
+    over classes of 1025, 900, 10, 2048 and 32 words: several 1024-word
+    passes per class, classes that are not whole 32-word rows, 64 classes,
+    and a layer that fills both 80 KiB activation buffers."""
+    spec = ("LogicNet", dict(in_dim=200, width=width, depth=2, num_classes=C, k=8))
+    model = build_product(spec)
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV).eval()
+    x = random_bits(333, 200)
+    xd = x.to(DEV)
+    codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
+    ref = torch_ref.forward_hard(spec, sd, x)
+    assert torch.equal(ops.fc_hard_net(xd, ops.ROWS_F32, 333, 200, codes, C).cpu(), ref)
+    assert torch.equal(ops.fc_hard_net(ops.pack_bits(xd, word_major=True), ops.PACKED_WORD_MAJOR,
+                                       333, 200, codes, C).cpu(), ref)
+    assert torch.equal(model.forward_hard(xd).cpu(), ref)
+
+
 @pytest.mark.parametrize("depth", [1, 2, 3, 6])
 def test_fused_rows_kernel_many_tiles(depth):
     """More 64-sample tiles than CUs (persistent loop, streamed next-tile input)
