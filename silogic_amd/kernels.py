@@ -9,11 +9,16 @@ meaning and ``HAS_*`` capability flags, implemented by the HIP library.
 * :func:`multilinear_logic` — silogic/kernels/multilinear.py:160-174 (hybrid LUT layer)
 * :func:`conv_hybrid` — silogic/kernels/conv_hybrid.py:196 (hybrid LUT trees of depth 1)
 
-The flags are True when ``libsilogic_hip.so`` loads.
+The flags are True when ``libsilogic_hip.so`` loads. Each function calls the
+``torch.ops.silogic_hip`` custom operator of its kernel (``library.py``:
+fake shapes for tracing, autograd through the HIP backward kernels).
 """
 import torch
 
 from . import _lib, ops
+from . import library as _ops_lib  # noqa: F401  (registers torch.ops.silogic_hip)
+
+_op = torch.ops.silogic_hip
 
 _OK = _lib.available()
 HAS_DENSE = HAS_WARP = HAS_CONV = HAS_CONV_TOPK = _OK
@@ -29,13 +34,17 @@ def _pack_ab(ca, cb, wa, wb):
 def dense_logic(x, ca, cb, wa, wb, coef):
     """x[B,IN], ca/cb[OUT,K] int32, wa/wb[OUT,K], coef[OUT,4] -> [B,OUT]."""
     cand, w = _pack_ab(ca, cb, wa, wb)
-    return ops.fc_soft(x, cand, w, coef, ops.GATE16, 1.0)
+    return _op.fc_soft(x, cand.to(torch.int32), w, coef, ops.GATE16, 1.0)
 
 
 def warp_logic(x, ca, cb, wa, wb, coef, inv_tau):
     """As :func:`dense_logic`, then ``sigmoid(z * inv_tau)``."""
     cand, w = _pack_ab(ca, cb, wa, wb)
-    return ops.fc_soft(x, cand, w, coef, ops.WALSH, float(inv_tau))
+    return _op.fc_soft(x, cand.to(torch.int32), w, coef, ops.WALSH, float(inv_tau))
+
+
+def _i32(t):
+    return t.to(torch.int32).contiguous()
 
 
 def _check_same(stride, pad, H, W, Ho, Wo):
@@ -48,14 +57,15 @@ def tree_conv(x, coef, cm, ch, cw, depth, stride, pad, Ho, Wo):
     _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
     N, leaves = cm.shape
     w = torch.ones(N, leaves, 1, device=x.device)
-    return ops.conv_soft(x, coef, w, cm.unsqueeze(-1), ch.unsqueeze(-1), cw.unsqueeze(-1),
-                         ops.GATE16, depth, 2, 1, pad, False)
+    return _op.conv_soft(x, coef, w, _i32(cm.unsqueeze(-1)), _i32(ch.unsqueeze(-1)),
+                         _i32(cw.unsqueeze(-1)), ops.GATE16, depth, 2, 1, pad, False)
 
 
 def tree_conv_topk(x, coef, w, cm, ch, cw, depth, K, stride, pad, Ho, Wo):
     """Top-K gate tree conv: w/cm/ch/cw [N,2^d,K]."""
     _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
-    return ops.conv_soft(x, coef, w, cm, ch, cw, ops.GATE16, depth, 2, K, pad, False)
+    return _op.conv_soft(x, coef, w, _i32(cm), _i32(ch), _i32(cw), ops.GATE16, depth, 2, K, pad,
+                         False)
 
 
 def multilinear_logic(x, cand, w, s, arity):
@@ -64,7 +74,7 @@ def multilinear_logic(x, cand, w, s, arity):
     operands thresholded at 0.5, with the multilinear gradient."""
     if cand.shape[1] != arity:
         raise ValueError("multilinear_logic: cand must be [OUT, arity, K]")
-    return ops.fc_lut_soft(x, cand, w, s, True)
+    return _op.fc_lut_soft(x, cand.to(torch.int32), w, s, True)
 
 
 def conv_hybrid(x, s, w, cm, ch, cw, depth, node_arity, K, stride, pad, Ho, Wo):
@@ -74,5 +84,5 @@ def conv_hybrid(x, s, w, cm, ch, cw, depth, node_arity, K, stride, pad, Ho, Wo):
     if depth != 1:
         raise NotImplementedError("conv_hybrid on MI355X: trees of depth 1")
     N = cm.shape[0]
-    return ops.conv_soft(x, s.reshape(N, 2 ** node_arity), w, cm, ch, cw, ops.HYBRID, 1,
-                         node_arity, K, pad, False)
+    return _op.conv_soft(x, s.reshape(N, 2 ** node_arity), w, _i32(cm), _i32(ch), _i32(cw),
+                         ops.HYBRID, 1, node_arity, K, pad, False)

@@ -1,0 +1,258 @@
+"""The HIP entry points as PyTorch custom operators (namespace ``silogic_hip``).
+
+Each op is registered with ``torch.library.custom_op``, a fake (meta)
+implementation that gives output shapes and dtypes without running a
+kernel, and, for the differentiable ops, ``register_autograd`` with a
+backward that is itself a custom op (the HIP backward kernels; shapes they
+do not take fall back to the composite torch backward inside the op). So
+``torch.compile`` / FX tracing see opaque operators instead of a graph
+break at the ctypes call. The drop-ins of ``silogic_amd.kernels`` (the
+reference's ``silogic.kernels``, kernels/__init__.py:21-55) call these ops.
+
+Gradients an op does not need come back from the backward ops as empty
+``[0]`` tensors (a custom op returns tensors, not None) and are turned into
+None before autograd sees them.
+"""
+from typing import List, Tuple
+
+import torch
+from torch import Tensor
+
+from . import ops
+
+_NS = "silogic_hip"
+
+
+def _none(t, need):
+    return t if need else None
+
+
+def _empty(ref):
+    return ref.new_empty((0,))
+
+
+# ---------------------------------------------------------------------------
+# FC soft layer (dense_logic / warp_logic)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{_NS}::fc_soft", mutates_args=())
+def fc_soft(x: Tensor, cand: Tensor, w: Tensor, npar: Tensor, node_kind: int,
+            inv_tau: float) -> Tensor:
+    """``x [B,IN]``, ``cand/w [OUT,2,K]``, ``npar [OUT,4]`` -> ``[B,OUT]``."""
+    ops.require_gpu(x, cand, w, npar)
+    return ops._fc_soft_launch(ops._as_f32(x), ops._c(cand, torch.int32),
+                               ops._c(w, torch.float32), ops._c(npar, torch.float32),
+                               node_kind, inv_tau)
+
+
+@fc_soft.register_fake
+def _(x, cand, w, npar, node_kind, inv_tau):
+    return x.new_empty((x.shape[0], cand.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::fc_soft_bwd", mutates_args=())
+def fc_soft_bwd(x: Tensor, cand: Tensor, w: Tensor, npar: Tensor, node_kind: int, inv_tau: float,
+                gy: Tensor, need_x: bool, need_w: bool,
+                need_np: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """``(gx, gw, gnp)`` of fc_soft; unneeded ones are empty."""
+    got = ops.fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need_x, need_w, need_np)
+    if got is None:   # shapes the HIP backward does not take: composite torch backward
+        with torch.enable_grad():
+            xs = ops._as_f32(x.detach()).requires_grad_(need_x)
+            ws = w.detach().float().requires_grad_(need_w)
+            ns = npar.detach().float().requires_grad_(need_np)
+            y = ops.fc_soft_torch(xs, cand, ws, ns, node_kind, inv_tau)
+            inputs = [t for t, n in ((xs, need_x), (ws, need_w), (ns, need_np)) if n]
+            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
+        got = tuple(grads.pop(0) if n else None for n in (need_x, need_w, need_np))
+    gx, gw, gn = got
+    return (gx if gx is not None else _empty(x), gw if gw is not None else _empty(x),
+            gn if gn is not None else _empty(x))
+
+
+@fc_soft_bwd.register_fake
+def _(x, cand, w, npar, node_kind, inv_tau, gy, need_x, need_w, need_np):
+    f32 = torch.float32
+    return (x.new_empty(x.shape, dtype=f32) if need_x else x.new_empty((0,), dtype=f32),
+            x.new_empty(w.shape, dtype=f32) if need_w else x.new_empty((0,), dtype=f32),
+            x.new_empty(npar.shape, dtype=f32) if need_np else x.new_empty((0,), dtype=f32))
+
+
+def _fc_soft_setup(ctx, inputs, output):
+    x, cand, w, npar, node_kind, inv_tau = inputs
+    ctx.save_for_backward(x, cand, w, npar)
+    ctx.meta = (node_kind, inv_tau)
+
+
+def _fc_soft_backward(ctx, gy):
+    x, cand, w, npar = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    gx, gw, gn = fc_soft_bwd(x, cand, w, npar, *ctx.meta, gy, need[0], need[2], need[3])
+    return _none(gx, need[0]), None, _none(gw, need[2]), _none(gn, need[3]), None, None
+
+
+fc_soft.register_autograd(_fc_soft_backward, setup_context=_fc_soft_setup)
+
+
+# ---------------------------------------------------------------------------
+# LUT FC layer (multilinear_logic)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{_NS}::fc_lut_soft", mutates_args=())
+def fc_lut_soft(x: Tensor, cand: Tensor, w: Tensor, s: Tensor, hybrid: bool) -> Tensor:
+    """``x [B,IN]``, ``cand/w [OUT,n,K]``, ``s [OUT,2^n]`` -> ``[B,OUT]``."""
+    ops.require_gpu(x, cand, w, s)
+    return ops._fc_lut_launch(ops._as_f32(x), ops._c(cand, torch.int32), ops._c(w, torch.float32),
+                              ops._c(s, torch.float32), hybrid)
+
+
+@fc_lut_soft.register_fake
+def _(x, cand, w, s, hybrid):
+    return x.new_empty((x.shape[0], cand.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::fc_lut_soft_bwd", mutates_args=())
+def fc_lut_soft_bwd(x: Tensor, cand: Tensor, w: Tensor, s: Tensor, gy: Tensor, need_x: bool,
+                    need_w: bool, need_s: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    got = ops.fc_lut_soft_bwd(x, cand, w, s, gy, need_x, need_w, need_s)
+    if got is None:
+        raise NotImplementedError("fc_lut_soft backward: the input width exceeds what the "
+                                  "kernels stage in LDS")
+    gx, gw, gs = got
+    return (gx if gx is not None else _empty(x), gw if gw is not None else _empty(x),
+            gs if gs is not None else _empty(x))
+
+
+@fc_lut_soft_bwd.register_fake
+def _(x, cand, w, s, gy, need_x, need_w, need_s):
+    f32 = torch.float32
+    return (x.new_empty(x.shape, dtype=f32) if need_x else x.new_empty((0,), dtype=f32),
+            x.new_empty(w.shape, dtype=f32) if need_w else x.new_empty((0,), dtype=f32),
+            x.new_empty(s.shape, dtype=f32) if need_s else x.new_empty((0,), dtype=f32))
+
+
+def _fc_lut_setup(ctx, inputs, output):
+    x, cand, w, s, hybrid = inputs
+    ctx.save_for_backward(x, cand, w, s)
+
+
+def _fc_lut_backward(ctx, gy):
+    x, cand, w, s = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    gx, gw, gs = fc_lut_soft_bwd(x, cand, w, s, gy, need[0], need[2], need[3])
+    return _none(gx, need[0]), None, _none(gw, need[2]), _none(gs, need[3]), None
+
+
+fc_lut_soft.register_autograd(_fc_lut_backward, setup_context=_fc_lut_setup)
+
+
+# ---------------------------------------------------------------------------
+# Conv tree layer with the fused 2x2 OrPool (tree_conv, tree_conv_topk,
+# conv_hybrid)
+# ---------------------------------------------------------------------------
+def _conv_out_shape(x, cm, pad, pool):
+    B, _, H, W = x.shape
+    kern = 2 * pad + 1
+    Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
+    Ho, Wo = (Hf // 2, Wf // 2) if pool else (Hf, Wf)
+    return (B, cm.shape[0], Ho, Wo)
+
+
+@torch.library.custom_op(f"{_NS}::conv_soft", mutates_args=())
+def conv_soft(x: Tensor, npar: Tensor, w: Tensor, cm: Tensor, ch: Tensor, cw: Tensor,
+              node_kind: int, depth: int, arity: int, K: int, pad: int, pool: bool) -> Tensor:
+    """``x [B,C,H,W]`` -> ``[B,N,Ho,Wo]`` (pooled when ``pool``)."""
+    ops.require_gpu(x, npar, w, cm)
+    return ops._conv_soft_launch(ops._as_f32(x), ops._c(npar, torch.float32),
+                                 ops._c(w, torch.float32), ops._c(cm, torch.int32),
+                                 ops._c(ch, torch.int32), ops._c(cw, torch.int32), node_kind,
+                                 depth, arity, K, pad, pool)
+
+
+@conv_soft.register_fake
+def _(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
+    return x.new_empty(_conv_out_shape(x, cm, pad, pool), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::conv_soft_bwd", mutates_args=())
+def conv_soft_bwd(x: Tensor, npar: Tensor, w: Tensor, cm: Tensor, ch: Tensor, cw: Tensor,
+                  node_kind: int, depth: int, arity: int, K: int, pad: int, pool: bool, gy: Tensor,
+                  need_x: bool, need_np: bool, need_w: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """``(gx, gnp, gw)`` of conv_soft; unneeded ones are empty."""
+    meta = (node_kind, depth, arity, K, pad, pool)
+    got = ops.conv_soft_bwd(x, npar, w, cm, ch, cw, *meta, gy, need_x, need_np, need_w)
+    if got is None:   # shapes the HIP backward does not take: composite torch backward
+        with torch.enable_grad():
+            xs = ops._as_f32(x.detach()).requires_grad_(need_x)
+            ns = npar.detach().float().requires_grad_(need_np)
+            ws = w.detach().float().requires_grad_(need_w)
+            y = ops.conv_soft_torch(xs, ns, ws, cm, ch, cw, *meta)
+            inputs = [t for t, n in ((xs, need_x), (ns, need_np), (ws, need_w)) if n]
+            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
+        got = tuple(grads.pop(0) if n else None for n in (need_x, need_np, need_w))
+    gx, gn, gw = got
+    return (gx if gx is not None else _empty(x), gn if gn is not None else _empty(x),
+            gw if gw is not None else _empty(x))
+
+
+@conv_soft_bwd.register_fake
+def _(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool, gy, need_x, need_np,
+      need_w):
+    f32 = torch.float32
+    return (x.new_empty(x.shape, dtype=f32) if need_x else x.new_empty((0,), dtype=f32),
+            x.new_empty(npar.shape, dtype=f32) if need_np else x.new_empty((0,), dtype=f32),
+            x.new_empty(w.shape, dtype=f32) if need_w else x.new_empty((0,), dtype=f32))
+
+
+def _conv_setup(ctx, inputs, output):
+    x, npar, w, cm, ch, cw = inputs[:6]
+    ctx.save_for_backward(x, npar, w, cm, ch, cw)
+    ctx.meta = tuple(inputs[6:])
+
+
+def _conv_backward(ctx, gy):
+    x, npar, w, cm, ch, cw = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    gx, gn, gw = conv_soft_bwd(x, npar, w, cm, ch, cw, *ctx.meta, gy, need[0], need[1], need[2])
+    return (_none(gx, need[0]), _none(gn, need[1]), _none(gw, need[2])) + (None,) * 9
+
+
+conv_soft.register_autograd(_conv_backward, setup_context=_conv_setup)
+
+
+# ---------------------------------------------------------------------------
+# Hard path: packing, the depth-fused network, the packed GroupSum
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{_NS}::pack_bits", mutates_args=())
+def pack_bits(x: Tensor, word_major: bool) -> Tensor:
+    """``[B, D]`` {0,1} -> ``[D, nw]`` int64 (``[nw, D]`` with word_major)."""
+    return ops.pack_bits(x, word_major)
+
+
+@pack_bits.register_fake
+def _(x, word_major):
+    B = x.shape[0]
+    D = x.numel() // B if B else x[0].numel()
+    nw = ops.n_words(B)
+    return x.new_empty((nw, D) if word_major else (D, nw), dtype=torch.int64)
+
+
+@torch.library.custom_op(f"{_NS}::fc_hard_net", mutates_args=())
+def fc_hard_net(x: Tensor, in_kind: int, B: int, in_dim: int, codes: List[Tensor], C: int,
+                wire_r: int) -> Tensor:
+    """Depth-fused packed FC network + GroupSum -> logits ``[B, C]`` (counts)."""
+    return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
+
+
+@fc_hard_net.register_fake
+def _(x, in_kind, B, in_dim, codes, C, wire_r):
+    return x.new_empty((B, C), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::groupsum_packed", mutates_args=())
+def groupsum_packed(xp: Tensor, B: int, C: int) -> Tensor:
+    """Packed ``[W, nw]`` -> per-class counts ``[B, C]`` (no tau)."""
+    return ops.groupsum_packed(xp, B, C)
+
+
+@groupsum_packed.register_fake
+def _(xp, B, C):
+    return xp.new_empty((B, C), dtype=torch.float32)
