@@ -160,6 +160,7 @@ struct HardPrepLayer {
   const float* raw;
   uint2* codes;
   int in_dim, out_dim, K, node;
+  int vec;  // parameters 16-byte aligned: the K = 8 path may use vector loads
 };
 struct HardPrepNet {
   HardPrepLayer L[kMaxPrepLayers];
@@ -173,13 +174,84 @@ __device__ inline uint32_t compact_code(uint2 c) {
   return (c.y & 0x3FFFu) | ((c.x & 0x3FFFu) << 14) | (c.y & 0xF0000000u);
 }
 
+// hard_code for TopK layers with K = 8, every parameter of the output loaded
+// before any is used (16-byte loads: 2 x 8 candidates, 2 x 8 connection
+// logits, the node's 16 or 4 parameters), instead of a load per step of the
+// argmax loops. Same argmax (first index on ties), truth table and clamp.
+__device__ inline uint2 hard_code_k8(const int32_t* __restrict__ cand,
+                                     const float* __restrict__ conn, int o, int IN, int node,
+                                     const float* __restrict__ raw) {
+  const int4* c4 = reinterpret_cast<const int4*>(cand + (int64_t)o * 16);
+  const float4* f4 = reinterpret_cast<const float4*>(conn + (int64_t)o * 16);
+  const int4 ca[4] = {c4[0], c4[1], c4[2], c4[3]};
+  const float4 cf[4] = {f4[0], f4[1], f4[2], f4[3]};
+  float r[16];
+  if (node == SLG_NODE_GATE16) {
+    const float4* r4 = reinterpret_cast<const float4*>(raw + (int64_t)o * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 t = r4[q];
+      r[4 * q] = t.x; r[4 * q + 1] = t.y; r[4 * q + 2] = t.z; r[4 * q + 3] = t.w;
+    }
+  } else {
+    const float4 t = reinterpret_cast<const float4*>(raw + (int64_t)o * 4)[0];
+    r[0] = t.x; r[1] = t.y; r[2] = t.z; r[3] = t.w;
+#pragma unroll
+    for (int i = 4; i < 16; ++i) r[i] = 0.0f;
+  }
+  int idx[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const float c[8] = {cf[2 * s].x, cf[2 * s].y, cf[2 * s].z, cf[2 * s].w,
+                        cf[2 * s + 1].x, cf[2 * s + 1].y, cf[2 * s + 1].z, cf[2 * s + 1].w};
+    int k[8] = {ca[2 * s].x, ca[2 * s].y, ca[2 * s].z, ca[2 * s].w,
+                ca[2 * s + 1].x, ca[2 * s + 1].y, ca[2 * s + 1].z, ca[2 * s + 1].w};
+    // opaque values: the select stays a register select instead of an
+    // indexed read of a stack copy of k
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(k[i]));
+    float bv = c[0];
+    int bi = k[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i)
+      if (c[i] > bv) { bv = c[i]; bi = k[i]; }
+    idx[s] = min(max(bi, 0), IN - 1);
+  }
+  uint32_t tt = 0;
+  if (node == SLG_NODE_GATE16) {
+    float bv = r[0];
+    int bi = 0;
+#pragma unroll
+    for (int i = 1; i < 16; ++i)
+      if (r[i] > bv) { bv = r[i]; bi = i; }
+    tt = c_tt16[bi];
+  } else if (node == SLG_NODE_WALSH) {  // as hard_code
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float u0 = (g >> 1) ? 1.0f : -1.0f, u1 = (g & 1) ? 1.0f : -1.0f;
+      float z = r[0];
+      z = z + r[1] * u0;
+      z = z + r[2] * u1;
+      z = z + r[3] * (u0 * u1);
+      if (z > 0.0f) tt |= 1u << g;
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      if (r[(g >> 1) + 2 * (g & 1)] > 0.0f) tt |= 1u << g;
+  }
+  return make_uint2((uint32_t)idx[0], (uint32_t)idx[1] | (tt << 28));
+}
+
 __global__ void __launch_bounds__(256) fc_hard_prep_net_kernel(HardPrepNet net, int compact) {
   int l = 0;
   while (l + 1 < net.n && (int)blockIdx.x >= net.blk_start[l + 1]) ++l;
   const HardPrepLayer& L = net.L[l];
   const int o = ((int)blockIdx.x - net.blk_start[l]) * blockDim.x + threadIdx.x;
   if (o >= L.out_dim) return;
-  const uint2 c = hard_code(L.cand, L.conn, o, L.K, L.in_dim, L.node, L.raw);
+  const uint2 c = (L.K == 8 && L.conn && L.vec)
+                      ? hard_code_k8(L.cand, L.conn, o, L.in_dim, L.node, L.raw)
+                      : hard_code(L.cand, L.conn, o, L.K, L.in_dim, L.node, L.raw);
   if (compact) reinterpret_cast<uint32_t*>(L.codes)[o] = compact_code(c);
   else L.codes[o] = c;
 }
@@ -826,8 +898,9 @@ int slg_fc_hard_prep_net(int32_t n_layers, const int32_t* const* cand, const flo
                 "fc_hard_prep_net: codes alignment");
     SLG_REQUIRE(!compact || in_dim[l] <= kMaxCompactIn, SLG_E_SHAPE,
                 "fc_hard_prep_net: compact codes need inputs <= %d wide (layer %d)", kMaxCompactIn, l);
+    const int vec = (((uintptr_t)cand[l] | (uintptr_t)conn[l] | (uintptr_t)raw[l]) % 16) == 0;
     net.L[l] = HardPrepLayer{cand[l], conn[l], raw[l], reinterpret_cast<uint2*>(codes[l]),
-                             (int)in_dim[l], (int)out_dim[l], K[l], node_kind[l]};
+                             (int)in_dim[l], (int)out_dim[l], K[l], node_kind[l], vec};
     net.blk_start[l] = (int)blocks;
     blocks += cdiv(out_dim[l], th);
   }
