@@ -405,6 +405,21 @@ int slg_conv_hard_prep(const int32_t* cm, const int32_t* ch, const int32_t* cw,
                        int32_t node_kind, int32_t depth, int32_t arity, const float* raw,
                        int32_t* leaf, uint64_t* tt, slg_stream_t stream);
 
+/* slg_conv_hard_prep for n_blocks (<= 8) conv blocks in one launch (the
+ * hard parameters of every ConvLogicTree of LogicConvNet.forward_hard,
+ * models.py:273-275). Host arrays of length n_blocks hold each block's
+ * arguments (conn[b] NULL = fixed wiring, K[b] = 1); raw holds 4 pointers
+ * per block, raw[4b + l]: for gate16, level l's gate logits
+ * [N, 2^(depth-1-l), 16] read in place (the per-level gate_logits
+ * parameters, layers.py:350-358, walked as layers.py:519-526), slots past
+ * depth unused; for multilinear, raw[4b] = logits [N, 2^arity]. */
+int slg_conv_hard_prep_net(int32_t n_blocks, const int32_t* const* cm,
+                           const int32_t* const* ch, const int32_t* const* cw,
+                           const float* const* conn, const float* const* raw, const int64_t* N,
+                           const int32_t* K, const int32_t* node_kind, const int32_t* depth,
+                           const int32_t* arity, int32_t* const* leaf, uint64_t* const* tt,
+                           slg_stream_t stream);
+
 /* ConvLogicTree.forward_hard + OrPool.forward_hard fused on packed
  * activations (replaces layers.py:529-541,561-563 and the reference's
  * packed_unfold / BitpackedConvTreeLayer / packed_or_pool,

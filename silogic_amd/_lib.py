@@ -76,6 +76,8 @@ SIGNATURES = {
                                             _I32, _P, _I32, _I32, _P, _P]),
     "slg_conv_hard_prep": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P,
                                      _P, _P]),
+    "slg_conv_hard_prep_net": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         _P]),
     "slg_conv_hard_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P,
                                     _I32, _I32, _I32, _P, _P]),
 }

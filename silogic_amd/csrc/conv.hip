@@ -496,39 +496,69 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
   rec[t] = v;
 }
 
-__global__ void conv_hard_prep_kernel(const int* __restrict__ cm, const int* __restrict__ ch,
-                                      const int* __restrict__ cw, const float* __restrict__ conn,
-                                      int N, int leaves, int K, int node, int nodes, int arity,
-                                      const float* __restrict__ raw, int* __restrict__ leaf,
-                                      uint64_t* __restrict__ tt) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+// Hard parameters of up to kMaxConvPrepBlocks conv blocks in one launch, one
+// thread per output channel; workgroups map to blocks through blk_start.
+// gate16 logits are read per tree level in place (level l: [N, 2^(depth-1-l),
+// 16] with row stride rstride[l] floats), the way the reference's hard tree
+// walks its per-level parameters (layers.py:515-527); multilinear nodes use
+// raw[0] = [N, 2^arity].
+constexpr int kMaxConvPrepBlocks = 8;
+struct ConvPrepBlock {
+  const int* cm;
+  const int* ch;
+  const int* cw;
+  const float* conn;
+  const float* raw[4];
+  int rstride[4];
+  int* leaf;
+  uint64_t* tt;
+  int N, leaves, K, node, depth, arity;
+};
+struct ConvPrepNet {
+  ConvPrepBlock b[kMaxConvPrepBlocks];
+  int blk_start[kMaxConvPrepBlocks + 1];
+  int n;
+};
+
+__global__ void __launch_bounds__(128) conv_hard_prep_kernel(ConvPrepNet net) {
+  int k = 0;
+  while (k + 1 < net.n && (int)blockIdx.x >= net.blk_start[k + 1]) ++k;
+  const ConvPrepBlock& P = net.b[k];
+  const int n = ((int)blockIdx.x - net.blk_start[k]) * blockDim.x + threadIdx.x;
+  if (n >= P.N) return;
+  const int leaves = P.leaves, K = P.K;
   for (int l = 0; l < leaves; ++l) {
     const int64_t base = ((int64_t)n * leaves + l) * K;
-    int k = 0;
-    if (conn) {  // first index of the max, as torch.argmax (layers.py:511-513)
-      float bv = conn[base];
+    int c = 0;
+    if (P.conn) {  // first index of the max, as torch.argmax (layers.py:511-513)
+      float bv = P.conn[base];
       for (int j = 1; j < K; ++j)
-        if (conn[base + j] > bv) { bv = conn[base + j]; k = j; }
+        if (P.conn[base + j] > bv) { bv = P.conn[base + j]; c = j; }
     }
-    leaf[n * leaves + l] = (cm[base + k] << 8) | ((ch[base + k] & 15) << 4) | (cw[base + k] & 15);
+    P.leaf[n * leaves + l] =
+        (P.cm[base + c] << 8) | ((P.ch[base + c] & 15) << 4) | (P.cw[base + c] & 15);
   }
   uint64_t t = 0;
-  if (node == SLG_NODE_GATE16) {
-    for (int j = 0; j < nodes; ++j) {
-      const float* g = raw + ((int64_t)n * nodes + j) * 16;
-      int bi = 0;
-      float bv = g[0];
-      for (int i = 1; i < 16; ++i)
-        if (g[i] > bv) { bv = g[i]; bi = i; }
-      t |= (uint64_t)c_tt16_conv[bi] << (4 * j);
+  if (P.node == SLG_NODE_GATE16) {
+    int j = 0;
+    for (int lv = 0; lv < P.depth; ++lv) {
+      const int m = 1 << (P.depth - 1 - lv);
+      const float* row = P.raw[lv] + (int64_t)n * P.rstride[lv];
+      for (int i = 0; i < m; ++i, ++j) {
+        const float* g = row + i * 16;
+        int bi = 0;
+        float bv = g[0];
+        for (int q = 1; q < 16; ++q)
+          if (g[q] > bv) { bv = g[q]; bi = q; }
+        t |= (uint64_t)c_tt16_conv[bi] << (4 * j);
+      }
     }
   } else {
-    const int P = 1 << arity;
-    for (int q = 0; q < P; ++q)
-      if (raw[(int64_t)n * P + q] > 0.0f) t |= 1ull << q;
+    const int Pn = 1 << P.arity;
+    for (int q = 0; q < Pn; ++q)
+      if (P.raw[0][(int64_t)n * P.rstride[0] + q] > 0.0f) t |= 1ull << q;
   }
-  tt[n] = t;
+  P.tt[n] = t;
 }
 
 template <typename T>
@@ -824,19 +854,102 @@ int slg_conv_soft_prep(const float* conn, int64_t N, int32_t leaves, int32_t K, 
   return 0;
 }
 
+static int conv_prep_block(ConvPrepBlock& P, const int32_t* cm, const int32_t* ch,
+                           const int32_t* cw, const float* conn, int64_t N, int32_t K,
+                           int32_t node_kind, int32_t depth, int32_t arity, int32_t* leaf,
+                           uint64_t* tt) {
+  SLG_REQUIRE(cm && ch && cw && leaf && tt, SLG_E_ARG, "conv_hard_prep: null pointer");
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_hard_prep: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(N > 0 && N < (1LL << 31) && N * nleaf < (1LL << 31) && K >= 1 && K <= 64,
+              SLG_E_SHAPE, "conv_hard_prep: sizes");
+  P = ConvPrepBlock{};
+  P.cm = cm;
+  P.ch = ch;
+  P.cw = cw;
+  P.conn = conn;
+  P.leaf = leaf;
+  P.tt = tt;
+  P.N = (int)N;
+  P.leaves = nleaf;
+  P.K = K;
+  P.node = node_kind;
+  P.depth = depth;
+  P.arity = arity;
+  return 0;
+}
+
+static int launch_conv_prep(ConvPrepNet& net, hipStream_t stream) {
+  int blocks = 0;
+  for (int k = 0; k < net.n; ++k) {
+    net.blk_start[k] = blocks;
+    blocks += (int)cdiv(net.b[k].N, 128);
+  }
+  net.blk_start[net.n] = blocks;
+  hipLaunchKernelGGL(conv_hard_prep_kernel, dim3((unsigned)blocks), dim3(128), 0, stream, net);
+  SLG_LAUNCH_CHECK("conv_hard_prep");
+  return 0;
+}
+
 int slg_conv_hard_prep(const int32_t* cm, const int32_t* ch, const int32_t* cw, const float* conn,
                        int64_t N, int32_t leaves, int32_t K, int32_t node_kind, int32_t depth,
                        int32_t arity, const float* raw, int32_t* leaf, uint64_t* tt,
                        slg_stream_t stream) {
-  SLG_REQUIRE(cm && ch && cw && raw && leaf && tt, SLG_E_ARG, "conv_hard_prep: null pointer");
-  const int nleaf = node_leaves(node_kind, depth, arity);
-  SLG_REQUIRE(nleaf > 0 && nleaf == leaves, SLG_E_UNSUPPORTED, "conv_hard_prep: leaves %d", leaves);
-  SLG_REQUIRE(N > 0 && N < (1LL << 31) && K >= 1 && K <= 64, SLG_E_SHAPE, "conv_hard_prep: sizes");
-  hipLaunchKernelGGL(conv_hard_prep_kernel, dim3((unsigned)cdiv(N, 128)), dim3(128), 0,
-                     as_stream(stream), cm, ch, cw, conn, (int)N, leaves, K, node_kind, nleaf - 1,
-                     arity, raw, leaf, tt);
-  SLG_LAUNCH_CHECK("conv_hard_prep");
-  return 0;
+  SLG_REQUIRE(raw, SLG_E_ARG, "conv_hard_prep: null pointer");
+  ConvPrepNet net{};
+  net.n = 1;
+  ConvPrepBlock& P = net.b[0];
+  if (int rc = conv_prep_block(P, cm, ch, cw, conn, N, K, node_kind, depth, arity, leaf, tt))
+    return rc;
+  SLG_REQUIRE(leaves == P.leaves, SLG_E_UNSUPPORTED, "conv_hard_prep: leaves %d", leaves);
+  if (node_kind == SLG_NODE_GATE16) {
+    // concatenated levels [N, 2^depth - 1, 16]: level l starts after the
+    // 2^depth - 2^(depth-l) nodes of the levels before it
+    const int nodes = P.leaves - 1;
+    for (int lv = 0; lv < depth; ++lv) {
+      P.raw[lv] = raw + (int64_t)16 * (P.leaves - (P.leaves >> lv));
+      P.rstride[lv] = nodes * 16;
+    }
+  } else {
+    P.raw[0] = raw;
+    P.rstride[0] = 1 << arity;
+  }
+  return launch_conv_prep(net, as_stream(stream));
+}
+
+int slg_conv_hard_prep_net(int32_t n_blocks, const int32_t* const* cm, const int32_t* const* ch,
+                           const int32_t* const* cw, const float* const* conn,
+                           const float* const* raw, const int64_t* N, const int32_t* K,
+                           const int32_t* node_kind, const int32_t* depth, const int32_t* arity,
+                           int32_t* const* leaf, uint64_t* const* tt, slg_stream_t stream) {
+  SLG_REQUIRE(n_blocks >= 1 && n_blocks <= kMaxConvPrepBlocks, SLG_E_SHAPE,
+              "conv_hard_prep_net: %d blocks outside 1..%d", n_blocks, kMaxConvPrepBlocks);
+  SLG_REQUIRE(cm && ch && cw && conn && raw && N && K && node_kind && depth && arity && leaf && tt,
+              SLG_E_ARG, "conv_hard_prep_net: null array");
+  ConvPrepNet net{};
+  net.n = n_blocks;
+  int64_t total = 0;
+  for (int k = 0; k < n_blocks; ++k) {
+    ConvPrepBlock& P = net.b[k];
+    if (int rc = conv_prep_block(P, cm[k], ch[k], cw[k], conn[k], N[k], K[k], node_kind[k],
+                                 depth[k], arity[k], leaf[k], tt[k]))
+      return rc;
+    total += cdiv(N[k], 128);
+    const float* const* r = raw + 4 * k;
+    if (node_kind[k] == SLG_NODE_GATE16) {
+      for (int lv = 0; lv < depth[k]; ++lv) {
+        SLG_REQUIRE(r[lv], SLG_E_ARG, "conv_hard_prep_net: block %d level %d logits null", k, lv);
+        P.raw[lv] = r[lv];
+        P.rstride[lv] = 16 << (depth[k] - 1 - lv);
+      }
+    } else {
+      SLG_REQUIRE(r[0], SLG_E_ARG, "conv_hard_prep_net: block %d logits null", k);
+      P.raw[0] = r[0];
+      P.rstride[0] = 1 << arity[k];
+    }
+  }
+  SLG_REQUIRE(total < (1LL << 31), SLG_E_SHAPE, "conv_hard_prep_net: sizes");
+  return launch_conv_prep(net, as_stream(stream));
 }
 
 int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64_t nw, int64_t N,

@@ -390,15 +390,23 @@ class ConvLogicTree(nn.Module):
         """``OrPool(2)(self(x))`` in one kernel (only the pooled map is written)."""
         return self._soft(x, pool=True)
 
-    def hard_params(self):
+    def hard_spec(self):
+        """Arguments of ``ops.conv_hard_prep_net`` for this block: taps,
+        connection logits and the node logits per tree level, read in place."""
         cm, ch, cw = self._taps()
         conn = None if self.connect == "fixed" else self.conn
-        return ops.conv_hard_prep(cm, ch, cw, conn, self._raw(), self._kind(), self.d,
-                                  self.node_arity)
+        levels = (list(self.gate_logits) if self.node_name == "gate16"
+                  else [self.tree_nodes[0].logits])
+        return cm, ch, cw, conn, levels, self._kind(), self.d, self.node_arity
 
-    def packed_forward(self, xp, chw, pool):
-        """Packed ``[C,H,W,nw]`` -> ``[n,Ho,Wo,nw]`` (2x2 OR-pooled if ``pool``)."""
-        leaf, tt = self.hard_params()
+    def hard_params(self):
+        """``(leaf [n, leaves] int32, tt [n] int64)`` of the hard forward."""
+        return ops.conv_hard_prep_net([self.hard_spec()])[0]
+
+    def packed_forward(self, xp, chw, pool, params=None):
+        """Packed ``[C,H,W,nw]`` -> ``[n,Ho,Wo,nw]`` (2x2 OR-pooled if ``pool``);
+        ``params`` = ``hard_params()`` when the caller computed them already."""
+        leaf, tt = self.hard_params() if params is None else params
         return ops.conv_hard(xp, chw, leaf, tt, self._kind(), self.d, self.node_arity,
                              self.kh, self.padding, pool)
 

@@ -262,9 +262,11 @@ class LogicConvNet(nn.Module):
         xp = ops._words_for(xp, B, "forward_hard_packed")
         if xp.shape[0] != C * H * W:
             raise ValueError("forward_hard_packed: %d rows for C*H*W = %d" % (xp.shape[0], C * H * W))
-        for conv in self._convs():
+        convs = list(self._convs())
+        params = ops.conv_hard_prep_net([conv.hard_spec() for conv in convs])
+        for conv, prm in zip(convs, params):
             x_in = xp
-            xp = conv.packed_forward(xp, (C, H, W), pool=True)
+            xp = conv.packed_forward(xp, (C, H, W), pool=True, params=prm)
             Ho, Wo = conv._hw_out(H, W)
             if self.wire_residual > 0:
                 # the first r channels copy the input before the OR-pool

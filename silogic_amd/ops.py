@@ -821,6 +821,58 @@ def conv_hard_prep(cm, ch, cw, conn, raw, node_kind, depth, arity):
     return leaf, tt
 
 
+MAX_CONV_PREP_BLOCKS = 8
+
+
+def conv_hard_prep_net(specs):
+    """Hard parameters of several conv blocks, one launch per 8 blocks.
+    ``specs``: ``(cm, ch, cw, conn or None, raw_levels, node_kind, depth,
+    arity)`` per block, ``raw_levels`` a list of the gate16 per-level logits
+    ``[N, 2^(depth-1-l), 16]`` or ``[logits [N, 2^arity]]``. Returns
+    ``[(leaf [N, leaves] int32, tt [N] int64)]``."""
+    out = []
+    for g in range(0, len(specs), MAX_CONV_PREP_BLOCKS):
+        part = specs[g:g + MAX_CONV_PREP_BLOCKS]
+        keep, cms, chs, cws, conns, raws, Ns, Ks, kinds, depths, ars, leafs, tts = \
+            [], [], [], [], [], [], [], [], [], [], [], [], []
+        for cm, ch, cw, conn, levels, kind, depth, arity in part:
+            require_gpu(cm, *levels)
+            cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
+            N, leaves, K = cm.shape
+            if ch.shape != cm.shape or cw.shape != cm.shape or (
+                    conn is not None and tuple(conn.shape) != (N, leaves, K)):
+                raise ValueError("conv_hard_prep_net: tap/conn shapes are inconsistent")
+            if kind == GATE16:
+                want = [(N, 2 ** (depth - 1 - l), 16) for l in range(depth)]
+            else:
+                want = [(N, 2 ** arity)]
+            if [tuple(t.shape) for t in levels] != want:
+                raise ValueError("conv_hard_prep_net: logits %s for node kind %d depth %d arity %d"
+                                 % ([tuple(t.shape) for t in levels], kind, depth, arity))
+            levels = [_c(t, torch.float32) for t in levels]
+            conn = _c(conn, torch.float32)
+            keep += [cm, ch, cw, conn] + levels
+            cms.append(cm)
+            chs.append(ch)
+            cws.append(cw)
+            conns.append(conn)
+            raws += levels + [None] * (4 - len(levels))
+            Ns.append(N)
+            Ks.append(K)
+            kinds.append(int(kind))
+            depths.append(int(depth))
+            ars.append(int(arity))
+            leafs.append(torch.empty((N, leaves), device=cm.device, dtype=torch.int32))
+            tts.append(torch.empty((N,), device=cm.device, dtype=torch.int64))
+        n = len(part)
+        _lib.call("slg_conv_hard_prep_net", n, _ptrs(cms), _ptrs(chs), _ptrs(cws), _ptrs(conns),
+                  _ptrs(raws), (ctypes.c_int64 * n)(*Ns), (ctypes.c_int32 * n)(*Ks),
+                  (ctypes.c_int32 * n)(*kinds), (ctypes.c_int32 * n)(*depths),
+                  (ctypes.c_int32 * n)(*ars), _ptrs(leafs), _ptrs(tts), _stream(cms[0]))
+        out.extend(zip(leafs, tts))
+    return out
+
+
 def conv_hard(xp, shape_chw, leaf, tt, node_kind, depth, arity, kernel, pad, pool):
     """Packed conv: ``xp`` [C,H,W,nw] -> [N,Ho,Wo,nw] (pooled if ``pool``)."""
     require_gpu(xp, leaf, tt)

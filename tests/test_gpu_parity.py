@@ -416,7 +416,7 @@ def test_wire_residual_hard_and_soft():
         assert_soft_close(model(x.to(DEV)), torch_ref.forward(spec, sd, x, ste=False), "logits")
 
 
-@pytest.mark.parametrize("depth", [1, 2, 3])
+@pytest.mark.parametrize("depth", [1, 2, 3, 4])
 @pytest.mark.parametrize("connect", ["topk", "fixed"])
 def test_conv_gate16_depths(depth, connect):
     conv = sl.ConvLogicTree(6, 12, kernel=3, tree_depth=depth, connect=connect, k=4, n_chan=2,
@@ -432,6 +432,32 @@ def test_conv_gate16_depths(depth, connect):
                           torch_ref.orpool_soft(torch_ref.conv_soft(blk, sd, x)), "pooled")
     xb = random_bits(70, 6, 9, 11)
     assert torch.equal(conv.forward_hard(xb.to(DEV)).cpu(), torch_ref.conv_hard(blk, sd, xb))
+
+
+def test_conv_hard_prep_net_blocks():
+    """One launch for the hard parameters of blocks of every node kind,
+    gate16 logits read per level in place, against the single-block entry
+    point on the concatenated levels; more than 8 blocks split launches."""
+    blocks = []
+    for i, (node, depth, arity, connect) in enumerate(
+            [("gate16", 1, 2, "topk"), ("gate16", 2, 2, "fixed"), ("gate16", 3, 2, "topk"),
+             ("gate16", 4, 2, "topk"), ("multilinear", 1, 3, "topk"), ("hybrid", 1, 4, "topk"),
+             ("gate16", 2, 2, "topk"), ("multilinear", 1, 2, "fixed"), ("gate16", 3, 2, "fixed")]):
+        conv = sl.ConvLogicTree(4, 130 + 70 * i, kernel=3, tree_depth=depth, connect=connect, k=5,
+                                n_chan=2, node=node, arity=arity, residual_init=False, seed=i)
+        blocks.append(conv.to(DEV).eval())
+    got = ops.conv_hard_prep_net([b.hard_spec() for b in blocks])
+    assert len(got) == len(blocks)
+    for b, (leaf, tt) in zip(blocks, got):
+        cm, ch, cw = b._taps()
+        want = ops.conv_hard_prep(cm, ch, cw, None if b.connect == "fixed" else b.conn, b._raw(),
+                                  b._kind(), b.d, b.node_arity)
+        assert torch.equal(leaf, want[0]) and torch.equal(tt, want[1])
+        assert torch.equal(b.hard_params()[1], tt)
+    bad = list(blocks[2].hard_spec())
+    bad[4] = bad[4][::-1]   # levels out of order
+    with pytest.raises(ValueError):
+        ops.conv_hard_prep_net([bad])
 
 
 @pytest.mark.parametrize("node", ["multilinear", "hybrid"])
