@@ -833,8 +833,8 @@ def conv_hard_prep_net(specs):
     out = []
     for g in range(0, len(specs), MAX_CONV_PREP_BLOCKS):
         part = specs[g:g + MAX_CONV_PREP_BLOCKS]
-        keep, cms, chs, cws, conns, raws, Ns, Ks, kinds, depths, ars, leafs, tts = \
-            [], [], [], [], [], [], [], [], [], [], [], [], []
+        cms, chs, cws, conns, raws, Ns, Ks, kinds, depths, ars, leafs, tts = \
+            [], [], [], [], [], [], [], [], [], [], [], []
         for cm, ch, cw, conn, levels, kind, depth, arity in part:
             require_gpu(cm, *levels)
             cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
@@ -851,7 +851,6 @@ def conv_hard_prep_net(specs):
                                  % ([tuple(t.shape) for t in levels], kind, depth, arity))
             levels = [_c(t, torch.float32) for t in levels]
             conn = _c(conn, torch.float32)
-            keep += [cm, ch, cw, conn] + levels
             cms.append(cm)
             chs.append(ch)
             cws.append(cw)
