@@ -100,11 +100,12 @@ int slg_fc_soft_prep(const float* conn, int64_t OUT, int32_t K, int32_t node_kin
                      const float* raw, float* w, float* node_param, slg_stream_t stream);
 
 /* The soft parameters of n_layers (<= 16) FC layers in one launch, as one
- * record per output: 4(K+1) 32-bit words idx_a[K], idx_b[K] (int32,
- * clamped into [0, in_dim)), w_a[K], w_b[K] (fp32 softmax over K),
- * node_param[4] (fp32, as slg_fc_soft_prep), stored as K+1 quads of 4 words
- * in a chunk-major layout: quad q of output o at quad index
- * ((o / 64) * (K+1) + q) * 64 + o % 64. rec[l] holds ceil(out_dim/64)*64
+ * record per output of RQ = (3K+3)/4 + 1 quads of 32-bit words: K words
+ * idx_a[k] | idx_b[k] << 16 (clamped into [0, in_dim), in_dim <= 65536),
+ * w_a[K], w_b[K] (fp32 softmax over K), zeros up to quad RQ-1, then
+ * node_param[4] (fp32, as slg_fc_soft_prep) in quad RQ-1, in a chunk-major
+ * layout: quad q of output o at quad index ((o / 64) * RQ + q) * 64 + o % 64.
+ * rec[l] holds ceil(out_dim/64)*64
  * records (the padding repeats the last output). The inputs of layer l are
  * cand[l] [out_dim,2,K] int32, conn[l] [out_dim,2,K] (NULL = fixed wiring)
  * and raw[l] as in slg_fc_soft_prep; order (may be NULL, or hold NULLs) gives

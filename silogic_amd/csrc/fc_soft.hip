@@ -397,9 +397,10 @@ __global__ void fc_soft_prep_kernel(const float* __restrict__ conn, int OUT, int
   reinterpret_cast<float4*>(np)[o] = node_param(node, raw, o);
 }
 
-// Records of several layers in one launch. Output o's record is 4(K+1)
-// 32-bit words: idx_a[K] idx_b[K] (int32, clamped into [0, IN)), w_a[K]
-// w_b[K] (softmax), param[4], stored as K+1 quads in the chunk-major layout
+// Records of several layers in one launch. Output o's record is
+// rec_quads(K) quads of 32-bit words: idx_a[k] | idx_b[k] << 16 (clamped into
+// [0, IN)) for k < K, w_a[K] w_b[K] (softmax), zeros to a whole quad,
+// param[4], in the chunk-major layout
 // read by load_params<.., REC = true>; outputs past OUT up to the next
 // multiple of 64 repeat output OUT-1. With a gather order (from
 // slg_fc_soft_schedule), step t of slot s holds candidate order[o][s][t].
@@ -428,24 +429,28 @@ __global__ void __launch_bounds__(256) fc_soft_records_kernel(RecNet net) {
   if (op >= n_pad) return;
   const int o = min(op, L.out_dim - 1);
   const int K = net.K;
-  float* base = L.rec + ((int64_t)(op >> 6) * (K + 1) * 64 + (op & 63)) * 4;
+  const int RQ = rec_quads(K);
+  float* base = L.rec + ((int64_t)(op >> 6) * RQ * 64 + (op & 63)) * 4;
   auto put = [&](int w, float v) { base[(w >> 2) * 256 + (w & 3)] = v; };
-  for (int s = 0; s < 2; ++s) {
-    const int64_t cb = ((int64_t)o * 2 + s) * K;
-    float w[16];
-    softmax_k(L.conn ? L.conn + cb : nullptr, K, w);
-    for (int t = 0; t < K; ++t) {
-      const int k = L.order ? min((int)L.order[cb + t], K - 1) : t;
-      const int idx = min(max(L.cand[cb + k], 0), L.in_dim - 1);
-      put(s * K + t, __int_as_float(idx));
-      put(2 * K + s * K + t, w[k]);
-    }
+  const int64_t ca = (int64_t)o * 2 * K, cb = ca + K;  // slot a, slot b
+  float wa[16], wb[16];
+  softmax_k(L.conn ? L.conn + ca : nullptr, K, wa);
+  softmax_k(L.conn ? L.conn + cb : nullptr, K, wb);
+  for (int t = 0; t < K; ++t) {
+    const int ka = L.order ? min((int)L.order[ca + t], K - 1) : t;
+    const int kb = L.order ? min((int)L.order[cb + t], K - 1) : t;
+    const uint32_t ia = (uint32_t)min(max(L.cand[ca + ka], 0), L.in_dim - 1);
+    const uint32_t ib = (uint32_t)min(max(L.cand[cb + kb], 0), L.in_dim - 1);
+    put(t, __uint_as_float(ia | (ib << 16)));
+    put(K + t, wa[ka]);
+    put(2 * K + t, wb[kb]);
   }
+  for (int w = 3 * K; w < 4 * (RQ - 1); ++w) put(w, 0.0f);
   const float4 p = node_param(L.node, L.raw, o);
-  put(4 * K + 0, p.x);
-  put(4 * K + 1, p.y);
-  put(4 * K + 2, p.z);
-  put(4 * K + 3, p.w);
+  put(4 * (RQ - 1) + 0, p.x);
+  put(4 * (RQ - 1) + 1, p.y);
+  put(4 * (RQ - 1) + 2, p.z);
+  put(4 * (RQ - 1) + 3, p.w);
 }
 
 // Bank-aware gather order. The soft kernel gathers one candidate per lane
@@ -615,6 +620,10 @@ int slg_fc_soft_records(int32_t n_layers, const int32_t* const* cand, const floa
     SLG_REQUIRE(cand[l] && raw[l] && rec[l], SLG_E_ARG, "fc_soft_records: null pointer, layer %d", l);
     SLG_REQUIRE(in_dim[l] > 0 && in_dim[l] < (1LL << 28) && out_dim[l] > 0 &&
                     out_dim[l] < (1LL << 28), SLG_E_SHAPE, "fc_soft_records: bad sizes, layer %d", l);
+    // records hold 16-bit input indices (inputs the soft kernels stage in LDS
+    // are far narrower)
+    SLG_REQUIRE(in_dim[l] <= 65536, SLG_E_UNSUPPORTED,
+                "fc_soft_records: in_dim %lld above 65536, layer %d", (long long)in_dim[l], l);
     SLG_REQUIRE(node_kind[l] >= 0 && node_kind[l] <= 2, SLG_E_ARG,
                 "fc_soft_records: node_kind %d", node_kind[l]);
     SLG_REQUIRE(((uintptr_t)rec[l] % 16) == 0, SLG_E_ARG, "fc_soft_records: rec alignment");

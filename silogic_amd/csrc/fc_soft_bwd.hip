@@ -60,31 +60,34 @@ __device__ inline void node_grad(float a, float b, float g, const float4& p, flo
 
 // Records from separate arrays: cand [OUT,2,K] int32 (clamped to IN),
 // w [OUT,2,K], np [OUT,4] -> the chunk-major records of fc_soft_kernel
-// (quad q of output o at ((o/64)*(K+1)+q)*64 + o%64; words idx_a, idx_b,
-// w_a, w_b, params). One thread per record word.
+// (quad q of output o at ((o/64)*rec_quads(K)+q)*64 + o%64; words
+// idx_a | idx_b << 16, w_a, w_b, zero padding, params). One thread per
+// record word.
 __global__ void __launch_bounds__(256) fc_soft_pack_records_kernel(const int* __restrict__ cand,
                                                                    const float* __restrict__ w,
                                                                    const float* __restrict__ np,
                                                                    int OUT, int K, int IN,
                                                                    float* __restrict__ rec) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nq = (int64_t)((OUT + 63) / 64) * (K + 1) * 64;
+  const int RQ = rec_quads(K);
+  const int64_t nq = (int64_t)((OUT + 63) / 64) * RQ * 64;
   if (t >= nq * 4) return;
   const int e = (int)(t & 3);
   const int64_t Q = t >> 2;
   const int lane = (int)(Q % 64);
-  const int q = (int)((Q / 64) % (K + 1));
-  const int c = (int)(Q / (64 * (int64_t)(K + 1)));
+  const int q = (int)((Q / 64) % RQ);
+  const int c = (int)(Q / (64 * (int64_t)RQ));
   const int o = min(c * 64 + lane, OUT - 1);
   const int word = q * 4 + e;
-  float v;
-  if (word < 2 * K) {
-    const int i = cand[(int64_t)o * 2 * K + word];  // side = word / K, k = word % K
-    v = __int_as_float(min(max(i, 0), IN - 1));
-  } else if (word < 4 * K) {
-    v = w[(int64_t)o * 2 * K + (word - 2 * K)];
-  } else {
-    v = np[(int64_t)o * 4 + (word - 4 * K)];
+  float v = 0.0f;
+  if (word < K) {
+    const uint32_t ia = (uint32_t)min(max(cand[(int64_t)o * 2 * K + word], 0), IN - 1);
+    const uint32_t ib = (uint32_t)min(max(cand[(int64_t)o * 2 * K + K + word], 0), IN - 1);
+    v = __uint_as_float(ia | (ib << 16));
+  } else if (word < 3 * K) {
+    v = w[(int64_t)o * 2 * K + (word - K)];  // w_a then w_b
+  } else if (word >= 4 * (RQ - 1)) {
+    v = np[(int64_t)o * 4 + (word - 4 * (RQ - 1))];
   }
   rec[t] = v;
 }
@@ -462,7 +465,7 @@ static BwdPlan bwd_plan(int64_t B, int64_t IN, int64_t OUT, int K) {
   p.tiles_per_range = (int)cdiv(n_tiles, p.NR);
   p.NR = (int)cdiv(n_tiles, p.tiles_per_range);
   const int64_t LB = cdiv(std::max<int64_t>(B, 1), kGatherSamples) * kGatherSamples;
-  p.rec_floats = cdiv(OUT, 64) * 64 * (int64_t)(K + 1) * 4;
+  p.rec_floats = cdiv(OUT, 64) * 64 * (int64_t)rec_quads(K) * 4;
   p.part_floats = round4((int64_t)p.NR * (2 * K + 4) * OUT);
   p.gbr_floats = 2 * OUT * LB;  // rows b < n_tiles * Sw <= LB
   p.in_floats = fc_input_grad_floats(B, IN, OUT, 2, K);
@@ -539,7 +542,8 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
                   (int64_t)B * IN < (1LL << 40),
               SLG_E_SHAPE, "fc_soft_bwd: bad sizes");
   const BwdPlan p = bwd_plan(B, IN, OUT, K);
-  SLG_REQUIRE(p.Sw, SLG_E_UNSUPPORTED, "fc_soft_bwd: IN=%lld does not fit LDS", (long long)IN);
+  SLG_REQUIRE(p.Sw && IN <= 65536, SLG_E_UNSUPPORTED, "fc_soft_bwd: IN=%lld does not fit LDS",
+              (long long)IN);
   SLG_REQUIRE(workspace_floats >= p.total(), SLG_E_ARG,
               "fc_soft_bwd: workspace of %lld floats, %lld needed", (long long)workspace_floats,
               (long long)p.total());

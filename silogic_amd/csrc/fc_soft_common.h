@@ -125,8 +125,13 @@ struct ParamView {
   const float* wb;
   const float* np;
   int cstride, wstride, npstride;
-  const float* rec;  // records (REC kernels): [ceil(OUT/64)][K+1][64][4] words
+  const float* rec;  // records (REC kernels): [ceil(OUT/64)][rec_quads(K)][64][4] words
 };
+
+// Quads per output record: K index words (idx_a | idx_b << 16, inputs below
+// 65536), K words w_a, K words w_b, zero padding to a whole quad, then one
+// quad of node parameters.
+__host__ __device__ constexpr int rec_quads(int K) { return (3 * K + 3) / 4 + 1; }
 
 // Per-output parameters held in registers: 2K candidate indices, 2K weights,
 // 4 node coefficients.
@@ -141,27 +146,30 @@ struct FcParams {
 // The loads are unconditional straight-line code, so the compiler's wait
 // counts stay exact across loop iterations.
 //
-// Records (REC): output o's K+1 quads of 4 words live at quad index
-// ((o / 64) * (K+1) + q) * 64 + o % 64, so one 16-byte load per quad moves
-// 1 KB of contiguous memory for the 64 outputs of a wave. Quads 0..K/4-1 hold
-// idx_a, then idx_b, w_a, w_b, and quad K the node parameters.
+// Records (REC): output o's rec_quads(K) quads of 4 words live at quad index
+// ((o / 64) * rec_quads(K) + q) * 64 + o % 64, so one 16-byte load per quad
+// moves 1 KB of contiguous memory for the 64 outputs of a wave. Words 0..K-1
+// hold idx_a | idx_b << 16, K..2K-1 w_a, 2K..3K-1 w_b, and the last quad the
+// node parameters. The soft kernels re-read every record once per sample
+// tile, so the 16-bit index pairs cut their record traffic by two quads of
+// nine at K = 8.
 template <int KC, int KM, bool REC>
 __device__ inline void load_params(FcParams<KM>& P, int o, int K, const ParamView& pv) {
   if constexpr (REC) {
+    const int RQ = rec_quads(K);
     const f32x4* r = reinterpret_cast<const f32x4*>(pv.rec) +
-                     ((int64_t)(o >> 6) * (K + 1)) * 64 + (o & 63);
+                     ((int64_t)(o >> 6) * RQ) * 64 + (o & 63);
     if constexpr (KC > 0 && (KC % 4) == 0) {
       constexpr int Q = KC / 4;
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
-        const i32x4 a4 = __builtin_bit_cast(i32x4, r[(0 * Q + q) * 64]);
-        const i32x4 b4 = __builtin_bit_cast(i32x4, r[(1 * Q + q) * 64]);
-        const f32x4 u4 = r[(2 * Q + q) * 64];
-        const f32x4 v4 = r[(3 * Q + q) * 64];
+        const i32x4 c4 = __builtin_bit_cast(i32x4, r[(0 * Q + q) * 64]);
+        const f32x4 u4 = r[(1 * Q + q) * 64];
+        const f32x4 v4 = r[(2 * Q + q) * 64];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          P.ia[4 * q + e] = a4[e];
-          P.ib[4 * q + e] = b4[e];
+          P.ia[4 * q + e] = (int)((uint32_t)c4[e] & 0xFFFFu);
+          P.ib[4 * q + e] = (int)((uint32_t)c4[e] >> 16);
           P.fa[4 * q + e] = u4[e];
           P.fb[4 * q + e] = v4[e];
         }
@@ -173,16 +181,17 @@ __device__ inline void load_params(FcParams<KM>& P, int o, int K, const ParamVie
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
         if (k < K) {
-          P.ia[k] = __float_as_int(word(k));
-          P.ib[k] = __float_as_int(word(K + k));
-          P.fa[k] = word(2 * K + k);
-          P.fb[k] = word(3 * K + k);
+          const uint32_t c = __float_as_uint(word(k));
+          P.ia[k] = (int)(c & 0xFFFFu);
+          P.ib[k] = (int)(c >> 16);
+          P.fa[k] = word(K + k);
+          P.fb[k] = word(2 * K + k);
         } else {
           P.ia[k] = 0; P.ib[k] = 0; P.fa[k] = 0.f; P.fb[k] = 0.f;
         }
       }
     }
-    const f32x4 p4 = r[K * 64];
+    const f32x4 p4 = r[(RQ - 1) * 64];
     P.p = make_float4(p4[0], p4[1], p4[2], p4[3]);
     return;
   }

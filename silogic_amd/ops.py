@@ -261,7 +261,7 @@ def fc_soft_records(specs, K):
     16 layers. ``specs``: ``(cand [OUT,2,K], conn [OUT,2,K] or None, raw,
     in_dim, node_kind, order or None)`` per layer (``raw``: gate logits
     [OUT,16], walsh theta or multilinear logits [OUT,4]; ``order`` from
-    :func:`fc_soft_schedule`). Returns ``[ceil(OUT/64), K+1, 64, 4]`` float32
+    :func:`fc_soft_schedule`). Returns ``[ceil(OUT/64), record_quads(K), 64, 4]`` float32
     tensors (the chunk-major record layout; index words reinterpreted)."""
     recs = []
     for g in range(0, len(specs), MAX_RECORD_LAYERS):
@@ -285,7 +285,8 @@ def fc_soft_records(specs, K):
             outs.append(OUT)
             kinds.append(int(kind))
         dev = raws[0].device
-        out = [torch.empty(((o + 63) // 64, K + 1, 64, 4), device=dev, dtype=torch.float32)
+        out = [torch.empty(((o + 63) // 64, record_quads(K), 64, 4), device=dev,
+                           dtype=torch.float32)
                for o in outs]
         n = len(part)
         _lib.call("slg_fc_soft_records", n, _ptrs(cands), _ptrs(conns), _ptrs(raws),
@@ -295,14 +296,22 @@ def fc_soft_records(specs, K):
     return recs
 
 
+def record_quads(K):
+    """Quads per soft FC record: K index words (idx_a | idx_b << 16), K words
+    w_a, K words w_b, zero padding to a whole quad, one quad of node
+    parameters."""
+    return (3 * K + 3) // 4 + 1
+
+
 def record_words(rec, out_dim):
-    """``[OUT, 4(K+1)]`` view of chunk-major records (for inspection)."""
+    """``[OUT, 4 * record_quads(K)]`` view of chunk-major records (for
+    inspection)."""
     n64, K1 = rec.shape[0], rec.shape[1]
     return rec.permute(0, 2, 1, 3).reshape(n64 * 64, 4 * K1)[:out_dim]
 
 
 def _check_rec(x, rec, out_dim, K):
-    if rec.dim() != 4 or tuple(rec.shape) != ((out_dim + 63) // 64, K + 1, 64, 4) or \
+    if rec.dim() != 4 or tuple(rec.shape) != ((out_dim + 63) // 64, record_quads(K), 64, 4) or \
             rec.dtype != torch.float32 or not rec.is_contiguous():
         raise ValueError(f"fc_soft: records {tuple(rec.shape)} {rec.dtype} for OUT={out_dim}, K={K}")
     if x.dim() != 2:

@@ -245,11 +245,14 @@ def test_records_of_mixed_layers_in_one_launch():
             order = layer.gather_order().long().cpu()                     # [OUT, 2, 8]
             assert torch.equal(order.sort(dim=2).values,
                                torch.arange(8).expand(OUT, 2, 8))        # a permutation
-            idx = words[:, :16].contiguous().view(torch.int32).view(OUT, 2, 8)
+            assert words.shape == (OUT, 4 * ops.record_quads(8)) == (OUT, 28)
+            pair = words[:, :8].contiguous().view(torch.int32).long() & 0xFFFFFFFF
+            idx = torch.stack([pair & 0xFFFF, pair >> 16], dim=1).to(torch.int32)  # [OUT,2,8]
             cand = sd[L["prefix"] + "_conn.cand"].to(torch.int32)
             assert torch.equal(idx, torch.gather(cand, 2, order))
             ref_w = torch.gather(torch.softmax(sd[L["prefix"] + "_conn.conn"], dim=2), 2, order)
-            assert_soft_close(words[:, 16:32].reshape(OUT, 2, 8), ref_w, "softmax weights")
+            assert_soft_close(words[:, 8:24].reshape(OUT, 2, 8), ref_w, "softmax weights")
+            assert not words[:, 24:28].isnan().any()   # node parameters in the last quad
             # natural order records give the same layer output within tolerance
             spec_nat = layer.record_spec()[:5] + (None,)
             rec_nat = ops.fc_soft_records([spec_nat], 8)[0]
