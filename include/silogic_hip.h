@@ -179,6 +179,18 @@ int slg_fc_lut_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int3
                         int32_t K, const int32_t* cand, const float* w, const float* s,
                         int32_t hybrid, float* y, float* workspace, int64_t workspace_floats,
                         slg_stream_t stream);
+/* slg_fc_lut_soft_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc); no counterpart in the reference. The
+ * records live in a static device array of the library (16 MiB per GPU,
+ * held until the process ends): layers needing more than 4 Mi record floats
+ * (slg_fc_lut_soft_workspace; about 26 000 outputs at arity 6, K = 8) are
+ * rejected with SLG_E_SHAPE. Every call on one GPU uses that GPU's one
+ * array, so calls that overlap on a GPU (different streams or threads) race;
+ * calls in one stream are ordered and safe. Allocates nothing. */
+int slg_fc_lut_soft_fwd_noalloc(const float* x, int64_t B, int64_t IN, int64_t OUT,
+                                int32_t arity, int32_t K, const int32_t* cand, const float* w,
+                                const float* s, int32_t hybrid, float* y, slg_stream_t stream);
 /* Backward of both (the gradient of the multilinear form, the hybrid node's
  * surrogate): gy [B,OUT] -> gx [B,IN], gw [OUT,n,K], gs [OUT,2^n]; any of the
  * three may be NULL. Every sum runs in a fixed order (the reference adds gx

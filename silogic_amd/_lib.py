@@ -51,6 +51,8 @@ SIGNATURES = {
     "slg_fc_lut_soft_workspace": (C.c_int64, [_I64, _I32, _I32]),
     "slg_fc_lut_soft_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _I32, _P, _P,
                                       _I64, _P]),
+    "slg_fc_lut_soft_fwd_noalloc": (C.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _I32,
+                                              _P, _P]),
     "slg_fc_lut_soft_bwd_workspace": (C.c_int64, [_I64, _I64, _I64, _I32, _I32]),
     "slg_fc_lut_soft_bwd": (C.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P,
                                       _P, _P, _I64, _P]),

@@ -31,6 +31,8 @@
 #include "fc_bwd_input.h"
 #include "fc_soft_common.h"
 
+#include <mutex>
+
 extern "C" int64_t slg_fc_lut_soft_workspace(int64_t OUT, int32_t arity, int32_t K);
 
 namespace slg {
@@ -40,12 +42,13 @@ namespace slg {
 __host__ __device__ constexpr int lut_nslot(int na, int km) { return 2 * na * km + (1 << na); }
 
 // Records from cand [OUT,n,K] int32 (clamped to IN), w [OUT,n,K] and s
-// [OUT,2^n]; K padded to KM with weight 0. One thread per record word.
+// [OUT,2^n]; K padded to KM with weight 0. One thread per record word; the
+// words are written as integers (index words are not float values).
 __global__ void __launch_bounds__(256) fc_lut_pack_kernel(const int* __restrict__ cand,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ s, int OUT,
                                                           int NA, int K, int KM, int IN,
-                                                          float* __restrict__ rec) {
+                                                          uint32_t* __restrict__ rec) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int nslot = lut_nslot(NA, KM);
   const int64_t n = (int64_t)((OUT + 63) / 64) * nslot * 64;
@@ -56,18 +59,18 @@ __global__ void __launch_bounds__(256) fc_lut_pack_kernel(const int* __restrict_
   const int chunk = (int)(q / nslot);
   const int o = min(chunk * 64 + lane, OUT - 1);
   const int NK = NA * KM;
-  float v;
+  uint32_t v;
   if (slot < 2 * NK) {
     const int jk = slot < NK ? slot : slot - NK;
     const int j = jk / KM, k = jk - j * KM;
     if (k >= K) {
-      v = slot < NK ? __int_as_float(0) : 0.0f;
+      v = 0u;  // index 0 / weight +0.0f
     } else {
       const int64_t idx = ((int64_t)o * NA + j) * K + k;
-      v = slot < NK ? __int_as_float(min(max(cand[idx], 0), IN - 1)) : w[idx];
+      v = slot < NK ? (uint32_t)min(max(cand[idx], 0), IN - 1) : __float_as_uint(w[idx]);
     }
   } else {
-    v = s[(int64_t)o * (1 << NA) + (slot - 2 * NK)];
+    v = __float_as_uint(s[(int64_t)o * (1 << NA) + (slot - 2 * NK)]);
   }
   rec[t] = v;
 }
@@ -580,6 +583,72 @@ static int lut_bwd_k(const float* x, int64_t B, int64_t IN, int64_t OUT, const f
   return lut_bwd_t<NA, 8>(x, B, IN, OUT, rec, gy, p, gbr, arows, partw, partc, st);
 }
 
+// The forward of both entry points: records into `rec` (rec_floats long),
+// then the layer.
+static int lut_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t arity,
+                        int32_t K, const int32_t* cand, const float* w, const float* s,
+                        int32_t hybrid, float* y, float* rec, int64_t rec_floats, hipStream_t st,
+                        const char* what) {
+  SLG_REQUIRE(cand && w && s && ((x && y) || B == 0), SLG_E_ARG, "%s: null pointer", what);
+  SLG_REQUIRE(arity >= 2 && arity <= 6 && K >= 1 && K <= 8, SLG_E_SHAPE,
+              "%s: arity %d / K %d outside 2..6 / 1..8", what, arity, K);
+  SLG_REQUIRE(B >= 0 && IN > 0 && OUT > 0 && B < (1LL << 31) && IN < (1LL << 28) &&
+                  OUT < (1LL << 26),
+              SLG_E_SHAPE, "%s: bad sizes", what);
+  const int S = lut_tile(IN);
+  SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "%s: IN=%lld does not fit LDS", what, (long long)IN);
+  const int KM = lut_km(K);
+  const int64_t need = slg_fc_lut_soft_workspace(OUT, arity, K);
+  SLG_REQUIRE(rec_floats >= need, SLG_E_ARG, "%s: workspace of %lld floats, %lld needed", what,
+              (long long)rec_floats, (long long)need);
+  hipLaunchKernelGGL(fc_lut_pack_kernel, dim3((unsigned)cdiv(need, 256)), dim3(256), 0, st, cand,
+                     w, s, (int)OUT, arity, K, KM, (int)IN, reinterpret_cast<uint32_t*>(rec));
+  SLG_LAUNCH_CHECK("fc_lut_pack");
+  if (B == 0) return 0;
+  return hybrid ? lut_fwd_n<true>(arity, KM, S, x, B, IN, OUT, rec, y, st)
+                : lut_fwd_n<false>(arity, KM, S, x, B, IN, OUT, rec, y, st);
+}
+
+// Static scratch of slg_fc_lut_soft_fwd_noalloc: the records of one layer,
+// at most kLutScratchFloats words (16 MiB; 26 214 outputs of arity 6 with
+// K = 8, 116 508 of arity 2). Every GPU the library runs on holds its own
+// copy until the process ends. Host code never passes the array's name to a
+// kernel: it is a host-side stand-in, and the device address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr int64_t kLutScratchFloats = int64_t(4) << 20;
+static __device__ __align__(256) float scratch[kLutScratchFloats];
+
+namespace {
+constexpr int kScratchDevices = 64;
+float* g_scratch[kScratchDevices];
+hipError_t g_scratch_rc[kScratchDevices];
+std::once_flag g_scratch_once[kScratchDevices];
+}  // namespace
+
+static int lut_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("fc_lut_soft_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  SLG_REQUIRE(dev >= 0 && dev < kScratchDevices, SLG_E_UNSUPPORTED,
+              "fc_lut_soft_noalloc: device %d beyond %d", dev, kScratchDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch[dev] = g_scratch_rc[dev] == hipSuccess ? static_cast<float*>(p) : nullptr;
+  });
+  if (g_scratch_rc[dev] != hipSuccess || !g_scratch[dev]) {
+    const hipError_t rc = g_scratch_rc[dev] != hipSuccess ? g_scratch_rc[dev] : hipErrorUnknown;
+    set_error("fc_lut_soft_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+              hipGetErrorString(rc));
+    return (int)rc;
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+
 }  // namespace slg
 
 using namespace slg;
@@ -595,26 +664,24 @@ int slg_fc_lut_soft_fwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int3
                         int32_t K, const int32_t* cand, const float* w, const float* s,
                         int32_t hybrid, float* y, float* workspace, int64_t workspace_floats,
                         slg_stream_t stream) {
-  SLG_REQUIRE(cand && w && s && workspace && ((x && y) || B == 0), SLG_E_ARG,
-              "fc_lut_soft: null pointer");
-  SLG_REQUIRE(arity >= 2 && arity <= 6 && K >= 1 && K <= 8, SLG_E_SHAPE,
-              "fc_lut_soft: arity %d / K %d outside 2..6 / 1..8", arity, K);
-  SLG_REQUIRE(B >= 0 && IN > 0 && OUT > 0 && B < (1LL << 31) && IN < (1LL << 28) &&
-                  OUT < (1LL << 26),
-              SLG_E_SHAPE, "fc_lut_soft: bad sizes");
-  const int S = lut_tile(IN);
-  SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "fc_lut_soft: IN=%lld does not fit LDS", (long long)IN);
-  const int KM = lut_km(K);
+  SLG_REQUIRE(workspace, SLG_E_ARG, "fc_lut_soft: null workspace");
+  return lut_soft_fwd(x, B, IN, OUT, arity, K, cand, w, s, hybrid, y, workspace,
+                      workspace_floats, as_stream(stream), "fc_lut_soft");
+}
+
+int slg_fc_lut_soft_fwd_noalloc(const float* x, int64_t B, int64_t IN, int64_t OUT,
+                                int32_t arity, int32_t K, const int32_t* cand, const float* w,
+                                const float* s, int32_t hybrid, float* y, slg_stream_t stream) {
   const int64_t need = slg_fc_lut_soft_workspace(OUT, arity, K);
-  SLG_REQUIRE(workspace_floats >= need, SLG_E_ARG, "fc_lut_soft: workspace of %lld floats, %lld needed",
-              (long long)workspace_floats, (long long)need);
-  hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(fc_lut_pack_kernel, dim3((unsigned)cdiv(need, 256)), dim3(256), 0, st, cand,
-                     w, s, (int)OUT, arity, K, KM, (int)IN, workspace);
-  SLG_LAUNCH_CHECK("fc_lut_pack");
-  if (B == 0) return 0;
-  return hybrid ? lut_fwd_n<true>(arity, KM, S, x, B, IN, OUT, workspace, y, st)
-                : lut_fwd_n<false>(arity, KM, S, x, B, IN, OUT, workspace, y, st);
+  SLG_REQUIRE(need <= kLutScratchFloats, SLG_E_SHAPE,
+              "fc_lut_soft_noalloc: %lld outputs need %lld record floats, the static scratch "
+              "holds %lld (use slg_fc_lut_soft_fwd with a workspace)",
+              (long long)OUT, (long long)need, (long long)kLutScratchFloats);
+  float* rec = nullptr;
+  const int rc = lut_scratch(&rec);
+  if (rc) return rc;
+  return lut_soft_fwd(x, B, IN, OUT, arity, K, cand, w, s, hybrid, y, rec, kLutScratchFloats,
+                      as_stream(stream), "fc_lut_soft_noalloc");
 }
 
 int64_t slg_fc_lut_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t arity,
@@ -652,7 +719,7 @@ int slg_fc_lut_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int3
   float* partc = partw + p.partw;
   float* inp = partc + p.partc;
   hipLaunchKernelGGL(fc_lut_pack_kernel, dim3((unsigned)cdiv(p.rec, 256)), dim3(256), 0, st, cand,
-                     w, s, (int)OUT, arity, K, p.KM, (int)IN, rec);
+                     w, s, (int)OUT, arity, K, p.KM, (int)IN, reinterpret_cast<uint32_t*>(rec));
   SLG_LAUNCH_CHECK("fc_lut_pack");
   if (B > 0 && (gx || gw || gs)) {
     int rc = 0;
