@@ -134,7 +134,7 @@ def kernels_only(reps=3):
         x_mid = torch.rand(4096, 10000, device=dev)
         rec = ops.fc_soft_records([model.layers[1].record_spec()], 8)[0]
         for _ in range(reps):
-            ops.fc_soft_rec(x_mid, rec, 10000, 8, ops.GATE16)
+            ops.fc_soft_rec(x_mid, rec, 10000, 10000, 8, ops.GATE16)
     torch.cuda.synchronize()
     log("kernels-only done")
 
@@ -198,7 +198,7 @@ def dominant_soft_kernel(cfg, model, B_soft, x_soft, dev):
         x_mid = torch.rand(B_soft, L.in_dim, device=dev)
         rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
         K, OUT = L.n_candidates, L.out_dim
-        fn = lambda: ops.fc_soft_rec(x_mid, rec, OUT, K, L.node.kind, L._inv_tau())  # noqa: E731
+        fn = lambda: ops.fc_soft_rec(x_mid, rec, L.in_dim, OUT, K, L.node.kind, L._inv_tau())  # noqa: E731
         nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * (K + 1)
         name = f"fc_soft_kernel ({L._node_name}, K={K}, IN={L.in_dim}, OUT={OUT}, B={B_soft})"
         return name, fn, nbytes

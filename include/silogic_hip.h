@@ -130,10 +130,13 @@ int slg_fc_soft_schedule(const int32_t* cand, int64_t OUT, int32_t K, int64_t IN
                          slg_stream_t stream);
 
 /* slg_fc_soft_fwd on records from slg_fc_soft_records (the forward of
- * LogicLayer, layers.py:107-123, without gradients). */
+ * LogicLayer, layers.py:107-123, without gradients). rec_in_dim is the
+ * in_dim the records were built for; x [B, IN] must have IN >= rec_in_dim
+ * (else SLG_E_SHAPE: the reference's x[:, cand] raises there). */
 int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
-                            const float* rec, int32_t node_kind, float inv_tau, float* out,
-                            int32_t tile_samples, int32_t threads, slg_stream_t stream);
+                            const float* rec, int64_t rec_in_dim, int32_t node_kind,
+                            float inv_tau, float* out, int32_t tile_samples, int32_t threads,
+                            slg_stream_t stream);
 
 /* The last LogicLayer of a LogicNet fused with its GroupSum head with the
  * feature STE (layers.py:107-123 then heads.py:34-39, as models.py:96-97
@@ -141,8 +144,9 @@ int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, 
  * output y is not written. Exact: the counts are integers. Returns
  * SLG_E_UNSUPPORTED when slg_fc_soft_groupsum_supported says 0. */
 int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
-                             const float* rec, int32_t node_kind, float inv_tau, int32_t C,
-                             float tau, float* logits, slg_stream_t stream);
+                             const float* rec, int64_t rec_in_dim, int32_t node_kind,
+                             float inv_tau, int32_t C, float tau, float* logits,
+                             slg_stream_t stream);
 /* 1 if slg_fc_soft_fwd_groupsum runs this shape (one workgroup holds every
  * output of its sample tile), else 0. */
 int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C);

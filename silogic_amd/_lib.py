@@ -25,10 +25,10 @@ SIGNATURES = {
     "slg_fc_soft_prep": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "slg_fc_soft_records": (C.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
     "slg_fc_soft_schedule": (C.c_int, [_P, _I64, _I32, _I64, _P, _P]),
-    "slg_fc_soft_fwd_records": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I32, _F32, _P, _I32,
-                                          _I32, _P]),
-    "slg_fc_soft_fwd_groupsum": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I32, _F32, _I32,
-                                           _F32, _P, _P]),
+    "slg_fc_soft_fwd_records": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _F32, _P,
+                                          _I32, _I32, _P]),
+    "slg_fc_soft_fwd_groupsum": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _F32,
+                                           _I32, _F32, _P, _P]),
     "slg_fc_soft_groupsum_supported": (C.c_int, [_I64, _I64, _I64, _I32]),
     "slg_groupsum_soft": (C.c_int, [_P, _I64, _I64, _I32, _F32, _I32, _P, _P]),
     "slg_groupsum_hard": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),

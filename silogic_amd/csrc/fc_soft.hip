@@ -430,8 +430,11 @@ __global__ void __launch_bounds__(256) fc_soft_records_kernel(RecNet net) {
   const int o = min(op, L.out_dim - 1);
   const int K = net.K;
   const int RQ = rec_quads(K);
-  float* base = L.rec + ((int64_t)(op >> 6) * RQ * 64 + (op & 63)) * 4;
-  auto put = [&](int w, float v) { base[(w >> 2) * 256 + (w & 3)] = v; };
+  // words are written as integers: an index pair with idx_b >= 32640 is a
+  // NaN bit pattern, which a float move could quieten
+  uint32_t* base =
+      reinterpret_cast<uint32_t*>(L.rec) + ((int64_t)(op >> 6) * RQ * 64 + (op & 63)) * 4;
+  auto put = [&](int w, uint32_t v) { base[(w >> 2) * 256 + (w & 3)] = v; };
   const int64_t ca = (int64_t)o * 2 * K, cb = ca + K;  // slot a, slot b
   float wa[16], wb[16];
   softmax_k(L.conn ? L.conn + ca : nullptr, K, wa);
@@ -441,16 +444,16 @@ __global__ void __launch_bounds__(256) fc_soft_records_kernel(RecNet net) {
     const int kb = L.order ? min((int)L.order[cb + t], K - 1) : t;
     const uint32_t ia = (uint32_t)min(max(L.cand[ca + ka], 0), L.in_dim - 1);
     const uint32_t ib = (uint32_t)min(max(L.cand[cb + kb], 0), L.in_dim - 1);
-    put(t, __uint_as_float(ia | (ib << 16)));
-    put(K + t, wa[ka]);
-    put(2 * K + t, wb[kb]);
+    put(t, ia | (ib << 16));
+    put(K + t, __float_as_uint(wa[ka]));
+    put(2 * K + t, __float_as_uint(wb[kb]));
   }
-  for (int w = 3 * K; w < 4 * (RQ - 1); ++w) put(w, 0.0f);
+  for (int w = 3 * K; w < 4 * (RQ - 1); ++w) put(w, 0u);
   const float4 p = node_param(L.node, L.raw, o);
-  put(4 * (RQ - 1) + 0, p.x);
-  put(4 * (RQ - 1) + 1, p.y);
-  put(4 * (RQ - 1) + 2, p.z);
-  put(4 * (RQ - 1) + 3, p.w);
+  put(4 * (RQ - 1) + 0, __float_as_uint(p.x));
+  put(4 * (RQ - 1) + 1, __float_as_uint(p.y));
+  put(4 * (RQ - 1) + 2, __float_as_uint(p.z));
+  put(4 * (RQ - 1) + 3, __float_as_uint(p.w));
 }
 
 // Bank-aware gather order. The soft kernel gathers one candidate per lane
@@ -660,10 +663,15 @@ int slg_fc_soft_schedule(const int32_t* cand, int64_t OUT, int32_t K, int64_t IN
 }
 
 int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
-                            const float* rec, int32_t node_kind, float inv_tau, float* out,
-                            int32_t tile_samples, int32_t threads, slg_stream_t stream) {
+                            const float* rec, int64_t rec_in_dim, int32_t node_kind,
+                            float inv_tau, float* out, int32_t tile_samples, int32_t threads,
+                            slg_stream_t stream) {
   SLG_REQUIRE(rec, SLG_E_ARG, "fc_soft_fwd_records: null rec");
   SLG_REQUIRE(K >= 1 && K <= 16, SLG_E_SHAPE, "fc_soft_fwd_records: K=%d outside 1..16", K);
+  // the records' indices lie below rec_in_dim; the kernel stages IN inputs
+  SLG_REQUIRE(rec_in_dim > 0 && IN >= rec_in_dim, SLG_E_SHAPE,
+              "fc_soft_fwd_records: x has %lld inputs, the records were built for %lld",
+              (long long)IN, (long long)rec_in_dim);
   SoftArgs a{x, B, IN, OUT, K, records_view(rec), inv_tau, out, tile_samples, threads,
              HeadArgs{nullptr, 0, 0, 1.0f}};
   return fc_soft_dispatch(a, node_kind, as_stream(stream));
@@ -682,10 +690,14 @@ int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C
 }
 
 int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t K,
-                             const float* rec, int32_t node_kind, float inv_tau, int32_t C,
-                             float tau, float* logits, slg_stream_t stream) {
+                             const float* rec, int64_t rec_in_dim, int32_t node_kind,
+                             float inv_tau, int32_t C, float tau, float* logits,
+                             slg_stream_t stream) {
   SLG_REQUIRE(rec && (logits || B == 0), SLG_E_ARG, "fc_soft_fwd_groupsum: null pointer");
   SLG_REQUIRE(K >= 1 && K <= 16, SLG_E_SHAPE, "fc_soft_fwd_groupsum: K=%d outside 1..16", K);
+  SLG_REQUIRE(rec_in_dim > 0 && IN >= rec_in_dim, SLG_E_SHAPE,
+              "fc_soft_fwd_groupsum: x has %lld inputs, the records were built for %lld",
+              (long long)IN, (long long)rec_in_dim);
   if (B == 0) return 0;
   SLG_REQUIRE(slg_fc_soft_groupsum_supported(B, IN, OUT, C), SLG_E_UNSUPPORTED,
               "fc_soft_fwd_groupsum: B=%lld IN=%lld OUT=%lld C=%d needs the unfused path",

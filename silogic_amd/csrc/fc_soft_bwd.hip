@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(256) fc_soft_pack_records_kernel(const int* __
                                                                    const float* __restrict__ w,
                                                                    const float* __restrict__ np,
                                                                    int OUT, int K, int IN,
-                                                                   float* __restrict__ rec) {
+                                                                   uint32_t* __restrict__ rec) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int RQ = rec_quads(K);
   const int64_t nq = (int64_t)((OUT + 63) / 64) * RQ * 64;
@@ -79,15 +79,17 @@ __global__ void __launch_bounds__(256) fc_soft_pack_records_kernel(const int* __
   const int c = (int)(Q / (64 * (int64_t)RQ));
   const int o = min(c * 64 + lane, OUT - 1);
   const int word = q * 4 + e;
-  float v = 0.0f;
+  // words are written as integers: an index pair with idx_b >= 32640 is a
+  // NaN bit pattern, which a float move could quieten
+  uint32_t v = 0u;
   if (word < K) {
     const uint32_t ia = (uint32_t)min(max(cand[(int64_t)o * 2 * K + word], 0), IN - 1);
     const uint32_t ib = (uint32_t)min(max(cand[(int64_t)o * 2 * K + K + word], 0), IN - 1);
-    v = __uint_as_float(ia | (ib << 16));
+    v = ia | (ib << 16);
   } else if (word < 3 * K) {
-    v = w[(int64_t)o * 2 * K + (word - K)];  // w_a then w_b
+    v = __float_as_uint(w[(int64_t)o * 2 * K + (word - K)]);  // w_a then w_b
   } else if (word >= 4 * (RQ - 1)) {
-    v = np[(int64_t)o * 4 + (word - 4 * (RQ - 1))];
+    v = __float_as_uint(np[(int64_t)o * 4 + (word - 4 * (RQ - 1))]);
   }
   rec[t] = v;
 }
@@ -523,7 +525,8 @@ extern "C" {
 int64_t slg_fc_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t K) {
   if (B < 0 || IN <= 0 || OUT <= 0 || K < 1 || K > 16 || 2 * OUT * K >= (1LL << 31)) return -1;
   const BwdPlan p = bwd_plan(B, IN, OUT, K);
-  if (!p.Sw) return -1;
+  // records hold 16-bit input indices: the same limit slg_fc_soft_bwd checks
+  if (!p.Sw || IN > 65536) return -1;
   return p.total();
 }
 
@@ -553,7 +556,8 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
   float* gbr = part + p.part_floats;
   float* in_ws = gbr + p.gbr_floats;
   hipLaunchKernelGGL(fc_soft_pack_records_kernel, dim3((unsigned)cdiv(p.rec_floats, 256)),
-                     dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN, rec);
+                     dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN,
+                     reinterpret_cast<uint32_t*>(rec));
   SLG_LAUNCH_CHECK("fc_soft_pack_records");
   const bool want_w = gw || gnp;
   const bool want_x = gx != nullptr && B > 0;

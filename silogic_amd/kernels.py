@@ -25,22 +25,18 @@ HAS_DENSE = HAS_WARP = HAS_CONV = HAS_CONV_TOPK = _OK
 HAS_MULTILINEAR = HAS_CONV_HYBRID = _OK
 
 
-def _pack_ab(ca, cb, wa, wb):
-    cand = torch.stack([ca, cb], dim=1)
-    w = torch.stack([wa, wb], dim=1)
-    return cand, w
-
-
 def dense_logic(x, ca, cb, wa, wb, coef):
-    """x[B,IN], ca/cb[OUT,K] int32, wa/wb[OUT,K], coef[OUT,4] -> [B,OUT]."""
-    cand, w = _pack_ab(ca, cb, wa, wb)
-    return _op.fc_soft(x, cand.to(torch.int32), w, coef, ops.GATE16, 1.0)
+    """x[B,IN], ca/cb[OUT,K] int32, wa/wb[OUT,K], coef[OUT,4] -> [B,OUT]
+    (``slg_dense_logic_fwd``)."""
+    return _op.dense_logic(x, ca.to(torch.int32), cb.to(torch.int32), wa, wb, coef,
+                           ops.GATE16, 1.0)
 
 
 def warp_logic(x, ca, cb, wa, wb, coef, inv_tau):
-    """As :func:`dense_logic`, then ``sigmoid(z * inv_tau)``."""
-    cand, w = _pack_ab(ca, cb, wa, wb)
-    return _op.fc_soft(x, cand.to(torch.int32), w, coef, ops.WALSH, float(inv_tau))
+    """As :func:`dense_logic`, then ``sigmoid(z * inv_tau)``
+    (``slg_warp_logic_fwd``)."""
+    return _op.dense_logic(x, ca.to(torch.int32), cb.to(torch.int32), wa, wb, coef,
+                           ops.WALSH, float(inv_tau))
 
 
 def _i32(t):
@@ -53,19 +49,19 @@ def _check_same(stride, pad, H, W, Ho, Wo):
 
 
 def tree_conv(x, coef, cm, ch, cw, depth, stride, pad, Ho, Wo):
-    """Fixed-wiring gate tree conv: coef [N,2^d-1,4], cm/ch/cw [N,2^d]."""
+    """Fixed-wiring gate tree conv: coef [N,2^d-1,4], cm/ch/cw [N,2^d]
+    (``slg_tree_conv_fwd`` with K = 1)."""
     _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
     N, leaves = cm.shape
     w = torch.ones(N, leaves, 1, device=x.device)
-    return _op.conv_soft(x, coef, w, _i32(cm.unsqueeze(-1)), _i32(ch.unsqueeze(-1)),
-                         _i32(cw.unsqueeze(-1)), ops.GATE16, depth, 2, 1, pad, False)
+    return _op.tree_conv(x, coef, w, _i32(cm.unsqueeze(-1)), _i32(ch.unsqueeze(-1)),
+                         _i32(cw.unsqueeze(-1)), depth, 1, pad)
 
 
 def tree_conv_topk(x, coef, w, cm, ch, cw, depth, K, stride, pad, Ho, Wo):
-    """Top-K gate tree conv: w/cm/ch/cw [N,2^d,K]."""
+    """Top-K gate tree conv: w/cm/ch/cw [N,2^d,K] (``slg_tree_conv_fwd``)."""
     _check_same(stride, pad, x.shape[2], x.shape[3], Ho, Wo)
-    return _op.conv_soft(x, coef, w, _i32(cm), _i32(ch), _i32(cw), ops.GATE16, depth, 2, K, pad,
-                         False)
+    return _op.tree_conv(x, coef, w, _i32(cm), _i32(ch), _i32(cw), depth, K, pad)
 
 
 def multilinear_logic(x, cand, w, s, arity):

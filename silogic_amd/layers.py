@@ -155,6 +155,7 @@ class LogicLayer(nn.Module):
 
     def forward(self, x):
         ops.require_gpu(x)
+        ops.check_width(x, self.in_dim)
         if self.is_lut:
             conn = self._conn
             return ops.fc_lut_soft(x, conn.candidates_i32(), conn.weights(),
@@ -165,7 +166,8 @@ class LogicLayer(nn.Module):
         if spec is not None:
             K = self.n_candidates
             rec = ops.fc_soft_records([spec], K)[0]
-            return ops.fc_soft_rec(x, rec, self.out_dim, K, self.node.kind, self._inv_tau())
+            return ops.fc_soft_rec(x, rec, self.in_dim, self.out_dim, K, self.node.kind,
+                                   self._inv_tau())
         cand, w, npar = self.soft_params(grad)
         return ops.fc_soft(x, cand, w, npar, self.node.kind, self._inv_tau())
 
@@ -188,6 +190,7 @@ class LogicLayer(nn.Module):
     @torch.no_grad()
     def forward_hard(self, x):
         ops.require_gpu(x)
+        ops.check_width(x, self.in_dim)
         B = x.shape[0]
         return ops.unpack_bits(self.packed_forward(ops.pack_bits(x)), B)
 

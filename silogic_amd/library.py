@@ -93,6 +93,98 @@ def _fc_soft_backward(ctx, gy):
 fc_soft.register_autograd(_fc_soft_backward, setup_context=_fc_soft_setup)
 
 
+# The reference's own signatures (kernels/dense.py:123-125, warp.py:104-105):
+# separate candidate and weight arrays per operand, through the C ABI's
+# slg_dense_logic_fwd / slg_warp_logic_fwd. The backward stacks them into the
+# [OUT,2,K] layout of fc_soft_bwd.
+@torch.library.custom_op(f"{_NS}::dense_logic", mutates_args=())
+def dense_logic(x: Tensor, ca: Tensor, cb: Tensor, wa: Tensor, wb: Tensor, coef: Tensor,
+                node_kind: int, inv_tau: float) -> Tensor:
+    """``x [B,IN]``, ``ca/cb [OUT,K]`` int32, ``wa/wb [OUT,K]``, ``coef [OUT,4]``
+    -> ``[B,OUT]`` (gate16: the BasisProj node; walsh: its sigmoid)."""
+    return ops.dense_logic_launch(x, ca, cb, wa, wb, coef, node_kind, inv_tau)
+
+
+@dense_logic.register_fake
+def _(x, ca, cb, wa, wb, coef, node_kind, inv_tau):
+    return x.new_empty((x.shape[0], ca.shape[0]), dtype=torch.float32)
+
+
+def _dense_setup(ctx, inputs, output):
+    x, ca, cb, wa, wb, coef, node_kind, inv_tau = inputs
+    ctx.save_for_backward(x, ca, cb, wa, wb, coef)
+    ctx.meta = (node_kind, inv_tau)
+
+
+def _dense_backward(ctx, gy):
+    x, ca, cb, wa, wb, coef = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    need_w = need[3] or need[4]
+    cand = torch.stack([ca, cb], dim=1).to(torch.int32)
+    w = torch.stack([wa, wb], dim=1)
+    gx, gw, gn = fc_soft_bwd(x, cand, w, coef, *ctx.meta, gy, need[0], need_w, need[5])
+    gwa = gw[:, 0] if need[3] else None
+    gwb = gw[:, 1] if need[4] else None
+    return _none(gx, need[0]), None, None, gwa, gwb, _none(gn, need[5]), None, None
+
+
+dense_logic.register_autograd(_dense_backward, setup_context=_dense_setup)
+
+
+# GroupSum.forward (heads.py:34-39): block sums of x (or of x > 0.5 with the
+# feature STE) / tau; both forms have d logit / d x = 1/tau on the block.
+@torch.library.custom_op(f"{_NS}::groupsum_soft", mutates_args=())
+def groupsum_soft(x: Tensor, C: int, tau: float, ste: bool) -> Tensor:
+    return ops.groupsum_soft_launch(x, C, tau, ste)
+
+
+@groupsum_soft.register_fake
+def _(x, C, tau, ste):
+    return x.new_empty((x.shape[0], C), dtype=torch.float32)
+
+
+def _groupsum_setup(ctx, inputs, output):
+    x, C, tau, ste = inputs
+    ctx.meta = (x.shape[1], C, tau)
+
+
+def _groupsum_backward(ctx, g):
+    W, C, tau = ctx.meta
+    gx = (g / tau).unsqueeze(2).expand(g.shape[0], C, W // C).reshape(g.shape[0], W)
+    return gx, None, None, None
+
+
+groupsum_soft.register_autograd(_groupsum_backward, setup_context=_groupsum_setup)
+
+
+# OrPool.forward (layers.py:558-559): 2x2 max pool; the gradient of
+# F.max_pool2d (to the first maximum of each window).
+@torch.library.custom_op(f"{_NS}::orpool", mutates_args=())
+def orpool(x: Tensor) -> Tensor:
+    return ops.orpool_launch(x)
+
+
+@orpool.register_fake
+def _(x):
+    B, C, H, W = x.shape
+    return x.new_empty((B, C, H // 2, W // 2))
+
+
+def _orpool_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+
+
+def _orpool_backward(ctx, g):
+    (x,) = ctx.saved_tensors
+    xf = x.float()
+    _, idx = torch.ops.aten.max_pool2d_with_indices(xf, [2, 2], [2, 2])
+    return torch.ops.aten.max_pool2d_with_indices_backward(g, xf, [2, 2], [2, 2], [0, 0],
+                                                          [1, 1], False, idx)
+
+
+orpool.register_autograd(_orpool_backward, setup_context=_orpool_setup)
+
+
 # ---------------------------------------------------------------------------
 # LUT FC layer (multilinear_logic)
 # ---------------------------------------------------------------------------
@@ -216,6 +308,36 @@ def _conv_backward(ctx, gy):
 
 
 conv_soft.register_autograd(_conv_backward, setup_context=_conv_setup)
+
+
+# The reference's tree_conv / tree_conv_topk signature (kernels/conv.py:399-400,
+# conv_topk.py:175-189) through slg_tree_conv_fwd: gate16 trees, Top-K leaves
+# (w [N,2^d,K]) or fixed ones (K = 1, w all ones), stride 1, 'same' padding.
+@torch.library.custom_op(f"{_NS}::tree_conv", mutates_args=())
+def tree_conv(x: Tensor, coef: Tensor, w: Tensor, cm: Tensor, ch: Tensor, cw: Tensor, depth: int,
+              K: int, pad: int) -> Tensor:
+    return ops.tree_conv_launch(x, coef, w, cm, ch, cw, depth, K, pad)
+
+
+@tree_conv.register_fake
+def _(x, coef, w, cm, ch, cw, depth, K, pad):
+    return x.new_empty(_conv_out_shape(x, cm, pad, False), dtype=torch.float32)
+
+
+def _tree_conv_setup(ctx, inputs, output):
+    x, coef, w, cm, ch, cw, depth, K, pad = inputs
+    ctx.save_for_backward(x, coef, w, cm, ch, cw)
+    ctx.meta = (ops.GATE16, depth, 2, K, pad, False)
+
+
+def _tree_conv_backward(ctx, gy):
+    x, coef, w, cm, ch, cw = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    gx, gn, gw = conv_soft_bwd(x, coef, w, cm, ch, cw, *ctx.meta, gy, need[0], need[1], need[2])
+    return (_none(gx, need[0]), _none(gn, need[1]), _none(gw, need[2])) + (None,) * 6
+
+
+tree_conv.register_autograd(_tree_conv_backward, setup_context=_tree_conv_setup)
 
 
 # ---------------------------------------------------------------------------

@@ -43,9 +43,9 @@ def _soft_fc_stack(layers, head, x, wire_r):
         if i == len(layers) - 1 and isinstance(head, GroupSum) and head.feature_ste and not (
                 wire_r and h.shape[1] == layer.out_dim) and ops.fc_soft_groupsum_supported(
                     h.shape[0], h.shape[1], layer.out_dim, head.num_classes):
-            return ops.fc_soft_rec_groupsum(h, rec, layer.out_dim, K, kind, inv_tau,
-                                            head.num_classes, head.tau)
-        y = ops.fc_soft_rec(h, rec, layer.out_dim, K, kind, inv_tau)
+            return ops.fc_soft_rec_groupsum(h, rec, layer.in_dim, layer.out_dim, K, kind,
+                                            inv_tau, head.num_classes, head.tau)
+        y = ops.fc_soft_rec(h, rec, layer.in_dim, layer.out_dim, K, kind, inv_tau)
         if wire_r and h.shape[1] == y.shape[1]:
             y = torch.cat([h[:, :wire_r], y[:, wire_r:]], dim=1)
         h = y
@@ -128,6 +128,7 @@ class LogicNet(nn.Module):
 
     def forward(self, x):
         ops.require_gpu(x)
+        ops.check_width(x, self.layers[0].in_dim)
         if not _needs_grad(self, x):
             out = _soft_fc_stack(self.layers, self.head, x, self.wire_r)
             if out is not None:
@@ -137,6 +138,7 @@ class LogicNet(nn.Module):
     @torch.no_grad()
     def forward_hard(self, x):
         ops.require_gpu(x)
+        ops.check_width(x, self.layers[0].in_dim)
         x, kind = ops._in_kind(x)
         return _hard_fc_stack(self.layers, x, kind, x.shape[0], x.shape[1],
                               self.head.num_classes, self.wire_r)

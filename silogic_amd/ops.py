@@ -5,11 +5,12 @@ torch, and launches the kernels of ``libsilogic_hip.so`` on torch's current
 stream. Nothing here computes on the CPU: a CPU tensor or a missing library
 raises.
 
-Autograd: the soft ops are ``torch.autograd.Function`` s whose forward is
-the HIP kernel. Their backward recomputes the op with differentiable torch
-GPU ops and backpropagates through that (a composite backward, the analogue
-of the reference's backward kernels in silogic/kernels/*.py, which are not
-part of this build's hot path).
+Autograd: with gradients the soft ops run as the ``torch.ops.silogic_hip``
+custom operators of ``library.py`` (opaque to ``torch.compile``), whose
+backward runs the HIP backward kernels; shapes those kernels do not take use
+a composite backward of differentiable torch ops (``fc_soft_torch``,
+``conv_soft_torch``). Without gradients the wrappers launch the kernels
+directly.
 """
 import ctypes
 
@@ -36,7 +37,17 @@ def require_gpu(*ts):
             raise RuntimeError(
                 "silogic_amd computes on the GPU only (HIP kernels, no CPU fallback): "
                 "move the module and its inputs to a ROCm device with .cuda()")
-    _lib.lib()
+    if not torch.compiler.is_compiling():   # traced code reaches the library in the ops
+        _lib.lib()
+
+
+def _grad_path(*ts):
+    """True when the op must run as a differentiable custom operator: some
+    input needs a gradient, or torch.compile is tracing."""
+    if torch.compiler.is_compiling():
+        return True
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
 
 
 def _c(t, dtype=None):
@@ -80,6 +91,30 @@ def _fc_soft_launch(x, cand, w, npar, node_kind, inv_tau, tile=0, threads=0):
     return y
 
 
+def dense_logic_launch(x, ca, cb, wa, wb, coef, node_kind, inv_tau):
+    """The reference's separate-array form through ``slg_dense_logic_fwd``
+    (gate16) / ``slg_warp_logic_fwd`` (walsh)."""
+    require_gpu(x, ca, cb, wa, wb, coef)
+    x = _as_f32(x)
+    ca, cb = _c(ca, torch.int32), _c(cb, torch.int32)
+    wa, wb, coef = _c(wa, torch.float32), _c(wb, torch.float32), _c(coef, torch.float32)
+    B, IN = x.shape
+    OUT, K = ca.shape
+    if cb.shape != ca.shape or wa.shape != ca.shape or wb.shape != ca.shape or \
+            coef.shape != (OUT, 4):
+        raise ValueError("dense_logic: ca/cb/wa/wb must be [OUT,K] and coef [OUT,4]")
+    y = torch.empty((B, OUT), device=x.device, dtype=torch.float32)
+    if node_kind == GATE16:
+        _lib.call("slg_dense_logic_fwd", _p(x), B, IN, OUT, K, _p(ca), _p(cb), _p(wa), _p(wb),
+                  _p(coef), _p(y), _stream(x))
+    elif node_kind == WALSH:
+        _lib.call("slg_warp_logic_fwd", _p(x), B, IN, OUT, K, _p(ca), _p(cb), _p(wa), _p(wb),
+                  _p(coef), float(inv_tau), _p(y), _stream(x))
+    else:
+        raise ValueError("dense_logic: node kind %d (gate16 or walsh)" % node_kind)
+    return y
+
+
 def fc_soft_torch(x, cand, w, npar, node_kind, inv_tau):
     """Differentiable torch expression of the FC soft op (backward only)."""
     g = x[:, cand.long()]                        # [B, OUT, 2, K]
@@ -115,43 +150,11 @@ def fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need_x=True, need_w=Tr
     return gx, gw, gn
 
 
-class FCSoftFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, cand, w, npar, node_kind, inv_tau):
-        x = _as_f32(x)
-        cand, w, npar = _c(cand, torch.int32), _c(w, torch.float32), _c(npar, torch.float32)
-        ctx.save_for_backward(x, cand, w, npar)
-        ctx.meta = (node_kind, inv_tau)
-        return _fc_soft_launch(x, cand, w, npar, node_kind, inv_tau)
-
-    @staticmethod
-    def backward(ctx, gy):
-        x, cand, w, npar = ctx.saved_tensors
-        node_kind, inv_tau = ctx.meta
-        need = ctx.needs_input_grad
-        got = fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need[0], need[2], need[3])
-        if got is not None:
-            gx, gw, gn = got
-            return gx, None, gw, gn, None, None
-        # shapes the HIP backward does not take: the composite torch backward
-        with torch.enable_grad():
-            xs = x.detach().requires_grad_(need[0])
-            ws = w.detach().requires_grad_(need[2])
-            ns = npar.detach().requires_grad_(need[3])
-            y = fc_soft_torch(xs, cand, ws, ns, node_kind, inv_tau)
-            inputs = [t for t, n in ((xs, need[0]), (ws, need[2]), (ns, need[3])) if n]
-            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
-        gx = grads.pop(0) if need[0] else None
-        gw = grads.pop(0) if need[2] else None
-        gn = grads.pop(0) if need[3] else None
-        return gx, None, gw, gn, None, None
-
-
 def fc_soft(x, cand, w, npar, node_kind, inv_tau=1.0):
     """``[B,IN] -> [B,OUT]`` soft FC layer (autograd-aware)."""
     require_gpu(x, cand, w, npar)
-    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or npar.requires_grad):
-        return FCSoftFn.apply(x, cand, w, npar, node_kind, inv_tau)
+    if _grad_path(x, w, npar):
+        return torch.ops.silogic_hip.fc_soft(x, cand, w, npar, node_kind, float(inv_tau))
     return _fc_soft_launch(_as_f32(x), _c(cand, torch.int32), _c(w, torch.float32),
                            _c(npar, torch.float32), node_kind, inv_tau)
 
@@ -195,32 +198,12 @@ def fc_lut_soft_bwd(x, cand, w, s, gy, need_x=True, need_w=True, need_s=True):
     return gx, gw, gs
 
 
-class FCLutFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, cand, w, s, hybrid):
-        x = _as_f32(x)
-        cand, w, s = _c(cand, torch.int32), _c(w, torch.float32), _c(s, torch.float32)
-        ctx.save_for_backward(x, cand, w, s)
-        return _fc_lut_launch(x, cand, w, s, hybrid)
-
-    @staticmethod
-    def backward(ctx, gy):
-        x, cand, w, s = ctx.saved_tensors
-        need = ctx.needs_input_grad
-        got = fc_lut_soft_bwd(x, cand, w, s, gy, need[0], need[2], need[3])
-        if got is None:
-            raise NotImplementedError("fc_lut_soft backward: the input width exceeds what the "
-                                      "kernels stage in LDS")
-        gx, gw, gs = got
-        return gx, None, gw, gs, None
-
-
 def fc_lut_soft(x, cand, w, s, hybrid):
     """``[B,IN] -> [B,OUT]`` LUT layer (multilinear interpolation of ``s``, or
     the hybrid lookup), autograd-aware (the multilinear gradient)."""
     require_gpu(x, cand, w, s)
-    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or s.requires_grad):
-        return FCLutFn.apply(x, cand, w, s, hybrid)
+    if _grad_path(x, w, s):
+        return torch.ops.silogic_hip.fc_lut_soft(x, cand, w, s, bool(hybrid))
     return _fc_lut_launch(_as_f32(x), _c(cand, torch.int32), _c(w, torch.float32),
                           _c(s, torch.float32), hybrid)
 
@@ -310,23 +293,34 @@ def record_words(rec, out_dim):
     return rec.permute(0, 2, 1, 3).reshape(n64 * 64, 4 * K1)[:out_dim]
 
 
-def _check_rec(x, rec, out_dim, K):
+def _check_rec(x, rec, in_dim, out_dim, K):
     if rec.dim() != 4 or tuple(rec.shape) != ((out_dim + 63) // 64, record_quads(K), 64, 4) or \
             rec.dtype != torch.float32 or not rec.is_contiguous():
         raise ValueError(f"fc_soft: records {tuple(rec.shape)} {rec.dtype} for OUT={out_dim}, K={K}")
     if x.dim() != 2:
         raise ValueError(f"fc_soft: x must be [B, IN], got {tuple(x.shape)}")
+    check_width(x, in_dim)
 
 
-def fc_soft_rec(x, rec, out_dim, K, node_kind, inv_tau=1.0, tile=0, threads=0):
-    """Soft FC layer on records (no autograd): ``[B,IN] -> [B,OUT]``."""
+def check_width(x, in_dim):
+    """Raise when ``x`` [B, IN] is narrower than the layer's ``in_dim`` (the
+    reference's ``x[:, cand]`` raises there; wider inputs are read as the
+    reference reads them, by index)."""
+    if x.shape[-1] < in_dim:
+        raise ValueError(f"LogicLayer: input has {x.shape[-1]} features, the layer reads "
+                         f"indices up to in_dim = {in_dim}")
+
+
+def fc_soft_rec(x, rec, in_dim, out_dim, K, node_kind, inv_tau=1.0, tile=0, threads=0):
+    """Soft FC layer on records built for ``in_dim`` inputs (no autograd):
+    ``[B,IN] -> [B,OUT]``."""
     require_gpu(x, rec)
     x = _as_f32(x)
-    _check_rec(x, rec, out_dim, K)
+    _check_rec(x, rec, in_dim, out_dim, K)
     B, IN = x.shape
     y = torch.empty((B, out_dim), device=x.device, dtype=torch.float32)
-    _lib.call("slg_fc_soft_fwd_records", _p(x), B, IN, out_dim, K, _p(rec), node_kind,
-              float(inv_tau), _p(y), int(tile), int(threads), _stream(x))
+    _lib.call("slg_fc_soft_fwd_records", _p(x), B, IN, out_dim, K, _p(rec), int(in_dim),
+              node_kind, float(inv_tau), _p(y), int(tile), int(threads), _stream(x))
     return y
 
 
@@ -334,44 +328,36 @@ def fc_soft_groupsum_supported(B, IN, OUT, C):
     return bool(_lib.lib().slg_fc_soft_groupsum_supported(B, IN, OUT, C))
 
 
-def fc_soft_rec_groupsum(x, rec, out_dim, K, node_kind, inv_tau, C, tau):
+def fc_soft_rec_groupsum(x, rec, in_dim, out_dim, K, node_kind, inv_tau, C, tau):
     """Last soft layer fused with the STE GroupSum head: ``[B,IN] -> [B,C]``."""
     require_gpu(x, rec)
     x = _as_f32(x)
-    _check_rec(x, rec, out_dim, K)
+    _check_rec(x, rec, in_dim, out_dim, K)
     B, IN = x.shape
     logits = torch.empty((B, C), device=x.device, dtype=torch.float32)
-    _lib.call("slg_fc_soft_fwd_groupsum", _p(x), B, IN, out_dim, K, _p(rec), node_kind,
-              float(inv_tau), int(C), float(tau), _p(logits), _stream(x))
+    _lib.call("slg_fc_soft_fwd_groupsum", _p(x), B, IN, out_dim, K, _p(rec), int(in_dim),
+              node_kind, float(inv_tau), int(C), float(tau), _p(logits), _stream(x))
     return logits
 
 
 # ---------------------------------------------------------------------------
 # GroupSum / OrPool
 # ---------------------------------------------------------------------------
-class GroupSumSoftFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, C, tau, ste):
-        x = _as_f32(x)
-        B, W = x.shape
-        out = torch.empty((B, C), device=x.device, dtype=torch.float32)
-        _lib.call("slg_groupsum_soft", _p(x), B, W, C, float(tau), int(bool(ste)), _p(out),
-                  _stream(x))
-        ctx.meta = (W, C, tau)
-        return out
-
-    @staticmethod
-    def backward(ctx, g):
-        # both the plain sum and the straight-through (x>0.5) + x - x.detach()
-        # have d logit / d x = 1/tau on the class block (silogic/heads.py:34-39)
-        W, C, tau = ctx.meta
-        gx = (g / tau).unsqueeze(2).expand(g.shape[0], C, W // C).reshape(g.shape[0], W)
-        return gx, None, None, None
+def groupsum_soft_launch(x, C, tau, ste):
+    require_gpu(x)
+    x = _as_f32(x)
+    B, W = x.shape
+    out = torch.empty((B, C), device=x.device, dtype=torch.float32)
+    _lib.call("slg_groupsum_soft", _p(x), B, W, C, float(tau), int(bool(ste)), _p(out),
+              _stream(x))
+    return out
 
 
 def groupsum_soft(x, C, tau, ste):
     require_gpu(x)
-    return GroupSumSoftFn.apply(x, C, tau, ste)
+    if _grad_path(x):
+        return torch.ops.silogic_hip.groupsum_soft(x, int(C), float(tau), bool(ste))
+    return groupsum_soft_launch(x, C, tau, ste)
 
 
 def groupsum_hard(x, C):
@@ -386,24 +372,7 @@ def groupsum_hard(x, C):
     return out
 
 
-class OrPoolFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x):
-        out = _orpool_launch(x)
-        ctx.save_for_backward(x)
-        return out
-
-    @staticmethod
-    def backward(ctx, g):
-        (x,) = ctx.saved_tensors
-        with torch.enable_grad():
-            xs = x.detach().requires_grad_(True)
-            y = F.max_pool2d(xs, 2, 2)
-            (gx,) = torch.autograd.grad(y, [xs], g)
-        return gx
-
-
-def _orpool_launch(x):
+def orpool_launch(x):
     dtype = 1 if x.dtype == torch.uint8 else 0
     x = x.contiguous() if dtype == 1 else _as_f32(x)
     B, Cc, H, W = x.shape
@@ -416,9 +385,9 @@ def orpool(x):
     require_gpu(x)
     if x.dtype == torch.bool:
         x = x.to(torch.uint8)
-    if torch.is_grad_enabled() and x.requires_grad:
-        return OrPoolFn.apply(x)
-    return _orpool_launch(x)
+    if x.is_floating_point() and _grad_path(x):
+        return torch.ops.silogic_hip.orpool(x)
+    return orpool_launch(x)
 
 
 # ---------------------------------------------------------------------------
@@ -735,44 +704,33 @@ def conv_soft_bwd(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool,
     return gx, gn, gw
 
 
-class ConvSoftFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
-        x = _as_f32(x)
-        npar, w = _c(npar, torch.float32), _c(w, torch.float32)
-        ctx.save_for_backward(x, npar, w, cm, ch, cw)
-        ctx.meta = (node_kind, depth, arity, K, pad, pool)
-        return _conv_soft_launch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool)
-
-    @staticmethod
-    def backward(ctx, gy):
-        x, npar, w, cm, ch, cw = ctx.saved_tensors
-        meta = ctx.meta
-        need = ctx.needs_input_grad
-        got = conv_soft_bwd(x, npar, w, cm, ch, cw, *meta, gy, need[0], need[1], need[2])
-        if got is not None:
-            return got + (None,) * 9
-        # shapes the HIP backward does not take: the composite torch backward
-        with torch.enable_grad():
-            xs = x.detach().requires_grad_(need[0])
-            ns = npar.detach().requires_grad_(need[1])
-            ws = w.detach().requires_grad_(need[2])
-            y = conv_soft_torch(xs, ns, ws, cm, ch, cw, *meta)
-            inputs = [t for t, n in ((xs, need[0]), (ns, need[1]), (ws, need[2])) if n]
-            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
-        gx = grads.pop(0) if need[0] else None
-        gn = grads.pop(0) if need[1] else None
-        gw = grads.pop(0) if need[2] else None
-        return (gx, gn, gw) + (None,) * 9
-
-
 def conv_soft(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
     require_gpu(x, npar, w, cm)
     cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
-    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or npar.requires_grad):
-        return ConvSoftFn.apply(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool)
+    if _grad_path(x, w, npar):
+        return torch.ops.silogic_hip.conv_soft(x, npar, w, cm, ch, cw, int(node_kind), int(depth),
+                                    int(arity), int(K), int(pad), bool(pool))
     return _conv_soft_launch(_as_f32(x), _c(npar, torch.float32), _c(w, torch.float32), cm, ch,
                              cw, node_kind, depth, arity, K, pad, pool)
+
+
+def tree_conv_launch(x, coef, w, cm, ch, cw, depth, K, pad):
+    """The reference's tree_conv / tree_conv_topk form through
+    ``slg_tree_conv_fwd`` (gate16 tree, stride 1, 'same' padding)."""
+    require_gpu(x, coef, w, cm)
+    x = _as_f32(x)
+    coef, w = _c(coef, torch.float32), _c(w, torch.float32)
+    cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
+    B, Cc, H, W = x.shape
+    N = cm.shape[0]
+    leaves = 2 ** depth
+    if cm.shape != (N, leaves, K) or ch.shape != cm.shape or cw.shape != cm.shape or \
+            w.shape != cm.shape or tuple(coef.shape) != (N, leaves - 1, 4):
+        raise ValueError("tree_conv: coef [N,2^d-1,4] and w/cm/ch/cw [N,2^d,K] expected")
+    out = torch.empty((B, N, H, W), device=x.device, dtype=torch.float32)
+    _lib.call("slg_tree_conv_fwd", _p(x), B, Cc, H, W, N, int(depth), int(K), _p(coef), _p(w),
+              _p(cm), _p(ch), _p(cw), 1, int(pad), H, W, _p(out), _stream(x))
+    return out
 
 
 def conv_soft_records(conn, cm, ch, cw, raw, node_kind, depth, arity, K, in_shape, pad, pool):
@@ -896,3 +854,8 @@ def conv_hard(xp, shape_chw, leaf, tt, node_kind, depth, arity, kernel, pad, poo
     _lib.call("slg_conv_hard_fwd", _p(xp), Cc, H, W, nw, N, node_kind, depth, arity, _p(leaf),
               _p(tt), kernel, pad, int(bool(pool)), _p(out), _stream(xp))
     return out
+
+
+# the custom operators the autograd paths above dispatch to (library.py uses
+# this module's launch helpers, so it is imported once they are defined)
+from . import library as _library  # noqa: E402,F401

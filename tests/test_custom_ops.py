@@ -10,8 +10,9 @@ from torch.fx.experimental.proxy_tensor import make_fx
 import silogic_amd  # noqa: F401  (registers the ops)
 from silogic_amd import kernels, ops
 
-OPS = ["fc_soft", "fc_soft_bwd", "fc_lut_soft", "fc_lut_soft_bwd", "conv_soft", "conv_soft_bwd",
-       "pack_bits", "fc_hard_net", "groupsum_packed"]
+OPS = ["fc_soft", "fc_soft_bwd", "dense_logic", "fc_lut_soft", "fc_lut_soft_bwd", "conv_soft",
+       "conv_soft_bwd", "tree_conv", "groupsum_soft", "orpool", "pack_bits", "fc_hard_net",
+       "groupsum_packed"]
 
 
 def test_every_op_is_registered():
@@ -68,7 +69,8 @@ def test_traced_forward_and_backward_is_a_graph_of_the_ops():
 
     gm = make_fx(step)(*args())
     text = str(gm.graph)
-    assert "silogic_hip.fc_soft.default" in text and "silogic_hip.fc_soft_bwd.default" in text
-    # only the x, wa and coef gradients are asked for: wb's slot is dropped
+    # the reference's separate-array op, then the HIP backward op
+    assert "silogic_hip.dense_logic.default" in text and "silogic_hip.fc_soft_bwd.default" in text
+    # x, wa and coef gradients are asked for: the weight gradient (wa's half) and coef
     bwd = [n for n in gm.graph.nodes if "fc_soft_bwd" in str(n.target)]
     assert len(bwd) == 1 and bwd[0].args[-3:] == (True, True, True)

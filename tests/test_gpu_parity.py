@@ -238,7 +238,8 @@ def test_records_of_mixed_layers_in_one_launch():
             x = torch.rand(37, spec[1]["in_dim"])
             layer = m.layers[0]
             OUT = layer.out_dim
-            y = ops.fc_soft_rec(x.to(DEV), rec, OUT, 8, layer.node.kind, layer._inv_tau())
+            y = ops.fc_soft_rec(x.to(DEV), rec, layer.in_dim, OUT, 8, layer.node.kind,
+                                layer._inv_tau())
             assert_soft_close(y, torch_ref.fc_layer_soft(L, sd, x), f"{spec[1]} records")
             # record words: candidates and weights in the scheduled gather order
             words = ops.record_words(rec, OUT).cpu()
@@ -256,7 +257,8 @@ def test_records_of_mixed_layers_in_one_launch():
             # natural order records give the same layer output within tolerance
             spec_nat = layer.record_spec()[:5] + (None,)
             rec_nat = ops.fc_soft_records([spec_nat], 8)[0]
-            y_nat = ops.fc_soft_rec(x.to(DEV), rec_nat, OUT, 8, layer.node.kind, layer._inv_tau())
+            y_nat = ops.fc_soft_rec(x.to(DEV), rec_nat, layer.in_dim, OUT, 8, layer.node.kind,
+                                    layer._inv_tau())
             assert_soft_close(y_nat, torch_ref.fc_layer_soft(L, sd, x), "natural order")
 
 
@@ -307,9 +309,10 @@ def test_fused_groupsum_head(node, width):
     with torch.no_grad():
         xd = x.to(DEV)
         rec = ops.fc_soft_records([layer.record_spec()], 8)[0]
-        logits = ops.fc_soft_rec_groupsum(xd, rec, width, 8, layer.node.kind, layer._inv_tau(),
+        logits = ops.fc_soft_rec_groupsum(xd, rec, layer.in_dim, width, 8, layer.node.kind,
+                                          layer._inv_tau(),
                                           10, 3.0)
-        feats = ops.fc_soft_rec(xd, rec, width, 8, layer.node.kind, layer._inv_tau())
+        feats = ops.fc_soft_rec(xd, rec, layer.in_dim, width, 8, layer.node.kind, layer._inv_tau())
         out = model(xd)
     feats_ref = torch_ref.fc_layer_soft(L, sd, x)
     assert_soft_close(feats, feats_ref, "features")

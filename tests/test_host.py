@@ -76,6 +76,15 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
                              None, ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                              1, 1, ctypes.c_void_p(16), None)
     assert rc == -3
+    # records built for 1000 inputs, x only 999 wide: rejected before any launch
+    fake = ctypes.c_void_p(256)
+    rc = L.slg_fc_soft_fwd_records(fake, 4, 999, 64, 8, fake, 1000, 0, 1.0, fake, 0, 0, None)
+    assert rc == -2 and b"built for 1000" in L.slg_last_error()
+    rc = L.slg_fc_soft_fwd_groupsum(fake, 4, 999, 60, 8, fake, 1000, 0, 1.0, 10, 1.0, fake,
+                                    None)
+    assert rc == -2 and b"built for 1000" in L.slg_last_error()
+    # the backward's workspace query agrees with the entry point's 16-bit index limit
+    assert L.slg_fc_soft_bwd_workspace(8, 65537, 16, 8) == -1
 
 
 def test_cpu_inputs_are_refused():
