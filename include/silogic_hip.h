@@ -250,10 +250,11 @@ int slg_groupsum_soft(const float* x, int64_t B, int64_t W, int32_t C, float tau
 int slg_groupsum_hard(const void* x, int32_t dtype, int64_t B, int64_t W, int32_t C,
                       float* logits, slg_stream_t stream);
 
-/* OrPool.forward / forward_hard (silogic/layers.py:548-563): 2x2 max pool
- * with floor on x [B,C,H,W] (dtype 0 = fp32, 1 = uint8) -> out. */
+/* OrPool.forward / forward_hard (silogic/layers.py:548-563): size x size
+ * max pool with stride size and floor on x [B,C,H,W] (dtype 0 = fp32,
+ * 1 = uint8) -> out [B,C,H/size,W/size]. */
 int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W,
-               void* out, slg_stream_t stream);
+               int32_t size, void* out, slg_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Hard (bit-packed) path                                                   */
@@ -334,7 +335,7 @@ int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C,
  * cm, ch, cw, depth, K, stride, pad, Ho, Wo)` (layers.py:458-463) and, with
  * K = 1 and w = NULL, kernels/conv.py:399-400 `tree_conv` (layers.py:453-
  * 457): x [B,C,H,W] fp32; coef [N, 2^depth-1, 4]; w [N, 2^depth, K];
- * cm/ch/cw [N, 2^depth, K] int32; out [B,N,Ho,Wo]. depth in 1..4. */
+ * cm/ch/cw [N, 2^depth, K] int32; out [B,N,Ho,Wo]. depth in 1..5. */
 int slg_tree_conv_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
                       int64_t N, int32_t depth, int32_t K, const float* coef,
                       const float* w, const int32_t* cm, const int32_t* ch,
@@ -342,11 +343,22 @@ int slg_tree_conv_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
                       int64_t Wo, float* out, slg_stream_t stream);
 
 /* ConvLogicTree.forward + OrPool.forward fused (layers.py:448-485 and
- * 558-559): as above for stride 1, with either a gate16 tree (node_kind 0,
- * node_param = coef [N, 2^depth-1, 4]) or a depth-1 multilinear LUT over
- * `arity` leaves (node_kind 2, node_param = sigmoid(logits) [N, 2^arity],
- * arity <= 6); writes only the 2x2-max-pooled map out [B,N,Ho/2,Wo/2]
- * (floor). pool = 0 writes the unpooled [B,N,Ho,Wo] instead. */
+ * 558-559): as above for stride 1, for every node tree the reference builds
+ * (layers.py:388-401, 432-446; node parameters level-major, level 0 being
+ * the nodes above the leaves, node m of a level combining values
+ * arity*m .. arity*m+arity-1 of the level below):
+ *   gate16 (node_kind 0): binary tree of depth 1-5, node_param = BasisProj
+ *     coef [N, 2^depth-1, 4];
+ *   walsh (node_kind 1): binary tree of depth 1-5 of nodes sigmoid(z / tau)
+ *     (nodes.py:145-150), node_param = z's (a, b)-space coefficients times
+ *     1/tau [N, 2^depth-1, 4];
+ *   multilinear (2) / hybrid (3) LUT trees of `arity` (2-6) and depth with
+ *     arity^depth <= 36 leaves, node_param = sigmoid(logits) [N, nodes,
+ *     2^arity] (multilinear interpolation, or the LUT at the leaves
+ *     thresholded at 0.5).
+ * Writes only the 2x2-max-pooled map out [B,N,Ho/2,Wo/2] (floor); pool = 0
+ * writes the unpooled [B,N,Ho,Wo] instead. Images whose padded planes do not
+ * fit LDS run on kernels that read the image through the caches. */
 int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
                       int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
                       int32_t K, const float* node_param, const float* w,
@@ -372,6 +384,11 @@ int slg_conv_soft_prep(const float* conn, int64_t N, int32_t leaves, int32_t K,
  * these parameters inside every forward (layers.py:487-497, 408-417,
  * nodes.py:178); a caller keeps the records while the parameters and the
  * geometry stay the same. */
+/* 1 if the LDS-staged conv kernels (and so the records forward) take images
+ * (C, H, W) with this tree, K, pad and pooling flag, else 0; the others run
+ * slg_conv_soft_fwd on the kernels that read the image through the caches. */
+int slg_conv_soft_lds_fit(int64_t C, int64_t H, int64_t W, int32_t node_kind, int32_t depth,
+                          int32_t arity, int32_t K, int32_t pad, int32_t pool);
 int64_t slg_conv_soft_record_floats(int32_t node_kind, int32_t depth, int32_t arity,
                                     int32_t K, int32_t pool);
 int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* ch,
@@ -396,10 +413,11 @@ int slg_conv_soft_fwd_records(const float* x, int64_t B, int64_t C, int64_t H, i
  * and dL/dnode_param into gnp; any of the three may be NULL (not computed).
  * A pooled output's gradient goes to the first window position (row-major)
  * that holds the window's maximum. No atomics on values: every sum runs in
- * a fixed order. Supports gate16 trees of depth 1-3 and LUTs of arity 2-6,
- * K <= 8, and images whose C*H*W floats fit LDS next to the per-tree state;
+ * a fixed order. Supports every tree slg_conv_soft_fwd takes with K <= 8
+ * (gate16 trees of depth 1-3 and depth-1 LUTs on an LDS-staged kernel where
+ * the image fits, the others on kernels that read it through the caches);
  * slg_conv_soft_bwd_workspace returns the workspace floats, or -1 for
- * shapes the kernel does not take. */
+ * shapes the kernels do not take. */
 int64_t slg_conv_soft_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
                                     int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
                                     int32_t pad, int32_t pool);
@@ -436,6 +454,30 @@ int slg_conv_hard_prep_net(int32_t n_blocks, const int32_t* const* cm,
                            const int32_t* K, const int32_t* node_kind, const int32_t* depth,
                            const int32_t* arity, int32_t* const* leaf, uint64_t* const* tt,
                            slg_stream_t stream);
+
+/* Hard parameters of any node tree of slg_conv_soft_fwd (ConvLogicTree.
+ * forward_hard, layers.py:505-541 with nodes.py:100-106, 152-156, 183-189):
+ * leaf [N, leaves] int32 (argmax tap cm<<8 | ch<<4 | cw over conn
+ * [N,leaves,K], conn NULL = fixed) and tables [N, nodes] uint64, one truth
+ * table per node, level-major, bit e = the node's output at address
+ * e = sum_j child_j << j. raw[i] is tree level i's parameters read in place:
+ * gate16 logits [N, m_i, 16], walsh theta [N*m_i, 4], LUT logits
+ * [N*m_i, 2^arity] (m_i nodes per channel at level i). */
+int slg_conv_tree_hard_prep(const int32_t* cm, const int32_t* ch, const int32_t* cw,
+                            const float* conn, int64_t N, int32_t K, int32_t node_kind,
+                            int32_t depth, int32_t arity, const float* const* raw, int32_t* leaf,
+                            uint64_t* tables, slg_stream_t stream);
+
+/* The packed node tree of slg_conv_tree_hard_prep with the 2x2 OR pool
+ * fused (pool = 1): xp [C,H,W,nw] -> out [N,Ho/2,Wo/2,nw] or [N,H,W,nw];
+ * stride 1, zero padding pad = (kernel-1)/2. arity is 2 for gate16 / walsh
+ * trees. Replaces the reference's packed_unfold + BitpackedConvTreeLayer /
+ * BitpackedConvLUTLayer + packed_or_pool (packed_layer.py:224-540) for trees
+ * of any depth. */
+int slg_conv_tree_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64_t nw,
+                           int64_t N, int32_t arity, int32_t depth, const int32_t* leaf,
+                           const uint64_t* tables, int32_t kernel, int32_t pad, int32_t pool,
+                           uint64_t* out, slg_stream_t stream);
 
 /* ConvLogicTree.forward_hard + OrPool.forward_hard fused on packed
  * activations (replaces layers.py:529-541,561-563 and the reference's

@@ -96,18 +96,38 @@ def gate_codes(L, sd):
     if L["node"] == "gate16":
         return sd[p + "node.gate_logits"].argmax(dim=1).numpy().astype(np.int32)
     if L["node"] == "walsh":
-        t = sd[p + "node.theta"].numpy()
-        t0, t1, t2, t3 = t[:, 0], t[:, 1], t[:, 2], t[:, 3]
-        b0 = (t0 - t1 - t2 + t3) > 0
-        b1 = (t0 - t1 + t2 - t3) > 0
-        b2 = (t0 + t1 - t2 - t3) > 0
-        b3 = (t0 + t1 + t2 + t3) > 0
-        code = (b0.astype(np.int32) | (b1.astype(np.int32) << 1)
-                | (b2.astype(np.int32) << 2) | (b3.astype(np.int32) << 3))
-        return code_to_gate16()[code]
+        return walsh2_gates(sd[p + "node.theta"].numpy())
     tt = (sd[p + "node.logits"].numpy() > 0).astype(np.int32)
     code = tt[:, 0] | (tt[:, 2] << 1) | (tt[:, 1] << 2) | (tt[:, 3] << 3)
     return code_to_gate16()[code]
+
+
+def walsh2_gates(t):
+    """Arity-2 walsh theta ``[rows, 4]`` -> gate16 index: the sign of z at the
+    four corners, as the converter evaluates it (convert.py:84-97)."""
+    t0, t1, t2, t3 = t[:, 0], t[:, 1], t[:, 2], t[:, 3]
+    b0 = (t0 - t1 - t2 + t3) > 0
+    b1 = (t0 - t1 + t2 - t3) > 0
+    b2 = (t0 + t1 - t2 - t3) > 0
+    b3 = (t0 + t1 + t2 + t3) > 0
+    code = (b0.astype(np.int32) | (b1.astype(np.int32) << 1)
+            | (b2.astype(np.int32) << 2) | (b3.astype(np.int32) << 3))
+    return code_to_gate16()[code]
+
+
+def walsh_truth(theta, n):
+    """``[rows, 2^n]`` truth tables of n-input walsh nodes: the node's own hard
+    rule evaluated at each corner (``_lut_truth_tables``, convert.py:100-123,
+    calling WalshNode.forward_hard, nodes.py:152-156)."""
+    theta = torch.as_tensor(theta)
+    rows = theta.shape[0]
+    cols = []
+    for p in range(2 ** n):
+        corner = torch.tensor([(p >> j) & 1 for j in range(n)], dtype=torch.float32)
+        u = (2 * corner - 1).view(1, 1, n).expand(1, rows, n)
+        z = (torch_ref.walsh_monomials(u) * theta[None]).sum(2)
+        cols.append((z > 0)[0])
+    return torch.stack(cols, dim=1).numpy()
 
 
 def fc_layer(L, sd, xp):
@@ -209,6 +229,18 @@ def conv_block(blk, sd, x3, H, W):
                     res[oi, ni] = GATE_OPS[g](a[oi, ni], b[oi, ni])
             cur = res
         return cur[:, 0]
+    if blk["node"] == "walsh":   # tree nodes as gate16 (convert.py:141-165)
+        for i in range(blk["depth"]):
+            m = cur.shape[1] // 2
+            gates = walsh2_gates(sd[f"{p}tree_nodes.{i}.theta"].numpy()).reshape(n, m)
+            a, b = cur[:, 0::2], cur[:, 1::2]
+            res = np.empty_like(a)
+            for g in range(16):
+                oi, ni = np.where(gates == g)
+                if len(oi):
+                    res[oi, ni] = GATE_OPS[g](a[oi, ni], b[oi, ni])
+            cur = res
+        return cur[:, 0]
     k = blk["node_arity"]
     for i in range(blk["depth"]):
         m = cur.shape[1] // k
@@ -258,5 +290,8 @@ def _fc_any(L, sd, xp):
     if L["arity"] == 2:
         return fc_layer(L, sd, xp)
     idx = torch_ref.hard_indices(L, sd).numpy()
-    tt = lut_truth(sd[L["prefix"] + "node.logits"].numpy())
+    if L["node"] == "walsh":
+        tt = walsh_truth(sd[L["prefix"] + "node.theta"], L["arity"])
+    else:
+        tt = lut_truth(sd[L["prefix"] + "node.logits"].numpy())
     return lut_eval(tt, [xp[idx[:, j]] for j in range(idx.shape[1])])

@@ -71,10 +71,18 @@ def structure(spec):
     """Layer-by-layer description of a reference model built from ``spec``."""
     ctor, a = spec
     a = dict(a)
-    if ctor in ("LogicNet", "WARPNet"):
-        if ctor == "WARPNet":   # models.py:107-114
-            node, arity, node_tau, tau = "walsh", 2, a.get("tau", 1.0), 20.0
+    if ctor in ("LogicNet", "WARPNet", "WARPNetN", "LUTkNet", "LUTNodeNet"):
+        if ctor in ("WARPNet", "WARPNetN"):   # models.py:107-125
+            arity = 2 if ctor == "WARPNet" else a.get("arity", 6)
+            node, node_tau, tau = "walsh", a.get("tau", 1.0), 20.0
             connectome, ste = "topk", True
+        elif ctor == "LUTkNet":               # models.py:128-138: arity k, cand_k candidates
+            node, arity, node_tau, tau = "multilinear", a.get("k", 4), 1.0, a.get("tau", 4.0)
+            connectome, ste = "topk", True
+            a["k"] = a.get("cand_k", 4)
+        elif ctor == "LUTNodeNet":            # models.py:141-147
+            node, arity, node_tau = a.get("relaxation", "probabilistic"), a.get("arity", 4), 1.0
+            tau, connectome, ste = a.get("tau", 10.0), "topk", True
         else:                   # models.py:59-79
             node, arity = a.get("node", "gate16"), a.get("arity", 2)
             node_tau, tau = a.get("node_tau", 1.0), a.get("tau", 1.0)
@@ -286,7 +294,14 @@ def _node_tree(blk, sd, vals, hard):
         n, km, L = vals.shape[1], vals.shape[2], vals.shape[3]
         m = km // k
         ops = vals.view(B, n, m, k, L).permute(0, 4, 1, 2, 3).reshape(B * L, n * m, k)
-        logits = sd[f"{blk['prefix']}tree_nodes.{i}.logits"]
+        logits = sd.get(f"{blk['prefix']}tree_nodes.{i}.logits")
+        if blk["node"] == "walsh":                            # nodes.py:145-156
+            theta = sd[f"{blk['prefix']}tree_nodes.{i}.theta"]
+            u = 2 * ops.float() - 1
+            z = (walsh_monomials(u) * theta[None]).sum(2)
+            out = (z > 0).to(torch.uint8) if hard else torch.sigmoid(z * (1.0 / blk["tau"]))
+            vals = out.view(B, L, n, m).permute(0, 2, 3, 1)
+            continue
         if blk["node"] not in ("multilinear", "hybrid"):
             raise NotImplementedError(blk["node"])
         if hard:

@@ -14,9 +14,10 @@ hand-written HIP kernels in ``libsilogic_hip.so`` behind a C ABI
 (torch.Size([256, 10]), torch.Size([256, 10]))
 
 Compute is GPU-only; CPU tensors raise. Covered: nodes ``gate16``,
-``walsh`` (arity 2), ``multilinear`` (arity 2 in FC layers, 2-6 in depth-1
-conv trees); wiring ``topk``, ``blocktopk``, ``fixed``; ``GroupSum`` heads;
-``ConvLogicTree`` + ``OrPool``.
+``walsh`` (any arity), ``multilinear`` and ``hybrid`` (arity 2-6) in FC
+layers and conv trees (binary trees of depth 1-5, LUT trees of at most 36
+leaves); wiring ``topk``, ``blocktopk``, ``fixed``; ``GroupSum`` heads;
+``ConvLogicTree`` + ``OrPool``; the layer and network presets.
 """
 
 __version__ = "0.1.0"
@@ -27,8 +28,9 @@ from .functional import (BASIS_COEFFS, TRUTH_TABLES, GATE_A, ste_threshold, sign
 from .connectomes import build_connectome
 from .nodes import build_node, NODES, RELAXATIONS
 from .heads import GroupSum, build_decoder
-from .layers import LogicLayer, WARPLayer, ConvLogicTree, ConvLogicLayer, OrPool
-from .models import LogicNet, WARPNet, LogicConvNet, LogicTreeNet
+from .layers import (LogicLayer, WARPLayer, WARPLayerN, LUTkLayer, LUTNodeLayer, ConvLogicTree,
+                     ConvLogicLayer, OrPool)
+from .models import LogicNet, WARPNet, WARPNetN, LUTkNet, LUTNodeNet, LogicConvNet, LogicTreeNet
 from .encoders import LearnedThermometerEncoder
 from .data import (binarize, binarize_spatial, binarize_packed, edge_bits, MNIST_THRESH,
                    SEVEN_THRESH, FOUR_THRESH, FIVE_THRESH, CIFAR3_THRESH, EDGE_THRESH)
@@ -38,8 +40,9 @@ __all__ = [
     "BASIS_COEFFS", "TRUTH_TABLES", "GATE_A", "ste_threshold", "sign_ste", "ternary_ste",
     "binarize_ste", "gate_probs", "residual_logit", "corner_bits", "walsh_monomials",
     "build_connectome", "build_node", "NODES", "RELAXATIONS", "GroupSum", "build_decoder",
-    "LogicLayer", "WARPLayer", "ConvLogicTree", "ConvLogicLayer", "OrPool",
-    "LogicNet", "WARPNet", "LogicConvNet", "LogicTreeNet", "kernels", "ops",
+    "LogicLayer", "WARPLayer", "WARPLayerN", "LUTkLayer", "LUTNodeLayer", "ConvLogicTree",
+    "ConvLogicLayer", "OrPool", "LogicNet", "WARPNet", "WARPNetN", "LUTkNet", "LUTNodeNet",
+    "LogicConvNet", "LogicTreeNet", "kernels", "ops",
     "LearnedThermometerEncoder", "binarize", "binarize_spatial", "binarize_packed", "edge_bits",
     "MNIST_THRESH", "SEVEN_THRESH", "FOUR_THRESH", "FIVE_THRESH", "CIFAR3_THRESH", "EDGE_THRESH",
 ]

@@ -32,7 +32,7 @@ SIGNATURES = {
     "slg_fc_soft_groupsum_supported": (C.c_int, [_I64, _I64, _I64, _I32]),
     "slg_groupsum_soft": (C.c_int, [_P, _I64, _I64, _I32, _F32, _I32, _P, _P]),
     "slg_groupsum_hard": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
-    "slg_orpool": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P]),
+    "slg_orpool": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P]),
     "slg_pack_bits": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_unpack_bits": (C.c_int, [_P, _I64, _I64, _P, _P]),
     "slg_fc_hard_prep": (C.c_int, [_P, _P, _I64, _I32, _I64, _I32, _P, _P, _P]),
@@ -71,6 +71,7 @@ SIGNATURES = {
     "slg_conv_soft_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P,
                                     _P, _P, _P, _P, _I32, _I32, _P, _P]),
     "slg_conv_soft_prep": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "slg_conv_soft_lds_fit": (C.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32]),
     "slg_conv_soft_record_floats": (C.c_int64, [_I32, _I32, _I32, _I32, _I32]),
     "slg_conv_soft_records": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _I64,
                                         _I64, _I64, _I32, _I32, _P, _P]),
@@ -80,6 +81,10 @@ SIGNATURES = {
                                      _P, _P]),
     "slg_conv_hard_prep_net": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                          _P]),
+    "slg_conv_tree_hard_prep": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
+                                          _P, _P]),
+    "slg_conv_tree_hard_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P,
+                                         _I32, _I32, _I32, _P, _P]),
     "slg_conv_hard_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P,
                                     _I32, _I32, _I32, _P, _P]),
 }

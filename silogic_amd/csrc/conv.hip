@@ -561,19 +561,24 @@ __global__ void __launch_bounds__(128) conv_hard_prep_kernel(ConvPrepNet net) {
   P.tt[n] = t;
 }
 
+// size x size max pool with stride size and floor (F.max_pool2d(x, s, s)),
+// the window scanned row-major.
 template <typename T>
-__global__ void orpool_kernel(const T* __restrict__ x, int64_t BC, int H, int W, T* __restrict__ out) {
-  const int Ho = H / 2, Wo = W / 2;
+__global__ void orpool_kernel(const T* __restrict__ x, int64_t BC, int H, int W, int size,
+                              T* __restrict__ out) {
+  const int Ho = H / size, Wo = W / size;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= BC * Ho * Wo) return;
   const int64_t bc = i / (Ho * Wo);
   const int r = (int)(i - bc * Ho * Wo);
   const int py = r / Wo, px = r - (r / Wo) * Wo;
-  const T* src = x + bc * H * W + (2 * py) * W + 2 * px;
+  const T* src = x + bc * H * W + (int64_t)(size * py) * W + size * px;
   T m = src[0];
-  m = m > src[1] ? m : src[1];
-  m = m > src[W] ? m : src[W];
-  m = m > src[W + 1] ? m : src[W + 1];
+  for (int dy = 0; dy < size; ++dy)
+    for (int dx = 0; dx < size; ++dx) {
+      const T v = src[dy * W + dx];
+      m = m > v ? m : v;
+    }
   out[i] = m;
 }
 
@@ -752,11 +757,13 @@ int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
                       const int32_t* cw, int32_t pad, int32_t pool, float* out, slg_stream_t stream) {
   SLG_REQUIRE(node_param && cm && ch && cw && ((x && out) || B == 0), SLG_E_ARG,
               "conv_soft: null pointer");
-  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2 ||
-                  node_kind == SLG_NODE_HYBRID,
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_WALSH ||
+                  node_kind == SLG_NODE_MULTILINEAR2 || node_kind == SLG_NODE_HYBRID,
               SLG_E_ARG, "conv_soft: node_kind %d", node_kind);
   const int nleaf = node_leaves(node_kind, depth, arity);
-  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft: depth %d / arity %d", depth, arity);
+  const bool generic = conv_generic_supported(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0 || generic, SLG_E_UNSUPPORTED, "conv_soft: node %d depth %d / arity %d",
+              node_kind, depth, arity);
   SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft: K=%d outside 1..%d", K, kMaxK);
   SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && N > 0 && pad >= 0 && pad <= 4 &&
                   B < (1LL << 31) && N < (1LL << 20) && C < (1LL << 20) && H < 4096 && W < 4096,
@@ -765,9 +772,33 @@ int slg_conv_soft_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
   const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
   const int64_t Ho = pool ? Hf / 2 : Hf, Wo = pool ? Wf / 2 : Wf;
   if (B == 0 || Ho == 0 || Wo == 0) return 0;
-  ConvSoftArgs a{x, B, C, H, W, N, K, kernel, pad, node_param, w, cm, ch, cw, out, Ho, Wo, nullptr};
-  return pool ? conv_soft_dispatch<true>(a, node_kind, nleaf, as_stream(stream))
-              : conv_soft_dispatch<false>(a, node_kind, nleaf, as_stream(stream));
+  if (nleaf > 0) {
+    ConvSoftArgs a{x, B, C, H, W, N, K, kernel, pad, node_param, w, cm, ch, cw, out, Ho, Wo,
+                   nullptr};
+    const int rc = pool ? conv_soft_dispatch<true>(a, node_kind, nleaf, as_stream(stream))
+                        : conv_soft_dispatch<false>(a, node_kind, nleaf, as_stream(stream));
+    // an image that does not fit LDS goes to the generic kernel (nothing was
+    // launched: the rejection comes before the launch)
+    if (rc != SLG_E_UNSUPPORTED || !generic) return rc;
+  }
+  return conv_generic_fwd(x, B, C, H, W, N, node_kind, depth, arity, K, kernel, pad, pool != 0,
+                          node_param, w, cm, ch, cw, out, Ho, Wo, as_stream(stream));
+}
+
+int slg_conv_soft_lds_fit(int64_t C, int64_t H, int64_t W, int32_t node_kind, int32_t depth,
+                          int32_t arity, int32_t K, int32_t pad, int32_t pool) {
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  if (nleaf <= 0 || K < 1 || K > kMaxK || C <= 0 || H <= 0 || W <= 0 || pad < 0 || pad > 4 ||
+      C >= (1LL << 20) || H >= 4096 || W >= 4096)
+    return 0;
+  const int kernel = 2 * pad + 1;
+  const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
+  const int64_t Ho = pool ? Hf / 2 : Hf, Wo = pool ? Wf / 2 : Wf;
+  const int km = K <= 4 ? 4 : kMaxK;
+  const ConvGeom g = conv_geom(C, H, W, pad, pool != 0, conv_phase_layout(pool != 0, nleaf, km),
+                               Ho, Wo);
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  return ((int64_t)g.SST * 4 + kConvExtra * 4 <= cap && C * H * W * 4 < (1LL << 31)) ? 1 : 0;
 }
 
 int64_t slg_conv_soft_record_floats(int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
@@ -973,20 +1004,23 @@ int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64
                                           pad, out, Ho, Wo, st);
 }
 
-int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W, void* out,
-               slg_stream_t stream) {
+int slg_orpool(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W,
+               int32_t size, void* out, slg_stream_t stream) {
   SLG_REQUIRE((x && out) || B == 0, SLG_E_ARG, "orpool: null pointer");
   SLG_REQUIRE(dtype == 0 || dtype == 1, SLG_E_ARG, "orpool: dtype %d", dtype);
+  SLG_REQUIRE(size >= 1 && size <= 64, SLG_E_SHAPE, "orpool: size %d", size);
   SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && B * C * H * W < (1LL << 46), SLG_E_SHAPE,
               "orpool: bad sizes");
-  const int64_t n = B * C * (H / 2) * (W / 2);
+  const int64_t n = B * C * (H / size) * (W / size);
   if (n == 0) return 0;
   if (dtype == 0)
     hipLaunchKernelGGL(orpool_kernel<float>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
-                       as_stream(stream), (const float*)x, B * C, (int)H, (int)W, (float*)out);
+                       as_stream(stream), (const float*)x, B * C, (int)H, (int)W, (int)size,
+                       (float*)out);
   else
     hipLaunchKernelGGL(orpool_kernel<uint8_t>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
-                       as_stream(stream), (const uint8_t*)x, B * C, (int)H, (int)W, (uint8_t*)out);
+                       as_stream(stream), (const uint8_t*)x, B * C, (int)H, (int)W, (int)size,
+                       (uint8_t*)out);
   SLG_LAUNCH_CHECK("orpool");
   return 0;
 }

@@ -726,20 +726,25 @@ int64_t slg_conv_soft_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, 
                                     int32_t node_kind, int32_t depth, int32_t arity, int32_t K,
                                     int32_t pad, int32_t pool) {
   const int nleaf = conv_bwd_leaves(node_kind, depth, arity);
-  if (nleaf <= 0 || K < 1 || K > kBwdMaxK || B < 0 || C <= 0 || H <= 0 || W <= 0 || N <= 0 ||
-      pad < 0 || pad > 4 || B >= (1LL << 31) || N >= (1LL << 20) || C >= (1LL << 20) ||
-      H >= 4096 || W >= 4096 || N * nleaf * K >= (1LL << 31))
+  if (K < 1 || K > kBwdMaxK || B < 0 || C <= 0 || H <= 0 || W <= 0 || N <= 0 || pad < 0 ||
+      pad > 4 || B >= (1LL << 31) || N >= (1LL << 20) || C >= (1LL << 20) || H >= 4096 ||
+      W >= 4096)
     return -1;
   const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
   if (Ho == 0 || Wo == 0) return 0;
-  ConvBwdPlan p{};
-  bool ok = false;
-  conv_bwd_dispatch(node_kind, nleaf, pool != 0, [&](auto nd, auto nl, auto pl) {
-    ok = conv_bwd_plan_t<decltype(nd)::value, decltype(nl)::value, decltype(pl)::value>(
-        std::max<int64_t>(B, 1), C, H, W, N, K, pad, Ho, Wo, p);
-    return 0;
-  });
-  return ok ? p.total() : -1;
+  if (nleaf > 0 && N * nleaf * K < (1LL << 31)) {
+    ConvBwdPlan p{};
+    bool ok = false;
+    conv_bwd_dispatch(node_kind, nleaf, pool != 0, [&](auto nd, auto nl, auto pl) {
+      ok = conv_bwd_plan_t<decltype(nd)::value, decltype(nl)::value, decltype(pl)::value>(
+          std::max<int64_t>(B, 1), C, H, W, N, K, pad, Ho, Wo, p);
+      return 0;
+    });
+    if (ok) return p.total();
+  }
+  // trees the LDS kernel does not take (walsh, deeper LUT trees, images past
+  // LDS): the generic kernels
+  return conv_generic_bwd_workspace(B, C, H, W, N, node_kind, depth, arity, K, pad, pool != 0);
 }
 
 int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
@@ -750,20 +755,41 @@ int slg_conv_soft_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W
                       int64_t workspace_floats, slg_stream_t stream) {
   SLG_REQUIRE(node_param && cm && ch && cw && workspace && ((x && gy) || B == 0), SLG_E_ARG,
               "conv_soft_bwd: null pointer");
-  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2 ||
-                  node_kind == SLG_NODE_HYBRID,
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_WALSH ||
+                  node_kind == SLG_NODE_MULTILINEAR2 || node_kind == SLG_NODE_HYBRID,
               SLG_E_ARG, "conv_soft_bwd: node_kind %d", node_kind);
   const int nleaf = conv_bwd_leaves(node_kind, depth, arity);
-  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_bwd: depth %d / arity %d", depth, arity);
+  const bool generic = conv_generic_supported(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0 || generic, SLG_E_UNSUPPORTED, "conv_soft_bwd: node %d depth %d / arity %d",
+              node_kind, depth, arity);
   SLG_REQUIRE(K >= 1 && K <= kBwdMaxK, SLG_E_SHAPE, "conv_soft_bwd: K=%d outside 1..%d", K,
               kBwdMaxK);
   SLG_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && N > 0 && pad >= 0 && pad <= 4 &&
                   B < (1LL << 31) && N < (1LL << 20) && C < (1LL << 20) && H < 4096 &&
-                  W < 4096 && N * nleaf * K < (1LL << 31),
+                  W < 4096 && N * std::max(nleaf, 1) * K < (1LL << 31),
               SLG_E_SHAPE, "conv_soft_bwd: bad sizes");
   const int kernel = 2 * pad + 1;  // 'same' convolution, stride 1 (models.py:222)
   const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
   hipStream_t st = as_stream(stream);
+  // the LDS kernel where its plan takes the shape, else the generic kernels
+  // (the same choice as slg_conv_soft_bwd_workspace)
+  bool lds_path = false;
+  if (nleaf > 0) {
+    ConvBwdPlan p0{};
+    conv_bwd_dispatch(node_kind, nleaf, pool != 0, [&](auto nd, auto nl, auto pl) {
+      lds_path = conv_bwd_plan_t<decltype(nd)::value, decltype(nl)::value, decltype(pl)::value>(
+          std::max<int64_t>(B, 1), C, H, W, N, K, pad, std::max<int64_t>(Ho, 1),
+          std::max<int64_t>(Wo, 1), p0);
+      return 0;
+    });
+  }
+  if (!lds_path) {
+    SLG_REQUIRE(generic, SLG_E_UNSUPPORTED, "conv_soft_bwd: image of %lld floats does not fit LDS",
+                (long long)(C * H * W));
+    return conv_generic_bwd(x, B, C, H, W, N, node_kind, depth, arity, K, pad, pool != 0,
+                            node_param, w, cm, ch, cw, gy, gx, gw, gnp, workspace,
+                            workspace_floats, st);
+  }
   const int64_t CHW = C * H * W;
   if (B == 0) {
     // no samples: zero weight / parameter gradients (a sum over no ranges)

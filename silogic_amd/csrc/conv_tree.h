@@ -64,4 +64,23 @@ __device__ inline float conv_tree_eval(const float (&v)[NLEAF], const float* par
   }
 }
 
+// Node trees on the generic kernels (conv_generic.hip): gate16 and walsh
+// binary trees of depth 1-5, multilinear and hybrid LUT trees with at most
+// 36 leaves (arity 2: depth <= 5; 3: <= 3; 4-6: <= 2), any image size.
+// Parameters [N][nodes][P] level-major, P = 4 (gate16 coefficients, walsh
+// coefficients times 1/tau) or 2^arity (LUT values).
+bool conv_generic_supported(int node, int depth, int arity);
+int conv_generic_params(int node, int depth, int arity);
+int conv_generic_fwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                     int node, int depth, int arity, int K, int kernel, int pad, bool pool,
+                     const float* np, const float* w, const int* cm, const int* ch, const int* cw,
+                     float* out, int64_t Ho, int64_t Wo, hipStream_t st);
+int64_t conv_generic_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t N, int node,
+                                   int depth, int arity, int K, int pad, bool pool);
+int conv_generic_bwd(const float* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t N,
+                     int node, int depth, int arity, int K, int pad, bool pool, const float* np,
+                     const float* w, const int* cm, const int* ch, const int* cw, const float* gy,
+                     float* gx, float* gw, float* gnp, float* ws, int64_t ws_floats,
+                     hipStream_t st);
+
 }  // namespace slg

@@ -85,10 +85,18 @@ class LogicLayer(nn.Module):
     # -- HIP dispatch ----------------------------------------------------------
     @property
     def is_lut(self):
-        """An n-input LUT layer (the hybrid node, or a multilinear node of
-        arity other than 2): ``slg_fc_lut_*`` instead of the gate kernels."""
+        """An n-input LUT layer (the hybrid node, or a multilinear or walsh
+        node of arity other than 2): ``slg_fc_lut_*`` instead of the gate
+        kernels."""
         return getattr(self.node, "hybrid", False) or (
-            self._node_name == "multilinear" and self.arity != 2)
+            self._node_name in ("multilinear", "walsh") and self.arity != 2)
+
+    @property
+    def is_walsh_n(self):
+        """An n-input walsh layer (nodes.py:130-156): z is multilinear in the
+        operands, so it is the LUT layer's interpolation of z's corner values
+        (``WalshNode.corner_z``), followed by sigmoid(z / tau)."""
+        return self._node_name == "walsh" and self.arity != 2
 
     def _check_supported(self):
         if self.arity != 2 or self.is_lut:
@@ -97,10 +105,14 @@ class LogicLayer(nn.Module):
                 "take arity-2 gate16 / walsh / multilinear nodes (LUT layers run slg_fc_lut_*)")
 
     def lut_hard_codes(self):
-        """``(idx [out, n] int32, tt [out] int64)`` of a LUT layer (HIP prep)."""
+        """``(idx [out, n] int32, tt [out] int64)`` of a LUT layer (HIP prep;
+        bit p of tt is ``logits[p] > 0``). For an n-input walsh node the
+        "logits" are z at the corners, evaluated on the CPU with the node's
+        own fp32 expression (nodes.py:152-156), so that its signs are the
+        reference's also at near-ties."""
         conn = None if isinstance(self._conn, FixedConnectome) else self._conn.conn
-        return ops.fc_lut_hard_codes(self._conn.candidates_i32(), conn, self.node.logits,
-                                     self.in_dim)
+        logits = self.node.corner_z_hard() if self.is_walsh_n else self.node.logits
+        return ops.fc_lut_hard_codes(self._conn.candidates_i32(), conn, logits, self.in_dim)
 
     def _inv_tau(self):
         return self.node.inv_tau if self._node_name == "walsh" else 1.0
@@ -158,6 +170,13 @@ class LogicLayer(nn.Module):
         ops.check_width(x, self.in_dim)
         if self.is_lut:
             conn = self._conn
+            if self.is_walsh_n:
+                if not self.node.plain_softmax():
+                    raise NotImplementedError("walsh Gumbel smoothing in training is not on the "
+                                              "MI355X path")
+                z = ops.fc_lut_soft(x, conn.candidates_i32(), conn.weights(),
+                                    self.node.corner_z(), False)
+                return torch.sigmoid(z * self.node.inv_tau)
             return ops.fc_lut_soft(x, conn.candidates_i32(), conn.weights(),
                                    torch.sigmoid(self.node.logits), self.node.hybrid)
         self._check_supported()
@@ -211,11 +230,78 @@ class WARPLayer(LogicLayer):
         return self.node.coef()
 
 
+class WARPLayerN(LogicLayer):
+    """Arity-``n`` Walsh (WARP) node with Top-K connectivity (preset,
+    silogic/layers.py:162-174)."""
+
+    def __init__(self, in_dim, out_dim, arity=6, k=8, tau=1.0, residual_p=0.0,
+                 seed=None, gate_select="softmax"):
+        super().__init__(in_dim, out_dim, node="walsh", connectome="topk", arity=arity,
+                         k=k, tau=tau, residual_p=residual_p, seed=seed,
+                         gate_select=gate_select)
+
+    @property
+    def theta(self):
+        return self.node.theta
+
+
+class LUTkLayer(LogicLayer):
+    """k-input multilinear LUT node (one FPGA LUT_k) with Top-K input
+    selection (preset, silogic/layers.py:177-199): ``k`` LUT inputs drawn
+    among ``cand_k`` candidates each."""
+
+    def __init__(self, in_dim, out_dim, k=4, learn_conn=True, cand_k=4, seed=None):
+        conn = "topk" if learn_conn else "fixed"
+        super().__init__(in_dim, out_dim, node="multilinear", connectome=conn,
+                         arity=k, k=cand_k, seed=seed)
+        self.k = k
+        self.learn_conn = learn_conn
+
+    @property
+    def lut(self):
+        return self.node.logits
+
+    @property
+    def conn(self):
+        return self._conn.conn
+
+    @property
+    def cand(self):
+        return self._conn.cand
+
+
+class LUTNodeLayer(LogicLayer):
+    """n-input LUT node with a selectable relaxation (preset,
+    silogic/layers.py:202-224): ``probabilistic`` (multilinear) or
+    ``hybrid`` on the HIP path."""
+
+    def __init__(self, in_dim, out_dim, arity=4, relaxation="probabilistic", k=8,
+                 degree=None, residual_p=0.0, seed=None):
+        super().__init__(in_dim, out_dim, node=relaxation, connectome="topk",
+                         arity=arity, k=k, degree=degree, residual_p=residual_p,
+                         seed=seed)
+        self.relaxation = relaxation
+        self.n = arity
+        self.k = self._conn.k
+
+    @property
+    def conn(self):
+        return self._conn.conn
+
+    @property
+    def cand(self):
+        return self._conn.cand
+
+
 class ConvLogicTree(nn.Module):
     """Logic-gate-tree convolution (arguments as silogic.layers.ConvLogicTree).
 
-    The HIP path covers gate16 trees of depth 1-4 and depth-1 multilinear or
-    hybrid LUT nodes of arity 2-6, stride 1 with ``padding = kernel // 2``."""
+    The HIP path covers every tree the reference builds for the gate16,
+    walsh, multilinear and hybrid nodes (binary trees of depth 1-5, LUT trees
+    of arity 2-6 with at most 36 leaves), stride 1 with ``padding = kernel //
+    2``. Gate16 trees of depth 1-4 and depth-1 LUTs run on the LDS-staged
+    kernels (records without gradients); the others on the generic tree
+    kernels, with parameters from differentiable torch ops."""
 
     def __init__(self, in_channels, out_channels, kernel=3, tree_depth=None,
                  stride=1, padding=1, connect="topk", k=4, n_chan=2,
@@ -240,11 +326,12 @@ class ConvLogicTree(nn.Module):
         self.k = k
         self.tau = tau
         self.use_triton = use_triton
-        if self.node_name not in ("gate16", "multilinear", "hybrid"):
+        if self.node_name not in ("gate16", "walsh", "multilinear", "hybrid"):
             raise NotImplementedError(f"conv node {node!r} is not on the MI355X path")
-        if self.node_name in ("multilinear", "hybrid") and (
-                tree_depth != 1 or not 2 <= arity <= 6):
-            raise NotImplementedError(f"{self.node_name} conv trees: depth 1, arity 2..6")
+        if not 2 <= self.node_arity <= 6 or self.leaves > 36 or tree_depth > 5:
+            raise NotImplementedError(
+                f"{self.node_name} conv trees: arity 2..6 with at most 36 leaves (depth <= 5), "
+                f"got arity {self.node_arity} depth {tree_depth}")
         if stride != 1 or 2 * padding + 1 != kernel:
             raise NotImplementedError("conv trees: stride 1 with padding = kernel // 2")
         gen = torch.Generator().manual_seed(seed)
@@ -326,9 +413,17 @@ class ConvLogicTree(nn.Module):
         return self.lc_cm, self.lc_ch, self.lc_cw
 
     def _kind(self):
+        return {"gate16": ops.GATE16, "walsh": ops.WALSH, "hybrid": ops.HYBRID}.get(
+            self.node_name, ops.MULTILINEAR2)
+
+    @property
+    def generic(self):
+        """True for trees outside the LDS-staged kernels' set (walsh trees,
+        LUT trees deeper than one level, gate16 trees of depth 5): their
+        parameters come from torch ops, the hard path from per-node tables."""
         if self.node_name == "gate16":
-            return ops.GATE16
-        return ops.HYBRID if self.node_name == "hybrid" else ops.MULTILINEAR2
+            return self.d > 4
+        return self.node_name == "walsh" or self.d != 1
 
     def _raw(self):
         if self.node_name == "gate16":
@@ -348,8 +443,26 @@ class ConvLogicTree(nn.Module):
                        gumbel_tau=self.gumbel_tau)
         return p @ self.basis
 
+    def _node_params(self):
+        """Differentiable node parameters ``[n, nodes, P]``, level-major (the
+        kernels' tree layout): gate16 BasisProj coefficients, walsh (a, b)
+        coefficients times 1/tau, LUT values sigmoid(logits) (the reference's
+        ``_hybrid_s``, layers.py:499-503)."""
+        if self.node_name == "gate16":
+            return self._basis_coef()
+        if self.node_name == "walsh":
+            return torch.cat([nd.coef().view(self.n, -1, 4) for nd in self.tree_nodes],
+                             dim=1) * (1.0 / self.tau)
+        P = 2 ** self.node_arity
+        return torch.cat([torch.sigmoid(nd.logits).view(self.n, -1, P)
+                          for nd in self.tree_nodes], dim=1)
+
     def soft_params(self, grad):
         K = 1 if self.connect == "fixed" else self.k
+        if self.generic:
+            w = (torch.ones(self.n, self.leaves, 1, device=self.cm_idx.device)
+                 if self.connect == "fixed" else self._topk_w())
+            return w, self._node_params()
         if grad or not self._plain_soft():
             w = (torch.ones(self.n, self.leaves, 1, device=self.cm_idx.device)
                  if self.connect == "fixed" else self._topk_w())
@@ -376,9 +489,15 @@ class ConvLogicTree(nn.Module):
 
     def _soft(self, x, pool):
         ops.require_gpu(x)
+        if x.shape[1] < self.cin:
+            raise ValueError(f"ConvLogicTree: input has {x.shape[1]} channels, the trees read "
+                             f"channels up to in_channels = {self.cin}")
         cm, ch, cw = self._taps()
         K = cm.shape[-1]
-        if not _needs_grad(self, x) and self._plain_soft():
+        if not self.generic and not _needs_grad(self, x) and self._plain_soft() and \
+                not torch.compiler.is_compiling() and ops.conv_fits_lds(tuple(x.shape[1:]), self.padding,
+                                                                        pool, self._kind(), self.d,
+                                                                        self.node_arity, K):
             rec = self.soft_records(x.shape[1:], pool)
             return ops.conv_soft_rec(x, rec, self.n, self._kind(), self.d, self.node_arity, K,
                                      self.padding, pool)
@@ -394,22 +513,34 @@ class ConvLogicTree(nn.Module):
         return self._soft(x, pool=True)
 
     def hard_spec(self):
-        """Arguments of ``ops.conv_hard_prep_net`` for this block: taps,
-        connection logits and the node logits per tree level, read in place."""
+        """Arguments of ``ops.conv_hard_prep_net`` (or, for a generic tree,
+        ``ops.conv_tree_hard_prep``) for this block: taps, connection logits
+        and the node parameters per tree level, read in place."""
         cm, ch, cw = self._taps()
         conn = None if self.connect == "fixed" else self.conn
-        levels = (list(self.gate_logits) if self.node_name == "gate16"
-                  else [self.tree_nodes[0].logits])
+        if self.node_name == "gate16":
+            levels = list(self.gate_logits)
+        elif self.node_name == "walsh":
+            levels = [nd.theta for nd in self.tree_nodes]
+        else:
+            levels = [nd.logits for nd in self.tree_nodes]
         return cm, ch, cw, conn, levels, self._kind(), self.d, self.node_arity
 
     def hard_params(self):
-        """``(leaf [n, leaves] int32, tt [n] int64)`` of the hard forward."""
+        """``(leaf [n, leaves] int32, tt)`` of the hard forward: ``tt`` [n]
+        int64 (one word of tables per channel) for the LDS-kernel trees,
+        [n, nodes] int64 per-node tables for a generic tree."""
+        if self.generic:
+            return ops.conv_tree_hard_prep(*self.hard_spec())
         return ops.conv_hard_prep_net([self.hard_spec()])[0]
 
     def packed_forward(self, xp, chw, pool, params=None):
         """Packed ``[C,H,W,nw]`` -> ``[n,Ho,Wo,nw]`` (2x2 OR-pooled if ``pool``);
         ``params`` = ``hard_params()`` when the caller computed them already."""
         leaf, tt = self.hard_params() if params is None else params
+        if self.generic:
+            return ops.conv_tree_hard(xp, chw, leaf, tt, self.node_arity, self.d, self.kh,
+                                      self.padding, pool)
         return ops.conv_hard(xp, chw, leaf, tt, self._kind(), self.d, self.node_arity,
                              self.kh, self.padding, pool)
 
@@ -427,17 +558,16 @@ ConvLogicLayer = ConvLogicTree
 
 
 class OrPool(nn.Module):
-    """Logical OR pooling = spatial 2x2 max-pool (floor)."""
+    """Logical OR pooling = spatial ``size`` x ``size`` max-pool with stride
+    ``size`` (floor), silogic/layers.py:548-563."""
 
     def __init__(self, size=2):
         super().__init__()
-        if size != 2:
-            raise NotImplementedError("OrPool: size 2 only on the MI355X path")
         self.size = size
 
     def forward(self, x):
-        return ops.orpool(x)
+        return ops.orpool(x, self.size)
 
     @torch.no_grad()
     def forward_hard(self, x):
-        return ops.orpool(x.to(torch.uint8))
+        return ops.orpool(x.to(torch.uint8), self.size)

@@ -160,26 +160,29 @@ groupsum_soft.register_autograd(_groupsum_backward, setup_context=_groupsum_setu
 # OrPool.forward (layers.py:558-559): 2x2 max pool; the gradient of
 # F.max_pool2d (to the first maximum of each window).
 @torch.library.custom_op(f"{_NS}::orpool", mutates_args=())
-def orpool(x: Tensor) -> Tensor:
-    return ops.orpool_launch(x)
+def orpool(x: Tensor, size: int) -> Tensor:
+    return ops.orpool_launch(x, size)
 
 
 @orpool.register_fake
-def _(x):
+def _(x, size):
     B, C, H, W = x.shape
-    return x.new_empty((B, C, H // 2, W // 2))
+    return x.new_empty((B, C, H // size, W // size))
 
 
 def _orpool_setup(ctx, inputs, output):
     ctx.save_for_backward(inputs[0])
+    ctx.size = inputs[1]
 
 
 def _orpool_backward(ctx, g):
     (x,) = ctx.saved_tensors
+    s = ctx.size
     xf = x.float()
-    _, idx = torch.ops.aten.max_pool2d_with_indices(xf, [2, 2], [2, 2])
-    return torch.ops.aten.max_pool2d_with_indices_backward(g, xf, [2, 2], [2, 2], [0, 0],
-                                                          [1, 1], False, idx)
+    _, idx = torch.ops.aten.max_pool2d_with_indices(xf, [s, s], [s, s])
+    gx = torch.ops.aten.max_pool2d_with_indices_backward(g, xf, [s, s], [s, s], [0, 0], [1, 1],
+                                                         False, idx)
+    return gx, None
 
 
 orpool.register_autograd(_orpool_backward, setup_context=_orpool_setup)

@@ -1,5 +1,6 @@
-"""Networks (mirror of silogic/models.py): ``LogicNet`` (+ ``WARPNet``,
-``LUTkNet``, ``LUTNodeNet`` presets) and ``LogicConvNet`` / ``LogicTreeNet``.
+"""Networks (mirror of silogic/models.py): ``LogicNet`` (+ the ``WARPNet``,
+``WARPNetN``, ``LUTkNet``, ``LUTNodeNet`` presets) and ``LogicConvNet`` /
+``LogicTreeNet``.
 
 Construction and ``state_dict`` keys follow the reference (per-layer seeds
 ``seed*seed_mult+i``, conv block seeds ``seed*17+i``, head seeds ``seed*31+j``;
@@ -178,6 +179,40 @@ class WARPNet(LogicNet):
                          seed=seed, gate_select=gate_select)
 
 
+class WARPNetN(LogicNet):
+    """Stack of arity-``n`` Walsh (WARP) layers + GroupSum head (preset,
+    silogic/models.py:117-125)."""
+
+    def __init__(self, in_dim, width, depth, arity=6, num_classes=10, k=8, tau=1.0,
+                 residual_p=0.0, seed=0, gate_select="softmax"):
+        super().__init__(in_dim, width, depth, num_classes=num_classes, node="walsh",
+                         arity=arity, k=k, node_tau=tau, tau=20.0, residual_p=residual_p,
+                         seed=seed, gate_select=gate_select)
+
+
+class LUTkNet(LogicNet):
+    """Stack of k-input multilinear LUT layers + GroupSum head (preset,
+    silogic/models.py:128-138)."""
+
+    def __init__(self, in_dim, width, depth, k=4, num_classes=10, tau=4.0, cand_k=4, seed=0):
+        super().__init__(in_dim, width, depth, num_classes=num_classes, node="multilinear",
+                         arity=k, k=cand_k, tau=tau, seed=seed)
+        self.lut_inputs = k
+
+    def num_luts(self):
+        return self.width * self.depth
+
+
+class LUTNodeNet(LogicNet):
+    """Stack of n-input LUT-node layers (selectable relaxation) + GroupSum
+    head (preset, silogic/models.py:141-147)."""
+
+    def __init__(self, in_dim, width, depth, arity=4, relaxation="probabilistic",
+                 num_classes=10, k=8, tau=10.0, residual_p=0.0, seed=0):
+        super().__init__(in_dim, width, depth, num_classes=num_classes, node=relaxation,
+                         arity=arity, k=k, tau=tau, residual_p=residual_p, seed=seed)
+
+
 class LogicConvNet(nn.Module):
     """Convolutional logic-gate-tree network with a logic head (arguments as
     silogic.models.LogicConvNet)."""
@@ -231,7 +266,7 @@ class LogicConvNet(nn.Module):
                 r = min(int(conv.n * self.wire_residual), x_in.shape[1])
                 if r > 0:
                     y = torch.cat([x_in[:, :r], y[:, r:]], dim=1)
-                x = ops.orpool(y)
+                x = ops.orpool(y, 2)
             else:
                 x = conv.forward_pooled(x)
         return x
@@ -265,7 +300,11 @@ class LogicConvNet(nn.Module):
         if xp.shape[0] != C * H * W:
             raise ValueError("forward_hard_packed: %d rows for C*H*W = %d" % (xp.shape[0], C * H * W))
         convs = list(self._convs())
-        params = ops.conv_hard_prep_net([conv.hard_spec() for conv in convs])
+        # the LDS-kernel trees of every block in one prep launch, generic
+        # trees (walsh, deeper LUT trees) with their own per-node tables
+        lds = [conv for conv in convs if not conv.generic]
+        batched = iter(ops.conv_hard_prep_net([conv.hard_spec() for conv in lds]) if lds else [])
+        params = [conv.hard_params() if conv.generic else next(batched) for conv in convs]
         for conv, prm in zip(convs, params):
             x_in = xp
             xp = conv.packed_forward(xp, (C, H, W), pool=True, params=prm)

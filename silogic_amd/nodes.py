@@ -121,6 +121,32 @@ class WalshNode(Node):
 
     kernel_param = coef
 
+    def _corner_monomials(self, device):
+        """``[2^n, 2^n]`` monomial values at the corners: row p is
+        walsh_monomials(2c - 1) for corner c = bits of p (entry q = product
+        of u_j over the bits j of q, functional.py:176-185)."""
+        u = 2 * corner_bits(self.arity).to(device) - 1                 # [P, n]
+        return walsh_monomials(u.unsqueeze(0))[0]                       # [P, P]
+
+    def corner_z(self):
+        """z at the ``2^n`` corners ``[out, 2^n]`` (differentiable): z is
+        multilinear in the operands, so the interpolation of these values is
+        z itself."""
+        return self.theta @ self._corner_monomials(self.theta.device).t()
+
+    @torch.no_grad()
+    def corner_z_hard(self):
+        """z at the corners with the fp32 expression of forward_hard
+        (``(walsh_monomials(u) * theta).sum(2)``, nodes.py:152-156), evaluated
+        on the CPU as the reference computes it, on the parameter's device."""
+        t = self.theta.detach().float().cpu()
+        P = 2 ** self.arity
+        cols = []
+        for p in range(P):
+            u = (2 * corner_bits(self.arity)[p] - 1).view(1, 1, -1).expand(1, t.shape[0], -1)
+            cols.append((walsh_monomials(u) * t[None]).sum(2)[0])
+        return torch.stack(cols, dim=1).to(self.theta.device)
+
     def plain_softmax(self):
         return not (self.training and self.gate_select == "gumbel")
 

@@ -372,22 +372,23 @@ def groupsum_hard(x, C):
     return out
 
 
-def orpool_launch(x):
+def orpool_launch(x, size=2):
     dtype = 1 if x.dtype == torch.uint8 else 0
     x = x.contiguous() if dtype == 1 else _as_f32(x)
     B, Cc, H, W = x.shape
-    out = torch.empty((B, Cc, H // 2, W // 2), device=x.device, dtype=x.dtype)
-    _lib.call("slg_orpool", _p(x), dtype, B, Cc, H, W, _p(out), _stream(x))
+    out = torch.empty((B, Cc, H // size, W // size), device=x.device, dtype=x.dtype)
+    _lib.call("slg_orpool", _p(x), dtype, B, Cc, H, W, int(size), _p(out), _stream(x))
     return out
 
 
-def orpool(x):
+def orpool(x, size=2):
+    """``size`` x ``size`` OR (max) pool with stride ``size`` and floor."""
     require_gpu(x)
     if x.dtype == torch.bool:
         x = x.to(torch.uint8)
     if x.is_floating_point() and _grad_path(x):
-        return torch.ops.silogic_hip.orpool(x)
-    return orpool_launch(x)
+        return torch.ops.silogic_hip.orpool(x, int(size))
+    return orpool_launch(x, size)
 
 
 # ---------------------------------------------------------------------------
@@ -613,13 +614,33 @@ def conv_soft_prep(conn, raw, node_kind, N, leaves, K, depth, arity):
     return w, npar
 
 
+def tree_shape(node_kind, depth, arity):
+    """``(leaves, nodes, params per node)`` of a conv node tree: binary
+    gate16 / walsh trees (4 coefficients a node) or arity-n LUT trees (2^n
+    values a node)."""
+    a = 2 if node_kind in (GATE16, WALSH) else arity
+    leaves = a ** depth
+    nodes = (leaves - 1) // (a - 1)
+    return leaves, nodes, 4 if node_kind in (GATE16, WALSH) else 2 ** a
+
+
+def conv_param_shapes(node_kind, depth, arity, N):
+    """Accepted node-parameter shapes: ``[N, nodes, P]``, and for a depth-1
+    LUT also ``[N, 2^arity]``."""
+    _, nodes, P = tree_shape(node_kind, depth, arity)
+    shapes = [(N, nodes, P)]
+    if node_kind not in (GATE16, WALSH) and depth == 1:
+        shapes.append((N, P))
+    return shapes
+
+
 def _conv_soft_launch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
     B, Cc, H, W = x.shape
     N = cm.shape[0]
-    leaves = 2 ** depth if node_kind == GATE16 else arity
-    nparam = (N, leaves - 1, 4) if node_kind == GATE16 else (N, 2 ** arity)
+    leaves, _, _ = tree_shape(node_kind, depth, arity)
     if (cm.shape != (N, leaves, K) or ch.shape != cm.shape or cw.shape != cm.shape
-            or w.shape != cm.shape or tuple(npar.shape) != nparam):
+            or w.shape != cm.shape
+            or tuple(npar.shape) not in conv_param_shapes(node_kind, depth, arity, N)):
         raise ValueError("conv_soft: tap / weight / node parameter shapes are inconsistent")
     kern = 2 * pad + 1
     Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
@@ -643,7 +664,12 @@ class _StraightThrough(torch.autograd.Function):
 
 
 def conv_soft_torch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool):
-    """Differentiable torch expression of the fused conv op (backward only)."""
+    """Differentiable torch expression of the fused conv op (backward only),
+    for the trees the LDS kernels take (gate16 trees, depth-1 LUTs)."""
+    if node_kind == WALSH or (node_kind != GATE16 and depth != 1):
+        raise NotImplementedError("conv_soft_torch: gate16 trees and depth-1 LUTs")
+    npar = npar.reshape(npar.shape[0], -1, 4) if node_kind == GATE16 else \
+        npar.reshape(npar.shape[0], -1)
     B, Cc, H, W = x.shape
     N, leaves = cm.shape[0], cm.shape[1]
     kern = 2 * pad + 1
@@ -733,6 +759,14 @@ def tree_conv_launch(x, coef, w, cm, ch, cw, depth, K, pad):
     return out
 
 
+def conv_fits_lds(chw, pad, pool, node_kind, depth, arity, K):
+    """True when the LDS-staged conv kernels (and the records forward) take
+    images of shape ``chw``; the others run on the generic kernels."""
+    C, H, W = chw
+    return bool(_lib.lib().slg_conv_soft_lds_fit(C, H, W, node_kind, depth, arity, K, pad,
+                                                 int(bool(pool))))
+
+
 def conv_soft_records(conn, cm, ch, cw, raw, node_kind, depth, arity, K, in_shape, pad, pool):
     """Per-channel records (taps resolved for in_shape = (C, H, W), pad and
     the pooling flag, leaf weights, node parameters) for conv_soft_rec;
@@ -773,6 +807,52 @@ def conv_soft_rec(x, rec, N, node_kind, depth, arity, K, pad, pool):
     out = torch.empty((B, N, Ho, Wo), device=x.device, dtype=torch.float32)
     _lib.call("slg_conv_soft_fwd_records", _p(x), B, Cc, H, W, N, node_kind, depth, arity, K,
               _p(rec), pad, int(bool(pool)), _p(out), _stream(x))
+    return out
+
+
+def conv_tree_hard_prep(cm, ch, cw, conn, levels, node_kind, depth, arity):
+    """Hard parameters of any conv node tree: ``(leaf [N, leaves] int32,
+    tables [N, nodes] int64)``; ``levels`` holds each tree level's parameters
+    as the module stores them (gate16 logits [N, m, 16], walsh theta
+    [N*m, 4], LUT logits [N*m, 2^arity])."""
+    require_gpu(cm, *levels)
+    cm, ch, cw = _c(cm, torch.int32), _c(ch, torch.int32), _c(cw, torch.int32)
+    N, leaves, K = cm.shape
+    want_leaves, nodes, _ = tree_shape(node_kind, depth, arity)
+    if leaves != want_leaves or len(levels) != depth or ch.shape != cm.shape or \
+            cw.shape != cm.shape or (conn is not None and tuple(conn.shape) != (N, leaves, K)):
+        raise ValueError("conv_tree_hard_prep: tap / level shapes do not match the tree")
+    a = 2 if node_kind in (GATE16, WALSH) else arity
+    for i, t in enumerate(levels):
+        m = a ** (depth - 1 - i)
+        want = {GATE16: (N, m, 16), WALSH: (N * m, 4)}.get(node_kind, (N * m, 2 ** a))
+        if tuple(t.shape) != want:
+            raise ValueError(f"conv_tree_hard_prep: level {i} parameters {tuple(t.shape)}, "
+                             f"expected {want}")
+    levels = [_c(t.detach(), torch.float32) for t in levels]
+    leaf = torch.empty((N, leaves), device=cm.device, dtype=torch.int32)
+    tables = torch.empty((N, nodes), device=cm.device, dtype=torch.int64)
+    conn = None if conn is None else _c(conn.detach(), torch.float32)
+    _lib.call("slg_conv_tree_hard_prep", _p(cm), _p(ch), _p(cw), _p(conn), N, K, node_kind,
+              depth, arity, _ptrs(levels), _p(leaf), _p(tables), _stream(cm))
+    return leaf, tables
+
+
+def conv_tree_hard(xp, shape_chw, leaf, tables, arity, depth, kernel, pad, pool):
+    """Packed node tree: ``xp`` [C,H,W,nw] -> [N,Ho,Wo,nw] (OR-pooled if ``pool``)."""
+    require_gpu(xp, leaf, tables)
+    Cc, H, W = shape_chw
+    nw = xp.shape[-1]
+    N = leaf.shape[0]
+    if xp.numel() != Cc * H * W * nw or leaf.shape != (N, arity ** depth) or \
+            tables.shape != (N, (arity ** depth - 1) // (arity - 1)):
+        raise ValueError("conv_tree_hard: packed input / leaf / table shapes are inconsistent")
+    Hf, Wf = H + 2 * pad - kernel + 1, W + 2 * pad - kernel + 1
+    Ho, Wo = (Hf // 2, Wf // 2) if pool else (Hf, Wf)
+    out = torch.empty((N, Ho, Wo, nw), device=xp.device, dtype=torch.int64)
+    if out.numel():
+        _lib.call("slg_conv_tree_hard_fwd", _p(_c(xp)), Cc, H, W, nw, N, arity, depth, _p(leaf),
+                  _p(tables), kernel, pad, int(bool(pool)), _p(out), _stream(xp))
     return out
 
 

@@ -16,7 +16,9 @@ Output (committed, numpy ``.npz`` with ``allow_pickle=False`` semantics):
 * ``construct_sha256.json`` — SHA-256 of every ``state_dict`` tensor of the
   FULL-size configs 1-5 (exact construction pin without storing megabytes).
 
-Run: ``python tests/golden/make_golden.py`` (takes about a minute).
+Run: ``python tests/golden/make_golden.py`` (takes about a minute);
+``--only=name,...`` writes just those tiny fixtures, ``--no-full`` skips the
+hashes.
 """
 import hashlib
 import json
@@ -36,7 +38,7 @@ if "silogic" not in sys.modules:
     pkg.__path__ = [REF]
     sys.modules["silogic"] = pkg
 
-from silogic.models import LogicNet, WARPNet, LogicConvNet, LogicTreeNet  # noqa: E402
+from silogic.models import LogicNet, WARPNet, WARPNetN, LogicConvNet, LogicTreeNet  # noqa: E402
 from silogic.heads import GroupSum  # noqa: E402
 
 from silogic_amd.synthetic import (bernoulli_inputs, cfg3_images,  # noqa: E402
@@ -173,6 +175,33 @@ TINY = {
                                 arity=6, tree_depth=1, connect="topk", k=4, n_chan=2,
                                 residual_init=False),
                       B=12, images="cfg5"),
+    # node trees beyond the configs (the reference's own test shapes,
+    # tests/test_conv.py:58-75, test_bitpacking.py:172-220): walsh trees,
+    # deeper multilinear / hybrid LUT trees, n-input walsh FC nodes
+    "conv_walsh": dict(kind="conv", ctor="LogicConvNet",
+                       args=dict(in_channels=3, in_hw=8, channels=[8, 16], head_widths=[40],
+                                 num_classes=10, node="walsh", tree_depth=2, connect="topk",
+                                 k=4, n_chan=2, node_tau=0.5, residual_init=False),
+                       B=12, images="cfg5_3"),
+    "conv_ml2_d3": dict(kind="conv", ctor="LogicConvNet",
+                        args=dict(in_channels=3, in_hw=8, channels=[8, 16], head_widths=[40],
+                                  num_classes=10, node="multilinear", arity=2, tree_depth=3,
+                                  connect="fixed", n_chan=2, residual_init=False),
+                        B=12, images="cfg5_3"),
+    "conv_ml4_d2": dict(kind="conv", ctor="LogicConvNet",
+                        args=dict(in_channels=6, in_hw=10, channels=[8, 16], head_widths=[40],
+                                  num_classes=10, node="multilinear", arity=4, tree_depth=2,
+                                  connect="topk", k=4, n_chan=2, residual_init=False),
+                        B=6, images="bits6"),
+    "conv_hybrid3_d2": dict(kind="conv", ctor="LogicConvNet",
+                            args=dict(in_channels=6, in_hw=10, channels=[8, 16],
+                                      head_widths=[40], num_classes=10, node="hybrid", arity=3,
+                                      tree_depth=2, connect="topk", k=4, n_chan=2,
+                                      residual_init=False),
+                            B=6, images="bits6"),
+    "warp_n4": dict(kind="fc", ctor="WARPNetN",
+                    args=dict(in_dim=64, width=120, depth=2, arity=4, num_classes=10, k=8),
+                    B=70, p=0.5),
 }
 
 # --- full-size configs (Appendix B choices) ------
@@ -192,12 +221,14 @@ FULL = {
                                   residual_init=False)),
 }
 
-CTORS = {"LogicNet": LogicNet, "WARPNet": WARPNet, "LogicConvNet": LogicConvNet,
-         "LogicTreeNet": LogicTreeNet}
+CTORS = {"LogicNet": LogicNet, "WARPNet": WARPNet, "WARPNetN": WARPNetN,
+         "LogicConvNet": LogicConvNet, "LogicTreeNet": LogicTreeNet}
 
 
-def make_tiny():
+def make_tiny(only=None):
     for name, spec in TINY.items():
+        if only and name not in only:
+            continue
         torch.manual_seed(0)
         model = CTORS[spec["ctor"]](seed=0, **spec["args"])
         g = torch.Generator().manual_seed(1)
@@ -205,6 +236,11 @@ def make_tiny():
             x = bernoulli_inputs(spec["B"], spec["args"]["in_dim"], spec["p"], g)
         elif spec["images"] == "cfg3":
             x = cfg3_images(spec["B"], spec["args"]["in_hw"], g)
+        elif spec["images"] == "cfg5_3":     # 3 of the 9 threshold planes
+            x = cfg5_images(spec["B"], spec["args"]["in_hw"], g)[:, :3].contiguous()
+        elif spec["images"] == "bits6":      # 6 random bit planes
+            hw = spec["args"]["in_hw"]
+            x = bernoulli_inputs(spec["B"], 6 * hw * hw, 0.5, g).view(spec["B"], 6, hw, hw)
         else:
             x = cfg5_images(spec["B"], spec["args"]["in_hw"], g)
         meta = dict(ctor=spec["ctor"], args=spec["args"], kind=spec["kind"],
@@ -231,6 +267,10 @@ def make_full_hashes():
 
 
 if __name__ == "__main__":
-    make_tiny()
-    if "--no-full" not in sys.argv:
+    only = None
+    for a in sys.argv[1:]:
+        if a.startswith("--only="):
+            only = set(a[len("--only="):].split(","))
+    make_tiny(only)
+    if "--no-full" not in sys.argv and only is None:
         make_full_hashes()

@@ -681,6 +681,15 @@ def test_fc_soft_backward_kernels(node, conn, k, IN, OUT, B):
     ("gate16", 2, 2, "topk", 4, 2, 6, 8, 600, True, True),      # several samples per range
     ("hybrid", 1, 6, "topk", 8, 9, 10, 16, 3, True, True),      # the CIFAR recipe's trees
     ("hybrid", 1, 4, "fixed", 1, 4, 8, 10, 4, False, False),
+    # trees on the generic kernels: walsh, deeper LUT trees, gate16 depth 5,
+    # and an image too large for LDS (48 x 32 x 32 floats)
+    ("walsh", 2, 2, "topk", 4, 5, 10, 12, 3, True, False),
+    ("walsh", 3, 2, "fixed", 1, 4, 9, 10, 3, False, False),
+    ("multilinear", 2, 4, "topk", 4, 6, 10, 8, 3, True, False),
+    ("multilinear", 3, 2, "fixed", 1, 4, 8, 8, 3, True, True),
+    ("hybrid", 2, 3, "topk", 4, 6, 10, 8, 3, True, False),
+    ("gate16", 5, 2, "topk", 4, 4, 8, 6, 2, True, False),
+    ("gate16", 2, 2, "topk", 4, 48, 32, 8, 2, True, False),
 ])
 def test_conv_soft_backward_kernel(node, depth, arity, connect, k, C, H, N, B, pool, binary):
     """The HIP conv backward (fused pooling or not) against fp32 autograd
@@ -688,10 +697,11 @@ def test_conv_soft_backward_kernel(node, depth, arity, connect, k, C, H, N, B, p
     connection and node-logit gradients."""
     layer = sl.ConvLogicTree(C, N, kernel=3, tree_depth=depth, connect=connect, k=k, seed=3,
                              node=node, arity=arity)
+    binary_node = node in ("gate16", "walsh")
     blk = dict(prefix="", cin=C, n=N, kernel=3, depth=depth, stride=1, padding=1,
                connect=connect, k=layer.k if connect != "fixed" else 1, node=node,
-               node_arity=2 if node == "gate16" else arity,
-               leaves=(2 if node == "gate16" else arity) ** depth, tau=1.0, hw=H)
+               node_arity=2 if binary_node else arity,
+               leaves=(2 if binary_node else arity) ** depth, tau=1.0, hw=H)
     params = {kk: v.clone().requires_grad_(v.is_floating_point())
               for kk, v in layer.state_dict().items()}
     gen = torch.Generator().manual_seed(11)

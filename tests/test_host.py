@@ -72,7 +72,8 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert rc == -1 and b"null" in L.slg_last_error()
     rc = L.slg_groupsum_soft(ctypes.c_void_p(16), 4, 25, 10, 1.0, 1, ctypes.c_void_p(16), None)
     assert rc == -2 and b"divisible" in L.slg_last_error()
-    rc = L.slg_conv_soft_fwd(ctypes.c_void_p(16), 1, 1, 4, 4, 1, 0, 5, 2, 1, ctypes.c_void_p(16),
+    # a gate16 tree of depth 6 (64 leaves) is beyond every conv kernel
+    rc = L.slg_conv_soft_fwd(ctypes.c_void_p(16), 1, 1, 4, 4, 1, 0, 6, 2, 1, ctypes.c_void_p(16),
                              None, ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                              1, 1, ctypes.c_void_p(16), None)
     assert rc == -3
@@ -123,11 +124,56 @@ def test_public_api_names_mirror_the_reference():
     for name in ["LogicLayer", "LogicNet", "WARPNet", "WARPLayer", "LogicConvNet",
                  "LogicTreeNet", "ConvLogicTree", "ConvLogicLayer", "OrPool", "GroupSum",
                  "BASIS_COEFFS", "TRUTH_TABLES", "build_connectome", "build_node",
-                 "build_decoder", "gate_probs", "binarize_ste"]:
+                 "build_decoder", "gate_probs", "binarize_ste", "WARPLayerN", "LUTkLayer",
+                 "LUTNodeLayer", "WARPNetN", "LUTkNet", "LUTNodeNet"]:
         assert hasattr(silogic_amd, name), name
-    for name in ["dense_logic", "warp_logic", "tree_conv", "tree_conv_topk", "HAS_DENSE",
-                 "HAS_WARP", "HAS_CONV", "HAS_CONV_TOPK"]:
+    for name in ["dense_logic", "warp_logic", "tree_conv", "tree_conv_topk", "tree_conv_af",
+                 "build_inverse_map", "multilinear_logic", "conv_hybrid", "HAS_DENSE",
+                 "HAS_WARP", "HAS_CONV", "HAS_CONV_TOPK", "HAS_MULTILINEAR", "HAS_CONV_HYBRID"]:
         assert hasattr(silogic_amd.kernels, name), name
+
+
+def test_presets_are_their_generic_constructors():
+    """The presets (layers.py:162-224, models.py:117-147) are the generic
+    constructors with fixed arguments: same parameters for the same seed."""
+    def sd(ctor, *a, **k):
+        torch.manual_seed(0)
+        return ctor(*a, **k).state_dict()
+
+    def same(a, b):
+        assert a.keys() == b.keys() and all(torch.equal(a[k], b[k]) for k in a)
+
+    same(sd(silogic_amd.LUTkNet, 30, 40, 2, k=3, cand_k=4, tau=4.0, seed=1),
+         sd(silogic_amd.LogicNet, 30, 40, 2, node="multilinear", arity=3, k=4, tau=4.0, seed=1))
+    same(sd(silogic_amd.LUTNodeNet, 30, 40, 2, arity=4, relaxation="hybrid", k=6, seed=2),
+         sd(silogic_amd.LogicNet, 30, 40, 2, node="hybrid", arity=4, k=6, tau=10.0, seed=2))
+    same(sd(silogic_amd.WARPNetN, 30, 40, 2, arity=5, k=8, seed=3),
+         sd(silogic_amd.LogicNet, 30, 40, 2, node="walsh", arity=5, k=8, tau=20.0, seed=3))
+    same(sd(silogic_amd.LUTkLayer, 30, 40, k=3, cand_k=5, seed=4),
+         sd(silogic_amd.LogicLayer, 30, 40, node="multilinear", arity=3, k=5, seed=4))
+    same(sd(silogic_amd.WARPLayerN, 30, 40, arity=4, seed=5),
+         sd(silogic_amd.LogicLayer, 30, 40, node="walsh", arity=4, k=8, seed=5))
+    lut = silogic_amd.LUTkLayer(30, 40, k=3, cand_k=5, learn_conn=False, seed=4)
+    assert lut.k == 3 and lut.lut.shape == (40, 8) and lut.is_lut
+    assert silogic_amd.WARPNetN(30, 40, 2, arity=5).head.tau == 20.0
+    assert silogic_amd.LUTkNet(30, 40, 2, k=3).num_luts() == 80
+    assert silogic_amd.WARPLayerN(30, 40, arity=4).is_walsh_n
+
+
+def test_inverse_map_matches_the_reference_layout():
+    """build_inverse_map (kernels/conv.py:247-265): channel buckets in
+    ascending (n, l) order, checked against a plain loop."""
+    g = torch.Generator().manual_seed(0)
+    cm = torch.randint(0, 5, (7, 4), generator=g)
+    ch = torch.randint(0, 3, (7, 4), generator=g)
+    cw = torch.randint(0, 3, (7, 4), generator=g)
+    off, en, el, edy, edx = silogic_amd.kernels.build_inverse_map(cm, ch, cw, 6)
+    rows = [(n, l, int(ch[n, l]), int(cw[n, l])) for c in range(6) for n in range(7)
+            for l in range(4) if int(cm[n, l]) == c]
+    assert [tuple(int(t[i]) for t in (en, el, edy, edx)) for i in range(len(en))] == rows
+    counts = [sum(1 for n in range(7) for l in range(4) if int(cm[n, l]) == c) for c in range(6)]
+    assert off.tolist() == [sum(counts[:c]) for c in range(7)]
+    assert off.dtype == en.dtype == torch.int32
 
 
 def test_bitpacking_api_names_and_host_tables():
