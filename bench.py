@@ -15,10 +15,13 @@ kernel (HBM: it must read the fp32 input), with the bit-op view in
 ``cpu_baseline`` times the oracle (the reference's PyTorch CPU path restated)
 on a bounded sample on this host.
 
-``--config N`` measures BASELINE config N (1-5) the same way: its forward_hard
-and soft forward at the config's batch sizes, the dominant soft kernel (the
-widest FC layer, or the first conv block with its OrPool) and, for FC
-networks, the fused hard-network kernel.
+The default run measures all five BASELINE configs the same way and adds
+them under ``configs`` (the headline keys stay config 2's): each one's
+forward_hard and soft forward at the config's batch sizes, its dominant soft
+kernel (the widest FC layer, HBM-bound; or the first conv block with its
+OrPool, FP32-bound against 157.3 TFLOP/s), for FC networks the fused
+hard-network kernel, and the CPU baseline. ``--config N`` measures config N
+alone.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N] [--no-cpu]
 """
@@ -188,10 +191,25 @@ WORKLOADS = {
 }
 
 
+FP32_PEAK_TFLOPS = 157.3                   # MI355X vector fp32 (spec, packed)
+
+
+def conv_flops_per_position(conv):
+    """FP32 operations of one pre-pool output position of a conv tree: the
+    leaf sums (K FMAs a leaf) and the nodes (gate16: c0 + c1 a + c2 b + c3 ab
+    = 7; LUT: the 2^n - 1 FMAs of a lerp tree), FMAs counted as 2."""
+    K = conv.k if conv.connect != "fixed" else 1
+    leaf = conv.leaves * K * 2
+    if conv.node_name in ("gate16", "walsh"):
+        return leaf + 7 * (conv.leaves - 1)
+    return leaf + 2 * ((2 ** conv.node_arity) - 1) * conv.gates_per_output
+
+
 def dominant_soft_kernel(cfg, model, B_soft, x_soft, dev):
-    """(name, launch function, algorithmic bytes per launch) of the soft
+    """(name, launch function, roofline dict builder inputs) of the soft
     kernel that dominates config ``cfg``'s forward: the widest FC layer on
-    records, or the first (largest) conv block with its OrPool."""
+    records (HBM-bound: bytes), or the first (largest) conv block with its
+    OrPool (FP32-bound: flops, with its bytes beside)."""
     from silogic_amd import ops
     if hasattr(model, "layers"):
         L = model.layers[1] if len(model.layers) > 1 else model.layers[0]
@@ -199,16 +217,18 @@ def dominant_soft_kernel(cfg, model, B_soft, x_soft, dev):
         rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
         K, OUT = L.n_candidates, L.out_dim
         fn = lambda: ops.fc_soft_rec(x_mid, rec, L.in_dim, OUT, K, L.node.kind, L._inv_tau())  # noqa: E731
-        nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * (K + 1)
+        # input rows read once, output rows written once, one record per output
+        nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * ops.record_quads(K)
         name = f"fc_soft_kernel ({L._node_name}, K={K}, IN={L.in_dim}, OUT={OUT}, B={B_soft})"
-        return name, fn, nbytes
+        return name, fn, nbytes, None
     conv = model._convs()[0]
     B, C, H, W = x_soft.shape
     fn = lambda: conv.forward_pooled(x_soft)  # noqa: E731
     nbytes = B * C * H * W * 4 + B * conv.n * (H // 2) * (W // 2) * 4
+    flops = B * conv.n * H * W * conv_flops_per_position(conv)
     name = (f"conv_soft_kernel (block 0: {C}->{conv.n} channels, {H}x{W}, "
             f"{conv.node_name}, pooled, B={B})")
-    return name, fn, nbytes
+    return name, fn, nbytes, flops
 
 
 def hard_units(cfg, model):
@@ -219,15 +239,19 @@ def hard_units(cfg, model):
     return model.gate_count(CONFIGS[cfg][1]["in_hw"])
 
 
-def measure(cfg, args):
+def measure_config(cfg, steps, warmup, with_cpu):
+    """Time config ``cfg``: ``steps`` steps of forward_hard (hard batch) +
+    soft forward (soft batch) after ``warmup`` untimed ones, then the
+    dominant kernels alone with HIP events, then (optionally) the CPU
+    baseline. Returns the config's result dict."""
     import silogic_amd as sl
     from silogic_amd import ops
     from silogic_amd.synthetic import build_config, config_inputs, BATCHES
 
     dev = torch.device("cuda:0")
-    log(f"building config {cfg} (seeded construction) ...")
+    log(f"config {cfg}: building (seeded construction) ...")
     model = build_config(cfg, sl).eval()
-    sd_cpu = {k: v.clone() for k, v in model.state_dict().items()}
+    sd_cpu = {k: v.clone() for k, v in model.state_dict().items()} if with_cpu else None
     model = model.to(dev)
     B_soft, B_hard, _, _ = BATCHES[cfg]
     x_hard_cpu = config_inputs(cfg, B_hard)
@@ -241,18 +265,17 @@ def measure(cfg, args):
             model.forward_hard(x_hard)
             model(x_soft)
 
-    log(f"warmup {args.warmup} ...")
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
 
-    # ---- timed region: exactly K steps between synchronisations ----
+    # ---- timed region: exactly `steps` steps between synchronisations ----
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         ev[i][0].record(stream)
         with torch.no_grad():
             model.forward_hard(x_hard)
@@ -263,7 +286,8 @@ def measure(cfg, args):
     wall = time.perf_counter() - t0
     t_hard = statistics.median(a.elapsed_time(b) for a, b, _ in ev) / 1e3
     t_soft = statistics.median(b.elapsed_time(c) for _, b, c in ev) / 1e3
-    log(f"step {wall / args.steps * 1e3:.3f} ms; hard {t_hard * 1e6:.1f} us; soft {t_soft * 1e6:.1f} us")
+    log(f"config {cfg}: step {wall / steps * 1e3:.3f} ms; hard {t_hard * 1e6:.1f} us; "
+        f"soft {t_soft * 1e6:.1f} us")
 
     # ---- dominant kernels alone, HIP events on the launch stream ----
     reps = 20
@@ -282,56 +306,90 @@ def measure(cfg, args):
                 hard_bytes = B_hard * in_dim * 4 + sum(w * 4 for w in widths) + B_hard * C * 4
                 hard = ("fc_hard_net_rows_kernel (packing + %d layers + GroupSum)" % len(widths),
                         k_hard, hard_bytes)
-        name, fn_soft, soft_bytes = dominant_soft_kernel(cfg, model, B_soft, x_soft, dev)
+        name, fn_soft, soft_bytes, soft_flops = dominant_soft_kernel(cfg, model, B_soft, x_soft,
+                                                                     dev)
         fn_soft()
         k_soft = _events_ms(fn_soft, reps) / 1e3
     soft_gbs = soft_bytes / k_soft / 1e9
     traffic = load_traffic() if cfg == 2 else {}
     bitops = B_hard * gates / t_hard
 
-    result = {
+    res = {
+        "workload": WORKLOADS[cfg], "hard_batch": B_hard, "soft_batch": B_soft,
+        "gates_per_sample": gates,
+        "hard_Ggate_evals_per_s": round(B_hard * gates / t_hard / 1e9, 3),
+        "soft_samples_per_s": round(B_soft / t_soft, 1),
+        "t_hard_us": round(t_hard * 1e6, 2), "t_soft_us": round(t_soft * 1e6, 2),
+        "ms_per_step": round(wall / steps * 1e3, 4),
+    }
+    if soft_flops is None:
+        soft_roof = {"kernel": name, "bound": "hbm", "achieved": round(soft_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("fc_soft_kernel"), "algorithmic_bytes": soft_bytes,
+                     "avg_kernel_us": round(k_soft * 1e6, 2)}
+    else:
+        tflops = soft_flops / k_soft / 1e12
+        soft_roof = {"kernel": name, "bound": "fp32", "achieved": round(tflops, 2),
+                     "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                     "algorithmic_flops": soft_flops, "algorithmic_bytes": soft_bytes,
+                     "hbm_frac": round(soft_gbs / HBM_PEAK_GBS, 4),
+                     "avg_kernel_us": round(k_soft * 1e6, 2)}
+    res["roofline_soft"] = soft_roof
+    if hard is not None:
+        hname, k_hard, hard_bytes = hard
+        hard_gbs = hard_bytes / k_hard / 1e9
+        res["roofline_hard"] = {"kernel": hname, "bound": "hbm", "achieved": round(hard_gbs, 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
+                                "traffic": traffic.get("fc_hard_net_rows_kernel"),
+                                "algorithmic_bytes": hard_bytes,
+                                "avg_kernel_us": round(k_hard * 1e6, 2)}
+    res["roofline_valu"] = {"kernel": "forward_hard (whole packed circuit)",
+                            "achieved_bitops_per_s": bitops, "peak": VALU_BITOPS_PEAK,
+                            "frac": round(bitops / VALU_BITOPS_PEAK, 6)}
+    if with_cpu:
+        log(f"config {cfg}: cpu baseline (oracle on host cores) ...")
+        res["cpu_baseline"] = cpu_baseline(cfg, sd_cpu, x_hard_cpu, x_hard_cpu[:B_soft], gates)
+    del model, x_hard, x_soft
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_line(head_cfg, res, steps, warmup, configs=None):
+    """The driver's JSON line: BASELINE.json's metric on config ``head_cfg``
+    (value = hard Ggate-evals/s, soft samples/s beside it), plus per-config
+    records when measured."""
+    roof = res.get("roofline_hard", res["roofline_soft"])
+    line = {
         "metric": "hard-circuit Ggate-evals/s + soft fwd samples/s; % HBM/VALU roofline, 1 GPU",
-        "value": round(B_hard * gates / t_hard / 1e9, 3),
+        "value": res["hard_Ggate_evals_per_s"],
         "unit": "Ggate-evals/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u64",
         "data": "synthetic",
-        "config": {"workload": WORKLOADS[cfg], "hard_batch": B_hard, "soft_batch": B_soft,
-                   "gates_per_sample": gates},
-        "soft_samples_per_s": round(B_soft / t_soft, 1),
+        "config": {"workload": res["workload"], "hard_batch": res["hard_batch"],
+                   "soft_batch": res["soft_batch"], "gates_per_sample": res["gates_per_sample"]},
+        "soft_samples_per_s": res["soft_samples_per_s"],
         "soft_dtype": "f32",
-        "t_hard_us": round(t_hard * 1e6, 2),
-        "t_soft_us": round(t_soft * 1e6, 2),
+        "t_hard_us": res["t_hard_us"],
+        "t_soft_us": res["t_soft_us"],
+        "roofline": roof,
+        "roofline_soft": res["roofline_soft"],
+        "roofline_valu": res["roofline_valu"],
     }
-    soft_roof = {"kernel": name, "bound": "hbm", "achieved": round(soft_gbs, 1),
-                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
-                 "traffic": traffic.get("fc_soft_kernel"), "algorithmic_bytes": soft_bytes,
-                 "avg_kernel_us": round(k_soft * 1e6, 2)}
-    if hard is not None:
-        hname, k_hard, hard_bytes = hard
-        hard_gbs = hard_bytes / k_hard / 1e9
-        result["roofline"] = {"kernel": hname, "bound": "hbm", "achieved": round(hard_gbs, 1),
-                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
-                              "traffic": traffic.get("fc_hard_net_rows_kernel"),
-                              "algorithmic_bytes": hard_bytes,
-                              "avg_kernel_us": round(k_hard * 1e6, 2)}
-        result["roofline_soft"] = soft_roof
-    else:
-        result["roofline"] = soft_roof
-    result["roofline_valu"] = {"kernel": "forward_hard (whole packed circuit)",
-                               "achieved_bitops_per_s": bitops, "peak": VALU_BITOPS_PEAK,
-                               "frac": round(bitops / VALU_BITOPS_PEAK, 4)}
-    if not args.no_cpu:
-        log("cpu baseline (oracle on host cores) ...")
-        result["cpu_baseline"] = cpu_baseline(cfg, sd_cpu, x_hard_cpu, x_hard_cpu[:B_soft], gates)
-    print(json.dumps(result), flush=True)
+    if "cpu_baseline" in res:
+        line["cpu_baseline"] = res["cpu_baseline"]
+    if configs:
+        line["configs"] = configs
+    return line
 
 
 def main():
@@ -339,9 +397,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
-                    help="BASELINE config to measure (default 2, the headline workload)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--config", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
+                    help="measure only BASELINE config N (default: the headline config 2 "
+                         "plus a record of every config)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the copy calibration and the dominant kernels (for --pmc)")
     ap.add_argument("--train-step", action="store_true",
@@ -351,7 +410,7 @@ def main():
         kernels_only()
         return
     if args.train_step:
-        train_step(args.config, args.steps, args.warmup)
+        train_step(args.config or 2, args.steps, args.warmup)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -359,7 +418,15 @@ def main():
               "(the workload shards by batch; see DESIGN.md). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    measure(args.config, args)
+    if args.config:
+        res = measure_config(args.config, args.steps, args.warmup, not args.no_cpu)
+        print(json.dumps(bench_line(args.config, res, args.steps, args.warmup)), flush=True)
+        return
+    # default: every config, the headline line on config 2
+    configs = {}
+    for cfg in (1, 2, 3, 4, 5):
+        configs[str(cfg)] = measure_config(cfg, args.steps, args.warmup, not args.no_cpu)
+    print(json.dumps(bench_line(2, configs["2"], args.steps, args.warmup, configs)), flush=True)
 
 
 if __name__ == "__main__":
