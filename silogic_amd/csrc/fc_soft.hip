@@ -463,69 +463,104 @@ __global__ void __launch_bounds__(256) fc_soft_records_kernel(RecNet net) {
 // mod 32; b32: 64 lanes, mod 64). For each group of N consecutive outputs
 // (N = lanes served per cycle) and each slot, this picks the step at which
 // each output reads each of its K candidates so that few reads of one step
-// share a bank: a greedy pass per step (least-used bank first, ties to the
-// bank with the most reads left), then pairwise step swaps within a lane
-// that even out the per-step bank counts. The sum over k is the same; only
-// the fp32 summation order changes.
+// share a bank:
+//  * a greedy pass per step, outputs in order (least-used bank first, ties
+//    to the bank with the most reads left);
+//  * then rounds of pairwise step swaps within an output that lower the sum
+//    of squared per-step bank counts of the two steps: every output finds
+//    its best swap in parallel against the round's counts, then the outputs
+//    apply theirs in order, each re-checked against the counts as they are.
+// One wave serves 64 / N groups of one slot (lane = group * N + output), the
+// counts live in LDS and only the serial steps run one output at a time. The
+// sum over k is the same; only the fp32 summation order changes.
+constexpr int kSchedMaxK = 16;
+
 template <int N>
 __global__ void __launch_bounds__(64) fc_soft_schedule_kernel(const int* __restrict__ cand, int OUT,
                                                               int K, uint8_t* __restrict__ order) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int G = 64 / N;
+  __shared__ int cnt[G][kSchedMaxK][N];   // reads of bank b at step t
+  __shared__ int dem[G][N];               // reads of bank b not yet placed
+  __shared__ uint8_t ord[64][kSchedMaxK];  // per lane: candidate read at step t
+  __shared__ uint8_t ob[64][kSchedMaxK];   // per lane: its bank
+  const int lane = threadIdx.x, g = lane / N, l = lane - g * N;
   const int ngroups = (OUT + N - 1) / N;
-  if (t >= ngroups * 2) return;
-  const int grp = t >> 1, s = t & 1;
-  const int o0 = grp * N, n = min(N, OUT - o0);
-  uint8_t bank[N][16];
-  uint8_t ord[N][16];
-  uint16_t used[N];
-  int demand[N];
-  uint8_t cnt[16][N];
-  for (int b = 0; b < N; ++b) demand[b] = 0;
-  for (int l = 0; l < n; ++l) {
-    used[l] = 0;
-    for (int k = 0; k < K; ++k) {
-      const int b = cand[((int64_t)(o0 + l) * 2 + s) * K + k] & (N - 1);
-      bank[l][k] = (uint8_t)b;
-      ++demand[b];
-    }
-  }
+  const int s = blockIdx.x & 1;
+  const int grp = (blockIdx.x >> 1) * G + g;
+  const int o = grp * N + l;
+  const bool active = grp < ngroups && o < OUT;
+  for (int i = lane; i < G * kSchedMaxK * N; i += 64) (&cnt[0][0][0])[i] = 0;
+  for (int i = lane; i < G * N; i += 64) (&dem[0][0])[i] = 0;
+  __syncthreads();
+  int bank[kSchedMaxK];
+#pragma unroll
+  for (int k = 0; k < kSchedMaxK; ++k)
+    bank[k] = (active && k < K) ? (cand[((int64_t)o * 2 + s) * K + k] & (N - 1)) : 0;
+  if (active)
+#pragma unroll
+    for (int k = 0; k < kSchedMaxK; ++k)
+      if (k < K) atomicAdd(&dem[g][bank[k]], 1);
+  __syncthreads();
+
+  // greedy placement, step by step, the outputs of a group in order
+  uint32_t used = 0;
   for (int st = 0; st < K; ++st) {
-    for (int b = 0; b < N; ++b) cnt[st][b] = 0;
-    for (int l = 0; l < n; ++l) {
-      int best = -1, bc = 0, bd = 0;
-      for (int k = 0; k < K; ++k) {
-        if (used[l] & (1u << k)) continue;
-        const int b = bank[l][k], c = cnt[st][b], d = demand[b];
-        if (best < 0 || c < bc || (c == bc && d > bd)) { best = k; bc = c; bd = d; }
+    for (int j = 0; j < N; ++j) {
+      if (active && l == j) {
+        int best = -1, bb = 0, bc = 0, bd = 0;
+#pragma unroll
+        for (int k = 0; k < kSchedMaxK; ++k) {
+          if (k >= K || (used & (1u << k))) continue;
+          const int b = bank[k], c = cnt[g][st][b], d = dem[g][b];
+          if (best < 0 || c < bc || (c == bc && d > bd)) { best = k; bb = b; bc = c; bd = d; }
+        }
+        used |= 1u << best;
+        ord[lane][st] = (uint8_t)best;
+        ob[lane][st] = (uint8_t)bb;
+        cnt[g][st][bb] += 1;
+        dem[g][bb] -= 1;
       }
-      used[l] |= (uint16_t)(1u << best);
-      ord[l][st] = (uint8_t)best;
-      ++cnt[st][bank[l][best]];
-      --demand[bank[l][best]];
+      __syncthreads();
     }
   }
-  // Pairwise step swaps within a lane while they lower the sum of squared
-  // per-step bank counts of the two steps (O(1) per test; spreading the
-  // counts evenly lowers their maxima).
-  for (int pass = 0; pass < 8; ++pass) {
-    bool improved = false;
-    for (int l = 0; l < n; ++l)
-      for (int t1 = 0; t1 < K; ++t1)
+
+  // swap rounds
+  for (int round = 0; round < 10; ++round) {
+    int p1 = -1, p2 = -1, pscore = 0;
+    if (active) {
+      for (int t1 = 0; t1 < K; ++t1) {
+        const int b1 = ob[lane][t1];
         for (int t2 = t1 + 1; t2 < K; ++t2) {
-          const int b1 = bank[l][ord[l][t1]], b2 = bank[l][ord[l][t2]];
+          const int b2 = ob[lane][t2];
           if (b1 == b2) continue;
-          if ((int)cnt[t1][b2] - (int)cnt[t1][b1] + (int)cnt[t2][b1] - (int)cnt[t2][b2] + 2 < 0) {
-            --cnt[t1][b1]; ++cnt[t1][b2]; --cnt[t2][b2]; ++cnt[t2][b1];
-            const uint8_t tmp = ord[l][t1];
-            ord[l][t1] = ord[l][t2];
-            ord[l][t2] = tmp;
-            improved = true;
-          }
+          const int sc = cnt[g][t1][b2] - cnt[g][t1][b1] + cnt[g][t2][b1] - cnt[g][t2][b2] + 2;
+          if (sc < pscore) { pscore = sc; p1 = t1; p2 = t2; }
         }
-    if (!improved) break;
+      }
+    }
+    bool applied = false;
+    for (int j = 0; j < N; ++j) {
+      if (active && l == j && p1 >= 0) {
+        const int b1 = ob[lane][p1], b2 = ob[lane][p2];
+        if (cnt[g][p1][b2] - cnt[g][p1][b1] + cnt[g][p2][b1] - cnt[g][p2][b2] + 2 < 0) {
+          cnt[g][p1][b1] -= 1;
+          cnt[g][p1][b2] += 1;
+          cnt[g][p2][b2] -= 1;
+          cnt[g][p2][b1] += 1;
+          const uint8_t k1 = ord[lane][p1], k2 = ord[lane][p2];
+          ord[lane][p1] = k2;
+          ord[lane][p2] = k1;
+          ob[lane][p1] = (uint8_t)b2;
+          ob[lane][p2] = (uint8_t)b1;
+          applied = true;
+        }
+      }
+      __syncthreads();
+    }
+    if (!__syncthreads_or(applied)) break;
   }
-  for (int l = 0; l < n; ++l)
-    for (int st = 0; st < K; ++st) order[((int64_t)(o0 + l) * 2 + s) * K + st] = ord[l][st];
+  if (active)
+    for (int st = 0; st < K; ++st) order[((int64_t)o * 2 + s) * K + st] = ord[lane][st];
 }
 
 // ---------------------------------------------------------------------------
@@ -649,8 +684,8 @@ int slg_fc_soft_schedule(const int32_t* cand, int64_t OUT, int32_t K, int64_t IN
               "fc_soft_schedule: bad sizes");
   const int S = pick_tile(IN, 0);
   const int lanes = S >= 4 ? 16 : (S == 2 ? 32 : 64);
-  const int64_t threads = cdiv(OUT, lanes) * 2;
-  const unsigned grid = (unsigned)cdiv(threads, 64);
+  // one 64-lane workgroup per (64 / lanes groups, slot)
+  const unsigned grid = (unsigned)(cdiv(cdiv(OUT, lanes), 64 / lanes) * 2);
   hipStream_t st = as_stream(stream);
   if (lanes == 16)
     hipLaunchKernelGGL(fc_soft_schedule_kernel<16>, dim3(grid), dim3(64), 0, st, cand, (int)OUT, K, order);
