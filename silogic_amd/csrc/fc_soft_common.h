@@ -50,13 +50,12 @@ __device__ inline float4 ld_stream4(const float* p) {
 // of 4 inputs from each row (NBAT batches in flight per thread), then scatter
 // them to 4 input slots; rows whose length is not a multiple of 4 go one
 // input at a time. STREAM: non-temporal loads (rows read once).
-template <int V, bool STREAM>
+template <int V, bool STREAM, int NBAT = (V == 4 ? 2 : 4)>
 __device__ inline void stage_rows(typename vecf<V>::t* __restrict__ dst,
                                   const float* __restrict__ x, int B, int IN, int b0) {
   using vt = typename vecf<V>::t;
   if ((IN & 3) == 0) {
     const int n4 = IN >> 2;
-    constexpr int NBAT = V == 4 ? 2 : 4;
     for (int q0 = threadIdx.x; q0 < n4; q0 += NBAT * blockDim.x) {
       float4 t[NBAT][V];
 #pragma unroll
