@@ -34,7 +34,7 @@ from .models import LogicNet, WARPNet, WARPNetN, LUTkNet, LUTNodeNet, LogicConvN
 from .encoders import LearnedThermometerEncoder
 from .data import (binarize, binarize_spatial, binarize_packed, edge_bits, MNIST_THRESH,
                    SEVEN_THRESH, FOUR_THRESH, FIVE_THRESH, CIFAR3_THRESH, EDGE_THRESH)
-from . import kernels, library, ops
+from . import derived, kernels, library, ops
 
 __all__ = [
     "BASIS_COEFFS", "TRUTH_TABLES", "GATE_A", "ste_threshold", "sign_ste", "ternary_ste",

@@ -19,6 +19,14 @@
 //    (py + (dy+h)/2, px + (dx+w)/2), so lanes that walk (py, px < Wo+pad)
 //    read consecutive floats of one sub-plane: four reads per tap at four
 //    offsets held in registers.
+//  * quad (pooled, phase-eligible taps, images small enough): four copies
+//    of the padded image, shifted by (sy, sx) in {0,1}^2, stored as 2x2
+//    blocks of four consecutive floats: block (by, bx) of copy (sy, sx)
+//    holds padded pixels (2by+sy+dy, 2bx+sx+dx) as component 2dy+dx. The
+//    2x2 window of pooled output (py, px) under tap (h, w) is then block
+//    (py + h/2, px + w/2) of copy (h&1, w&1): one ds_read_b128 and one
+//    address add per tap instead of four of each. Lanes walk exactly the
+//    (py, px < Wo) outputs, so no lane idles on padding columns.
 // Where lanes read consecutive floats, the sample stride is padded to equal
 // the lanes per sample modulo 64, so that a chunk that spans two samples
 // still hits 64 distinct LDS banks.
@@ -32,6 +40,8 @@
 #include "conv_tree.h"
 
 namespace slg {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline float sigmoidc(float z) { return 1.0f / (1.0f + expf(-z)); }
 
@@ -67,6 +77,7 @@ struct ConvGeom {
   int plane;  // channel stride
   int SST;    // sample stride
   int LPS;    // lanes per sample
+  int BH, BW; // quad: blocks per copy (rows, columns); 0 otherwise
 };
 
 // One output channel's parameters in registers: LDS tap offsets, leaf
@@ -82,6 +93,10 @@ struct ConvParams {
 // phase-split) or the tap itself (NW = 1, row-major).
 __host__ __device__ inline int conv_tap_offset(const ConvGeom& g, int NW, int c, int h, int w,
                                                int q) {
+  if (g.BH > 0)  // quad: the tap's block in float4 units, in slot q = 0
+    return q == 0 ? (c * g.plane) / 4 + ((h & 1) * 2 + (w & 1)) * g.BH * g.BW +
+                        (h >> 1) * g.BW + (w >> 1)
+                  : 0;
   if (NW == 1) return c * g.plane + h * g.RS + w;
   const int Y = (q >> 1) + h, X = (q & 1) + w;
   return c * g.plane + (Y & 1) * 2 * g.PP + (X & 1) * g.PP + (Y >> 1) * g.RS + (X >> 1);
@@ -156,15 +171,21 @@ __device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM, NW>& P, co
   for (int i = 0; i < ConvNode<NODE, NLEAF>::NPR; ++i) P.par[i] = v[LK * (NW + 1) + i];
 }
 
-template <int NODE, int NLEAF, bool POOL, int KM, bool REC>
-__global__ void __launch_bounds__((ConvCfg<NODE, NLEAF, KM, POOL>::THREADS))
+// Quad-layout workgroups: 16 waves (the layout takes most of the LDS, so one
+// workgroup per CU; its per-tap state is one offset, which leaves room in
+// 128 VGPRs).
+constexpr int kQuadThreads = 1024;
+
+template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD>
+__global__ void __launch_bounds__((QUAD ? kQuadThreads : ConvCfg<NODE, NLEAF, KM, POOL>::THREADS))
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
                  int pad, ConvGeom g, const float* __restrict__ np, const float* __restrict__ wts,
                  const int* __restrict__ cm, const int* __restrict__ ch, const int* __restrict__ cw,
                  const float* __restrict__ rec, int S, float* __restrict__ out, int Ho, int Wo) {
   using Cfg = ConvCfg<NODE, NLEAF, KM, POOL>;
-  constexpr bool PHASE = Cfg::PHASE;
+  constexpr bool PHASE = Cfg::PHASE && !QUAD;
   constexpr int NW = Cfg::NW;
+  static_assert(!QUAD || Cfg::PHASE, "the quad layout keeps the phase records");
   extern __shared__ float lds[];
   const int b0 = blockIdx.x * S;
   const int ns = min(S, B - b0);
@@ -201,7 +222,23 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       for (int u = 0; u < kStage; ++u) {
         int at;
         bool keep = ps < ns;
-        if constexpr (PHASE) {
+        if constexpr (QUAD) {
+          // one float to each copy whose blocks hold the pixel
+          const int Y = py + pad, X = px + pad;
+          const int sb = __umul24(ps, g.SST) + __umul24(pc, g.plane);
+#pragma unroll
+          for (int sy = 0; sy < 2; ++sy)
+#pragma unroll
+            for (int sx = 0; sx < 2; ++sx) {
+              const int by = (Y - sy) >> 1, bx = (X - sx) >> 1;
+              const bool in = keep && Y >= sy && X >= sx && by < g.BH && bx < g.BW;
+              const int a = sb + 4 * (__umul24(sy * 2 + sx, g.BH * g.BW) + __umul24(by, g.BW) + bx) +
+                            ((Y - sy) & 1) * 2 + ((X - sx) & 1);
+              lds[in ? a : dump] = v[u];
+            }
+          at = 0;
+          keep = false;  // written above; the common store below goes to the dump slot
+        } else if constexpr (PHASE) {
           const int Y = py + pad, X = px + pad;
           keep = keep && (Y >> 1) < g.PR && (X >> 1) < g.RS;  // rows/columns no window reads
           at = ((Y & 1) ? 2 * g.PP : 0) + ((X & 1) ? g.PP : 0) + __umul24(Y >> 1, g.RS) + (X >> 1);
@@ -209,7 +246,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
           at = __umul24(py + pad, g.RS) + pad + px;
         }
         // elements that are not kept go to this lane's dump slot
-        lds[keep ? __umul24(ps, g.SST) + __umul24(pc, g.plane) + at : dump] = v[u];
+        if constexpr (!QUAD) lds[keep ? __umul24(ps, g.SST) + __umul24(pc, g.plane) + at : dump] = v[u];
         px += tx;
         const int cy = px >= W;
         px -= cy ? W : 0;
@@ -228,7 +265,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   const int P = Ho * Wo;
   const int nchunks = (ns * g.LPS + 63) / 64;
   const float inv_lps = 1.0f / (float)g.LPS;
-  const float inv_col = 1.0f / (float)(PHASE || !POOL ? g.RS : Wo);
+  const float inv_col = 1.0f / (float)((PHASE || !POOL) ? g.RS : Wo);
   auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int n) {
     int nv;  // the channel in a vector register: vector loads, VGPR parameters
     asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
@@ -252,7 +289,8 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       const int col = rem - (int)__umul24(row, LINEAR ? g.RS : Wo);
       active = active && col < Wo;
       const int p = (int)__umul24(row, Wo) + col;
-      const int bofs = LINEAR ? rem : 2 * (int)__umul24(row, g.RS) + 2 * col;
+      const int bofs = QUAD ? 4 * ((int)__umul24(row, g.BW) + col)
+                            : (LINEAR ? rem : 2 * (int)__umul24(row, g.RS) + 2 * col);
       const float* base = lds + (active ? __umul24(s, g.SST) + bofs : 0);
 
       // Tap k of every leaf per step: the guard k < K is uniform, and one
@@ -269,7 +307,11 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
           float t[NLEAF][NQ];
 #pragma unroll
           for (int l = 0; l < NLEAF; ++l) {
-            if constexpr (PHASE) {
+            if constexpr (QUAD) {
+              const f32x4 w4 = reinterpret_cast<const f32x4*>(base)[Pc.off[l][k][0]];
+#pragma unroll
+              for (int qq = 0; qq < 4; ++qq) t[l][qq] = w4[qq];
+            } else if constexpr (PHASE) {
 #pragma unroll
               for (int qq = 0; qq < 4; ++qq) t[l][qq] = base[Pc.off[l][k][qq]];
             } else {
@@ -592,6 +634,29 @@ struct ConvSoftArgs {
   const float* rec;  // records (REC kernels) or null
 };
 
+// Quad geometry (pooled; see the layouts above): BH x BW blocks per copy
+// cover every window of Ho x Wo pooled outputs under kernel x kernel taps.
+static ConvGeom conv_geom_quad(int64_t C, int64_t Ho, int64_t Wo, int kernel) {
+  ConvGeom g{};
+  g.BH = (int)(Ho + (kernel - 1) / 2);
+  g.BW = (int)(Wo + (kernel - 1) / 2);
+  g.plane = 16 * g.BH * g.BW;  // floats: four copies of BH x BW blocks of four
+  g.LPS = (int)(Ho * Wo);
+  g.SST = (int)(C * g.plane);
+  return g;
+}
+
+// The quad layout is used for pooled blocks with phase-eligible taps whose
+// four image copies fit the LDS of one workgroup.
+static bool conv_use_quad(bool pool, int nleaf, int km, int64_t C, int64_t Ho, int64_t Wo,
+                          int kernel) {
+  if (!conv_phase_layout(pool, nleaf, km) || Ho <= 0 || Wo <= 0) return false;
+  if (C * 16 * (Ho + kernel) * (Wo + kernel) >= (1LL << 29)) return false;
+  const ConvGeom g = conv_geom_quad(C, Ho, Wo, kernel);
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  return (int64_t)g.SST * 4 + kConvExtra * 4 <= cap;
+}
+
 // LDS geometry for images (C, H, W) with 'same' padding pad, pooled to
 // (Ho, Wo) or not (Ho = H, Wo = W).
 static ConvGeom conv_geom(int64_t C, int64_t H, int64_t W, int pad, bool pool, bool phase,
@@ -614,10 +679,11 @@ static ConvGeom conv_geom(int64_t C, int64_t H, int64_t W, int pad, bool pool, b
   return g;
 }
 
-template <int NODE, int NLEAF, bool POOL, int KM, bool REC>
+template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD>
 static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   using Cfg = ConvCfg<NODE, NLEAF, KM, POOL>;
-  const ConvGeom g = conv_geom(a.C, a.H, a.W, a.pad, POOL, Cfg::PHASE, a.Ho, a.Wo);
+  const ConvGeom g = QUAD ? conv_geom_quad(a.C, a.Ho, a.Wo, a.kernel)
+                          : conv_geom(a.C, a.H, a.W, a.pad, POOL, Cfg::PHASE, a.Ho, a.Wo);
   const int64_t per_sample = (int64_t)g.SST * 4;
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
   SLG_REQUIRE(per_sample + kConvExtra * 4 <= cap && (int64_t)a.C * a.H * a.W * 4 < (1LL << 31),
@@ -634,8 +700,9 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   else S = std::min(S, std::max<int64_t>(1, std::min(room / per_sample, cdiv(64, g.LPS))));
   S = std::min<int64_t>(S, std::max<int64_t>(1, a.B / device_cus()));
   S = std::min<int64_t>(S, a.B);
+  if (QUAD) S = 1;
   const size_t lds = (size_t)(S * per_sample + kConvExtra * 4);
-  auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC>;
+  auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -644,7 +711,8 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
       return (int)e;
     }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(Cfg::THREADS), lds, st, a.x,
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(QUAD ? kQuadThreads : Cfg::THREADS),
+                     lds, st, a.x,
                      (int)a.B, (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, g,
                      a.np, a.w, a.cm, a.ch, a.cw, a.rec, (int)S, a.out, (int)a.Ho, (int)a.Wo);
   SLG_LAUNCH_CHECK("conv_soft");
@@ -654,11 +722,22 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
 template <int NODE, int NLEAF, bool POOL>
 static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
   // taps per leaf: 4 registers when K <= 4 (TopK k=4, fixed wiring), else 8
-  if (a.K <= 4)
-    return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true>(a, st)
-                 : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false>(a, st);
-  return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true>(a, st)
-               : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false>(a, st);
+  if (a.K <= 4) {
+    if constexpr (conv_phase_layout(POOL, NLEAF, 4)) {
+      if (conv_use_quad(POOL, NLEAF, 4, a.C, a.Ho, a.Wo, a.kernel))
+        return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true, true>(a, st)
+                     : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false, true>(a, st);
+    }
+    return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true, false>(a, st)
+                 : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false, false>(a, st);
+  }
+  if constexpr (conv_phase_layout(POOL, NLEAF, kMaxK)) {
+    if (conv_use_quad(POOL, NLEAF, kMaxK, a.C, a.Ho, a.Wo, a.kernel))
+      return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true, true>(a, st)
+                   : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false, true>(a, st);
+  }
+  return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true, false>(a, st)
+               : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false, false>(a, st);
 }
 
 template <bool POOL>
@@ -827,7 +906,11 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
   const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
   SLG_REQUIRE(C * ((H + 2 * pad) * (W + 2 * pad) + 64) < (1LL << 31), SLG_E_SHAPE,
               "conv_soft_records: image too large");
-  const ConvGeom g = conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo);
+  // the layout the forward will choose for these shapes (quad offsets sit in
+  // slot 0 of the phase records)
+  const ConvGeom g = conv_use_quad(pool != 0, nleaf, km, C, Ho, Wo, 2 * pad + 1)
+                         ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
+                         : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo);
   const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K, pool);
   hipLaunchKernelGGL(conv_soft_records_kernel, dim3((unsigned)cdiv(N * R, 256)), dim3(256), 0,
                      as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km, phase ? 4 : 1,

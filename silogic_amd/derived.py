@@ -1,0 +1,44 @@
+"""Per-module caches of tables derived from the parameters.
+
+A forward without gradients reduces the parameters to device tables before
+its kernels run: soft records (resolved taps, softmax weights, node
+coefficients), hard codes (argmax gates as truth tables). For a model whose
+weights do not change between calls these tables are the same every time,
+so they are kept on the module and rebuilt only when one of the tensors they
+come from changes. The key of a table is the storage address and version
+counter of every parameter and buffer of the modules it reads: in-place
+updates (optimizer steps, ``copy_``, ``load_state_dict``) bump the version,
+and moving or replacing a tensor changes its storage. Writes through
+``tensor.data`` bypass the version counter; call :func:`clear` on a model
+after such writes. Tracing under ``torch.compile`` builds the tables afresh.
+"""
+import torch
+
+
+def state_key(*modules):
+    """Storage and version of every parameter and buffer of ``modules``."""
+    key = []
+    for m in modules:
+        for t in list(m.parameters()) + list(m.buffers()):
+            key.append((t.data_ptr(), t._version, t.device.index))
+    return tuple(key)
+
+
+def cached(owner, name, key, build):
+    """``build()``'s result, kept on ``owner`` under ``name`` while ``key``
+    (from :func:`state_key` plus the call's shapes) stays the same."""
+    if torch.compiler.is_compiling():
+        return build()
+    slot = owner.__dict__.get(name)
+    if slot is not None and slot[0] == key:
+        return slot[1]
+    value = build()
+    owner.__dict__[name] = (key, value)
+    return value
+
+
+def clear(model):
+    """Drop every cached table of ``model`` and its submodules."""
+    for m in model.modules():
+        for name in [n for n in m.__dict__ if n.startswith("_derived_")]:
+            del m.__dict__[name]

@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops
+from . import derived, ops
 from .connectomes import build_connectome, FixedConnectome
 from .functional import BASIS_COEFFS, TRUTH_TABLES, GATE_A, gate_probs
 from .nodes import build_node, _NODE_ALIASES
@@ -184,7 +184,8 @@ class LogicLayer(nn.Module):
         spec = None if grad else self.record_spec()
         if spec is not None:
             K = self.n_candidates
-            rec = ops.fc_soft_records([spec], K)[0]
+            rec = derived.cached(self, "_derived_records", (derived.state_key(self), K),
+                                 lambda: ops.fc_soft_records([spec], K)[0])
             return ops.fc_soft_rec(x, rec, self.in_dim, self.out_dim, K, self.node.kind,
                                    self._inv_tau())
         cand, w, npar = self.soft_params(grad)
@@ -481,11 +482,14 @@ class ConvLogicTree(nn.Module):
         """Per-channel records for input (C, H, W) and the pooled or plain
         forward: resolved taps, softmax leaf weights and node parameters
         (forward only, plain softmax)."""
-        cm, ch, cw = self._taps()
-        conn = None if self.connect == "fixed" else self.conn
-        return ops.conv_soft_records(conn, cm, ch, cw, self._raw(), self._kind(), self.d,
-                                     self.node_arity, cm.shape[-1], tuple(in_shape),
-                                     self.padding, pool)
+        def build():
+            cm, ch, cw = self._taps()
+            conn = None if self.connect == "fixed" else self.conn
+            return ops.conv_soft_records(conn, cm, ch, cw, self._raw(), self._kind(), self.d,
+                                         self.node_arity, cm.shape[-1], tuple(in_shape),
+                                         self.padding, pool)
+        key = (derived.state_key(self), tuple(in_shape), bool(pool))
+        return derived.cached(self, "_derived_records", key, build)
 
     def _soft(self, x, pool):
         ops.require_gpu(x)

@@ -19,7 +19,7 @@ reference's ``GroupSum.forward_hard`` (heads.py:41-45).
 import torch
 import torch.nn as nn
 
-from . import ops
+from . import derived, ops
 from .heads import GroupSum, build_decoder
 from .layers import LogicLayer, ConvLogicTree, OrPool, _needs_grad
 
@@ -37,7 +37,8 @@ def _soft_fc_stack(layers, head, x, wire_r):
     if not layers or any(s is None for s in specs) or len(Ks) != 1:
         return None
     K = Ks.pop()
-    recs = ops.fc_soft_records(specs, K)
+    recs = derived.cached(layers[0], "_derived_net_records", (derived.state_key(*layers), K),
+                          lambda: ops.fc_soft_records(specs, K))
     h = x
     for i, (layer, rec) in enumerate(zip(layers, recs)):
         kind, inv_tau = layer.node.kind, layer._inv_tau()
@@ -73,7 +74,8 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     widths = [layer.out_dim for layer in layers]
     spw = ops.fc_hard_net_supported(in_dim, widths, C)
     if spw:
-        codes = ops.fc_hard_codes_net(specs, compact=True)
+        codes = derived.cached(layers[0], "_derived_net_codes", derived.state_key(*layers),
+                               lambda: ops.fc_hard_codes_net(specs, compact=True))
         if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
@@ -303,7 +305,9 @@ class LogicConvNet(nn.Module):
         # the LDS-kernel trees of every block in one prep launch, generic
         # trees (walsh, deeper LUT trees) with their own per-node tables
         lds = [conv for conv in convs if not conv.generic]
-        batched = iter(ops.conv_hard_prep_net([conv.hard_spec() for conv in lds]) if lds else [])
+        batched = iter(derived.cached(
+            self, "_derived_conv_codes", derived.state_key(*lds),
+            lambda: ops.conv_hard_prep_net([conv.hard_spec() for conv in lds])) if lds else [])
         params = [conv.hard_params() if conv.generic else next(batched) for conv in convs]
         for conv, prm in zip(convs, params):
             x_in = xp

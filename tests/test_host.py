@@ -210,3 +210,26 @@ def test_bitpacking_without_a_gpu_raises():
     from silogic_amd import bitpacking as bp
     with pytest.raises((RuntimeError, AssertionError)):
         bp.pack_bits(np.zeros((4, 3), dtype=np.uint8))
+
+
+def test_derived_cache_follows_parameter_versions():
+    """Tables derived from parameters are rebuilt exactly when a parameter or
+    buffer changes in place, moves, or the cache is cleared."""
+    from silogic_amd import derived
+    m = torch.nn.Linear(3, 2)
+    m.register_buffer("idx", torch.arange(4))
+    calls = []
+
+    def get():
+        return derived.cached(m, "_derived_t", derived.state_key(m),
+                              lambda: calls.append(1) or len(calls))
+    assert get() == 1 and get() == 1
+    with torch.no_grad():
+        m.weight.add_(1.0)                  # in-place update: version bump
+    assert get() == 2 and get() == 2
+    m.idx[0] = 7                            # buffer write
+    assert get() == 3
+    m.weight = torch.nn.Parameter(m.weight.detach().clone())   # new storage
+    assert get() == 4
+    derived.clear(m)
+    assert get() == 5
