@@ -266,19 +266,31 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   const int nchunks = (ns * g.LPS + 63) / 64;
   const float inv_lps = 1.0f / (float)g.LPS;
   const float inv_col = 1.0f / (float)((PHASE || !POOL) ? g.RS : Wo);
+  // Quad layout: a wave takes four channels at once, one per 16-lane LDS
+  // conflict group of ds_read_b128 (lanes 0-3, 12-15, 20-27 / 4-11, 16-19,
+  // 28-31, and the same in the upper half), each group walking 16
+  // consecutive outputs; the chunks of 16 leave fewer idle lanes at the end
+  // of a sample than chunks of 64. Otherwise one channel per wave.
+  constexpr int CPW = QUAD ? 4 : 1;       // channels per wave
+  constexpr int LPC = 64 / CPW;           // lanes per channel
+  const int cslot = QUAD ? 2 * (lane >> 5) + (__popc((lane >> 2) & 7) & 1) : 0;
+  const int rank = QUAD ? (((lane & 31) >> 3) * 4 + (lane & 3)) : lane;
+  const int nchunks_c = QUAD ? (ns * g.LPS + LPC - 1) / LPC : nchunks;
   auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int n) {
     int nv;  // the channel in a vector register: vector loads, VGPR parameters
-    asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
+    if constexpr (QUAD) nv = min(n + cslot, N - 1);
+    else asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
     if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
     else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, nv, K, C, kernel, g, np, wts, cm, ch, cw);
   };
 
   ConvParams<NODE, NLEAF, KM, NW> Pc;
-  if (wave < N) load(Pc, wave);
-  for (int n = wave; n < N; n += nwaves) {
-    for (int chunk = 0; chunk < nchunks; ++chunk) {
-      const int q = chunk * 64 + lane;
-      bool active = q < ns * g.LPS;
+  if (wave * CPW < N) load(Pc, wave * CPW);
+  for (int nb = wave * CPW; nb < N; nb += nwaves * CPW) {
+    const int n = nb + cslot;  // this lane's channel
+    for (int chunk = 0; chunk < nchunks_c; ++chunk) {
+      const int q = chunk * LPC + rank;
+      bool active = q < ns * g.LPS && n < N;
       // (sample, row, column) of the lane: pooled row-major lanes walk Wo
       // columns, the others RS columns (those >= Wo idle). Idle lanes read
       // at the start of the staged region.
@@ -339,7 +351,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       }
       if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
     }
-    if (n + nwaves < N) load(Pc, n + nwaves);
+    if (nb + nwaves * CPW < N) load(Pc, nb + nwaves * CPW);
   }
 }
 
