@@ -171,6 +171,37 @@ __device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM, NW>& P, co
   for (int i = 0; i < ConvNode<NODE, NLEAF>::NPR; ++i) P.par[i] = v[LK * (NW + 1) + i];
 }
 
+// Channel parameters from a quad record: the records of phase-eligible
+// trees keep their phase size R, but a quad-layout record packs one offset
+// per tap (float4 units), then the weights, then the node parameters, so
+// only 2*L*KM + NPR floats are read.
+template <int NODE, int NLEAF, int KM, int NW, int R>
+__device__ inline void conv_params_record_quad(ConvParams<NODE, NLEAF, KM, NW>& P, const float* rec,
+                                               int nv) {
+  constexpr int LK = NLEAF * KM;
+  constexpr int NPR = ConvNode<NODE, NLEAF>::NPR;
+  constexpr int USED = (2 * LK + NPR + 3) & ~3;
+  static_assert(USED <= R, "quad records fit the phase record size");
+  float v[USED];
+  const float4* r4 = reinterpret_cast<const float4*>(rec + (int64_t)nv * R);
+#pragma unroll
+  for (int q = 0; q < USED / 4; ++q) {
+    const float4 t = r4[q];
+    v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+  }
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      P.off[l][k][0] = __float_as_int(v[l * KM + k]);
+#pragma unroll
+      for (int q = 1; q < NW; ++q) P.off[l][k][q] = 0;
+      P.wt[l][k] = v[LK + l * KM + k];
+    }
+#pragma unroll
+  for (int i = 0; i < NPR; ++i) P.par[i] = v[2 * LK + i];
+}
+
 // Quad-layout workgroups: 16 waves (the layout takes most of the LDS, so one
 // workgroup per CU; its per-tap state is one offset, which leaves room in
 // 128 VGPRs).
@@ -197,7 +228,12 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   // floats (contiguous in memory) to their padded positions. Every thread
   // issues kStage loads before it writes them, so that the copy is not one
   // load latency per row.
-  for (int i = threadIdx.x; i < ns * g.SST; i += blockDim.x) lds[i] = 0.0f;
+  if constexpr (QUAD) {  // the quad region is a whole number of 16-byte blocks
+    for (int i = threadIdx.x; i < ns * g.SST / 4; i += blockDim.x)
+      reinterpret_cast<f32x4*>(lds)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    for (int i = threadIdx.x; i < ns * g.SST; i += blockDim.x) lds[i] = 0.0f;
+  }
   __syncthreads();
   {
     // Thread t takes elements e = t + i*T (T = blockDim.x) and steps its
@@ -280,14 +316,20 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
     int nv;  // the channel in a vector register: vector loads, VGPR parameters
     if constexpr (QUAD) nv = min(n + cslot, N - 1);
     else asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
-    if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
+    if constexpr (REC && QUAD) conv_params_record_quad<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
+    else if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
     else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, nv, K, C, kernel, g, np, wts, cm, ch, cw);
   };
 
   ConvParams<NODE, NLEAF, KM, NW> Pc;
   if (wave * CPW < N) load(Pc, wave * CPW);
+  // quad (one sample per workgroup): the lane's output (row, col) advances
+  // by LPC outputs per chunk, carried incrementally
+  const int d_row = QUAD ? LPC / Wo : 0, d_col = QUAD ? LPC - d_row * Wo : 0;
   for (int nb = wave * CPW; nb < N; nb += nwaves * CPW) {
     const int n = nb + cslot;  // this lane's channel
+    float* out_n = out + ((int64_t)b0 * N + min(n, N - 1)) * P;  // quad: sample b0
+    int q_row = QUAD ? rank / Wo : 0, q_col = QUAD ? rank - (rank / Wo) * Wo : 0;
     for (int chunk = 0; chunk < nchunks_c; ++chunk) {
       const int q = chunk * LPC + rank;
       bool active = q < ns * g.LPS && n < N;
@@ -295,52 +337,81 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       // columns, the others RS columns (those >= Wo idle). Idle lanes read
       // at the start of the staged region.
       constexpr bool LINEAR = PHASE || !POOL;
-      const int s = active ? div_small(q, g.LPS, inv_lps) : 0;
-      const int rem = active ? q - (int)__umul24(s, g.LPS) : 0;
-      const int row = div_small(rem, LINEAR ? g.RS : Wo, inv_col);
-      const int col = rem - (int)__umul24(row, LINEAR ? g.RS : Wo);
+      int s, row, col;
+      if constexpr (QUAD) {
+        s = 0;
+        row = q_row;
+        col = q_col;
+        q_col += d_col;
+        q_row += d_row;
+        if (q_col >= Wo) { q_col -= Wo; ++q_row; }
+      } else {
+        s = active ? div_small(q, g.LPS, inv_lps) : 0;
+        const int rem = active ? q - (int)__umul24(s, g.LPS) : 0;
+        row = div_small(rem, LINEAR ? g.RS : Wo, inv_col);
+        col = rem - (int)__umul24(row, LINEAR ? g.RS : Wo);
+      }
       active = active && col < Wo;
       const int p = (int)__umul24(row, Wo) + col;
       const int bofs = QUAD ? 4 * ((int)__umul24(row, g.BW) + col)
-                            : (LINEAR ? rem : 2 * (int)__umul24(row, g.RS) + 2 * col);
+                            : (LINEAR ? q - (int)__umul24(s, g.LPS)
+                                      : 2 * (int)__umul24(row, g.RS) + 2 * col);
       const float* base = lds + (active ? __umul24(s, g.SST) + bofs : 0);
 
       // Tap k of every leaf per step: the guard k < K is uniform, and one
-      // step issues all NLEAF * NQ LDS reads before its first wait.
+      // step issues all NLEAF * NQ LDS reads before its first wait. With
+      // every candidate slot in use (K == KM) the steps are pipelined: the
+      // reads of step k+1 go out before the FMAs of step k.
       constexpr int NQ = POOL ? 4 : 1;
       float v[NQ][NLEAF];
 #pragma unroll
       for (int l = 0; l < NLEAF; ++l)
 #pragma unroll
         for (int qq = 0; qq < NQ; ++qq) v[qq][l] = 0.0f;
+      auto read_step = [&](int k, float (&t)[NLEAF][NQ]) {
 #pragma unroll
-      for (int k = 0; k < KM; ++k) {
-        if (k < K) {
-          float t[NLEAF][NQ];
+        for (int l = 0; l < NLEAF; ++l) {
+          if constexpr (QUAD) {
+            const f32x4 w4 = reinterpret_cast<const f32x4*>(base)[Pc.off[l][k][0]];
 #pragma unroll
-          for (int l = 0; l < NLEAF; ++l) {
-            if constexpr (QUAD) {
-              const f32x4 w4 = reinterpret_cast<const f32x4*>(base)[Pc.off[l][k][0]];
+            for (int qq = 0; qq < 4; ++qq) t[l][qq] = w4[qq];
+          } else if constexpr (PHASE) {
 #pragma unroll
-              for (int qq = 0; qq < 4; ++qq) t[l][qq] = w4[qq];
-            } else if constexpr (PHASE) {
-#pragma unroll
-              for (int qq = 0; qq < 4; ++qq) t[l][qq] = base[Pc.off[l][k][qq]];
-            } else {
-              const float* t0 = base + Pc.off[l][k][0];
-              t[l][0] = t0[0];
-              if constexpr (POOL) {
-                t[l][1] = t0[1];
-                t[l][2] = t0[g.RS];
-                t[l][3] = t0[g.RS + 1];
-              }
+            for (int qq = 0; qq < 4; ++qq) t[l][qq] = base[Pc.off[l][k][qq]];
+          } else {
+            const float* t0 = base + Pc.off[l][k][0];
+            t[l][0] = t0[0];
+            if constexpr (POOL) {
+              t[l][1] = t0[1];
+              t[l][2] = t0[g.RS];
+              t[l][3] = t0[g.RS + 1];
             }
           }
-          __builtin_amdgcn_sched_barrier(0);  // all reads of the step, then the FMAs
+        }
+      };
+      auto fma_step = [&](int k, const float (&t)[NLEAF][NQ]) {
 #pragma unroll
-          for (int l = 0; l < NLEAF; ++l)
+        for (int l = 0; l < NLEAF; ++l)
 #pragma unroll
-            for (int qq = 0; qq < NQ; ++qq) v[qq][l] = fmaf(Pc.wt[l][k], t[l][qq], v[qq][l]);
+          for (int qq = 0; qq < NQ; ++qq) v[qq][l] = fmaf(Pc.wt[l][k], t[l][qq], v[qq][l]);
+      };
+      if (QUAD && K == KM) {
+        float t[2][NLEAF][NQ];
+        read_step(0, t[0]);
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (k + 1 < KM) read_step(k + 1, t[(k + 1) & 1]);
+          fma_step(k, t[k & 1]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (k < K) {
+            float t[NLEAF][NQ];
+            read_step(k, t);
+            __builtin_amdgcn_sched_barrier(0);  // all reads of the step, then the FMAs
+            fma_step(k, t);
+          }
         }
       }
       float best = -INFINITY;
@@ -349,9 +420,146 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
         const float val = conv_tree_eval<NODE, NLEAF>(v[qq], Pc.par);
         best = fmaxf(best, val);
       }
-      if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
+      if constexpr (QUAD) {
+        if (active) out_n[p] = best;
+      } else {
+        if (active) out[((int64_t)(b0 + s) * N + n) * P + p] = best;
+      }
     }
     if (nb + nwaves * CPW < N) load(Pc, nb + nwaves * CPW);
+  }
+}
+
+// Quad layout, persistent: workgroup w takes samples w, w + grid, ... and
+// keeps one staged sample in LDS. The padding blocks are cleared once (the
+// staging writes only image pixels); the next sample's C*H*W floats ride in
+// registers (at most kQuadRegs per thread) while this sample computes, so
+// the input's HBM latency overlaps the compute; after the last read of the
+// sample they are scattered into the four copies. The arithmetic per output
+// is conv_soft_kernel's, in the same order.
+constexpr int kQuadRegs = 7;
+
+template <int NODE, int NLEAF, int KM, bool REC>
+__global__ void __launch_bounds__(kQuadThreads)
+conv_soft_quad_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K,
+                      int kernel, int pad, ConvGeom g, const float* __restrict__ np,
+                      const float* __restrict__ wts, const int* __restrict__ cm,
+                      const int* __restrict__ ch, const int* __restrict__ cw,
+                      const float* __restrict__ rec, float* __restrict__ out, int Ho, int Wo) {
+  using Cfg = ConvCfg<NODE, NLEAF, KM, true>;
+  static_assert(Cfg::PHASE, "the quad layout keeps the phase records");
+  constexpr int NW = Cfg::NW;
+  constexpr int CPW = 4, LPC = 16;
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int T = blockDim.x;
+  const int HW = H * W, total = C * HW;
+  const int P = Ho * Wo;
+
+  for (int i = threadIdx.x; i < g.SST / 4 + kConvExtra / 4; i += T)
+    reinterpret_cast<f32x4*>(lds)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // this thread's elements e = tid + u*T of a sample
+  float pf[kQuadRegs];
+  auto issue = [&](int b) {
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + (int64_t)b * total), (short)0, total * 4, kBufferWord3);
+#pragma unroll
+    for (int u = 0; u < kQuadRegs; ++u)  // offsets past the image read 0
+      pf[u] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(src, (threadIdx.x + u * T) * 4, 0, 0));
+  };
+  const int dump = g.SST + lane;
+  auto scatter = [&] {
+    const int tx = T % W, ty = (T / W) % H, tc = T / HW;
+    int px = threadIdx.x % W, py = (threadIdx.x / W) % H, pc = threadIdx.x / HW;
+#pragma unroll
+    for (int u = 0; u < kQuadRegs; ++u) {
+      const int Y = py + pad, X = px + pad;
+      const int sb = __umul24(pc, g.plane);
+      const bool keep = pc < C;
+#pragma unroll
+      for (int sy = 0; sy < 2; ++sy)
+#pragma unroll
+        for (int sx = 0; sx < 2; ++sx) {
+          const int by = (Y - sy) >> 1, bx = (X - sx) >> 1;
+          const bool in = keep && Y >= sy && X >= sx && by < g.BH && bx < g.BW;
+          const int a = sb + 4 * (__umul24(sy * 2 + sx, g.BH * g.BW) + __umul24(by, g.BW) + bx) +
+                        ((Y - sy) & 1) * 2 + ((X - sx) & 1);
+          lds[in ? a : dump] = pf[u];
+        }
+      px += tx;
+      const int cy = px >= W;
+      px -= cy ? W : 0;
+      py += ty + cy;
+      const int cc = py >= H;
+      py -= cc ? H : 0;
+      pc += tc + cc;
+    }
+  };
+
+  // four channels per wave on the ds_read_b128 conflict groups (see
+  // conv_soft_kernel's quad path)
+  const int cslot = 2 * (lane >> 5) + (__popc((lane >> 2) & 7) & 1);
+  const int rank = ((lane & 31) >> 3) * 4 + (lane & 3);
+  const int nchunks = (P + LPC - 1) / LPC;
+  const int d_row = LPC / Wo, d_col = LPC - d_row * Wo;
+  auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int nb) {
+    const int nv = min(nb + cslot, N - 1);
+    if constexpr (REC) conv_params_record_quad<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
+    else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, nv, K, C, kernel, g, np, wts, cm, ch, cw);
+  };
+  // with one channel group per wave the parameters stay for every sample
+  const bool one_group = N <= nwaves * CPW;
+  ConvParams<NODE, NLEAF, KM, NW> Pc;
+  if (one_group && wave * CPW < N) load(Pc, wave * CPW);
+
+  if (blockIdx.x < (unsigned)B) issue(blockIdx.x);
+  __syncthreads();  // cleared before the first scatter
+  for (int b = blockIdx.x; b < B; b += gridDim.x) {
+    scatter();
+    __syncthreads();
+    if (b + (int)gridDim.x < B) issue(b + gridDim.x);
+    for (int nb = wave * CPW; nb < N; nb += nwaves * CPW) {
+      if (!one_group) load(Pc, nb);
+      const int n = nb + cslot;
+      float* out_n = out + ((int64_t)b * N + min(n, N - 1)) * P;
+      int q_row = rank / Wo, q_col = rank - (rank / Wo) * Wo;
+      for (int chunk = 0; chunk < nchunks; ++chunk) {
+        const int q = chunk * LPC + rank;
+        const bool active = q < P && n < N;
+        const int row = q_row, col = q_col;
+        q_col += d_col;
+        q_row += d_row;
+        if (q_col >= Wo) { q_col -= Wo; ++q_row; }
+        const f32x4* base =
+            reinterpret_cast<const f32x4*>(lds) + (active ? (int)__umul24(row, g.BW) + col : 0);
+        float v[4][NLEAF];
+#pragma unroll
+        for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) v[qq][l] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (k < K) {
+            f32x4 t[NLEAF];
+#pragma unroll
+            for (int l = 0; l < NLEAF; ++l) t[l] = base[Pc.off[l][k][0]];
+#pragma unroll
+            for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+              for (int qq = 0; qq < 4; ++qq) v[qq][l] = fmaf(Pc.wt[l][k], t[l][qq], v[qq][l]);
+          }
+        }
+        float best = -INFINITY;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) best = fmaxf(best, conv_tree_eval<NODE, NLEAF>(v[qq], Pc.par));
+        if (active) out_n[(int)__umul24(row, Wo) + col] = best;
+      }
+    }
+    __syncthreads();  // every read of this sample precedes the next scatter
   }
 }
 
@@ -714,6 +922,25 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   S = std::min<int64_t>(S, a.B);
   if (QUAD) S = 1;
   const size_t lds = (size_t)(S * per_sample + kConvExtra * 4);
+  if constexpr (QUAD && POOL) {
+    if (a.C * a.H * a.W <= (int64_t)kQuadRegs * kQuadThreads) {
+      auto qk = conv_soft_quad_kernel<NODE, NLEAF, KM, REC>;
+      if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void*)qk,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) {
+          set_error("conv_soft: LDS %zu: %s", lds, hipGetErrorString(e));
+          return (int)e;
+        }
+      }
+      const int64_t grid = std::min<int64_t>(a.B, device_cus());
+      hipLaunchKernelGGL(qk, dim3((unsigned)grid), dim3(kQuadThreads), lds, st, a.x, (int)a.B,
+                         (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, g, a.np,
+                         a.w, a.cm, a.ch, a.cw, a.rec, a.out, (int)a.Ho, (int)a.Wo);
+      SLG_LAUNCH_CHECK("conv_soft");
+      return 0;
+    }
+  }
   auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -920,13 +1147,14 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
               "conv_soft_records: image too large");
   // the layout the forward will choose for these shapes (quad offsets sit in
   // slot 0 of the phase records)
-  const ConvGeom g = conv_use_quad(pool != 0, nleaf, km, C, Ho, Wo, 2 * pad + 1)
-                         ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
-                         : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo);
+  const bool quad = conv_use_quad(pool != 0, nleaf, km, C, Ho, Wo, 2 * pad + 1);
+  const ConvGeom g = quad ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
+                          : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo);
   const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K, pool);
   hipLaunchKernelGGL(conv_soft_records_kernel, dim3((unsigned)cdiv(N * R, 256)), dim3(256), 0,
-                     as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km, phase ? 4 : 1,
-                     node_kind, arity, raw, (int)C, 2 * pad + 1, g, R, rec);
+                     as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km,
+                     quad ? 1 : (phase ? 4 : 1), node_kind, arity, raw, (int)C, 2 * pad + 1, g, R,
+                     rec);
   SLG_LAUNCH_CHECK("conv_soft_records");
   return 0;
 }

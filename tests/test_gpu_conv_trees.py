@@ -51,6 +51,8 @@ def _blk(conv, H):
     ("hybrid", 2, 5, "fixed", 3, 8, 6, 2),       # 32 leaves
     ("gate16", 2, 5, "topk", 4, 8, 6, 2),
     ("gate16", 2, 2, "topk", 48, 32, 8, 2),      # 196 KB image: past LDS
+    ("gate16", 2, 2, "topk", 13, 24, 8, 3),      # quad layout, staged without registers
+    ("gate16", 2, 2, "topk", 7, 14, 10, 300),    # quad layout, persistent: 300 samples
 ])
 def test_conv_tree_forward_and_hard(node, arity, depth, connect, C, H, N, B):
     conv = sl.ConvLogicTree(C, N, kernel=3, tree_depth=depth, connect=connect, k=4, n_chan=2,
