@@ -394,6 +394,75 @@ fc_soft_rec_kernel(const float* __restrict__ x, int B, int IN, int OUT,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Inputs wider than LDS: slab staging
+// ---------------------------------------------------------------------------
+// A workgroup owns 4 samples and one output per thread. The rows are staged
+// slab by slab (SL inputs at a time, transposed as in fc_soft_kernel: one
+// 16-byte slot per input holds the 4 samples); every thread keeps the
+// gathered operand vectors of its output's 2K candidates in registers,
+// filling those that fall in the current slab, and after the last slab
+// accumulates them in candidate order: the fmaf sequence of fc_soft_kernel,
+// so the same bits. The rows are read once per workgroup, so ceil(OUT /
+// threads) times per tile: a path for widths the one-pass kernels cannot
+// stage, not a fast one.
+template <int NODE, int KC, bool REC>
+__global__ void __launch_bounds__(KC > 0 ? 1024 : 512)
+fc_soft_wide_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, ParamView pv,
+                    float inv_tau, float* __restrict__ y, int SL) {
+  constexpr int S = 4;
+  constexpr int KM = KC > 0 ? KC : 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  f32x4* lds = reinterpret_cast<f32x4*>(smem);
+  const int K = KC > 0 ? KC : Kr;
+  const int b0 = blockIdx.x * S;
+  const int rows = min(S, B - b0);
+  const int o = blockIdx.y * blockDim.x + threadIdx.x;
+  const bool valid = o < OUT;
+  FcParams<KM> P;
+  load_params<KC, KM, REC>(P, min(o, OUT - 1), K, pv);
+  const uint32_t lim = (uint32_t)IN - 1u;
+  f32x4 xa[KM], xb[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    xa[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    xb[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s0 = 0; s0 < IN; s0 += SL) {
+    const int sl = min(SL, IN - s0);
+    __syncthreads();  // the previous slab's reads are done
+    for (int i = threadIdx.x; i < sl; i += blockDim.x) {
+      float e[S];
+#pragma unroll
+      for (int v = 0; v < S; ++v)
+        e[v] = (v < rows) ? __builtin_nontemporal_load(x + (int64_t)(b0 + v) * IN + s0 + i) : 0.f;
+      lds[i] = f32x4{e[0], e[1], e[2], e[3]};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      if (KC > 0 || k < K) {
+        const uint32_t ra = min((uint32_t)P.ia[k], lim) - (uint32_t)s0;
+        const uint32_t rb = min((uint32_t)P.ib[k], lim) - (uint32_t)s0;
+        if (ra < (uint32_t)sl) xa[k] = lds[ra];
+        if (rb < (uint32_t)sl) xb[k] = lds[rb];
+      }
+    }
+  }
+  f32x4 A = zero_vec<f32x4>(), Bv = zero_vec<f32x4>();
+#pragma unroll
+  for (int k = 0; k < KM; ++k)
+    if (KC > 0 || k < K) fma_acc(A, P.fa[k], xa[k]);
+#pragma unroll
+  for (int k = 0; k < KM; ++k)
+    if (KC > 0 || k < K) fma_acc(Bv, P.fb[k], xb[k]);
+  if (valid) {
+#pragma unroll
+    for (int v = 0; v < S; ++v)
+      if (v < rows) y[(int64_t)(b0 + v) * OUT + o] = node_eval<NODE>(A[v], Bv[v], P.p, inv_tau);
+  }
+}
+
 struct SoftArgs {
   const float* x; int64_t B, IN, OUT; int K;
   ParamView pv;
@@ -525,6 +594,55 @@ static int pick_threads(int64_t IN, int S, int requested) {
   return 1024;  // capped per variant by soft_max_threads
 }
 
+template <int NODE, int KC, bool REC>
+static int launch_soft_wide(const SoftArgs& a, hipStream_t st) {
+  auto kern = fc_soft_wide_kernel<NODE, KC, REC>;
+  const int threads = KC > 0 ? 1024 : 512;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  const int SL = (int)(cap / 16);  // inputs per slab: 16 bytes (4 samples) each
+  const size_t lds = (size_t)SL * 16;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("fc_soft: cannot reserve %zu B LDS: %s", lds, hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  const int64_t tiles = cdiv(a.B, 4), oblocks = cdiv(a.OUT, threads);
+  SLG_REQUIRE(tiles < (1LL << 31) && oblocks < 65536, SLG_E_SHAPE, "fc_soft: grid too large");
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)oblocks), dim3(threads), lds, st, a.x,
+                     (int)a.B, (int)a.IN, (int)a.OUT, a.K, a.pv, a.inv_tau, a.y, SL);
+  SLG_LAUNCH_CHECK("fc_soft");
+  return 0;
+}
+
+template <int NODE>
+static int launch_soft_wide_node(const SoftArgs& a, hipStream_t st) {
+  const ParamView& v = a.pv;
+  if (v.rec) {
+    if (a.K == 8) return launch_soft_wide<NODE, 8, true>(a, st);
+    if (a.K == 4) return launch_soft_wide<NODE, 4, true>(a, st);
+    return launch_soft_wide<NODE, 0, true>(a, st);
+  }
+  const bool vec = al16(v.ca) && al16(v.cb) && al16(v.wa) && al16(v.wb) &&
+                   v.cstride % 4 == 0 && v.wstride % 4 == 0;
+  if (a.K == 8 && vec) return launch_soft_wide<NODE, 8, false>(a, st);
+  if (a.K == 4 && vec) return launch_soft_wide<NODE, 4, false>(a, st);
+  return launch_soft_wide<NODE, 0, false>(a, st);
+}
+
+static int fc_soft_wide(const SoftArgs& a, int node_kind, hipStream_t st) {
+  switch (node_kind) {
+    case SLG_NODE_GATE16: return launch_soft_wide_node<SLG_NODE_GATE16>(a, st);
+    case SLG_NODE_WALSH: return launch_soft_wide_node<SLG_NODE_WALSH>(a, st);
+    case SLG_NODE_MULTILINEAR2: return launch_soft_wide_node<SLG_NODE_MULTILINEAR2>(a, st);
+    default: break;
+  }
+  set_error("fc_soft: unknown node_kind %d", node_kind);
+  return SLG_E_ARG;
+}
+
 static int fc_soft_dispatch(SoftArgs a, int node_kind, hipStream_t st) {
   const ParamView& v = a.pv;
   const bool head = a.hd.logits != nullptr;
@@ -541,6 +659,11 @@ static int fc_soft_dispatch(SoftArgs a, int node_kind, hipStream_t st) {
     SLG_REQUIRE(a.hd.C > 0 && a.OUT % a.hd.C == 0 && a.B * a.hd.C < (1LL << 31), SLG_E_SHAPE,
                 "fc_soft: OUT=%lld not divisible by C=%d", (long long)a.OUT, a.hd.C);
   if (a.B == 0) return 0;
+  if (a.S == 0 && pick_tile(a.IN, 0) == 0) {  // rows wider than LDS: slab staging
+    SLG_REQUIRE(!head, SLG_E_UNSUPPORTED, "fc_soft: the fused GroupSum needs IN <= %lld",
+                (long long)(device_lds_bytes() / 4));
+    return fc_soft_wide(a, node_kind, st);
+  }
   a.S = pick_tile(a.IN, a.S);
   SLG_REQUIRE(a.S > 0 && (int64_t)a.IN * a.S * 4 <= device_lds_bytes(), SLG_E_SHAPE,
               "fc_soft: IN=%lld does not fit LDS", (long long)a.IN);

@@ -253,11 +253,17 @@ __global__ void __launch_bounds__(256) fc_soft_bwd_gather_kernel(const float* __
 // w_b[0..K), param[0..4)); with gbr, also the node's operand gradients
 // ga, gb of every (sample, output) at gbr[b][o], gbr[b][OUT+o] (rows of
 // 2*OUT, coalesced along the outputs), transposed for the gather kernel.
-template <int NODE, int KC, int S>
+//
+// WIDE (rows wider than LDS): one sample per tile, staged slab by slab (SL
+// inputs at a time); each thread keeps its output's 2K gathered operands in
+// registers, filling those in the current slab, then runs the same math.
+// Parameters come from the separate arrays (32-bit indices).
+template <int NODE, int KC, int S, bool WIDE>
 __global__ void __launch_bounds__((bwd_threads<KC>()))
 fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr, ParamView pv,
                      float inv_tau, const float* __restrict__ gy, int n_orange, int tiles_per_range,
-                     float* __restrict__ part, float* __restrict__ gbr) {
+                     float* __restrict__ part, float* __restrict__ gbr, int SL) {
+  static_assert(!WIDE || S == 1, "slab staging takes one sample per tile");
   constexpr int KM = KC > 0 ? KC : 16;
   using vt = typename vecf<S>::t;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -268,7 +274,7 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
   const int o = r_o * blockDim.x + threadIdx.x;
   const bool valid = o < OUT;
   FcParams<KM> P;
-  load_params<KC, KM, true>(P, min(o, OUT - 1), K, pv);
+  load_params<KC, KM, !WIDE>(P, min(o, OUT - 1), K, pv);
   const uint32_t lim = (uint32_t)IN - 1u;
 #pragma unroll
   for (int k = 0; k < KM; ++k) {  // clamp in place: one copy of the indices
@@ -285,15 +291,42 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
   const int t_end = min(n_tiles, (r_b + 1) * tiles_per_range);
   for (int t = r_b * tiles_per_range; t < t_end; ++t) {
     const int b0 = t * S;
-    __syncthreads();  // the previous tile's reads are done
-    stage_rows<S, false>(xs, x, B, IN, b0);  // the other output ranges re-read these rows
-    __syncthreads();
+    vt xa[WIDE ? KM : 1], xb[WIDE ? KM : 1];  // wide: the gathered operands
+    if constexpr (WIDE) {
+#pragma unroll
+      for (int k = 0; k < KM; ++k) xa[k] = xb[k] = 0.0f;
+      for (int s0 = 0; s0 < IN; s0 += SL) {
+        const int sl = min(SL, IN - s0);
+        __syncthreads();  // the previous slab's reads are done
+        for (int i = threadIdx.x; i < sl; i += blockDim.x)
+          xs[i] = b0 < B ? x[(int64_t)b0 * IN + s0 + i] : 0.0f;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (KC > 0 || k < K) {
+            const uint32_t ra = (uint32_t)ia[k] - (uint32_t)s0, rb = (uint32_t)ib[k] - (uint32_t)s0;
+            if (ra < (uint32_t)sl) xa[k] = xs[ra];
+            if (rb < (uint32_t)sl) xb[k] = xs[rb];
+          }
+        }
+      }
+    } else {
+      __syncthreads();  // the previous tile's reads are done
+      stage_rows<S, false>(xs, x, B, IN, b0);  // the other output ranges re-read these rows
+      __syncthreads();
+    }
+    auto opa = [&](int k) -> vt {
+      if constexpr (WIDE) return xa[k]; else return xs[ia[k]];
+    };
+    auto opb = [&](int k) -> vt {
+      if constexpr (WIDE) return xb[k]; else return xs[ib[k]];
+    };
     vt A = zero_vec<vt>(), Bv = zero_vec<vt>();
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
       if (KC > 0 || k < K) {
-        fma_acc(A, P.fa[k], xs[ia[k]]);
-        fma_acc(Bv, P.fb[k], xs[ib[k]]);
+        fma_acc(A, P.fa[k], opa(k));
+        fma_acc(Bv, P.fb[k], opb(k));
       }
     }
     float ga[S], gb[S];
@@ -316,7 +349,7 @@ fc_soft_bwd_w_kernel(const float* __restrict__ x, int B, int IN, int OUT, int Kr
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
       if (KC > 0 || k < K) {
-        const vt va = xs[ia[k]], vb = xs[ib[k]];
+        const vt va = opa(k), vb = opb(k);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           swa[k] = fmaf(ga[s], lanev(va, s), swa[k]);
@@ -388,6 +421,7 @@ inline int64_t round4(int64_t n) { return (n + 3) & ~int64_t(3); }
 // Workspace (in 4-byte words): records | partials | gbr | input-gradient part.
 struct BwdPlan {
   int Sw;              // samples per LDS tile of the weight kernel (0 = unsupported)
+  int SL;              // > 0: rows wider than LDS, staged SL inputs at a time (Sw = 1)
   int n_orange, NR, tiles_per_range;
   int64_t rec_floats, part_floats, gbr_floats, in_floats;
   int64_t total() const { return rec_floats + part_floats + gbr_floats + in_floats; }
@@ -454,32 +488,36 @@ static BwdPlan bwd_plan(int64_t B, int64_t IN, int64_t OUT, int K) {
   BwdPlan p{};
   p.Sw = bwd_tile(IN, 4);   // x tile
   if (K == 8) p.Sw = std::min(p.Sw, 2);  // 4-sample tiles overflow 128 VGPRs at 1024 threads
+  if (p.Sw == 0) {  // slab staging, one sample per tile
+    p.Sw = 1;
+    p.SL = (int)(std::min<int64_t>(device_lds_bytes(), 160 * 1024) / 4);
+  }
   const int threads = K == 8 || K == 4 ? 1024 : 512;
   p.n_orange = (int)cdiv(OUT, threads);
   const int64_t n_tiles = p.Sw ? cdiv(std::max<int64_t>(B, 1), p.Sw) : 1;
   // one round of workgroups: as many sample ranges as resident slots allow
   // (2048 threads and 160 KB of LDS per CU); a partial second round would
   // double the kernel's time
-  const int64_t lds = std::max<int64_t>(IN * std::max(p.Sw, 1) * 4, 1);
+  const int64_t lds = p.SL ? (int64_t)p.SL * 4 : std::max<int64_t>(IN * std::max(p.Sw, 1) * 4, 1);
   const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(2048 / threads, (160 * 1024) / lds));
   const int64_t slots = per_cu * device_cus();
   p.NR = (int)std::max<int64_t>(1, std::min<int64_t>(n_tiles, slots / p.n_orange));
   p.tiles_per_range = (int)cdiv(n_tiles, p.NR);
   p.NR = (int)cdiv(n_tiles, p.tiles_per_range);
   const int64_t LB = cdiv(std::max<int64_t>(B, 1), kGatherSamples) * kGatherSamples;
-  p.rec_floats = cdiv(OUT, 64) * 64 * (int64_t)rec_quads(K) * 4;
+  p.rec_floats = p.SL ? 0 : cdiv(OUT, 64) * 64 * (int64_t)rec_quads(K) * 4;
   p.part_floats = round4((int64_t)p.NR * (2 * K + 4) * OUT);
   p.gbr_floats = 2 * OUT * LB;  // rows b < n_tiles * Sw <= LB
   p.in_floats = fc_input_grad_floats(B, IN, OUT, 2, K);
   return p;
 }
 
-template <int NODE, int KC, int S>
+template <int NODE, int KC, int S, bool WIDE = false>
 static int launch_bwd_w(const float* x, int64_t B, int64_t IN, int64_t OUT, int K,
                         const ParamView& pv, float inv_tau, const float* gy, const BwdPlan& p,
                         float* part, float* gbr, hipStream_t st) {
-  auto kern = fc_soft_bwd_w_kernel<NODE, KC, S>;
-  const size_t lds = (size_t)IN * S * 4;
+  auto kern = fc_soft_bwd_w_kernel<NODE, KC, S, WIDE>;
+  const size_t lds = WIDE ? (size_t)p.SL * 4 : (size_t)IN * S * 4;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -490,7 +528,7 @@ static int launch_bwd_w(const float* x, int64_t B, int64_t IN, int64_t OUT, int 
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)(p.n_orange * p.NR)), dim3(bwd_threads<KC>()), lds, st,
                      x, (int)B, (int)IN, (int)OUT, K, pv, inv_tau, gy, p.n_orange,
-                     p.tiles_per_range, part, gbr);
+                     p.tiles_per_range, part, gbr, p.SL);
   SLG_LAUNCH_CHECK("fc_soft_bwd_w");
   return 0;
 }
@@ -499,6 +537,7 @@ template <int NODE, int KC>
 static int bwd_node_k(const float* x, int64_t B, int64_t IN, int64_t OUT, int K,
                       const ParamView& pv, float inv_tau, const float* gy, float* part, float* gbr,
                       const BwdPlan& p, hipStream_t st) {
+  if (p.SL) return launch_bwd_w<NODE, KC, 1, true>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, gbr, st);
   if constexpr (KC != 8) {  // K = 8 tiles stop at 2 samples (the plan caps them)
     if (p.Sw == 4)
       return launch_bwd_w<NODE, KC, 4>(x, B, IN, OUT, K, pv, inv_tau, gy, p, part, gbr, st);
@@ -525,8 +564,9 @@ extern "C" {
 int64_t slg_fc_soft_bwd_workspace(int64_t B, int64_t IN, int64_t OUT, int32_t K) {
   if (B < 0 || IN <= 0 || OUT <= 0 || K < 1 || K > 16 || 2 * OUT * K >= (1LL << 31)) return -1;
   const BwdPlan p = bwd_plan(B, IN, OUT, K);
-  // records hold 16-bit input indices: the same limit slg_fc_soft_bwd checks
-  if (!p.Sw || IN > 65536) return -1;
+  // records hold 16-bit input indices; wider rows take the slab kernel,
+  // which reads the separate arrays
+  if (!p.Sw || (IN > 65536 && !p.SL)) return -1;
   return p.total();
 }
 
@@ -545,8 +585,8 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
                   (int64_t)B * IN < (1LL << 40),
               SLG_E_SHAPE, "fc_soft_bwd: bad sizes");
   const BwdPlan p = bwd_plan(B, IN, OUT, K);
-  SLG_REQUIRE(p.Sw && IN <= 65536, SLG_E_UNSUPPORTED, "fc_soft_bwd: IN=%lld does not fit LDS",
-              (long long)IN);
+  SLG_REQUIRE(p.Sw && (IN <= 65536 || p.SL), SLG_E_UNSUPPORTED,
+              "fc_soft_bwd: IN=%lld does not fit LDS", (long long)IN);
   SLG_REQUIRE(workspace_floats >= p.total(), SLG_E_ARG,
               "fc_soft_bwd: workspace of %lld floats, %lld needed", (long long)workspace_floats,
               (long long)p.total());
@@ -555,15 +595,28 @@ int slg_fc_soft_bwd(const float* x, int64_t B, int64_t IN, int64_t OUT, int32_t 
   float* part = rec + p.rec_floats;
   float* gbr = part + p.part_floats;
   float* in_ws = gbr + p.gbr_floats;
-  hipLaunchKernelGGL(fc_soft_pack_records_kernel, dim3((unsigned)cdiv(p.rec_floats, 256)),
-                     dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN,
-                     reinterpret_cast<uint32_t*>(rec));
-  SLG_LAUNCH_CHECK("fc_soft_pack_records");
+  if (!p.SL) {
+    hipLaunchKernelGGL(fc_soft_pack_records_kernel, dim3((unsigned)cdiv(p.rec_floats, 256)),
+                       dim3(256), 0, st, cand, w, node_param, (int)OUT, K, (int)IN,
+                       reinterpret_cast<uint32_t*>(rec));
+    SLG_LAUNCH_CHECK("fc_soft_pack_records");
+  }
   const bool want_w = gw || gnp;
   const bool want_x = gx != nullptr && B > 0;
   if (B > 0 && (want_w || want_x)) {
     ParamView pv{};
-    pv.rec = rec;
+    if (p.SL) {  // the slab kernel reads the separate arrays
+      pv.ca = cand;
+      pv.cb = cand + K;
+      pv.wa = w;
+      pv.wb = w + K;
+      pv.np = node_param;
+      pv.cstride = 2 * K;
+      pv.wstride = 2 * K;
+      pv.npstride = 4;
+    } else {
+      pv.rec = rec;
+    }
     float* pp = want_w ? part : nullptr;
     float* pg = want_x ? gbr : nullptr;
     int rc = 0;

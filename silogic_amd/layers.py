@@ -136,7 +136,7 @@ class LogicLayer(nn.Module):
         """``(cand, conn, raw, in_dim, node_kind, order)`` for
         ``ops.fc_soft_records`` when the forward without gradients is a plain
         softmax selection, else ``None`` (also for LUT layers)."""
-        if self.is_lut:
+        if self.is_lut or self.in_dim > 65536:   # records hold 16-bit input indices
             return None
         self._check_supported()
         conn = self._conn

@@ -3,8 +3,9 @@
 Each op is registered with ``torch.library.custom_op``, a fake (meta)
 implementation that gives output shapes and dtypes without running a
 kernel, and, for the differentiable ops, ``register_autograd`` with a
-backward that is itself a custom op (the HIP backward kernels; shapes they
-do not take fall back to the composite torch backward inside the op). So
+backward that is itself a custom op (the HIP backward kernels; for shapes
+they do not take, the autograd backward differentiates the op's torch
+expression instead). So
 ``torch.compile`` / FX tracing see opaque operators instead of a graph
 break at the ctypes call. The drop-ins of ``silogic_amd.kernels`` (the
 reference's ``silogic.kernels``, kernels/__init__.py:21-55) call these ops.
@@ -31,6 +32,18 @@ def _empty(ref):
     return ref.new_empty((0,))
 
 
+def _composite(fn, tensors, needs, gy):
+    """Gradients of ``fn(*tensors)`` by autograd on its torch expression: the
+    backward of shapes the HIP kernels do not take. Runs in the autograd
+    backward itself (an op's implementation cannot record a graph)."""
+    with torch.enable_grad():
+        leaves = [t.detach().float().requires_grad_(n) for t, n in zip(tensors, needs)]
+        y = fn(*leaves)
+        inputs = [t for t, n in zip(leaves, needs) if n]
+        grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
+    return tuple(grads.pop(0) if n else None for n in needs)
+
+
 # ---------------------------------------------------------------------------
 # FC soft layer (dense_logic / warp_logic)
 # ---------------------------------------------------------------------------
@@ -55,15 +68,9 @@ def fc_soft_bwd(x: Tensor, cand: Tensor, w: Tensor, npar: Tensor, node_kind: int
                 need_np: bool) -> Tuple[Tensor, Tensor, Tensor]:
     """``(gx, gw, gnp)`` of fc_soft; unneeded ones are empty."""
     got = ops.fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need_x, need_w, need_np)
-    if got is None:   # shapes the HIP backward does not take: composite torch backward
-        with torch.enable_grad():
-            xs = ops._as_f32(x.detach()).requires_grad_(need_x)
-            ws = w.detach().float().requires_grad_(need_w)
-            ns = npar.detach().float().requires_grad_(need_np)
-            y = ops.fc_soft_torch(xs, cand, ws, ns, node_kind, inv_tau)
-            inputs = [t for t, n in ((xs, need_x), (ws, need_w), (ns, need_np)) if n]
-            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
-        got = tuple(grads.pop(0) if n else None for n in (need_x, need_w, need_np))
+    if got is None:
+        raise NotImplementedError("fc_soft backward: shape outside the HIP kernels "
+                                  "(K > 16 or 2*OUT*K >= 2^31)")
     gx, gw, gn = got
     return (gx if gx is not None else _empty(x), gw if gw is not None else _empty(x),
             gn if gn is not None else _empty(x))
@@ -86,6 +93,10 @@ def _fc_soft_setup(ctx, inputs, output):
 def _fc_soft_backward(ctx, gy):
     x, cand, w, npar = ctx.saved_tensors
     need = ctx.needs_input_grad
+    if not ops.fc_soft_bwd_supported(x, cand):
+        gx, gw, gn = _composite(lambda a, b, c: ops.fc_soft_torch(a, cand, b, c, *ctx.meta),
+                                (x, w, npar), (need[0], need[2], need[3]), gy)
+        return gx, None, gw, gn, None, None
     gx, gw, gn = fc_soft_bwd(x, cand, w, npar, *ctx.meta, gy, need[0], need[2], need[3])
     return _none(gx, need[0]), None, _none(gw, need[2]), _none(gn, need[3]), None, None
 
@@ -122,7 +133,11 @@ def _dense_backward(ctx, gy):
     need_w = need[3] or need[4]
     cand = torch.stack([ca, cb], dim=1).to(torch.int32)
     w = torch.stack([wa, wb], dim=1)
-    gx, gw, gn = fc_soft_bwd(x, cand, w, coef, *ctx.meta, gy, need[0], need_w, need[5])
+    if not ops.fc_soft_bwd_supported(x, cand):
+        gx, gw, gn = _composite(lambda a, b, c: ops.fc_soft_torch(a, cand, b, c, *ctx.meta),
+                                (x, w, coef), (need[0], need_w, need[5]), gy)
+    else:
+        gx, gw, gn = fc_soft_bwd(x, cand, w, coef, *ctx.meta, gy, need[0], need_w, need[5])
     gwa = gw[:, 0] if need[3] else None
     gwb = gw[:, 1] if need[4] else None
     return _none(gx, need[0]), None, None, gwa, gwb, _none(gn, need[5]), None, None
@@ -274,15 +289,8 @@ def conv_soft_bwd(x: Tensor, npar: Tensor, w: Tensor, cm: Tensor, ch: Tensor, cw
     """``(gx, gnp, gw)`` of conv_soft; unneeded ones are empty."""
     meta = (node_kind, depth, arity, K, pad, pool)
     got = ops.conv_soft_bwd(x, npar, w, cm, ch, cw, *meta, gy, need_x, need_np, need_w)
-    if got is None:   # shapes the HIP backward does not take: composite torch backward
-        with torch.enable_grad():
-            xs = ops._as_f32(x.detach()).requires_grad_(need_x)
-            ns = npar.detach().float().requires_grad_(need_np)
-            ws = w.detach().float().requires_grad_(need_w)
-            y = ops.conv_soft_torch(xs, ns, ws, cm, ch, cw, *meta)
-            inputs = [t for t, n in ((xs, need_x), (ns, need_np), (ws, need_w)) if n]
-            grads = list(torch.autograd.grad(y, inputs, gy)) if inputs else []
-        got = tuple(grads.pop(0) if n else None for n in (need_x, need_np, need_w))
+    if got is None:
+        raise NotImplementedError("conv_soft backward: shape outside the HIP kernels")
     gx, gn, gw = got
     return (gx if gx is not None else _empty(x), gn if gn is not None else _empty(x),
             gw if gw is not None else _empty(x))
@@ -306,6 +314,11 @@ def _conv_setup(ctx, inputs, output):
 def _conv_backward(ctx, gy):
     x, npar, w, cm, ch, cw = ctx.saved_tensors
     need = ctx.needs_input_grad
+    if not ops.conv_soft_bwd_supported(x, cm, *ctx.meta):
+        gx, gn, gw = _composite(
+            lambda a, b, c: ops.conv_soft_torch(a, b, c, cm, ch, cw, *ctx.meta), (x, npar, w),
+            need[:3], gy)
+        return (gx, gn, gw) + (None,) * 9
     gx, gn, gw = conv_soft_bwd(x, npar, w, cm, ch, cw, *ctx.meta, gy, need[0], need[1], need[2])
     return (_none(gx, need[0]), _none(gn, need[1]), _none(gw, need[2])) + (None,) * 9
 

@@ -7,10 +7,10 @@ raises.
 
 Autograd: with gradients the soft ops run as the ``torch.ops.silogic_hip``
 custom operators of ``library.py`` (opaque to ``torch.compile``), whose
-backward runs the HIP backward kernels; shapes those kernels do not take use
-a composite backward of differentiable torch ops (``fc_soft_torch``,
-``conv_soft_torch``). Without gradients the wrappers launch the kernels
-directly.
+backward runs the HIP backward kernels; for shapes those kernels do not take,
+the autograd backward differentiates the op's torch expression
+(``fc_soft_torch``, ``conv_soft_torch``). Without gradients the wrappers
+launch the kernels directly.
 """
 import ctypes
 
@@ -126,6 +126,13 @@ def fc_soft_torch(x, cand, w, npar, node_kind, inv_tau):
         return (ua * ub) * c[:, 0] + (a * ub) * c[:, 1] + (ua * b) * c[:, 2] + (a * b) * c[:, 3]
     z = c[:, 0] + c[:, 1] * a + c[:, 2] * b + c[:, 3] * (a * b)
     return torch.sigmoid(z * inv_tau) if node_kind == WALSH else z
+
+
+def fc_soft_bwd_supported(x, cand):
+    """Whether the HIP backward takes ``x [B,IN]`` against ``cand [OUT,2,K]``."""
+    B, IN = x.shape
+    OUT, _, K = cand.shape
+    return _lib.lib().slg_fc_soft_bwd_workspace(B, IN, OUT, K) >= 0
 
 
 def fc_soft_bwd(x, cand, w, npar, node_kind, inv_tau, gy, need_x=True, need_w=True,
@@ -703,6 +710,13 @@ def conv_soft_torch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, poo
     Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
     out = out.view(B, N, Hf, Wf)
     return F.max_pool2d(out, 2, 2) if pool else out
+
+
+def conv_soft_bwd_supported(x, cm, node_kind, depth, arity, K, pad, pool):
+    """Whether the HIP backward takes this conv layer shape."""
+    B, Cc, H, W = x.shape
+    return _lib.lib().slg_conv_soft_bwd_workspace(B, Cc, H, W, cm.shape[0], node_kind, depth,
+                                                  arity, K, pad, int(bool(pool))) >= 0
 
 
 def conv_soft_bwd(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, pool, gy,

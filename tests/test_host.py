@@ -84,8 +84,11 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = L.slg_fc_soft_fwd_groupsum(fake, 4, 999, 60, 8, fake, 1000, 0, 1.0, 10, 1.0, fake,
                                     None)
     assert rc == -2 and b"built for 1000" in L.slg_last_error()
-    # the backward's workspace query agrees with the entry point's 16-bit index limit
-    assert L.slg_fc_soft_bwd_workspace(8, 65537, 16, 8) == -1
+    # the backward takes rows wider than 16-bit record indices (slab staging),
+    # and refuses fan-ins beyond 16
+    assert L.slg_fc_soft_bwd_workspace(8, 65537, 16, 8) > 0
+    assert L.slg_fc_soft_bwd_workspace(8, 1 << 20, 16, 8) > 0
+    assert L.slg_fc_soft_bwd_workspace(8, 1000, 16, 17) == -1
 
 
 def test_cpu_inputs_are_refused():
