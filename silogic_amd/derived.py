@@ -15,13 +15,21 @@ after such writes. Tracing under ``torch.compile`` builds the tables afresh.
 import torch
 
 
+def _tensors(m, out):
+    out.extend(m._parameters.values())
+    out.extend(m._buffers.values())
+    for child in m._modules.values():
+        if child is not None:
+            _tensors(child, out)
+
+
 def state_key(*modules):
-    """Storage and version of every parameter and buffer of ``modules``."""
-    key = []
+    """Storage and version of every parameter and buffer of ``modules`` (a
+    direct walk of the module dictionaries: this runs on every forward)."""
+    ts = []
     for m in modules:
-        for t in list(m.parameters()) + list(m.buffers()):
-            key.append((t.data_ptr(), t._version, t.device.index))
-    return tuple(key)
+        _tensors(m, ts)
+    return tuple((t.data_ptr(), t._version, t.get_device()) for t in ts if t is not None)
 
 
 def cached(owner, name, key, build):

@@ -132,16 +132,21 @@ class LogicLayer(nn.Module):
                                    conn.k)
         return cand, w, npar
 
+    def records_ok(self):
+        """Whether the forward without gradients runs on per-output records:
+        a plain softmax selection over inputs below 65536 (records hold 16-bit
+        input indices), not a LUT layer."""
+        if self.is_lut or self.in_dim > 65536:
+            return False
+        self._check_supported()
+        return self.node.plain_softmax() and not getattr(self._conn, "ste", False)
+
     def record_spec(self):
         """``(cand, conn, raw, in_dim, node_kind, order)`` for
-        ``ops.fc_soft_records`` when the forward without gradients is a plain
-        softmax selection, else ``None`` (also for LUT layers)."""
-        if self.is_lut or self.in_dim > 65536:   # records hold 16-bit input indices
+        ``ops.fc_soft_records`` when :meth:`records_ok`, else ``None``."""
+        if not self.records_ok():
             return None
-        self._check_supported()
         conn = self._conn
-        if not self.node.plain_softmax() or getattr(conn, "ste", False):
-            return None
         raw_conn = None if isinstance(conn, FixedConnectome) else conn.conn
         cand = conn.candidates_i32()
         return cand, raw_conn, self.node.raw(), self.in_dim, self.node.kind, self.gather_order(cand)
@@ -181,11 +186,10 @@ class LogicLayer(nn.Module):
                                    torch.sigmoid(self.node.logits), self.node.hybrid)
         self._check_supported()
         grad = _needs_grad(self, x)
-        spec = None if grad else self.record_spec()
-        if spec is not None:
+        if not grad and self.records_ok():
             K = self.n_candidates
             rec = derived.cached(self, "_derived_records", (derived.state_key(self), K),
-                                 lambda: ops.fc_soft_records([spec], K)[0])
+                                 lambda: ops.fc_soft_records([self.record_spec()], K)[0])
             return ops.fc_soft_rec(x, rec, self.in_dim, self.out_dim, K, self.node.kind,
                                    self._inv_tau())
         cand, w, npar = self.soft_params(grad)

@@ -32,13 +32,13 @@ def _soft_fc_stack(layers, head, x, wire_r):
     """Soft forward of arity-2 FC layers + GroupSum head on records (no
     gradients). Returns ``None`` when a layer needs the autograd path (a
     non-softmax selection) so the caller runs layer by layer."""
-    specs = [layer.record_spec() for layer in layers]
     Ks = {layer.n_candidates for layer in layers}
-    if not layers or any(s is None for s in specs) or len(Ks) != 1:
+    if not layers or not all(layer.records_ok() for layer in layers) or len(Ks) != 1:
         return None
     K = Ks.pop()
-    recs = derived.cached(layers[0], "_derived_net_records", (derived.state_key(*layers), K),
-                          lambda: ops.fc_soft_records(specs, K))
+    recs = derived.cached(
+        layers[0], "_derived_net_records", (derived.state_key(*layers), K),
+        lambda: ops.fc_soft_records([layer.record_spec() for layer in layers], K))
     h = x
     for i, (layer, rec) in enumerate(zip(layers, recs)):
         kind, inv_tau = layer.node.kind, layer._inv_tau()
@@ -70,16 +70,17 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
                 yp[:wire_r] = xp[:wire_r]
             xp = yp
         return ops.groupsum_packed(xp, B, C)
-    specs = [layer.hard_spec() for layer in layers]
     widths = [layer.out_dim for layer in layers]
-    spw = ops.fc_hard_net_supported(in_dim, widths, C)
+    spw = derived.cached(layers[0], "_derived_net_spw", (in_dim, C, tuple(widths)),
+                         lambda: ops.fc_hard_net_supported(in_dim, widths, C))
     if spw:
-        codes = derived.cached(layers[0], "_derived_net_codes", derived.state_key(*layers),
-                               lambda: ops.fc_hard_codes_net(specs, compact=True))
+        codes = derived.cached(
+            layers[0], "_derived_net_codes", derived.state_key(*layers),
+            lambda: ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True))
         if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
-    codes = ops.fc_hard_codes_net(specs)
+    codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers])
     xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
     for c in codes:
         yp = ops.fc_hard_layer(xp, c)

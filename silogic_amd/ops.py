@@ -27,7 +27,13 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t):
+    """torch's current stream on ``t``'s device, as a raw handle."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.get_device()))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
