@@ -106,23 +106,26 @@ def cpu_baseline(cfg, sd, x_hard, x_soft, gates):
     }
 
 
-def load_traffic():
-    """HBM bytes per launch of the dominant kernels, measured with rocprofv3
-    --pmc FETCH_SIZE / WRITE_SIZE and scaled by the same counters' reading for
-    a plain copy of known size (profiles/hbm_traffic.json; see --kernels-only)."""
+def load_traffic(cfg):
+    """HBM bytes per launch of config ``cfg``'s dominant kernels, measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and scaled by the same counters'
+    reading for a plain copy of known size (profiles/hbm_traffic.json, keyed
+    by config; see --kernels-only)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     if not os.path.exists(path):
         return {}
     with open(path) as fh:
-        return json.load(fh)
+        return json.load(fh).get(f"cfg{cfg}", {})
 
 
 def kernels_only(reps=3):
-    """Workload for counter passes: a 256 MiB copy (calibration), then the
-    fused hard network and one soft hidden layer of config 2, ``reps`` times."""
+    """Workload for counter passes: a 256 MiB copy (calibration), then
+    ``reps`` times each: config 2's fused hard network and one soft hidden
+    layer, config 4's walsh hidden layer, and the first conv block (with its
+    OrPool) of configs 3 and 5, at the bench's batch sizes."""
     import silogic_amd as sl
     from silogic_amd import ops
-    from silogic_amd.synthetic import build_config, config_inputs
+    from silogic_amd.synthetic import BATCHES, build_config, config_inputs
     dev = torch.device("cuda:0")
     src = torch.ones(64 << 20, device=dev)          # 256 MiB
     dst = torch.empty_like(src)
@@ -134,10 +137,20 @@ def kernels_only(reps=3):
         codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
         for _ in range(reps):
             ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
-        x_mid = torch.rand(4096, 10000, device=dev)
-        rec = ops.fc_soft_records([model.layers[1].record_spec()], 8)[0]
-        for _ in range(reps):
-            ops.fc_soft_rec(x_mid, rec, 10000, 10000, 8, ops.GATE16)
+        for cfg in (2, 4):
+            m = model if cfg == 2 else build_config(cfg, sl).eval().to(dev)
+            L = m.layers[1]
+            x_mid = torch.rand(BATCHES[cfg][0], L.in_dim, device=dev)
+            rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
+            for _ in range(reps):
+                ops.fc_soft_rec(x_mid, rec, L.in_dim, L.out_dim, L.n_candidates, L.node.kind,
+                                L._inv_tau())
+        for cfg in (3, 5):
+            m = build_config(cfg, sl).eval().to(dev)
+            x = config_inputs(cfg, BATCHES[cfg][0]).to(dev)
+            conv = m._convs()[0]
+            for _ in range(reps):
+                conv.forward_pooled(x)
     torch.cuda.synchronize()
     log("kernels-only done")
 
@@ -311,7 +324,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
         fn_soft()
         k_soft = _events_ms(fn_soft, reps) / 1e3
     soft_gbs = soft_bytes / k_soft / 1e9
-    traffic = load_traffic() if cfg == 2 else {}
+    traffic = load_traffic(cfg)
     bitops = B_hard * gates / t_hard
 
     res = {
@@ -332,7 +345,8 @@ def measure_config(cfg, steps, warmup, with_cpu):
         tflops = soft_flops / k_soft / 1e12
         soft_roof = {"kernel": name, "bound": "fp32", "achieved": round(tflops, 2),
                      "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+                     "traffic": traffic.get("conv_soft_kernel"),
                      "algorithmic_flops": soft_flops, "algorithmic_bytes": soft_bytes,
                      "hbm_frac": round(soft_gbs / HBM_PEAK_GBS, 4),
                      "avg_kernel_us": round(k_soft * 1e6, 2)}
