@@ -9,9 +9,10 @@
 //     reads are the widest LDS gather gfx950 has; b64 and b32 move fewer
 //     bytes per LDS cycle.
 //   * Lanes walk outputs. Each lane loads its output's 2K candidate indices,
-//     2K weights and 4 node coefficients (144 B at K = 8) with 16-byte loads
-//     and reuses them for all S samples. With the per-output record layout
-//     (slg_fc_soft_records) the 144 B are contiguous.
+//     2K weights and 4 node coefficients with 16-byte loads and reuses them
+//     for all S samples: 144 B at K = 8 from the separate arrays, 112
+//     contiguous bytes from a per-output record (slg_fc_soft_records, the
+//     indices as 16-bit pairs).
 //   * Output stores are coalesced along the output dimension. The fused
 //     GroupSum variant stores nothing per output: it counts (y > 0.5) per
 //     class with a wave ballot + popcount into LDS counters and writes the
