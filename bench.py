@@ -5,7 +5,8 @@ gate16, TopK k=8, GroupSum 10 classes, tau 10), seeded random parameters
 (torch.manual_seed(0), seed=0), synthetic Bernoulli(0.2) inputs. One step =
 ``forward_hard`` on B = 65536 samples (bit-packed circuit, 64 samples per
 word) + soft ``forward`` on the first 4096 of them. Inputs are resident in
-HBM before timing starts.
+HBM before timing starts. HIP events before each part of each step give
+the per-part times (medians over the steps).
 
 ``value`` = hard-circuit Ggate-evals/s = 65536 * 60000 / t_hard (the
 reference's gate count, models.py:103-104); the soft rate is reported beside
@@ -283,22 +284,26 @@ def measure_config(cfg, steps, warmup, with_cpu):
     torch.cuda.synchronize()
 
     # ---- timed region: exactly `steps` steps between synchronisations ----
+    # Each step is forward_hard then the soft forward. An event goes before
+    # each part and one after the last: a step boundary is one event, not
+    # two, since each event's queue marker holds the next kernel back by
+    # about 5 us, which the part after it is charged with.
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i][0].record(stream)
-        with torch.no_grad():
+    with torch.no_grad():
+        for i in range(steps):
+            ev[2 * i].record(stream)
             model.forward_hard(x_hard)
-            ev[i][1].record(stream)
+            ev[2 * i + 1].record(stream)
             model(x_soft)
-            ev[i][2].record(stream)
+        ev[2 * steps].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    t_hard = statistics.median(a.elapsed_time(b) for a, b, _ in ev) / 1e3
-    t_soft = statistics.median(b.elapsed_time(c) for _, b, c in ev) / 1e3
+    t_hard = statistics.median(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)) / 1e3
+    t_soft = statistics.median(ev[2 * i + 1].elapsed_time(ev[2 * i + 2])
+                               for i in range(steps)) / 1e3
     log(f"config {cfg}: step {wall / steps * 1e3:.3f} ms; hard {t_hard * 1e6:.1f} us; "
         f"soft {t_soft * 1e6:.1f} us")
 
@@ -410,7 +415,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the GPU runs at lower clocks after the idle of each config's build:
+    # a timed block after 5 warm-up steps measured up to 20% slower than after 50
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
                     help="measure only BASELINE config N (default: the headline config 2 "
                          "plus a record of every config)")

@@ -29,7 +29,9 @@ def state_key(*modules):
     ts = []
     for m in modules:
         _tensors(m, ts)
-    return tuple((t.data_ptr(), t._version, t.get_device()) for t in ts if t is not None)
+    # device allocations have distinct addresses across devices (one
+    # virtual address space), so the pointer also tells the device apart
+    return tuple((t.data_ptr(), t._version) for t in ts if t is not None)
 
 
 def cached(owner, name, key, build):

@@ -61,7 +61,14 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
     fused into it when the input is at most 1024 features wide; otherwise one
     packed kernel per layer."""
-    if any(layer.is_lut for layer in layers):
+    def plan():
+        widths = [layer.out_dim for layer in layers]
+        lut = any(layer.is_lut for layer in layers)
+        return lut, widths, 0 if lut else ops.fc_hard_net_supported(in_dim, widths, C)
+
+    lut, widths, spw = derived.cached(layers[0], "_derived_net_plan",
+                                      (in_dim, C, tuple(id(layer) for layer in layers)), plan)
+    if lut:
         # LUT layers: one packed kernel per layer (gate or LUT)
         xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
         for layer in layers:
@@ -70,13 +77,11 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
                 yp[:wire_r] = xp[:wire_r]
             xp = yp
         return ops.groupsum_packed(xp, B, C)
-    widths = [layer.out_dim for layer in layers]
-    spw = derived.cached(layers[0], "_derived_net_spw", (in_dim, C, tuple(widths)),
-                         lambda: ops.fc_hard_net_supported(in_dim, widths, C))
     if spw:
         codes = derived.cached(
             layers[0], "_derived_net_codes", derived.state_key(*layers),
-            lambda: ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True))
+            lambda: ops.NetCodes(ops.fc_hard_codes_net([layer.hard_spec() for layer in layers],
+                                                       compact=True)))
         if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)

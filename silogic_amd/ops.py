@@ -523,18 +523,31 @@ def fc_hard_net_supported(in_dim, widths, C):
 ROWS_F32, ROWS_U8, PACKED, PACKED_WORD_MAJOR = 0, 1, 2, 3
 
 
+class NetCodes(list):
+    """Compact per-layer codes of a fused hard network (a list of ``[OUT]``
+    int32 tensors) with their width and pointer arrays for the C ABI, built
+    once: the tensors must not be replaced or resized afterwards."""
+
+    def __init__(self, codes):
+        super().__init__(codes)
+        require_gpu(*self)
+        if any(c.dim() != 1 or c.dtype != torch.int32 or not c.is_contiguous() for c in self):
+            raise ValueError("fc_hard_net: codes must be compact [OUT] int32 codes")
+        self.widths = (ctypes.c_int64 * len(self))(*[c.shape[0] for c in self])
+        self.ptrs = (ctypes.c_void_p * len(self))(*[c.data_ptr() for c in self])
+
+
 def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
     """Depth-fused packed FC network + GroupSum -> logits ``[B, C]``.
 
     ``in_kind``: ROWS_F32 / ROWS_U8 ([B, in_dim], packed inside the kernel),
     PACKED ([in_dim, nw]) or PACKED_WORD_MAJOR ([nw, in_dim]). ``codes``:
-    compact per-layer codes from ``fc_hard_codes_net(..., compact=True)``."""
-    require_gpu(x, *codes)
-    if any(c.dim() != 1 or c.dtype != torch.int32 for c in codes):
-        raise ValueError("fc_hard_net: codes must be compact [OUT] int32 codes")
-    widths = [c.shape[0] for c in codes]
-    w_arr = (ctypes.c_int64 * len(widths))(*widths)
-    c_arr = (ctypes.c_void_p * len(codes))(*[c.data_ptr() for c in codes])
+    compact per-layer codes from ``fc_hard_codes_net(..., compact=True)``
+    (a list of tensors, or a :class:`NetCodes`)."""
+    if not isinstance(codes, NetCodes):
+        codes = NetCodes(codes)
+    require_gpu(x)
+    w_arr, c_arr = codes.widths, codes.ptrs
     out = torch.empty((B, C), device=x.device, dtype=torch.float32)
     _lib.call("slg_fc_hard_net", _p(x), in_kind, B, in_dim, len(codes), w_arr, c_arr, C,
               int(wire_r), _p(out), _stream(x))
