@@ -31,27 +31,39 @@ def _per_layer(v, i):
 def _soft_fc_stack(layers, head, x, wire_r):
     """Soft forward of arity-2 FC layers + GroupSum head on records (no
     gradients). Returns ``None`` when a layer needs the autograd path (a
-    non-softmax selection) so the caller runs layer by layer."""
-    Ks = {layer.n_candidates for layer in layers}
-    if not layers or not all(layer.records_ok() for layer in layers) or len(Ks) != 1:
+    non-softmax selection) so the caller runs layer by layer. The records
+    are built once per parameter version and the launches once per batch
+    shape (``ops.SoftStackPlan``)."""
+    if x.dtype != torch.float32:
+        x = x.float()
+    pkey = derived.state_key(*layers)
+    shape_key = (pkey, tuple(x.shape), tuple(layer.training for layer in layers), id(head),
+                 getattr(head, "feature_ste", None), getattr(head, "tau", None), wire_r)
+
+    def build():
+        Ks = {layer.n_candidates for layer in layers}
+        if not layers or not all(layer.records_ok() for layer in layers) or len(Ks) != 1:
+            return None
+        K = Ks.pop()
+        recs = derived.cached(
+            layers[0], "_derived_net_records", (pkey, K),
+            lambda: ops.fc_soft_records([layer.record_spec() for layer in layers], K))
+        B, IN = x.shape
+        last = layers[-1]
+        w_last = layers[-2].out_dim if len(layers) > 1 else IN    # the last layer's input width
+        fuse = (isinstance(head, GroupSum) and head.feature_ste
+                and not (wire_r and w_last == last.out_dim)
+                and ops.fc_soft_groupsum_supported(B, w_last, last.out_dim, head.num_classes))
+        return ops.SoftStackPlan(
+            [(rec, layer.in_dim, layer.out_dim, K, layer.node.kind, layer._inv_tau())
+             for layer, rec in zip(layers, recs)], B, IN,
+            (head.num_classes, float(head.tau)) if fuse else None, wire_r)
+
+    plan = derived.cached(layers[0], "_derived_soft_plan", shape_key, build)
+    if plan is None:
         return None
-    K = Ks.pop()
-    recs = derived.cached(
-        layers[0], "_derived_net_records", (derived.state_key(*layers), K),
-        lambda: ops.fc_soft_records([layer.record_spec() for layer in layers], K))
-    h = x
-    for i, (layer, rec) in enumerate(zip(layers, recs)):
-        kind, inv_tau = layer.node.kind, layer._inv_tau()
-        if i == len(layers) - 1 and isinstance(head, GroupSum) and head.feature_ste and not (
-                wire_r and h.shape[1] == layer.out_dim) and ops.fc_soft_groupsum_supported(
-                    h.shape[0], h.shape[1], layer.out_dim, head.num_classes):
-            return ops.fc_soft_rec_groupsum(h, rec, layer.in_dim, layer.out_dim, K, kind,
-                                            inv_tau, head.num_classes, head.tau)
-        y = ops.fc_soft_rec(h, rec, layer.in_dim, layer.out_dim, K, kind, inv_tau)
-        if wire_r and h.shape[1] == y.shape[1]:
-            y = torch.cat([h[:, :wire_r], y[:, wire_r:]], dim=1)
-        h = y
-    return head(h)
+    out = plan(x)
+    return out if plan.head is not None else head(out)
 
 
 def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):

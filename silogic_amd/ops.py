@@ -353,6 +353,56 @@ def fc_soft_rec_groupsum(x, rec, in_dim, out_dim, K, node_kind, inv_tau, C, tau)
     return logits
 
 
+class SoftStackPlan:
+    """Launches of a soft FC stack on records without gradients (the layers
+    of one network, the last one fused with the STE GroupSum head when
+    ``head`` is given), prepared once for a batch size and input width:
+    a call allocates the activations and launches, nothing else.
+
+    ``layers``: ``(rec, in_dim, out_dim, K, node_kind, inv_tau)`` per layer;
+    ``head``: ``(C, tau)`` or None; ``wire_r``: wire residual width."""
+
+    def __init__(self, layers, B, IN, head, wire_r):
+        self.B, self.IN, self.wire_r = B, IN, wire_r
+        self.layers = []
+        width = IN
+        for rec, in_dim, out_dim, K, kind, inv_tau in layers:
+            require_gpu(rec)
+            x_like = torch.empty((0, width), device=rec.device)
+            _check_rec(x_like, rec, in_dim, out_dim, K)
+            self.layers.append((rec, ctypes.c_void_p(rec.data_ptr()), int(width), int(in_dim),
+                                int(out_dim), int(K), int(kind), float(inv_tau)))
+            width = out_dim
+        self.head = head
+        self.fwd = _lib.lib().slg_fc_soft_fwd_records
+        self.fwd_head = _lib.lib().slg_fc_soft_fwd_groupsum
+
+    def __call__(self, x):
+        """``x`` [B, IN] float32 -> the last layer's ``[B, OUT]`` activations, or
+        the ``[B, C]`` logits when the head is fused."""
+        if x.shape != (self.B, self.IN) or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"soft stack planned for [{self.B}, {self.IN}] float32 input, "
+                             f"got {tuple(x.shape)} {x.dtype}")
+        h = x.contiguous()
+        st = _stream(h)
+        B, last = self.B, len(self.layers) - 1
+        for i, (_, rec_p, width, in_dim, out_dim, K, kind, inv_tau) in enumerate(self.layers):
+            if i == last and self.head is not None:
+                C, tau = self.head
+                logits = torch.empty((B, C), device=h.device, dtype=torch.float32)
+                _lib.check(self.fwd_head(_p(h), B, width, out_dim, K, rec_p, in_dim, kind,
+                                         inv_tau, C, tau, _p(logits), st),
+                           "slg_fc_soft_fwd_groupsum")
+                return logits
+            y = torch.empty((B, out_dim), device=h.device, dtype=torch.float32)
+            _lib.check(self.fwd(_p(h), B, width, out_dim, K, rec_p, in_dim, kind, inv_tau, _p(y),
+                                0, 0, st), "slg_fc_soft_fwd_records")
+            if self.wire_r and width == out_dim:
+                y = torch.cat([h[:, :self.wire_r], y[:, self.wire_r:]], dim=1)
+            h = y
+        return h
+
+
 # ---------------------------------------------------------------------------
 # GroupSum / OrPool
 # ---------------------------------------------------------------------------
