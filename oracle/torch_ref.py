@@ -224,6 +224,21 @@ def fc_layer_soft(L, sd, x):
     return node_soft(L, sd, select_soft(L, sd, x))
 
 
+def gumbel(shape, device):
+    """The reference's Gumbel draw (nodes.py:46-48)."""
+    u = torch.rand(shape, device=device).clamp_(1e-6, 1 - 1e-6)
+    return -torch.log(-torch.log(u))
+
+
+def fc_layer_soft_gumbel(L, sd, x, g1, g2):
+    """Walsh layer in training with Gumbel-sigmoid smoothing (nodes.py:145-149):
+    ``sigmoid((z + g1 - g2) / tau)`` for given draws ``g1``, ``g2`` [B, out]."""
+    p = L["prefix"]
+    u = 2 * select_soft(L, sd, x) - 1
+    z = (walsh_monomials(u) * sd[p + "node.theta"][None]).sum(2)
+    return torch.sigmoid((z + g1 - g2) * (1.0 / L["node_tau"]))
+
+
 def fc_layer_hard(L, sd, x):
     x = x.to(torch.uint8)                                      # layers.py:131-135
     ops = x[:, hard_indices(L, sd)]

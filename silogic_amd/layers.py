@@ -124,8 +124,9 @@ class LogicLayer(nn.Module):
         plain = self.node.plain_softmax() and not getattr(conn, "ste", False)
         if grad or not plain:
             if self._node_name == "walsh" and not self.node.plain_softmax():
-                raise NotImplementedError("walsh Gumbel smoothing in training is not on the "
-                                          "MI355X path")
+                raise NotImplementedError("walsh Gumbel smoothing adds noise per (sample, "
+                                          "output), which no kernel parameter holds: "
+                                          "LogicLayer.forward runs it")
             return cand, conn.weights(), self.node.kernel_param()
         raw_conn = None if isinstance(conn, FixedConnectome) else conn.conn
         w, npar = ops.fc_soft_prep(raw_conn, self.node.raw(), self.node.kind, self.out_dim,
@@ -173,12 +174,23 @@ class LogicLayer(nn.Module):
     def forward(self, x):
         ops.require_gpu(x)
         ops.check_width(x, self.in_dim)
+        if self._node_name == "walsh" and not self.node.plain_softmax():
+            # Gumbel-sigmoid smoothing in training (nodes.py:145-149): the
+            # kernels return z (arity 2: the gate kernel on z's (a, b)-space
+            # coefficients; arity n: the LUT kernel on z's corner values),
+            # the noise and the sigmoid are torch ops on [B, out]
+            conn = self._conn
+            if self.is_walsh_n:
+                z = ops.fc_lut_soft(x, conn.candidates_i32(), conn.weights(),
+                                    self.node.corner_z(), False)
+            else:
+                self._check_supported()
+                z = ops.fc_soft(x, conn.candidates_i32(), conn.weights(), self.node.coef(),
+                                ops.GATE16, 1.0)
+            return self.node.gumbel_sigmoid(z)
         if self.is_lut:
             conn = self._conn
             if self.is_walsh_n:
-                if not self.node.plain_softmax():
-                    raise NotImplementedError("walsh Gumbel smoothing in training is not on the "
-                                              "MI355X path")
                 z = ops.fc_lut_soft(x, conn.candidates_i32(), conn.weights(),
                                     self.node.corner_z(), False)
                 return torch.sigmoid(z * self.node.inv_tau)

@@ -89,6 +89,14 @@ class Gate16Node(Node):
         self.gate_logits[:, GATE_A] = residual_logit(p)
 
 
+def gumbel_noise(shape, device):
+    """Standard Gumbel samples ``-log(-log u)``, ``u`` uniform from torch's
+    generator clamped to ``[1e-6, 1 - 1e-6]`` (nodes.py:46-48): the same
+    draws as the reference for the same generator state."""
+    u = torch.rand(shape, device=device).clamp_(1e-6, 1 - 1e-6)
+    return -torch.log(-torch.log(u))
+
+
 class WalshNode(Node):
     """Walsh-Hadamard node ``z = sum_i theta_i phi_i(2a-1)``, ``sigmoid(z/tau)``."""
 
@@ -149,6 +157,14 @@ class WalshNode(Node):
 
     def plain_softmax(self):
         return not (self.training and self.gate_select == "gumbel")
+
+    def gumbel_sigmoid(self, z):
+        """Training output with Gumbel-sigmoid smoothing (nodes.py:147-149):
+        ``sigmoid((z + g1 - g2) / tau)`` with two fresh Gumbel draws per
+        element, in the reference's order."""
+        g1 = gumbel_noise(z.shape, z.device)
+        g2 = gumbel_noise(z.shape, z.device)
+        return torch.sigmoid((z + g1 - g2) * self.inv_tau)
 
     def raw(self):
         return self.theta

@@ -298,3 +298,18 @@ def test_planted_wrong_leaf_pairing_is_caught(monkeypatch):
     # caught by the first conv map (the error shrinks through the later layers
     # of a random-init net, so end-to-end soft logits alone would miss it)
     assert (tr["conv/0"] - fx.arrays["conv/0"]).abs().max() > 1e-4
+
+
+def test_oracle_gumbel_draws_follow_the_gumbel_law():
+    """torch_ref.gumbel: -log(-log u) of clamped uniforms has the standard
+    Gumbel mean (Euler-Mascheroni) and variance pi^2 / 6, and re-seeding
+    repeats the draws."""
+    import math
+    torch.manual_seed(3)
+    a = torch_ref.gumbel((200000,), "cpu")
+    torch.manual_seed(3)
+    b = torch_ref.gumbel((200000,), "cpu")
+    assert torch.equal(a, b)
+    assert abs(a.mean().item() - 0.5772156649) < 0.01
+    assert abs(a.var().item() - math.pi ** 2 / 6) < 0.03
+    assert a.max().item() <= -math.log(-math.log(1 - 1e-6)) + 1e-4
