@@ -135,7 +135,8 @@ def kernels_only(reps=3):
     model = build_config(2, sl).eval().to(dev)
     xh = config_inputs(2, 65536).to(dev)
     with torch.no_grad():
-        codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
+        codes = ops.fc_hard_place_net(
+            ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True))
         for _ in range(reps):
             ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
         for cfg in (2, 4):
@@ -317,7 +318,9 @@ def measure_config(cfg, steps, warmup, with_cpu):
             C = model.head.num_classes
             in_dim = x_hard.shape[1]
             if ops.fc_hard_net_supported(in_dim, widths, C) == 64 and in_dim <= 1024:
-                codes = ops.fc_hard_codes_net(specs, compact=True)
+                # the codes forward_hard runs: placed, as LogicNet caches them
+                codes = ops.NetCodes(ops.fc_hard_place_net(ops.fc_hard_codes_net(specs,
+                                                                                 compact=True)))
                 fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, in_dim, codes, C)  # noqa: E731
                 fn_net()
                 k_hard = _events_ms(fn_net, reps) / 1e3

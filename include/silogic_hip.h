@@ -319,6 +319,21 @@ int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw,
 int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
                     const int64_t* widths, const uint32_t* const* codes, int32_t C,
                     int64_t wire_r, float* logits, slg_stream_t stream);
+/* Bank-aware placement of a fused network's outputs (no counterpart in the
+ * reference: a relabelling of LogicNet.forward_hard's circuit, models.py:
+ * 99-101, that leaves the logits unchanged). codes[l] are compact codes
+ * [widths[l]] from slg_fc_hard_prep_net (compact = 1); writes placed[l]
+ * (distinct buffers): for l < n_layers - 1, round_up(widths[l], 32) slots
+ * holding the layer's outputs so that each 32 consecutive slots read
+ * operands of distinct LDS bank classes where the counts allow (unused
+ * slots hold code 0), with the next layer's operands renamed to the slots;
+ * the last layer keeps its order. Pass placed[] with those slot counts as
+ * widths to slg_fc_hard_net (wire_r must be 0). perm_ws: int32 workspace of
+ * widths[0] + .. + widths[n_layers-2] entries (output -> slot). Widths at
+ * most 16384. One workgroup; parameter-sized. */
+int slg_fc_hard_place_net(int32_t n_layers, const int64_t* widths, const uint32_t* const* codes,
+                          uint32_t* const* placed, int32_t* perm_ws, int64_t perm_ws_len,
+                          slg_stream_t stream);
 /* 64 or 32 = samples per workgroup slg_fc_hard_net would use, 0 = unsupported. */
 int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C);
 

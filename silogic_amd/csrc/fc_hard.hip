@@ -707,6 +707,207 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
 }
 
 // ---------------------------------------------------------------------------
+// operand placement for the fused network (bank-aware output order)
+// ---------------------------------------------------------------------------
+// In the fused network a wave's operand reads are ds_read_b64 of random
+// activation words, served per 32-lane half with one cycle per distinct word
+// of each bank class (word index mod 32). A layer's outputs may sit at any
+// slot of its activation buffer as long as the next layer reads them there,
+// so the outputs of every layer but the last are placed so that the 32
+// outputs computed by one half-wave (32 consecutive slots, a "group") read
+// operands of distinct bank classes, as far as the counts allow:
+//  * Latin part: output o with operand classes (ca, cb) and rank k among
+//    the outputs of its (ca, cb) cell (in index order) goes to lane ca of
+//    group r + 32k, r = (cb - ca) mod 32, while that group exists. In every
+//    group lane c then reads a-class c and b-class (g + c) mod 32: no
+//    conflict on either read.
+//  * the rest of a-class c takes the free lane-c slots, first in groups
+//    whose Latin part lacks its b-class, in ascending order;
+//  * what is left fills the remaining free slots in index order.
+// The next layer's operand indices are renamed to the slots; the last layer
+// keeps its order (the GroupSum reads its class blocks). The result is a
+// relabelling of the circuit: the logits are the same bits. Deterministic
+// (stable ranks by sorting, each search in a fixed order). One workgroup
+// walks the layers in order, since each placement renames the next layer's
+// operands.
+constexpr int kPlaceThreads = 1024;
+constexpr int kPlaceMax = 1 << 14;   // outputs per layer (14-bit slots)
+struct PlaceNet {
+  const uint32_t* in[kMaxLayers];    // compact codes, W[l] each
+  uint32_t* out[kMaxLayers];         // placed codes: S[l] = round up(W[l], 32) slots, last W[l]
+  int32_t* perm[kMaxLayers];         // output -> slot, layers 0 .. L-2
+  int W[kMaxLayers];
+  int L;
+};
+
+__device__ inline uint32_t remap_code(const PlaceNet& n, int l, int o) {
+  const uint32_t c = n.in[l][o];
+  uint32_t a = (c >> 14) & 0x3FFFu, b = c & 0x3FFFu;
+  if (l > 0) {   // the prep clamps operands below the input width; kept in range here too
+    const uint32_t lim = (uint32_t)n.W[l - 1] - 1u;
+    a = (uint32_t)n.perm[l - 1][min(a, lim)];
+    b = (uint32_t)n.perm[l - 1][min(b, lim)];
+  }
+  return b | (a << 14) | (c & 0xF0000000u);
+}
+
+__global__ void __launch_bounds__(kPlaceThreads) fc_hard_place_kernel(PlaceNet n) {
+  __shared__ uint32_t keys[kPlaceMax];            // cell << 14 | output, sorted
+  __shared__ int start[1024];                      // first sorted position of each cell
+  __shared__ uint32_t taken[kPlaceMax / 32];       // slot occupied, one bit per lane
+  __shared__ uint32_t bmask[kPlaceMax / 32];       // b-classes of each group's Latin part
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int l = 0; l + 1 < n.L; ++l) {
+    const int W = n.W[l], NG = (W + 31) >> 5, S = NG * 32;
+    int P = 32;
+    while (P < W) P <<= 1;
+    for (int i = tid; i < 1024; i += kPlaceThreads) start[i] = 0;
+    for (int i = tid; i < NG; i += kPlaceThreads) taken[i] = bmask[i] = 0u;
+    for (int s = tid; s < S; s += kPlaceThreads) n.out[l][s] = 0u;   // unused slots: code 0
+    __syncthreads();
+    for (int i = tid; i < P; i += kPlaceThreads) {
+      uint32_t key = 0xFFFFFFFFu;
+      if (i < W) {
+        const uint32_t c = remap_code(n, l, i);
+        const uint32_t cell = (((c >> 14) & 31u) << 5) | (c & 31u);
+        key = (cell << 14) | (uint32_t)i;
+        atomicAdd(&start[cell], 1);
+      }
+      keys[i] = key;
+    }
+    __syncthreads();
+    // bitonic sort of the P keys (ascending: by cell, then by output)
+    for (int k = 2; k <= P; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < P; i += kPlaceThreads) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const uint32_t x = keys[i], y = keys[ixj];
+            if ((x > y) == ((i & k) == 0)) {
+              keys[i] = y;
+              keys[ixj] = x;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // cell counts -> exclusive starts (one thread per cell, Hillis-Steele)
+    {
+      const int cnt = start[tid];
+      __syncthreads();
+      int v = cnt;
+      start[tid] = v;
+      __syncthreads();
+      for (int off = 1; off < 1024; off <<= 1) {
+        const int add = tid >= off ? start[tid - off] : 0;
+        __syncthreads();
+        v += add;
+        start[tid] = v;
+        __syncthreads();
+      }
+      start[tid] = v - cnt;
+      __syncthreads();
+    }
+    // Latin part
+    for (int p = tid; p < W; p += kPlaceThreads) {
+      const uint32_t key = keys[p];
+      const int o = (int)(key & 0x3FFFu), cell = (int)(key >> 14);
+      const int ca = cell >> 5, cb = cell & 31;
+      const int k = p - start[cell], r = (cb - ca) & 31;
+      const int navail = (NG - r + 31) >> 5;
+      if (k < navail) {
+        const int g = r + 32 * k, slot = 32 * g + ca;
+        n.perm[l][o] = slot;
+        n.out[l][slot] = remap_code(n, l, o);
+        atomicOr(&taken[g], 1u << ca);
+        atomicOr(&bmask[g], 1u << cb);
+      } else {
+        n.perm[l][o] = -1;
+      }
+    }
+    __syncthreads();
+    // the rest of a-class c on free lane-c slots (wave w: classes w, w + 16);
+    // only this wave changes lane c's bits of `taken`
+    for (int c = wave; c < 32; c += kPlaceThreads / 64) {
+      const int p0 = start[c * 32], p1 = c == 31 ? W : start[c * 32 + 32];
+      for (int q0 = p0; q0 < p1; q0 += 64) {
+        const int p = q0 + lane;
+        bool over = false;
+        int o = 0, cb = 0;
+        if (p < p1) {
+          const uint32_t key = keys[p];
+          o = (int)(key & 0x3FFFu);
+          const int cell = (int)(key >> 14);
+          cb = cell & 31;
+          const int r = (cb - c) & 31;
+          over = (p - start[cell]) >= ((NG - r + 31) >> 5);
+        }
+        uint64_t m = __ballot(over);
+        while (m) {
+          const int src = __ffsll((long long)m) - 1;
+          m &= m - 1;
+          const int oo = __shfl(o, src), bb = __shfl(cb, src);
+          int best = -1, any = -1;
+          for (int g0 = 0; g0 < NG && best < 0; g0 += 64) {
+            const int g = g0 + lane;
+            const bool fr = g < NG && !((taken[min(g, NG - 1)] >> c) & 1u);
+            const bool nob = fr && !((bmask[min(g, NG - 1)] >> bb) & 1u);
+            const uint64_t mb = __ballot(nob), mf = __ballot(fr);
+            if (mb) best = g0 + __ffsll((long long)mb) - 1;
+            else if (any < 0 && mf) any = g0 + __ffsll((long long)mf) - 1;
+          }
+          const int g = best >= 0 ? best : any;
+          if (g >= 0) {
+            if (lane == 0) {
+              const int slot = 32 * g + c;
+              n.perm[l][oo] = slot;
+              n.out[l][slot] = remap_code(n, l, oo);
+              atomicOr(&taken[g], 1u << c);
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0);   // lane 0's LDS update before the next search
+          __builtin_amdgcn_wave_barrier();
+        }
+      }
+    }
+    __syncthreads();
+    // leftovers (index order) onto the free slots (ascending), by wave 0;
+    // the sorted keys are no longer needed and hold the list
+    if (wave == 0) {
+      int cnt = 0;
+      for (int o0 = 0; o0 < W; o0 += 64) {
+        const int o = o0 + lane;
+        const bool left = o < W && n.perm[l][o] < 0;
+        const uint64_t m = __ballot(left);
+        if (left) keys[cnt + __popcll(m & ((1ull << lane) - 1))] = (uint32_t)o;
+        cnt += __popcll(m);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_wave_barrier();
+      int j = 0;
+      for (int s0 = 0; s0 < S && j < cnt; s0 += 64) {
+        const int s = s0 + lane;
+        const bool fr = s < S && !((taken[min(s >> 5, NG - 1)] >> (s & 31)) & 1u);
+        const uint64_t m = __ballot(fr);
+        const int rk = j + __popcll(m & ((1ull << lane) - 1));
+        if (fr && rk < cnt) {
+          const int o = (int)keys[rk];
+          n.perm[l][o] = s;
+          n.out[l][s] = remap_code(n, l, o);
+        }
+        j += __popcll(m);
+      }
+    }
+    __syncthreads();
+    __threadfence_block();
+  }
+  // last layer: its own order, operands renamed
+  const int l = n.L - 1;
+  for (int o = tid; o < n.W[l]; o += kPlaceThreads) n.out[l][o] = remap_code(n, l, o);
+}
+
+// ---------------------------------------------------------------------------
 // packed GroupSum (layer-wise path): one workgroup per 64-sample word column
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) groupsum_packed_kernel(const uint64_t* __restrict__ xp, int W,
@@ -922,6 +1123,36 @@ int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw, const uint32_
                      as_stream(stream), xin, (int)nw, reinterpret_cast<const uint2*>(codes),
                      (int)OUT, xout);
   SLG_LAUNCH_CHECK("fc_hard_layer");
+  return 0;
+}
+
+int slg_fc_hard_place_net(int32_t n_layers, const int64_t* widths, const uint32_t* const* codes,
+                          uint32_t* const* placed, int32_t* perm_ws, int64_t perm_ws_len,
+                          slg_stream_t stream) {
+  SLG_REQUIRE(widths && codes && placed && (perm_ws || n_layers == 1), SLG_E_ARG,
+              "fc_hard_place_net: null pointer");
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE,
+              "fc_hard_place_net: %d layers", n_layers);
+  PlaceNet n{};
+  n.L = n_layers;
+  int64_t used = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(codes[l] && placed[l] && widths[l] > 0 && widths[l] <= kPlaceMax, SLG_E_SHAPE,
+                "fc_hard_place_net: layer %d width %lld outside 1..%d", l, (long long)widths[l],
+                kPlaceMax);
+    SLG_REQUIRE(codes[l] != placed[l], SLG_E_ARG, "fc_hard_place_net: in place, layer %d", l);
+    n.in[l] = codes[l];
+    n.out[l] = placed[l];
+    n.W[l] = (int)widths[l];
+    if (l + 1 < n_layers) {
+      n.perm[l] = perm_ws + used;
+      used += widths[l];
+    }
+  }
+  SLG_REQUIRE(used <= perm_ws_len, SLG_E_ARG, "fc_hard_place_net: workspace of %lld ints, %lld needed",
+              (long long)perm_ws_len, (long long)used);
+  hipLaunchKernelGGL(fc_hard_place_kernel, dim3(1), dim3(kPlaceThreads), 0, as_stream(stream), n);
+  SLG_LAUNCH_CHECK("fc_hard_place");
   return 0;
 }
 

@@ -90,10 +90,14 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
             xp = yp
         return ops.groupsum_packed(xp, B, C)
     if spw:
-        codes = derived.cached(
-            layers[0], "_derived_net_codes", derived.state_key(*layers),
-            lambda: ops.NetCodes(ops.fc_hard_codes_net([layer.hard_spec() for layer in layers],
-                                                       compact=True)))
+        def build():
+            codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True)
+            # bank-aware output order (the logits are the same bits); the
+            # wire residual copies inputs by position, so it keeps the order
+            return ops.NetCodes(codes if wire_r else ops.fc_hard_place_net(codes))
+
+        codes = derived.cached(layers[0], "_derived_net_codes",
+                               (derived.state_key(*layers), bool(wire_r)), build)
         if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)

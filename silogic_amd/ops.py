@@ -573,6 +573,27 @@ def fc_hard_net_supported(in_dim, widths, C):
 ROWS_F32, ROWS_U8, PACKED, PACKED_WORD_MAJOR = 0, 1, 2, 3
 
 
+def fc_hard_place_net(codes):
+    """Bank-aware placement of a fused network's compact codes
+    (``slg_fc_hard_place_net``): every layer but the last becomes
+    ``round_up(OUT, 32)`` slots with the next layer's operands renamed; the
+    logits of ``fc_hard_net`` are unchanged. Returns the placed codes."""
+    require_gpu(*codes)
+    if any(c.dim() != 1 or c.dtype != torch.int32 for c in codes):
+        raise ValueError("fc_hard_place_net: codes must be compact [OUT] int32 codes")
+    codes = [c.contiguous() for c in codes]
+    L = len(codes)
+    widths = [c.shape[0] for c in codes]
+    dev = codes[0].device
+    placed = [torch.empty(((w + 31) // 32 * 32 if l + 1 < L else w,), device=dev,
+                          dtype=torch.int32) for l, w in enumerate(widths)]
+    n_ws = max(1, sum(widths[:-1]))
+    ws = torch.empty(n_ws, device=dev, dtype=torch.int32)
+    _lib.call("slg_fc_hard_place_net", L, (ctypes.c_int64 * L)(*widths), _ptrs(codes),
+              _ptrs(placed), _p(ws), n_ws, _stream(codes[0]))
+    return placed
+
+
 class NetCodes(list):
     """Compact per-layer codes of a fused hard network (a list of ``[OUT]``
     int32 tensors) with their width and pointer arrays for the C ABI, built
