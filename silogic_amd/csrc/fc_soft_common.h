@@ -31,6 +31,14 @@ __device__ inline void fma_acc(VT& acc, float w, VT v) {
 template <typename T> __device__ inline T zero_vec() { return (T)0.0f; }
 
 __device__ inline float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
+// The per-(sample, output) sigmoid of the walsh node: 1 / (1 + 2^(-z log2 e))
+// with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp
+// each, against some twenty instructions for expf and an IEEE divide). Large
+// |z| saturates to exactly 0 or 1 as the divide form does.
+__device__ inline float sigmoid_hw(float z) {
+  const float e = __builtin_amdgcn_exp2f(z * -1.4426950408889634f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 template <int V> __device__ inline typename vecf<V>::t make_vec(const float (&e)[V]);
 template <> __device__ inline float make_vec<1>(const float (&e)[1]) { return e[0]; }
@@ -106,7 +114,7 @@ __device__ inline float node_eval(float a, float b, const float4& p, float inv_t
   if constexpr (NODE == SLG_NODE_GATE16) {
     return p.x + p.y * a + p.z * b + p.w * (a * b);
   } else if constexpr (NODE == SLG_NODE_WALSH) {
-    return sigmoidf_((p.x + p.y * a + p.z * b + p.w * (a * b)) * inv_tau);
+    return sigmoid_hw((p.x + p.y * a + p.z * b + p.w * (a * b)) * inv_tau);
   } else {
     // corners P = 0:(0,0) 1:(1,0) 2:(0,1) 3:(1,1) (bit j of P = slot j)
     const float ua = 1.0f - a, ub = 1.0f - b;
