@@ -579,10 +579,14 @@ static int launch_soft_node(const SoftArgs& a, hipStream_t st) {
 // tile takes the largest power of two <= 8 whose rows fit 160 KB of LDS less
 // 1 KB for the fused head's counters (4 for narrow inputs, where more,
 // smaller workgroups per CU win).
-static int pick_tile(int64_t IN, int requested) {
+static int pick_tile(int64_t IN, int requested, int64_t B = INT64_MAX) {
   if (requested > 0) return requested;
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024) - 1024;
   if (IN <= 1280) return 4;
+  // small batches: fewer than two 8-sample tiles per CU leave most of the
+  // chip idle, 4-sample tiles double the workgroups (B = 256, IN = 2000:
+  // 13.1 -> 8.6 us per layer)
+  if (IN * 16 <= cap && B < 16 * (int64_t)device_cus()) return 4;
   for (int s : {8, 4, 2, 1})
     if (IN * s * 4 <= cap) return s;
   return 0;
@@ -665,7 +669,7 @@ static int fc_soft_dispatch(SoftArgs a, int node_kind, hipStream_t st) {
                 (long long)(device_lds_bytes() / 4));
     return fc_soft_wide(a, node_kind, st);
   }
-  a.S = pick_tile(a.IN, a.S);
+  a.S = pick_tile(a.IN, a.S, a.B);
   SLG_REQUIRE(a.S > 0 && (int64_t)a.IN * a.S * 4 <= device_lds_bytes(), SLG_E_SHAPE,
               "fc_soft: IN=%lld does not fit LDS", (long long)a.IN);
   a.threads = pick_threads(a.IN, a.S, a.threads);
@@ -1060,7 +1064,7 @@ int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C
   if (B >= (1LL << 31) || IN >= (1LL << 28) || OUT >= (1LL << 31)) return 0;
   SoftArgs a{};
   a.B = B; a.IN = IN; a.OUT = OUT;
-  a.S = pick_tile(IN, 0);
+  a.S = pick_tile(IN, 0, B);
   if (a.S <= 0 || IN * a.S * 4 + (int64_t)a.S * C * 4 > device_lds_bytes()) return 0;
   int64_t n_chunks, chunk;
   soft_grid(a, &n_chunks, &chunk);
