@@ -147,6 +147,24 @@ int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT,
                              const float* rec, int64_t rec_in_dim, int32_t node_kind,
                              float inv_tau, int32_t C, float tau, float* logits,
                              slg_stream_t stream);
+/* A network of soft FC layers on records in one launch (the soft forward of
+ * LogicNet / WARPNet, models.py:96-101, for narrow layers and small
+ * batches): rec[l] from slg_fc_soft_records for in_dim[l] inputs, layer l
+ * with out_dim[l] outputs, all layers of one node kind, K candidates and
+ * inv_tau. x [B, IN] fp32 (IN >= in_dim[0]). A workgroup takes 4 samples
+ * through every layer with the activations in LDS; each layer computes as
+ * slg_fc_soft_fwd_records does (the same bits). C > 0: the last layer feeds
+ * the STE GroupSum head and out = logits [B, C] (counts of y > 0.5 / tau);
+ * C = 0: out = the last layer's activations [B, out_dim[n_layers-1]].
+ * SLG_E_UNSUPPORTED when the widths do not fit LDS. */
+int slg_fc_soft_net_records(const float* x, int64_t B, int64_t IN, int32_t n_layers,
+                            const float* const* rec, const int64_t* in_dim,
+                            const int64_t* out_dim, int32_t K, int32_t node_kind, float inv_tau,
+                            int32_t C, float tau, float* out, slg_stream_t stream);
+/* 1 when slg_fc_soft_net_records takes these shapes and is the faster path
+ * (batches below two 8-sample tiles per CU), else 0. */
+int slg_fc_soft_net_supported(int64_t B, int64_t IN, int32_t n_layers, const int64_t* out_dim,
+                              int32_t K, int32_t C);
 /* 1 if slg_fc_soft_fwd_groupsum runs this shape (one workgroup holds every
  * output of its sample tile), else 0. */
 int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C);

@@ -30,6 +30,9 @@ SIGNATURES = {
     "slg_fc_soft_fwd_groupsum": (C.c_int, [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _F32,
                                            _I32, _F32, _P, _P]),
     "slg_fc_soft_groupsum_supported": (C.c_int, [_I64, _I64, _I64, _I32]),
+    "slg_fc_soft_net_supported": (C.c_int, [_I64, _I64, _I32, _P, _I32, _I32]),
+    "slg_fc_soft_net_records": (C.c_int, [_P, _I64, _I64, _I32, _P, _P, _P, _I32, _I32, _F32, _I32,
+                                          _F32, _P, _P]),
     "slg_groupsum_soft": (C.c_int, [_P, _I64, _I64, _I32, _F32, _I32, _P, _P]),
     "slg_groupsum_hard": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P]),
     "slg_orpool": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P]),

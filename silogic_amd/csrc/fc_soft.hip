@@ -396,6 +396,136 @@ fc_soft_rec_kernel(const float* __restrict__ x, int B, int IN, int OUT,
 }
 
 // ---------------------------------------------------------------------------
+// A whole narrow network in one launch (small batches)
+// ---------------------------------------------------------------------------
+// With few samples a launch per layer is mostly latency: staging, record
+// loads and the launch itself. Here a workgroup takes 4 samples through
+// every layer: the activations stay in LDS (two buffers of float4 slots, one
+// per input, ping-ponged), each layer reads its records as the records
+// kernel does and accumulates in the same order (the same bits per layer),
+// and the last layer either writes its activations or, with the STE GroupSum
+// head, only the per-class counts (wave ballots into LDS counters, integers,
+// so exact) / tau.
+constexpr int kMaxNetLayers = 16;
+constexpr int kNetSoftThreads = 1024;
+struct SoftNetDesc {
+  const float* rec[kMaxNetLayers];
+  int out_dim[kMaxNetLayers];
+  int L, K, maxw;   // maxw: float4 slots per activation buffer
+  float inv_tau;
+};
+
+template <int NODE, int KC, bool HEAD>
+__global__ void __launch_bounds__(kNetSoftThreads)
+fc_soft_net_kernel(const float* __restrict__ x, int B, int IN, SoftNetDesc d,
+                   float* __restrict__ y, HeadArgs hd) {
+  constexpr int KM = KC > 0 ? KC : 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  f32x4* cur = reinterpret_cast<f32x4*>(smem);
+  f32x4* nxt = cur + d.maxw;
+  unsigned* cnt = reinterpret_cast<unsigned*>(cur + 2 * d.maxw);
+  const int K = KC > 0 ? KC : d.K;
+  const int b0 = blockIdx.x * 4;
+  const int lane = threadIdx.x & 63;
+  if constexpr (HEAD) {
+    for (int t = threadIdx.x; t < 4 * hd.C; t += blockDim.x) cnt[t] = 0u;
+  }
+  stage_rows<4, true>(cur, x, B, IN, b0);
+  __syncthreads();
+  for (int l = 0; l < d.L; ++l) {
+    const int OUT = d.out_dim[l];
+    const bool last = l + 1 == d.L;
+    ParamView pv{};
+    pv.rec = d.rec[l];
+    // whole waves iterate (the head's ballots need every lane)
+    const int n_iter = (OUT + (int)blockDim.x - 1) / (int)blockDim.x;
+    for (int it = 0; it < n_iter; ++it) {
+      const int o = it * (int)blockDim.x + (int)threadIdx.x;
+      const bool valid = o < OUT;
+      FcParams<KM> P;
+      load_params<KC, KM, true>(P, min(o, OUT - 1), K, pv);
+      f32x4 A = zero_vec<f32x4>(), Bv = zero_vec<f32x4>();
+#pragma unroll
+      for (int k = 0; k < KM; ++k)
+        if (KC > 0 || k < K) fma_acc(A, P.fa[k], cur[P.ia[k]]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < KM; ++k)
+        if (KC > 0 || k < K) fma_acc(Bv, P.fb[k], cur[P.ib[k]]);
+      float yv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) yv[v] = node_eval<NODE>(A[v], Bv[v], P.p, d.inv_tau);
+      if (!last) {
+        if (valid) nxt[o] = f32x4{yv[0], yv[1], yv[2], yv[3]};
+      } else if constexpr (HEAD) {
+        const int c = valid ? o / hd.per : -1;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const bool hit = valid && b0 + s < B && yv[s] > 0.5f;
+          uint64_t todo = __ballot(valid);
+          while (todo) {   // the classes this wave's outputs fall in, in order
+            const int cc = __shfl(c, __ffsll((long long)todo) - 1);
+            const uint64_t mine = __ballot(c == cc);
+            const unsigned n = (unsigned)__popcll(__ballot(hit && c == cc));
+            if (lane == 0 && n) atomicAdd(&cnt[s * hd.C + cc], n);
+            todo &= ~mine;
+          }
+        }
+      } else {
+        if (valid) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            if (b0 + s < B) y[(int64_t)(b0 + s) * OUT + o] = yv[s];
+        }
+      }
+    }
+    __syncthreads();
+    f32x4* t = cur;
+    cur = nxt;
+    nxt = t;
+  }
+  if constexpr (HEAD) {
+    for (int t = threadIdx.x; t < 4 * hd.C; t += blockDim.x) {
+      const int s = t / hd.C, c = t % hd.C;
+      if (b0 + s < B) hd.logits[(int64_t)(b0 + s) * hd.C + c] = (float)cnt[t] / hd.tau;
+    }
+  }
+}
+
+// LDS bytes of fc_soft_net_kernel for the widths, or 0 when they do not fit.
+static int64_t soft_net_lds(int64_t IN, int L, const int64_t* out_dim, int C) {
+  int64_t maxw = IN;
+  for (int l = 0; l < L; ++l) maxw = std::max<int64_t>(maxw, out_dim[l]);
+  const int64_t bytes = 2 * maxw * 16 + (int64_t)4 * std::max(C, 0) * 4;
+  return bytes <= std::min<int64_t>(device_lds_bytes(), 160 * 1024) ? bytes : 0;
+}
+
+template <int NODE, int KC, bool HEAD>
+static int launch_soft_net(const float* x, int64_t B, int64_t IN, const SoftNetDesc& d, float* y,
+                           const HeadArgs& hd, size_t lds, hipStream_t st) {
+  auto kern = fc_soft_net_kernel<NODE, KC, HEAD>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("fc_soft_net: cannot reserve %zu B LDS: %s", lds, hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(B, 4)), dim3(kNetSoftThreads), lds, st, x, (int)B,
+                     (int)IN, d, y, hd);
+  SLG_LAUNCH_CHECK("fc_soft_net");
+  return 0;
+}
+
+template <int NODE, bool HEAD>
+static int soft_net_node(const float* x, int64_t B, int64_t IN, const SoftNetDesc& d, float* y,
+                         const HeadArgs& hd, size_t lds, hipStream_t st) {
+  if (d.K == 8) return launch_soft_net<NODE, 8, HEAD>(x, B, IN, d, y, hd, lds, st);
+  return launch_soft_net<NODE, 0, HEAD>(x, B, IN, d, y, hd, lds, st);
+}
+
+// ---------------------------------------------------------------------------
 // Inputs wider than LDS: slab staging
 // ---------------------------------------------------------------------------
 // A workgroup owns 4 samples and one output per thread. The rows are staged
@@ -1057,6 +1187,74 @@ int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, 
   SoftArgs a{x, B, IN, OUT, K, records_view(rec), inv_tau, out, tile_samples, threads,
              HeadArgs{nullptr, 0, 0, 1.0f}};
   return fc_soft_dispatch(a, node_kind, as_stream(stream));
+}
+
+int slg_fc_soft_net_supported(int64_t B, int64_t IN, int32_t n_layers, const int64_t* out_dim,
+                              int32_t K, int32_t C) {
+  if (B <= 0 || B >= (1LL << 31) || IN <= 0 || IN > 65536 || !out_dim || n_layers < 1 ||
+      n_layers > kMaxNetLayers || K < 1 || K > 16 || C < 0)
+    return 0;
+  for (int l = 0; l < n_layers; ++l)
+    if (out_dim[l] <= 0 || out_dim[l] > 65536) return 0;
+  if (C > 0 && out_dim[n_layers - 1] % C != 0) return 0;
+  if (!soft_net_lds(IN, n_layers, out_dim, C)) return 0;
+  // a launch per layer fills the chip once the batch gives two 8-sample
+  // tiles per CU; below that one launch for the network is faster
+  return B < 16 * (int64_t)device_cus() ? 1 : 0;
+}
+
+int slg_fc_soft_net_records(const float* x, int64_t B, int64_t IN, int32_t n_layers,
+                            const float* const* rec, const int64_t* in_dim,
+                            const int64_t* out_dim, int32_t K, int32_t node_kind, float inv_tau,
+                            int32_t C, float tau, float* out, slg_stream_t stream) {
+  SLG_REQUIRE(rec && in_dim && out_dim && (out || B == 0) && (x || B == 0), SLG_E_ARG,
+              "fc_soft_net: null pointer");
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxNetLayers, SLG_E_SHAPE, "fc_soft_net: %d layers",
+              n_layers);
+  SLG_REQUIRE(K >= 1 && K <= 16 && B >= 0 && B < (1LL << 31) && IN > 0 && IN <= 65536 && C >= 0,
+              SLG_E_SHAPE, "fc_soft_net: bad sizes");
+  SLG_REQUIRE(node_kind >= 0 && node_kind <= 2, SLG_E_ARG, "fc_soft_net: node_kind %d", node_kind);
+  SoftNetDesc d{};
+  d.L = n_layers;
+  d.K = K;
+  d.inv_tau = inv_tau;
+  int64_t width = IN, maxw = IN;
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(rec[l] && ((uintptr_t)rec[l] % 16) == 0, SLG_E_ARG,
+                "fc_soft_net: records of layer %d null or misaligned", l);
+    SLG_REQUIRE(out_dim[l] > 0 && out_dim[l] <= 65536, SLG_E_SHAPE,
+                "fc_soft_net: layer %d width %lld", l, (long long)out_dim[l]);
+    // records hold indices below their layer's in_dim: the input must be
+    // at least that wide (the layer reads it by index)
+    SLG_REQUIRE(in_dim[l] > 0 && in_dim[l] <= width, SLG_E_SHAPE,
+                "fc_soft_net: layer %d reads %lld inputs of %lld", l, (long long)in_dim[l],
+                (long long)width);
+    d.rec[l] = rec[l];
+    d.out_dim[l] = (int)out_dim[l];
+    width = out_dim[l];
+    maxw = std::max(maxw, width);
+  }
+  SLG_REQUIRE(C == 0 || out_dim[n_layers - 1] % C == 0, SLG_E_SHAPE,
+              "fc_soft_net: last width %lld not divisible by %d classes",
+              (long long)out_dim[n_layers - 1], C);
+  const int64_t lds = soft_net_lds(IN, n_layers, out_dim, C);
+  SLG_REQUIRE(lds > 0, SLG_E_UNSUPPORTED, "fc_soft_net: widths do not fit LDS");
+  d.maxw = (int)maxw;
+  if (B == 0) return 0;
+  HeadArgs hd{out, C, C > 0 ? (int)(out_dim[n_layers - 1] / C) : 0, tau};
+  hipStream_t st = as_stream(stream);
+  const bool head = C > 0;
+  switch (node_kind) {
+    case SLG_NODE_GATE16:
+      return head ? soft_net_node<SLG_NODE_GATE16, true>(x, B, IN, d, nullptr, hd, lds, st)
+                  : soft_net_node<SLG_NODE_GATE16, false>(x, B, IN, d, out, hd, lds, st);
+    case SLG_NODE_WALSH:
+      return head ? soft_net_node<SLG_NODE_WALSH, true>(x, B, IN, d, nullptr, hd, lds, st)
+                  : soft_net_node<SLG_NODE_WALSH, false>(x, B, IN, d, out, hd, lds, st);
+    default:
+      return head ? soft_net_node<SLG_NODE_MULTILINEAR2, true>(x, B, IN, d, nullptr, hd, lds, st)
+                  : soft_net_node<SLG_NODE_MULTILINEAR2, false>(x, B, IN, d, out, hd, lds, st);
+  }
 }
 
 int slg_fc_soft_groupsum_supported(int64_t B, int64_t IN, int64_t OUT, int32_t C) {

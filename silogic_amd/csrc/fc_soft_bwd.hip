@@ -46,7 +46,7 @@ __device__ inline void node_grad(float a, float b, float g, const float4& p, flo
     float gz = g;
     if constexpr (NODE == SLG_NODE_WALSH) {
       // y = sigmoid(z * inv_tau), z = c0 + c1 a + c2 b + c3 ab (warp.py:14-31)
-      const float y = sigmoid_hw((p.x + p.y * a + p.z * b + p.w * (a * b)) * inv_tau);
+      const float y = sigmoid_hw(bilinear(a, b, p) * inv_tau);
       gz = g * (y * (1.0f - y)) * inv_tau;
     }
     gp[0] = gz;

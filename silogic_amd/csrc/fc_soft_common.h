@@ -108,17 +108,23 @@ __device__ inline void stage_rows(typename vecf<V>::t* __restrict__ dst,
 
 // Node evaluation on the two gathered operands (silogic/nodes.py:86-91 for
 // gate16, the warp_logic form of kernels/warp.py:14-31 for walsh,
-// nodes.py:174-178 with n = 2 for multilinear).
+// nodes.py:174-178 with n = 2 for multilinear). Written as explicit fmaf
+// chains, so every kernel that evaluates a node (per layer, whole network,
+// wide rows, backward recompute) rounds it the same way whatever the
+// compiler would contract.
+__device__ inline float bilinear(float a, float b, const float4& p) {
+  return fmaf(p.w, a * b, fmaf(p.z, b, fmaf(p.y, a, p.x)));
+}
 template <int NODE>
 __device__ inline float node_eval(float a, float b, const float4& p, float inv_tau) {
   if constexpr (NODE == SLG_NODE_GATE16) {
-    return p.x + p.y * a + p.z * b + p.w * (a * b);
+    return bilinear(a, b, p);
   } else if constexpr (NODE == SLG_NODE_WALSH) {
-    return sigmoid_hw((p.x + p.y * a + p.z * b + p.w * (a * b)) * inv_tau);
+    return sigmoid_hw(bilinear(a, b, p) * inv_tau);
   } else {
     // corners P = 0:(0,0) 1:(1,0) 2:(0,1) 3:(1,1) (bit j of P = slot j)
     const float ua = 1.0f - a, ub = 1.0f - b;
-    return (((ua * ub) * p.x + (a * ub) * p.y) + (ua * b) * p.z) + (a * b) * p.w;
+    return fmaf(a * b, p.w, fmaf(ua * b, p.z, fmaf(a * ub, p.y, (ua * ub) * p.x)));
   }
 }
 

@@ -376,6 +376,20 @@ class SoftStackPlan:
         self.head = head
         self.fwd = _lib.lib().slg_fc_soft_fwd_records
         self.fwd_head = _lib.lib().slg_fc_soft_fwd_groupsum
+        # narrow layers and a small batch: the whole stack in one launch
+        # (slg_fc_soft_net_records), activations kept in LDS
+        L = len(self.layers)
+        kinds = {t[6] for t in self.layers}
+        taus = {t[7] for t in self.layers}
+        Ks = {t[5] for t in self.layers}
+        out_arr = (ctypes.c_int64 * L)(*[t[4] for t in self.layers])
+        C = head[0] if head is not None else 0
+        self.net = None
+        if (not wire_r and len(kinds) == 1 and len(taus) == 1 and len(Ks) == 1
+                and _lib.lib().slg_fc_soft_net_supported(B, IN, L, out_arr, Ks.pop(), C)):
+            self.net = ((ctypes.c_void_p * L)(*[t[1].value for t in self.layers]),
+                        (ctypes.c_int64 * L)(*[t[3] for t in self.layers]), out_arr)
+        self.fwd_net = _lib.lib().slg_fc_soft_net_records
 
     def __call__(self, x):
         """``x`` [B, IN] float32 -> the last layer's ``[B, OUT]`` activations, or
@@ -386,6 +400,19 @@ class SoftStackPlan:
         h = x.contiguous()
         st = _stream(h)
         B, last = self.B, len(self.layers) - 1
+        if self.net is not None:
+            recs, ins, outs = self.net
+            _, _, _, _, out_dim, K, kind, inv_tau = self.layers[-1]
+            if self.head is not None:
+                C, tau = self.head
+                res = torch.empty((B, C), device=h.device, dtype=torch.float32)
+            else:
+                C, tau = 0, 1.0
+                res = torch.empty((B, out_dim), device=h.device, dtype=torch.float32)
+            _lib.check(self.fwd_net(_p(h), B, self.IN, last + 1, recs, ins, outs, K, kind,
+                                    inv_tau, C, float(tau), _p(res), st),
+                       "slg_fc_soft_net_records")
+            return res
         for i, (_, rec_p, width, in_dim, out_dim, K, kind, inv_tau) in enumerate(self.layers):
             if i == last and self.head is not None:
                 C, tau = self.head
