@@ -227,6 +227,21 @@ def dominant_soft_kernel(cfg, model, B_soft, x_soft, dev):
     OrPool (FP32-bound: flops, with its bytes beside)."""
     from silogic_amd import ops
     if hasattr(model, "layers"):
+        with torch.no_grad():
+            model(x_soft)                      # builds (or reuses) the forward's launch plan
+        slot = model.layers[0].__dict__.get("_derived_soft_plan")
+        plan = slot[1] if slot else None
+        if plan is not None and plan.net is not None:
+            # small batch, narrow layers: the forward is one launch for the
+            # whole network (with its head); that launch is the kernel
+            K = model.layers[0].n_candidates
+            fn = lambda: plan(x_soft)  # noqa: E731
+            C = model.head.num_classes
+            nbytes = (B_soft * (x_soft.shape[1] + C) * 4 +
+                      sum(l.out_dim * 16 * ops.record_quads(K) for l in model.layers))
+            name = (f"fc_soft_net_kernel ({len(model.layers)} layers + GroupSum, "
+                    f"{model.layers[0]._node_name}, K={K}, B={B_soft})")
+            return name, fn, nbytes, None
         L = model.layers[1] if len(model.layers) > 1 else model.layers[0]
         x_mid = torch.rand(B_soft, L.in_dim, device=dev)
         rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
