@@ -51,13 +51,18 @@ def _soft_fc_stack(layers, head, x, wire_r):
         B, IN = x.shape
         last = layers[-1]
         w_last = layers[-2].out_dim if len(layers) > 1 else IN    # the last layer's input width
-        fuse = (isinstance(head, GroupSum) and head.feature_ste
-                and not (wire_r and w_last == last.out_dim)
-                and ops.fc_soft_groupsum_supported(B, w_last, last.out_dim, head.num_classes))
-        return ops.SoftStackPlan(
-            [(rec, layer.in_dim, layer.out_dim, K, layer.node.kind, layer._inv_tau())
-             for layer, rec in zip(layers, recs)], B, IN,
-            (head.num_classes, float(head.tau)) if fuse else None, wire_r)
+        ste = (isinstance(head, GroupSum) and head.feature_ste
+               and not (wire_r and w_last == last.out_dim))
+        spec = [(rec, layer.in_dim, layer.out_dim, K, layer.node.kind, layer._inv_tau())
+                for layer, rec in zip(layers, recs)]
+        head_args = (head.num_classes, float(head.tau)) if ste else None
+        plan = ops.SoftStackPlan(spec, B, IN, head_args, wire_r)
+        # a launch per layer fuses the head only where one workgroup holds
+        # every output of its tile; the one-launch network always can
+        if ste and plan.net is None and not ops.fc_soft_groupsum_supported(
+                B, w_last, last.out_dim, head.num_classes):
+            plan = ops.SoftStackPlan(spec, B, IN, None, wire_r)
+        return plan
 
     plan = derived.cached(layers[0], "_derived_soft_plan", shape_key, build)
     if plan is None:
