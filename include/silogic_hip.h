@@ -354,6 +354,35 @@ int slg_fc_hard_place_net(int32_t n_layers, const int64_t* widths, const uint32_
                           slg_stream_t stream);
 /* 64 or 32 = samples per workgroup slg_fc_hard_net would use, 0 = unsupported. */
 int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C);
+/* Slots per layer (MAXO * 1024) of the type-uniform layout below for a
+ * network of inputs IN0 (at most 1024) and these widths, or 0 when it does
+ * not apply (a 64-sample column must fit LDS). */
+int64_t slg_fc_hard_type_slots(int64_t IN0, int32_t n_layers, const int64_t* widths);
+/* Type-uniform placement of a fused network's outputs (no counterpart in the
+ * reference: a relabelling of LogicNet.forward_hard's circuit, models.py:
+ * 99-101, that leaves the logits unchanged). codes[l] are compact codes
+ * [widths[l]] from slg_fc_hard_prep_net (compact = 1). Writes, per layer,
+ * placed[l] of S = slg_fc_hard_type_slots() slots (slot j*1024 + t stored at
+ * t*(S/1024) + j) and a plan row (plan[l*18 ..]: U, rows, then a truth
+ * table per wave): for every layer but the last, rows 0..U-1 hold in each
+ * 64-slot wave row outputs of one gate type (codes (a << 16) | b with word
+ * indices of the two activation buffers) and the remaining rows compact
+ * codes; within that, each 32 consecutive slots read operands of distinct
+ * LDS bank classes where the counts allow. The last layer keeps its order
+ * (compact codes, operands renamed; plan row U = 0). perm_ws: int32
+ * workspace of widths[0] + .. + widths[n_layers-2] entries. One workgroup;
+ * parameter-sized. */
+int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* widths,
+                               const uint32_t* const* codes, uint32_t* const* placed,
+                               int32_t* plan, int32_t* perm_ws, int64_t perm_ws_len,
+                               slg_stream_t stream);
+/* slg_fc_hard_net (in_kind 0 or 1, no wire residual) on the placed codes and
+ * plan of slg_fc_hard_type_place_net; widths are the layers' widths, as
+ * given to the placement. Same logits, bit for bit. No counterpart in the
+ * reference beyond slg_fc_hard_net's. */
+int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
+                          const int64_t* widths, const uint32_t* const* codes, const int32_t* plan,
+                          int32_t C, float* logits, slg_stream_t stream);
 
 /* Packed GroupSum.forward_hard on xp [W,nw] (W % C == 0): logits [B,C] fp32
  * raw counts (ops.py:66-104 without the /tau, as heads.py:41-45). */

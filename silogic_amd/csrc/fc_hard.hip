@@ -290,6 +290,7 @@ struct NetDesc {
   int width[kMaxLayers];
   int n_layers, in0, C, wire_r;
   int maxw;  // words per activation buffer: MAXO * 1024 (every row of every layer)
+  const int32_t* plan;  // type-uniform layout ([n_layers][kPlanStride]), or null
 };
 
 // Codes of this thread's outputs o = tid + j*1024 of a W-wide layer, read
@@ -302,6 +303,16 @@ __device__ inline void load_codes(uint32_t (&cb)[MAXO], const uint32_t* __restri
   const int v = threadIdx.x * 4;
 #pragma unroll
   for (int j = 0; j < MAXO; ++j) cb[j] = __builtin_amdgcn_raw_buffer_load_b32(r, v + j * kNetThreads * 4, 0, 0);
+}
+
+// Codes of a placed (type-uniform) layer, stored thread-major: the MAXO
+// codes of thread tid are contiguous at tid * MAXO, so one address register
+// and immediate offsets read them (the wave's loads stay contiguous).
+template <int MAXO>
+__device__ inline void load_codes_tm(uint32_t (&cb)[MAXO], const uint32_t* __restrict__ codes) {
+  const uint32_t* p = codes + threadIdx.x * MAXO;
+#pragma unroll
+  for (int j = 0; j < MAXO; ++j) cb[j] = p[j];
 }
 
 __device__ inline uint32_t bfi32(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }
@@ -359,6 +370,208 @@ __device__ __forceinline__ void layer_step(WT* lds, int cur, int nxt, int W,
 #pragma unroll
     for (int u = 0; u < GRP; ++u) dst[(g0 + u) * kNetThreads] = r[u];
   }
+}
+
+// ---------------------------------------------------------------------------
+// type-uniform rows
+// ---------------------------------------------------------------------------
+// With a placement plan (slg_fc_hard_type_place_net) the first U rows of a
+// layer hold, in each wave, outputs of one gate type: wave w computes gate
+// tt[w] in rows 0..U-1 and generic gates (compact codes) in rows U..rows-1.
+// A wave then branches once per layer to code specialised for its gate, where
+// a 32-bit half of an output word is one v_bitop3 with the truth table as
+// immediate (or nothing: constants and pass-throughs), and gates that ignore
+// an operand do not read it. A uniform row's code is (a << 16) | b with a, b
+// word indices counted from the start of the first activation buffer (the
+// read buffer's offset included), so an operand's LDS byte address is one
+// v_mad_u32_u16 (16-bit field x word size + LDS base).
+constexpr int kPlanStride = 18;  // per layer: U, rows, truth table of waves 0..15
+
+// tt bit k = output for address k = (a << 1) | b (compact-code order)
+__host__ __device__ constexpr bool tt_needs_a(int tt) { return (tt & 3) != (tt >> 2); }
+__host__ __device__ constexpr bool tt_needs_b(int tt) { return (tt & 5) != ((tt >> 1) & 5); }
+// v_bitop3 truth table of (a, b, 0): entry (a << 2 | b << 1 | c) = tt bit (a << 1 | b)
+__host__ __device__ constexpr uint32_t tt_bitop3(int tt) {
+  return ((tt & 1) ? 0x03u : 0u) | ((tt & 2) ? 0x0Cu : 0u) | ((tt & 4) ? 0x30u : 0u) |
+         ((tt & 8) ? 0xC0u : 0u);
+}
+
+template <int TT>
+__device__ __forceinline__ uint32_t gate_tt32(uint32_t a, uint32_t b) {
+  if constexpr (TT == 0) return 0u;
+  else if constexpr (TT == 15) return 0xFFFFFFFFu;
+  else if constexpr (TT == 12) return a;
+  else if constexpr (TT == 10) return b;
+  else if constexpr (TT == 3) return ~a;
+  else if constexpr (TT == 5) return ~b;
+  else return __builtin_amdgcn_bitop3_b32(a, b, 0u, (unsigned char)tt_bitop3(TT));
+}
+
+template <int TT, typename WT>
+__device__ __forceinline__ WT gate_tt(WT a, WT b) {
+  if constexpr (sizeof(WT) == 8) {
+    const uint32_t lo = gate_tt32<TT>((uint32_t)a, (uint32_t)b);
+    const uint32_t hi = gate_tt32<TT>((uint32_t)(a >> 32), (uint32_t)(b >> 32));
+    return ((uint64_t)hi << 32) | lo;
+  } else {
+    return gate_tt32<TT>(a, b);
+  }
+}
+
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+typedef __attribute__((address_space(3))) uint64_t lds_u64_t;
+
+// LDS byte address of word (c >> 16) (HI) or (c & 0xFFFF) of words of SZ bytes
+// counted from LDS byte `base`
+template <int SZ, bool HI>
+__device__ __forceinline__ uint32_t field_addr(uint32_t c, uint32_t base) {
+  uint32_t r;
+  if constexpr (SZ == 8 && HI) asm("v_mad_u32_u16 %0, %1, 8, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(c), "s"(base));
+  else if constexpr (SZ == 8) asm("v_mad_u32_u16 %0, %1, 8, %2" : "=v"(r) : "v"(c), "s"(base));
+  else if constexpr (HI) asm("v_mad_u32_u16 %0, %1, 4, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(c), "s"(base));
+  else asm("v_mad_u32_u16 %0, %1, 4, %2" : "=v"(r) : "v"(c), "s"(base));
+  return r;
+}
+
+template <typename WT>
+__device__ __forceinline__ WT lds_word(uint32_t addr) {
+  if constexpr (sizeof(WT) == 8) return *(const lds_u64_t*)(uintptr_t)addr;
+  else return *(const lds_u32_t*)(uintptr_t)addr;
+}
+
+// Rows [g0, g0 + N) of gate TT: every operand read first, then the gates,
+// then the writes.
+template <typename WT, int MAXO, int TT, int N>
+__device__ __forceinline__ void uniform_group(uint32_t base, WT* dst, int g0,
+                                              const uint32_t (&cb)[MAXO]) {
+  constexpr int SZ = (int)sizeof(WT);
+  WT va[N], vb[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    va[u] = vb[u] = (WT)0;
+    if constexpr (tt_needs_a(TT)) va[u] = lds_word<WT>(field_addr<SZ, true>(cb[g0 + u], base));
+    if constexpr (tt_needs_b(TT)) vb[u] = lds_word<WT>(field_addr<SZ, false>(cb[g0 + u], base));
+  }
+  WT r[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) r[u] = gate_tt<TT, WT>(va[u], vb[u]);
+#pragma unroll
+  for (int u = 0; u < N; ++u) dst[(g0 + u) * kNetThreads] = r[u];
+}
+
+// A group of N = 1..GRP-1 rows at g0 (N wave-uniform), as one batch.
+template <typename WT, int MAXO, int TT, int G0, int N>
+__device__ __forceinline__ void uniform_tail(uint32_t base, WT* dst, int n,
+                                             const uint32_t (&cb)[MAXO]) {
+  if constexpr (N >= 1 && G0 + N <= MAXO) {
+    if (n == N) uniform_group<WT, MAXO, TT, N>(base, dst, G0, cb);
+    else uniform_tail<WT, MAXO, TT, G0, N - 1>(base, dst, n, cb);
+  }
+}
+
+// Rows 0..U-1 of a wave of gate TT (U wave-uniform), in groups of GRP rows
+// and one shorter group for the rest.
+template <typename WT, int MAXO, int GRP, int TT, int G0 = 0>
+__device__ __forceinline__ void uniform_rows(uint32_t base, WT* dst, int U,
+                                             const uint32_t (&cb)[MAXO]) {
+  if constexpr (G0 < MAXO) {
+    if (G0 + GRP <= U) {
+      uniform_group<WT, MAXO, TT, GRP>(base, dst, G0, cb);
+      uniform_rows<WT, MAXO, GRP, TT, G0 + GRP>(base, dst, U, cb);
+    } else if (U > G0) {
+      uniform_tail<WT, MAXO, TT, G0, GRP - 1>(base, dst, U - G0, cb);
+    }
+  }
+}
+
+// Generic rows J..rows-1 (U == J) from compact codes, one at a time; the
+// compile-time start keeps the register indexing static.
+template <typename WT, int MAXO, int J>
+__device__ __forceinline__ void generic_rows(const WT* src, WT* dst, int U, int rows,
+                                             const uint32_t (&cb)[MAXO]) {
+  if constexpr (J <= MAXO) {
+    if (U != J) {
+      generic_rows<WT, MAXO, J + 1>(src, dst, U, rows, cb);
+      return;
+    }
+#pragma unroll
+    for (int j = J; j < MAXO; ++j) {
+      if (j >= rows) break;                              // wave-uniform
+      const uint32_t c = cb[j];
+      const WT a = src[(c >> 14) & 0x3FFFu], b = src[c & 0x3FFFu];
+      dst[j * kNetThreads] = gate_compact<WT>(a, b, c);
+    }
+  }
+}
+
+// The usual plan, U = MAXO - 1 and rows = MAXO: uniform rows in groups of
+// GRP, the last group read and computed in one batch with the generic row
+// MAXO - 1. No branch inside.
+template <typename WT, int MAXO, int GRP, int TT>
+__device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT* dst,
+                                                const uint32_t (&cb)[MAXO]) {
+  constexpr int SZ = (int)sizeof(WT);
+  constexpr int LG = ((MAXO - 2) / GRP) * GRP;       // first row of the last group
+  constexpr int N = MAXO - 1 - LG;                   // its uniform rows (>= 1)
+#pragma unroll
+  for (int g0 = 0; g0 < LG; g0 += GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, g0, cb);
+  WT va[N], vb[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    va[u] = vb[u] = (WT)0;
+    if constexpr (tt_needs_a(TT)) va[u] = lds_word<WT>(field_addr<SZ, true>(cb[LG + u], base));
+    if constexpr (tt_needs_b(TT)) vb[u] = lds_word<WT>(field_addr<SZ, false>(cb[LG + u], base));
+  }
+  const uint32_t c = cb[MAXO - 1];
+  const WT ga = src[(c >> 14) & 0x3FFFu], gb = src[c & 0x3FFFu];
+  WT r[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) r[u] = gate_tt<TT, WT>(va[u], vb[u]);
+#pragma unroll
+  for (int u = 0; u < N; ++u) dst[(LG + u) * kNetThreads] = r[u];
+  dst[(MAXO - 1) * kNetThreads] = gate_compact<WT>(ga, gb, c);
+}
+
+// One layer of a planned network: the wave's uniform rows, then rows
+// U..rows-1 from compact codes (as layer_step).
+// The plan is read as constant memory, so its loads are scalar: a vector
+// load would retire in order behind the layer's input-row loads and wait
+// for them.
+typedef __attribute__((address_space(4))) const int32_t const_i32_t;
+
+template <typename WT, int MAXO, int GRP>
+__device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, const int32_t* plan,
+                                           const uint32_t (&cb)[MAXO]) {
+  const const_i32_t* pl = (const const_i32_t*)plan;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int U = __builtin_amdgcn_readfirstlane(pl[0]);
+  const int rows = __builtin_amdgcn_readfirstlane(pl[1]);
+  const int tt = __builtin_amdgcn_readfirstlane(pl[2 + wave]);
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  const WT* src = lds + cur;
+  WT* dst = lds + nxt + threadIdx.x;
+  if (MAXO > 1 && U == MAXO - 1 && rows == MAXO) {
+    switch (tt & 15) {
+#define SLG_TT_CASE(T) \
+      case T: typed_rows_full<WT, MAXO, GRP, T>(base, src, dst, cb); break;
+      SLG_TT_CASE(0) SLG_TT_CASE(1) SLG_TT_CASE(2) SLG_TT_CASE(3)
+      SLG_TT_CASE(4) SLG_TT_CASE(5) SLG_TT_CASE(6) SLG_TT_CASE(7)
+      SLG_TT_CASE(8) SLG_TT_CASE(9) SLG_TT_CASE(10) SLG_TT_CASE(11)
+      SLG_TT_CASE(12) SLG_TT_CASE(13) SLG_TT_CASE(14) SLG_TT_CASE(15)
+#undef SLG_TT_CASE
+    }
+    return;
+  }
+  switch (tt & 15) {
+#define SLG_TT_CASE(T) \
+    case T: uniform_rows<WT, MAXO, GRP, T>(base, dst, U, cb); break;
+    SLG_TT_CASE(0) SLG_TT_CASE(1) SLG_TT_CASE(2) SLG_TT_CASE(3)
+    SLG_TT_CASE(4) SLG_TT_CASE(5) SLG_TT_CASE(6) SLG_TT_CASE(7)
+    SLG_TT_CASE(8) SLG_TT_CASE(9) SLG_TT_CASE(10) SLG_TT_CASE(11)
+    SLG_TT_CASE(12) SLG_TT_CASE(13) SLG_TT_CASE(14) SLG_TT_CASE(15)
+#undef SLG_TT_CASE
+  }
+  generic_rows<WT, MAXO, 0>(src, dst, U, rows, cb);
 }
 
 // wire residual (models.py:88-94): the first `keep` outputs copy the inputs
@@ -605,31 +818,45 @@ __device__ inline IT load_row(__amdgpu_buffer_rsrc_t r, int voff) {
   else return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
 }
 
-// The next tile streams as 4 chunks of 16 samples: chunk c is issued during
-// layer c and folded during layer c + 2 (or after the last layer); networks
-// with fewer than 4 layers load the remaining chunks after their last layer.
-constexpr int kChunk = 16, kChunks = 4;
+// The next tile streams as chunks of CH samples (16 for networks of up to 4
+// layers, 11 for deeper ones, so the stream spreads over every layer):
+// chunk c is issued during layer c and folded during layer c + 2 (or after
+// the last layer); chunks no layer issued load after the last layer. The
+// last chunk may run past sample 63: those rows lie past the tile's buffer
+// resource and read 0.
+template <int CH>
+constexpr int n_chunks() { return (64 + CH - 1) / CH; }
 
-template <typename IT>
-__device__ inline void issue_chunk(IT (&val)[kChunk], __amdgpu_buffer_rsrc_t r, int voff0,
+template <int CH, typename IT>
+__device__ inline void issue_chunk(IT (&val)[CH], __amdgpu_buffer_rsrc_t r, int voff0,
                                    int rowb, int chunk) {
-  const int v = voff0 + chunk * kChunk * rowb;
+  const int v = voff0 + chunk * CH * rowb;
 #pragma unroll
-  for (int j = 0; j < kChunk; ++j) val[j] = load_row<IT>(r, v + j * rowb);
+  for (int j = 0; j < CH; ++j) val[j] = load_row<IT>(r, v + j * rowb);
 }
 
-template <typename IT>
-__device__ inline void fold_chunk(uint64_t& word, const IT (&val)[kChunk], int chunk) {
+// Horner order (bit j ends at position j) keeps every constant inline: a
+// select of 1 << j would hold the large shifts in registers.
+template <int CH, typename IT>
+__device__ inline void fold_chunk(uint64_t& word, const IT (&val)[CH], int chunk) {
   uint32_t bits = 0;
 #pragma unroll
-  for (int j = 0; j < kChunk; ++j) bits |= (input_bit(val[j]) ? 1u : 0u) << j;
-  word |= (uint64_t)bits << (chunk * kChunk);
+  for (int j = CH - 1; j >= 0; --j) bits = (bits << 1) | (input_bit(val[j]) ? 1u : 0u);
+  word |= (uint64_t)bits << (chunk * CH);
 }
 
-template <typename IT, int MAXO>
+// The descriptor is the kernel's first argument and is read through the
+// kernel-argument segment (constant memory): its per-layer arrays are
+// indexed by the layer number, and read that way the loads stay scalar
+// instead of going through a private copy of the struct.
+typedef __attribute__((address_space(4))) const NetDesc const_netdesc_t;
+
+template <typename IT, int MAXO, bool TYPED, int CH>
 __global__ void __launch_bounds__(kNetThreads)
-fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
+fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_tiles,
                         float* __restrict__ logits) {
+  constexpr int NCH = n_chunks<CH>();
+  const_netdesc_t& d = *(const_netdesc_t*)__builtin_amdgcn_kernarg_segment_ptr();
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* lds = reinterpret_cast<uint64_t*>(smem);
   const int f = threadIdx.x;
@@ -637,24 +864,28 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
   const int voff0 = f * (int)sizeof(IT);
   const int rowb = d.in0 * (int)sizeof(IT);
   const int L = d.n_layers;
-  IT val0[kChunk], val1[kChunk];
+  IT val0[CH], val1[CH];
   int tile = blockIdx.x;
   uint64_t word = 0;
   {
     // first tile: two chunks in flight at a time
-    static_assert(kChunks == 4, "the first tile's loads are written out for four chunks");
     const __amdgpu_buffer_rsrc_t r = tile_rows(x, B, d.in0, tile * 64);
-    issue_chunk(val0, r, voff0, rowb, 0);
-    issue_chunk(val1, r, voff0, rowb, 1);
-    fold_chunk(word, val0, 0);
-    issue_chunk(val0, r, voff0, rowb, 2);
-    fold_chunk(word, val1, 1);
-    issue_chunk(val1, r, voff0, rowb, 3);
-    fold_chunk(word, val0, 2);
-    fold_chunk(word, val1, 3);
+    issue_chunk<CH>(val0, r, voff0, rowb, 0);
+    issue_chunk<CH>(val1, r, voff0, rowb, 1);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c & 1) {
+        fold_chunk<CH>(word, val1, c);
+        if (c + 2 < NCH) issue_chunk<CH>(val1, r, voff0, rowb, c + 2);
+      } else {
+        fold_chunk<CH>(word, val0, c);
+        if (c + 2 < NCH) issue_chunk<CH>(val0, r, voff0, rowb, c + 2);
+      }
+    }
   }
   uint32_t cb[MAXO];
-  load_codes(cb, d.codes[0], d.width[0]);
+  if constexpr (TYPED) load_codes_tm(cb, d.codes[0]);
+  else load_codes(cb, d.codes[0], d.width[0]);
 
   for (; tile < n_tiles; tile += gridDim.x) {
     if (fv) lds[f] = word;
@@ -667,15 +898,21 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
     // tile's resource and read 0 without memory traffic) and the loop is
     // unrolled by two, so each layer issues the same loads into the same
     // registers: the compiler then waits only for the loads a step needs.
-    auto layer = [&](int l, IT (&val)[kChunk]) {
+    auto layer = [&](int l, IT (&val)[CH]) __attribute__((always_inline)) {
       const int W = d.width[l];
       const int ln = (l + 1 < L) ? l + 1 : 0;  // after the last layer: layer 0 of the next tile
       uint32_t nb[MAXO];
-      load_codes(nb, d.codes[ln], d.width[ln]);
-      if (l >= 2 && l - 2 < kChunks) fold_chunk(nword, val, l - 2);
-      issue_chunk(val, r, voff0, rowb, l);
-      layer_step<uint64_t, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(lds, cur, nxt, W, cb);
-      if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
+      if constexpr (TYPED) load_codes_tm(nb, d.codes[ln]);
+      else load_codes(nb, d.codes[ln], d.width[ln]);
+      if (l >= 2 && l - 2 < NCH) fold_chunk<CH>(nword, val, l - 2);
+      issue_chunk<CH>(val, r, voff0, rowb, l);
+      constexpr int GRP = (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO;
+      if constexpr (TYPED) {
+        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, d.plan + l * kPlanStride, cb);
+      } else {
+        layer_step<uint64_t, MAXO, GRP>(lds, cur, nxt, W, cb);
+        if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
+      }
       __syncthreads();
       const int t = cur; cur = nxt; nxt = t;
       cur_w = W;
@@ -687,19 +924,19 @@ fc_hard_net_rows_kernel(const IT* __restrict__ x, int B, int n_tiles, NetDesc d,
       if (l + 1 < L) layer(l + 1, val1);
     }
     // chunks issued during the last two layers, then chunks no layer issued
-    for (int c = max(0, L - 2); c < min(L, kChunks); ++c) {
-      if (c & 1) fold_chunk(nword, val1, c);
-      else fold_chunk(nword, val0, c);
+    for (int c = max(0, L - 2); c < min(L, NCH); ++c) {
+      if (c & 1) fold_chunk<CH>(nword, val1, c);
+      else fold_chunk<CH>(nword, val0, c);
     }
-    for (int c = L; c < kChunks; ++c) {
-      issue_chunk(val0, r, voff0, rowb, c);
-      fold_chunk(nword, val0, c);
+    for (int c = L; c < NCH; ++c) {
+      issue_chunk<CH>(val0, r, voff0, rowb, c);
+      fold_chunk<CH>(nword, val0, c);
     }
     // every chunk is folded: the chunk registers hold nothing the next tile
     // reads before writing, but the layer loop's control flow does not show
     // it; constants here let the GroupSum below have those registers
 #pragma unroll
-    for (int j = 0; j < kChunk; ++j) val0[j] = val1[j] = (IT)0;
+    for (int j = 0; j < CH; ++j) val0[j] = val1[j] = (IT)0;
     groupsum_tile<uint64_t>(lds + cur, cur_w, d.C, tile * 64, B, logits);
     __syncthreads();
     word = fv ? nword : 0ull;
@@ -908,6 +1145,232 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_place_kernel(PlaceNet n
 }
 
 // ---------------------------------------------------------------------------
+// type-uniform placement for the fused network on unpacked rows
+// ---------------------------------------------------------------------------
+// Every layer but the last gets MAXO * 1024 slots, slot s = j * 1024 + tid in
+// row j of thread tid (wave w = tid / 64), in groups of 32 (s / 32). A plan
+// per layer picks U and gives each type T m[T] waves whose rows 0..U-1 hold
+// type-T outputs (64 U per wave, in index order); what does not fit, and the
+// types left without a wave, go to the generic rows U..rows-1. The 16 waves
+// go one at a time to the type with the most outputs not yet given a wave
+// (ties: the lower type); U is the largest value whose overflow fits the
+// rows left (U = 0: all rows generic). Within its groups a bin's outputs
+// are placed greedily in index order: each goes to the group where it adds
+// the fewest repeated operand bank classes (word index mod 32, only for the
+// operands its gate reads: the highest count first, then the sum, then the
+// lowest group), among groups with a free slot. Type bins are placed by one
+// wave each (wave T, type T), then wave 0 places the generic bin. Uniform
+// rows get codes (a << 16) | b with absolute word indices (the read buffer
+// of layer l starts at word (l & 1) * MAXO * 1024); generic rows get compact
+// codes on the renamed operands; unused slots get codes reading word 0 of
+// the read buffer. The last layer keeps its order and compact codes, with
+// operands renamed (slots past its width: code 0). Every layer's codes are
+// stored thread-major (slot j * 1024 + tid at tid * MAXO + j). The result is
+// a relabelling: the logits are the same.
+constexpr int kTypeMaxGroups = 512;     // 16 rows x 32 groups
+struct TypePlaceNet {
+  const uint32_t* in[kMaxLayers];    // compact codes, W[l] each
+  uint32_t* out[kMaxLayers];         // MAXO * 1024 slots per layer, stored thread-major
+  int32_t* perm[kMaxLayers];         // output -> slot, layers 0 .. L-2
+  int32_t* plan;                     // [L][kPlanStride]
+  int W[kMaxLayers];
+  int L, maxo;
+};
+
+__device__ inline void type_operands(const TypePlaceNet& n, int l, int o, uint32_t& a, uint32_t& b,
+                                     uint32_t& tt) {
+  const uint32_t c = n.in[l][o];
+  a = (c >> 14) & 0x3FFFu;
+  b = c & 0x3FFFu;
+  tt = c >> 28;
+  if (l > 0) {   // the prep clamps operands below the input width; kept in range here too
+    const uint32_t lim = (uint32_t)n.W[l - 1] - 1u;
+    a = (uint32_t)n.perm[l - 1][min(a, lim)];
+    b = (uint32_t)n.perm[l - 1][min(b, lim)];
+  }
+}
+
+// Wave-wide minimum of a 32-bit key.
+__device__ __forceinline__ uint32_t wave_min(uint32_t k) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) k = min(k, (uint32_t)__shfl_xor((int)k, off));
+  return k;
+}
+
+// Group of candidate q of a bin: uniform bin of type T (waves w0.., U rows
+// each, two groups per row) or the generic bin (rows U.., 32 groups per row).
+__device__ __forceinline__ int bin_group(bool generic, int q, int U, int w0) {
+  if (generic) return U * 32 + q;
+  const int i = q / (2 * U), r = q - i * 2 * U;
+  return (r >> 1) * 32 + (w0 + i) * 2 + (r & 1);
+}
+
+// Place output o (classes ca, cb) in the best group of a bin of G groups;
+// the calling wave owns the bin's groups. Returns the slot.
+__device__ int place_greedy(uint8_t (*cnt)[64], int* fill, bool generic, int G, int U, int w0,
+                            bool na, bool nb, int ca, int cb, int lane) {
+  uint32_t best = 0xFFFFFFFFu;
+  for (int q = lane; q < G; q += 64) {
+    const int g = bin_group(generic, q, U, w0);
+    if (fill[g] >= 32) continue;
+    const uint32_t pa = na ? cnt[g][ca] : 0u, pb = nb ? cnt[g][32 + cb] : 0u;
+    const uint32_t key = ((max(pa, pb) << 7 | (pa + pb)) << 16) | (uint32_t)q;
+    best = min(best, key);
+  }
+  best = wave_min(best);
+  int slot = -1;
+  if (best != 0xFFFFFFFFu) {
+    const int g = bin_group(generic, (int)(best & 0xFFFFu), U, w0);
+    slot = g * 32 + fill[g];
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+      fill[g] += 1;
+      if (na) cnt[g][ca] += 1;
+      if (nb) cnt[g][32 + cb] += 1;
+    }
+    __builtin_amdgcn_s_waitcnt(0);     // lane 0's LDS updates before the next search
+    __builtin_amdgcn_wave_barrier();
+  }
+  return slot;
+}
+
+// slot s = j * 1024 + tid of a layer's codes is stored at tid * MAXO + j
+__device__ __forceinline__ int tm_index(int s, int maxo) { return (s & (kNetThreads - 1)) * maxo + (s >> 10); }
+
+__global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypePlaceNet n) {
+  __shared__ uint8_t cnt[kTypeMaxGroups][64];      // per group: a-class counts, b-class counts
+  __shared__ int fill[kTypeMaxGroups];             // slots taken in each group
+  __shared__ uint16_t slot_of[kPlaceMax];          // output -> slot (0xFFFF: generic, unplaced)
+  __shared__ int hist[16], m[16], w0[16], wtt[16];
+  __shared__ int plan_u, plan_rows;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int maxo = n.maxo, S = maxo * kNetThreads;
+  for (int l = 0; l + 1 < n.L; ++l) {
+    const int W = n.W[l];
+    for (int i = tid; i < kTypeMaxGroups * 16; i += kPlaceThreads)
+      reinterpret_cast<uint32_t*>(&cnt[0][0])[i] = 0u;
+    for (int i = tid; i < kTypeMaxGroups; i += kPlaceThreads) fill[i] = 0;
+    if (tid < 16) hist[tid] = 0;
+    __syncthreads();
+    for (int o = tid; o < W; o += kPlaceThreads) atomicAdd(&hist[n.in[l][o] >> 28], 1);
+    __syncthreads();
+    if (tid == 0) {
+      int U = 0, rows = (W + kNetThreads - 1) / kNetThreads;
+      int mm[16];
+      for (int T = 0; T < 16; ++T) mm[T] = 0;
+      for (int u = maxo - 1; u >= 1; --u) {
+        const int cap = 64 * u;
+        for (int T = 0; T < 16; ++T) mm[T] = 0;
+        for (int waves = 0; waves < 16; ++waves) {
+          int bt = -1, br = 0;
+          for (int T = 0; T < 16; ++T) {
+            const int rem = hist[T] - mm[T] * cap;
+            if (rem > br) { br = rem; bt = T; }
+          }
+          if (bt < 0) break;
+          mm[bt] += 1;
+        }
+        int over = 0;
+        for (int T = 0; T < 16; ++T) over += max(0, hist[T] - mm[T] * cap);
+        const int rg = (over + kNetThreads - 1) / kNetThreads;
+        if (u + rg <= maxo) { U = u; rows = u + rg; break; }
+      }
+      if (U == 0)
+        for (int T = 0; T < 16; ++T) mm[T] = 0;
+      int w = 0;
+      for (int T = 0; T < 16; ++T) {
+        m[T] = mm[T];
+        w0[T] = w;
+        for (int i = 0; i < mm[T]; ++i) wtt[w++] = T;
+      }
+      for (; w < 16; ++w) wtt[w] = 0;
+      plan_u = U;
+      plan_rows = rows;
+      int32_t* pl = n.plan + l * kPlanStride;
+      pl[0] = U;
+      pl[1] = rows;
+      for (int i = 0; i < 16; ++i) pl[2 + i] = wtt[i];
+    }
+    __syncthreads();
+    const int U = plan_u;
+    // type bins: wave T walks its type's outputs in index order
+    {
+      const int T = wave, cap = 64 * U * m[T], G = 2 * U * m[T];
+      const bool na = tt_needs_a(T), nb = tt_needs_b(T);
+      int rank = 0;
+      for (int o0 = 0; o0 < W; o0 += 64) {
+        const int o = o0 + lane;
+        uint32_t a = 0, b = 0, tt = 16;
+        if (o < W) type_operands(n, l, o, a, b, tt);
+        uint64_t mk = __ballot(tt == (uint32_t)T);
+        while (mk) {
+          const int src = __ffsll((long long)mk) - 1;
+          mk &= mk - 1;
+          const int oo = o0 + src;
+          if (rank < cap) {
+            const int ca = __shfl((int)(a & 31u), src), cb = __shfl((int)(b & 31u), src);
+            const int s = place_greedy(cnt, fill, false, G, U, w0[T], na, nb, ca, cb, lane);
+            if (lane == 0) slot_of[oo] = (uint16_t)s;
+          } else if (lane == 0) {
+            slot_of[oo] = 0xFFFFu;
+          }
+          ++rank;
+        }
+      }
+    }
+    __syncthreads();
+    // generic bin (wave 0): what the type bins left, in index order
+    if (wave == 0) {
+      const int G = 32 * (plan_rows - U);
+      for (int o0 = 0; o0 < W; o0 += 64) {
+        const int o = o0 + lane;
+        const bool left = o < W && slot_of[o] == 0xFFFFu;
+        uint32_t a = 0, b = 0, tt = 0;
+        if (left) type_operands(n, l, o, a, b, tt);
+        uint64_t mk = __ballot(left);
+        while (mk) {
+          const int src = __ffsll((long long)mk) - 1;
+          mk &= mk - 1;
+          const int ca = __shfl((int)(a & 31u), src), cb = __shfl((int)(b & 31u), src);
+          const int s = place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
+          if (lane == 0) slot_of[o0 + src] = (uint16_t)s;
+        }
+      }
+    }
+    __syncthreads();
+    // codes, slots and unused slots (codes stored thread-major)
+    const uint32_t base = (uint32_t)((l & 1) * S);
+    for (int o = tid; o < W; o += kPlaceThreads) {
+      uint32_t a, b, tt;
+      type_operands(n, l, o, a, b, tt);
+      const int s = slot_of[o];
+      n.perm[l][o] = s;
+      n.out[l][tm_index(s, maxo)] =
+          (s >> 10) < U ? ((a + base) << 16) | (b + base) : (b | (a << 14) | (tt << 28));
+    }
+    for (int s = tid; s < S; s += kPlaceThreads) {
+      if ((s & 31) >= fill[s >> 5])
+        n.out[l][tm_index(s, maxo)] = (s >> 10) < U ? (base << 16) | base : 0u;
+    }
+    __syncthreads();
+    __threadfence_block();
+  }
+  // last layer: its own order, compact codes, operands renamed
+  const int l = n.L - 1;
+  for (int s = tid; s < S; s += kPlaceThreads) {
+    uint32_t a = 0, b = 0, tt = 0;
+    if (s < n.W[l]) type_operands(n, l, s, a, b, tt);
+    n.out[l][tm_index(s, maxo)] = b | (a << 14) | (tt << 28);
+  }
+  if (tid == 0) {
+    int32_t* pl = n.plan + l * kPlanStride;
+    pl[0] = 0;
+    pl[1] = (n.W[l] + kNetThreads - 1) / kNetThreads;
+    for (int i = 0; i < 16; ++i) pl[2 + i] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // packed GroupSum (layer-wise path): one workgroup per 64-sample word column
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) groupsum_packed_kernel(const uint64_t* __restrict__ xp, int W,
@@ -995,9 +1458,13 @@ static int launch_net_rows(const IT* x, int B, const NetDesc& d, size_t lds, flo
                            hipStream_t st) {
   const int64_t tiles = cdiv(B, 64);
   const int64_t grid = std::min<int64_t>(tiles, device_cus());
-  auto kern = fc_hard_net_rows_kernel<IT, MAXO>;
+  auto kern = d.n_layers <= 4
+                  ? (d.plan ? fc_hard_net_rows_kernel<IT, MAXO, true, 16>
+                            : fc_hard_net_rows_kernel<IT, MAXO, false, 16>)
+                  : (d.plan ? fc_hard_net_rows_kernel<IT, MAXO, true, 11>
+                            : fc_hard_net_rows_kernel<IT, MAXO, false, 11>);
   if (int rc = set_lds(kern, lds, "fc_hard_net_rows")) return rc;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kNetThreads), lds, st, x, B, (int)tiles, d,
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kNetThreads), lds, st, d, x, B, (int)tiles,
                      logits);
   SLG_LAUNCH_CHECK("fc_hard_net_rows");
   return 0;
@@ -1154,6 +1621,87 @@ int slg_fc_hard_place_net(int32_t n_layers, const int64_t* widths, const uint32_
   hipLaunchKernelGGL(fc_hard_place_kernel, dim3(1), dim3(kPlaceThreads), 0, as_stream(stream), n);
   SLG_LAUNCH_CHECK("fc_hard_place");
   return 0;
+}
+
+int64_t slg_fc_hard_type_slots(int64_t IN0, int32_t n_layers, const int64_t* widths) {
+  if (!widths || n_layers < 1 || n_layers > kMaxLayers || IN0 < 1 || IN0 > kNetThreads) return 0;
+  int64_t maxw = IN0;
+  for (int l = 0; l < n_layers; ++l) {
+    if (widths[l] < 1) return 0;
+    maxw = std::max<int64_t>(maxw, widths[l]);
+  }
+  const int maxo = maxw <= kPlaceMax ? pick_maxo(maxw) : 0;
+  if (maxo == 0 || net_spw(IN0, n_layers, widths, 1) != 64) return 0;
+  return (int64_t)maxo * kNetThreads;
+}
+
+int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* widths,
+                               const uint32_t* const* codes, uint32_t* const* placed,
+                               int32_t* plan, int32_t* perm_ws, int64_t perm_ws_len,
+                               slg_stream_t stream) {
+  SLG_REQUIRE(widths && codes && placed && plan && (perm_ws || n_layers == 1), SLG_E_ARG,
+              "fc_hard_type_place_net: null pointer");
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE,
+              "fc_hard_type_place_net: %d layers", n_layers);
+  const int64_t S = slg_fc_hard_type_slots(IN0, n_layers, widths);
+  SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED,
+              "fc_hard_type_place_net: needs inputs <= %d wide and a network whose 64-sample "
+              "column fits LDS", kNetThreads);
+  TypePlaceNet n{};
+  n.L = n_layers;
+  n.maxo = (int)(S / kNetThreads);
+  n.plan = plan;
+  int64_t used = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(codes[l] && placed[l], SLG_E_ARG, "fc_hard_type_place_net: null codes, layer %d", l);
+    SLG_REQUIRE(codes[l] != placed[l], SLG_E_ARG, "fc_hard_type_place_net: in place, layer %d", l);
+    n.in[l] = codes[l];
+    n.out[l] = placed[l];
+    n.W[l] = (int)widths[l];
+    if (l + 1 < n_layers) {
+      n.perm[l] = perm_ws + used;
+      used += widths[l];
+    }
+  }
+  SLG_REQUIRE(used <= perm_ws_len, SLG_E_ARG,
+              "fc_hard_type_place_net: workspace of %lld ints, %lld needed",
+              (long long)perm_ws_len, (long long)used);
+  hipLaunchKernelGGL(fc_hard_type_place_kernel, dim3(1), dim3(kPlaceThreads), 0, as_stream(stream), n);
+  SLG_LAUNCH_CHECK("fc_hard_type_place");
+  return 0;
+}
+
+int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
+                          const int64_t* widths, const uint32_t* const* codes, const int32_t* plan,
+                          int32_t C, float* logits, slg_stream_t stream) {
+  SLG_REQUIRE(widths && codes && plan && ((x && logits) || B == 0), SLG_E_ARG,
+              "fc_hard_net_typed: null pointer");
+  SLG_REQUIRE(in_kind == 0 || in_kind == 1, SLG_E_ARG,
+              "fc_hard_net_typed: in_kind %d (unpacked fp32 or uint8 rows only)", in_kind);
+  SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE, "fc_hard_net_typed: %d layers",
+              n_layers);
+  SLG_REQUIRE(B >= 0 && B < (1LL << 31) && IN0 > 0 && IN0 <= kNetThreads, SLG_E_SHAPE,
+              "fc_hard_net_typed: bad sizes");
+  const int64_t S = slg_fc_hard_type_slots(IN0, n_layers, widths);
+  SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "fc_hard_net_typed: widths do not fit LDS");
+  NetDesc d{};
+  for (int l = 0; l < n_layers; ++l) {
+    SLG_REQUIRE(codes[l], SLG_E_ARG, "fc_hard_net_typed: layer %d", l);
+    d.codes[l] = codes[l];
+    d.width[l] = (int)widths[l];
+  }
+  SLG_REQUIRE(C > 0 && C <= 64 && widths[n_layers - 1] % C == 0, SLG_E_SHAPE,
+              "fc_hard_net_typed: last width %lld not divisible by %d classes",
+              (long long)widths[n_layers - 1], C);
+  if (B == 0) return 0;
+  d.n_layers = n_layers; d.in0 = (int)IN0; d.C = C; d.wire_r = 0;
+  d.maxw = (int)S;
+  d.plan = plan;
+  const int maxo = (int)(S / kNetThreads);
+  const size_t lds = (size_t)2 * d.maxw * 8;
+  hipStream_t st = as_stream(stream);
+  if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
+  return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
 }
 
 int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C) {

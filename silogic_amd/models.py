@@ -81,10 +81,11 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     def plan():
         widths = [layer.out_dim for layer in layers]
         lut = any(layer.is_lut for layer in layers)
-        return lut, widths, 0 if lut else ops.fc_hard_net_supported(in_dim, widths, C)
+        spw = 0 if lut else ops.fc_hard_net_supported(in_dim, widths, C)
+        return lut, widths, spw, spw and ops.fc_hard_type_slots(in_dim, widths) > 0
 
-    lut, widths, spw = derived.cached(layers[0], "_derived_net_plan",
-                                      (in_dim, C, tuple(id(layer) for layer in layers)), plan)
+    lut, widths, spw, typable = derived.cached(
+        layers[0], "_derived_net_plan", (in_dim, C, tuple(id(layer) for layer in layers)), plan)
     if lut:
         # LUT layers: one packed kernel per layer (gate or LUT)
         xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
@@ -95,15 +96,22 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
             xp = yp
         return ops.groupsum_packed(xp, B, C)
     if spw:
+        rows = in_kind in (ops.ROWS_F32, ops.ROWS_U8) and spw == 64 and in_dim <= 1024
+        # one gate type per wave row where the rows kernel runs (rows of
+        # inputs, no wire residual), else a bank-aware output order; both
+        # relabel the circuit (the logits are the same bits). The wire
+        # residual copies inputs by position, so it keeps the order.
+        typed = rows and not wire_r and typable
+
         def build():
             codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True)
-            # bank-aware output order (the logits are the same bits); the
-            # wire residual copies inputs by position, so it keeps the order
+            if typed:
+                return ops.fc_hard_type_place_net(codes, in_dim)
             return ops.NetCodes(codes if wire_r else ops.fc_hard_place_net(codes))
 
         codes = derived.cached(layers[0], "_derived_net_codes",
-                               (derived.state_key(*layers), bool(wire_r)), build)
-        if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not (spw == 64 and in_dim <= 1024):
+                               (derived.state_key(*layers), bool(wire_r), typed), build)
+        if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not rows:
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
     codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers])

@@ -621,18 +621,56 @@ def fc_hard_place_net(codes):
     return placed
 
 
+def fc_hard_type_slots(in_dim, widths):
+    """Slots per layer of the type-uniform layout (0: it does not apply)."""
+    arr = (ctypes.c_int64 * len(widths))(*widths)
+    return _lib.lib().slg_fc_hard_type_slots(in_dim, len(widths), arr)
+
+
+def fc_hard_type_place_net(codes, in_dim):
+    """Type-uniform placement of a fused network's compact codes
+    (``slg_fc_hard_type_place_net``) for unpacked-row inputs ``in_dim`` wide:
+    every layer but the last becomes ``fc_hard_type_slots`` slots whose first
+    rows hold one gate type per wave, with the next layer's operands renamed;
+    the logits of ``fc_hard_net`` are unchanged. Returns a :class:`NetCodes`
+    carrying the plan."""
+    require_gpu(*codes)
+    if any(c.dim() != 1 or c.dtype != torch.int32 for c in codes):
+        raise ValueError("fc_hard_type_place_net: codes must be compact [OUT] int32 codes")
+    codes = [c.contiguous() for c in codes]
+    L = len(codes)
+    widths = [c.shape[0] for c in codes]
+    S = fc_hard_type_slots(in_dim, widths)
+    if S <= 0:
+        raise ValueError("fc_hard_type_place_net: the type-uniform layout does not apply to "
+                         "inputs %d wide and widths %s" % (in_dim, widths))
+    dev = codes[0].device
+    placed = [torch.empty((S,), device=dev, dtype=torch.int32) for _ in widths]
+    plan = torch.empty((L, 18), device=dev, dtype=torch.int32)
+    n_ws = max(1, sum(widths[:-1]))
+    ws = torch.empty(n_ws, device=dev, dtype=torch.int32)
+    _lib.call("slg_fc_hard_type_place_net", L, in_dim, (ctypes.c_int64 * L)(*widths),
+              _ptrs(codes), _ptrs(placed), _p(plan), _p(ws), n_ws, _stream(codes[0]))
+    return NetCodes(placed, plan=plan, in_dim=in_dim, widths=widths)
+
+
 class NetCodes(list):
     """Compact per-layer codes of a fused hard network (a list of ``[OUT]``
     int32 tensors) with their width and pointer arrays for the C ABI, built
-    once: the tensors must not be replaced or resized afterwards."""
+    once: the tensors must not be replaced or resized afterwards. ``plan``
+    (with the ``in_dim`` it was placed for) marks codes laid out by
+    :func:`fc_hard_type_place_net`, which only the unpacked-row network
+    kernel reads."""
 
-    def __init__(self, codes):
+    def __init__(self, codes, plan=None, in_dim=None, widths=None):
         super().__init__(codes)
         require_gpu(*self)
         if any(c.dim() != 1 or c.dtype != torch.int32 or not c.is_contiguous() for c in self):
             raise ValueError("fc_hard_net: codes must be compact [OUT] int32 codes")
-        self.widths = (ctypes.c_int64 * len(self))(*[c.shape[0] for c in self])
+        widths = widths if widths is not None else [c.shape[0] for c in self]
+        self.widths = (ctypes.c_int64 * len(self))(*widths)
         self.ptrs = (ctypes.c_void_p * len(self))(*[c.data_ptr() for c in self])
+        self.plan, self.in_dim = plan, in_dim
 
 
 def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
@@ -647,6 +685,13 @@ def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
     require_gpu(x)
     w_arr, c_arr = codes.widths, codes.ptrs
     out = torch.empty((B, C), device=x.device, dtype=torch.float32)
+    if codes.plan is not None:
+        if in_kind not in (ROWS_F32, ROWS_U8) or wire_r or in_dim != codes.in_dim:
+            raise ValueError("fc_hard_net: type-placed codes take unpacked rows %s wide and no "
+                             "wire residual" % codes.in_dim)
+        _lib.call("slg_fc_hard_net_typed", _p(x), in_kind, B, in_dim, len(codes), w_arr, c_arr,
+                  _p(codes.plan), C, _p(out), _stream(x))
+        return out
     _lib.call("slg_fc_hard_net", _p(x), in_kind, B, in_dim, len(codes), w_arr, c_arr, C,
               int(wire_r), _p(out), _stream(x))
     return out

@@ -1,0 +1,105 @@
+"""Type-uniform placement of the fused hard network on unpacked rows
+(slg_fc_hard_type_place_net + slg_fc_hard_net_typed): a relabelling of the
+circuit in which each wave's first rows hold one gate type, so the logits
+must be the same bits as the unplaced network's, whatever the mix of gate
+types (uniform draws, or one type dominating so that it takes several waves
+and the plan shrinks U)."""
+import pytest
+import torch
+
+import silogic_amd as sl
+from oracle import torch_ref
+from silogic_amd import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _net(in_dim, widths, skew=None, seed=11):
+    torch.manual_seed(0)
+    layers, d = [], in_dim
+    for i, w in enumerate(widths):
+        layer = sl.LogicLayer(d, w, k=4, seed=seed + i)
+        if skew is not None:
+            gate, frac = skew
+            g = torch.Generator().manual_seed(seed + 100 + i)
+            pick = torch.rand(w, generator=g) < frac
+            with torch.no_grad():
+                layer.node.gate_logits[pick, gate] += 10.0
+        layers.append(layer)
+        d = w
+    net = torch.nn.Module()
+    net.layers = torch.nn.ModuleList(layers).to(DEV)
+    return net
+
+
+def _codes(net):
+    return ops.fc_hard_codes_net([l.hard_spec() for l in net.layers], compact=True)
+
+
+def _check_plan(typed, widths, in_dim):
+    S = ops.fc_hard_type_slots(in_dim, widths)
+    maxo = S // 1024
+    plan = typed.plan.cpu()
+    for l, w in enumerate(widths):
+        U, rows = int(plan[l, 0]), int(plan[l, 1])
+        assert 0 <= U <= rows <= maxo, (l, U, rows)
+        assert rows * 1024 >= (w if U == 0 else 0)
+        assert all(0 <= int(t) < 16 for t in plan[l, 2:])
+    assert int(plan[-1, 0]) == 0
+    return plan
+
+
+@pytest.mark.parametrize("in_dim,widths,C,skew", [
+    (784, [2000, 2000, 2000], 10, None),
+    (200, [300, 250, 90], 10, None),
+    (64, [1000, 1000, 1000], 10, (6, 0.7)),     # xor dominates: several waves of one type
+    (100, [4000, 4000, 40], 4, (3, 0.5)),       # pass-through a
+    (100, [3000, 3000, 30], 5, (0, 0.6)),       # constant 0
+    (50, [40], 4, None),                        # one layer: nothing to place
+    (1024, [9000, 7000, 5000, 100], 10, (12, 0.4)),
+])
+def test_typed_network_is_bit_exact(in_dim, widths, C, skew):
+    net = _net(in_dim, widths, skew)
+    codes = _codes(net)
+    typed = ops.fc_hard_type_place_net(codes, in_dim)
+    again = ops.fc_hard_type_place_net(codes, in_dim)
+    assert all(torch.equal(a, b) for a, b in zip(typed, again))      # deterministic
+    assert torch.equal(typed.plan, again.plan)
+    plan = _check_plan(typed, widths, in_dim)
+    if len(widths) > 1 and widths[0] >= 1000:
+        assert int(plan[0, 0]) >= 1                                   # uniform rows in use
+    g = torch.Generator().manual_seed(1)
+    B = 64 * 9 + 17
+    x = (torch.rand(B, in_dim, generator=g) < 0.4).float()
+    ref = ops.fc_hard_net(x.to(DEV), ops.ROWS_F32, B, in_dim, codes, C)
+    got = ops.fc_hard_net(x.to(DEV), ops.ROWS_F32, B, in_dim, typed, C)
+    assert torch.equal(got, ref)
+    got8 = ops.fc_hard_net(x.to(torch.uint8).to(DEV), ops.ROWS_U8, B, in_dim, typed, C)
+    assert torch.equal(got8, ref)
+
+
+def test_typed_codes_refuse_packed_input():
+    net = _net(100, [300, 300, 30])
+    typed = ops.fc_hard_type_place_net(_codes(net), 100)
+    xp = ops.pack_bits(torch.zeros(64, 100, device=DEV), word_major=True)
+    with pytest.raises(ValueError):
+        ops.fc_hard_net(xp, ops.PACKED_WORD_MAJOR, 64, 100, typed, 10)
+
+
+def test_config_2_typed_forward_hard_matches_the_oracle():
+    """Config 2 (784 -> 6 x 10000): forward_hard on fp32 rows takes the
+    type-uniform layout (at least eight uniform rows of ten per hidden layer) and
+    matches the oracle bit for bit on a batch slice."""
+    from silogic_amd.synthetic import CONFIGS, build_config, config_inputs
+    model = build_config(2, sl).eval()
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV)
+    x = config_inputs(2, 64 * 3 + 9)
+    with torch.no_grad():
+        got = model.forward_hard(x.to(DEV)).cpu()
+    codes = model.layers[0].__dict__["_derived_net_codes"][1]
+    assert codes.plan is not None
+    plan = codes.plan.cpu()
+    assert all(int(plan[l, 0]) >= 8 and int(plan[l, 1]) <= 10 for l in range(5)), plan[:, :2]
+    assert torch.equal(got, torch_ref.forward_hard(CONFIGS[2], sd, x))
