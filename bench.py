@@ -119,6 +119,15 @@ def load_traffic(cfg):
         return json.load(fh).get(f"cfg{cfg}", {})
 
 
+def hard_net_codes(ops, model, in_dim):
+    """The codes LogicNet.forward_hard runs on unpacked rows: the type-uniform
+    layout where it applies, else the bank-aware order."""
+    codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
+    if ops.fc_hard_type_slots(in_dim, [l.out_dim for l in model.layers]) > 0:
+        return ops.fc_hard_type_place_net(codes, in_dim)
+    return ops.NetCodes(ops.fc_hard_place_net(codes))
+
+
 def kernels_only(reps=3):
     """Workload for counter passes: a 256 MiB copy (calibration), then
     ``reps`` times each: config 2's fused hard network and one soft hidden
@@ -135,8 +144,7 @@ def kernels_only(reps=3):
     model = build_config(2, sl).eval().to(dev)
     xh = config_inputs(2, 65536).to(dev)
     with torch.no_grad():
-        codes = ops.fc_hard_place_net(
-            ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True))
+        codes = hard_net_codes(ops, model, 784)
         for _ in range(reps):
             ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
         for cfg in (2, 4):
@@ -328,14 +336,11 @@ def measure_config(cfg, steps, warmup, with_cpu):
     hard = None
     with torch.no_grad():
         if hasattr(model, "layers"):
-            specs = [l.hard_spec() for l in model.layers]
             widths = [l.out_dim for l in model.layers]
             C = model.head.num_classes
             in_dim = x_hard.shape[1]
             if ops.fc_hard_net_supported(in_dim, widths, C) == 64 and in_dim <= 1024:
-                # the codes forward_hard runs: placed, as LogicNet caches them
-                codes = ops.NetCodes(ops.fc_hard_place_net(ops.fc_hard_codes_net(specs,
-                                                                                 compact=True)))
+                codes = hard_net_codes(ops, model, in_dim)
                 fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, in_dim, codes, C)  # noqa: E731
                 fn_net()
                 k_hard = _events_ms(fn_net, reps) / 1e3

@@ -1190,11 +1190,18 @@ __device__ inline void type_operands(const TypePlaceNet& n, int l, int o, uint32
   }
 }
 
-// Wave-wide minimum of a 32-bit key.
+// Wave-wide minimum of a 32-bit key, in every lane (every lane active):
+// DPP quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror
+// within 16-lane rows, then permlane16/32 swaps across rows.
 __device__ __forceinline__ uint32_t wave_min(uint32_t k) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) k = min(k, (uint32_t)__shfl_xor((int)k, off));
-  return k;
+  k = min(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, 0xB1, 0xF, 0xF, false));
+  k = min(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, 0x4E, 0xF, 0xF, false));
+  k = min(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, 0x141, 0xF, 0xF, false));
+  k = min(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, 0x140, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(k, k, false, false);
+  k = min(r16[0], r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(k, k, false, false);
+  return min(r32[0], r32[1]);
 }
 
 // Group of candidate q of a bin: uniform bin of type T (waves w0.., U rows
@@ -1228,7 +1235,7 @@ __device__ int place_greedy(uint8_t (*cnt)[64], int* fill, bool generic, int G, 
       if (na) cnt[g][ca] += 1;
       if (nb) cnt[g][32 + cb] += 1;
     }
-    __builtin_amdgcn_s_waitcnt(0);     // lane 0's LDS updates before the next search
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): lane 0's LDS updates land first
     __builtin_amdgcn_wave_barrier();
   }
   return slot;
@@ -1241,6 +1248,7 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
   __shared__ uint8_t cnt[kTypeMaxGroups][64];      // per group: a-class counts, b-class counts
   __shared__ int fill[kTypeMaxGroups];             // slots taken in each group
   __shared__ uint16_t slot_of[kPlaceMax];          // output -> slot (0xFFFF: generic, unplaced)
+  __shared__ uint16_t info[kPlaceMax];             // a-class | b-class << 5 | type << 10
   __shared__ int hist[16], m[16], w0[16], wtt[16];
   __shared__ int plan_u, plan_rows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1252,7 +1260,12 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
     for (int i = tid; i < kTypeMaxGroups; i += kPlaceThreads) fill[i] = 0;
     if (tid < 16) hist[tid] = 0;
     __syncthreads();
-    for (int o = tid; o < W; o += kPlaceThreads) atomicAdd(&hist[n.in[l][o] >> 28], 1);
+    for (int o = tid; o < W; o += kPlaceThreads) {
+      uint32_t a, b, tt;
+      type_operands(n, l, o, a, b, tt);
+      info[o] = (uint16_t)((a & 31u) | ((b & 31u) << 5) | (tt << 10));
+      atomicAdd(&hist[tt], 1);
+    }
     __syncthreads();
     if (tid == 0) {
       int U = 0, rows = (W + kNetThreads - 1) / kNetThreads;
@@ -1300,15 +1313,16 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
       int rank = 0;
       for (int o0 = 0; o0 < W; o0 += 64) {
         const int o = o0 + lane;
-        uint32_t a = 0, b = 0, tt = 16;
-        if (o < W) type_operands(n, l, o, a, b, tt);
+        const uint32_t in = o < W ? info[o] : 0xFFFFu;
+        const uint32_t a = in & 31u, b = (in >> 5) & 31u, tt = in >> 10;
         uint64_t mk = __ballot(tt == (uint32_t)T);
         while (mk) {
           const int src = __ffsll((long long)mk) - 1;
           mk &= mk - 1;
           const int oo = o0 + src;
           if (rank < cap) {
-            const int ca = __shfl((int)(a & 31u), src), cb = __shfl((int)(b & 31u), src);
+            const int ca = __builtin_amdgcn_readlane((int)(a & 31u), src);
+            const int cb = __builtin_amdgcn_readlane((int)(b & 31u), src);
             const int s = place_greedy(cnt, fill, false, G, U, w0[T], na, nb, ca, cb, lane);
             if (lane == 0) slot_of[oo] = (uint16_t)s;
           } else if (lane == 0) {
@@ -1325,13 +1339,14 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
       for (int o0 = 0; o0 < W; o0 += 64) {
         const int o = o0 + lane;
         const bool left = o < W && slot_of[o] == 0xFFFFu;
-        uint32_t a = 0, b = 0, tt = 0;
-        if (left) type_operands(n, l, o, a, b, tt);
+        const uint32_t in = left ? info[o] : 0u;
+        const uint32_t a = in & 31u, b = (in >> 5) & 31u;
         uint64_t mk = __ballot(left);
         while (mk) {
           const int src = __ffsll((long long)mk) - 1;
           mk &= mk - 1;
-          const int ca = __shfl((int)(a & 31u), src), cb = __shfl((int)(b & 31u), src);
+          const int ca = __builtin_amdgcn_readlane((int)(a & 31u), src);
+          const int cb = __builtin_amdgcn_readlane((int)(b & 31u), src);
           const int s = place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
           if (lane == 0) slot_of[o0 + src] = (uint16_t)s;
         }
