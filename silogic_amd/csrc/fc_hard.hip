@@ -439,11 +439,15 @@ __device__ __forceinline__ WT lds_word(uint32_t addr) {
   else return *(const lds_u32_t*)(uintptr_t)addr;
 }
 
-// Rows [g0, g0 + N) of gate TT: every operand read first, then the gates,
-// then the writes.
-template <typename WT, int MAXO, int TT, int N>
+// Rows [g0, g0 + N) of gate TT: every operand read first, then `between`
+// (work that overlaps the reads), then the gates, then the writes.
+struct NoWork {
+  __device__ void operator()() const {}
+};
+
+template <typename WT, int MAXO, int TT, int N, typename F = NoWork>
 __device__ __forceinline__ void uniform_group(uint32_t base, WT* dst, int g0,
-                                              const uint32_t (&cb)[MAXO]) {
+                                              const uint32_t (&cb)[MAXO], F&& between = F()) {
   constexpr int SZ = (int)sizeof(WT);
   WT va[N], vb[N];
 #pragma unroll
@@ -452,6 +456,7 @@ __device__ __forceinline__ void uniform_group(uint32_t base, WT* dst, int g0,
     if constexpr (tt_needs_a(TT)) va[u] = lds_word<WT>(field_addr<SZ, true>(cb[g0 + u], base));
     if constexpr (tt_needs_b(TT)) vb[u] = lds_word<WT>(field_addr<SZ, false>(cb[g0 + u], base));
   }
+  between();
   WT r[N];
 #pragma unroll
   for (int u = 0; u < N; ++u) r[u] = gate_tt<TT, WT>(va[u], vb[u]);
@@ -506,15 +511,18 @@ __device__ __forceinline__ void generic_rows(const WT* src, WT* dst, int U, int 
 
 // The usual plan, U = MAXO - 1 and rows = MAXO: uniform rows in groups of
 // GRP, the last group read and computed in one batch with the generic row
-// MAXO - 1. No branch inside.
-template <typename WT, int MAXO, int GRP, int TT>
+// MAXO - 1. No branch inside. `filler` (the layer's input-row work) runs
+// while the first group's reads are in flight.
+template <typename WT, int MAXO, int GRP, int TT, typename F>
 __device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT* dst,
-                                                const uint32_t (&cb)[MAXO]) {
+                                                const uint32_t (&cb)[MAXO], F&& filler) {
   constexpr int SZ = (int)sizeof(WT);
   constexpr int LG = ((MAXO - 2) / GRP) * GRP;       // first row of the last group
   constexpr int N = MAXO - 1 - LG;                   // its uniform rows (>= 1)
+  if constexpr (LG >= GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, 0, cb, filler);
+  else filler();
 #pragma unroll
-  for (int g0 = 0; g0 < LG; g0 += GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, g0, cb);
+  for (int g0 = GRP; g0 < LG; g0 += GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, g0, cb);
   WT va[N], vb[N];
 #pragma unroll
   for (int u = 0; u < N; ++u) {
@@ -539,9 +547,9 @@ __device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT
 // for them.
 typedef __attribute__((address_space(4))) const int32_t const_i32_t;
 
-template <typename WT, int MAXO, int GRP>
+template <typename WT, int MAXO, int GRP, typename F>
 __device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, const int32_t* plan,
-                                           const uint32_t (&cb)[MAXO]) {
+                                           const uint32_t (&cb)[MAXO], F&& filler) {
   const const_i32_t* pl = (const const_i32_t*)plan;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int U = __builtin_amdgcn_readfirstlane(pl[0]);
@@ -553,7 +561,7 @@ __device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, const int3
   if (MAXO > 1 && U == MAXO - 1 && rows == MAXO) {
     switch (tt & 15) {
 #define SLG_TT_CASE(T) \
-      case T: typed_rows_full<WT, MAXO, GRP, T>(base, src, dst, cb); break;
+      case T: typed_rows_full<WT, MAXO, GRP, T>(base, src, dst, cb, filler); break;
       SLG_TT_CASE(0) SLG_TT_CASE(1) SLG_TT_CASE(2) SLG_TT_CASE(3)
       SLG_TT_CASE(4) SLG_TT_CASE(5) SLG_TT_CASE(6) SLG_TT_CASE(7)
       SLG_TT_CASE(8) SLG_TT_CASE(9) SLG_TT_CASE(10) SLG_TT_CASE(11)
@@ -562,6 +570,7 @@ __device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, const int3
     }
     return;
   }
+  filler();
   switch (tt & 15) {
 #define SLG_TT_CASE(T) \
     case T: uniform_rows<WT, MAXO, GRP, T>(base, dst, U, cb); break;
@@ -904,12 +913,20 @@ fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_til
       uint32_t nb[MAXO];
       if constexpr (TYPED) load_codes_tm(nb, d.codes[ln]);
       else load_codes(nb, d.codes[ln], d.width[ln]);
-      if (l >= 2 && l - 2 < NCH) fold_chunk<CH>(nword, val, l - 2);
-      issue_chunk<CH>(val, r, voff0, rowb, l);
+      auto rows_work = [&]() __attribute__((always_inline)) {
+        if (l >= 2 && l - 2 < NCH) fold_chunk<CH>(nword, val, l - 2);
+        issue_chunk<CH>(val, r, voff0, rowb, l);
+      };
       constexpr int GRP = (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO;
-      if constexpr (TYPED) {
-        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, d.plan + l * kPlanStride, cb);
+      if constexpr (TYPED && CH < 16) {
+        // the row work overlaps the first operand reads (16-sample chunks
+        // hold too many registers for that)
+        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, d.plan + l * kPlanStride, cb, rows_work);
+      } else if constexpr (TYPED) {
+        rows_work();
+        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, d.plan + l * kPlanStride, cb, NoWork());
       } else {
+        rows_work();
         layer_step<uint64_t, MAXO, GRP>(lds, cur, nxt, W, cb);
         if (d.wire_r > 0 && cur_w == W) keep_inputs<uint64_t, MAXO>(lds, cur, nxt, min(d.wire_r, W));
       }
