@@ -103,3 +103,23 @@ def test_config_2_typed_forward_hard_matches_the_oracle():
     plan = codes.plan.cpu()
     assert all(int(plan[l, 0]) >= 8 and int(plan[l, 1]) <= 10 for l in range(5)), plan[:, :2]
     assert torch.equal(got, torch_ref.forward_hard(CONFIGS[2], sd, x))
+
+
+@pytest.mark.parametrize("in_dim,widths,C,B", [
+    (784, [2000, 2000], 10, 1),                       # 16-sample chunks, one sample
+    (784, [2000, 2000, 2000, 2000], 10, 63),          # four layers, a partial tile
+    (300, [1500] * 5, 10, 64),                        # 11-sample chunks, one chunk after the loop
+    (1024, [3000] * 8, 10, 65),                       # deeper than the chunks
+    (128, [700, 900, 300], 3, 130),
+])
+def test_typed_network_edge_batches_and_depths(in_dim, widths, C, B):
+    net = _net(in_dim, widths, seed=31)
+    codes = _codes(net)
+    typed = ops.fc_hard_type_place_net(codes, in_dim)
+    _check_plan(typed, widths, in_dim)
+    g = torch.Generator().manual_seed(B)
+    x = (torch.rand(B, in_dim, generator=g) < 0.5).float()
+    ref = ops.fc_hard_net(x.to(DEV), ops.ROWS_F32, B, in_dim, codes, C)
+    assert torch.equal(ops.fc_hard_net(x.to(DEV), ops.ROWS_F32, B, in_dim, typed, C), ref)
+    x8 = x.to(torch.uint8).to(DEV)
+    assert torch.equal(ops.fc_hard_net(x8, ops.ROWS_U8, B, in_dim, typed, C), ref)
