@@ -331,8 +331,16 @@ def measure_config(cfg, steps, warmup, with_cpu):
 
     t_hard, wall = timed(lambda: model.forward_hard(x_hard))
     t_soft, _ = timed(lambda: model(x_soft))
-    log(f"config {cfg}: hard step {t_hard * 1e6:.1f} us (wall {wall / steps * 1e6:.1f} us); "
-        f"soft forward {t_soft * 1e6:.1f} us")
+    # the same hard step replayed from a captured graph (no per-call host
+    # work): where the eager loop is host-bound, this is the GPU's rate
+    from silogic_amd.graphs import CapturedForward
+    captured = CapturedForward(model.forward_hard, x_hard)
+    for _ in range(warmup):
+        captured()
+    t_hard_graph, _ = timed(captured)
+    del captured
+    log(f"config {cfg}: hard step {t_hard * 1e6:.1f} us (wall {wall / steps * 1e6:.1f} us, "
+        f"graph replay {t_hard_graph * 1e6:.1f} us); soft forward {t_soft * 1e6:.1f} us")
 
     # ---- dominant kernels alone, HIP events on the launch stream ----
     reps = 20
@@ -364,6 +372,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
         "hard_Ggate_evals_per_s": round(B_hard * gates / t_hard / 1e9, 3),
         "soft_samples_per_s": round(B_soft / t_soft, 1),
         "t_hard_us": round(t_hard * 1e6, 2), "t_soft_us": round(t_soft * 1e6, 2),
+        "t_hard_graph_us": round(t_hard_graph * 1e6, 2),
         "ms_per_step": round(t_hard * 1e3, 4),
     }
     if soft_flops is None:
@@ -425,6 +434,7 @@ def bench_line(head_cfg, res, steps, warmup, configs=None):
         "soft_samples_per_s": res["soft_samples_per_s"],
         "soft_dtype": "f32",
         "t_hard_us": res["t_hard_us"],
+        "t_hard_graph_us": res["t_hard_graph_us"],
         "t_soft_us": res["t_soft_us"],
         "roofline": roof,
         "roofline_soft": res["roofline_soft"],
