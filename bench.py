@@ -450,7 +450,7 @@ def bench_line(head_cfg, res, steps, warmup, configs=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     # the GPU runs at lower clocks after the idle of each config's build:
     # a timed block after 5 warm-up steps measured up to 20% slower than after 50
     ap.add_argument("--warmup", type=int, default=50)
