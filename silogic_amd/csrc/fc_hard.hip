@@ -1175,7 +1175,8 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_place_kernel(PlaceNet n
 // are placed greedily in index order: each goes to the group where it adds
 // the fewest repeated operand bank classes (word index mod 32, only for the
 // operands its gate reads: the highest count first, then the sum, then the
-// lowest group), among groups with a free slot. Type bins are placed by one
+// lowest group), among groups with a free slot (bins of up to 64 groups keep
+// their counts in registers, saturating at 3). Type bins are placed by one
 // wave each (wave T, type T), then wave 0 places the generic bin. Uniform
 // rows get codes (a << 16) | b with absolute word indices (the read buffer
 // of layer l starts at word (l & 1) * MAXO * 1024); generic rows get compact
@@ -1261,6 +1262,36 @@ __device__ int place_greedy(uint8_t (*cnt)[64], int* fill, bool generic, int G, 
 // slot s = j * 1024 + tid of a layer's codes is stored at tid * MAXO + j
 __device__ __forceinline__ int tm_index(int s, int maxo) { return (s & (kNetThreads - 1)) * maxo + (s >> 10); }
 
+// Greedy state of a bin of at most 64 groups held in registers: lane q owns
+// group q (its fill count and, per operand side, the bank classes it reads
+// at least once, twice and three times: counts saturate at 3 here). A step
+// is then a few VALU operations and the DPP minimum, with no LDS round trip;
+// the key and the tie order are those of place_greedy. Every lane of the
+// wave must call place() together.
+struct RegBin {
+  int fill = 0;
+  uint32_t a1 = 0, a2 = 0, a3 = 0, b1 = 0, b2 = 0, b3 = 0;
+
+  __device__ int place(bool generic, int G, int U, int w0, bool na, bool nb, int ca, int cb,
+                       int lane) {
+    const uint32_t ba = 1u << ca, bb = 1u << cb;
+    const uint32_t pa = na ? (uint32_t)((a1 & ba) != 0) + ((a2 & ba) != 0) + ((a3 & ba) != 0) : 0u;
+    const uint32_t pb = nb ? (uint32_t)((b1 & bb) != 0) + ((b2 & bb) != 0) + ((b3 & bb) != 0) : 0u;
+    const bool ok = lane < G && fill < 32;
+    const uint32_t key = wave_min(ok ? ((max(pa, pb) << 7 | (pa + pb)) << 16) | (uint32_t)lane
+                                     : 0xFFFFFFFFu);
+    if (key == 0xFFFFFFFFu) return -1;
+    const int q = (int)(key & 0xFFFFu);
+    const int f = __builtin_amdgcn_readlane(fill, q);
+    if (lane == q) {
+      fill += 1;
+      if (na) { a3 |= a2 & ba; a2 |= a1 & ba; a1 |= ba; }
+      if (nb) { b3 |= b2 & bb; b2 |= b1 & bb; b1 |= bb; }
+    }
+    return bin_group(generic, q, U, w0) * 32 + f;
+  }
+};
+
 __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypePlaceNet n) {
   __shared__ uint8_t cnt[kTypeMaxGroups][64];      // per group: a-class counts, b-class counts
   __shared__ int fill[kTypeMaxGroups];             // slots taken in each group
@@ -1327,6 +1358,8 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
     {
       const int T = wave, cap = 64 * U * m[T], G = 2 * U * m[T];
       const bool na = tt_needs_a(T), nb = tt_needs_b(T);
+      const bool regs = G <= 64;
+      RegBin rb;
       int rank = 0;
       for (int o0 = 0; o0 < W; o0 += 64) {
         const int o = o0 + lane;
@@ -1340,7 +1373,8 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
           if (rank < cap) {
             const int ca = __builtin_amdgcn_readlane((int)(a & 31u), src);
             const int cb = __builtin_amdgcn_readlane((int)(b & 31u), src);
-            const int s = place_greedy(cnt, fill, false, G, U, w0[T], na, nb, ca, cb, lane);
+            const int s = regs ? rb.place(false, G, U, w0[T], na, nb, ca, cb, lane)
+                               : place_greedy(cnt, fill, false, G, U, w0[T], na, nb, ca, cb, lane);
             if (lane == 0) slot_of[oo] = (uint16_t)s;
           } else if (lane == 0) {
             slot_of[oo] = 0xFFFFu;
@@ -1348,11 +1382,14 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
           ++rank;
         }
       }
+      if (regs && lane < G) fill[bin_group(false, lane, U, w0[T])] = rb.fill;
     }
     __syncthreads();
     // generic bin (wave 0): what the type bins left, in index order
     if (wave == 0) {
       const int G = 32 * (plan_rows - U);
+      const bool regs = G <= 64;
+      RegBin rb;
       for (int o0 = 0; o0 < W; o0 += 64) {
         const int o = o0 + lane;
         const bool left = o < W && slot_of[o] == 0xFFFFu;
@@ -1364,10 +1401,12 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
           mk &= mk - 1;
           const int ca = __builtin_amdgcn_readlane((int)(a & 31u), src);
           const int cb = __builtin_amdgcn_readlane((int)(b & 31u), src);
-          const int s = place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
+          const int s = regs ? rb.place(true, G, U, 0, true, true, ca, cb, lane)
+                             : place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
           if (lane == 0) slot_of[o0 + src] = (uint16_t)s;
         }
       }
+      if (regs && lane < G) fill[bin_group(true, lane, U, 0)] = rb.fill;
     }
     __syncthreads();
     // codes, slots and unused slots (codes stored thread-major)
