@@ -705,7 +705,7 @@ static int launch_soft_node(const SoftArgs& a, hipStream_t st) {
 
 // Samples per workgroup tile and workgroup size, from a sweep on MI355X
 // (B = 4096, OUT = 10000-16380, K = 8): IN = 784 -> 4 samples / 256 threads,
-// IN = 4096 -> 8 / 512, IN = 10000 -> 4 / 1024, IN = 16380 -> 2 / 1024. The
+// IN = 4096 -> 8 / 512, IN = 10000 -> 4 / 512, IN = 16380 -> 2 / 512. The
 // tile takes the largest power of two <= 8 whose rows fit 160 KB of LDS less
 // 1 KB for the fused head's counters (4 for narrow inputs, where more,
 // smaller workgroups per CU win).
@@ -722,11 +722,15 @@ static int pick_tile(int64_t IN, int requested, int64_t B = INT64_MAX) {
   return 0;
 }
 
+// Workgroup size: 256 threads for tiles of at most 40 KB (several workgroups
+// per CU), else 512: with one workgroup per CU, eight waves beat sixteen on
+// MI355X (config 2 hidden layer 103.2 -> 99.6 us, config 4 walsh layer
+// 220.7 -> 203.1 us on records; the array path likewise).
 static int pick_threads(int64_t IN, int S, int requested) {
   if (requested > 0) return requested;
   const int64_t lds = IN * S * 4;
   if (lds <= 40 * 1024) return 256;
-  return 1024;  // capped per variant by soft_max_threads
+  return 512;
 }
 
 template <int NODE, int KC, bool REC>
