@@ -1176,8 +1176,10 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_place_kernel(PlaceNet n
 // the fewest repeated operand bank classes (word index mod 32, only for the
 // operands its gate reads: the highest count first, then the sum, then the
 // lowest group), among groups with a free slot (bins of up to 64 groups keep
-// their counts in registers, saturating at 3). Type bins are placed by one
-// wave each (wave T, type T), then wave 0 places the generic bin. Uniform
+// their counts in registers, saturating at 3). Each wave places the outputs
+// of its own rows (the k-th wave of type T takes that type's ranks
+// [64 U k, 64 U (k + 1))), all waves at once; then wave 0 places the
+// generic bin. Uniform
 // rows get codes (a << 16) | b with absolute word indices (the read buffer
 // of layer l starts at word (l & 1) * MAXO * 1024); generic rows get compact
 // codes on the renamed operands; unused slots get codes reading word 0 of
@@ -1297,6 +1299,7 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
   __shared__ int fill[kTypeMaxGroups];             // slots taken in each group
   __shared__ uint16_t slot_of[kPlaceMax];          // output -> slot (0xFFFF: generic, unplaced)
   __shared__ uint16_t info[kPlaceMax];             // a-class | b-class << 5 | type << 10
+  __shared__ uint16_t rank_of[kPlaceMax];          // rank of an output within its type
   __shared__ int hist[16], m[16], w0[16], wtt[16];
   __shared__ int plan_u, plan_rows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1354,35 +1357,49 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
     }
     __syncthreads();
     const int U = plan_u;
-    // type bins: wave T walks its type's outputs in index order
+    // ranks within each type (wave T scans type T in index order, one ballot
+    // prefix per 64 outputs); what lies past the type's waves goes generic
     {
-      const int T = wave, cap = 64 * U * m[T], G = 2 * U * m[T];
-      const bool na = tt_needs_a(T), nb = tt_needs_b(T);
-      const bool regs = G <= 64;
-      RegBin rb;
-      int rank = 0;
+      const int T = wave, cap = 64 * U * m[T];
+      int base = 0;
       for (int o0 = 0; o0 < W; o0 += 64) {
         const int o = o0 + lane;
-        const uint32_t in = o < W ? info[o] : 0xFFFFu;
-        const uint32_t a = in & 31u, b = (in >> 5) & 31u, tt = in >> 10;
-        uint64_t mk = __ballot(tt == (uint32_t)T);
-        while (mk) {
-          const int src = __ffsll((long long)mk) - 1;
-          mk &= mk - 1;
-          const int oo = o0 + src;
-          if (rank < cap) {
-            const int ca = __builtin_amdgcn_readlane((int)(a & 31u), src);
-            const int cb = __builtin_amdgcn_readlane((int)(b & 31u), src);
-            const int s = regs ? rb.place(false, G, U, w0[T], na, nb, ca, cb, lane)
-                               : place_greedy(cnt, fill, false, G, U, w0[T], na, nb, ca, cb, lane);
-            if (lane == 0) slot_of[oo] = (uint16_t)s;
-          } else if (lane == 0) {
-            slot_of[oo] = 0xFFFFu;
-          }
-          ++rank;
+        const bool mine = o < W && (info[o] >> 10) == (uint32_t)T;
+        const uint64_t mk = __ballot(mine);
+        const int r = base + (int)__popcll(mk & ((1ull << lane) - 1ull));
+        if (mine) {
+          rank_of[o] = (uint16_t)r;
+          if (r >= cap) slot_of[o] = 0xFFFFu;
         }
+        base += (int)__popcll(mk);
       }
-      if (regs && lane < G) fill[bin_group(false, lane, U, w0[T])] = rb.fill;
+    }
+    __syncthreads();
+    // type bins: wave w, the k-th wave of its type, places that type's ranks
+    // [64 U k, 64 U (k + 1)) into its own 2 U groups
+    {
+      const int T = wtt[wave], k = wave - w0[T];
+      if (U > 0 && m[T] > 0 && k >= 0 && k < m[T]) {
+        const int lo = 64 * U * k, hi = lo + 64 * U, G = 2 * U;
+        const bool na = tt_needs_a(T), nb = tt_needs_b(T);
+        RegBin rb;
+        for (int o0 = 0; o0 < W; o0 += 64) {
+          const int o = o0 + lane;
+          const uint32_t in = o < W ? info[o] : 0xFFFFu;
+          const int r = o < W ? (int)rank_of[o] : -1;
+          const uint64_t mk0 = __ballot((in >> 10) == (uint32_t)T && r >= lo && r < hi);
+          uint64_t mk = mk0;
+          while (mk) {
+            const int src = __ffsll((long long)mk) - 1;
+            mk &= mk - 1;
+            const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
+            const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
+            const int sl = rb.place(false, G, U, wave, na, nb, ca, cb, lane);
+            if (lane == 0) slot_of[o0 + src] = (uint16_t)sl;
+          }
+        }
+        if (lane < G) fill[bin_group(false, lane, U, wave)] = rb.fill;
+      }
     }
     __syncthreads();
     // generic bin (wave 0): what the type bins left, in index order
