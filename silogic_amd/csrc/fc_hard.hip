@@ -1178,8 +1178,8 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_place_kernel(PlaceNet n
 // lowest group), among groups with a free slot (bins of up to 64 groups keep
 // their counts in registers, saturating at 3). Each wave places the outputs
 // of its own rows (the k-th wave of type T takes that type's ranks
-// [64 U k, 64 U (k + 1))), all waves at once; then wave 0 places the
-// generic bin. Uniform
+// [64 U k, 64 U (k + 1))), all waves at once; then four waves place the
+// generic bin, each every fourth output into every fourth group. Uniform
 // rows get codes (a << 16) | b with absolute word indices (the read buffer
 // of layer l starts at word (l & 1) * MAXO * 1024); generic rows get compact
 // codes on the renamed operands; unused slots get codes reading word 0 of
@@ -1274,8 +1274,10 @@ struct RegBin {
   int fill = 0;
   uint32_t a1 = 0, a2 = 0, a3 = 0, b1 = 0, b2 = 0, b3 = 0;
 
+  // group q of the bin: bin_group(generic, q, U, w0), or for a generic
+  // sub-bin of every gs-th group from go: U * 32 + q * gs + go
   __device__ int place(bool generic, int G, int U, int w0, bool na, bool nb, int ca, int cb,
-                       int lane) {
+                       int lane, int gs = 1, int go = 0) {
     const uint32_t ba = 1u << ca, bb = 1u << cb;
     const uint32_t pa = na ? (uint32_t)((a1 & ba) != 0) + ((a2 & ba) != 0) + ((a3 & ba) != 0) : 0u;
     const uint32_t pb = nb ? (uint32_t)((b1 & bb) != 0) + ((b2 & bb) != 0) + ((b3 & bb) != 0) : 0u;
@@ -1290,7 +1292,7 @@ struct RegBin {
       if (na) { a3 |= a2 & ba; a2 |= a1 & ba; a1 |= ba; }
       if (nb) { b3 |= b2 & bb; b2 |= b1 & bb; b1 |= bb; }
     }
-    return bin_group(generic, q, U, w0) * 32 + f;
+    return (generic ? U * 32 + q * gs + go : bin_group(false, q, U, w0)) * 32 + f;
   }
 };
 
@@ -1402,28 +1404,40 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
       }
     }
     __syncthreads();
-    // generic bin (wave 0): what the type bins left, in index order
-    if (wave == 0) {
+    // generic bin: what the type bins left, in index order. Up to 256
+    // groups it is split over four waves: wave j takes the outputs of
+    // generic rank j, j + 4, ... into groups j, j + 4, ...; larger bins are
+    // placed by wave 0 alone.
+    {
       const int G = 32 * (plan_rows - U);
-      const bool regs = G <= 64;
-      RegBin rb;
-      for (int o0 = 0; o0 < W; o0 += 64) {
-        const int o = o0 + lane;
-        const bool left = o < W && slot_of[o] == 0xFFFFu;
-        const uint32_t in = left ? info[o] : 0u;
-        const uint32_t a = in & 31u, b = (in >> 5) & 31u;
-        uint64_t mk = __ballot(left);
-        while (mk) {
-          const int src = __ffsll((long long)mk) - 1;
-          mk &= mk - 1;
-          const int ca = __builtin_amdgcn_readlane((int)(a & 31u), src);
-          const int cb = __builtin_amdgcn_readlane((int)(b & 31u), src);
-          const int s = regs ? rb.place(true, G, U, 0, true, true, ca, cb, lane)
-                             : place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
-          if (lane == 0) slot_of[o0 + src] = (uint16_t)s;
+      const int NS = G <= 256 ? 4 : 1;
+      if (wave < NS) {
+        const int Gs = G / NS;
+        const bool regs = Gs <= 64;
+        RegBin rb;
+        int base = 0;
+        for (int o0 = 0; o0 < W; o0 += 64) {
+          const int o = o0 + lane;
+          // generic: ranked past its type's waves (a test on data no wave
+          // writes here, so all four waves see the same ranks)
+          const bool left = o < W && (int)rank_of[o] >= 64 * U * m[info[o] >> 10];
+          const uint64_t ml = __ballot(left);
+          const int r = base + (int)__popcll(ml & ((1ull << lane) - 1ull));
+          base += (int)__popcll(ml);
+          const uint32_t in = left ? info[o] : 0u;
+          uint64_t mk = __ballot(left && r % NS == wave);
+          while (mk) {
+            const int src = __ffsll((long long)mk) - 1;
+            mk &= mk - 1;
+            const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
+            const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
+            const int sl = regs ? rb.place(true, Gs, U, 0, true, true, ca, cb, lane, NS, wave)
+                                : place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
+            if (lane == 0) slot_of[o0 + src] = (uint16_t)sl;
+          }
         }
+        if (regs && lane < Gs) fill[U * 32 + lane * NS + wave] = rb.fill;
       }
-      if (regs && lane < G) fill[bin_group(true, lane, U, 0)] = rb.fill;
     }
     __syncthreads();
     // codes, slots and unused slots (codes stored thread-major)
