@@ -355,8 +355,8 @@ int slg_fc_hard_place_net(int32_t n_layers, const int64_t* widths, const uint32_
 /* 64 or 32 = samples per workgroup slg_fc_hard_net would use, 0 = unsupported. */
 int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C);
 /* Slots per layer (MAXO * 1024) of the type-uniform layout below for a
- * network of inputs IN0 (at most 1024) and these widths, or 0 when it does
- * not apply (a 64-sample column must fit LDS). */
+ * network of inputs IN0 and these widths (each at most 16384), or 0 when it
+ * does not apply (a 32-sample column must fit LDS). */
 int64_t slg_fc_hard_type_slots(int64_t IN0, int32_t n_layers, const int64_t* widths);
 /* Type-uniform placement of a fused network's outputs (no counterpart in the
  * reference: a relabelling of LogicNet.forward_hard's circuit, models.py:
@@ -376,10 +376,12 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
                                const uint32_t* const* codes, uint32_t* const* placed,
                                int32_t* plan, int32_t* perm_ws, int64_t perm_ws_len,
                                slg_stream_t stream);
-/* slg_fc_hard_net (in_kind 0 or 1, no wire residual) on the placed codes and
- * plan of slg_fc_hard_type_place_net; widths are the layers' widths, as
- * given to the placement. Same logits, bit for bit. No counterpart in the
- * reference beyond slg_fc_hard_net's. */
+/* slg_fc_hard_net (no wire residual) on the placed codes and plan of
+ * slg_fc_hard_type_place_net; widths are the layers' widths, as given to the
+ * placement. Unpacked rows (in_kind 0 or 1) need IN0 <= 1024 and 64-sample
+ * tiles (slg_fc_hard_net_supported() == 64); packed input (2 or 3) takes
+ * either. Same logits, bit for bit. No counterpart in the reference beyond
+ * slg_fc_hard_net's. */
 int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
                           const int64_t* widths, const uint32_t* const* codes, const int32_t* plan,
                           int32_t C, float* logits, slg_stream_t stream);

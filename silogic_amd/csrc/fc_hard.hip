@@ -292,6 +292,11 @@ struct NetDesc {
   int maxw;  // words per activation buffer: MAXO * 1024 (every row of every layer)
   const int32_t* plan;  // type-uniform layout ([n_layers][kPlanStride]), or null
 };
+// The network kernels take the descriptor as their first argument and read
+// it through the kernel-argument segment (constant memory): its per-layer
+// arrays are indexed by the layer number, and read that way the loads stay
+// scalar instead of going through a private copy of the struct.
+typedef __attribute__((address_space(4))) const NetDesc const_netdesc_t;
 
 // Codes of this thread's outputs o = tid + j*1024 of a W-wide layer, read
 // through a raw buffer resource of W codes: offsets past it read 0 (a valid
@@ -763,16 +768,18 @@ __device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int b
 }
 
 // Pre-packed input: LAYOUT 0 = [in0][nw] (reference layout), 1 = [nw][in0].
-template <int LAYOUT, typename WT, int MAXO>
+template <int LAYOUT, typename WT, int MAXO, bool TYPED>
 __global__ void __launch_bounds__(kNetThreads)
-fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDesc d,
+fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, int nw,
                           float* __restrict__ logits) {
+  const_netdesc_t& d = *(const_netdesc_t*)__builtin_amdgcn_kernarg_segment_ptr();
   constexpr int SPW = (int)sizeof(WT) * 8;
   extern __shared__ __align__(16) unsigned char smem[];
   WT* lds = reinterpret_cast<WT*>(smem);
   const int tile = blockIdx.x;
   uint32_t cb[MAXO];
-  load_codes(cb, d.codes[0], d.width[0]);
+  if constexpr (TYPED) load_codes_tm(cb, d.codes[0]);
+  else load_codes(cb, d.codes[0], d.width[0]);
   const int w64 = tile / (64 / SPW);
   for (int i = threadIdx.x; i < d.in0; i += kNetThreads) {
     const uint64_t word = LAYOUT == 0 ? xp[(int64_t)i * nw + w64] : xp[(int64_t)w64 * d.in0 + i];
@@ -785,9 +792,15 @@ fc_hard_net_packed_kernel(const uint64_t* __restrict__ xp, int B, int nw, NetDes
     const int W = d.width[l];
     uint32_t nb[MAXO];
     const int ln = (l + 1 < d.n_layers) ? l + 1 : l;
-    load_codes(nb, d.codes[ln], d.width[ln]);
-    layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cb);
-    if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
+    if constexpr (TYPED) {
+      load_codes_tm(nb, d.codes[ln]);
+      typed_step<WT, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(
+          lds, cur, nxt, d.plan + l * kPlanStride, cb, NoWork());
+    } else {
+      load_codes(nb, d.codes[ln], d.width[ln]);
+      layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cb);
+      if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
+    }
     __syncthreads();
     const int t = cur; cur = nxt; nxt = t;
     cur_w = W;
@@ -853,12 +866,6 @@ __device__ inline void fold_chunk(uint64_t& word, const IT (&val)[CH], int chunk
   for (int j = CH - 1; j >= 0; --j) bits = (bits << 1) | (input_bit(val[j]) ? 1u : 0u);
   word |= (uint64_t)bits << (chunk * CH);
 }
-
-// The descriptor is the kernel's first argument and is read through the
-// kernel-argument segment (constant memory): its per-layer arrays are
-// indexed by the layer number, and read that way the loads stay scalar
-// instead of going through a private copy of the struct.
-typedef __attribute__((address_space(4))) const NetDesc const_netdesc_t;
 
 template <typename IT, int MAXO, bool TYPED, int CH>
 __global__ void __launch_bounds__(kNetThreads)
@@ -1535,10 +1542,11 @@ static int set_lds(K kern, size_t lds, const char* what) {
 template <int LAYOUT, typename WT, int MAXO>
 static int launch_net_packed(const uint64_t* xp, int B, const NetDesc& d, size_t lds, int64_t tiles,
                              float* logits, hipStream_t st) {
-  auto kern = fc_hard_net_packed_kernel<LAYOUT, WT, MAXO>;
+  auto kern = d.plan ? fc_hard_net_packed_kernel<LAYOUT, WT, MAXO, true>
+                     : fc_hard_net_packed_kernel<LAYOUT, WT, MAXO, false>;
   if (int rc = set_lds(kern, lds, "fc_hard_net")) return rc;
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kNetThreads), lds, st, xp, B,
-                     (int)cdiv(B, 64), d, logits);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kNetThreads), lds, st, d, xp, B,
+                     (int)cdiv(B, 64), logits);
   SLG_LAUNCH_CHECK("fc_hard_net");
   return 0;
 }
@@ -1726,14 +1734,14 @@ int slg_fc_hard_place_net(int32_t n_layers, const int64_t* widths, const uint32_
 }
 
 int64_t slg_fc_hard_type_slots(int64_t IN0, int32_t n_layers, const int64_t* widths) {
-  if (!widths || n_layers < 1 || n_layers > kMaxLayers || IN0 < 1 || IN0 > kNetThreads) return 0;
+  if (!widths || n_layers < 1 || n_layers > kMaxLayers || IN0 < 1 || IN0 > kPlaceMax) return 0;
   int64_t maxw = IN0;
   for (int l = 0; l < n_layers; ++l) {
     if (widths[l] < 1) return 0;
     maxw = std::max<int64_t>(maxw, widths[l]);
   }
   const int maxo = maxw <= kPlaceMax ? pick_maxo(maxw) : 0;
-  if (maxo == 0 || net_spw(IN0, n_layers, widths, 1) != 64) return 0;
+  if (maxo == 0 || net_spw(IN0, n_layers, widths, 1) == 0) return 0;
   return (int64_t)maxo * kNetThreads;
 }
 
@@ -1747,8 +1755,8 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
               "fc_hard_type_place_net: %d layers", n_layers);
   const int64_t S = slg_fc_hard_type_slots(IN0, n_layers, widths);
   SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED,
-              "fc_hard_type_place_net: needs inputs <= %d wide and a network whose 64-sample "
-              "column fits LDS", kNetThreads);
+              "fc_hard_type_place_net: needs inputs and widths <= %d and a network whose "
+              "32-sample column fits LDS", kPlaceMax);
   TypePlaceNet n{};
   n.L = n_layers;
   n.maxo = (int)(S / kNetThreads);
@@ -1778,14 +1786,18 @@ int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0
                           int32_t C, float* logits, slg_stream_t stream) {
   SLG_REQUIRE(widths && codes && plan && ((x && logits) || B == 0), SLG_E_ARG,
               "fc_hard_net_typed: null pointer");
-  SLG_REQUIRE(in_kind == 0 || in_kind == 1, SLG_E_ARG,
-              "fc_hard_net_typed: in_kind %d (unpacked fp32 or uint8 rows only)", in_kind);
+  SLG_REQUIRE(in_kind >= 0 && in_kind <= 3, SLG_E_ARG, "fc_hard_net_typed: in_kind %d", in_kind);
   SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE, "fc_hard_net_typed: %d layers",
               n_layers);
-  SLG_REQUIRE(B >= 0 && B < (1LL << 31) && IN0 > 0 && IN0 <= kNetThreads, SLG_E_SHAPE,
+  SLG_REQUIRE(B >= 0 && B < (1LL << 31) && IN0 > 0 && IN0 <= kPlaceMax, SLG_E_SHAPE,
               "fc_hard_net_typed: bad sizes");
   const int64_t S = slg_fc_hard_type_slots(IN0, n_layers, widths);
   SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "fc_hard_net_typed: widths do not fit LDS");
+  const int spw = net_spw(IN0, n_layers, widths, 1);
+  const bool rows = in_kind <= 1;
+  SLG_REQUIRE(!rows || (spw == 64 && IN0 <= kNetThreads), SLG_E_UNSUPPORTED,
+              "fc_hard_net_typed: unpacked rows need 64-sample tiles and IN0 <= %d; pack first",
+              kNetThreads);
   NetDesc d{};
   for (int l = 0; l < n_layers; ++l) {
     SLG_REQUIRE(codes[l], SLG_E_ARG, "fc_hard_net_typed: layer %d", l);
@@ -1800,10 +1812,17 @@ int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0
   d.maxw = (int)S;
   d.plan = plan;
   const int maxo = (int)(S / kNetThreads);
-  const size_t lds = (size_t)2 * d.maxw * 8;
+  const size_t lds = (size_t)2 * d.maxw * (spw / 8);
   hipStream_t st = as_stream(stream);
   if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
-  return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
+  if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
+  const int64_t tiles = cdiv(B, spw);
+  const uint64_t* xp = (const uint64_t*)x;
+  if (in_kind == 2)
+    return spw == 64 ? net_packed_maxo<0, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
+                     : net_packed_maxo<0, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
+  return spw == 64 ? net_packed_maxo<1, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
+                   : net_packed_maxo<1, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
 }
 
 int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C) {

@@ -97,11 +97,11 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
         return ops.groupsum_packed(xp, B, C)
     if spw:
         rows = in_kind in (ops.ROWS_F32, ops.ROWS_U8) and spw == 64 and in_dim <= 1024
-        # one gate type per wave row where the rows kernel runs (rows of
-        # inputs, no wire residual), else a bank-aware output order; both
-        # relabel the circuit (the logits are the same bits). The wire
-        # residual copies inputs by position, so it keeps the order.
-        typed = rows and not wire_r and typable
+        # one gate type per wave row where the layout fits, else a bank-aware
+        # output order; both relabel the circuit (the logits are the same
+        # bits). The wire residual copies inputs by position, so it keeps
+        # the order.
+        typed = not wire_r and typable
 
         def build():
             codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True)

@@ -629,7 +629,7 @@ def fc_hard_type_slots(in_dim, widths):
 
 def fc_hard_type_place_net(codes, in_dim):
     """Type-uniform placement of a fused network's compact codes
-    (``slg_fc_hard_type_place_net``) for unpacked-row inputs ``in_dim`` wide:
+    (``slg_fc_hard_type_place_net``) for inputs ``in_dim`` wide:
     every layer but the last becomes ``fc_hard_type_slots`` slots whose first
     rows hold one gate type per wave, with the next layer's operands renamed;
     the logits of ``fc_hard_net`` are unchanged. Returns a :class:`NetCodes`
@@ -659,8 +659,8 @@ class NetCodes(list):
     int32 tensors) with their width and pointer arrays for the C ABI, built
     once: the tensors must not be replaced or resized afterwards. ``plan``
     (with the ``in_dim`` it was placed for) marks codes laid out by
-    :func:`fc_hard_type_place_net`, which only the unpacked-row network
-    kernel reads."""
+    :func:`fc_hard_type_place_net`, which the network kernels read without a
+    wire residual."""
 
     def __init__(self, codes, plan=None, in_dim=None, widths=None):
         super().__init__(codes)
@@ -686,8 +686,8 @@ def fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r=0):
     w_arr, c_arr = codes.widths, codes.ptrs
     out = torch.empty((B, C), device=x.device, dtype=torch.float32)
     if codes.plan is not None:
-        if in_kind not in (ROWS_F32, ROWS_U8) or wire_r or in_dim != codes.in_dim:
-            raise ValueError("fc_hard_net: type-placed codes take unpacked rows %s wide and no "
+        if wire_r or in_dim != codes.in_dim:
+            raise ValueError("fc_hard_net: type-placed codes take inputs %s wide and no "
                              "wire residual" % codes.in_dim)
         _lib.call("slg_fc_hard_net_typed", _p(x), in_kind, B, in_dim, len(codes), w_arr, c_arr,
                   _p(codes.plan), C, _p(out), _stream(x))

@@ -1,15 +1,16 @@
-"""Type-uniform placement of the fused hard network on unpacked rows
-(slg_fc_hard_type_place_net + slg_fc_hard_net_typed): a relabelling of the
-circuit in which each wave's first rows hold one gate type, so the logits
-must be the same bits as the unplaced network's, whatever the mix of gate
-types (uniform draws, or one type dominating so that it takes several waves
-and the plan shrinks U)."""
+"""Type-uniform placement of the fused hard network
+(slg_fc_hard_type_place_net + slg_fc_hard_net_typed) on unpacked rows and
+packed words: a relabelling of the circuit in which each wave's first rows
+hold one gate type, so the logits must be the same bits as the unplaced
+network's, whatever the mix of gate types (uniform draws, or one type
+dominating so that it takes several waves and the plan shrinks U)."""
 import pytest
 import torch
 
 import silogic_amd as sl
 from oracle import torch_ref
 from silogic_amd import ops
+from silogic_amd._lib import HipError
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -79,12 +80,40 @@ def test_typed_network_is_bit_exact(in_dim, widths, C, skew):
     assert torch.equal(got8, ref)
 
 
-def test_typed_codes_refuse_packed_input():
-    net = _net(100, [300, 300, 30])
-    typed = ops.fc_hard_type_place_net(_codes(net), 100)
-    xp = ops.pack_bits(torch.zeros(64, 100, device=DEV), word_major=True)
+@pytest.mark.parametrize("in_dim,widths,C,skew", [
+    (784, [2000, 2000, 2000], 10, None),        # 64-sample words, MAXO 2
+    (1500, [1500, 1500, 30], 5, (6, 0.6)),      # inputs wider than a workgroup
+    (4096, [8000, 8000, 50], 10, None),         # MAXO 8
+    (2000, [16380, 16380, 100], 10, (3, 0.3)),  # MAXO 16: 32-sample words
+])
+def test_typed_network_on_packed_input_is_bit_exact(in_dim, widths, C, skew):
+    """Packed input ([in0][nw] and [nw][in0]) through the type-placed codes:
+    the logits of the unplaced network, bit for bit, for 64- and 32-sample
+    words."""
+    net = _net(in_dim, widths, skew, seed=41)
+    codes = _codes(net)
+    typed = ops.fc_hard_type_place_net(codes, in_dim)
+    _check_plan(typed, widths, in_dim)
+    g = torch.Generator().manual_seed(7)
+    B = 64 * 5 + 29
+    x = (torch.rand(B, in_dim, generator=g) < 0.45).float().to(DEV)
+    ref = ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, codes, C) if in_dim <= 1024 else None
+    for word_major, kind in ((False, ops.PACKED), (True, ops.PACKED_WORD_MAJOR)):
+        xp = ops.pack_bits(x, word_major=word_major)
+        plain = ops.fc_hard_net(xp, kind, B, in_dim, codes, C)
+        if ref is not None:
+            assert torch.equal(plain, ref)
+        assert torch.equal(ops.fc_hard_net(xp, kind, B, in_dim, typed, C), plain)
+
+
+def test_typed_codes_refuse_rows_wider_than_a_workgroup():
+    net = _net(1500, [1500, 30])
+    typed = ops.fc_hard_type_place_net(_codes(net), 1500)
+    x = torch.zeros(64, 1500, device=DEV)
+    with pytest.raises(HipError):
+        ops.fc_hard_net(x, ops.ROWS_F32, 64, 1500, typed, 10)
     with pytest.raises(ValueError):
-        ops.fc_hard_net(xp, ops.PACKED_WORD_MAJOR, 64, 100, typed, 10)
+        ops.fc_hard_net(ops.pack_bits(x), ops.PACKED, 64, 1500, typed, 10, wire_r=8)
 
 
 def test_config_2_typed_forward_hard_matches_the_oracle():
