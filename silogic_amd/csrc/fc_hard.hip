@@ -341,6 +341,15 @@ __device__ inline WT gate_compact(WT a, WT b, uint32_t c) {
   }
 }
 
+// Operand reads are issued at raised wave priority. Every wave of the
+// workgroup is in the same phase of a layer (a barrier ends each one), so
+// the waves that still have LDS reads to issue would otherwise wait behind
+// those already computing gates; with the reads first, the LDS queue fills
+// sooner and the gate math overlaps it (config 2's fused network 63.2 ->
+// 61.4 us, the same bits).
+__device__ __forceinline__ void reads_begin() { __builtin_amdgcn_s_setprio(1); }
+__device__ __forceinline__ void reads_end() { __builtin_amdgcn_s_setprio(0); }
+
 // One layer on the LDS column: lds[nxt + o] = gate_o(lds[cur + a_o], lds[cur + b_o])
 // for this thread's outputs o = tid + j*1024, in groups of GRP outputs: all
 // operand reads of a group are issued before its results are computed, so
@@ -362,12 +371,14 @@ __device__ __forceinline__ void layer_step(WT* lds, int cur, int nxt, int W,
   for (int g0 = 0; g0 < MAXO; g0 += GRP) {
     if (g0 >= rows) break;                               // wave-uniform
     WT va[GRP], vb[GRP];
+    reads_begin();
 #pragma unroll
     for (int u = 0; u < GRP; ++u) {
       const uint32_t c = cb[g0 + u];
       va[u] = src[(c >> 14) & 0x3FFFu];
       vb[u] = src[c & 0x3FFFu];
     }
+    reads_end();
     // all gate math, then all writes: no LDS access between the computes
     WT r[GRP];
 #pragma unroll
@@ -455,12 +466,14 @@ __device__ __forceinline__ void uniform_group(uint32_t base, WT* dst, int g0,
                                               const uint32_t (&cb)[MAXO], F&& between = F()) {
   constexpr int SZ = (int)sizeof(WT);
   WT va[N], vb[N];
+  reads_begin();
 #pragma unroll
   for (int u = 0; u < N; ++u) {
     va[u] = vb[u] = (WT)0;
     if constexpr (tt_needs_a(TT)) va[u] = lds_word<WT>(field_addr<SZ, true>(cb[g0 + u], base));
     if constexpr (tt_needs_b(TT)) vb[u] = lds_word<WT>(field_addr<SZ, false>(cb[g0 + u], base));
   }
+  reads_end();
   between();
   WT r[N];
 #pragma unroll
@@ -508,7 +521,9 @@ __device__ __forceinline__ void generic_rows(const WT* src, WT* dst, int U, int 
     for (int j = J; j < MAXO; ++j) {
       if (j >= rows) break;                              // wave-uniform
       const uint32_t c = cb[j];
+      reads_begin();
       const WT a = src[(c >> 14) & 0x3FFFu], b = src[c & 0x3FFFu];
+      reads_end();
       dst[j * kNetThreads] = gate_compact<WT>(a, b, c);
     }
   }
@@ -529,6 +544,7 @@ __device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT
 #pragma unroll
   for (int g0 = GRP; g0 < LG; g0 += GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, g0, cb);
   WT va[N], vb[N];
+  reads_begin();
 #pragma unroll
   for (int u = 0; u < N; ++u) {
     va[u] = vb[u] = (WT)0;
@@ -537,6 +553,7 @@ __device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT
   }
   const uint32_t c = cb[MAXO - 1];
   const WT ga = src[(c >> 14) & 0x3FFFu], gb = src[c & 0x3FFFu];
+  reads_end();
   WT r[N];
 #pragma unroll
   for (int u = 0; u < N; ++u) r[u] = gate_tt<TT, WT>(va[u], vb[u]);
@@ -714,11 +731,13 @@ __device__ __forceinline__ int class_count(const uint32_t* cls32, int G, int lan
     const int nvalid = G - q0;
     const uint32_t* p = cls32 + (q0 + l) * NH + h;
     uint32_t w[WPL];
+    reads_begin();
 #pragma unroll
     for (int j = 0; j < WPL; ++j) {
       if (j * LSTRIDE + LSTRIDE <= nvalid) w[j] = p[j * LSTRIDE * NH];
       else w[j] = j * LSTRIDE + l < nvalid ? p[j * LSTRIDE * NH] : 0u;
     }
+    reads_end();
     uint32_t x[11];
 #pragma unroll
     for (int k = 0; k < 11; ++k) x[k] = 0;
