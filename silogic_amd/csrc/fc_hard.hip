@@ -562,21 +562,29 @@ __device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT
   dst[(MAXO - 1) * kNetThreads] = gate_compact<WT>(ga, gb, c);
 }
 
-// One layer of a planned network: the wave's uniform rows, then rows
-// U..rows-1 from compact codes (as layer_step).
-// The plan is read as constant memory, so its loads are scalar: a vector
-// load would retire in order behind the layer's input-row loads and wait
-// for them.
+// A layer's plan as the wave reads it: U, the rows computed, its truth
+// table. The plan is read as constant memory, so its loads are scalar: a
+// vector load would retire in order behind the layer's input-row loads and
+// wait for them.
 typedef __attribute__((address_space(4))) const int32_t const_i32_t;
 
-template <typename WT, int MAXO, int GRP, typename F>
-__device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, const int32_t* plan,
-                                           const uint32_t (&cb)[MAXO], F&& filler) {
-  const const_i32_t* pl = (const const_i32_t*)plan;
+struct PlanRow {
+  int U, rows, tt;
+};
+
+__device__ __forceinline__ PlanRow plan_row(const int32_t* plan, int l) {
+  const const_i32_t* pl = (const const_i32_t*)(plan + l * kPlanStride);
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int U = __builtin_amdgcn_readfirstlane(pl[0]);
-  const int rows = __builtin_amdgcn_readfirstlane(pl[1]);
-  const int tt = __builtin_amdgcn_readfirstlane(pl[2 + wave]);
+  return {__builtin_amdgcn_readfirstlane(pl[0]), __builtin_amdgcn_readfirstlane(pl[1]),
+          __builtin_amdgcn_readfirstlane(pl[2 + wave])};
+}
+
+// One layer of a planned network: the wave's uniform rows, then rows
+// U..rows-1 from compact codes (as layer_step).
+template <typename WT, int MAXO, int GRP, typename F>
+__device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, PlanRow pr,
+                                           const uint32_t (&cb)[MAXO], F&& filler) {
+  const int U = pr.U, rows = pr.rows, tt = pr.tt;
   const uint32_t base = (uint32_t)(uintptr_t)lds;
   const WT* src = lds + cur;
   WT* dst = lds + nxt + threadIdx.x;
@@ -814,7 +822,7 @@ fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, 
     if constexpr (TYPED) {
       load_codes_tm(nb, d.codes[ln]);
       typed_step<WT, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(
-          lds, cur, nxt, d.plan + l * kPlanStride, cb, NoWork());
+          lds, cur, nxt, plan_row(d.plan, l), cb, NoWork());
     } else {
       load_codes(nb, d.codes[ln], d.width[ln]);
       layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cb);
@@ -921,6 +929,15 @@ fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_til
   uint32_t cb[MAXO];
   if constexpr (TYPED) load_codes_tm(cb, d.codes[0]);
   else load_codes(cb, d.codes[0], d.width[0]);
+  // typed: the plan row of the layer about to run and the codes pointer of
+  // the one after it are scalar-loaded a layer ahead, so no layer starts
+  // with two dependent scalar-load round trips after its barrier
+  PlanRow pc{};
+  const uint32_t* cn = nullptr;
+  if constexpr (TYPED) {
+    pc = plan_row(d.plan, 0);
+    cn = d.codes[L > 1 ? 1 : 0];
+  }
 
   for (; tile < n_tiles; tile += gridDim.x) {
     if (fv) lds[f] = word;
@@ -937,8 +954,15 @@ fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_til
       const int W = d.width[l];
       const int ln = (l + 1 < L) ? l + 1 : 0;  // after the last layer: layer 0 of the next tile
       uint32_t nb[MAXO];
-      if constexpr (TYPED) load_codes_tm(nb, d.codes[ln]);
-      else load_codes(nb, d.codes[ln], d.width[ln]);
+      PlanRow pn{};
+      const uint32_t* cnn = nullptr;
+      if constexpr (TYPED) {
+        load_codes_tm(nb, cn);
+        pn = plan_row(d.plan, ln);
+        cnn = d.codes[(ln + 1 < L) ? ln + 1 : 0];
+      } else {
+        load_codes(nb, d.codes[ln], d.width[ln]);
+      }
       auto rows_work = [&]() __attribute__((always_inline)) {
         if (l >= 2 && l - 2 < NCH) fold_chunk<CH>(nword, val, l - 2);
         issue_chunk<CH>(val, r, voff0, rowb, l);
@@ -947,10 +971,10 @@ fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_til
       if constexpr (TYPED && CH < 16) {
         // the row work overlaps the first operand reads (16-sample chunks
         // hold too many registers for that)
-        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, d.plan + l * kPlanStride, cb, rows_work);
+        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, pc, cb, rows_work);
       } else if constexpr (TYPED) {
         rows_work();
-        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, d.plan + l * kPlanStride, cb, NoWork());
+        typed_step<uint64_t, MAXO, GRP>(lds, cur, nxt, pc, cb, NoWork());
       } else {
         rows_work();
         layer_step<uint64_t, MAXO, GRP>(lds, cur, nxt, W, cb);
@@ -961,6 +985,10 @@ fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_til
       cur_w = W;
 #pragma unroll
       for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
+      if constexpr (TYPED) {
+        pc = pn;
+        cn = cnn;
+      }
     };
     for (int l = 0; l < L; l += 2) {
       layer(l, val0);
