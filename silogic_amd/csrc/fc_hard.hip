@@ -815,14 +815,26 @@ fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, 
   }
   __syncthreads();
   int cur = 0, nxt = d.maxw, cur_w = d.in0;
-  for (int l = 0; l < d.n_layers; ++l) {
+  const int L = d.n_layers;
+  // typed: plan row and next codes pointer scalar-loaded a layer ahead
+  PlanRow pc{};
+  const uint32_t* cn = nullptr;
+  if constexpr (TYPED) {
+    pc = plan_row(d.plan, 0);
+    cn = d.codes[L > 1 ? 1 : 0];
+  }
+  for (int l = 0; l < L; ++l) {
     const int W = d.width[l];
     uint32_t nb[MAXO];
-    const int ln = (l + 1 < d.n_layers) ? l + 1 : l;
+    const int ln = (l + 1 < L) ? l + 1 : l;
     if constexpr (TYPED) {
-      load_codes_tm(nb, d.codes[ln]);
+      load_codes_tm(nb, cn);
+      const PlanRow pn = plan_row(d.plan, ln);
+      const uint32_t* cnn = d.codes[(ln + 1 < L) ? ln + 1 : ln];
       typed_step<WT, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(
-          lds, cur, nxt, plan_row(d.plan, l), cb, NoWork());
+          lds, cur, nxt, pc, cb, NoWork());
+      pc = pn;
+      cn = cnn;
     } else {
       load_codes(nb, d.codes[ln], d.width[ln]);
       layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cb);
