@@ -1,10 +1,10 @@
 """A forward replayed from a HIP graph, for callers with static input buffers
 (serving loops, fixed-shape batches).
 
-``forward_hard`` of a conv network is a dozen short kernels, and the host
-work around them (cache-key walks over the parameters, argument marshalling,
-output allocation) takes longer than the kernels themselves; captured once,
-each call is one graph launch. The graph keeps the tensors it was captured
+A forward of several short kernels costs host work around them (cache-key
+walks over the parameters, argument marshalling, output allocation) that can
+take as long as the kernels themselves; captured once, each call is one
+graph launch. The graph keeps the tensors it was captured
 on: each call writes its batch into the captured inputs (or passes them
 unchanged) and reads the captured output, which the next call overwrites.
 The parameters must not be replaced or modified after capture (the derived

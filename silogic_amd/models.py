@@ -16,6 +16,8 @@ GroupSum popcount at the end (``slg_fc_hard_net``), conv blocks as packed
 tree + OR-pool kernels. It returns the same raw integer counts as the
 reference's ``GroupSum.forward_hard`` (heads.py:41-45).
 """
+import ctypes
+
 import torch
 import torch.nn as nn
 
@@ -71,6 +73,34 @@ def _soft_fc_stack(layers, head, x, wire_r):
     return out if plan.head is not None else head(out)
 
 
+def _hard_fc_plan(layers, in_dim, C):
+    """``(lut, widths, spw, typable)`` of an FC stack's hard forward: LUT
+    layers run one packed kernel each; otherwise ``spw`` (64 or 32) says the
+    fused network fits LDS and ``typable`` that the type-uniform layout
+    applies."""
+    def plan():
+        widths = [layer.out_dim for layer in layers]
+        lut = any(layer.is_lut for layer in layers)
+        spw = 0 if lut else ops.fc_hard_net_supported(in_dim, widths, C)
+        return lut, widths, spw, spw and ops.fc_hard_type_slots(in_dim, widths) > 0
+
+    return derived.cached(
+        layers[0], "_derived_net_plan", (in_dim, C, tuple(id(layer) for layer in layers)), plan)
+
+
+def _hard_fc_net_codes(layers, in_dim, wire_r, typed):
+    """The fused network's codes (cached per parameter version): type-placed
+    when ``typed``, bank-placed without a wire residual, else in index order."""
+    def build():
+        codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True)
+        if typed:
+            return ops.fc_hard_type_place_net(codes, in_dim)
+        return ops.NetCodes(codes if wire_r else ops.fc_hard_place_net(codes))
+
+    return derived.cached(layers[0], "_derived_net_codes",
+                          (derived.state_key(*layers), bool(wire_r), typed), build)
+
+
 def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     """Run arity-2 FC layers as a packed circuit and return class counts.
 
@@ -78,14 +108,7 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
     fused into it when the input is at most 1024 features wide; otherwise one
     packed kernel per layer."""
-    def plan():
-        widths = [layer.out_dim for layer in layers]
-        lut = any(layer.is_lut for layer in layers)
-        spw = 0 if lut else ops.fc_hard_net_supported(in_dim, widths, C)
-        return lut, widths, spw, spw and ops.fc_hard_type_slots(in_dim, widths) > 0
-
-    lut, widths, spw, typable = derived.cached(
-        layers[0], "_derived_net_plan", (in_dim, C, tuple(id(layer) for layer in layers)), plan)
+    lut, widths, spw, typable = _hard_fc_plan(layers, in_dim, C)
     if lut:
         # LUT layers: one packed kernel per layer (gate or LUT)
         xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
@@ -101,16 +124,8 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
         # output order; both relabel the circuit (the logits are the same
         # bits). The wire residual copies inputs by position, so it keeps
         # the order.
-        typed = not wire_r and typable
-
-        def build():
-            codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers], compact=True)
-            if typed:
-                return ops.fc_hard_type_place_net(codes, in_dim)
-            return ops.NetCodes(codes if wire_r else ops.fc_hard_place_net(codes))
-
-        codes = derived.cached(layers[0], "_derived_net_codes",
-                               (derived.state_key(*layers), bool(wire_r), typed), build)
+        typed = bool(not wire_r and typable)
+        codes = _hard_fc_net_codes(layers, in_dim, wire_r, typed)
         if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not rows:
             x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
@@ -322,9 +337,23 @@ class LogicConvNet(nn.Module):
     @torch.no_grad()
     def forward_hard(self, x):
         ops.require_gpu(x)
+        step = self._hard_step(x)
+        if step is not None:
+            return step(x)
         B, C, H, W = x.shape
         xp = ops.pack_bits(x.reshape(B, -1))                  # [C*H*W, nw] = [C,H,W,nw]
         return self.forward_hard_packed(xp, B, (C, H, W))
+
+    def _hard_step(self, x):
+        """The launch sequence of ``forward_hard`` for ``x``'s shape on the
+        current stream (:class:`_HardConvStep`, cached per parameter
+        version), or None where the general path runs."""
+        if (x.dim() != 4 or x.dtype not in (torch.float32, torch.uint8) or not x.is_contiguous()
+                or self.wire_residual > 0 or torch.compiler.is_compiling()):
+            return None
+        key = (derived.state_key(self), tuple(x.shape), x.dtype, x.get_device(),
+               ops._stream(x).value)
+        return derived.cached(self, "_derived_hard_step", key, lambda: _HardConvStep.build(self, x))
 
     @torch.no_grad()
     def forward_hard_packed(self, xp, B, chw):
@@ -371,6 +400,80 @@ class LogicConvNet(nn.Module):
                 hw = hw // 2
         total += sum(self._head_widths)
         return total
+
+
+class _HardConvStep:
+    """``LogicConvNet.forward_hard`` for one input shape on one stream as a
+    fixed sequence of C-ABI launches: packing, every conv block (pooled),
+    the fused head. The per-call host work of the general path (parameter
+    walks for each table, shape checks, wrapper calls, an allocation per
+    intermediate) is done once here: the intermediate words live in buffers
+    this object keeps (the launches run in stream order, so a call's packing
+    cannot overtake the previous call's reads of them) and a call allocates
+    only its logits. The tables are the general path's own, so the logits
+    are the same bits."""
+
+    def __init__(self, calls, out_shape, in_slot, out_slot, bufs, tables):
+        self.calls, self.out_shape = calls, out_shape
+        self.in_slot, self.out_slot = in_slot, out_slot
+        self.bufs, self.tables = bufs, tables          # kept alive for the pointers
+
+    @staticmethod
+    def build(model, x):
+        from . import _lib
+        convs = list(model._convs())
+        if not convs or any(conv.generic for conv in convs):
+            return None
+        B, C, H, W = x.shape
+        nw = ops.n_words(B)
+        dev, st, lib = x.device, ops._stream(x), _lib.lib()
+        xp = torch.empty((C * H * W, nw), device=dev, dtype=torch.int64)
+        calls = [(lib.slg_pack_bits, "slg_pack_bits",
+                  [None, 1 if x.dtype == torch.uint8 else 0, B, C * H * W, 0, ops._p(xp), st])]
+        bufs, tables = [xp], []
+        params = derived.cached(
+            model, "_derived_conv_codes", derived.state_key(*convs),
+            lambda: ops.conv_hard_prep_net([conv.hard_spec() for conv in convs]))
+        cur = xp
+        for conv, (leaf, tt) in zip(convs, params):
+            k, pad = conv.kh, conv.padding
+            Hf, Wf = H + 2 * pad - k + 1, W + 2 * pad - k + 1
+            Ho, Wo = Hf // 2, Wf // 2                     # every block is OR-pooled
+            out = torch.empty((conv.n, Ho, Wo, nw), device=dev, dtype=torch.int64)
+            calls.append((lib.slg_conv_hard_fwd, "slg_conv_hard_fwd",
+                          [ops._p(cur), C, H, W, nw, conv.n, conv._kind(), conv.d,
+                           conv.node_arity, ops._p(leaf), ops._p(tt), k, pad, 1, ops._p(out), st]))
+            bufs.append(out)
+            tables += [leaf, tt]
+            cur, (C, H, W) = out, (conv.n, Ho, Wo)
+        in_dim, n_cls, layers = C * H * W, model.head.num_classes, list(model.head_layers)
+        if not layers:
+            return None
+        lut, widths, spw, typable = _hard_fc_plan(layers, in_dim, n_cls)
+        if lut or not spw:
+            return None
+        codes = _hard_fc_net_codes(layers, in_dim, 0, bool(typable))
+        tables.append(codes)
+        if codes.plan is not None:
+            head = (lib.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
+                    [ops._p(cur), ops.PACKED, B, in_dim, len(codes), codes.widths, codes.ptrs,
+                     ops._p(codes.plan), n_cls, None, st])
+        else:
+            head = (lib.slg_fc_hard_net, "slg_fc_hard_net",
+                    [ops._p(cur), ops.PACKED, B, in_dim, len(codes), codes.widths, codes.ptrs,
+                     n_cls, 0, None, st])
+        calls.append(head)
+        return _HardConvStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(head[2]) - 2),
+                             bufs, tables)
+
+    def __call__(self, x):
+        from . import _lib
+        out = torch.empty(self.out_shape, device=x.device, dtype=torch.float32)
+        self.calls[self.in_slot[0]][2][self.in_slot[1]] = ctypes.c_void_p(x.data_ptr())
+        self.calls[self.out_slot[0]][2][self.out_slot[1]] = ctypes.c_void_p(out.data_ptr())
+        for fn, name, args in self.calls:
+            _lib.check(fn(*args), name)
+        return out
 
 
 class LogicTreeNet(LogicConvNet):
