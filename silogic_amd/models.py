@@ -192,6 +192,14 @@ class LogicNet(nn.Module):
     def forward_hard(self, x):
         ops.require_gpu(x)
         ops.check_width(x, self.layers[0].in_dim)
+        if (x.dim() == 2 and x.dtype in (torch.float32, torch.uint8) and x.is_contiguous()
+                and not torch.compiler.is_compiling()):
+            key = (derived.state_key(self), tuple(x.shape), x.dtype, x.get_device(),
+                   ops._stream(x).value)
+            step = derived.cached(self, "_derived_hard_step", key,
+                                  lambda: _HardStep.for_fc(self, x))
+            if step is not None:
+                return step(x)
         x, kind = ops._in_kind(x)
         return _hard_fc_stack(self.layers, x, kind, x.shape[0], x.shape[1],
                               self.head.num_classes, self.wire_r)
@@ -346,14 +354,15 @@ class LogicConvNet(nn.Module):
 
     def _hard_step(self, x):
         """The launch sequence of ``forward_hard`` for ``x``'s shape on the
-        current stream (:class:`_HardConvStep`, cached per parameter
+        current stream (:class:`_HardStep`, cached per parameter
         version), or None where the general path runs."""
         if (x.dim() != 4 or x.dtype not in (torch.float32, torch.uint8) or not x.is_contiguous()
                 or self.wire_residual > 0 or torch.compiler.is_compiling()):
             return None
         key = (derived.state_key(self), tuple(x.shape), x.dtype, x.get_device(),
                ops._stream(x).value)
-        return derived.cached(self, "_derived_hard_step", key, lambda: _HardConvStep.build(self, x))
+        return derived.cached(self, "_derived_hard_step", key,
+                              lambda: _HardStep.for_conv(self, x))
 
     @torch.no_grad()
     def forward_hard_packed(self, xp, B, chw):
@@ -402,16 +411,29 @@ class LogicConvNet(nn.Module):
         return total
 
 
-class _HardConvStep:
-    """``LogicConvNet.forward_hard`` for one input shape on one stream as a
-    fixed sequence of C-ABI launches: packing, every conv block (pooled),
-    the fused head. The per-call host work of the general path (parameter
-    walks for each table, shape checks, wrapper calls, an allocation per
-    intermediate) is done once here: the intermediate words live in buffers
-    this object keeps (the launches run in stream order, so a call's packing
-    cannot overtake the previous call's reads of them) and a call allocates
-    only its logits. The tables are the general path's own, so the logits
-    are the same bits."""
+def _fc_net_call(lib, x_ptr, in_kind, B, in_dim, codes, n_cls, wire_r, st):
+    """The fused network's entry point and arguments (logits slot None), as
+    ``ops.fc_hard_net`` passes them."""
+    if codes.plan is not None:
+        return (lib.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
+                [x_ptr, in_kind, B, in_dim, len(codes), codes.widths, codes.ptrs,
+                 ops._p(codes.plan), n_cls, None, st])
+    return (lib.slg_fc_hard_net, "slg_fc_hard_net",
+            [x_ptr, in_kind, B, in_dim, len(codes), codes.widths, codes.ptrs, n_cls,
+             int(wire_r), None, st])
+
+
+class _HardStep:
+    """A network's ``forward_hard`` for one input shape on one stream as a
+    fixed sequence of C-ABI launches: for a conv network packing, every conv
+    block (pooled) and the fused head; for an FC network the fused network
+    (with packing before it where the kernel takes words). The per-call host
+    work of the general path (parameter walks for each table, shape checks,
+    wrapper calls, an allocation per intermediate) is done once here: the
+    intermediate words live in buffers this object keeps (the launches run
+    in stream order, so a call's packing cannot overtake the previous call's
+    reads of them) and a call allocates only its logits. The tables are the
+    general path's own, so the logits are the same bits."""
 
     def __init__(self, calls, out_shape, in_slot, out_slot, bufs, tables):
         self.calls, self.out_shape = calls, out_shape
@@ -419,7 +441,35 @@ class _HardConvStep:
         self.bufs, self.tables = bufs, tables          # kept alive for the pointers
 
     @staticmethod
-    def build(model, x):
+    def for_fc(model, x):
+        """LogicNet: the fused network on rows (packed by a launch of its own
+        where the fused packing does not apply); None for LUT layers or
+        widths past LDS."""
+        from . import _lib
+        layers, n_cls = list(model.layers), model.head.num_classes
+        B, in_dim = x.shape
+        lut, widths, spw, typable = _hard_fc_plan(layers, in_dim, n_cls)
+        if lut or not spw:
+            return None
+        wire_r = model.wire_r
+        codes = _hard_fc_net_codes(layers, in_dim, wire_r, bool(not wire_r and typable))
+        st, lib = ops._stream(x), _lib.lib()
+        kind = 1 if x.dtype == torch.uint8 else 0
+        calls, bufs = [], []
+        if spw == 64 and in_dim <= 1024:
+            calls.append(_fc_net_call(lib, None, kind, B, in_dim, codes, n_cls, wire_r, st))
+        else:
+            xp = torch.empty((ops.n_words(B), in_dim), device=x.device, dtype=torch.int64)
+            calls.append((lib.slg_pack_bits, "slg_pack_bits",
+                          [None, kind, B, in_dim, 1, ops._p(xp), st]))
+            calls.append(_fc_net_call(lib, ops._p(xp), ops.PACKED_WORD_MAJOR, B, in_dim, codes,
+                                      n_cls, wire_r, st))
+            bufs.append(xp)
+        return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(calls[-1][2]) - 2),
+                             bufs, [codes])
+
+    @staticmethod
+    def for_conv(model, x):
         from . import _lib
         convs = list(model._convs())
         if not convs or any(conv.generic for conv in convs):
@@ -454,16 +504,9 @@ class _HardConvStep:
             return None
         codes = _hard_fc_net_codes(layers, in_dim, 0, bool(typable))
         tables.append(codes)
-        if codes.plan is not None:
-            head = (lib.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
-                    [ops._p(cur), ops.PACKED, B, in_dim, len(codes), codes.widths, codes.ptrs,
-                     ops._p(codes.plan), n_cls, None, st])
-        else:
-            head = (lib.slg_fc_hard_net, "slg_fc_hard_net",
-                    [ops._p(cur), ops.PACKED, B, in_dim, len(codes), codes.widths, codes.ptrs,
-                     n_cls, 0, None, st])
+        head = _fc_net_call(lib, ops._p(cur), ops.PACKED, B, in_dim, codes, n_cls, 0, st)
         calls.append(head)
-        return _HardConvStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(head[2]) - 2),
+        return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(head[2]) - 2),
                              bufs, tables)
 
     def __call__(self, x):
