@@ -466,10 +466,12 @@ class _HardStep:
                                       n_cls, wire_r, st))
             bufs.append(xp)
         return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(calls[-1][2]) - 2),
-                             bufs, [codes])
+                         bufs, [codes])
 
     @staticmethod
     def for_conv(model, x):
+        """LogicConvNet: packing, the pooled conv blocks, the fused head; None
+        for generic trees, LUT head layers or head widths past LDS."""
         from . import _lib
         convs = list(model._convs())
         if not convs or any(conv.generic for conv in convs):
@@ -507,7 +509,7 @@ class _HardStep:
         head = _fc_net_call(lib, ops._p(cur), ops.PACKED, B, in_dim, codes, n_cls, 0, st)
         calls.append(head)
         return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(head[2]) - 2),
-                             bufs, tables)
+                         bufs, tables)
 
     def __call__(self, x):
         from . import _lib
