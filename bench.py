@@ -11,19 +11,32 @@ give the time per step.
 
 ``value`` = hard-circuit Ggate-evals/s = 65536 * 60000 / t_hard (the
 reference's gate count, models.py:103-104); the soft rate is reported beside
-it (``soft_samples_per_s``). ``roofline`` is that of the fused hard-network
-kernel (HBM: it must read the fp32 input), with the bit-op view in
-``roofline_valu``; ``roofline_soft`` is the soft Top-K layer kernel's.
-``cpu_baseline`` times the oracle (the reference's PyTorch CPU path restated)
-on a bounded sample on this host.
+it (``soft_samples_per_s``). ``cpu_baseline`` times the oracle (the
+reference's PyTorch CPU path restated) on a bounded sample on this host.
+
+Before the timed regions, after the ``--warmup`` steps, a settle phase runs
+untimed steps for 300 ms of wall time (``settle_ms``), so a short warm-up
+does not time the GPU while its clocks are still rising.
+
+Every launch is then timed alone with HIP events on its stream:
+``hard_kernels`` lists each launch of ``forward_hard`` (packing, conv blocks,
+fused networks) with its algorithmic bytes and bit-ops and both fractions;
+``soft_kernels`` each timed stage of the soft forward (the FC hidden layer,
+or every conv block with its OrPool and the FC head). Bit-ops count one per
+two-input gate and 2^k - 1 per arity-k LUT node, plus three ORs per pooled
+output.
+* ``roofline`` (config 2: the fused hard network) = ``roofline_hard``: for FC
+  networks the launches from fp32 rows to logits (HBM-bound on the input
+  read); for conv networks the conv block that takes the most time
+  (VALU-bound, bit-ops against 1.258e15/s).
+* ``roofline_soft``: the soft stage with the largest share of the forward's
+  time (HBM for FC layers; FP32 against 157.3 TFLOP/s for conv blocks).
+* ``roofline_valu``: bit-ops of the whole eager hard step.
 
 The default run measures all five BASELINE configs the same way and adds
-them under ``configs`` (the headline keys stay config 2's): each one's
-forward_hard and soft forward at the config's batch sizes, its dominant soft
-kernel (the widest FC layer, HBM-bound; or the first conv block with its
-OrPool, FP32-bound against 157.3 TFLOP/s), for FC networks the fused
-hard-network kernel, and the CPU baseline. ``--config N`` measures config N
-alone.
+them under ``configs`` (the headline keys stay config 2's). ``--config N``
+measures config N alone; ``--kernels-only`` runs every launch three times
+for counter passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N] [--no-cpu]
 """
@@ -120,49 +133,37 @@ def load_traffic(cfg):
         return json.load(fh).get(f"cfg{cfg}", {})
 
 
-def hard_net_codes(ops, model, in_dim):
-    """The codes LogicNet.forward_hard runs on unpacked rows: the type-uniform
-    layout where it applies, else the bank-aware order."""
-    codes = ops.fc_hard_codes_net([l.hard_spec() for l in model.layers], compact=True)
-    if ops.fc_hard_type_slots(in_dim, [l.out_dim for l in model.layers]) > 0:
-        return ops.fc_hard_type_place_net(codes, in_dim)
-    return ops.NetCodes(ops.fc_hard_place_net(codes))
-
-
 def kernels_only(reps=3):
-    """Workload for counter passes: a 256 MiB copy (calibration), then
-    ``reps`` times each: config 2's fused hard network and one soft hidden
-    layer, config 4's walsh hidden layer, and the first conv block (with its
-    OrPool) of configs 3 and 5, at the bench's batch sizes."""
+    """Workload for counter passes: a 256 MiB copy (calibration), then, per
+    config at the bench's batch sizes, ``reps`` launches each of every
+    launch of ``forward_hard`` (packing, conv blocks, fused networks) and of
+    every stage of the soft forward the bench times (the FC hidden layer, or
+    each conv block with its OrPool and the FC head)."""
     import silogic_amd as sl
-    from silogic_amd import ops
     from silogic_amd.synthetic import BATCHES, build_config, config_inputs
     dev = torch.device("cuda:0")
     src = torch.ones(64 << 20, device=dev)          # 256 MiB
     dst = torch.empty_like(src)
     for _ in range(reps):
         dst.copy_(src)
-    model = build_config(2, sl).eval().to(dev)
-    xh = config_inputs(2, 65536).to(dev)
-    with torch.no_grad():
-        codes = hard_net_codes(ops, model, 784)
-        for _ in range(reps):
-            ops.fc_hard_net(xh, ops.ROWS_F32, 65536, 784, codes, 10)
-        for cfg in (2, 4):
-            m = model if cfg == 2 else build_config(cfg, sl).eval().to(dev)
-            L = m.layers[1]
-            x_mid = torch.rand(BATCHES[cfg][0], L.in_dim, device=dev)
-            rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
-            for _ in range(reps):
-                ops.fc_soft_rec(x_mid, rec, L.in_dim, L.out_dim, L.n_candidates, L.node.kind,
-                                L._inv_tau())
-        for cfg in (3, 5):
-            m = build_config(cfg, sl).eval().to(dev)
-            x = config_inputs(cfg, BATCHES[cfg][0]).to(dev)
-            conv = m._convs()[0]
-            for _ in range(reps):
-                conv.forward_pooled(x)
     torch.cuda.synchronize()
+    del src, dst
+    for cfg in (1, 2, 3, 4, 5):
+        model = build_config(cfg, sl).eval().to(dev)
+        B_soft, B_hard = BATCHES[cfg][:2]
+        x_hard = config_inputs(cfg, B_hard).to(dev)
+        x_soft = x_hard[:B_soft].contiguous()
+        with torch.no_grad():
+            for name, fn, _, _ in hard_launches(cfg, model, x_hard):
+                for _ in range(reps):
+                    fn()
+            for name, fn, _, _, _ in soft_stages(cfg, model, B_soft, x_soft, dev):
+                for _ in range(reps):
+                    fn()
+        torch.cuda.synchronize()
+        log(f"kernels-only: config {cfg} done")
+        del model, x_hard, x_soft
+        torch.cuda.empty_cache()
     log("kernels-only done")
 
 
@@ -229,45 +230,35 @@ def conv_flops_per_position(conv):
     return leaf + 2 * ((2 ** conv.node_arity) - 1) * conv.gates_per_output
 
 
-def dominant_soft_kernel(cfg, model, B_soft, x_soft, dev):
-    """(name, launch function, roofline dict builder inputs) of the soft
-    kernel that dominates config ``cfg``'s forward: the widest FC layer on
-    records (HBM-bound: bytes), or the first (largest) conv block with its
-    OrPool (FP32-bound: flops, with its bytes beside)."""
-    from silogic_amd import ops
-    if hasattr(model, "layers"):
-        with torch.no_grad():
-            model(x_soft)                      # builds (or reuses) the forward's launch plan
-        slot = model.layers[0].__dict__.get("_derived_soft_plan")
-        plan = slot[1] if slot else None
-        if plan is not None and plan.net is not None:
-            # small batch, narrow layers: the forward is one launch for the
-            # whole network (with its head); that launch is the kernel
-            K = model.layers[0].n_candidates
-            fn = lambda: plan(x_soft)  # noqa: E731
-            C = model.head.num_classes
-            nbytes = (B_soft * (x_soft.shape[1] + C) * 4 +
-                      sum(l.out_dim * 16 * ops.record_quads(K) for l in model.layers))
-            name = (f"fc_soft_net_kernel ({len(model.layers)} layers + GroupSum, "
-                    f"{model.layers[0]._node_name}, K={K}, B={B_soft})")
-            return name, fn, nbytes, None
-        L = model.layers[1] if len(model.layers) > 1 else model.layers[0]
-        x_mid = torch.rand(B_soft, L.in_dim, device=dev)
-        rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
-        K, OUT = L.n_candidates, L.out_dim
-        fn = lambda: ops.fc_soft_rec(x_mid, rec, L.in_dim, OUT, K, L.node.kind, L._inv_tau())  # noqa: E731
-        # input rows read once, output rows written once, one record per output
-        nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * ops.record_quads(K)
-        name = f"fc_soft_kernel ({L._node_name}, K={K}, IN={L.in_dim}, OUT={OUT}, B={B_soft})"
-        return name, fn, nbytes, None
-    conv = model._convs()[0]
-    B, C, H, W = x_soft.shape
-    fn = lambda: conv.forward_pooled(x_soft)  # noqa: E731
-    nbytes = B * C * H * W * 4 + B * conv.n * (H // 2) * (W // 2) * 4
-    flops = B * conv.n * H * W * conv_flops_per_position(conv)
-    name = (f"conv_soft_kernel (block 0: {C}->{conv.n} channels, {H}x{W}, "
-            f"{conv.node_name}, pooled, B={B})")
-    return name, fn, nbytes, flops
+def node_bitops(name, arity):
+    """Bit-operations of one hard node on one sample: a two-input gate
+    (gate16, or walsh hardened to its truth table) is one; an arity-k LUT
+    node (multilinear, hybrid) is a Shannon tree of 2^k - 1 two-to-one muxes."""
+    if name in ("gate16", "walsh") and arity == 2:
+        return 1
+    return (1 << arity) - 1
+
+
+def conv_geometry(model, in_hw):
+    """``[(conv, H, W, Ho, Wo)]`` per block (square inputs, every block pooled 2x2)."""
+    out, hw = [], in_hw
+    for conv in model._convs():
+        Hf = hw + 2 * conv.padding - conv.kh + 1
+        out.append((conv, hw, hw, Hf // 2, Hf // 2))
+        hw = Hf // 2
+    return out
+
+
+def conv_block_bitops(conv, H, W, Ho, Wo):
+    """Bit-ops per sample of one hard conv block: the reference's gate count
+    for it (n * H * W * gates_per_output, models.py:277-288) times the node's
+    bit-ops, plus the 2x2 OR-pool's three ORs per pooled output."""
+    return (conv.n * H * W * conv.gates_per_output * node_bitops(conv.node_name, conv.node_arity)
+            + 3 * conv.n * Ho * Wo)
+
+
+def fc_bitops(layers):
+    return sum(l.out_dim * node_bitops(l._node_name, l.arity) for l in layers)
 
 
 def hard_units(cfg, model):
@@ -278,13 +269,155 @@ def hard_units(cfg, model):
     return model.gate_count(CONFIGS[cfg][1]["in_hw"])
 
 
+def hard_bitops(cfg, model):
+    """Bit-ops per sample of the whole hard circuit (gate-evals x bit-ops per node,
+    plus the OR-pools)."""
+    if hasattr(model, "layers"):
+        return fc_bitops(model.layers)
+    from silogic_amd.synthetic import CONFIGS
+    geo = conv_geometry(model, CONFIGS[cfg][1]["in_hw"])
+    return sum(conv_block_bitops(*g) for g in geo) + fc_bitops(model.head_layers)
+
+
+def soft_stages(cfg, model, B_soft, x_soft, dev):
+    """The launches of config ``cfg``'s soft forward that can be timed alone:
+    ``[(name, fn, bytes, flops, count)]``. FC networks: the widest hidden
+    layer on records (``count`` = how many such layers the forward runs;
+    HBM-bound: bytes), or the one-launch network. Conv networks: every conv
+    block with its OrPool on its real input (FP32-bound: flops, bytes
+    beside) and the FC head."""
+    from silogic_amd import ops
+    stages = []
+    if hasattr(model, "layers"):
+        with torch.no_grad():
+            model(x_soft)                      # builds (or reuses) the forward's launch plan
+        slot = model.layers[0].__dict__.get("_derived_soft_plan")
+        plan = slot[1] if slot else None
+        K = model.layers[0].n_candidates
+        if plan is not None and plan.net is not None:
+            # small batch, narrow layers: the forward is one launch for the
+            # whole network (with its head); that launch is the kernel
+            C = model.head.num_classes
+            nbytes = (B_soft * (x_soft.shape[1] + C) * 4 +
+                      sum(l.out_dim * 16 * ops.record_quads(K) for l in model.layers))
+            name = (f"fc_soft_net_kernel ({len(model.layers)} layers + GroupSum, "
+                    f"{model.layers[0]._node_name}, K={K}, B={B_soft})")
+            return [(name, lambda: plan(x_soft), nbytes, None, 1)]
+        L = model.layers[1] if len(model.layers) > 1 else model.layers[0]
+        x_mid = torch.rand(B_soft, L.in_dim, device=dev)
+        rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
+        OUT = L.out_dim
+        fn = lambda: ops.fc_soft_rec(x_mid, rec, L.in_dim, OUT, K, L.node.kind, L._inv_tau())  # noqa: E731
+        # input rows read once, output rows written once, one record per output
+        nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * ops.record_quads(K)
+        name = f"fc_soft_kernel ({L._node_name}, K={K}, IN={L.in_dim}, OUT={OUT}, B={B_soft})"
+        n_same = sum(1 for l in model.layers[1:] if l.in_dim == L.in_dim and l.out_dim == OUT)
+        return [(name, fn, nbytes, None, max(1, n_same))]
+    x = x_soft
+    with torch.no_grad():
+        for i, conv in enumerate(model._convs()):
+            B, C, H, W = x.shape
+            xin = x
+            fn = (lambda c=conv, t=xin: c.forward_pooled(t))
+            y = fn()
+            nbytes = xin.numel() * 4 + y.numel() * 4
+            flops = B * conv.n * H * W * conv_flops_per_position(conv)
+            name = (f"conv_soft block {i}: {C}->{conv.n} channels, {H}x{W}, "
+                    f"{conv.node_name}, pooled, B={B}")
+            stages.append((name, fn, nbytes, flops, 1))
+            x = y
+        feats = x.flatten(1).contiguous()
+        from silogic_amd.models import _soft_fc_stack
+        fn = lambda: _soft_fc_stack(model.head_layers, model.head, feats, 0)  # noqa: E731
+        fn()
+        nbytes = feats.numel() * 4 + B_soft * model.head.num_classes * 4 + sum(
+            l.out_dim * 16 * ops.record_quads(l.n_candidates) for l in model.head_layers)
+        stages.append((f"head: {len(model.head_layers)} FC layers + GroupSum, B={B_soft}",
+                       fn, nbytes, None, 1))
+    return stages
+
+
+def hard_launches(cfg, model, x_hard):
+    """The C-ABI launches of ``forward_hard`` on ``x_hard`` (the cached launch
+    sequence), each with what it moves and computes:
+    ``[(name, fn, bytes, bitops)]``. ``fn`` re-launches that one kernel on the
+    sequence's own buffers."""
+    import ctypes
+    from silogic_amd import ops
+    from silogic_amd.synthetic import CONFIGS
+    with torch.no_grad():
+        model.forward_hard(x_hard)
+    slot = model.__dict__.get("_derived_hard_step")
+    step = slot[1] if slot else None
+    if step is None:
+        return []
+    out = torch.empty(step.out_shape, device=x_hard.device)
+    B = x_hard.shape[0]
+    nw = ops.n_words(B)
+    isz = x_hard.element_size()
+    res = []
+    geo = None if hasattr(model, "layers") else conv_geometry(model, CONFIGS[cfg][1]["in_hw"])
+    conv_i = 0
+    for i, (fn, name, args) in enumerate(step.calls):
+        a = list(args)
+        if i == step.in_slot[0]:
+            a[step.in_slot[1]] = ctypes.c_void_p(x_hard.data_ptr())
+        if i == step.out_slot[0]:
+            a[step.out_slot[1]] = ctypes.c_void_p(out.data_ptr())
+        launch = (lambda f=fn, aa=a: f(*aa))
+        if name == "slg_pack_bits":
+            D = x_hard[0].numel()
+            res.append(("pack_kernel", launch, B * D * isz + D * nw * 8, 0))
+        elif name == "slg_conv_hard_fwd":
+            conv, H, W, Ho, Wo = geo[conv_i]
+            nbytes = (a[1] * H * W + conv.n * Ho * Wo) * nw * 8
+            res.append((f"conv_hard_kernel block {conv_i}: {a[1]}->{conv.n} channels, {H}x{W}, "
+                        f"{conv.node_name} arity {conv.node_arity}, pooled",
+                        launch, nbytes, B * conv_block_bitops(conv, H, W, Ho, Wo)))
+            conv_i += 1
+        else:
+            layers = model.layers if hasattr(model, "layers") else model.head_layers
+            in_dim, C = a[3], model.head.num_classes
+            widths = [l.out_dim for l in layers]
+            codes = sum(widths) * 4
+            if a[1] in (0, 1):       # rows: packing inside
+                nbytes = B * in_dim * isz + B * C * 4 + codes
+                kname = f"fc_hard_net_rows_kernel (packing + {len(widths)} layers + GroupSum)"
+            else:
+                nbytes = in_dim * nw * 8 + B * C * 4 + codes
+                kname = f"fc_hard_net_packed_kernel ({len(widths)} layers + GroupSum)"
+            res.append((kname, launch, nbytes, B * fc_bitops(layers)))
+    return res
+
+
+def settle(step, ms=300.0):
+    """Untimed steps until ``ms`` of wall time has passed (synchronising every
+    few steps), so the timed region starts at the clocks the GPU keeps under
+    load whatever the warm-up count. Returns (wall ms, steps)."""
+    t0, n = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            step()
+        n += 8
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3, n
+
+
+def _roof_hbm(name, nbytes, t, traffic=None, **extra):
+    gbs = nbytes / t / 1e9
+    d = {"kernel": name, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+         "algorithmic_bytes": nbytes, "avg_kernel_us": round(t * 1e6, 2)}
+    d.update(extra)
+    return d
+
+
 def measure_config(cfg, steps, warmup, with_cpu):
     """Time config ``cfg``: ``steps`` steps of forward_hard (hard batch) +
-    soft forward (soft batch) after ``warmup`` untimed ones, then the
-    dominant kernels alone with HIP events, then (optionally) the CPU
-    baseline. Returns the config's result dict."""
+    soft forward (soft batch) after ``warmup`` untimed ones and a settle
+    phase, then every hard launch and soft stage alone with HIP events, then
+    (optionally) the CPU baseline. Returns the config's result dict."""
     import silogic_amd as sl
-    from silogic_amd import ops
     from silogic_amd.synthetic import build_config, config_inputs, BATCHES
 
     dev = torch.device("cuda:0")
@@ -297,6 +430,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
     x_hard = x_hard_cpu.to(dev)
     x_soft = x_hard[:B_soft].contiguous()
     gates = hard_units(cfg, model)
+    bitops_ps = hard_bitops(cfg, model)
     torch.cuda.synchronize()
 
     def step():
@@ -307,6 +441,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    settle_ms, settle_steps = settle(step)
 
     # ---- timed regions: exactly `steps` steps between synchronisations ----
     # A step is forward_hard on the batch (the metric's unit of work); the
@@ -342,65 +477,86 @@ def measure_config(cfg, steps, warmup, with_cpu):
     log(f"config {cfg}: hard step {t_hard * 1e6:.1f} us (wall {wall / steps * 1e6:.1f} us, "
         f"graph replay {t_hard_graph * 1e6:.1f} us); soft forward {t_soft * 1e6:.1f} us")
 
-    # ---- dominant kernels alone, HIP events on the launch stream ----
+    # ---- every launch alone, HIP events on the launch stream ----
     reps = 20
-    hard = None
-    with torch.no_grad():
-        if hasattr(model, "layers"):
-            widths = [l.out_dim for l in model.layers]
-            C = model.head.num_classes
-            in_dim = x_hard.shape[1]
-            if ops.fc_hard_net_supported(in_dim, widths, C) == 64 and in_dim <= 1024:
-                codes = hard_net_codes(ops, model, in_dim)
-                fn_net = lambda: ops.fc_hard_net(x_hard, ops.ROWS_F32, B_hard, in_dim, codes, C)  # noqa: E731
-                fn_net()
-                k_hard = _events_ms(fn_net, reps) / 1e3
-                hard_bytes = B_hard * in_dim * 4 + sum(w * 4 for w in widths) + B_hard * C * 4
-                hard = ("fc_hard_net_rows_kernel (packing + %d layers + GroupSum)" % len(widths),
-                        k_hard, hard_bytes)
-        name, fn_soft, soft_bytes, soft_flops = dominant_soft_kernel(cfg, model, B_soft, x_soft,
-                                                                     dev)
-        fn_soft()
-        k_soft = _events_ms(fn_soft, reps) / 1e3
-    soft_gbs = soft_bytes / k_soft / 1e9
     traffic = load_traffic(cfg)
-    bitops = B_hard * gates / t_hard
+    with torch.no_grad():
+        hard_k = []
+        for name, fn, nbytes, bops in hard_launches(cfg, model, x_hard):
+            fn()
+            t = _events_ms(fn, reps) / 1e3
+            hard_k.append({"kernel": name, "avg_kernel_us": round(t * 1e6, 2),
+                           "algorithmic_bytes": nbytes,
+                           "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                           "bitops": bops,
+                           "valu_frac": round(bops / t / VALU_BITOPS_PEAK, 4)})
+        soft_k = []
+        for name, fn, nbytes, flops, count in soft_stages(cfg, model, B_soft, x_soft, dev):
+            fn()
+            t = _events_ms(fn, reps) / 1e3
+            rec = {"kernel": name, "avg_kernel_us": round(t * 1e6, 2), "launches_per_forward": count,
+                   "algorithmic_bytes": nbytes,
+                   "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+            if flops is not None:
+                rec["algorithmic_flops"] = flops
+                rec["fp32_frac"] = round(flops / t / 1e12 / FP32_PEAK_TFLOPS, 4)
+            soft_k.append(rec)
 
     res = {
         "workload": WORKLOADS[cfg], "hard_batch": B_hard, "soft_batch": B_soft,
-        "gates_per_sample": gates,
+        "gates_per_sample": gates, "bitops_per_sample": bitops_ps,
         "hard_Ggate_evals_per_s": round(B_hard * gates / t_hard / 1e9, 3),
         "soft_samples_per_s": round(B_soft / t_soft, 1),
         "t_hard_us": round(t_hard * 1e6, 2), "t_soft_us": round(t_soft * 1e6, 2),
         "t_hard_graph_us": round(t_hard_graph * 1e6, 2),
         "ms_per_step": round(t_hard * 1e3, 4),
+        "settle_ms": round(settle_ms, 1), "settle_steps": settle_steps,
+        "hard_kernels": hard_k, "soft_kernels": soft_k,
     }
-    if soft_flops is None:
-        soft_roof = {"kernel": name, "bound": "hbm", "achieved": round(soft_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(soft_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("fc_soft_kernel"), "algorithmic_bytes": soft_bytes,
-                     "avg_kernel_us": round(k_soft * 1e6, 2)}
+    # soft roofline: the stage with the largest share of the forward's time
+    dom = max(soft_k, key=lambda r: r["avg_kernel_us"] * r["launches_per_forward"])
+    t_dom = dom["avg_kernel_us"] / 1e6
+    if "algorithmic_flops" in dom:
+        tflops = dom["algorithmic_flops"] / t_dom / 1e12
+        res["roofline_soft"] = {
+            "kernel": dom["kernel"], "bound": "fp32", "achieved": round(tflops, 2),
+            "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+            "traffic": traffic.get(dom["kernel"].split(":")[0]),
+            "algorithmic_flops": dom["algorithmic_flops"],
+            "algorithmic_bytes": dom["algorithmic_bytes"], "hbm_frac": dom["hbm_frac"],
+            "avg_kernel_us": dom["avg_kernel_us"],
+            "share_of_forward": round(dom["avg_kernel_us"] / (t_soft * 1e6), 3)}
     else:
-        tflops = soft_flops / k_soft / 1e12
-        soft_roof = {"kernel": name, "bound": "fp32", "achieved": round(tflops, 2),
-                     "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
-                     "traffic": traffic.get("conv_soft_kernel"),
-                     "algorithmic_flops": soft_flops, "algorithmic_bytes": soft_bytes,
-                     "hbm_frac": round(soft_gbs / HBM_PEAK_GBS, 4),
-                     "avg_kernel_us": round(k_soft * 1e6, 2)}
-    res["roofline_soft"] = soft_roof
-    if hard is not None:
-        hname, k_hard, hard_bytes = hard
-        hard_gbs = hard_bytes / k_hard / 1e9
-        res["roofline_hard"] = {"kernel": hname, "bound": "hbm", "achieved": round(hard_gbs, 1),
-                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                "frac": round(hard_gbs / HBM_PEAK_GBS, 4),
-                                "traffic": traffic.get("fc_hard_net_rows_kernel"),
-                                "algorithmic_bytes": hard_bytes,
-                                "avg_kernel_us": round(k_hard * 1e6, 2)}
-    res["roofline_valu"] = {"kernel": "forward_hard (whole packed circuit)",
+        res["roofline_soft"] = _roof_hbm(
+            dom["kernel"], dom["algorithmic_bytes"], t_dom,
+            traffic.get(dom["kernel"].split(" ")[0]),
+            share_of_forward=round(dom["avg_kernel_us"] * dom["launches_per_forward"]
+                                   / (t_soft * 1e6), 3))
+    # hard roofline. FC networks: the launches from the fp32 rows to the
+    # logits (packing, where it is a launch of its own, plus the fused
+    # network), HBM-bound on the input read. Conv networks: the conv block
+    # that takes the most time, VALU-bound (bit-ops).
+    if hard_k:
+        if hasattr(model, "layers"):
+            t = sum(r["avg_kernel_us"] for r in hard_k) / 1e6
+            nbytes = B_hard * x_hard.shape[1] * 4 + B_hard * model.head.num_classes * 4 + \
+                sum(l.out_dim for l in model.layers) * 4
+            name = " + ".join(r["kernel"] for r in hard_k)
+            res["roofline_hard"] = _roof_hbm(
+                name, nbytes, t, traffic.get(hard_k[-1]["kernel"].split(" ")[0]),
+                valu_frac=round(B_hard * bitops_ps / t / VALU_BITOPS_PEAK, 4))
+        else:
+            convs = [r for r in hard_k if r["kernel"].startswith("conv_hard")]
+            d = max(convs, key=lambda r: r["avg_kernel_us"])
+            t = d["avg_kernel_us"] / 1e6
+            res["roofline_hard"] = {
+                "kernel": d["kernel"], "bound": "valu",
+                "achieved": d["bitops"] / t, "peak": VALU_BITOPS_PEAK, "unit": "bit-ops/s",
+                "frac": d["valu_frac"], "traffic": traffic.get("conv_hard_kernel"),
+                "algorithmic_bitops": d["bitops"], "algorithmic_bytes": d["algorithmic_bytes"],
+                "hbm_frac": d["hbm_frac"], "avg_kernel_us": d["avg_kernel_us"]}
+    bitops = B_hard * bitops_ps / t_hard
+    res["roofline_valu"] = {"kernel": "forward_hard (whole packed circuit, eager step)",
                             "achieved_bitops_per_s": bitops, "peak": VALU_BITOPS_PEAK,
                             "frac": round(bitops / VALU_BITOPS_PEAK, 6)}
     if with_cpu:
@@ -436,9 +592,12 @@ def bench_line(head_cfg, res, steps, warmup, configs=None):
         "t_hard_us": res["t_hard_us"],
         "t_hard_graph_us": res["t_hard_graph_us"],
         "t_soft_us": res["t_soft_us"],
+        "settle_ms": res["settle_ms"],
         "roofline": roof,
         "roofline_soft": res["roofline_soft"],
         "roofline_valu": res["roofline_valu"],
+        "hard_kernels": res["hard_kernels"],
+        "soft_kernels": res["soft_kernels"],
     }
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]

@@ -363,8 +363,8 @@ int64_t slg_fc_hard_type_slots(int64_t IN0, int32_t n_layers, const int64_t* wid
  * 99-101, that leaves the logits unchanged). codes[l] are compact codes
  * [widths[l]] from slg_fc_hard_prep_net (compact = 1). Writes, per layer,
  * placed[l] of S = slg_fc_hard_type_slots() slots (slot j*1024 + t stored at
- * t*(S/1024) + j) and a plan row (plan[l*18 ..]: U, rows, then a truth
- * table per wave): for every layer but the last, rows 0..U-1 hold in each
+ * t*(S/1024) + j) and a plan row (plan[l*20 ..]: U, rows, a truth table
+ * per wave, then S/1024 and IN0): for every layer but the last, rows 0..U-1 hold in each
  * 64-slot wave row outputs of one gate type (codes (a << 16) | b with word
  * indices of the two activation buffers) and the remaining rows compact
  * codes; within that, each 32 consecutive slots read operands of distinct
@@ -380,7 +380,9 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
  * slg_fc_hard_type_place_net; widths are the layers' widths, as given to the
  * placement. Unpacked rows (in_kind 0 or 1) need IN0 <= 1024 and 64-sample
  * tiles (slg_fc_hard_net_supported() == 64); packed input (2 or 3) takes
- * either. Same logits, bit for bit. No counterpart in the reference beyond
+ * either. Same logits, bit for bit. A plan placed for another IN0 (hence
+ * another slot count) is detected on the device from its own record: the
+ * logits are then NaN. No counterpart in the reference beyond
  * slg_fc_hard_net's. */
 int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,
                           const int64_t* widths, const uint32_t* const* codes, const int32_t* plan,

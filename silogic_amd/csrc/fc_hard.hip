@@ -401,7 +401,9 @@ __device__ __forceinline__ void layer_step(WT* lds, int cur, int nxt, int W,
 // word indices counted from the start of the first activation buffer (the
 // read buffer's offset included), so an operand's LDS byte address is one
 // v_mad_u32_u16 (16-bit field x word size + LDS base).
-constexpr int kPlanStride = 18;  // per layer: U, rows, truth table of waves 0..15
+// per layer: U, rows, truth table of waves 0..15, then the slots per thread
+// (MAXO) and the input width the layout was placed for
+constexpr int kPlanStride = 20;
 
 // tt bit k = output for address k = (a << 1) | b (compact-code order)
 __host__ __device__ constexpr bool tt_needs_a(int tt) { return (tt & 3) != (tt >> 2); }
@@ -571,6 +573,22 @@ typedef __attribute__((address_space(4))) const int32_t const_i32_t;
 struct PlanRow {
   int U, rows, tt;
 };
+
+// The codes of a placed layout are read at a stride of MAXO slots, which
+// follows the input width it was placed for: a plan placed for another
+// width or slot count would index past its codes, so the network kernels
+// check the plan's own record first and write NaN logits instead.
+__device__ __forceinline__ bool plan_fits(const int32_t* plan, int maxo, int in0) {
+  const const_i32_t* pl = (const const_i32_t*)plan;
+  return __builtin_amdgcn_readfirstlane(pl[18]) == maxo &&
+         __builtin_amdgcn_readfirstlane(pl[19]) == in0;
+}
+
+__device__ inline void nan_logits(float* __restrict__ logits, int B, int C) {
+  const int64_t n = (int64_t)B * C, step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+    logits[i] = __int_as_float(0x7FC00000);
+}
 
 __device__ __forceinline__ PlanRow plan_row(const int32_t* plan, int l) {
   const const_i32_t* pl = (const const_i32_t*)(plan + l * kPlanStride);
@@ -801,6 +819,12 @@ fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, 
                           float* __restrict__ logits) {
   const_netdesc_t& d = *(const_netdesc_t*)__builtin_amdgcn_kernarg_segment_ptr();
   constexpr int SPW = (int)sizeof(WT) * 8;
+  if constexpr (TYPED) {
+    if (!plan_fits(d.plan, MAXO, d.in0)) {
+      nan_logits(logits, B, d.C);
+      return;
+    }
+  }
   extern __shared__ __align__(16) unsigned char smem[];
   WT* lds = reinterpret_cast<WT*>(smem);
   const int tile = blockIdx.x;
@@ -912,6 +936,12 @@ fc_hard_net_rows_kernel(NetDesc desc, const IT* __restrict__ x, int B, int n_til
                         float* __restrict__ logits) {
   constexpr int NCH = n_chunks<CH>();
   const_netdesc_t& d = *(const_netdesc_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  if constexpr (TYPED) {
+    if (!plan_fits(d.plan, MAXO, d.in0)) {
+      nan_logits(logits, B, d.C);
+      return;
+    }
+  }
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* lds = reinterpret_cast<uint64_t*>(smem);
   const int f = threadIdx.x;
@@ -1260,7 +1290,7 @@ struct TypePlaceNet {
   int32_t* perm[kMaxLayers];         // output -> slot, layers 0 .. L-2
   int32_t* plan;                     // [L][kPlanStride]
   int W[kMaxLayers];
-  int L, maxo;
+  int L, maxo, in0;
 };
 
 __device__ inline void type_operands(const TypePlaceNet& n, int l, int o, uint32_t& a, uint32_t& b,
@@ -1422,6 +1452,8 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
       pl[0] = U;
       pl[1] = rows;
       for (int i = 0; i < 16; ++i) pl[2 + i] = wtt[i];
+      pl[18] = n.maxo;
+      pl[19] = n.in0;
     }
     __syncthreads();
     const int U = plan_u;
@@ -1535,6 +1567,8 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypeP
     pl[0] = 0;
     pl[1] = (n.W[l] + kNetThreads - 1) / kNetThreads;
     for (int i = 0; i < 16; ++i) pl[2 + i] = 0;
+    pl[18] = n.maxo;
+    pl[19] = n.in0;
   }
 }
 
@@ -1819,6 +1853,7 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
   TypePlaceNet n{};
   n.L = n_layers;
   n.maxo = (int)(S / kNetThreads);
+  n.in0 = (int)IN0;
   n.plan = plan;
   int64_t used = 0;
   for (int l = 0; l < n_layers; ++l) {

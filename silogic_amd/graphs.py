@@ -21,8 +21,9 @@ class CapturedForward:
         if not inputs or any(not torch.is_tensor(t) or t.device.type != "cuda" for t in inputs):
             raise ValueError("CapturedForward: inputs must be device tensors")
         self.fn, self.inputs = fn, inputs
-        # build every cached table (hard codes, placements, plans) outside the
-        # capture, on the stream the capture will use
+        # build every cached table (hard codes, placements, plans, launch
+        # sequences keyed by stream) outside the capture, on the stream the
+        # capture then uses, so the capture records launches and builds nothing
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.no_grad(), torch.cuda.stream(side):
@@ -31,7 +32,7 @@ class CapturedForward:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.no_grad(), torch.cuda.graph(self.graph):
+        with torch.no_grad(), torch.cuda.graph(self.graph, stream=side):
             self.output = fn(*inputs)
 
     def __call__(self, *batch):

@@ -17,6 +17,7 @@ tree + OR-pool kernels. It returns the same raw integer counts as the
 reference's ``GroupSum.forward_hard`` (heads.py:41-45).
 """
 import ctypes
+import threading
 
 import torch
 import torch.nn as nn
@@ -97,8 +98,10 @@ def _hard_fc_net_codes(layers, in_dim, wire_r, typed):
             return ops.fc_hard_type_place_net(codes, in_dim)
         return ops.NetCodes(codes if wire_r else ops.fc_hard_place_net(codes))
 
+    # the type-uniform layout's slot count follows the input width, so the
+    # width is part of the key
     return derived.cached(layers[0], "_derived_net_codes",
-                          (derived.state_key(*layers), bool(wire_r), typed), build)
+                          (derived.state_key(*layers), int(in_dim), bool(wire_r), typed), build)
 
 
 def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
@@ -415,6 +418,9 @@ def _fc_net_call(lib, x_ptr, in_kind, B, in_dim, codes, n_cls, wire_r, st):
     """The fused network's entry point and arguments (logits slot None), as
     ``ops.fc_hard_net`` passes them."""
     if codes.plan is not None:
+        if wire_r or in_dim != codes.in_dim:
+            raise ValueError("forward_hard: type-placed codes take inputs %s wide and no wire "
+                             "residual (got %d, wire_r %d)" % (codes.in_dim, in_dim, wire_r))
         return (lib.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
                 [x_ptr, in_kind, B, in_dim, len(codes), codes.widths, codes.ptrs,
                  ops._p(codes.plan), n_cls, None, st])
@@ -439,6 +445,10 @@ class _HardStep:
         self.calls, self.out_shape = calls, out_shape
         self.in_slot, self.out_slot = in_slot, out_slot
         self.bufs, self.tables = bufs, tables          # kept alive for the pointers
+        # one call's launches go out as one run: ctypes releases the GIL
+        # around each launch, and a second host thread's packing must not
+        # land between this call's packing and the conv blocks that read it
+        self.lock = threading.Lock()
 
     @staticmethod
     def for_fc(model, x):
@@ -514,10 +524,18 @@ class _HardStep:
     def __call__(self, x):
         from . import _lib
         out = torch.empty(self.out_shape, device=x.device, dtype=torch.float32)
-        self.calls[self.in_slot[0]][2][self.in_slot[1]] = ctypes.c_void_p(x.data_ptr())
-        self.calls[self.out_slot[0]][2][self.out_slot[1]] = ctypes.c_void_p(out.data_ptr())
-        for fn, name, args in self.calls:
-            _lib.check(fn(*args), name)
+        (xi, xs), (oi, os_) = self.in_slot, self.out_slot
+        with self.lock:
+            for i, (fn, name, args) in enumerate(self.calls):
+                if i == xi or i == oi:
+                    # this call's own argument list: the shared one holds no
+                    # per-call pointer
+                    args = list(args)
+                    if i == xi:
+                        args[xs] = ctypes.c_void_p(x.data_ptr())
+                    if i == oi:
+                        args[os_] = ctypes.c_void_p(out.data_ptr())
+                _lib.check(fn(*args), name)
         return out
 
 

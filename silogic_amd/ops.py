@@ -646,7 +646,7 @@ def fc_hard_type_place_net(codes, in_dim):
                          "inputs %d wide and widths %s" % (in_dim, widths))
     dev = codes[0].device
     placed = [torch.empty((S,), device=dev, dtype=torch.int32) for _ in widths]
-    plan = torch.empty((L, 18), device=dev, dtype=torch.int32)
+    plan = torch.empty((L, 20), device=dev, dtype=torch.int32)
     n_ws = max(1, sum(widths[:-1]))
     ws = torch.empty(n_ws, device=dev, dtype=torch.int32)
     _lib.call("slg_fc_hard_type_place_net", L, in_dim, (ctypes.c_int64 * L)(*widths),

@@ -51,3 +51,41 @@ def test_fc_hard_step_with_a_wire_residual():
             x = (torch.rand(B, 200, generator=g) < 0.5).float().to(DEV)
             assert torch.equal(model.forward_hard(x), _general(model, x))
             assert model.__dict__["_derived_hard_step"][1] is not None
+
+
+@pytest.mark.parametrize("cfg,B", [(3, 70), (1, 130)])
+def test_hard_step_calls_from_two_threads(cfg, B):
+    """Two host threads call forward_hard on one model and one stream with
+    different inputs, interleaved: each call returns its own logits (a
+    call's launches go out as one run and carry its own pointers)."""
+    import threading
+    model = build_config(cfg, sl).eval().to(DEV)
+    xs = [config_inputs(cfg, B, seed=s).to(DEV) for s in (21, 22)]
+    with torch.no_grad():
+        refs = [_general(model, x) for x in xs]
+        model.forward_hard(xs[0])                      # build the launch sequence once
+    torch.cuda.synchronize()
+    results = {0: [], 1: []}
+    errors = []
+    start = threading.Barrier(2)
+
+    def worker(i):
+        try:
+            start.wait()
+            with torch.no_grad():
+                for _ in range(40):
+                    results[i].append(model.forward_hard(xs[i]))
+        except Exception as e:                         # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in (0, 1)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i in (0, 1):
+        assert len(results[i]) == 40
+        for got in results[i]:
+            assert torch.equal(got, refs[i])

@@ -46,7 +46,9 @@ def _check_plan(typed, widths, in_dim):
         U, rows = int(plan[l, 0]), int(plan[l, 1])
         assert 0 <= U <= rows <= maxo, (l, U, rows)
         assert rows * 1024 >= (w if U == 0 else 0)
-        assert all(0 <= int(t) < 16 for t in plan[l, 2:])
+        assert all(0 <= int(t) < 16 for t in plan[l, 2:18])
+        # each row records the layout it belongs to: slots per thread, input width
+        assert int(plan[l, 18]) == maxo and int(plan[l, 19]) == in_dim
     assert int(plan[-1, 0]) == 0
     return plan
 
@@ -152,3 +154,51 @@ def test_typed_network_edge_batches_and_depths(in_dim, widths, C, B):
     assert torch.equal(ops.fc_hard_net(x.to(DEV), ops.ROWS_F32, B, in_dim, typed, C), ref)
     x8 = x.to(torch.uint8).to(DEV)
     assert torch.equal(ops.fc_hard_net(x8, ops.ROWS_U8, B, in_dim, typed, C), ref)
+
+
+def test_typed_plan_for_another_width_gives_nan_logits():
+    """Codes placed for one input width, run through the C ABI for another:
+    a different slot count (1500 -> 2 slots per thread, 2500 -> 4) and the
+    same slot count with another width both give NaN logits (the kernel
+    checks the plan's own record before it reads a code)."""
+    import ctypes
+    from silogic_amd import _lib
+    net = _net(100, [1500, 1500, 40])
+    widths = [1500, 1500, 40]
+    typed = ops.fc_hard_type_place_net(_codes(net), 100)
+    _check_plan(typed, widths, 100)
+    B = 70
+    for in_dim in (2500, 1000):
+        assert ops.fc_hard_type_slots(in_dim, widths) > 0
+        x = (torch.rand(B, in_dim, generator=torch.Generator().manual_seed(5)) < 0.5).float()
+        xp = ops.pack_bits(x.to(DEV), word_major=True)
+        out = torch.zeros((B, 4), device=DEV)
+        _lib.call("slg_fc_hard_net_typed", ops._p(xp), ops.PACKED_WORD_MAJOR, B, in_dim,
+                  len(typed), typed.widths, typed.ptrs, ops._p(typed.plan), 4, ops._p(out),
+                  ops._stream(xp))
+        torch.cuda.synchronize()
+        assert torch.isnan(out).all(), in_dim
+        with pytest.raises(ValueError):
+            ops.fc_hard_net(xp, ops.PACKED_WORD_MAJOR, B, in_dim, typed, 4)
+
+
+def test_forward_hard_on_inputs_of_two_widths():
+    """One model, forward_hard on inputs 100 wide and then 2500 wide (the
+    layer reads indices below 100, so the extra columns change nothing):
+    the type-placed codes are kept per input width (the slot count differs:
+    2 and 4 per thread), and both calls give the oracle's logits."""
+    torch.manual_seed(0)
+    model = sl.LogicNet(in_dim=100, width=1500, depth=2, num_classes=10, k=4, seed=5).eval()
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to(DEV)
+    g = torch.Generator().manual_seed(6)
+    x = (torch.rand(130, 100, generator=g) < 0.5).float()
+    wide = torch.cat([x, (torch.rand(130, 2400, generator=g) < 0.5).float()], dim=1)
+    ref = torch_ref.forward_hard(("LogicNet", dict(in_dim=100, width=1500, depth=2,
+                                                   num_classes=10, k=4)), sd, x)
+    with torch.no_grad():
+        for inp in (x, wide, x, wide):
+            got = model.forward_hard(inp.to(DEV)).cpu()
+            assert torch.equal(got, ref)
+            codes = model.layers[0].__dict__["_derived_net_codes"][1]
+            assert codes.plan is not None and codes.in_dim == inp.shape[1]
