@@ -365,13 +365,14 @@ def hard_launches(cfg, model, x_hard):
         if i == step.out_slot[0]:
             a[step.out_slot[1]] = ctypes.c_void_p(out.data_ptr())
         launch = (lambda f=fn, aa=a: f(*aa))
-        if name == "slg_pack_bits":
+        if name in ("slg_pack_bits", "slg_pack_image_wm"):
             D = x_hard[0].numel()
             res.append(("pack_kernel", launch, B * D * isz + D * nw * 8, 0))
-        elif name == "slg_conv_hard_fwd":
+        elif name in ("slg_conv_hard_fwd", "slg_conv_hard_fwd_wm"):
             conv, H, W, Ho, Wo = geo[conv_i]
-            nbytes = (a[1] * H * W + conv.n * Ho * Wo) * nw * 8
-            res.append((f"conv_hard_kernel block {conv_i}: {a[1]}->{conv.n} channels, {H}x{W}, "
+            Cin = a[1] if name == "slg_conv_hard_fwd" else a[2]
+            nbytes = (Cin * H * W + conv.n * Ho * Wo) * nw * 8
+            res.append((f"conv_hard block {conv_i}: {Cin}->{conv.n} channels, {H}x{W}, "
                         f"{conv.node_name} arity {conv.node_arity}, pooled",
                         launch, nbytes, B * conv_block_bitops(conv, H, W, Ho, Wo)))
             conv_i += 1

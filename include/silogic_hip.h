@@ -554,6 +554,28 @@ int slg_conv_hard_fwd(const uint64_t* xp, int64_t C, int64_t H, int64_t W, int64
                       int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
                       const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
                       int32_t pool, uint64_t* out, slg_stream_t stream);
+/* slg_conv_hard_fwd (pooled) on word-major, zero-bordered images, the
+ * layout of LogicConvNet.forward_hard's launch sequence: xp [nw][C][H+2pad]
+ * [W+2pad] uint64 (nw = ceil(B/64); the border, `pad` words wide, must be
+ * zero) -> the interior of out [nw][N][Ho/2+2out_pad][Wo/2+2out_pad] (its
+ * border is not written: a buffer cleared once keeps it, ready as the next
+ * block's input with pad = out_pad; out_pad = 0 gives the head's
+ * PACKED_WORD_MAJOR input). The same bits as slg_conv_hard_fwd on the
+ * transposed layout. No counterpart in the reference beyond
+ * slg_conv_hard_fwd's (a layout of the same computation, layers.py:
+ * 529-541,561-563): with the padding stored, every leaf read is
+ * unconditional, and LUTs of arity 3-6 are evaluated as 3-input functions. */
+int slg_conv_hard_fwd_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, int64_t W,
+                         int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
+                         const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
+                         uint64_t* out, int32_t out_pad, slg_stream_t stream);
+/* pack_bits for images x [B,C,H,W] (dtype 0 fp32: x >= 1, 1 uint8: x != 0)
+ * into the interior of the zero-bordered word-major layout [nw][C][H+2pad]
+ * [W+2pad] (the border is not written). No counterpart in the reference
+ * (the input of slg_conv_hard_fwd_wm; bitpacking/ops.py:27-49 packs the
+ * same bits). */
+int slg_pack_image_wm(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W,
+                      int32_t pad, uint64_t* xp, slg_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Packed building blocks of the silogic.bitpacking API                      */

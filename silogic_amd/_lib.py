@@ -94,6 +94,9 @@ SIGNATURES = {
                                          _I32, _I32, _I32, _P, _P]),
     "slg_conv_hard_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P,
                                     _I32, _I32, _I32, _P, _P]),
+    "slg_conv_hard_fwd_wm": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P,
+                                       _P, _I32, _I32, _P, _I32, _P]),
+    "slg_pack_image_wm": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P]),
 }
 
 _lock = threading.Lock()

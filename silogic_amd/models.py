@@ -480,8 +480,12 @@ class _HardStep:
 
     @staticmethod
     def for_conv(model, x):
-        """LogicConvNet: packing, the pooled conv blocks, the fused head; None
-        for generic trees, LUT head layers or head widths past LDS."""
+        """LogicConvNet: packing, the pooled conv blocks, the fused head, all
+        on word-major words (one 64-sample column of an image contiguous).
+        The images between blocks keep a zero border as wide as the next
+        block's padding (cleared here, once; the kernels write only the
+        interiors), so the conv kernels read every leaf unconditionally.
+        None for generic trees, LUT head layers or head widths past LDS."""
         from . import _lib
         convs = list(model._convs())
         if not convs or any(conv.generic for conv in convs):
@@ -489,22 +493,25 @@ class _HardStep:
         B, C, H, W = x.shape
         nw = ops.n_words(B)
         dev, st, lib = x.device, ops._stream(x), _lib.lib()
-        xp = torch.empty((C * H * W, nw), device=dev, dtype=torch.int64)
-        calls = [(lib.slg_pack_bits, "slg_pack_bits",
-                  [None, 1 if x.dtype == torch.uint8 else 0, B, C * H * W, 0, ops._p(xp), st])]
+        pads = [conv.padding for conv in convs] + [0]
+        xp = torch.zeros((nw, C, H + 2 * pads[0], W + 2 * pads[0]), device=dev, dtype=torch.int64)
+        calls = [(lib.slg_pack_image_wm, "slg_pack_image_wm",
+                  [None, 1 if x.dtype == torch.uint8 else 0, B, C, H, W, pads[0], ops._p(xp), st])]
         bufs, tables = [xp], []
         params = derived.cached(
             model, "_derived_conv_codes", derived.state_key(*convs),
             lambda: ops.conv_hard_prep_net([conv.hard_spec() for conv in convs]))
         cur = xp
-        for conv, (leaf, tt) in zip(convs, params):
-            k, pad = conv.kh, conv.padding
+        for i, (conv, (leaf, tt)) in enumerate(zip(convs, params)):
+            k, pad, opad = conv.kh, conv.padding, pads[i + 1]
             Hf, Wf = H + 2 * pad - k + 1, W + 2 * pad - k + 1
             Ho, Wo = Hf // 2, Wf // 2                     # every block is OR-pooled
-            out = torch.empty((conv.n, Ho, Wo, nw), device=dev, dtype=torch.int64)
-            calls.append((lib.slg_conv_hard_fwd, "slg_conv_hard_fwd",
-                          [ops._p(cur), C, H, W, nw, conv.n, conv._kind(), conv.d,
-                           conv.node_arity, ops._p(leaf), ops._p(tt), k, pad, 1, ops._p(out), st]))
+            out = torch.zeros((nw, conv.n, Ho + 2 * opad, Wo + 2 * opad), device=dev,
+                              dtype=torch.int64)
+            calls.append((lib.slg_conv_hard_fwd_wm, "slg_conv_hard_fwd_wm",
+                          [ops._p(cur), B, C, H, W, conv.n, conv._kind(), conv.d,
+                           conv.node_arity, ops._p(leaf), ops._p(tt), k, pad, ops._p(out), opad,
+                           st]))
             bufs.append(out)
             tables += [leaf, tt]
             cur, (C, H, W) = out, (conv.n, Ho, Wo)
@@ -516,7 +523,8 @@ class _HardStep:
             return None
         codes = _hard_fc_net_codes(layers, in_dim, 0, bool(typable))
         tables.append(codes)
-        head = _fc_net_call(lib, ops._p(cur), ops.PACKED, B, in_dim, codes, n_cls, 0, st)
+        head = _fc_net_call(lib, ops._p(cur), ops.PACKED_WORD_MAJOR, B, in_dim, codes, n_cls, 0,
+                            st)
         calls.append(head)
         return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(head[2]) - 2),
                          bufs, tables)

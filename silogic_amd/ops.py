@@ -1112,6 +1112,41 @@ def conv_hard(xp, shape_chw, leaf, tt, node_kind, depth, arity, kernel, pad, poo
     return out
 
 
+def pack_image_wm(x, pad):
+    """``[B, C, H, W]`` images (fp32 or uint8) -> word-major packed words
+    ``[nw, C, H + 2 pad, W + 2 pad]`` with a zero border (``slg_pack_image_wm``
+    writes the interior into a zeroed buffer)."""
+    require_gpu(x)
+    x, kind = _in_kind(x)
+    if x.dim() != 4:
+        raise ValueError("pack_image_wm: x must be [B, C, H, W], got %s" % (tuple(x.shape),))
+    B, C, H, W = x.shape
+    xp = torch.zeros((n_words(B), C, H + 2 * pad, W + 2 * pad), device=x.device, dtype=torch.int64)
+    _lib.call("slg_pack_image_wm", _p(x), kind, B, C, H, W, pad, _p(xp), _stream(x))
+    return xp
+
+
+def conv_hard_wm(xp, B, shape_chw, leaf, tt, node_kind, depth, arity, kernel, pad, out_pad=0):
+    """Pooled packed conv on zero-bordered word-major words: ``xp``
+    [nw, C, H + 2 pad, W + 2 pad] -> [nw, N, Ho + 2 out_pad, Wo + 2 out_pad]
+    with a zero border (``slg_conv_hard_fwd_wm`` writes the interior of a
+    zeroed buffer)."""
+    require_gpu(xp, leaf, tt)
+    Cc, H, W = shape_chw
+    nw = n_words(B)
+    N = leaf.shape[0]
+    leaves = 2 ** depth if node_kind == GATE16 else arity
+    if (tuple(xp.shape) != (nw, Cc, H + 2 * pad, W + 2 * pad) or not xp.is_contiguous()
+            or leaf.shape != (N, leaves) or tt.shape != (N,)):
+        raise ValueError("conv_hard_wm: packed input / leaf / truth-table shapes are inconsistent")
+    Ho, Wo = (H + 2 * pad - kernel + 1) // 2, (W + 2 * pad - kernel + 1) // 2
+    out = torch.zeros((nw, N, Ho + 2 * out_pad, Wo + 2 * out_pad), device=xp.device,
+                      dtype=torch.int64)
+    _lib.call("slg_conv_hard_fwd_wm", _p(xp), B, Cc, H, W, N, node_kind, depth, arity, _p(leaf),
+              _p(tt), kernel, pad, _p(out), out_pad, _stream(xp))
+    return out
+
+
 # the custom operators the autograd paths above dispatch to (library.py uses
 # this module's launch helpers, so it is imported once they are defined)
 from . import library as _library  # noqa: E402,F401
