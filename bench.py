@@ -157,7 +157,7 @@ def kernels_only(reps=3):
             for name, fn, _, _ in hard_launches(cfg, model, x_hard):
                 for _ in range(reps):
                     fn()
-            for name, fn, _, _, _ in soft_stages(cfg, model, B_soft, x_soft, dev):
+            for name, fn, _, _, _, _ in soft_stages(cfg, model, B_soft, x_soft, dev):
                 for _ in range(reps):
                     fn()
         torch.cuda.synchronize()
@@ -281,7 +281,7 @@ def hard_bitops(cfg, model):
 
 def soft_stages(cfg, model, B_soft, x_soft, dev):
     """The launches of config ``cfg``'s soft forward that can be timed alone:
-    ``[(name, fn, bytes, flops, count)]``. FC networks: the widest hidden
+    ``[(name, fn, bytes, flops, count, extra)]``. FC networks: the widest hidden
     layer on records (``count`` = how many such layers the forward runs;
     HBM-bound: bytes), or the one-launch network. Conv networks: every conv
     block with its OrPool on its real input (FP32-bound: flops, bytes
@@ -295,14 +295,32 @@ def soft_stages(cfg, model, B_soft, x_soft, dev):
         plan = slot[1] if slot else None
         K = model.layers[0].n_candidates
         if plan is not None and plan.net is not None:
-            # small batch, narrow layers: the forward is one launch for the
-            # whole network (with its head); that launch is the kernel
+            # the forward is one launch for the whole network (with its
+            # head): activations stay in LDS. Its bytes are counted as the
+            # per-layer schedule moves them (every layer reads its input
+            # rows, writes its outputs and reads its records; the head is
+            # fused in the last layer), beside the HBM bytes it moves (the
+            # input rows, the logits and each layer's records once) and
+            # the record stream from L2 (every tile reads every record)
             C = model.head.num_classes
-            nbytes = (B_soft * (x_soft.shape[1] + C) * 4 +
-                      sum(l.out_dim * 16 * ops.record_quads(K) for l in model.layers))
-            name = (f"fc_soft_net_kernel ({len(model.layers)} layers + GroupSum, "
-                    f"{model.layers[0]._node_name}, K={K}, B={B_soft})")
-            return [(name, lambda: plan(x_soft), nbytes, None, 1)]
+            rec_b = [-(-l.out_dim // 64) * 64 * 16 * ops.record_quads(K)
+                     for l in model.layers]
+            sched, w = 0, x_soft.shape[1]
+            for i, l in enumerate(model.layers):
+                out_w = C if (i + 1 == len(model.layers) and plan.head is not None) else l.out_dim
+                sched += B_soft * (w + out_w) * 4 + rec_b[i]
+                w = l.out_dim
+            moved = B_soft * (x_soft.shape[1] + C) * 4 + sum(rec_b)
+            maxw = max([x_soft.shape[1]] + [l.out_dim for l in model.layers])
+            S = 4 if (plan.net_kind == 1 or maxw * 16 + 16 * C <= 160 * 1024) else 2
+            stream = -(-B_soft // S) * sum(rec_b)
+            kname = "fc_soft_rec_net_kernel" if plan.net_kind == 2 else "fc_soft_net_kernel"
+            name = (f"{kname} ({len(model.layers)} layers + GroupSum, "
+                    f"{model.layers[0]._node_name}, K={K}, B={B_soft}, {S}-sample tiles)")
+            extra = {"hbm_bytes_moved": moved, "l2_record_stream_bytes": stream,
+                     "bytes_counted_as": "per-layer schedule (input rows + outputs + records "
+                                         "per layer, head fused)"}
+            return [(name, lambda: plan(x_soft), sched, None, 1, extra)]
         L = model.layers[1] if len(model.layers) > 1 else model.layers[0]
         x_mid = torch.rand(B_soft, L.in_dim, device=dev)
         rec = ops.fc_soft_records([L.record_spec()], L.n_candidates)[0]
@@ -312,7 +330,7 @@ def soft_stages(cfg, model, B_soft, x_soft, dev):
         nbytes = B_soft * (L.in_dim + OUT) * 4 + OUT * 16 * ops.record_quads(K)
         name = f"fc_soft_kernel ({L._node_name}, K={K}, IN={L.in_dim}, OUT={OUT}, B={B_soft})"
         n_same = sum(1 for l in model.layers[1:] if l.in_dim == L.in_dim and l.out_dim == OUT)
-        return [(name, fn, nbytes, None, max(1, n_same))]
+        return [(name, fn, nbytes, None, max(1, n_same), {})]
     x = x_soft
     with torch.no_grad():
         for i, conv in enumerate(model._convs()):
@@ -324,7 +342,7 @@ def soft_stages(cfg, model, B_soft, x_soft, dev):
             flops = B * conv.n * H * W * conv_flops_per_position(conv)
             name = (f"conv_soft block {i}: {C}->{conv.n} channels, {H}x{W}, "
                     f"{conv.node_name}, pooled, B={B}")
-            stages.append((name, fn, nbytes, flops, 1))
+            stages.append((name, fn, nbytes, flops, 1, {}))
             x = y
         feats = x.flatten(1).contiguous()
         from silogic_amd.models import _soft_fc_stack
@@ -333,7 +351,7 @@ def soft_stages(cfg, model, B_soft, x_soft, dev):
         nbytes = feats.numel() * 4 + B_soft * model.head.num_classes * 4 + sum(
             l.out_dim * 16 * ops.record_quads(l.n_candidates) for l in model.head_layers)
         stages.append((f"head: {len(model.head_layers)} FC layers + GroupSum, B={B_soft}",
-                       fn, nbytes, None, 1))
+                       fn, nbytes, None, 1, {}))
     return stages
 
 
@@ -492,12 +510,15 @@ def measure_config(cfg, steps, warmup, with_cpu):
                            "bitops": bops,
                            "valu_frac": round(bops / t / VALU_BITOPS_PEAK, 4)})
         soft_k = []
-        for name, fn, nbytes, flops, count in soft_stages(cfg, model, B_soft, x_soft, dev):
+        for name, fn, nbytes, flops, count, extra in soft_stages(cfg, model, B_soft, x_soft, dev):
             fn()
             t = _events_ms(fn, reps) / 1e3
             rec = {"kernel": name, "avg_kernel_us": round(t * 1e6, 2), "launches_per_forward": count,
                    "algorithmic_bytes": nbytes,
                    "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+            rec.update(extra)
+            if "l2_record_stream_bytes" in extra:
+                rec["l2_record_GBps"] = round(extra["l2_record_stream_bytes"] / t / 1e9, 1)
             if flops is not None:
                 rec["algorithmic_flops"] = flops
                 rec["fp32_frac"] = round(flops / t / 1e12 / FP32_PEAK_TFLOPS, 4)
@@ -528,11 +549,13 @@ def measure_config(cfg, steps, warmup, with_cpu):
             "avg_kernel_us": dom["avg_kernel_us"],
             "share_of_forward": round(dom["avg_kernel_us"] / (t_soft * 1e6), 3)}
     else:
+        extra = {k: dom[k] for k in ("hbm_bytes_moved", "l2_record_stream_bytes",
+                                     "l2_record_GBps", "bytes_counted_as") if k in dom}
         res["roofline_soft"] = _roof_hbm(
             dom["kernel"], dom["algorithmic_bytes"], t_dom,
             traffic.get(dom["kernel"].split(" ")[0]),
             share_of_forward=round(dom["avg_kernel_us"] * dom["launches_per_forward"]
-                                   / (t_soft * 1e6), 3))
+                                   / (t_soft * 1e6), 3), **extra)
     # hard roofline. FC networks: the launches from the fp32 rows to the
     # logits (packing, where it is a launch of its own, plus the fused
     # network), HBM-bound on the input read. Conv networks: the conv block

@@ -148,21 +148,28 @@ int slg_fc_soft_fwd_groupsum(const float* x, int64_t B, int64_t IN, int64_t OUT,
                              float inv_tau, int32_t C, float tau, float* logits,
                              slg_stream_t stream);
 /* A network of soft FC layers on records in one launch (the soft forward of
- * LogicNet / WARPNet, models.py:96-101, for narrow layers and small
- * batches): rec[l] from slg_fc_soft_records for in_dim[l] inputs, layer l
- * with out_dim[l] outputs, all layers of one node kind, K candidates and
- * inv_tau. x [B, IN] fp32 (IN >= in_dim[0]). A workgroup takes 4 samples
- * through every layer with the activations in LDS; each layer computes as
- * slg_fc_soft_fwd_records does (the same bits). C > 0: the last layer feeds
- * the STE GroupSum head and out = logits [B, C] (counts of y > 0.5 / tau);
- * C = 0: out = the last layer's activations [B, out_dim[n_layers-1]].
- * SLG_E_UNSUPPORTED when the widths do not fit LDS. */
+ * LogicNet / WARPNet, models.py:96-101): rec[l] from slg_fc_soft_records
+ * for in_dim[l] inputs, layer l with out_dim[l] outputs, all layers of one
+ * node kind, K candidates and inv_tau. x [B, IN] fp32 (IN >= in_dim[0]). A
+ * workgroup takes a tile of samples through every layer with the
+ * activations in LDS, so only x and the result touch HBM: narrow layers and
+ * small batches keep two buffers of 4-sample slots; wide layers (K = 8) and
+ * batches that give every CU a tile keep one buffer of 4 or 2 samples and
+ * hold a layer's outputs in registers until every wave has read its input.
+ * Each layer computes as slg_fc_soft_fwd_records does (the same bits). C > 0:
+ * the last layer feeds the STE GroupSum head and out = logits [B, C] (counts
+ * of y > 0.5 / tau); C = 0: out = the last layer's activations
+ * [B, out_dim[n_layers-1]]. SLG_E_UNSUPPORTED when neither kernel takes the
+ * shapes (slg_fc_soft_net_supported says 0). */
 int slg_fc_soft_net_records(const float* x, int64_t B, int64_t IN, int32_t n_layers,
                             const float* const* rec, const int64_t* in_dim,
                             const int64_t* out_dim, int32_t K, int32_t node_kind, float inv_tau,
                             int32_t C, float tau, float* out, slg_stream_t stream);
-/* 1 when slg_fc_soft_net_records takes these shapes and is the faster path
- * (batches below two 8-sample tiles per CU), else 0. */
+/* Which kernel slg_fc_soft_net_records runs for these shapes, where it is
+ * the faster path: 1 = two LDS buffers (every activation buffer fits LDS
+ * twice, batches below two 8-sample tiles per CU), 2 = one LDS buffer (K =
+ * 8, widths whose 4- or 2-sample tile fits LDS, at least one tile per CU);
+ * 0 = a launch per layer (slg_fc_soft_fwd_records). */
 int slg_fc_soft_net_supported(int64_t B, int64_t IN, int32_t n_layers, const int64_t* out_dim,
                               int32_t K, int32_t C);
 /* 1 if slg_fc_soft_fwd_groupsum runs this shape (one workgroup holds every

@@ -492,6 +492,272 @@ fc_soft_net_kernel(const float* __restrict__ x, int B, int IN, SoftNetDesc d,
   }
 }
 
+// ---------------------------------------------------------------------------
+// A whole wide network per sample tile (large batches)
+// ---------------------------------------------------------------------------
+// A layer launched on its own stages its S-sample tile from HBM, computes
+// every output and writes them back: at config 2 (10000-wide layers, 4-sample
+// tiles) the staging cannot overlap the compute (the tile fills LDS) and
+// costs about a quarter of the layer. Here a workgroup takes its tile through
+// every layer with one LDS buffer: a layer computes all of the tile's
+// outputs with fc_soft_rec_kernel's arithmetic (same records, the same fmaf
+// sequence per output and sample, so the same bits), holds them in
+// registers (each wave its CPW chunks of 64 outputs, S values per lane and
+// chunk), and after a barrier writes them over its input. HBM then sees the
+// first layer's input rows and the logits (or the last activations) only;
+// what remains per layer is the record stream from L2 and the LDS gathers.
+constexpr int kRecNetThreads = 512;
+struct RecNetDesc {
+  const uint32_t* rec[kMaxNetLayers];
+  int out_dim[kMaxNetLayers];
+  int L;
+  float inv_tau;
+};
+
+template <int NODE, int KC, int S, int CPW, bool HEAD>
+__global__ void __launch_bounds__(kRecNetThreads)
+fc_soft_rec_net_kernel(const float* __restrict__ x, int B, int IN, RecNetDesc d,
+                       float* __restrict__ y, int maxw, HeadArgs hd) {
+  static_assert(KC == 4 || KC == 8, "records take 4 or 8 candidates");
+  static_assert(S == 2 || S == 4, "tiles of 2 or 4 samples");
+  constexpr int RQ = rec_quads(KC);
+  constexpr int SH = S == 4 ? 4 : 3;  // log2 of the slot bytes
+  using vt = typename vecf<S>::t;
+  extern __shared__ __align__(16) unsigned char smem[];
+  vt* lds = reinterpret_cast<vt*>(smem);
+  unsigned* cnt = reinterpret_cast<unsigned*>(smem + (size_t)maxw * S * sizeof(float));
+  const int b0 = blockIdx.x * S;
+  const int rows = min(S, B - b0);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int nwaves = kRecNetThreads / 64;
+  const int lane16 = lane * 16;
+  if constexpr (HEAD) {
+    for (int t = threadIdx.x; t < S * hd.C; t += blockDim.x) cnt[t] = 0u;
+  }
+
+  // a chunk's record quads: wave-uniform offset + the lane's 16 bytes
+  auto load_rec = [&](u32x4 (&R)[RQ], const __amdgpu_buffer_rsrc_t& rr, int c, int c_last) {
+    const int so = min(c, c_last) * (RQ * 1024);
+#pragma unroll
+    for (int q = 0; q < RQ; ++q)
+      R[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, lane16, so + q * 1024, 0));
+  };
+  // one chunk of 64 outputs for the tile's S samples (fc_soft_rec_kernel's
+  // chunk arithmetic)
+  auto chunk_vals = [&](const u32x4 (&R)[RQ], float (&yv)[S]) __attribute__((always_inline)) {
+    auto word = [&](int w) { return R[w >> 2][w & 3]; };
+    vt A = zero_vec<vt>(), Bv = zero_vec<vt>();
+    {
+      vt ga[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) ga[k] = lds_at<vt>(idx_lo_bytes<SH>(word(k)));
+#pragma unroll
+      for (int k = 0; k < KC; ++k) fma_acc(A, __uint_as_float(word(KC + k)), ga[k]);
+    }
+    asm volatile("" : "+v"(A)::"memory");
+    {
+      vt gb[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) gb[k] = lds_at<vt>(idx_hi_bytes<SH>(word(k)));
+#pragma unroll
+      for (int k = 0; k < KC; ++k) fma_acc(Bv, __uint_as_float(word(2 * KC + k)), gb[k]);
+    }
+    const float4 p = make_float4(__uint_as_float(word(4 * (RQ - 1))),
+                                 __uint_as_float(word(4 * (RQ - 1) + 1)),
+                                 __uint_as_float(word(4 * (RQ - 1) + 2)),
+                                 __uint_as_float(word(4 * (RQ - 1) + 3)));
+#pragma unroll
+    for (int v = 0; v < S; ++v) yv[v] = node_eval<NODE>(lanev(A, v), lanev(Bv, v), p, d.inv_tau);
+  };
+
+  constexpr int NB = S == 4 ? 3 : 5;
+  stage_rows<S, true, NB>(lds, x, B, IN, b0);
+  __syncthreads();
+
+  // every layer but the last: outputs held in registers, then written over
+  // the tile after every wave has read it
+  for (int l = 0; l + 1 < d.L; ++l) {
+    const int OUT = d.out_dim[l];
+    const int n64 = (OUT + 63) >> 6;
+    const int cpw = (n64 + nwaves - 1) / nwaves;   // <= CPW (checked on the host)
+    const int j_begin = wave * cpw, j_end = min(n64, j_begin + cpw);
+    const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(d.rec[l], n64 * RQ * 1024);
+    u32x4 R[2][RQ];
+    float res[CPW][S];
+    if (j_begin < j_end) load_rec(R[0], rr, j_begin, n64 - 1);
+#pragma unroll
+    for (int jj = 0; jj < CPW; ++jj) {
+      if (j_begin + jj < j_end) {
+        load_rec(R[(jj + 1) & 1], rr, j_begin + jj + 1, n64 - 1);
+        chunk_vals(R[jj & 1], res[jj]);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < CPW; ++jj) {
+      const int o = (j_begin + jj) * 64 + lane;
+      if (j_begin + jj < j_end && o < OUT) lds[o] = make_vec<S>(res[jj]);
+    }
+    __syncthreads();
+  }
+
+  // the last layer: the STE GroupSum's class counts, or the activations
+  {
+    const int l = d.L - 1;
+    const int OUT = d.out_dim[l];
+    const int n64 = (OUT + 63) >> 6;
+    const int cpw = (n64 + nwaves - 1) / nwaves;
+    const int j_begin = wave * cpw, j_end = min(n64, j_begin + cpw);
+    const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(d.rec[l], n64 * RQ * 1024);
+    __amdgpu_buffer_rsrc_t yrows;
+    if constexpr (!HEAD) yrows = uniform_rsrc(y + (int64_t)b0 * OUT, rows * OUT * 4);
+    int cur_c = 0, hi_b = 0;
+    unsigned acc[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[s] = 0u;
+    if constexpr (HEAD) {
+      if (j_begin < j_end) {
+        cur_c = (j_begin * 64) / hd.per;
+        hi_b = (cur_c + 1) * hd.per;
+      }
+    }
+    u32x4 P[RQ], Q[RQ];
+    auto emit = [&](const u32x4 (&R)[RQ], int j) __attribute__((always_inline)) {
+      float yv[S];
+      chunk_vals(R, yv);
+      const int oc0 = j * 64;
+      const int o = oc0 + lane;
+      const bool valid = o < OUT;
+      if constexpr (HEAD) {
+        const int oc1 = min(oc0 + 63, OUT - 1);
+        if (oc1 < hi_b) {  // the whole chunk lies in class cur_c (wave-uniform)
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            acc[s] += (unsigned)__popcll(__ballot(valid && s < rows && yv[s] > 0.5f));
+        } else {
+          if (lane == 0) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+              if (acc[s]) atomicAdd(&cnt[s * hd.C + cur_c], acc[s]);
+          }
+#pragma unroll
+          for (int s = 0; s < S; ++s) acc[s] = 0u;
+          if (valid) {
+            const int c = o / hd.per;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+              if (s < rows && yv[s] > 0.5f) atomicAdd(&cnt[s * hd.C + c], 1u);
+          }
+          cur_c = (oc1 + 1) / hd.per;
+          hi_b = (cur_c + 1) * hd.per;
+        }
+      } else {
+        const uint32_t vo = valid ? (uint32_t)o * 4u : 0x80000000u;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+          if (s < rows)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv[s]), yrows, (int)vo,
+                                                  s * OUT * 4, 0);
+      }
+    };
+    if (j_begin < j_end) {
+      load_rec(P, rr, j_begin, n64 - 1);
+      int j = j_begin;
+      while (true) {
+        load_rec(Q, rr, j + 1, n64 - 1);
+        emit(P, j);
+        if (++j >= j_end) break;
+        load_rec(P, rr, j + 1, n64 - 1);
+        emit(Q, j);
+        if (++j >= j_end) break;
+      }
+      if constexpr (HEAD) {
+        if (lane == 0) {
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            if (acc[s]) atomicAdd(&cnt[s * hd.C + cur_c], acc[s]);
+        }
+      }
+    }
+  }
+  if constexpr (HEAD) {
+    __syncthreads();
+    for (int t = threadIdx.x; t < S * hd.C; t += blockDim.x) {
+      const int s = t / hd.C, c = t % hd.C;
+      if (b0 + s < B) hd.logits[(int64_t)(b0 + s) * hd.C + c] = (float)cnt[t] / hd.tau;
+    }
+  }
+}
+
+// Tile and chunk bound of fc_soft_rec_net_kernel for a network (K = 8):
+// 4-sample tiles where every width fits LDS four times over, else 2; the
+// chunks per wave of the widest layer must fit one of the compiled bounds.
+// 0: the kernel does not apply.
+struct RecNetShape {
+  int S, CPW;
+  size_t lds;
+};
+static RecNetShape rec_net_shape(int64_t IN, int L, const int64_t* out_dim, int K, int C) {
+  RecNetShape r{0, 0, 0};
+  if (K != 8 || L < 2) return r;
+  int64_t maxw = IN, max_out = 0;
+  for (int l = 0; l < L; ++l) {
+    maxw = std::max<int64_t>(maxw, out_dim[l]);
+    if (l + 1 < L) max_out = std::max<int64_t>(max_out, out_dim[l]);
+  }
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  const int waves = kRecNetThreads / 64;
+  const int64_t cpw = cdiv(cdiv(max_out, 64), waves);
+  for (int s : {4, 2}) {
+    const int64_t lds = maxw * s * 4 + (int64_t)s * std::max(C, 0) * 4;
+    if (lds > cap) continue;
+    const int bound = s == 4 ? (cpw <= 12 ? 12 : (cpw <= 20 ? 20 : 0))
+                             : (cpw <= 16 ? 16 : (cpw <= 32 ? 32 : 0));
+    if (bound == 0) continue;
+    r.S = s;
+    r.CPW = bound;
+    r.lds = (size_t)lds;
+    return r;
+  }
+  return r;
+}
+
+template <int NODE, int S, int CPW, bool HEAD>
+static int launch_rec_net(const float* x, int64_t B, int64_t IN, const RecNetDesc& d, float* y,
+                          int maxw, const HeadArgs& hd, size_t lds, hipStream_t st) {
+  auto kern = fc_soft_rec_net_kernel<NODE, 8, S, CPW, HEAD>;
+  static const size_t static_lds = [&] {
+    hipFuncAttributes fa{};
+    return hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess ? fa.sharedSizeBytes
+                                                                        : (size_t)-1;
+  }();
+  SLG_REQUIRE(static_lds == 0, SLG_E_UNSUPPORTED,
+              "fc_soft_rec_net: the kernel expects its LDS tile at address 0");
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("fc_soft_rec_net: cannot reserve %zu B LDS: %s", lds, hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(B, S)), dim3(kRecNetThreads), lds, st, x, (int)B,
+                     (int)IN, d, y, maxw, hd);
+  SLG_LAUNCH_CHECK("fc_soft_rec_net");
+  return 0;
+}
+
+template <int NODE, bool HEAD>
+static int rec_net_node(const RecNetShape& sh, const float* x, int64_t B, int64_t IN,
+                        const RecNetDesc& d, float* y, int maxw, const HeadArgs& hd,
+                        hipStream_t st) {
+  if (sh.S == 4 && sh.CPW == 12) return launch_rec_net<NODE, 4, 12, HEAD>(x, B, IN, d, y, maxw, hd, sh.lds, st);
+  if (sh.S == 4) return launch_rec_net<NODE, 4, 20, HEAD>(x, B, IN, d, y, maxw, hd, sh.lds, st);
+  if (sh.CPW == 16) return launch_rec_net<NODE, 2, 16, HEAD>(x, B, IN, d, y, maxw, hd, sh.lds, st);
+  return launch_rec_net<NODE, 2, 32, HEAD>(x, B, IN, d, y, maxw, hd, sh.lds, st);
+}
+
 // LDS bytes of fc_soft_net_kernel for the widths, or 0 when they do not fit.
 static int64_t soft_net_lds(int64_t IN, int L, const int64_t* out_dim, int C) {
   int64_t maxw = IN;
@@ -1193,6 +1459,19 @@ int slg_fc_soft_fwd_records(const float* x, int64_t B, int64_t IN, int64_t OUT, 
   return fc_soft_dispatch(a, node_kind, as_stream(stream));
 }
 
+// Which whole-network kernel a stack takes: 1 = fc_soft_net_kernel (every
+// activation buffer fits LDS twice, a batch below two 8-sample tiles per
+// CU: one launch for the network beats a launch per layer); 2 =
+// fc_soft_rec_net_kernel (K = 8, a tile of 4 or 2 samples per workgroup
+// through every layer, for batches that give every CU a tile); 0 = a
+// launch per layer.
+static int soft_net_kind(int64_t B, int64_t IN, int L, const int64_t* out_dim, int K, int C) {
+  if (soft_net_lds(IN, L, out_dim, C) && B < 16 * (int64_t)device_cus()) return 1;
+  const RecNetShape sh = rec_net_shape(IN, L, out_dim, K, C);
+  if (sh.S > 0 && cdiv(B, sh.S) >= device_cus()) return 2;
+  return 0;
+}
+
 int slg_fc_soft_net_supported(int64_t B, int64_t IN, int32_t n_layers, const int64_t* out_dim,
                               int32_t K, int32_t C) {
   if (B <= 0 || B >= (1LL << 31) || IN <= 0 || IN > 65536 || !out_dim || n_layers < 1 ||
@@ -1201,10 +1480,7 @@ int slg_fc_soft_net_supported(int64_t B, int64_t IN, int32_t n_layers, const int
   for (int l = 0; l < n_layers; ++l)
     if (out_dim[l] <= 0 || out_dim[l] > 65536) return 0;
   if (C > 0 && out_dim[n_layers - 1] % C != 0) return 0;
-  if (!soft_net_lds(IN, n_layers, out_dim, C)) return 0;
-  // a launch per layer fills the chip once the batch gives two 8-sample
-  // tiles per CU; below that one launch for the network is faster
-  return B < 16 * (int64_t)device_cus() ? 1 : 0;
+  return soft_net_kind(B, IN, n_layers, out_dim, K, C);
 }
 
 int slg_fc_soft_net_records(const float* x, int64_t B, int64_t IN, int32_t n_layers,
@@ -1241,13 +1517,37 @@ int slg_fc_soft_net_records(const float* x, int64_t B, int64_t IN, int32_t n_lay
   SLG_REQUIRE(C == 0 || out_dim[n_layers - 1] % C == 0, SLG_E_SHAPE,
               "fc_soft_net: last width %lld not divisible by %d classes",
               (long long)out_dim[n_layers - 1], C);
-  const int64_t lds = soft_net_lds(IN, n_layers, out_dim, C);
-  SLG_REQUIRE(lds > 0, SLG_E_UNSUPPORTED, "fc_soft_net: widths do not fit LDS");
-  d.maxw = (int)maxw;
   if (B == 0) return 0;
+  const int kind = soft_net_kind(B, IN, n_layers, out_dim, K, C);
+  SLG_REQUIRE(kind != 0, SLG_E_UNSUPPORTED,
+              "fc_soft_net: no whole-network kernel for these widths and this batch");
+  d.maxw = (int)maxw;
   HeadArgs hd{out, C, C > 0 ? (int)(out_dim[n_layers - 1] / C) : 0, tau};
   hipStream_t st = as_stream(stream);
   const bool head = C > 0;
+  if (kind == 2) {
+    RecNetDesc rd{};
+    rd.L = n_layers;
+    rd.inv_tau = inv_tau;
+    for (int l = 0; l < n_layers; ++l) {
+      rd.rec[l] = reinterpret_cast<const uint32_t*>(rec[l]);
+      rd.out_dim[l] = (int)out_dim[l];
+    }
+    const RecNetShape sh = rec_net_shape(IN, n_layers, out_dim, K, C);
+    switch (node_kind) {
+      case SLG_NODE_GATE16:
+        return head ? rec_net_node<SLG_NODE_GATE16, true>(sh, x, B, IN, rd, nullptr, (int)maxw, hd, st)
+                    : rec_net_node<SLG_NODE_GATE16, false>(sh, x, B, IN, rd, out, (int)maxw, hd, st);
+      case SLG_NODE_WALSH:
+        return head ? rec_net_node<SLG_NODE_WALSH, true>(sh, x, B, IN, rd, nullptr, (int)maxw, hd, st)
+                    : rec_net_node<SLG_NODE_WALSH, false>(sh, x, B, IN, rd, out, (int)maxw, hd, st);
+      default:
+        return head ? rec_net_node<SLG_NODE_MULTILINEAR2, true>(sh, x, B, IN, rd, nullptr, (int)maxw, hd, st)
+                    : rec_net_node<SLG_NODE_MULTILINEAR2, false>(sh, x, B, IN, rd, out, (int)maxw, hd,
+                                                                 st);
+    }
+  }
+  const int64_t lds = soft_net_lds(IN, n_layers, out_dim, C);
   switch (node_kind) {
     case SLG_NODE_GATE16:
       return head ? soft_net_node<SLG_NODE_GATE16, true>(x, B, IN, d, nullptr, hd, lds, st)

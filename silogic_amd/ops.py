@@ -385,8 +385,12 @@ class SoftStackPlan:
         out_arr = (ctypes.c_int64 * L)(*[t[4] for t in self.layers])
         C = head[0] if head is not None else 0
         self.net = None
-        if (not wire_r and len(kinds) == 1 and len(taus) == 1 and len(Ks) == 1
-                and _lib.lib().slg_fc_soft_net_supported(B, IN, L, out_arr, Ks.pop(), C)):
+        # which one-launch kernel (1: two LDS buffers, 2: one buffer, tiles
+        # through every layer); 0: a launch per layer
+        self.net_kind = 0
+        if not wire_r and len(kinds) == 1 and len(taus) == 1 and len(Ks) == 1:
+            self.net_kind = _lib.lib().slg_fc_soft_net_supported(B, IN, L, out_arr, Ks.pop(), C)
+        if self.net_kind:
             self.net = ((ctypes.c_void_p * L)(*[t[1].value for t in self.layers]),
                         (ctypes.c_int64 * L)(*[t[3] for t in self.layers]), out_arr)
         self.fwd_net = _lib.lib().slg_fc_soft_net_records
