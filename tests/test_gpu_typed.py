@@ -156,6 +156,26 @@ def test_typed_network_edge_batches_and_depths(in_dim, widths, C, B):
     assert torch.equal(ops.fc_hard_net(x8, ops.ROWS_U8, B, in_dim, typed, C), ref)
 
 
+@pytest.mark.parametrize("in_dim", [784, 786, 200, 1024])
+@pytest.mark.parametrize("B", [1, 63, 64 * 3 + 5, 64 * 300 + 7])
+def test_row_streams_match_the_packed_path(in_dim, B):
+    """The rows kernel's fused packing (one feature a thread, chunks of
+    samples streamed during the layers) must give the bits pack_bits gives
+    (v >= 1, NaN and negatives 0) on non-binary fp32 rows, on partial tiles
+    and on more tiles than workgroups, through plain and type-placed codes."""
+    net = _net(in_dim, [1200, 1100, 900], seed=57)
+    codes = _codes(net)
+    typed = ops.fc_hard_type_place_net(codes, in_dim)
+    g = torch.Generator().manual_seed(B + in_dim)
+    x = torch.rand(B, in_dim, generator=g) * 3.0 - 1.0
+    x[torch.rand(B, in_dim, generator=g) < 0.1] = 1.0
+    x[torch.rand(B, in_dim, generator=g) < 0.01] = float("nan")
+    x = x.to(DEV)
+    ref = ops.fc_hard_net(ops.pack_bits(x), ops.PACKED, B, in_dim, codes, 10)
+    assert torch.equal(ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, codes, 10), ref)
+    assert torch.equal(ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, typed, 10), ref)
+
+
 def test_typed_plan_for_another_width_gives_nan_logits():
     """Codes placed for one input width, run through the C ABI for another:
     a different slot count (1500 -> 2 slots per thread, 2500 -> 4) and the
