@@ -406,9 +406,14 @@ def hard_launches(cfg, model, x_hard):
             in_dim, C = a[3], model.head.num_classes
             widths = [l.out_dim for l in layers]
             codes = sum(widths) * 4
+            cus = torch.cuda.get_device_properties(x_hard.device).multi_processor_count
             if a[1] in (0, 1):       # rows: packing inside
                 nbytes = B * in_dim * isz + B * C * 4 + codes
                 kname = f"fc_hard_net_rows_kernel (packing + {len(widths)} layers + GroupSum)"
+            elif len(widths) == 1 and 2 * nw < cus and widths[0] // C <= 8192:
+                # one layer, few words: a workgroup per (word, class)
+                nbytes = in_dim * nw * 8 + B * C * 4 + codes
+                kname = f"fc_hard_head_kernel (1 layer + GroupSum, {nw} words x {C} classes)"
             else:
                 nbytes = in_dim * nw * 8 + B * C * 4 + codes
                 kname = f"fc_hard_net_packed_kernel ({len(widths)} layers + GroupSum)"

@@ -337,7 +337,10 @@ int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw,
  * n_layers arity-2 layers whose widths and device code arrays are given
  * by the host arrays widths[n_layers] and codes[n_layers], then writes logits [B,C] fp32 = per-class popcounts of
  * the last layer (no tau). One workgroup keeps a 64-sample (or, for wide
- * layers, 32-sample) column of every activation in LDS across all layers.
+ * layers, 32-sample) column of every activation in LDS across all layers;
+ * a one-layer network on packed input with fewer 64-sample words than half
+ * the CUs instead takes one workgroup per (word, class), which reads its
+ * gates' operand words from memory (same logits).
  * wire_r > 0 replaces the first wire_r outputs of a same-width layer by its
  * inputs (models.py:88-94). Returns SLG_E_UNSUPPORTED when the widths do not
  * fit LDS (see slg_fc_hard_net_supported). */

@@ -812,6 +812,72 @@ __device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int b
   }
 }
 
+// One-layer networks at small batches (a conv network's head on a few
+// sample words): the fused kernel's one workgroup per word would leave most
+// CUs idle and stage every input word in LDS although each gate reads two.
+// Here workgroup (w, c) evaluates the G = W / C gates of class c on word w
+// straight from the packed words in memory, writes them to LDS and counts
+// them as the fused kernel's GroupSum does (class_count, wave 0): nw * C
+// workgroups, the logits the same integers. Codes: compact codes in index
+// order, or (type-placed, with a plan) stored thread-major at TM slots per
+// thread, output o at (o % 1024) * TM + o / 1024. (Two-layer heads, layer 0
+// evaluated per workgroup from memory, measured no faster than the fused
+// kernel at config 3's head and are left to it.)
+constexpr int kHeadThreads = 256;
+constexpr int kHeadMaxG = 8192;   // a class's gate words in 64 KiB of LDS
+
+template <int LAYOUT>
+__global__ void __launch_bounds__(kHeadThreads)
+fc_hard_head_kernel(const uint64_t* __restrict__ xp, int B, int nw, int in0, int G, int C,
+                    const uint32_t* __restrict__ codes, int tm, const int32_t* plan,
+                    float* __restrict__ logits) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* cls = reinterpret_cast<uint64_t*>(smem);
+  const int w = blockIdx.x, c = blockIdx.y;
+  if (plan && !plan_fits(plan, tm, in0)) {   // typed codes placed for another layout
+    if (threadIdx.x < 64 && w * 64 + (int)threadIdx.x < B)
+      logits[(int64_t)(w * 64 + threadIdx.x) * C + c] = __int_as_float(0x7FC00000);
+    return;
+  }
+  for (int i = threadIdx.x; i < G; i += kHeadThreads) {
+    const int o = c * G + i;
+    const uint32_t code = codes[tm ? (o & (kNetThreads - 1)) * tm + (o >> 10) : o];
+    // the prep keeps operands below the width; a read never leaves it
+    const int a = min((int)((code >> 14) & 0x3FFFu), in0 - 1);
+    const int b = min((int)(code & 0x3FFFu), in0 - 1);
+    const uint64_t va = LAYOUT == 0 ? xp[(int64_t)a * nw + w] : xp[(int64_t)w * in0 + a];
+    const uint64_t vb = LAYOUT == 0 ? xp[(int64_t)b * nw + w] : xp[(int64_t)w * in0 + b];
+    cls[i] = gate_compact<uint64_t>(va, vb, code);
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int n = class_count<2>(reinterpret_cast<const uint32_t*>(cls), G, lane);
+    const int b = w * 64 + lane;
+    if (b < B) logits[(int64_t)b * C + c] = (float)n;
+  }
+}
+
+// Whether a one-layer network on packed words takes fc_hard_head_kernel:
+// fewer sample words than half the CUs (the fused kernel's workgroups), no
+// wire residual, a class in LDS.
+static bool use_head(int n_layers, int64_t wire_r, int in_kind, int64_t B, int64_t width, int C) {
+  return n_layers == 1 && wire_r <= 0 && in_kind >= 2 && B > 0 &&
+         2 * cdiv(B, 64) < device_cus() && width / C <= kHeadMaxG;
+}
+
+static int launch_head(const uint64_t* xp, int in_kind, int64_t B, int64_t IN0, int64_t width,
+                       int C, const uint32_t* codes, int tm, const int32_t* plan, float* logits,
+                       hipStream_t st) {
+  const int64_t nw = cdiv(B, 64);
+  const int G = (int)(width / C);
+  auto kern = in_kind == 2 ? fc_hard_head_kernel<0> : fc_hard_head_kernel<1>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nw, (unsigned)C), dim3(kHeadThreads), (size_t)G * 8, st,
+                     xp, (int)B, (int)nw, (int)IN0, G, C, codes, tm, plan, logits);
+  SLG_LAUNCH_CHECK("fc_hard_head");
+  return 0;
+}
+
 // Pre-packed input: LAYOUT 0 = [in0][nw] (reference layout), 1 = [nw][in0].
 template <int LAYOUT, typename WT, int MAXO, bool TYPED>
 __global__ void __launch_bounds__(kNetThreads)
@@ -1908,6 +1974,10 @@ int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0
   const int maxo = (int)(S / kNetThreads);
   const size_t lds = (size_t)2 * d.maxw * (spw / 8);
   hipStream_t st = as_stream(stream);
+  // one layer at a small batch: per (word, class) workgroups
+  if (use_head(n_layers, 0, in_kind, B, widths[0], C))
+    return launch_head((const uint64_t*)x, in_kind, B, IN0, widths[0], C, codes[0], maxo, plan,
+                       logits, st);
   if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
   if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
   const int64_t tiles = cdiv(B, spw);
@@ -1958,6 +2028,10 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
   d.maxw = maxo * kNetThreads;
   const size_t lds = (size_t)2 * d.maxw * (spw / 8);
   hipStream_t st = as_stream(stream);
+  // one layer at a small batch: per (word, class) workgroups
+  if (use_head(n_layers, wire_r, in_kind, B, widths[0], C))
+    return launch_head((const uint64_t*)x, in_kind, B, IN0, widths[0], C, codes[0], 0, nullptr,
+                       logits, st);
   if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
   if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
   const int64_t tiles = cdiv(B, spw);
