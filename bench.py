@@ -129,10 +129,10 @@ def cpu_baseline(cfg, sd, x_hard, x_soft, gates):
 
 
 def load_traffic(cfg):
-    """HBM bytes per launch of config ``cfg``'s dominant kernels, measured with
-    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and scaled by the same counters'
-    reading for a plain copy of known size (profiles/hbm_traffic.json, keyed
-    by config; see --kernels-only)."""
+    """HBM bytes per launch of config ``cfg``'s launches, measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over ``--kernels-only`` and
+    scaled by the same counters' reading for a plain copy of known size
+    (profiles/hbm_traffic.json: per config, launch name -> bytes)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     if not os.path.exists(path):
         return {}
@@ -141,19 +141,34 @@ def load_traffic(cfg):
 
 
 def kernels_only(reps=3):
-    """Workload for counter passes: a 256 MiB copy (calibration), then, per
-    config at the bench's batch sizes, ``reps`` launches each of every
+    """Workload for counter passes: a 256 MiB device copy (calibration), then,
+    per config at the bench's batch sizes, ``reps`` launches each of every
     launch of ``forward_hard`` (packing, conv blocks, fused networks) and of
-    every stage of the soft forward the bench times (the FC hidden layer, or
-    each conv block with its OrPool and the FC head)."""
+    every stage of the soft forward the bench times. Each group of ``reps``
+    launches runs after one untimed launch and between two one-byte
+    ``bitwise_not_`` launches (no other code here runs that op), so that a
+    trace can assign its dispatches to the group; the groups' names, in
+    order, are printed as one JSON line on stdout (``cfgN | <launch name>``,
+    the names the bench's per-launch records use)."""
     import silogic_amd as sl
     from silogic_amd.synthetic import BATCHES, build_config, config_inputs
     dev = torch.device("cuda:0")
+    marker = torch.zeros(1, device=dev, dtype=torch.uint8)
+    groups = []
+
+    def group(label, fn, nbytes, work):
+        fn()
+        torch.cuda.synchronize()
+        marker.bitwise_not_()
+        for _ in range(reps):
+            fn()
+        marker.bitwise_not_()
+        torch.cuda.synchronize()
+        groups.append({"launch": label, "algorithmic_bytes": nbytes, "work": work})
+
     src = torch.ones(64 << 20, device=dev)          # 256 MiB
     dst = torch.empty_like(src)
-    for _ in range(reps):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    group("calibration | 256 MiB copy", lambda: dst.copy_(src), 2 * src.numel() * 4, None)
     del src, dst
     for cfg in (1, 2, 3, 4, 5):
         model = build_config(cfg, sl).eval().to(dev)
@@ -161,16 +176,14 @@ def kernels_only(reps=3):
         x_hard = config_inputs(cfg, B_hard).to(dev)
         x_soft = x_hard[:B_soft].contiguous()
         with torch.no_grad():
-            for name, fn, _, _ in hard_launches(cfg, model, x_hard):
-                for _ in range(reps):
-                    fn()
-            for name, fn, _, _, _, _ in soft_stages(cfg, model, B_soft, x_soft, dev):
-                for _ in range(reps):
-                    fn()
-        torch.cuda.synchronize()
+            for name, fn, nbytes, bops in hard_launches(cfg, model, x_hard):
+                group(f"cfg{cfg} | {name}", fn, nbytes, {"bitops": bops})
+            for name, fn, nbytes, flops, _, _ in soft_stages(cfg, model, B_soft, x_soft, dev):
+                group(f"cfg{cfg} | {name}", fn, nbytes, {"flops": flops})
         log(f"kernels-only: config {cfg} done")
         del model, x_hard, x_soft
         torch.cuda.empty_cache()
+    print(json.dumps({"kernels_only_groups": groups, "reps": reps}), flush=True)
     log("kernels-only done")
 
 
@@ -520,14 +533,16 @@ def measure_config(cfg, steps, warmup, with_cpu):
                            "algorithmic_bytes": nbytes,
                            "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
                            "bitops": bops,
-                           "valu_frac": round(bops / t / VALU_BITOPS_PEAK, 4)})
+                           "valu_frac": round(bops / t / VALU_BITOPS_PEAK, 4),
+                           "traffic": traffic.get(name)})
         soft_k = []
         for name, fn, nbytes, flops, count, extra in soft_stages(cfg, model, B_soft, x_soft, dev):
             fn()
             t = _events_ms(fn, reps) / 1e3
             rec = {"kernel": name, "avg_kernel_us": round(t * 1e6, 2), "launches_per_forward": count,
                    "algorithmic_bytes": nbytes,
-                   "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+                   "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                   "traffic": traffic.get(name)}
             rec.update(extra)
             if "l2_record_stream_bytes" in extra:
                 rec["l2_record_GBps"] = round(extra["l2_record_stream_bytes"] / t / 1e9, 1)
@@ -555,7 +570,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
         res["roofline_soft"] = {
             "kernel": dom["kernel"], "bound": "fp32", "achieved": round(tflops, 2),
             "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
-            "traffic": traffic.get(dom["kernel"].split(":")[0]),
+            "traffic": traffic.get(dom["kernel"]),
             "algorithmic_flops": dom["algorithmic_flops"],
             "algorithmic_bytes": dom["algorithmic_bytes"], "hbm_frac": dom["hbm_frac"],
             "avg_kernel_us": dom["avg_kernel_us"],
@@ -565,7 +580,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
                                      "l2_record_GBps", "bytes_counted_as") if k in dom}
         res["roofline_soft"] = _roof_hbm(
             dom["kernel"], dom["algorithmic_bytes"], t_dom,
-            traffic.get(dom["kernel"].split(" ")[0]),
+            traffic.get(dom["kernel"]),
             share_of_forward=round(dom["avg_kernel_us"] * dom["launches_per_forward"]
                                    / (t_soft * 1e6), 3), **extra)
     # hard roofline. FC networks: the launches from the fp32 rows to the
@@ -578,8 +593,9 @@ def measure_config(cfg, steps, warmup, with_cpu):
             nbytes = B_hard * x_hard.shape[1] * 4 + B_hard * model.head.num_classes * 4 + \
                 sum(l.out_dim for l in model.layers) * 4
             name = " + ".join(r["kernel"] for r in hard_k)
+            moved = [traffic.get(r["kernel"]) for r in hard_k]
             res["roofline_hard"] = _roof_hbm(
-                name, nbytes, t, traffic.get(hard_k[-1]["kernel"].split(" ")[0]),
+                name, nbytes, t, None if None in moved else sum(moved),
                 valu_frac=round(B_hard * bitops_ps / t / VALU_BITOPS_PEAK, 4))
         else:
             convs = [r for r in hard_k if r["kernel"].startswith("conv_hard")]
@@ -588,7 +604,7 @@ def measure_config(cfg, steps, warmup, with_cpu):
             res["roofline_hard"] = {
                 "kernel": d["kernel"], "bound": "valu",
                 "achieved": d["bitops"] / t, "peak": VALU_BITOPS_PEAK, "unit": "bit-ops/s",
-                "frac": d["valu_frac"], "traffic": traffic.get("conv_hard_kernel"),
+                "frac": d["valu_frac"], "traffic": traffic.get(d["kernel"]),
                 "algorithmic_bitops": d["bitops"], "algorithmic_bytes": d["algorithmic_bytes"],
                 "hbm_frac": d["hbm_frac"], "avg_kernel_us": d["avg_kernel_us"]}
     bitops = B_hard * bitops_ps / t_hard

@@ -207,7 +207,13 @@ __device__ inline void conv_params_record_quad(ConvParams<NODE, NLEAF, KM, NW>& 
 // 128 VGPRs).
 constexpr int kQuadThreads = 1024;
 
-template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD>
+// SWAP (pooled row-major layout only): lanes of odd pooled columns take the
+// window's two columns in the other order, so that each of the four reads
+// of a tap hits even and odd LDS banks alike (in index order every lane of
+// a read is on a bank of one parity). Each lane keeps its order for every
+// leaf and tap, and the pooled output is the maximum over the four
+// positions, so the result is the same.
+template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD, bool SWAP = false>
 __global__ void __launch_bounds__((QUAD ? kQuadThreads : ConvCfg<NODE, NLEAF, KM, POOL>::THREADS))
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
                  int pad, ConvGeom g, const float* __restrict__ np, const float* __restrict__ wts,
@@ -357,6 +363,12 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
                             : (LINEAR ? q - (int)__umul24(s, g.LPS)
                                       : 2 * (int)__umul24(row, g.RS) + 2 * col);
       const float* base = lds + (active ? __umul24(s, g.SST) + bofs : 0);
+      static_assert(!SWAP || (POOL && !PHASE && !QUAD), "SWAP is for the pooled row-major layout");
+      const int sw = SWAP ? (col & 1) : 0;
+      const float* bq0 = base + sw;
+      const float* bq1 = base + 1 - sw;
+      const float* bq2 = base + g.RS + sw;
+      const float* bq3 = base + g.RS + 1 - sw;
 
       // Tap k of every leaf per step: the guard k < K is uniform, and one
       // step issues all NLEAF * NQ LDS reads before its first wait. With
@@ -378,6 +390,12 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
           } else if constexpr (PHASE) {
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq) t[l][qq] = base[Pc.off[l][k][qq]];
+          } else if constexpr (SWAP) {
+            const int o = Pc.off[l][k][0];
+            t[l][0] = bq0[o];
+            t[l][1] = bq1[o];
+            t[l][2] = bq2[o];
+            t[l][3] = bq3[o];
           } else {
             const float* t0 = base + Pc.off[l][k][0];
             t[l][0] = t0[0];
@@ -899,6 +917,41 @@ static ConvGeom conv_geom(int64_t C, int64_t H, int64_t W, int pad, bool pool, b
   return g;
 }
 
+// LDS cycles of the four reads of a tap over a wave's first chunk in the
+// pooled row-major layout, modelled as 32 banks of 4 bytes served per half
+// wave (distinct words of one bank serialise, equal words broadcast), with
+// the window's columns in index order (swap = false) or swapped on odd
+// pooled columns. The counters of the config blocks follow this model's
+// ratios.
+static int pooled_read_cycles(const ConvGeom& g, int Wo, bool swap) {
+  int total = 0;
+  for (int i = 0; i < 4; ++i) {
+    for (int h = 0; h < 2; ++h) {
+      int words[32][32], n[32] = {0}, worst = 0;
+      for (int ln = 32 * h; ln < 32 * h + 32; ++ln) {
+        const int s = ln / g.LPS, rem = ln % g.LPS, row = rem / Wo, col = rem % Wo;
+        const int sw = swap ? (col & 1) : 0;
+        const int dy = i >> 1, dx = (i & 1) ^ sw;
+        const int w = s * g.SST + 2 * row * g.RS + 2 * col + dy * g.RS + dx;
+        const int b = w & 31;
+        bool seen = false;
+        for (int j = 0; j < n[b]; ++j) seen = seen || words[b][j] == w;
+        if (!seen) words[b][n[b]++] = w;
+        worst = std::max(worst, n[b]);
+      }
+      total += worst;
+    }
+  }
+  return total;
+}
+
+// The swapped order where the model halves the reads' cycles from at least
+// 6 per read (a VALU add more per read: worth it where the reads stall).
+static bool conv_swap_pays(const ConvGeom& g, int Wo) {
+  const int plain = pooled_read_cycles(g, Wo, false), swapped = pooled_read_cycles(g, Wo, true);
+  return plain >= 24 && 2 * swapped <= plain;
+}
+
 template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD>
 static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   using Cfg = ConvCfg<NODE, NLEAF, KM, POOL>;
@@ -942,6 +995,9 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
     }
   }
   auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD>;
+  if constexpr (POOL && !Cfg::PHASE && !QUAD) {
+    if (conv_swap_pays(g, (int)a.Wo)) kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, true>;
+  }
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

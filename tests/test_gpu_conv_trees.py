@@ -53,6 +53,11 @@ def _blk(conv, H):
     ("gate16", 2, 2, "topk", 48, 32, 8, 2),      # 196 KB image: past LDS
     ("gate16", 2, 2, "topk", 13, 24, 8, 3),      # quad layout, staged without registers
     ("gate16", 2, 2, "topk", 7, 14, 10, 300),    # quad layout, persistent: 300 samples
+    # pooled row-major layout with the window's columns swapped on odd pooled
+    # columns (the read pattern of config 5's block 1: 128 channels, 16x16)
+    ("multilinear", 6, 1, "topk", 128, 16, 24, 2),
+    ("multilinear", 6, 1, "fixed", 128, 16, 12, 3),
+    ("gate16", 2, 3, "topk", 128, 16, 16, 2),
 ])
 def test_conv_tree_forward_and_hard(node, arity, depth, connect, C, H, N, B):
     conv = sl.ConvLogicTree(C, N, kernel=3, tree_depth=depth, connect=connect, k=4, n_chan=2,
