@@ -28,7 +28,6 @@
 // 6), the same bits.
 #include <algorithm>
 
-#include "pack_cols.h"
 #include "slg_common.h"
 
 namespace slg {
@@ -268,36 +267,65 @@ conv_hard_wm_kernel(const uint64_t* __restrict__ xp, int C, int H, int W, int nw
 
 // Packing of [B, C, H, W] images (fp32: x >= 1, bytes: x != 0; the
 // pack_bits rule) into the zero-bordered word-major layout: the interior of
-// [nw][C][H + 2p][W + 2p] (the border is left as it is). A lane takes V
-// consecutive pixels of one row (V = 4: W % 4 == 0, read as one vector);
-// the four waves of a workgroup take four consecutive words.
+// [nw][C][H + 2p][W + 2p] (the border is left as it is). A workgroup takes
+// one word and 64 V pixels; its four waves take the word's four 16-sample
+// quarters, a lane V consecutive pixels of one row (V = 4: W % 4 == 0, read
+// as one vector per sample), and each lane writes its 16 bits of each word
+// as one 2-byte store. (A lane taking all 64 samples of its pixels gave a
+// quarter of the workgroups: config 3's 24 MB packed at 3.3 TB/s.)
 template <typename T, int V>
 __global__ void __launch_bounds__(256)
 pack_image_kernel(const T* __restrict__ x, int B, int C, int H, int W, int pad, int nw, int dtiles,
                   uint64_t* __restrict__ xp) {
   const int lane = threadIdx.x & 63;
   const int D = C * H * W;
-  const int w = (int)(blockIdx.x / (uint32_t)dtiles) * 4 + (int)(threadIdx.x >> 6);
+  const int w = (int)(blockIdx.x / (uint32_t)dtiles);
+  const int q = (int)(threadIdx.x >> 6);                 // quarter of the word
   const int d0 = (int)(blockIdx.x % (uint32_t)dtiles) * 64 * V + lane * V;
-  if (w >= nw || d0 >= D) return;                       // no barriers below
+  if (w >= nw || d0 >= D) return;                        // no barriers below
+  const int nr = min(64, B - w * 64);                    // samples of the word
+  const int r0 = 16 * q;
   int src[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) src[v] = min(d0 + v, D - 1);
-  uint64_t word[V];
-  pack_cols<V, V == 4>(x + (int64_t)w * 64 * D, D, min(64, B - w * 64), src,
-                       [](T v, int) {
-                         if constexpr (sizeof(T) == 1) return v != 0;
-                         else return v >= (T)1;
-                       },
-                       word);
+  for (int v = 0; v < V; ++v) src[v] = min(d0 + v, D - 1);  // tail lanes: stores are guarded
+  auto bit = [](T v) {
+    if constexpr (sizeof(T) == 1) return v != 0;
+    else return v >= (T)1;
+  };
+  const T* xr = x + (int64_t)w * 64 * D;
+  uint32_t m[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) m[v] = 0;
+  // rows past the word's samples read its last row; their bits are cleared
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const T* row = xr + (int64_t)min(r0 + i, nr - 1) * D;
+    if constexpr (V == 4) {
+      if constexpr (sizeof(T) == 1) {
+        const uint32_t v4 = *reinterpret_cast<const uint32_t*>(row + src[0]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) m[v] |= (bit((T)(v4 >> (8 * v))) ? 1u : 0u) << i;
+      } else {
+        const float4 v4 = *reinterpret_cast<const float4*>(row + src[0]);
+        const float qv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) m[v] |= (bit(qv[v]) ? 1u : 0u) << i;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) m[v] |= (bit(row[src[v]]) ? 1u : 0u) << i;
+    }
+  }
+  const int valid = max(0, min(16, nr - r0));
+  const uint32_t keep = valid == 16 ? 0xFFFFu : (1u << valid) - 1u;
   const int Hp = H + 2 * pad, Wp = W + 2 * pad;
-  uint64_t* dst = xp + (int64_t)w * C * Hp * Wp;
+  uint16_t* dst = reinterpret_cast<uint16_t*>(xp + (int64_t)w * C * Hp * Wp);
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int d = d0 + v;
     if (d < D) {
       const int c = d / (H * W), r = d - c * H * W, y = r / W, xx = r - y * W;
-      dst[((int64_t)c * Hp + y + pad) * Wp + xx + pad] = word[v];
+      dst[(((int64_t)c * Hp + y + pad) * Wp + xx + pad) * 4 + q] = (uint16_t)(m[v] & keep);
     }
   }
 }
@@ -376,8 +404,8 @@ int slg_pack_image_wm(const void* x, int32_t dtype, int64_t B, int64_t C, int64_
   const size_t esz = dtype == 0 ? 4 : 1;
   const bool vec = W % 4 == 0 && (uintptr_t)x % (4 * esz) == 0;
   const int64_t dtiles = cdiv(D, vec ? 256 : 64);
-  SLG_REQUIRE(cdiv(nw, 4) * dtiles < (1LL << 31), SLG_E_SHAPE, "pack_image_wm: too many tiles");
-  dim3 grid((unsigned)(cdiv(nw, 4) * dtiles));
+  SLG_REQUIRE(nw * dtiles < (1LL << 31), SLG_E_SHAPE, "pack_image_wm: too many tiles");
+  dim3 grid((unsigned)(nw * dtiles));
   hipStream_t st = as_stream(stream);
 #define SLG_PI(T, V)                                                                          \
   hipLaunchKernelGGL((pack_image_kernel<T, V>), grid, dim3(256), 0, st, (const T*)x, (int)B,  \
