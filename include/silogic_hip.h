@@ -380,8 +380,14 @@ int64_t slg_fc_hard_type_slots(int64_t IN0, int32_t n_layers, const int64_t* wid
  * codes; within that, each 32 consecutive slots read operands of distinct
  * LDS bank classes where the counts allow. The last layer keeps its order
  * (compact codes, operands renamed; plan row U = 0). perm_ws: int32
- * workspace of widths[0] + .. + widths[n_layers-2] entries. One workgroup;
- * parameter-sized. */
+ * workspace of slg_fc_hard_type_place_workspace() entries (the renaming
+ * tables, then the placement's scratch). Per layer three launches: the
+ * plan (one workgroup), the greedy bins (one workgroup per bin) and the
+ * codes; parameter-sized. */
+/* int32 entries of slg_fc_hard_type_place_net's workspace for these widths
+ * (widths[0] + .. + widths[n_layers-2] for the renaming tables plus a fixed
+ * scratch), or -1. No counterpart in the reference. */
+int64_t slg_fc_hard_type_place_workspace(int32_t n_layers, const int64_t* widths);
 int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* widths,
                                const uint32_t* const* codes, uint32_t* const* placed,
                                int32_t* plan, int32_t* perm_ws, int64_t perm_ws_len,

@@ -44,6 +44,7 @@ SIGNATURES = {
     "slg_fc_hard_net": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _I32, _I64, _P, _P]),
     "slg_fc_hard_place_net": (C.c_int, [_I32, _P, _P, _P, _P, _I64, _P]),
     "slg_fc_hard_type_slots": (C.c_int64, [_I64, _I32, _P]),
+    "slg_fc_hard_type_place_workspace": (_I64, [_I32, _P]),
     "slg_fc_hard_type_place_net": (C.c_int, [_I32, _I64, _P, _P, _P, _P, _P, _I64, _P]),
     "slg_fc_hard_net_typed": (C.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _P, _I32, _P, _P]),
     "slg_fc_hard_net_supported": (C.c_int, [_I64, _I32, _P, _I32]),

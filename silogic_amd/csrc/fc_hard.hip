@@ -1458,177 +1458,250 @@ struct RegBin {
   }
 };
 
-__global__ void __launch_bounds__(kPlaceThreads) fc_hard_type_place_kernel(TypePlaceNet n) {
-  __shared__ uint8_t cnt[kTypeMaxGroups][64];      // per group: a-class counts, b-class counts
-  __shared__ int fill[kTypeMaxGroups];             // slots taken in each group
-  __shared__ uint16_t slot_of[kPlaceMax];          // output -> slot (0xFFFF: generic, unplaced)
-  __shared__ uint16_t info[kPlaceMax];             // a-class | b-class << 5 | type << 10
-  __shared__ uint16_t rank_of[kPlaceMax];          // rank of an output within its type
-  __shared__ int hist[16], m[16], w0[16], wtt[16];
-  __shared__ int plan_u, plan_rows;
+// The placement runs per layer as three launches, so that the greedy
+// steps of the bins run on as many CUs as there are bins (one workgroup of
+// one wave per bin) instead of sharing one CU's VALU: plan (one
+// workgroup), bins (one workgroup per type bin and per generic sub-bin),
+// codes (every output and slot). Scratch between them, in the caller's
+// workspace after the renaming tables (TypePlaceScratch).
+struct TypePlaceScratch {
+  uint32_t* info;   // [kPlaceMax] output -> a-class | b-class << 5 | type << 10
+  int32_t* olist;   // [kPlaceMax] outputs of the type bins, by type then rank
+  int32_t* glist;   // [kPlaceMax] generic outputs in index order
+  int32_t* slot;    // [kPlaceMax] output -> slot
+  int32_t* fill;    // [kTypeMaxGroups] slots taken in each group
+  int32_t* meta;    // U, rows, n_generic, then m, w0, wtt, tstart, tcount (16 each)
+};
+constexpr int kTypeMetaInts = 128;
+constexpr int kTypeScratchInts = 4 * kPlaceMax + kTypeMaxGroups + kTypeMetaInts;
+enum { kMetaU = 0, kMetaRows = 1, kMetaNGen = 2, kMetaM = 3, kMetaW0 = 19, kMetaWtt = 35,
+       kMetaTStart = 51, kMetaTCount = 67 };
+
+// Plan of layer l: operand classes and types, the plan row (U, rows, a
+// type per wave; the planner gives the 16 waves one at a time to the type
+// with the most outputs not yet given a wave and takes the largest U whose
+// overflow fits the rows left), the type bins' outputs by type in index
+// order, and the generic outputs in index order.
+__global__ void __launch_bounds__(kPlaceThreads)
+fc_hard_type_plan_kernel(TypePlaceNet n, TypePlaceScratch ws, int l) {
+  __shared__ uint16_t info[kPlaceMax];   // as ws.info, read back here from LDS
+  __shared__ uint8_t generic[kPlaceMax];
+  __shared__ int hist[16], m[16], w0[16], wtt[16], tstart[16];
+  __shared__ int plan_u;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int maxo = n.maxo, S = maxo * kNetThreads;
-  for (int l = 0; l + 1 < n.L; ++l) {
-    const int W = n.W[l];
-    for (int i = tid; i < kTypeMaxGroups * 16; i += kPlaceThreads)
-      reinterpret_cast<uint32_t*>(&cnt[0][0])[i] = 0u;
-    for (int i = tid; i < kTypeMaxGroups; i += kPlaceThreads) fill[i] = 0;
-    if (tid < 16) hist[tid] = 0;
-    __syncthreads();
-    for (int o = tid; o < W; o += kPlaceThreads) {
-      uint32_t a, b, tt;
-      type_operands(n, l, o, a, b, tt);
-      info[o] = (uint16_t)((a & 31u) | ((b & 31u) << 5) | (tt << 10));
-      atomicAdd(&hist[tt], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int U = 0, rows = (W + kNetThreads - 1) / kNetThreads;
-      int mm[16];
-      for (int T = 0; T < 16; ++T) mm[T] = 0;
-      for (int u = maxo - 1; u >= 1; --u) {
-        const int cap = 64 * u;
-        for (int T = 0; T < 16; ++T) mm[T] = 0;
-        for (int waves = 0; waves < 16; ++waves) {
-          int bt = -1, br = 0;
-          for (int T = 0; T < 16; ++T) {
-            const int rem = hist[T] - mm[T] * cap;
-            if (rem > br) { br = rem; bt = T; }
-          }
-          if (bt < 0) break;
-          mm[bt] += 1;
-        }
-        int over = 0;
-        for (int T = 0; T < 16; ++T) over += max(0, hist[T] - mm[T] * cap);
-        const int rg = (over + kNetThreads - 1) / kNetThreads;
-        if (u + rg <= maxo) { U = u; rows = u + rg; break; }
-      }
-      if (U == 0)
-        for (int T = 0; T < 16; ++T) mm[T] = 0;
-      int w = 0;
-      for (int T = 0; T < 16; ++T) {
-        m[T] = mm[T];
-        w0[T] = w;
-        for (int i = 0; i < mm[T]; ++i) wtt[w++] = T;
-      }
-      for (; w < 16; ++w) wtt[w] = 0;
-      plan_u = U;
-      plan_rows = rows;
-      int32_t* pl = n.plan + l * kPlanStride;
-      pl[0] = U;
-      pl[1] = rows;
-      for (int i = 0; i < 16; ++i) pl[2 + i] = wtt[i];
-      pl[18] = n.maxo;
-      pl[19] = n.in0;
-    }
-    __syncthreads();
-    const int U = plan_u;
-    // ranks within each type (wave T scans type T in index order, one ballot
-    // prefix per 64 outputs); what lies past the type's waves goes generic
-    {
-      const int T = wave, cap = 64 * U * m[T];
-      int base = 0;
-      for (int o0 = 0; o0 < W; o0 += 64) {
-        const int o = o0 + lane;
-        const bool mine = o < W && (info[o] >> 10) == (uint32_t)T;
-        const uint64_t mk = __ballot(mine);
-        const int r = base + (int)__popcll(mk & ((1ull << lane) - 1ull));
-        if (mine) {
-          rank_of[o] = (uint16_t)r;
-          if (r >= cap) slot_of[o] = 0xFFFFu;
-        }
-        base += (int)__popcll(mk);
-      }
-    }
-    __syncthreads();
-    // type bins: wave w, the k-th wave of its type, places that type's ranks
-    // [64 U k, 64 U (k + 1)) into its own 2 U groups
-    {
-      const int T = wtt[wave], k = wave - w0[T];
-      if (U > 0 && m[T] > 0 && k >= 0 && k < m[T]) {
-        const int lo = 64 * U * k, hi = lo + 64 * U, G = 2 * U;
-        const bool na = tt_needs_a(T), nb = tt_needs_b(T);
-        RegBin rb;
-        for (int o0 = 0; o0 < W; o0 += 64) {
-          const int o = o0 + lane;
-          const uint32_t in = o < W ? info[o] : 0xFFFFu;
-          const int r = o < W ? (int)rank_of[o] : -1;
-          const uint64_t mk0 = __ballot((in >> 10) == (uint32_t)T && r >= lo && r < hi);
-          uint64_t mk = mk0;
-          while (mk) {
-            const int src = __ffsll((long long)mk) - 1;
-            mk &= mk - 1;
-            const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
-            const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
-            const int sl = rb.place(false, G, U, wave, na, nb, ca, cb, lane);
-            if (lane == 0) slot_of[o0 + src] = (uint16_t)sl;
-          }
-        }
-        if (lane < G) fill[bin_group(false, lane, U, wave)] = rb.fill;
-      }
-    }
-    __syncthreads();
-    // generic bin: what the type bins left, in index order. Up to 256
-    // groups it is split over four waves: wave j takes the outputs of
-    // generic rank j, j + 4, ... into groups j, j + 4, ...; larger bins are
-    // placed by wave 0 alone.
-    {
-      const int G = 32 * (plan_rows - U);
-      const int NS = G <= 256 ? 4 : 1;
-      if (wave < NS) {
-        const int Gs = G / NS;
-        const bool regs = Gs <= 64;
-        RegBin rb;
-        int base = 0;
-        for (int o0 = 0; o0 < W; o0 += 64) {
-          const int o = o0 + lane;
-          // generic: ranked past its type's waves (a test on data no wave
-          // writes here, so all four waves see the same ranks)
-          const bool left = o < W && (int)rank_of[o] >= 64 * U * m[info[o] >> 10];
-          const uint64_t ml = __ballot(left);
-          const int r = base + (int)__popcll(ml & ((1ull << lane) - 1ull));
-          base += (int)__popcll(ml);
-          const uint32_t in = left ? info[o] : 0u;
-          uint64_t mk = __ballot(left && r % NS == wave);
-          while (mk) {
-            const int src = __ffsll((long long)mk) - 1;
-            mk &= mk - 1;
-            const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
-            const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
-            const int sl = regs ? rb.place(true, Gs, U, 0, true, true, ca, cb, lane, NS, wave)
-                                : place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
-            if (lane == 0) slot_of[o0 + src] = (uint16_t)sl;
-          }
-        }
-        if (regs && lane < Gs) fill[U * 32 + lane * NS + wave] = rb.fill;
-      }
-    }
-    __syncthreads();
-    // codes, slots and unused slots (codes stored thread-major)
-    const uint32_t base = (uint32_t)((l & 1) * S);
-    for (int o = tid; o < W; o += kPlaceThreads) {
-      uint32_t a, b, tt;
-      type_operands(n, l, o, a, b, tt);
-      const int s = slot_of[o];
-      n.perm[l][o] = s;
-      n.out[l][tm_index(s, maxo)] =
-          (s >> 10) < U ? ((a + base) << 16) | (b + base) : (b | (a << 14) | (tt << 28));
-    }
-    for (int s = tid; s < S; s += kPlaceThreads) {
-      if ((s & 31) >= fill[s >> 5])
-        n.out[l][tm_index(s, maxo)] = (s >> 10) < U ? (base << 16) | base : 0u;
-    }
-    __syncthreads();
-    __threadfence_block();
+  const int maxo = n.maxo, W = n.W[l];
+  if (tid < 16) hist[tid] = 0;
+  for (int i = tid; i < kTypeMaxGroups; i += kPlaceThreads) ws.fill[i] = 0;
+  __syncthreads();
+  for (int o = tid; o < W; o += kPlaceThreads) {
+    uint32_t a, b, tt;
+    type_operands(n, l, o, a, b, tt);
+    const uint32_t v = (a & 31u) | ((b & 31u) << 5) | (tt << 10);
+    info[o] = (uint16_t)v;
+    ws.info[o] = v;
+    atomicAdd(&hist[tt], 1);
   }
-  // last layer: its own order, compact codes, operands renamed
+  __syncthreads();
+  if (tid == 0) {
+    int U = 0, rows = (W + kNetThreads - 1) / kNetThreads;
+    int mm[16];
+    for (int T = 0; T < 16; ++T) mm[T] = 0;
+    for (int u = maxo - 1; u >= 1; --u) {
+      const int cap = 64 * u;
+      for (int T = 0; T < 16; ++T) mm[T] = 0;
+      for (int waves = 0; waves < 16; ++waves) {
+        int bt = -1, br = 0;
+        for (int T = 0; T < 16; ++T) {
+          const int rem = hist[T] - mm[T] * cap;
+          if (rem > br) { br = rem; bt = T; }
+        }
+        if (bt < 0) break;
+        mm[bt] += 1;
+      }
+      int over = 0;
+      for (int T = 0; T < 16; ++T) over += max(0, hist[T] - mm[T] * cap);
+      const int rg = (over + kNetThreads - 1) / kNetThreads;
+      if (u + rg <= maxo) { U = u; rows = u + rg; break; }
+    }
+    if (U == 0)
+      for (int T = 0; T < 16; ++T) mm[T] = 0;
+    int w = 0, ts = 0;
+    for (int T = 0; T < 16; ++T) {
+      m[T] = mm[T];
+      w0[T] = w;
+      for (int i = 0; i < mm[T]; ++i) wtt[w++] = T;
+      tstart[T] = ts;
+      ts += min(hist[T], 64 * U * mm[T]);
+    }
+    for (; w < 16; ++w) wtt[w] = 0;
+    plan_u = U;
+    int32_t* pl = n.plan + l * kPlanStride;
+    pl[0] = U;
+    pl[1] = rows;
+    for (int i = 0; i < 16; ++i) pl[2 + i] = wtt[i];
+    pl[18] = n.maxo;
+    pl[19] = n.in0;
+    ws.meta[kMetaU] = U;
+    ws.meta[kMetaRows] = rows;
+    for (int i = 0; i < 16; ++i) {
+      ws.meta[kMetaM + i] = m[i];
+      ws.meta[kMetaW0 + i] = w0[i];
+      ws.meta[kMetaWtt + i] = wtt[i];
+      ws.meta[kMetaTStart + i] = tstart[i];
+      ws.meta[kMetaTCount + i] = min(hist[i], 64 * U * m[i]);
+    }
+  }
+  __syncthreads();
+  const int U = plan_u;
+  // ranks within each type (wave T scans type T in index order, one ballot
+  // prefix per 64 outputs): ranks below the type's waves' capacity go to
+  // the type's list in rank order, the rest are generic
+  {
+    const int T = wave, cap = 64 * U * m[T];
+    int base = 0;
+    for (int o0 = 0; o0 < W; o0 += 64) {
+      const int o = o0 + lane;
+      const bool mine = o < W && (info[o] >> 10) == (uint32_t)T;
+      const uint64_t mk = __ballot(mine);
+      const int r = base + (int)__popcll(mk & ((1ull << lane) - 1ull));
+      if (mine) {
+        if (r < cap) ws.olist[tstart[T] + r] = o;
+        generic[o] = r >= cap ? 1 : 0;
+      }
+      base += (int)__popcll(mk);
+    }
+  }
+  __syncthreads();
+  // the generic outputs in index order (wave 0)
+  if (wave == 0) {
+    int gbase = 0;
+    for (int o0 = 0; o0 < W; o0 += 64) {
+      const int o = o0 + lane;
+      const bool left = o < W && generic[o];
+      const uint64_t ml = __ballot(left);
+      if (left) ws.glist[gbase + (int)__popcll(ml & ((1ull << lane) - 1ull))] = o;
+      gbase += (int)__popcll(ml);
+    }
+    if (lane == 0) ws.meta[kMetaNGen] = gbase;
+  }
+}
+
+// The bins of layer l: workgroup w < 16 is wave w of the type-uniform rows
+// (the k-th wave of type T places that type's ranks [64 U k, 64 U (k + 1))
+// into its own 2 U groups), workgroups 16.. the generic sub-bins (up to 256
+// groups: sub-bin j takes the generic outputs of rank j, j + NS, ... into
+// groups j, j + NS, ...; larger bins: one workgroup places them all, with
+// the counts in LDS). Each places its outputs greedily in index order and
+// writes their slots and its groups' fill.
+__global__ void __launch_bounds__(64) fc_hard_type_bins_kernel(TypePlaceNet n, TypePlaceScratch ws) {
+  __shared__ uint8_t cnt[kTypeMaxGroups][64];
+  __shared__ int fill[kTypeMaxGroups];
+  const int lane = threadIdx.x;
+  const int U = ws.meta[kMetaU], rows = ws.meta[kMetaRows];
+  const int bin = blockIdx.x;
+  if (bin < 16) {
+    const int T = ws.meta[kMetaWtt + bin], k = bin - ws.meta[kMetaW0 + T];
+    const int mT = ws.meta[kMetaM + T];
+    if (U == 0 || mT == 0 || k < 0 || k >= mT) return;
+    // the type's list holds its first min(count, 64 U m) outputs by rank:
+    // this bin takes ranks [lo, hi) of them
+    const int start = ws.meta[kMetaTStart + T], count = ws.meta[kMetaTCount + T];
+    const int lo = 64 * U * k, hi = min(lo + 64 * U, count), G = 2 * U;
+    const bool na = tt_needs_a(T), nb = tt_needs_b(T);
+    RegBin rb;
+    for (int r0 = lo; r0 < hi; r0 += 64) {
+      const int r = r0 + lane;
+      const bool ok = r < hi;
+      const int o = ok ? ws.olist[start + r] : -1;
+      const uint32_t in = ok ? ws.info[o] : 0u;
+      uint64_t mk = __ballot(ok);
+      while (mk) {
+        const int src = __ffsll((long long)mk) - 1;
+        mk &= mk - 1;
+        const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
+        const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
+        const int oo = __builtin_amdgcn_readlane(o, src);
+        const int sl = rb.place(false, G, U, bin, na, nb, ca, cb, lane);
+        if (lane == 0) ws.slot[oo] = sl;
+      }
+    }
+    if (lane < G) ws.fill[bin_group(false, lane, U, bin)] = rb.fill;
+    return;
+  }
+  const int G = 32 * (rows - U);
+  const int NS = G <= 256 ? 4 : 1;
+  const int j = bin - 16;
+  if (j >= NS || G == 0) return;
+  const int Gs = G / NS;
+  const bool regs = Gs <= 64;
+  if (!regs) {
+    for (int i = lane; i < kTypeMaxGroups * 16; i += 64)
+      reinterpret_cast<uint32_t*>(&cnt[0][0])[i] = 0u;
+    for (int i = lane; i < kTypeMaxGroups; i += 64) fill[i] = 0;
+    __syncthreads();
+  }
+  const int ng = ws.meta[kMetaNGen];
+  RegBin rb;
+  for (int r0 = 0; r0 < ng; r0 += 64) {
+    const int r = r0 + lane;
+    const bool ok = r < ng && r % NS == j;
+    const int o = ok ? ws.glist[r] : -1;
+    const uint32_t in = ok ? ws.info[o] : 0u;
+    uint64_t mk = __ballot(ok);
+    while (mk) {
+      const int src = __ffsll((long long)mk) - 1;
+      mk &= mk - 1;
+      const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
+      const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
+      const int oo = __builtin_amdgcn_readlane(o, src);
+      const int sl = regs ? rb.place(true, Gs, U, 0, true, true, ca, cb, lane, NS, j)
+                          : place_greedy(cnt, fill, true, G, U, 0, true, true, ca, cb, lane);
+      if (lane == 0) ws.slot[oo] = sl;
+    }
+  }
+  if (regs) {
+    if (lane < Gs) ws.fill[U * 32 + lane * NS + j] = rb.fill;
+  } else {
+    __syncthreads();
+    for (int g = lane; g < G; g += 64) ws.fill[U * 32 + g] = fill[U * 32 + g];
+  }
+}
+
+// Codes of layer l (every output) and its unused slots (every slot), and
+// the renaming table the next layer reads.
+__global__ void __launch_bounds__(256) fc_hard_type_codes_kernel(TypePlaceNet n, TypePlaceScratch ws,
+                                                                 int l) {
+  const int U = ws.meta[kMetaU];
+  const int maxo = n.maxo, S = maxo * kNetThreads, W = n.W[l];
+  const uint32_t base = (uint32_t)((l & 1) * S);
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < W) {
+    uint32_t a, b, tt;
+    type_operands(n, l, i, a, b, tt);
+    const int s = ws.slot[i];
+    n.perm[l][i] = s;
+    n.out[l][tm_index(s, maxo)] =
+        (s >> 10) < U ? ((a + base) << 16) | (b + base) : (b | (a << 14) | (tt << 28));
+  }
+  if (i < S) {
+    // groups no bin filled were cleared by the plan kernel
+    if ((i & 31) >= ws.fill[i >> 5])
+      n.out[l][tm_index(i, maxo)] = (i >> 10) < U ? (base << 16) | base : 0u;
+  }
+}
+
+// The last layer: its own order, compact codes, operands renamed (slots
+// past its width: code 0), and its plan row.
+__global__ void __launch_bounds__(256) fc_hard_type_last_kernel(TypePlaceNet n) {
   const int l = n.L - 1;
-  for (int s = tid; s < S; s += kPlaceThreads) {
+  const int maxo = n.maxo, S = maxo * kNetThreads;
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s < S) {
     uint32_t a = 0, b = 0, tt = 0;
     if (s < n.W[l]) type_operands(n, l, s, a, b, tt);
     n.out[l][tm_index(s, maxo)] = b | (a << 14) | (tt << 28);
   }
-  if (tid == 0) {
+  if (s == 0) {
     int32_t* pl = n.plan + l * kPlanStride;
     pl[0] = 0;
     pl[1] = (n.W[l] + kNetThreads - 1) / kNetThreads;
@@ -1908,7 +1981,7 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
                                const uint32_t* const* codes, uint32_t* const* placed,
                                int32_t* plan, int32_t* perm_ws, int64_t perm_ws_len,
                                slg_stream_t stream) {
-  SLG_REQUIRE(widths && codes && placed && plan && (perm_ws || n_layers == 1), SLG_E_ARG,
+  SLG_REQUIRE(widths && codes && placed && plan && perm_ws, SLG_E_ARG,
               "fc_hard_type_place_net: null pointer");
   SLG_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, SLG_E_SHAPE,
               "fc_hard_type_place_net: %d layers", n_layers);
@@ -1933,12 +2006,33 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
       used += widths[l];
     }
   }
-  SLG_REQUIRE(used <= perm_ws_len, SLG_E_ARG,
+  // the placement's scratch follows the renaming tables
+  const int64_t need = slg_fc_hard_type_place_workspace(n_layers, widths);
+  SLG_REQUIRE(need > 0 && need <= perm_ws_len && perm_ws, SLG_E_ARG,
               "fc_hard_type_place_net: workspace of %lld ints, %lld needed",
-              (long long)perm_ws_len, (long long)used);
-  hipLaunchKernelGGL(fc_hard_type_place_kernel, dim3(1), dim3(kPlaceThreads), 0, as_stream(stream), n);
+              (long long)perm_ws_len, (long long)need);
+  int32_t* sc = perm_ws + used;
+  TypePlaceScratch ws{reinterpret_cast<uint32_t*>(sc), sc + kPlaceMax, sc + 2 * kPlaceMax,
+                      sc + 3 * kPlaceMax, sc + 4 * kPlaceMax,
+                      sc + 4 * kPlaceMax + kTypeMaxGroups};
+  hipStream_t st = as_stream(stream);
+  const int S_i = (int)S;
+  for (int l = 0; l + 1 < n_layers; ++l) {
+    hipLaunchKernelGGL(fc_hard_type_plan_kernel, dim3(1), dim3(kPlaceThreads), 0, st, n, ws, l);
+    hipLaunchKernelGGL(fc_hard_type_bins_kernel, dim3(16 + 4), dim3(64), 0, st, n, ws);
+    hipLaunchKernelGGL(fc_hard_type_codes_kernel, dim3((unsigned)cdiv(std::max(S_i, n.W[l]), 256)),
+                       dim3(256), 0, st, n, ws, l);
+  }
+  hipLaunchKernelGGL(fc_hard_type_last_kernel, dim3((unsigned)cdiv(S_i, 256)), dim3(256), 0, st, n);
   SLG_LAUNCH_CHECK("fc_hard_type_place");
   return 0;
+}
+
+int64_t slg_fc_hard_type_place_workspace(int32_t n_layers, const int64_t* widths) {
+  if (!widths || n_layers < 1 || n_layers > kMaxLayers) return -1;
+  int64_t perm = 0;
+  for (int l = 0; l + 1 < n_layers; ++l) perm += widths[l];
+  return perm + kTypeScratchInts;
 }
 
 int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int32_t n_layers,

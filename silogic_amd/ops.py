@@ -651,9 +651,10 @@ def fc_hard_type_place_net(codes, in_dim):
     dev = codes[0].device
     placed = [torch.empty((S,), device=dev, dtype=torch.int32) for _ in widths]
     plan = torch.empty((L, 20), device=dev, dtype=torch.int32)
-    n_ws = max(1, sum(widths[:-1]))
+    w_arr = (ctypes.c_int64 * L)(*widths)
+    n_ws = _lib.lib().slg_fc_hard_type_place_workspace(L, w_arr)
     ws = torch.empty(n_ws, device=dev, dtype=torch.int32)
-    _lib.call("slg_fc_hard_type_place_net", L, in_dim, (ctypes.c_int64 * L)(*widths),
+    _lib.call("slg_fc_hard_type_place_net", L, in_dim, w_arr,
               _ptrs(codes), _ptrs(placed), _p(plan), _p(ws), n_ws, _stream(codes[0]))
     return NetCodes(placed, plan=plan, in_dim=in_dim, widths=widths)
 
