@@ -36,7 +36,8 @@ output.
 The default run measures all five BASELINE configs the same way and adds
 them under ``configs`` (the headline keys stay config 2's). ``--config N``
 measures config N alone; ``--kernels-only`` runs every launch three times
-for counter passes.
+for counter passes; ``--param-change`` times ``forward_hard``'s first call
+after a parameter change (the one-time re-derivation of its tables).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N] [--no-cpu]
 """
@@ -185,6 +186,57 @@ def kernels_only(reps=3):
         torch.cuda.empty_cache()
     print(json.dumps({"kernels_only_groups": groups, "reps": reps}), flush=True)
     log("kernels-only done")
+
+
+def param_change(cfg, reps=5):
+    """The one-time cost of ``forward_hard`` after a parameter change on
+    config ``cfg``: after a settle phase of steady calls, ``reps`` times an
+    in-place update of the first layer's first parameter (the new
+    parameter version makes every derived table stale: hard codes, the
+    type-uniform placement, launch plans) followed by one timed call, then
+    the steady call time. Prints one JSON line (wall and HIP-event times)."""
+    import silogic_amd as sl
+    from silogic_amd.synthetic import BATCHES, build_config, config_inputs
+    dev = torch.device("cuda:0")
+    model = build_config(cfg, sl).eval().to(dev)
+    B_hard = BATCHES[cfg][1]
+    x = config_inputs(cfg, B_hard).to(dev)
+    first = model.layers[0] if hasattr(model, "layers") else model._convs()[0]
+    param = next(first.parameters())     # the connection logits
+
+    def call():
+        with torch.no_grad():
+            model.forward_hard(x)
+
+    settle(call, 200.0)
+
+    def timed(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3, e0.elapsed_time(e1)
+
+    after = []
+    for _ in range(reps):
+        with torch.no_grad():
+            param.add_(0.0)            # a new version of the same values
+        after.append(timed(call))
+        for _ in range(3):
+            call()
+    steady = [timed(call) for _ in range(20)]
+    wall = sorted(a[0] for a in after)[len(after) // 2]
+    gpu = sorted(a[1] for a in after)[len(after) // 2]
+    swall = sorted(a[0] for a in steady)[len(steady) // 2]
+    sgpu = sorted(a[1] for a in steady)[len(steady) // 2]
+    print(json.dumps({
+        "config": cfg, "what": "forward_hard after a parameter change (median of %d)" % reps,
+        "after_change_wall_ms": round(wall, 3), "after_change_gpu_ms": round(gpu, 3),
+        "steady_wall_ms": round(swall, 3), "steady_gpu_ms": round(sgpu, 3),
+        "overhead_wall_ms": round(wall - swall, 3)}), flush=True)
 
 
 def train_step(cfg, steps, warmup):
@@ -671,11 +723,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the copy calibration and the dominant kernels (for --pmc)")
+    ap.add_argument("--param-change", action="store_true",
+                    help="time forward_hard's first call after a parameter change instead")
     ap.add_argument("--train-step", action="store_true",
                     help="time a training step (soft forward + backward + Adam) instead")
     args = ap.parse_args()
     if args.kernels_only:
         kernels_only()
+        return
+    if args.param_change:
+        param_change(args.config or 2)
         return
     if args.train_step:
         train_step(args.config or 2, args.steps, args.warmup)
