@@ -135,12 +135,15 @@ __device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM, NW>& P, in
 #pragma unroll
     for (int i = 0; i < NP; ++i) P.par[i] = np[(int64_t)nv * NP + i];
   } else {
-    constexpr int H2 = 1 << (NLEAF - 1);
+    constexpr int LG = ConvNode<NODE, NLEAF>::LG;
 #pragma unroll
-    for (int m = 0; m < H2; ++m) {
-      const float e = np[(int64_t)nv * NP + 2 * m], o = np[(int64_t)nv * NP + 2 * m + 1];
-      P.par[m] = e;
-      P.par[H2 + m] = o - e;
+    for (int g = 0; g < (NP >> LG); ++g) {
+      float c[1 << LG];
+#pragma unroll
+      for (int i = 0; i < (1 << LG); ++i) c[i] = np[(int64_t)nv * NP + (g << LG) + i];
+      lut_group_coeffs<LG>(c);
+#pragma unroll
+      for (int i = 0; i < (1 << LG); ++i) P.par[(g << LG) + i] = c[i];
     }
   }
 }
@@ -765,12 +768,28 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
     const int P = 1 << arity, q = slot - LK * (NW + 1);
     if (q < P) v = sigmoidc(raw[(int64_t)n * P + q]);
   } else {
-    const int H2 = 1 << (arity - 1), q = slot - LK * (NW + 1);
-    const float* s_ = raw + (int64_t)n * 2 * H2;
-    if (q < H2) {
-      v = sigmoidc(s_[2 * q]);
-    } else if (q < 2 * H2) {
-      v = sigmoidc(s_[2 * (q - H2) + 1]) - sigmoidc(s_[2 * (q - H2)]);
+    // the kept form of conv_tree.h: per group of corners, its polynomial's
+    // coefficients (lut_group_coeffs over the group's sigmoid values)
+    const int P = 1 << arity, q = slot - LK * (NW + 1);
+    const float* s_ = raw + (int64_t)n * P;
+    if (q < P) {
+      if (arity >= 3) {
+        float c[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = sigmoidc(s_[(q & ~7) + i]);
+        lut_group_coeffs<3>(c);
+        v = c[q & 7];
+      } else if (arity == 2) {
+        float c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c[i] = sigmoidc(s_[i]);
+        lut_group_coeffs<2>(c);
+        v = c[q & 3];
+      } else {
+        float c[2] = {sigmoidc(s_[0]), sigmoidc(s_[1])};
+        lut_group_coeffs<1>(c);
+        v = c[q & 1];
+      }
     }
   }
   rec[t] = v;

@@ -248,9 +248,17 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
       if constexpr (NODE == SLG_NODE_HYBRID) {
         par[i] = v;  // the values as they are (the forward's lookup)
       } else {
-        // kept form: even corners, then odd - even (as the forward keeps them)
-        if ((q & 1) == 0) par[t * NPR + q / 2] = v;
-        else par[t * NPR + H2 + q / 2] = v - np[(int64_t)n * NP + q - 1];
+        // kept form: per group of corners its polynomial's coefficients
+        // (lut_group_coeffs, as the forward keeps them)
+        constexpr int LG = Nd::LG, GM = (1 << LG) - 1;
+        float c[1 << LG];
+#pragma unroll
+        for (int u = 0; u <= GM; ++u) c[u] = np[(int64_t)n * NP + (q & ~GM) + u];
+        lut_group_coeffs<LG>(c);
+        float cq = c[0];
+#pragma unroll
+        for (int u = 1; u <= GM; ++u) cq = (q & GM) == u ? c[u] : cq;
+        par[t * NPR + q] = cq;
       }
       // leaf differences D[j][qq] = s[p | bit j] - s[p] at the p with bit j set
 #pragma unroll

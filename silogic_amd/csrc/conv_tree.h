@@ -15,11 +15,30 @@ template <int NODE, int NLEAF>
 struct ConvNode {
   static constexpr int NN = (NODE == SLG_NODE_GATE16) ? NLEAF - 1 : 1;  // tree nodes
   // parameters kept per channel: gate16 coefficients [NN][4]; for the
-  // multilinear LUT the even corner values s[2m] and the differences
-  // s[2m+1] - s[2m]; for the hybrid LUT the values s[p] as they are
+  // multilinear LUT, per group of 2^LG corners (LG = min(NLEAF, 3): the
+  // corners that differ in leaves 0..LG-1) the group's polynomial
+  // coefficients (lut_group_coeffs); for the hybrid LUT the values s[p] as
+  // they are
   static constexpr int NPR = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);
+  static constexpr int LG = NLEAF < 3 ? NLEAF : 3;
   static constexpr int NP = (NODE == SLG_NODE_GATE16) ? 4 * NN : (1 << NLEAF);  // raw params
 };
+
+// The multilinear LUT's kept form: the corners of a group (index i over
+// leaves 0..G-1) as the coefficients of the group's multilinear polynomial
+// in those leaves, c[i] = sum over subsets j of i of (-1)^|i-j| s[j] (the
+// subset-difference transform, one bit at a time in this fixed order, so
+// every kernel that keeps them gets the same bits). The interpolation over
+// the group's leaves is then 2^G - 1 FMAs (conv_tree_eval) where the lerp
+// tree takes 2^(G-1) FMAs and 2^(G-1) - 1 subtract-FMA pairs.
+template <int G>
+__device__ inline void lut_group_coeffs(float (&c)[1 << G]) {
+#pragma unroll
+  for (int b = 0; b < G; ++b)
+#pragma unroll
+    for (int i = 0; i < (1 << G); ++i)
+      if ((i >> b) & 1) c[i] = c[i] - c[i ^ (1 << b)];
+}
 
 // Tree value at leaf values v with kept parameters par (ConvNode::NPR).
 template <int NODE, int NLEAF>
@@ -49,13 +68,26 @@ __device__ inline float conv_tree_eval(const float (&v)[NLEAF], const float* par
     return par[addr];
   } else {
     // multilinear interpolation of s over the leaves (corner bit j = leaf
-    // j), silogic/nodes.py:174-178, as a lerp tree
-    constexpr int H2 = 1 << (NLEAF - 1);
-    float t[H2];
+    // j), silogic/nodes.py:174-178: each group's polynomial in leaves
+    // 0..LG-1 nested in Horner form, then a lerp tree over the rest
+    constexpr int LG = ConvNode<NODE, NLEAF>::LG;
+    constexpr int NG = 1 << (NLEAF - LG);
+    float t[NG];
 #pragma unroll
-    for (int m = 0; m < H2; ++m) t[m] = fmaf(v[0], par[H2 + m], par[m]);
+    for (int g = 0; g < NG; ++g) {
+      const float* c = par + (g << LG);
+      if constexpr (LG == 3) {
+        const float p = fmaf(v[1], fmaf(v[0], c[3], c[2]), fmaf(v[0], c[1], c[0]));
+        const float q = fmaf(v[1], fmaf(v[0], c[7], c[6]), fmaf(v[0], c[5], c[4]));
+        t[g] = fmaf(v[2], q, p);
+      } else if constexpr (LG == 2) {
+        t[g] = fmaf(v[1], fmaf(v[0], c[3], c[2]), fmaf(v[0], c[1], c[0]));
+      } else {
+        t[g] = fmaf(v[0], c[1], c[0]);
+      }
+    }
 #pragma unroll
-    for (int j = 1; j < NLEAF; ++j) {
+    for (int j = LG; j < NLEAF; ++j) {
 #pragma unroll
       for (int m = 0; m < (1 << (NLEAF - 1 - j)); ++m)
         t[m] = fmaf(v[j], t[2 * m + 1] - t[2 * m], t[2 * m]);
