@@ -41,6 +41,7 @@
 
 namespace slg {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline float sigmoidc(float z) { return 1.0f / (1.0f + expf(-z)); }
@@ -77,7 +78,9 @@ struct ConvGeom {
   int plane;  // channel stride
   int SST;    // sample stride
   int LPS;    // lanes per sample
-  int BH, BW; // quad: blocks per copy (rows, columns); 0 otherwise
+  int BH, BW; // quad: blocks per copy (rows, columns); pair: half-rows and
+              // pairs per row of a copy; 0 otherwise
+  int PAIR;   // 1: the pair layout
 };
 
 // One output channel's parameters in registers: LDS tap offsets, leaf
@@ -93,6 +96,12 @@ struct ConvParams {
 // phase-split) or the tap itself (NW = 1, row-major).
 __host__ __device__ inline int conv_tap_offset(const ConvGeom& g, int NW, int c, int h, int w,
                                                int q) {
+  if (g.PAIR) {  // pair: the tap's pair in rows h (q = 0) and h + 1 (q = 1), in pair units
+    const int Y = h + q;
+    return q < 2 ? c * (g.plane / 2) + (w & 1) * 2 * g.BH * g.BW + (Y & 1) * g.BH * g.BW +
+                       (Y >> 1) * g.BW + (w >> 1)
+                 : 0;
+  }
   if (g.BH > 0)  // quad: the tap's block in float4 units, in slot q = 0
     return q == 0 ? (c * g.plane) / 4 + ((h & 1) * 2 + (w & 1)) * g.BH * g.BW +
                         (h >> 1) * g.BW + (w >> 1)
@@ -154,10 +163,14 @@ __device__ inline void conv_params_arrays(ConvParams<NODE, NLEAF, KM, NW>& P, in
 template <int NODE, int NLEAF, int KM, int NW, int R>
 __device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM, NW>& P, const float* rec,
                                           int nv) {
-  float v[R];
+  // the floats in use: records of phase-eligible trees keep room for four
+  // offsets per tap, the pair layout fills two
+  constexpr int USED = (NLEAF * KM * (NW + 1) + ConvNode<NODE, NLEAF>::NPR + 3) & ~3;
+  static_assert(USED <= R, "the record holds the parameters");
+  float v[USED];
   const float4* r4 = reinterpret_cast<const float4*>(rec + (int64_t)nv * R);
 #pragma unroll
-  for (int q = 0; q < R / 4; ++q) {
+  for (int q = 0; q < USED / 4; ++q) {
     const float4 t = r4[q];
     v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
   }
@@ -584,6 +597,151 @@ conv_soft_quad_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
   }
 }
 
+// Pair layout (pooled, phase-eligible taps, images whose four quad copies
+// do not fit one workgroup's LDS but two copies do): copy sx in {0, 1} of
+// the padded image holds, by row parity ry and half-row iy, BW pairs of
+// floats per row, pair j being padded pixels (2iy+ry, 2j+sx) and
+// (2iy+ry, 2j+sx+1). The 2x2 window of pooled output (py, px) under tap
+// (h, w) is pair px + w/2 of copy w&1 in rows 2py+h and 2py+h+1: two
+// ds_read_b64 at two per-tap offsets (pair units) from the lane's pair
+// q = py*BW + px. Lanes walk (py, px < BW), one channel per chunk, so the
+// 32 lanes of a b64 conflict group read 32 consecutive pairs of one row
+// parity. Persistent like conv_soft_quad_kernel (one staged sample per
+// workgroup, the next one's C*H*W floats in registers); a wave takes one
+// channel at a time with its parameters in scalar registers (uniform loads
+// through the scalar cache), so that a channel's parameters cost no vector
+// memory or LDS traffic per sample. The arithmetic per output is
+// conv_soft_kernel's, in the same order.
+constexpr int kPairRegs = 13;
+constexpr int kPairMaxChunks = 2;
+
+template <int NODE, int NLEAF, int KM, bool REC>
+__global__ void __launch_bounds__(kQuadThreads)
+conv_soft_pair_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K,
+                      int kernel, int pad, ConvGeom g, const float* __restrict__ np,
+                      const float* __restrict__ wts, const int* __restrict__ cm,
+                      const int* __restrict__ ch, const int* __restrict__ cw,
+                      const float* __restrict__ rec, float* __restrict__ out, int Ho, int Wo) {
+  using Cfg = ConvCfg<NODE, NLEAF, KM, true>;
+  static_assert(Cfg::PHASE, "the pair layout keeps the phase records");
+  constexpr int NW = 2;
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int T = blockDim.x;
+  const int HW = H * W, total = C * HW;
+  const int P = Ho * Wo;
+  const int BH = g.BH, BW = g.BW;
+  const int HALF = 2 * BH * BW;  // floats of one row-parity plane of a copy
+
+  for (int i = threadIdx.x; i < (g.SST + kConvExtra) / 4; i += T)
+    reinterpret_cast<f32x4*>(lds)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // this thread's elements e = tid + u*T of a sample
+  float pf[kPairRegs];
+  auto issue = [&](int b) {
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + (int64_t)b * total), (short)0, total * 4, kBufferWord3);
+#pragma unroll
+    for (int u = 0; u < kPairRegs; ++u)  // offsets past the image read 0
+      pf[u] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(src, (threadIdx.x + u * T) * 4, 0, 0));
+  };
+  const int dump = g.SST + lane;
+  auto scatter = [&] {
+    const int tx = T % W, ty = (T / W) % H, tc = T / HW;
+    int px = threadIdx.x % W, py = (threadIdx.x / W) % H, pc = threadIdx.x / HW;
+#pragma unroll
+    for (int u = 0; u < kPairRegs; ++u) {
+      const int Y = py + pad, X = px + pad;
+      const bool keep = pc < C && (Y >> 1) < BH;
+      const int rb = __umul24(pc, g.plane) + (Y & 1) * HALF + __umul24(Y >> 1, 2 * BW);
+#pragma unroll
+      for (int sx = 0; sx < 2; ++sx) {
+        const int Xs = X - sx;
+        const bool in = keep && Xs >= 0 && (Xs >> 1) < BW;
+        lds[in ? rb + sx * 2 * HALF + Xs : dump] = pf[u];  // pair Xs/2, element Xs&1
+      }
+      px += tx;
+      const int cy = px >= W;
+      px -= cy ? W : 0;
+      py += ty + cy;
+      const int cc = py >= H;
+      py -= cc ? H : 0;
+      pc += tc + cc;
+    }
+  };
+
+  // the lane's pair, output index and activity per chunk (the same for every
+  // channel and sample); lanes past the sample's LPS read the pair of the
+  // lane 32 below, which keeps a conflict group's pairs distinct
+  int qp[kPairMaxChunks], pidx[kPairMaxChunks];
+  bool act[kPairMaxChunks];
+  const int nchunks = (g.LPS + 63) / 64;
+#pragma unroll
+  for (int c = 0; c < kPairMaxChunks; ++c) {
+    const int q = c * 64 + lane;
+    const int py = q / BW, px = q - py * BW;
+    act[c] = q < g.LPS && px < Wo;
+    pidx[c] = py * Wo + px;
+    qp[c] = q < g.LPS ? q : max(0, min(q - 32, g.LPS - 1));
+  }
+
+  auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int n) {
+    if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, n);
+    else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, n, K, C, kernel, g, np, wts, cm, ch, cw);
+  };
+  const bool one_group = N <= nwaves;
+  ConvParams<NODE, NLEAF, KM, NW> Pc;
+  if (one_group && wave < N) load(Pc, wave);
+
+  if (blockIdx.x < (unsigned)B) issue(blockIdx.x);
+  __syncthreads();  // cleared before the first scatter
+  for (int b = blockIdx.x; b < B; b += gridDim.x) {
+    scatter();
+    __syncthreads();
+    if (b + (int)gridDim.x < B) issue(b + gridDim.x);
+    for (int n = wave; n < N; n += nwaves) {
+      if (!one_group) load(Pc, n);
+      float* out_n = out + ((int64_t)b * N + n) * P;
+#pragma unroll
+      for (int c = 0; c < kPairMaxChunks; ++c) {
+        if (c >= nchunks) break;
+        const f32x2* base = reinterpret_cast<const f32x2*>(lds) + qp[c];
+        float v[4][NLEAF];
+#pragma unroll
+        for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) v[qq][l] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (k < K) {
+            f32x2 t0[NLEAF], t1[NLEAF];
+#pragma unroll
+            for (int l = 0; l < NLEAF; ++l) {
+              t0[l] = base[Pc.off[l][k][0]];
+              t1[l] = base[Pc.off[l][k][1]];
+            }
+#pragma unroll
+            for (int l = 0; l < NLEAF; ++l) {
+              v[0][l] = fmaf(Pc.wt[l][k], t0[l][0], v[0][l]);
+              v[1][l] = fmaf(Pc.wt[l][k], t0[l][1], v[1][l]);
+              v[2][l] = fmaf(Pc.wt[l][k], t1[l][0], v[2][l]);
+              v[3][l] = fmaf(Pc.wt[l][k], t1[l][1], v[3][l]);
+            }
+          }
+        }
+        float best = -INFINITY;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) best = fmaxf(best, conv_tree_eval<NODE, NLEAF>(v[qq], Pc.par));
+        if (act[c]) out_n[pidx[c]] = best;
+      }
+    }
+    __syncthreads();  // every read of this sample precedes the next scatter
+  }
+}
+
 template <int NODE, int NLEAF, bool POOL>
 __global__ void __launch_bounds__(256)
 conv_hard_kernel(const uint64_t* __restrict__ xp, int C, int H, int W, int nw, int N,
@@ -914,6 +1072,35 @@ static bool conv_use_quad(bool pool, int nleaf, int km, int64_t C, int64_t Ho, i
   return (int64_t)g.SST * 4 + kConvExtra * 4 <= cap;
 }
 
+// Pair geometry (pooled; see the layouts above): BH half-rows of BW pairs per
+// row parity and copy cover every window of Ho x Wo pooled outputs.
+static ConvGeom conv_geom_pair(int64_t C, int64_t Ho, int64_t Wo, int kernel) {
+  ConvGeom g{};
+  g.BH = (int)(Ho + (kernel - 1) / 2);
+  g.BW = (int)(Wo + (kernel - 1) / 2);
+  g.plane = 8 * g.BH * g.BW;  // floats: two copies of two row parities of BH x BW pairs
+  g.LPS = (int)(Ho * g.BW);
+  g.SST = (int)(C * g.plane);
+  g.PAIR = 1;
+  return g;
+}
+
+// The pair layout is used for pooled blocks with phase-eligible taps whose
+// quad copies do not fit but whose two pair copies do, whose image rides in
+// kPairRegs registers per thread and whose pooled rows take at most
+// kPairMaxChunks chunks of 64 lanes.
+static bool conv_use_pair(bool pool, int nleaf, int km, int64_t C, int64_t H, int64_t W,
+                          int64_t Ho, int64_t Wo, int kernel) {
+  if (!conv_phase_layout(pool, nleaf, km) || Ho <= 0 || Wo <= 0) return false;
+  if (conv_use_quad(pool, nleaf, km, C, Ho, Wo, kernel)) return false;
+  if (C * H * W > (int64_t)kPairRegs * kQuadThreads) return false;
+  if (C * 8 * (Ho + kernel) * (Wo + kernel) >= (1LL << 29)) return false;
+  const ConvGeom g = conv_geom_pair(C, Ho, Wo, kernel);
+  if (g.LPS > 64 * kPairMaxChunks) return false;
+  const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+  return (int64_t)g.SST * 4 + kConvExtra * 4 <= cap;
+}
+
 // LDS geometry for images (C, H, W) with 'same' padding pad, pooled to
 // (Ho, Wo) or not (Ho = H, Wo = W).
 static ConvGeom conv_geom(int64_t C, int64_t H, int64_t W, int pad, bool pool, bool phase,
@@ -1033,6 +1220,27 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   return 0;
 }
 
+template <int NODE, int NLEAF, int KM, bool REC>
+static int launch_conv_soft_pair(const ConvSoftArgs& a, hipStream_t st) {
+  const ConvGeom g = conv_geom_pair(a.C, a.Ho, a.Wo, a.kernel);
+  const size_t lds = (size_t)(g.SST + kConvExtra) * 4;
+  auto pk = conv_soft_pair_kernel<NODE, NLEAF, KM, REC>;
+  if (lds > 65536) {
+    hipError_t e =
+        hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("conv_soft: LDS %zu: %s", lds, hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  const int64_t grid = std::min<int64_t>(a.B, device_cus());
+  hipLaunchKernelGGL(pk, dim3((unsigned)grid), dim3(kQuadThreads), lds, st, a.x, (int)a.B,
+                     (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, g, a.np, a.w,
+                     a.cm, a.ch, a.cw, a.rec, a.out, (int)a.Ho, (int)a.Wo);
+  SLG_LAUNCH_CHECK("conv_soft");
+  return 0;
+}
+
 template <int NODE, int NLEAF, bool POOL>
 static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
   // taps per leaf: 4 registers when K <= 4 (TopK k=4, fixed wiring), else 8
@@ -1041,6 +1249,9 @@ static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
       if (conv_use_quad(POOL, NLEAF, 4, a.C, a.Ho, a.Wo, a.kernel))
         return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true, true>(a, st)
                      : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false, true>(a, st);
+      if (conv_use_pair(POOL, NLEAF, 4, a.C, a.H, a.W, a.Ho, a.Wo, a.kernel))
+        return a.rec ? launch_conv_soft_pair<NODE, NLEAF, 4, true>(a, st)
+                     : launch_conv_soft_pair<NODE, NLEAF, 4, false>(a, st);
     }
     return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true, false>(a, st)
                  : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false, false>(a, st);
@@ -1049,6 +1260,9 @@ static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
     if (conv_use_quad(POOL, NLEAF, kMaxK, a.C, a.Ho, a.Wo, a.kernel))
       return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true, true>(a, st)
                    : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false, true>(a, st);
+    if (conv_use_pair(POOL, NLEAF, kMaxK, a.C, a.H, a.W, a.Ho, a.Wo, a.kernel))
+      return a.rec ? launch_conv_soft_pair<NODE, NLEAF, kMaxK, true>(a, st)
+                   : launch_conv_soft_pair<NODE, NLEAF, kMaxK, false>(a, st);
   }
   return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true, false>(a, st)
                : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false, false>(a, st);
@@ -1221,14 +1435,17 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
   SLG_REQUIRE(C * ((H + 2 * pad) * (W + 2 * pad) + 64) < (1LL << 31), SLG_E_SHAPE,
               "conv_soft_records: image too large");
   // the layout the forward will choose for these shapes (quad offsets sit in
-  // slot 0 of the phase records)
+  // slot 0 of the phase records, pair offsets in slots 0 and 1)
   const bool quad = conv_use_quad(pool != 0, nleaf, km, C, Ho, Wo, 2 * pad + 1);
+  const bool pair = conv_use_pair(pool != 0, nleaf, km, C, H, W, Ho, Wo, 2 * pad + 1);
   const ConvGeom g = quad ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
-                          : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo);
+                          : (pair ? conv_geom_pair(C, Ho, Wo, 2 * pad + 1)
+                                  : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo));
   const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K, pool);
   hipLaunchKernelGGL(conv_soft_records_kernel, dim3((unsigned)cdiv(N * R, 256)), dim3(256), 0,
                      as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km,
-                     quad ? 1 : (phase ? 4 : 1), node_kind, arity, raw, (int)C, 2 * pad + 1, g, R,
+                     quad ? 1 : (pair ? 2 : (phase ? 4 : 1)), node_kind, arity, raw, (int)C,
+                     2 * pad + 1, g, R,
                      rec);
   SLG_LAUNCH_CHECK("conv_soft_records");
   return 0;

@@ -112,7 +112,7 @@ __device__ inline void conv_tree_leaf_grad(const float (&v)[NLEAF], const float*
           const float* c = par + 4 * (nb + m);
           na[nb + m] = a;
           nb_[nb + m] = b;
-          nv[nb + m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+          nv[nb + m] = fmaf(b, fmaf(a, c[3], c[2]), fmaf(a, c[1], c[0]));
         }
         prev = nb;
         nb += cnt / 2;

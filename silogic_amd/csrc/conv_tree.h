@@ -45,7 +45,8 @@ template <int NODE, int NLEAF>
 __device__ inline float conv_tree_eval(const float (&v)[NLEAF], const float* par) {
   if constexpr (NODE == SLG_NODE_GATE16) {
     // level i combines children 2m (a) and 2m+1 (b), node ids level-major
-    // (silogic/layers.py:388-401, 408-417)
+    // (silogic/layers.py:388-401, 408-417); c0 + c1 a + c2 b + c3 ab as
+    // c0 + c1 a + b (c2 + c3 a), three FMAs
     float u[NLEAF];
 #pragma unroll
     for (int l = 0; l < NLEAF; ++l) u[l] = v[l];
@@ -56,7 +57,7 @@ __device__ inline float conv_tree_eval(const float (&v)[NLEAF], const float* par
       for (int m = 0; m < cnt / 2; ++m) {
         const float a = u[2 * m], b = u[2 * m + 1];
         const float* c = par + 4 * (nb + m);
-        u[m] = c[0] + c[1] * a + c[2] * b + c[3] * (a * b);
+        u[m] = fmaf(b, fmaf(a, c[3], c[2]), fmaf(a, c[1], c[0]));
       }
       nb += cnt / 2;
     }

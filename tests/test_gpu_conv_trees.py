@@ -122,6 +122,36 @@ def test_conv_net_with_node_trees(node):
     assert any(gr.abs().sum() > 0 for gr in grads)
 
 
+@pytest.mark.parametrize("node,arity,depth,K,C,H,N,B", [
+    ("gate16", 2, 2, 4, 64, 14, 128, 3),      # config 3 block 1: one 56-lane chunk per channel
+    ("gate16", 2, 2, 4, 40, 16, 24, 2),       # 72 lanes per channel: two chunks
+    ("gate16", 2, 2, 4, 64, 13, 20, 2),       # odd map (floor pooling)
+    ("gate16", 2, 1, 8, 64, 14, 12, 2),       # eight taps per leaf; parameters kept per wave
+    ("multilinear", 4, 1, 4, 64, 14, 10, 2),  # LUT4 trees
+    ("hybrid", 2, 1, 4, 64, 14, 10, 2),
+    ("gate16", 2, 2, 4, 64, 14, 8, 300),      # more samples than workgroups (persistent)
+])
+def test_pair_layout(node, arity, depth, K, C, H, N, B):
+    """Pooled blocks whose four quad copies exceed LDS but two column-shifted
+    copies fit (the pair layout): eval (records) and gradient-mode (separate
+    arrays) forwards against the oracle."""
+    conv = sl.ConvLogicTree(C, N, kernel=3, tree_depth=depth, connect="topk", k=K, n_chan=2,
+                            residual_init=False, seed=C + N, node=node, arity=arity, tau=0.7)
+    sd = {k: v.clone() for k, v in conv.state_dict().items()}
+    g = torch.Generator().manual_seed(C + H)
+    x = torch.rand(B, C, H, H, generator=g)
+    ref = torch_ref.orpool_soft(torch_ref.conv_soft(_blk(conv, H), sd, x))
+    conv = conv.to(DEV).eval()
+    with torch.no_grad():
+        y = conv.forward_pooled(x.to(DEV))
+    yg = conv.forward_pooled(x.to(DEV).requires_grad_(True)).detach()
+    for got, what in ((y, "records"), (yg, "arrays")):
+        if node == "hybrid":
+            assert (got.cpu() - ref).abs().max() <= 1.2e-7, what
+        else:
+            _close(got, ref, f"{node} a{arity} d{depth} K{K} {what}")
+
+
 @pytest.mark.parametrize("size", [1, 2, 3, 4])
 def test_orpool_any_size(size):
     x = torch.rand(3, 5, 11, 13, generator=torch.Generator().manual_seed(size))
