@@ -141,9 +141,9 @@ def load_traffic(cfg):
         return json.load(fh).get(f"cfg{cfg}", {})
 
 
-def kernels_only(reps=3):
+def kernels_only(reps=3, cfgs=(1, 2, 3, 4, 5)):
     """Workload for counter passes: a 256 MiB device copy (calibration), then,
-    per config at the bench's batch sizes, ``reps`` launches each of every
+    per config of ``cfgs`` at the bench's batch sizes, ``reps`` launches each of every
     launch of ``forward_hard`` (packing, conv blocks, fused networks) and of
     every stage of the soft forward the bench times. Each group of ``reps``
     launches runs after one untimed launch and between two one-byte
@@ -171,7 +171,7 @@ def kernels_only(reps=3):
     dst = torch.empty_like(src)
     group("calibration | 256 MiB copy", lambda: dst.copy_(src), 2 * src.numel() * 4, None)
     del src, dst
-    for cfg in (1, 2, 3, 4, 5):
+    for cfg in cfgs:
         model = build_config(cfg, sl).eval().to(dev)
         B_soft, B_hard = BATCHES[cfg][:2]
         x_hard = config_inputs(cfg, B_hard).to(dev)
@@ -729,7 +729,7 @@ def main():
                     help="time a training step (soft forward + backward + Adam) instead")
     args = ap.parse_args()
     if args.kernels_only:
-        kernels_only()
+        kernels_only(cfgs=(args.config,) if args.config else (1, 2, 3, 4, 5))
         return
     if args.param_change:
         param_change(args.config or 2)

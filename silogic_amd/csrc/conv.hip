@@ -742,6 +742,194 @@ conv_soft_pair_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
   }
 }
 
+// Pair layout with flat lanes: lane f of a sample's chunks takes output
+// f % P of channel f / P (P = Ho*Wo pooled outputs), so that every lane of
+// a chunk computes an output even where P is far from a multiple of 64 (a
+// one-channel chunk of the pair kernel leaves 64 - P lanes of a 7x7 map
+// idle, and a 3x3 map fills 9 of 16). Each lane reads its channel's
+// parameters from a table that the workgroup stages in LDS once, so a chunk
+// that spans channels costs LDS reads, not vector memory traffic: per
+// channel FW floats, for each tap step k the LDS byte offsets of both
+// window rows and the weight of every leaf (KS floats, read as the step
+// starts, so that only one step's worth is held in registers), then the
+// node parameters. Staging, layout and arithmetic per output are
+// conv_soft_pair_kernel's, in the same order.
+template <int NODE, int NLEAF, int KM>
+struct FlatRec {
+  static constexpr int KS = (3 * NLEAF + 3) & ~3;                    // floats per tap step
+  static constexpr int NPR4 = (ConvNode<NODE, NLEAF>::NPR + 3) & ~3;  // node parameters
+  static constexpr int FW = KM * KS + NPR4;                           // floats per channel
+};
+
+template <int NODE, int NLEAF, int KM, bool REC>
+__global__ void __launch_bounds__(kQuadThreads)
+conv_soft_flat_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K,
+                      int kernel, int pad, ConvGeom g, const float* __restrict__ np,
+                      const float* __restrict__ wts, const int* __restrict__ cm,
+                      const int* __restrict__ ch, const int* __restrict__ cw,
+                      const float* __restrict__ rec, float* __restrict__ out, int Ho, int Wo) {
+  using Cfg = ConvCfg<NODE, NLEAF, KM, true>;
+  static_assert(Cfg::PHASE, "the pair layout keeps the phase records");
+  constexpr int NW = 2;
+  constexpr int NPR = ConvNode<NODE, NLEAF>::NPR;
+  constexpr int FW = FlatRec<NODE, NLEAF, KM>::FW, KS = FlatRec<NODE, NLEAF, KM>::KS;
+  constexpr int NPR4 = FlatRec<NODE, NLEAF, KM>::NPR4;
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int T = blockDim.x;
+  const int HW = H * W, total = C * HW;
+  const int P = Ho * Wo;
+  const int BH = g.BH, BW = g.BW;
+  const int HALF = 2 * BH * BW;
+  float* table = lds + g.SST + kConvExtra;
+
+  for (int i = threadIdx.x; i < (g.SST + kConvExtra) / 4; i += T)
+    reinterpret_cast<f32x4*>(lds)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // the parameter table: per tap step, the LDS byte offsets of the two
+  // window rows and the weight of every leaf; then the node parameters
+  for (int n = threadIdx.x; n < N; n += T) {
+    ConvParams<NODE, NLEAF, KM, NW> Pr;
+    if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, n);
+    else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, n, K, C, kernel, g, np, wts, cm, ch, cw);
+    float* tr = table + n * FW;
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+#pragma unroll
+      for (int l = 0; l < NLEAF; ++l) {
+        tr[k * KS + 3 * l] = __int_as_float(Pr.off[l][k][0] * 8);
+        tr[k * KS + 3 * l + 1] = __int_as_float(Pr.off[l][k][1] * 8);
+        tr[k * KS + 3 * l + 2] = Pr.wt[l][k];
+      }
+#pragma unroll
+      for (int i = 3 * NLEAF; i < KS; ++i) tr[k * KS + i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NPR4; ++i) tr[KM * KS + i] = i < NPR ? Pr.par[i] : 0.0f;
+  }
+
+  float pf[kPairRegs];
+  auto issue = [&](int b) {
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + (int64_t)b * total), (short)0, total * 4, kBufferWord3);
+#pragma unroll
+    for (int u = 0; u < kPairRegs; ++u)  // offsets past the image read 0
+      pf[u] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(src, (threadIdx.x + u * T) * 4, 0, 0));
+  };
+  const int dump = g.SST + lane;
+  auto scatter = [&] {
+    const int tx = T % W, ty = (T / W) % H, tc = T / HW;
+    int px = threadIdx.x % W, py = (threadIdx.x / W) % H, pc = threadIdx.x / HW;
+#pragma unroll
+    for (int u = 0; u < kPairRegs; ++u) {
+      const int Y = py + pad, X = px + pad;
+      const bool keep = pc < C && (Y >> 1) < BH;
+      const int rb = __umul24(pc, g.plane) + (Y & 1) * HALF + __umul24(Y >> 1, 2 * BW);
+#pragma unroll
+      for (int sx = 0; sx < 2; ++sx) {
+        const int Xs = X - sx;
+        const bool in = keep && Xs >= 0 && (Xs >> 1) < BW;
+        lds[in ? rb + sx * 2 * HALF + Xs : dump] = pf[u];
+      }
+      px += tx;
+      const int cy = px >= W;
+      px -= cy ? W : 0;
+      py += ty + cy;
+      const int cc = py >= H;
+      py -= cc ? H : 0;
+      pc += tc + cc;
+    }
+  };
+
+  // the lane's first (channel, pooled row, column) and the step between a
+  // wave's chunks (64 * nwaves outputs), carried incrementally
+  const int NP_ = N * P;
+  const int nchunks = (NP_ + 63) / 64;
+  const int f0 = wave * 64 + lane;
+  const int n0 = f0 / P, p0 = f0 - (f0 / P) * P;
+  const int r0 = p0 / Wo, c0 = p0 - (p0 / Wo) * Wo;
+  const int dF = 64 * nwaves;
+  const int dn = dF / P, dp = dF - dn * P;
+  const int dr = dp / Wo, dc = dp - dr * Wo;
+
+  if (blockIdx.x < (unsigned)B) issue(blockIdx.x);
+  __syncthreads();  // cleared and the table written before the first scatter
+  for (int b = blockIdx.x; b < B; b += gridDim.x) {
+    scatter();
+    __syncthreads();
+    if (b + (int)gridDim.x < B) issue(b + gridDim.x);
+    float* out_b = out + (int64_t)b * NP_;
+    int n = n0, row = r0, col = c0;
+    for (int c = wave; c < nchunks; c += nwaves) {
+      const int f = c * 64 + lane;
+      const bool active = f < NP_;
+      const int nn = active ? n : N - 1;
+      const int q = active ? (int)__umul24(row, BW) + col : 0;
+      const uint32_t qb = (uint32_t)q * 8u;
+      const float* trow = table + nn * FW;  // the lane's channel in the table
+      float v[4][NLEAF];
+#pragma unroll
+      for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) v[qq][l] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        if (k < K) {
+          float st[KS];  // this step's offsets and weights
+#pragma unroll
+          for (int i = 0; i < KS / 4; ++i) {
+            const f32x4 v4 = reinterpret_cast<const f32x4*>(trow + k * KS)[i];
+            st[4 * i] = v4[0]; st[4 * i + 1] = v4[1]; st[4 * i + 2] = v4[2]; st[4 * i + 3] = v4[3];
+          }
+          f32x2 t0[NLEAF], t1[NLEAF];
+#pragma unroll
+          for (int l = 0; l < NLEAF; ++l) {
+            const uint32_t a0 = qb + (uint32_t)__float_as_int(st[3 * l]);
+            const uint32_t a1 = qb + (uint32_t)__float_as_int(st[3 * l + 1]);
+            t0[l] = *reinterpret_cast<const f32x2*>(reinterpret_cast<const char*>(lds) + a0);
+            t1[l] = *reinterpret_cast<const f32x2*>(reinterpret_cast<const char*>(lds) + a1);
+          }
+#pragma unroll
+          for (int l = 0; l < NLEAF; ++l) {
+            const float w = st[3 * l + 2];
+            v[0][l] = fmaf(w, t0[l][0], v[0][l]);
+            v[1][l] = fmaf(w, t0[l][1], v[1][l]);
+            v[2][l] = fmaf(w, t1[l][0], v[2][l]);
+            v[3][l] = fmaf(w, t1[l][1], v[3][l]);
+          }
+        }
+      }
+      // node parameters: into registers, except a hybrid LUT's, which is
+      // read at a data-dependent address and so stays in LDS
+      float best = -INFINITY;
+      if constexpr (NODE == SLG_NODE_HYBRID) {
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+          best = fmaxf(best, conv_tree_eval<NODE, NLEAF>(v[qq], trow + KM * KS));
+      } else {
+        float par[NPR4];
+#pragma unroll
+        for (int i = 0; i < NPR4 / 4; ++i) {
+          const f32x4 v4 = reinterpret_cast<const f32x4*>(trow + KM * KS)[i];
+          par[4 * i] = v4[0]; par[4 * i + 1] = v4[1]; par[4 * i + 2] = v4[2]; par[4 * i + 3] = v4[3];
+        }
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) best = fmaxf(best, conv_tree_eval<NODE, NLEAF>(v[qq], par));
+      }
+      if (active) out_b[f] = best;
+      // next chunk of this wave
+      n += dn;
+      col += dc;
+      row += dr;
+      if (col >= Wo) { col -= Wo; ++row; }
+      if (row >= Ho) { row -= Ho; ++n; }
+    }
+    __syncthreads();  // every read of this sample precedes the next scatter
+  }
+}
+
 template <int NODE, int NLEAF, bool POOL>
 __global__ void __launch_bounds__(256)
 conv_hard_kernel(const uint64_t* __restrict__ xp, int C, int H, int W, int nw, int N,
@@ -1085,20 +1273,46 @@ static ConvGeom conv_geom_pair(int64_t C, int64_t Ho, int64_t Wo, int kernel) {
   return g;
 }
 
-// The pair layout is used for pooled blocks with phase-eligible taps whose
-// quad copies do not fit but whose two pair copies do, whose image rides in
-// kPairRegs registers per thread and whose pooled rows take at most
-// kPairMaxChunks chunks of 64 lanes.
-static bool conv_use_pair(bool pool, int nleaf, int km, int64_t C, int64_t H, int64_t W,
-                          int64_t Ho, int64_t Wo, int kernel) {
-  if (!conv_phase_layout(pool, nleaf, km) || Ho <= 0 || Wo <= 0) return false;
-  if (conv_use_quad(pool, nleaf, km, C, Ho, Wo, kernel)) return false;
-  if (C * H * W > (int64_t)kPairRegs * kQuadThreads) return false;
-  if (C * 8 * (Ho + kernel) * (Wo + kernel) >= (1LL << 29)) return false;
-  const ConvGeom g = conv_geom_pair(C, Ho, Wo, kernel);
-  if (g.LPS > 64 * kPairMaxChunks) return false;
+// Floats per channel of the flat pair kernel's parameter table (FlatRec::FW).
+static int conv_flat_fw(int node, int nleaf, int km) {
+  const int npr = node == SLG_NODE_GATE16 ? 4 * (nleaf - 1) : (1 << nleaf);
+  return km * ((3 * nleaf + 3) & ~3) + ((npr + 3) & ~3);
+}
+
+// Flat lanes where the parameter table fits beside the image and a
+// channel's pooled map is not a whole number of 64-lane chunks.
+static bool conv_pair_flat(const ConvGeom& g, int64_t N, int64_t Ho, int64_t Wo, int fw) {
   const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
-  return (int64_t)g.SST * 4 + kConvExtra * 4 <= cap;
+  if (((int64_t)g.SST + kConvExtra + N * fw) * 4 > cap) return false;
+  return (Ho * Wo) % 64 != 0;
+}
+
+enum { kLayoutPlain = 0, kLayoutQuad = 1, kLayoutPair = 2 };
+
+// Layout of a pooled block with phase-eligible taps: quad where its four
+// copies fit one workgroup's LDS and a channel's outputs fill at least 7/8
+// of its 16-lane groups; else pair where the two pair copies fit, the image
+// rides in kPairRegs registers per thread and either the flat kernel's
+// parameter table fits too or a channel's lanes take at most kPairMaxChunks
+// chunks; else quad where it fits; else the phase-split layout.
+static int conv_pooled_layout(bool pool, int node, int nleaf, int km, int64_t C, int64_t H,
+                              int64_t W, int64_t Ho, int64_t Wo, int kernel, int64_t N) {
+  if (!conv_phase_layout(pool, nleaf, km) || Ho <= 0 || Wo <= 0) return kLayoutPlain;
+  const bool quad = conv_use_quad(pool, nleaf, km, C, Ho, Wo, kernel);
+  bool pair = C * H * W <= (int64_t)kPairRegs * kQuadThreads &&
+              C * 8 * (Ho + kernel) * (Wo + kernel) < (1LL << 29);
+  bool flat = false;
+  if (pair) {
+    const ConvGeom g = conv_geom_pair(C, Ho, Wo, kernel);
+    const int64_t cap = std::min<int64_t>(device_lds_bytes(), 160 * 1024);
+    flat = conv_pair_flat(g, N, Ho, Wo, conv_flat_fw(node, nleaf, km));
+    pair = (int64_t)g.SST * 4 + kConvExtra * 4 <= cap && (flat || g.LPS <= 64 * kPairMaxChunks);
+  }
+  if (quad) {
+    const int64_t P = Ho * Wo, lanes = 16 * cdiv(P, 16);
+    return (pair && flat && 8 * P < 7 * lanes) ? kLayoutPair : kLayoutQuad;
+  }
+  return pair ? kLayoutPair : kLayoutPlain;
 }
 
 // LDS geometry for images (C, H, W) with 'same' padding pad, pooled to
@@ -1223,8 +1437,11 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
 template <int NODE, int NLEAF, int KM, bool REC>
 static int launch_conv_soft_pair(const ConvSoftArgs& a, hipStream_t st) {
   const ConvGeom g = conv_geom_pair(a.C, a.Ho, a.Wo, a.kernel);
-  const size_t lds = (size_t)(g.SST + kConvExtra) * 4;
-  auto pk = conv_soft_pair_kernel<NODE, NLEAF, KM, REC>;
+  constexpr int FW = FlatRec<NODE, NLEAF, KM>::FW;
+  const bool flat = conv_pair_flat(g, a.N, a.Ho, a.Wo, FW);
+  const size_t lds = (size_t)(g.SST + kConvExtra + (flat ? a.N * FW : 0)) * 4;
+  auto pk = flat ? conv_soft_flat_kernel<NODE, NLEAF, KM, REC>
+                 : conv_soft_pair_kernel<NODE, NLEAF, KM, REC>;
   if (lds > 65536) {
     hipError_t e =
         hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1246,10 +1463,12 @@ static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
   // taps per leaf: 4 registers when K <= 4 (TopK k=4, fixed wiring), else 8
   if (a.K <= 4) {
     if constexpr (conv_phase_layout(POOL, NLEAF, 4)) {
-      if (conv_use_quad(POOL, NLEAF, 4, a.C, a.Ho, a.Wo, a.kernel))
+      const int lay = conv_pooled_layout(POOL, NODE, NLEAF, 4, a.C, a.H, a.W, a.Ho, a.Wo,
+                                         a.kernel, a.N);
+      if (lay == kLayoutQuad)
         return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, 4, true, true>(a, st)
                      : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false, true>(a, st);
-      if (conv_use_pair(POOL, NLEAF, 4, a.C, a.H, a.W, a.Ho, a.Wo, a.kernel))
+      if (lay == kLayoutPair)
         return a.rec ? launch_conv_soft_pair<NODE, NLEAF, 4, true>(a, st)
                      : launch_conv_soft_pair<NODE, NLEAF, 4, false>(a, st);
     }
@@ -1257,10 +1476,12 @@ static int launch_conv_soft(const ConvSoftArgs& a, hipStream_t st) {
                  : launch_conv_soft_k<NODE, NLEAF, POOL, 4, false, false>(a, st);
   }
   if constexpr (conv_phase_layout(POOL, NLEAF, kMaxK)) {
-    if (conv_use_quad(POOL, NLEAF, kMaxK, a.C, a.Ho, a.Wo, a.kernel))
+    const int lay = conv_pooled_layout(POOL, NODE, NLEAF, kMaxK, a.C, a.H, a.W, a.Ho, a.Wo,
+                                       a.kernel, a.N);
+    if (lay == kLayoutQuad)
       return a.rec ? launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, true, true>(a, st)
                    : launch_conv_soft_k<NODE, NLEAF, POOL, kMaxK, false, true>(a, st);
-    if (conv_use_pair(POOL, NLEAF, kMaxK, a.C, a.H, a.W, a.Ho, a.Wo, a.kernel))
+    if (lay == kLayoutPair)
       return a.rec ? launch_conv_soft_pair<NODE, NLEAF, kMaxK, true>(a, st)
                    : launch_conv_soft_pair<NODE, NLEAF, kMaxK, false>(a, st);
   }
@@ -1436,8 +1657,9 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
               "conv_soft_records: image too large");
   // the layout the forward will choose for these shapes (quad offsets sit in
   // slot 0 of the phase records, pair offsets in slots 0 and 1)
-  const bool quad = conv_use_quad(pool != 0, nleaf, km, C, Ho, Wo, 2 * pad + 1);
-  const bool pair = conv_use_pair(pool != 0, nleaf, km, C, H, W, Ho, Wo, 2 * pad + 1);
+  const int lay = conv_pooled_layout(pool != 0, node_kind, nleaf, km, C, H, W, Ho, Wo,
+                                     2 * pad + 1, N);
+  const bool quad = lay == kLayoutQuad, pair = lay == kLayoutPair;
   const ConvGeom g = quad ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
                           : (pair ? conv_geom_pair(C, Ho, Wo, 2 * pad + 1)
                                   : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo));

@@ -52,7 +52,7 @@ def _blk(conv, H):
     ("gate16", 2, 5, "topk", 4, 8, 6, 2),
     ("gate16", 2, 2, "topk", 48, 32, 8, 2),      # 196 KB image: past LDS
     ("gate16", 2, 2, "topk", 13, 24, 8, 3),      # quad layout, staged without registers
-    ("gate16", 2, 2, "topk", 7, 14, 10, 300),    # quad layout, persistent: 300 samples
+    ("gate16", 2, 2, "topk", 7, 16, 10, 300),    # quad layout, persistent: 300 samples
     # pooled row-major layout with the window's columns swapped on odd pooled
     # columns (the read pattern of config 5's block 1: 128 channels, 16x16)
     ("multilinear", 6, 1, "topk", 128, 16, 24, 2),
@@ -130,11 +130,15 @@ def test_conv_net_with_node_trees(node):
     ("multilinear", 4, 1, 4, 64, 14, 10, 2),  # LUT4 trees
     ("hybrid", 2, 1, 4, 64, 14, 10, 2),
     ("gate16", 2, 2, 4, 64, 14, 8, 300),      # more samples than workgroups (persistent)
+    ("gate16", 2, 2, 4, 128, 7, 256, 3),      # config 3 block 2: 3x3 maps, flat lanes over quad
+    ("gate16", 2, 2, 4, 7, 14, 10, 300),      # 7x7 maps of a small image, 300 samples
 ])
 def test_pair_layout(node, arity, depth, K, C, H, N, B):
-    """Pooled blocks whose four quad copies exceed LDS but two column-shifted
-    copies fit (the pair layout): eval (records) and gradient-mode (separate
-    arrays) forwards against the oracle."""
+    """Pooled blocks on the pair layout (two column-shifted copies: images
+    whose quad copies exceed LDS, or whose pooled maps fill few lanes of the
+    quad kernel's 16-lane groups), one channel per chunk or flat lanes over
+    channels: eval (records) and gradient-mode (separate arrays) forwards
+    against the oracle."""
     conv = sl.ConvLogicTree(C, N, kernel=3, tree_depth=depth, connect="topk", k=K, n_chan=2,
                             residual_init=False, seed=C + N, node=node, arity=arity, tau=0.7)
     sd = {k: v.clone() for k, v in conv.state_dict().items()}
