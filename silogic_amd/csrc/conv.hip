@@ -440,7 +440,7 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
       } else {
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
-          if (k < K) {
+          if (k == 0 || k < K) {  // K >= 1: step 0 always runs
             float t[NLEAF][NQ];
             read_step(k, t);
             __builtin_amdgcn_sched_barrier(0);  // all reads of the step, then the FMAs
@@ -538,8 +538,13 @@ conv_soft_quad_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
   // conv_soft_kernel's quad path)
   const int cslot = 2 * (lane >> 5) + (__popc((lane >> 2) & 7) & 1);
   const int rank = ((lane & 31) >> 3) * 4 + (lane & 3);
-  const int nchunks = (P + LPC - 1) / LPC;
-  const int d_row = LPC / Wo, d_col = LPC - d_row * Wo;
+  // lanes walk rows of WW = g.RS columns: Wo, or BW (the copies' blocks per
+  // row) where runs of 16 consecutive outputs would put two blocks of one
+  // bank class in a conflict group; lanes on a padding column read their
+  // own block (in bounds: at most one block past a copy) and store nothing
+  const int WW = g.RS;
+  const int nchunks = (Ho * WW + LPC - 1) / LPC;
+  const int d_row = LPC / WW, d_col = LPC - d_row * WW;
   auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int nb) {
     const int nv = min(nb + cslot, N - 1);
     if constexpr (REC) conv_params_record_quad<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
@@ -560,16 +565,17 @@ conv_soft_quad_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
       if (!one_group) load(Pc, nb);
       const int n = nb + cslot;
       float* out_n = out + ((int64_t)b * N + min(n, N - 1)) * P;
-      int q_row = rank / Wo, q_col = rank - (rank / Wo) * Wo;
+      int q_row = rank / WW, q_col = rank - (rank / WW) * WW;
       for (int chunk = 0; chunk < nchunks; ++chunk) {
         const int q = chunk * LPC + rank;
-        const bool active = q < P && n < N;
+        const bool inside = q < Ho * WW;
         const int row = q_row, col = q_col;
+        const bool active = inside && col < Wo && n < N;
         q_col += d_col;
         q_row += d_row;
-        if (q_col >= Wo) { q_col -= Wo; ++q_row; }
+        if (q_col >= WW) { q_col -= WW; ++q_row; }
         const f32x4* base =
-            reinterpret_cast<const f32x4*>(lds) + (active ? (int)__umul24(row, g.BW) + col : 0);
+            reinterpret_cast<const f32x4*>(lds) + (inside ? (int)__umul24(row, g.BW) + col : 0);
         float v[4][NLEAF];
 #pragma unroll
         for (int l = 0; l < NLEAF; ++l)
@@ -577,7 +583,7 @@ conv_soft_quad_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
           for (int qq = 0; qq < 4; ++qq) v[qq][l] = 0.0f;
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
-          if (k < K) {
+          if (k == 0 || k < K) {  // K >= 1: step 0 always runs
             f32x4 t[NLEAF];
 #pragma unroll
             for (int l = 0; l < NLEAF; ++l) t[l] = base[Pc.off[l][k][0]];
@@ -716,7 +722,7 @@ conv_soft_pair_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
           for (int qq = 0; qq < 4; ++qq) v[qq][l] = 0.0f;
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
-          if (k < K) {
+          if (k == 0 || k < K) {  // K >= 1: step 0 always runs
             f32x2 t0[NLEAF], t1[NLEAF];
 #pragma unroll
             for (int l = 0; l < NLEAF; ++l) {
@@ -876,7 +882,7 @@ conv_soft_flat_kernel(const float* __restrict__ x, int B, int C, int H, int W, i
         for (int qq = 0; qq < 4; ++qq) v[qq][l] = 0.0f;
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
-        if (k < K) {
+        if (k == 0 || k < K) {  // K >= 1: step 0 always runs
           float st[KS];  // this step's offsets and weights
 #pragma unroll
           for (int i = 0; i < KS / 4; ++i) {
@@ -1246,7 +1252,42 @@ static ConvGeom conv_geom_quad(int64_t C, int64_t Ho, int64_t Wo, int kernel) {
   g.plane = 16 * g.BH * g.BW;  // floats: four copies of BH x BW blocks of four
   g.LPS = (int)(Ho * Wo);
   g.SST = (int)(C * g.plane);
+  g.RS = (int)Wo;  // the persistent kernel's lane walk (conv_quad_walk)
   return g;
+}
+
+// b128 conflict groups of the persistent quad kernel's chunks whose 16 blocks
+// (one per lane, outputs walked in rows of ww columns) hold two distinct
+// blocks of one bank class (block mod 16), over one channel's chunks.
+static int quad_colliding_groups(int64_t Ho, int64_t Wo, int BW, int64_t ww) {
+  const int64_t n = Ho * ww;
+  int bad = 0;
+  for (int64_t c0 = 0; c0 < n; c0 += 16) {
+    int seen[16];
+    for (int i = 0; i < 16; ++i) seen[i] = -1;
+    bool clash = false;
+    for (int64_t q = c0; q < std::min<int64_t>(c0 + 16, n); ++q) {
+      const int64_t row = q / ww, col = q % ww;
+      if (col >= Wo) continue;
+      const int blk = (int)(row * BW + col);
+      if (seen[blk & 15] >= 0 && seen[blk & 15] != blk) clash = true;
+      seen[blk & 15] = blk;
+    }
+    bad += clash;
+  }
+  return bad;
+}
+
+// The persistent quad kernel walks rows of BW columns (padding lanes idle)
+// where the dense walk has a bank-class collision in most 16-lane groups and
+// the padded walk takes at most 1/8 more chunks.
+static int conv_quad_walk(int64_t Ho, int64_t Wo, int BW) {
+  const int64_t dense = cdiv(Ho * Wo, 16), padded = cdiv(Ho * BW, 16);
+  if (8 * padded > 9 * dense) return (int)Wo;
+  return 2 * quad_colliding_groups(Ho, Wo, BW, Wo) > dense &&
+                 quad_colliding_groups(Ho, Wo, BW, BW) < quad_colliding_groups(Ho, Wo, BW, Wo)
+             ? BW
+             : (int)Wo;
 }
 
 // The quad layout is used for pooled blocks with phase-eligible taps whose
@@ -1407,8 +1448,10 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
         }
       }
       const int64_t grid = std::min<int64_t>(a.B, device_cus());
+      ConvGeom gq = g;
+      gq.RS = conv_quad_walk(a.Ho, a.Wo, g.BW);
       hipLaunchKernelGGL(qk, dim3((unsigned)grid), dim3(kQuadThreads), lds, st, a.x, (int)a.B,
-                         (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, g, a.np,
+                         (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, gq, a.np,
                          a.w, a.cm, a.ch, a.cw, a.rec, a.out, (int)a.Ho, (int)a.Wo);
       SLG_LAUNCH_CHECK("conv_soft");
       return 0;

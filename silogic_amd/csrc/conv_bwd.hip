@@ -317,7 +317,7 @@ conv_soft_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gy, 
           for (int l = 0; l < NLEAF; ++l) v[q][l] = 0.0f;
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
-          if (k < K) {
+          if (k == 0 || k < K) {  // K >= 1: step 0 always runs
 #pragma unroll
             for (int l = 0; l < NLEAF; ++l) {
               const int4 e = tp[l * K + k];

@@ -53,6 +53,7 @@ def _blk(conv, H):
     ("gate16", 2, 2, "topk", 48, 32, 8, 2),      # 196 KB image: past LDS
     ("gate16", 2, 2, "topk", 13, 24, 8, 3),      # quad layout, staged without registers
     ("gate16", 2, 2, "topk", 7, 16, 10, 300),    # quad layout, persistent: 300 samples
+    ("gate16", 2, 2, "topk", 7, 28, 16, 3),      # quad, lanes walking padded rows (14x14 maps)
     # pooled row-major layout with the window's columns swapped on odd pooled
     # columns (the read pattern of config 5's block 1: 128 channels, 16x16)
     ("multilinear", 6, 1, "topk", 128, 16, 24, 2),
