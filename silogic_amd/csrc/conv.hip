@@ -47,6 +47,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ inline float sigmoidc(float z) { return 1.0f / (1.0f + expf(-z)); }
 
 constexpr int kMaxK = 8;
+constexpr int kQuadThreadsC = 1024;  // quad-layout workgroups (kQuadThreads)
 
 
 // Layout choice and register budget of one kernel variant (host and device).
@@ -64,7 +65,22 @@ struct ConvCfg {
   // eight waves per workgroup where the parameters leave room for two waves
   // per SIMD, else four
   static constexpr int THREADS = PARAMS <= 128 ? 512 : 256;
+  // row-major records whose taps and weights fit the scalar file
+  // (conv_params_record_split): those in scalar registers, the node
+  // parameters in VGPRs, which leaves room for four waves per SIMD: such
+  // kernels are built for up to 1024 threads and launched with 1024 where
+  // one workgroup fills a CU's LDS, else 512 (two workgroups per CU)
+  static constexpr bool SPLIT_OK = NW == 1 && 2 * NLEAF * KM <= 48 &&
+                                   ConvNode<NODE, NLEAF>::NPR % 4 == 0;
+  static constexpr int SPLIT_THREADS = 1024;
 };
+
+// Threads per workgroup of conv_soft_kernel (at most; see SPLIT_OK).
+template <int NODE, int NLEAF, int KM, bool POOL, bool REC, bool QUAD>
+__host__ __device__ constexpr int conv_soft_threads() {
+  using Cfg = ConvCfg<NODE, NLEAF, KM, POOL>;
+  return QUAD ? kQuadThreadsC : (REC && Cfg::SPLIT_OK ? Cfg::SPLIT_THREADS : Cfg::THREADS);
+}
 
 // LDS floats after the S staged samples: 64 dump slots, one per lane, that
 // take the staged floats no window reads.
@@ -187,6 +203,40 @@ __device__ inline void conv_params_record(ConvParams<NODE, NLEAF, KM, NW>& P, co
   for (int i = 0; i < ConvNode<NODE, NLEAF>::NPR; ++i) P.par[i] = v[LK * (NW + 1) + i];
 }
 
+// Channel parameters from a record with the taps and weights read at the
+// wave-uniform channel n (scalar loads: scalar registers, no vector memory
+// traffic per lane) and the node parameters at the same channel held in a
+// vector register nv (vector loads: VGPRs, since an FMA takes one scalar
+// operand and the tree's FMAs would take two).
+template <int NODE, int NLEAF, int KM, int NW, int R>
+__device__ inline void conv_params_record_split(ConvParams<NODE, NLEAF, KM, NW>& P,
+                                                const float* rec, int n, int nv) {
+  constexpr int LK = NLEAF * KM;
+  constexpr int NPR = ConvNode<NODE, NLEAF>::NPR;
+  static_assert((LK * (NW + 1)) % 4 == 0 && NPR % 4 == 0, "16-byte record parts");
+  float v[LK * (NW + 1)];
+  const float4* r4 = reinterpret_cast<const float4*>(rec + (int64_t)n * R);
+#pragma unroll
+  for (int q = 0; q < LK * (NW + 1) / 4; ++q) {
+    const float4 t = r4[q];
+    v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+  }
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l)
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+#pragma unroll
+      for (int q = 0; q < NW; ++q) P.off[l][k][q] = __float_as_int(v[(l * KM + k) * NW + q]);
+      P.wt[l][k] = v[LK * NW + l * KM + k];
+    }
+  const float4* p4 = reinterpret_cast<const float4*>(rec + (int64_t)nv * R + LK * (NW + 1));
+#pragma unroll
+  for (int q = 0; q < NPR / 4; ++q) {
+    const float4 t = p4[q];
+    P.par[4 * q] = t.x; P.par[4 * q + 1] = t.y; P.par[4 * q + 2] = t.z; P.par[4 * q + 3] = t.w;
+  }
+}
+
 // Channel parameters from a quad record: the records of phase-eligible
 // trees keep their phase size R, but a quad-layout record packs one offset
 // per tap (float4 units), then the weights, then the node parameters, so
@@ -221,7 +271,7 @@ __device__ inline void conv_params_record_quad(ConvParams<NODE, NLEAF, KM, NW>& 
 // Quad-layout workgroups: 16 waves (the layout takes most of the LDS, so one
 // workgroup per CU; its per-tap state is one offset, which leaves room in
 // 128 VGPRs).
-constexpr int kQuadThreads = 1024;
+constexpr int kQuadThreads = kQuadThreadsC;
 
 // SWAP (pooled row-major layout only): lanes of odd pooled columns take the
 // window's two columns in the other order, so that each of the four reads
@@ -230,7 +280,7 @@ constexpr int kQuadThreads = 1024;
 // leaf and tap, and the pooled output is the maximum over the four
 // positions, so the result is the same.
 template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD, bool SWAP = false>
-__global__ void __launch_bounds__((QUAD ? kQuadThreads : ConvCfg<NODE, NLEAF, KM, POOL>::THREADS))
+__global__ void __launch_bounds__((conv_soft_threads<NODE, NLEAF, KM, POOL, REC, QUAD>()))
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
                  int pad, ConvGeom g, const float* __restrict__ np, const float* __restrict__ wts,
                  const int* __restrict__ cm, const int* __restrict__ ch, const int* __restrict__ cw,
@@ -334,11 +384,15 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
   const int cslot = QUAD ? 2 * (lane >> 5) + (__popc((lane >> 2) & 7) & 1) : 0;
   const int rank = QUAD ? (((lane & 31) >> 3) * 4 + (lane & 3)) : lane;
   const int nchunks_c = QUAD ? (ns * g.LPS + LPC - 1) / LPC : nchunks;
+  // row-major records whose taps and weights fit the scalar file: those in
+  // scalar registers, the node parameters in VGPRs
+  constexpr bool SPLIT = REC && !QUAD && Cfg::SPLIT_OK;
   auto load = [&](ConvParams<NODE, NLEAF, KM, NW>& Pr, int n) {
     int nv;  // the channel in a vector register: vector loads, VGPR parameters
     if constexpr (QUAD) nv = min(n + cslot, N - 1);
     else asm volatile("v_mov_b32 %0, %1" : "=v"(nv) : "s"(n));
     if constexpr (REC && QUAD) conv_params_record_quad<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
+    else if constexpr (SPLIT) conv_params_record_split<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, n, nv);
     else if constexpr (REC) conv_params_record<NODE, NLEAF, KM, NW, Cfg::REC>(Pr, rec, nv);
     else conv_params_arrays<NODE, NLEAF, KM, NW>(Pr, nv, K, C, kernel, g, np, wts, cm, ch, cw);
   };
@@ -1469,7 +1523,9 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
       return (int)e;
     }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(QUAD ? kQuadThreads : Cfg::THREADS),
+  int threads = conv_soft_threads<NODE, NLEAF, KM, POOL, REC, QUAD>();
+  if (REC && !QUAD && Cfg::SPLIT_OK && 2 * (int64_t)lds <= cap) threads = 512;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.B, S)), dim3(threads),
                      lds, st, a.x,
                      (int)a.B, (int)a.C, (int)a.H, (int)a.W, (int)a.N, a.K, a.kernel, a.pad, g,
                      a.np, a.w, a.cm, a.ch, a.cw, a.rec, (int)S, a.out, (int)a.Ho, (int)a.Wo);
