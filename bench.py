@@ -428,10 +428,10 @@ def soft_stages(cfg, model, B_soft, x_soft, dev):
 
 
 def hard_launches(cfg, model, x_hard):
-    """The C-ABI launches of ``forward_hard`` on ``x_hard`` (the cached launch
-    sequence), each with what it moves and computes:
+    """The C-ABI launches of ``forward_hard`` on ``x_hard`` (the cached
+    ``slg_hard_step`` descriptor), each with what it moves and computes:
     ``[(name, fn, bytes, bitops)]``. ``fn`` re-launches that one kernel on the
-    sequence's own buffers."""
+    descriptor's own buffers."""
     import ctypes
     from silogic_amd import ops
     from silogic_amd.synthetic import CONFIGS
@@ -445,15 +445,35 @@ def hard_launches(cfg, model, x_hard):
     B = x_hard.shape[0]
     nw = ops.n_words(B)
     isz = x_hard.element_size()
+    # the descriptor's launches as separate C-ABI calls (what slg_hard_step
+    # makes), each on the descriptor's own buffers
+    from silogic_amd import _lib
+    L, d, st = _lib.lib(), step.step, step.st
+    xv, ov = ctypes.c_void_p(x_hard.data_ptr()), ctypes.c_void_p(out.data_ptr())
+    calls = []
+    if d.pack == 1:
+        calls.append((L.slg_pack_image_wm, "slg_pack_image_wm",
+                      [xv, d.dtype, B, d.C, d.H, d.W, d.pack_pad, d.packed, st]))
+    elif d.pack == 2:
+        calls.append((L.slg_pack_bits, "slg_pack_bits",
+                      [xv, d.dtype, B, d.C * d.H * d.W, 1, d.packed, st]))
+    for c in d.conv[:d.n_conv]:
+        calls.append((L.slg_conv_hard_fwd_wm, "slg_conv_hard_fwd_wm",
+                      [c.inp, B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity, c.leaf, c.tt,
+                       c.kernel, c.pad, c.out, c.out_pad, st]))
+    hin = d.head_in if d.head_in else xv
+    if d.plan:
+        calls.append((L.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
+                      [hin, d.head_in_kind, B, d.head_in_dim, d.n_layers, d.widths, d.codes,
+                       d.plan, d.n_classes, ov, st]))
+    else:
+        calls.append((L.slg_fc_hard_net, "slg_fc_hard_net",
+                      [hin, d.head_in_kind, B, d.head_in_dim, d.n_layers, d.widths, d.codes,
+                       d.n_classes, d.wire_r, ov, st]))
     res = []
     geo = None if hasattr(model, "layers") else conv_geometry(model, CONFIGS[cfg][1]["in_hw"])
     conv_i = 0
-    for i, (fn, name, args) in enumerate(step.calls):
-        a = list(args)
-        if i == step.in_slot[0]:
-            a[step.in_slot[1]] = ctypes.c_void_p(x_hard.data_ptr())
-        if i == step.out_slot[0]:
-            a[step.out_slot[1]] = ctypes.c_void_p(out.data_ptr())
+    for fn, name, a in calls:
         launch = (lambda f=fn, aa=a: f(*aa))
         if name in ("slg_pack_bits", "slg_pack_image_wm"):
             D = x_hard[0].numel()

@@ -593,6 +593,49 @@ int slg_conv_hard_fwd_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, in
 int slg_pack_image_wm(const void* x, int32_t dtype, int64_t B, int64_t C, int64_t H, int64_t W,
                       int32_t pad, uint64_t* xp, slg_stream_t stream);
 
+/* A network's forward_hard as one call (no counterpart in the reference,
+ * whose LogicNet / LogicConvNet.forward_hard run their layers from Python,
+ * models.py:99-101 and 283-293): the launches of its packing
+ * (slg_pack_image_wm or slg_pack_bits, word-major), of slg_conv_hard_fwd_wm
+ * for each conv block and of slg_fc_hard_net_typed (plan set) or
+ * slg_fc_hard_net for the head, in that order on one stream, from a
+ * descriptor built once per input shape. Every pointer in it must stay
+ * valid while it is used; the intermediate buffers are the descriptor's,
+ * so calls that overlap on one descriptor race (serialise them). For
+ * callers that run one network many times and would otherwise pay each
+ * launch's C-ABI argument conversion per call. Returns the first error of
+ * the calls it makes (their checks and codes). */
+#define SLG_STEP_MAX_CONV 8
+typedef struct {
+  const uint64_t* in;  /* word-major zero-bordered input images (pad words) */
+  uint64_t* out;       /* its pooled output, out_pad words of zero border */
+  int64_t C, H, W, N;
+  int32_t node_kind, depth, arity, kernel, pad, out_pad;
+  const int32_t* leaf;
+  const uint64_t* tt;
+} slg_step_conv_t;
+typedef struct {
+  int32_t pack;        /* 0: the head reads x; 1: slg_pack_image_wm; 2: slg_pack_bits */
+  int32_t dtype;       /* x: 0 fp32, 1 uint8 */
+  int64_t B;
+  int64_t C, H, W;     /* pack 1: the image; pack 2: C*H*W features per sample */
+  int32_t pack_pad;    /* pack 1: the packed image's zero border */
+  uint64_t* packed;    /* the packing's output */
+  int32_t n_conv;      /* 0..SLG_STEP_MAX_CONV */
+  slg_step_conv_t conv[SLG_STEP_MAX_CONV];
+  const void* head_in; /* null: x (pack 0) */
+  int32_t head_in_kind;
+  int64_t head_in_dim;
+  int32_t n_layers;
+  const int64_t* widths;
+  const uint32_t* const* codes;
+  const int32_t* plan; /* type-placed codes' plan, or null */
+  int32_t n_classes;
+  int64_t wire_r;
+} slg_hard_step_t;
+int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
+                  slg_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Packed building blocks of the silogic.bitpacking API                      */
 /* ---------------------------------------------------------------------- */

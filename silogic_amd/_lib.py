@@ -95,6 +95,7 @@ SIGNATURES = {
                                          _I32, _I32, _I32, _P, _P]),
     "slg_conv_hard_fwd": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P,
                                     _I32, _I32, _I32, _P, _P]),
+    "slg_hard_step": (C.c_int, [_P, _P, _P, _P]),
     "slg_conv_hard_fwd_wm": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P,
                                        _P, _I32, _I32, _P, _I32, _P]),
     "slg_pack_image_wm": (C.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P]),
@@ -103,6 +104,25 @@ SIGNATURES = {
 _lock = threading.Lock()
 _lib = None
 _load_error = None
+
+
+class StepConv(C.Structure):
+    """``slg_step_conv_t``: one conv block of a ``slg_hard_step_t``."""
+    _fields_ = [("inp", _P), ("out", _P), ("C", _I64), ("H", _I64), ("W", _I64), ("N", _I64),
+                ("node_kind", _I32), ("depth", _I32), ("arity", _I32), ("kernel", _I32),
+                ("pad", _I32), ("out_pad", _I32), ("leaf", _P), ("tt", _P)]
+
+
+STEP_MAX_CONV = 8
+
+
+class HardStep(C.Structure):
+    """``slg_hard_step_t``: a network's forward_hard launch sequence."""
+    _fields_ = [("pack", _I32), ("dtype", _I32), ("B", _I64), ("C", _I64), ("H", _I64),
+                ("W", _I64), ("pack_pad", _I32), ("packed", _P), ("n_conv", _I32),
+                ("conv", StepConv * STEP_MAX_CONV), ("head_in", _P), ("head_in_kind", _I32),
+                ("head_in_dim", _I64), ("n_layers", _I32), ("widths", _P), ("codes", _P),
+                ("plan", _P), ("n_classes", _I32), ("wire_r", _I64)]
 
 
 def library_path():

@@ -1,0 +1,36 @@
+// A network's forward_hard as one C-ABI call: the launch sequence of
+// LogicNet / LogicConvNet.forward_hard (silogic/models.py:99-101, 283-293)
+// from a descriptor built once per input shape. Host code only: it calls
+// the entry points that a launch-per-call caller would.
+#include "slg_common.h"
+
+extern "C" {
+
+int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
+                  slg_stream_t stream) {
+  SLG_REQUIRE(step && x && logits, SLG_E_ARG, "hard_step: null pointer");
+  const slg_hard_step_t& s = *step;
+  SLG_REQUIRE(s.n_conv >= 0 && s.n_conv <= SLG_STEP_MAX_CONV && s.pack >= 0 && s.pack <= 2,
+              SLG_E_ARG, "hard_step: pack %d, %d conv blocks", s.pack, s.n_conv);
+  int rc = 0;
+  if (s.pack == 1) {
+    rc = slg_pack_image_wm(x, s.dtype, s.B, s.C, s.H, s.W, s.pack_pad, s.packed, stream);
+  } else if (s.pack == 2) {
+    rc = slg_pack_bits(x, s.dtype, s.B, s.C * s.H * s.W, 1, s.packed, stream);  // word-major
+  }
+  if (rc) return rc;
+  for (int i = 0; i < s.n_conv; ++i) {
+    const slg_step_conv_t& c = s.conv[i];
+    rc = slg_conv_hard_fwd_wm(c.in, s.B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity,
+                              c.leaf, c.tt, c.kernel, c.pad, c.out, c.out_pad, stream);
+    if (rc) return rc;
+  }
+  const void* hin = s.head_in ? s.head_in : x;
+  if (s.plan)
+    return slg_fc_hard_net_typed(hin, s.head_in_kind, s.B, s.head_in_dim, s.n_layers, s.widths,
+                                 s.codes, s.plan, s.n_classes, logits, stream);
+  return slg_fc_hard_net(hin, s.head_in_kind, s.B, s.head_in_dim, s.n_layers, s.widths, s.codes,
+                         s.n_classes, s.wire_r, logits, stream);
+}
+
+}  // extern "C"

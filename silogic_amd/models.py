@@ -414,41 +414,41 @@ class LogicConvNet(nn.Module):
         return total
 
 
-def _fc_net_call(lib, x_ptr, in_kind, B, in_dim, codes, n_cls, wire_r, st):
-    """The fused network's entry point and arguments (logits slot None), as
-    ``ops.fc_hard_net`` passes them."""
-    if codes.plan is not None:
-        if wire_r or in_dim != codes.in_dim:
-            raise ValueError("forward_hard: type-placed codes take inputs %s wide and no wire "
-                             "residual (got %d, wire_r %d)" % (codes.in_dim, in_dim, wire_r))
-        return (lib.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
-                [x_ptr, in_kind, B, in_dim, len(codes), codes.widths, codes.ptrs,
-                 ops._p(codes.plan), n_cls, None, st])
-    return (lib.slg_fc_hard_net, "slg_fc_hard_net",
-            [x_ptr, in_kind, B, in_dim, len(codes), codes.widths, codes.ptrs, n_cls,
-             int(wire_r), None, st])
-
-
 class _HardStep:
-    """A network's ``forward_hard`` for one input shape on one stream as a
-    fixed sequence of C-ABI launches: for a conv network packing, every conv
+    """A network's ``forward_hard`` for one input shape on one stream as one
+    C-ABI call (``slg_hard_step``): for a conv network packing, every conv
     block (pooled) and the fused head; for an FC network the fused network
     (with packing before it where the kernel takes words). The per-call host
     work of the general path (parameter walks for each table, shape checks,
-    wrapper calls, an allocation per intermediate) is done once here: the
-    intermediate words live in buffers this object keeps (the launches run
-    in stream order, so a call's packing cannot overtake the previous call's
-    reads of them) and a call allocates only its logits. The tables are the
-    general path's own, so the logits are the same bits."""
+    wrapper calls, an allocation per intermediate, a C-ABI call per launch
+    with its argument conversion) is done once here, into a
+    ``slg_hard_step_t`` descriptor: the intermediate words live in buffers
+    this object keeps (the launches run in stream order, so a call's packing
+    cannot overtake the previous call's reads of them) and a call allocates
+    only its logits. The tables are the general path's own, so the logits
+    are the same bits."""
 
-    def __init__(self, calls, out_shape, in_slot, out_slot, bufs, tables):
-        self.calls, self.out_shape = calls, out_shape
-        self.in_slot, self.out_slot = in_slot, out_slot
+    def __init__(self, step, out_shape, st, bufs, tables):
+        from . import _lib
+        self.step, self.out_shape, self.st = step, out_shape, st
         self.bufs, self.tables = bufs, tables          # kept alive for the pointers
-        # one call's launches go out as one run: ctypes releases the GIL
-        # around each launch, and a second host thread's packing must not
-        # land between this call's packing and the conv blocks that read it
+        self.fn, self.ref = _lib.lib().slg_hard_step, ctypes.byref(step)
+        # the descriptor's buffers are shared by every call: a second host
+        # thread's packing must not land between this call's packing and
+        # the launches that read it
         self.lock = threading.Lock()
+
+    @staticmethod
+    def _head(step, head_in, head_kind, in_dim, codes, n_cls, wire_r):
+        """The fused head's fields, as ``ops.fc_hard_net`` passes them."""
+        if codes.plan is not None and (wire_r or in_dim != codes.in_dim):
+            raise ValueError("forward_hard: type-placed codes take inputs %s wide and no wire "
+                             "residual (got %d, wire_r %d)" % (codes.in_dim, in_dim, wire_r))
+        step.head_in, step.head_in_kind, step.head_in_dim = head_in, head_kind, in_dim
+        step.n_layers, step.n_classes, step.wire_r = len(codes), n_cls, int(wire_r)
+        step.widths = ctypes.cast(codes.widths, ctypes.c_void_p)
+        step.codes = ctypes.cast(codes.ptrs, ctypes.c_void_p)
+        step.plan = ops._p(codes.plan) if codes.plan is not None else None
 
     @staticmethod
     def for_fc(model, x):
@@ -463,20 +463,19 @@ class _HardStep:
             return None
         wire_r = model.wire_r
         codes = _hard_fc_net_codes(layers, in_dim, wire_r, bool(not wire_r and typable))
-        st, lib = ops._stream(x), _lib.lib()
         kind = 1 if x.dtype == torch.uint8 else 0
-        calls, bufs = [], []
+        step, bufs = _lib.HardStep(), []
+        step.dtype, step.B = kind, B
         if spw == 64 and in_dim <= 1024:
-            calls.append(_fc_net_call(lib, None, kind, B, in_dim, codes, n_cls, wire_r, st))
+            step.pack = 0
+            _HardStep._head(step, None, kind, in_dim, codes, n_cls, wire_r)
         else:
             xp = torch.empty((ops.n_words(B), in_dim), device=x.device, dtype=torch.int64)
-            calls.append((lib.slg_pack_bits, "slg_pack_bits",
-                          [None, kind, B, in_dim, 1, ops._p(xp), st]))
-            calls.append(_fc_net_call(lib, ops._p(xp), ops.PACKED_WORD_MAJOR, B, in_dim, codes,
-                                      n_cls, wire_r, st))
+            step.pack, step.C, step.H, step.W, step.packed = 2, in_dim, 1, 1, ops._p(xp)
+            _HardStep._head(step, ops._p(xp), ops.PACKED_WORD_MAJOR, in_dim, codes, n_cls,
+                            wire_r)
             bufs.append(xp)
-        return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(calls[-1][2]) - 2),
-                         bufs, [codes])
+        return _HardStep(step, (B, n_cls), ops._stream(x), bufs, [codes])
 
     @staticmethod
     def for_conv(model, x):
@@ -485,18 +484,21 @@ class _HardStep:
         The images between blocks keep a zero border as wide as the next
         block's padding (cleared here, once; the kernels write only the
         interiors), so the conv kernels read every leaf unconditionally.
-        None for generic trees, LUT head layers or head widths past LDS."""
+        None for generic trees, LUT head layers, head widths past LDS or more
+        blocks than the descriptor holds."""
         from . import _lib
         convs = list(model._convs())
-        if not convs or any(conv.generic for conv in convs):
+        if not convs or any(conv.generic for conv in convs) or \
+                len(convs) > _lib.STEP_MAX_CONV:
             return None
         B, C, H, W = x.shape
         nw = ops.n_words(B)
-        dev, st, lib = x.device, ops._stream(x), _lib.lib()
+        dev = x.device
         pads = [conv.padding for conv in convs] + [0]
         xp = torch.zeros((nw, C, H + 2 * pads[0], W + 2 * pads[0]), device=dev, dtype=torch.int64)
-        calls = [(lib.slg_pack_image_wm, "slg_pack_image_wm",
-                  [None, 1 if x.dtype == torch.uint8 else 0, B, C, H, W, pads[0], ops._p(xp), st])]
+        step = _lib.HardStep()
+        step.pack, step.dtype, step.B = 1, 1 if x.dtype == torch.uint8 else 0, B
+        step.C, step.H, step.W, step.pack_pad, step.packed = C, H, W, pads[0], ops._p(xp)
         bufs, tables = [xp], []
         params = derived.cached(
             model, "_derived_conv_codes", derived.state_key(*convs),
@@ -508,13 +510,13 @@ class _HardStep:
             Ho, Wo = Hf // 2, Wf // 2                     # every block is OR-pooled
             out = torch.zeros((nw, conv.n, Ho + 2 * opad, Wo + 2 * opad), device=dev,
                               dtype=torch.int64)
-            calls.append((lib.slg_conv_hard_fwd_wm, "slg_conv_hard_fwd_wm",
-                          [ops._p(cur), B, C, H, W, conv.n, conv._kind(), conv.d,
-                           conv.node_arity, ops._p(leaf), ops._p(tt), k, pad, ops._p(out), opad,
-                           st]))
+            step.conv[i] = _lib.StepConv(ops._p(cur), ops._p(out), C, H, W, conv.n,
+                                         conv._kind(), conv.d, conv.node_arity, k, pad, opad,
+                                         ops._p(leaf), ops._p(tt))
             bufs.append(out)
             tables += [leaf, tt]
             cur, (C, H, W) = out, (conv.n, Ho, Wo)
+        step.n_conv = len(convs)
         in_dim, n_cls, layers = C * H * W, model.head.num_classes, list(model.head_layers)
         if not layers:
             return None
@@ -523,27 +525,14 @@ class _HardStep:
             return None
         codes = _hard_fc_net_codes(layers, in_dim, 0, bool(typable))
         tables.append(codes)
-        head = _fc_net_call(lib, ops._p(cur), ops.PACKED_WORD_MAJOR, B, in_dim, codes, n_cls, 0,
-                            st)
-        calls.append(head)
-        return _HardStep(calls, (B, n_cls), (0, 0), (len(calls) - 1, len(head[2]) - 2),
-                         bufs, tables)
+        _HardStep._head(step, ops._p(cur), ops.PACKED_WORD_MAJOR, in_dim, codes, n_cls, 0)
+        return _HardStep(step, (B, n_cls), ops._stream(x), bufs, tables)
 
     def __call__(self, x):
         from . import _lib
         out = torch.empty(self.out_shape, device=x.device, dtype=torch.float32)
-        (xi, xs), (oi, os_) = self.in_slot, self.out_slot
         with self.lock:
-            for i, (fn, name, args) in enumerate(self.calls):
-                if i == xi or i == oi:
-                    # this call's own argument list: the shared one holds no
-                    # per-call pointer
-                    args = list(args)
-                    if i == xi:
-                        args[xs] = ctypes.c_void_p(x.data_ptr())
-                    if i == oi:
-                        args[os_] = ctypes.c_void_p(out.data_ptr())
-                _lib.check(fn(*args), name)
+            _lib.check(self.fn(self.ref, x.data_ptr(), out.data_ptr(), self.st), "slg_hard_step")
         return out
 
 

@@ -91,6 +91,45 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert L.slg_fc_soft_bwd_workspace(8, 1000, 16, 17) == -1
 
 
+def test_hard_step_descriptor_layout_matches_the_header(tmp_path):
+    """``slg_hard_step_t`` / ``slg_step_conv_t`` as ctypes lays them out, field
+    by field, against the header compiled by the host C compiler; and the
+    entry point's argument checks (before any launch)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    fields = {"slg_step_conv_t": _lib.StepConv, "slg_hard_step_t": _lib.HardStep}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "silogic_hip.h"',
+             "int main(void) {"]
+    for cname, cls in fields.items():
+        lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            cf = "in" if f == "inp" else f
+            lines.append(f'  printf("{cname}.{f} %zu\\n", offsetof({cname}, {cf}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True,
+                                                        text=True, check=True).stdout.split("\n")
+               if l)
+    for cname, cls in fields.items():
+        assert int(got[cname]) == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, (cname, f)
+    L = _lib.lib()
+    step = _lib.HardStep()
+    assert L.slg_hard_step(None, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
+    assert b"null" in L.slg_last_error()
+    step.n_conv = _lib.STEP_MAX_CONV + 1
+    assert L.slg_hard_step(ctypes.byref(step), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                           None) == -1
+
+
 def test_cpu_inputs_are_refused():
     net = silogic_amd.LogicNet(16, 20, 2, k=4)
     x = torch.zeros(3, 16)
