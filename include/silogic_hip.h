@@ -478,6 +478,18 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
                           int32_t depth, int32_t arity, const float* raw, int64_t C,
                           int64_t H, int64_t W, int32_t pad, int32_t pool, float* rec,
                           slg_stream_t stream);
+/* The same records from slg_conv_soft_fwd's separate arrays (node_param and
+ * w as that entry point takes them; gate16, multilinear or hybrid trees):
+ * slg_conv_soft_fwd_records on them gives slg_conv_soft_fwd's output bit for
+ * bit. For a forward whose parameters change every call (training), where
+ * building the records once per call and running the records kernels is
+ * faster than the separate-array kernels (no counterpart in the reference:
+ * the same computation as layers.py:487-497, 408-417, nodes.py:178). */
+int slg_conv_soft_records_arrays(const float* node_param, const float* w, const int32_t* cm,
+                                 const int32_t* ch, const int32_t* cw, int64_t N, int32_t K,
+                                 int32_t node_kind, int32_t depth, int32_t arity, int64_t C,
+                                 int64_t H, int64_t W, int32_t pad, int32_t pool, float* rec,
+                                 slg_stream_t stream);
 
 /* slg_conv_soft_fwd with the channel parameters taken from records built for
  * the same (C, H, W, pad, pool, K, node_kind, depth, arity); same output. */
@@ -604,7 +616,7 @@ int slg_pack_image_wm(const void* x, int32_t dtype, int64_t B, int64_t C, int64_
  * so calls that overlap on one descriptor race (serialise them). For
  * callers that run one network many times and would otherwise pay each
  * launch's C-ABI argument conversion per call. Returns the first error of
- * the calls it makes (their checks and codes). */
+ * the calls it makes (their checks and codes); B = 0 launches nothing. */
 #define SLG_STEP_MAX_CONV 8
 typedef struct {
   const uint64_t* in;  /* word-major zero-bordered input images (pad words) */

@@ -83,6 +83,8 @@ SIGNATURES = {
     "slg_conv_soft_record_floats": (C.c_int64, [_I32, _I32, _I32, _I32, _I32]),
     "slg_conv_soft_records": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _I64,
                                         _I64, _I64, _I32, _I32, _P, _P]),
+    "slg_conv_soft_records_arrays": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32,
+                                               _I64, _I64, _I64, _I32, _I32, _P, _P]),
     "slg_conv_soft_fwd_records": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32,
                                             _I32, _P, _I32, _I32, _P, _P]),
     "slg_conv_hard_prep": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P,

@@ -1116,6 +1116,11 @@ __global__ void conv_soft_prep_kernel(const float* __restrict__ conn, int N, int
 // softmax(logits) @ BASIS per node; LUT: sigmoid(s) of the even corners,
 // then odd - even differences), zeros to R. One thread per record word, so
 // that the loads of different words overlap.
+// ARR: from the separate arrays of slg_conv_soft_fwd instead (conn = the
+// leaf weights w [N,L,K], raw = the node parameters as that entry point takes
+// them: gate16 coefficients, LUT corner values), so that the records hold
+// what conv_params_arrays computes in the kernel, bit for bit.
+template <bool ARR>
 __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const int* __restrict__ cm,
                                          const int* __restrict__ ch, const int* __restrict__ cw,
                                          int N, int leaves, int K, int KM, int NW, int node,
@@ -1139,6 +1144,8 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
         v = __int_as_float(conv_tap_offset(g, NW, c_, h_, w_, slot - lk * NW));
       } else if (!conn) {
         v = 1.0f;
+      } else if (ARR) {
+        v = conn[base + k];
       } else {
         float c[kMaxK];
 #pragma unroll
@@ -1152,6 +1159,10 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
         v = expf(conn[base + k] - m) / sum;
       }
     }
+  } else if (ARR && node != SLG_NODE_MULTILINEAR2) {  // gate16 coefficients, hybrid values
+    const int q = slot - LK * (NW + 1);
+    const int NP = node == SLG_NODE_GATE16 ? 4 * (leaves - 1) : (1 << arity);
+    if (q < NP) v = raw[(int64_t)n * NP + q];
   } else if (node == SLG_NODE_GATE16) {
     const int q = slot - LK * (NW + 1), j = q >> 2;
     if (j < leaves - 1) {
@@ -1175,24 +1186,26 @@ __global__ void conv_soft_records_kernel(const float* __restrict__ conn, const i
     if (q < P) v = sigmoidc(raw[(int64_t)n * P + q]);
   } else {
     // the kept form of conv_tree.h: per group of corners, its polynomial's
-    // coefficients (lut_group_coeffs over the group's sigmoid values)
+    // coefficients (lut_group_coeffs over the group's corner values: the
+    // sigmoid of the logits, or the values as given)
     const int P = 1 << arity, q = slot - LK * (NW + 1);
     const float* s_ = raw + (int64_t)n * P;
+    auto val = [&](int i) { return ARR ? s_[i] : sigmoidc(s_[i]); };
     if (q < P) {
       if (arity >= 3) {
         float c[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) c[i] = sigmoidc(s_[(q & ~7) + i]);
+        for (int i = 0; i < 8; ++i) c[i] = val((q & ~7) + i);
         lut_group_coeffs<3>(c);
         v = c[q & 7];
       } else if (arity == 2) {
         float c[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) c[i] = sigmoidc(s_[i]);
+        for (int i = 0; i < 4; ++i) c[i] = val(i);
         lut_group_coeffs<2>(c);
         v = c[q & 3];
       } else {
-        float c[2] = {sigmoidc(s_[0]), sigmoidc(s_[1])};
+        float c[2] = {val(0), val(1)};
         lut_group_coeffs<1>(c);
         v = c[q & 1];
       }
@@ -1672,6 +1685,44 @@ static int node_leaves(int node, int depth, int arity) {
   return -1;
 }
 
+// Records of slg_conv_soft_records (ARR = false: from the connection logits
+// and raw node parameters) or slg_conv_soft_records_arrays (ARR = true: from
+// slg_conv_soft_fwd's separate arrays), for the layout the forward picks.
+template <bool ARR>
+static int conv_records_launch(const float* conn, const int32_t* cm, const int32_t* ch,
+                               const int32_t* cw, int64_t N, int32_t K, int32_t node_kind,
+                               int32_t depth, int32_t arity, const float* raw, int64_t C,
+                               int64_t H, int64_t W, int32_t pad, int32_t pool, float* rec,
+                               slg_stream_t stream) {
+  SLG_REQUIRE(cm && ch && cw && raw && rec, SLG_E_ARG, "conv_soft_records: null pointer");
+  const int nleaf = node_leaves(node_kind, depth, arity);
+  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_records: depth %d / arity %d", depth, arity);
+  SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft_records: K=%d outside 1..%d", K, kMaxK);
+  SLG_REQUIRE(N > 0 && N < (1LL << 20) && C > 0 && C < (1LL << 20) && H > 0 && H < 4096 &&
+                  W > 0 && W < 4096 && pad >= 0 && pad <= 4,
+              SLG_E_SHAPE, "conv_soft_records: bad sizes");
+  const int km = K <= 4 ? 4 : kMaxK;
+  const bool phase = conv_phase_layout(pool != 0, nleaf, km);
+  const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
+  SLG_REQUIRE(C * ((H + 2 * pad) * (W + 2 * pad) + 64) < (1LL << 31), SLG_E_SHAPE,
+              "conv_soft_records: image too large");
+  // the layout the forward will choose for these shapes (quad offsets sit in
+  // slot 0 of the phase records, pair offsets in slots 0 and 1)
+  const int lay = conv_pooled_layout(pool != 0, node_kind, nleaf, km, C, H, W, Ho, Wo,
+                                     2 * pad + 1, N);
+  const bool quad = lay == kLayoutQuad, pair = lay == kLayoutPair;
+  const ConvGeom g = quad ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
+                          : (pair ? conv_geom_pair(C, Ho, Wo, 2 * pad + 1)
+                                  : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo));
+  const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K, pool);
+  hipLaunchKernelGGL(conv_soft_records_kernel<ARR>, dim3((unsigned)cdiv(N * R, 256)), dim3(256),
+                     0, as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km,
+                     quad ? 1 : (pair ? 2 : (phase ? 4 : 1)), node_kind, arity, raw, (int)C,
+                     2 * pad + 1, g, R, rec);
+  SLG_LAUNCH_CHECK("conv_soft_records");
+  return 0;
+}
+
 }  // namespace slg
 
 using namespace slg;
@@ -1742,34 +1793,20 @@ int slg_conv_soft_records(const float* conn, const int32_t* cm, const int32_t* c
                           const int32_t* cw, int64_t N, int32_t K, int32_t node_kind, int32_t depth,
                           int32_t arity, const float* raw, int64_t C, int64_t H, int64_t W,
                           int32_t pad, int32_t pool, float* rec, slg_stream_t stream) {
-  SLG_REQUIRE(cm && ch && cw && raw && rec, SLG_E_ARG, "conv_soft_records: null pointer");
-  const int nleaf = node_leaves(node_kind, depth, arity);
-  SLG_REQUIRE(nleaf > 0, SLG_E_UNSUPPORTED, "conv_soft_records: depth %d / arity %d", depth, arity);
-  SLG_REQUIRE(K >= 1 && K <= kMaxK, SLG_E_SHAPE, "conv_soft_records: K=%d outside 1..%d", K, kMaxK);
-  SLG_REQUIRE(N > 0 && N < (1LL << 20) && C > 0 && C < (1LL << 20) && H > 0 && H < 4096 &&
-                  W > 0 && W < 4096 && pad >= 0 && pad <= 4,
-              SLG_E_SHAPE, "conv_soft_records: bad sizes");
-  const int km = K <= 4 ? 4 : kMaxK;
-  const bool phase = conv_phase_layout(pool != 0, nleaf, km);
-  const int64_t Ho = pool ? H / 2 : H, Wo = pool ? W / 2 : W;
-  SLG_REQUIRE(C * ((H + 2 * pad) * (W + 2 * pad) + 64) < (1LL << 31), SLG_E_SHAPE,
-              "conv_soft_records: image too large");
-  // the layout the forward will choose for these shapes (quad offsets sit in
-  // slot 0 of the phase records, pair offsets in slots 0 and 1)
-  const int lay = conv_pooled_layout(pool != 0, node_kind, nleaf, km, C, H, W, Ho, Wo,
-                                     2 * pad + 1, N);
-  const bool quad = lay == kLayoutQuad, pair = lay == kLayoutPair;
-  const ConvGeom g = quad ? conv_geom_quad(C, Ho, Wo, 2 * pad + 1)
-                          : (pair ? conv_geom_pair(C, Ho, Wo, 2 * pad + 1)
-                                  : conv_geom(C, H, W, pad, pool != 0, phase, Ho, Wo));
-  const int R = (int)slg_conv_soft_record_floats(node_kind, depth, arity, K, pool);
-  hipLaunchKernelGGL(conv_soft_records_kernel, dim3((unsigned)cdiv(N * R, 256)), dim3(256), 0,
-                     as_stream(stream), conn, cm, ch, cw, (int)N, nleaf, K, km,
-                     quad ? 1 : (pair ? 2 : (phase ? 4 : 1)), node_kind, arity, raw, (int)C,
-                     2 * pad + 1, g, R,
-                     rec);
-  SLG_LAUNCH_CHECK("conv_soft_records");
-  return 0;
+  return conv_records_launch<false>(conn, cm, ch, cw, N, K, node_kind, depth, arity, raw, C, H, W,
+                                    pad, pool, rec, stream);
+}
+
+int slg_conv_soft_records_arrays(const float* node_param, const float* w, const int32_t* cm,
+                                 const int32_t* ch, const int32_t* cw, int64_t N, int32_t K,
+                                 int32_t node_kind, int32_t depth, int32_t arity, int64_t C,
+                                 int64_t H, int64_t W, int32_t pad, int32_t pool, float* rec,
+                                 slg_stream_t stream) {
+  SLG_REQUIRE(node_kind == SLG_NODE_GATE16 || node_kind == SLG_NODE_MULTILINEAR2 ||
+                  node_kind == SLG_NODE_HYBRID,
+              SLG_E_ARG, "conv_soft_records_arrays: node_kind %d", node_kind);
+  return conv_records_launch<true>(w, cm, ch, cw, N, K, node_kind, depth, arity, node_param, C,
+                                   H, W, pad, pool, rec, stream);
 }
 
 int slg_conv_soft_fwd_records(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,

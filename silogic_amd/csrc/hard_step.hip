@@ -8,10 +8,14 @@ extern "C" {
 
 int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
                   slg_stream_t stream) {
-  SLG_REQUIRE(step && x && logits, SLG_E_ARG, "hard_step: null pointer");
+  SLG_REQUIRE(step, SLG_E_ARG, "hard_step: null pointer");
   const slg_hard_step_t& s = *step;
-  SLG_REQUIRE(s.n_conv >= 0 && s.n_conv <= SLG_STEP_MAX_CONV && s.pack >= 0 && s.pack <= 2,
-              SLG_E_ARG, "hard_step: pack %d, %d conv blocks", s.pack, s.n_conv);
+  SLG_REQUIRE(s.n_conv >= 0 && s.n_conv <= SLG_STEP_MAX_CONV && s.pack >= 0 && s.pack <= 2 &&
+                  s.B >= 0,
+              SLG_E_ARG, "hard_step: pack %d, %d conv blocks, B %lld", s.pack, s.n_conv,
+              (long long)s.B);
+  if (s.B == 0) return 0;  // an empty batch: no launch (x and logits may be null)
+  SLG_REQUIRE(x && logits, SLG_E_ARG, "hard_step: null pointer");
   int rc = 0;
   if (s.pack == 1) {
     rc = slg_pack_image_wm(x, s.dtype, s.B, s.C, s.H, s.W, s.pack_pad, s.packed, stream);

@@ -820,6 +820,19 @@ def _conv_soft_launch(x, npar, w, cm, ch, cw, node_kind, depth, arity, K, pad, p
     Hf, Wf = H + 2 * pad - kern + 1, W + 2 * pad - kern + 1
     Ho, Wo = (Hf // 2, Wf // 2) if pool else (Hf, Wf)
     out = torch.empty((B, N, Ho, Wo), device=x.device, dtype=torch.float32)
+    if B > 0 and node_kind in (GATE16, MULTILINEAR2, HYBRID) and \
+            conv_fits_lds((Cc, H, W), pad, pool, node_kind, depth, arity, K):
+        # records built from these arrays, then the records kernels: the same
+        # bits as slg_conv_soft_fwd, with the per-channel parameter work done
+        # once per channel instead of once per workgroup and chunk
+        R = _lib.lib().slg_conv_soft_record_floats(node_kind, depth, arity, K, int(bool(pool)))
+        rec = torch.empty((N, R), device=x.device, dtype=torch.float32)
+        st = _stream(x)
+        _lib.call("slg_conv_soft_records_arrays", _p(npar), _p(w), _p(cm), _p(ch), _p(cw), N, K,
+                  node_kind, depth, arity, Cc, H, W, pad, int(bool(pool)), _p(rec), st)
+        _lib.call("slg_conv_soft_fwd_records", _p(x), B, Cc, H, W, N, node_kind, depth, arity, K,
+                  _p(rec), pad, int(bool(pool)), _p(out), st)
+        return out
     _lib.call("slg_conv_soft_fwd", _p(x), B, Cc, H, W, N, node_kind, depth, arity, K, _p(npar),
               _p(w), _p(cm), _p(ch), _p(cw), pad, int(bool(pool)), _p(out), _stream(x))
     return out

@@ -125,6 +125,10 @@ def test_hard_step_descriptor_layout_matches_the_header(tmp_path):
     step = _lib.HardStep()
     assert L.slg_hard_step(None, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
     assert b"null" in L.slg_last_error()
+    step.B = 5
+    assert L.slg_hard_step(ctypes.byref(step), None, ctypes.c_void_p(16), None) == -1
+    step.B = 0                        # an empty batch launches nothing
+    assert L.slg_hard_step(ctypes.byref(step), None, None, None) == 0
     step.n_conv = _lib.STEP_MAX_CONV + 1
     assert L.slg_hard_step(ctypes.byref(step), ctypes.c_void_p(16), ctypes.c_void_p(16),
                            None) == -1
