@@ -279,7 +279,13 @@ constexpr int kQuadThreads = kQuadThreadsC;
 // a read is on a bank of one parity). Each lane keeps its order for every
 // leaf and tap, and the pooled output is the maximum over the four
 // positions, so the result is the same.
-template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD, bool SWAP = false>
+//
+// RSC (pooled row-major layout only): the row stride g.RS as a compile-time
+// constant (0: read from g), so that a window's second row is an immediate
+// offset of the first row's LDS read and each tap takes one address add (two
+// with SWAP) instead of two (four).
+template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD, bool SWAP = false,
+          int RSC = 0>
 __global__ void __launch_bounds__((conv_soft_threads<NODE, NLEAF, KM, POOL, REC, QUAD>()))
 conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N, int K, int kernel,
                  int pad, ConvGeom g, const float* __restrict__ np, const float* __restrict__ wts,
@@ -434,11 +440,11 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
                                       : 2 * (int)__umul24(row, g.RS) + 2 * col);
       const float* base = lds + (active ? __umul24(s, g.SST) + bofs : 0);
       static_assert(!SWAP || (POOL && !PHASE && !QUAD), "SWAP is for the pooled row-major layout");
+      static_assert(RSC == 0 || (POOL && !PHASE && !QUAD), "RSC is for the pooled row-major layout");
+      const int RS = RSC > 0 ? RSC : g.RS;
       const int sw = SWAP ? (col & 1) : 0;
       const float* bq0 = base + sw;
       const float* bq1 = base + 1 - sw;
-      const float* bq2 = base + g.RS + sw;
-      const float* bq3 = base + g.RS + 1 - sw;
 
       // Tap k of every leaf per step: the guard k < K is uniform, and one
       // step issues all NLEAF * NQ LDS reads before its first wait. With
@@ -462,17 +468,19 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
             for (int qq = 0; qq < 4; ++qq) t[l][qq] = base[Pc.off[l][k][qq]];
           } else if constexpr (SWAP) {
             const int o = Pc.off[l][k][0];
-            t[l][0] = bq0[o];
-            t[l][1] = bq1[o];
-            t[l][2] = bq2[o];
-            t[l][3] = bq3[o];
+            const float* ta = bq0 + o;
+            const float* tb = bq1 + o;
+            t[l][0] = ta[0];
+            t[l][1] = tb[0];
+            t[l][2] = ta[RS];
+            t[l][3] = tb[RS];
           } else {
             const float* t0 = base + Pc.off[l][k][0];
             t[l][0] = t0[0];
             if constexpr (POOL) {
               t[l][1] = t0[1];
-              t[l][2] = t0[g.RS];
-              t[l][3] = t0[g.RS + 1];
+              t[l][2] = t0[RS];
+              t[l][3] = t0[RS + 1];
             }
           }
         }
@@ -1473,11 +1481,14 @@ static int pooled_read_cycles(const ConvGeom& g, int Wo, bool swap) {
   return total;
 }
 
-// The swapped order where the model halves the reads' cycles from at least
-// 6 per read (a VALU add more per read: worth it where the reads stall).
-static bool conv_swap_pays(const ConvGeom& g, int Wo) {
+// The swapped order where the model halves the reads' cycles: from at least
+// 6 per read with a runtime row stride (two VALU adds more per tap: worth it
+// where the reads stall), from any count with a constant one (`cheap`: one
+// add more per tap; config 5 block 0, 2 -> 1 modelled cycles per read:
+// 196 -> 174 us).
+static bool conv_swap_pays(const ConvGeom& g, int Wo, bool cheap) {
   const int plain = pooled_read_cycles(g, Wo, false), swapped = pooled_read_cycles(g, Wo, true);
-  return plain >= 24 && 2 * swapped <= plain;
+  return (cheap || plain >= 24) && 2 * swapped <= plain;
 }
 
 template <int NODE, int NLEAF, bool POOL, int KM, bool REC, bool QUAD>
@@ -1526,7 +1537,17 @@ static int launch_conv_soft_k(const ConvSoftArgs& a, hipStream_t st) {
   }
   auto kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD>;
   if constexpr (POOL && !Cfg::PHASE && !QUAD) {
-    if (conv_swap_pays(g, (int)a.Wo)) kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, true>;
+    // LUT trees of 5-6 leaves (VALU-bound): the row strides of 16- and
+    // 32-wide images with 'same' padding 1 as constants
+    constexpr bool kRsc = NODE == SLG_NODE_MULTILINEAR2 && NLEAF >= 5 && KM == 4;
+    const bool swap = conv_swap_pays(g, (int)a.Wo, kRsc && (g.RS == 17 || g.RS == 33));
+    if (swap) kern = conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, true>;
+    if constexpr (kRsc) {
+      if (g.RS == 17) kern = swap ? conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, true, 17>
+                                  : conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, false, 17>;
+      if (g.RS == 33) kern = swap ? conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, true, 33>
+                                  : conv_soft_kernel<NODE, NLEAF, POOL, KM, REC, QUAD, false, 33>;
+    }
   }
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,

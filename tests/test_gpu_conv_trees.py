@@ -157,6 +157,26 @@ def test_pair_layout(node, arity, depth, K, C, H, N, B):
             _close(got, ref, f"{node} a{arity} d{depth} K{K} {what}")
 
 
+@pytest.mark.parametrize("H,W", [(4, 16), (2, 32), (32, 16), (16, 32)])
+def test_lut6_constant_row_stride(H, W):
+    """LUT6 trees on 16- and 32-wide maps run with the row stride as a
+    compile-time constant, with and without the swapped window read (tiny
+    maps, whose chunks span samples, keep the plain order): records and
+    gradient-mode forwards against the oracle, non-square maps."""
+    C, N, B = 5, 12, 9
+    conv = sl.ConvLogicTree(C, N, kernel=3, tree_depth=1, connect="topk", k=4, n_chan=2,
+                            residual_init=False, seed=H + W, node="multilinear", arity=6)
+    sd = {k: v.clone() for k, v in conv.state_dict().items()}
+    x = torch.rand(B, C, H, W, generator=torch.Generator().manual_seed(W))
+    ref = torch_ref.orpool_soft(torch_ref.conv_soft(_blk(conv, H), sd, x))
+    conv = conv.to(DEV).eval()
+    with torch.no_grad():
+        y = conv.forward_pooled(x.to(DEV))
+    yg = conv.forward_pooled(x.to(DEV).requires_grad_(True)).detach()
+    _close(y, ref, f"LUT6 {H}x{W} records")
+    _close(yg, ref, f"LUT6 {H}x{W} arrays")
+
+
 @pytest.mark.parametrize("size", [1, 2, 3, 4])
 def test_orpool_any_size(size):
     x = torch.rand(3, 5, 11, 13, generator=torch.Generator().manual_seed(size))
