@@ -869,13 +869,19 @@ struct SoftArgs {
 };
 
 // Output chunks per sample tile: enough workgroups to fill the chip twice
-// over (at the LDS-limited occupancy), whole 64-output wave runs per chunk.
+// over (at the LDS-limited occupancy) where the tiles fill it less than once,
+// whole 64-output wave runs per chunk.
 static void soft_grid(const SoftArgs& a, int64_t* n_chunks_out, int64_t* chunk_out) {
   const int64_t tiles = cdiv(a.B, a.S);
   const size_t lds = (size_t)a.IN * a.S * sizeof(float);
   const int per_cu = (int)std::max<int64_t>(1, (int64_t)device_lds_bytes() / std::max<size_t>(lds, 1));
   const int64_t target = (int64_t)device_cus() * std::min(per_cu, 4) * 2;
   int64_t n_chunks = std::max<int64_t>(1, cdiv(target, tiles));
+  // tiles that fill every CU's resident workgroups once take the whole
+  // output range, so that the GroupSum head can be fused (config 5's head:
+  // 256 two-sample tiles, 20.2 us split in two chunks plus a GroupSum
+  // launch, 12.4 us fused)
+  if (tiles >= (int64_t)device_cus() * std::min(per_cu, 4)) n_chunks = 1;
   n_chunks = std::min<int64_t>(n_chunks, std::max<int64_t>(1, cdiv(a.OUT, 64)));
   const int64_t chunk = cdiv(cdiv(a.OUT, n_chunks), 64) * 64;
   *n_chunks_out = cdiv(a.OUT, chunk);
