@@ -378,8 +378,6 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
 
   const int P = Ho * Wo;
   const int nchunks = (ns * g.LPS + 63) / 64;
-  const float inv_lps = 1.0f / (float)g.LPS;
-  const float inv_col = 1.0f / (float)((PHASE || !POOL) ? g.RS : Wo);
   // Quad layout: a wave takes four channels at once, one per 16-lane LDS
   // conflict group of ds_read_b128 (lanes 0-3, 12-15, 20-27 / 4-11, 16-19,
   // 28-31, and the same in the upper half), each group walking 16
@@ -405,34 +403,32 @@ conv_soft_kernel(const float* __restrict__ x, int B, int C, int H, int W, int N,
 
   ConvParams<NODE, NLEAF, KM, NW> Pc;
   if (wave * CPW < N) load(Pc, wave * CPW);
-  // quad (one sample per workgroup): the lane's output (row, col) advances
-  // by LPC outputs per chunk, carried incrementally
-  const int d_row = QUAD ? LPC / Wo : 0, d_col = QUAD ? LPC - d_row * Wo : 0;
+  // the lane's output (sample, row, column) advances by LPC outputs per
+  // chunk, carried incrementally (no division per chunk): pooled row-major
+  // lanes walk rows of Wo columns, the others rows of RS columns (those >= Wo
+  // idle), LPS lanes per sample; the quad layout takes one sample
+  constexpr bool LINEAR = PHASE || !POOL;
+  const int WW = QUAD ? Wo : (LINEAR ? g.RS : Wo);
+  const int HH = QUAD ? (1 << 30) : g.LPS / WW;
+  const int l_s = QUAD ? 0 : rank / g.LPS, l_rem = QUAD ? rank : rank - l_s * g.LPS;
+  const int l_row = l_rem / WW, l_col = l_rem - (l_rem / WW) * WW;
+  const int d_s = QUAD ? 0 : LPC / g.LPS, d_rem = QUAD ? LPC : LPC - d_s * g.LPS;
+  const int d_row = d_rem / WW, d_col = d_rem - d_row * WW;
   for (int nb = wave * CPW; nb < N; nb += nwaves * CPW) {
     const int n = nb + cslot;  // this lane's channel
     float* out_n = out + ((int64_t)b0 * N + min(n, N - 1)) * P;  // quad: sample b0
-    int q_row = QUAD ? rank / Wo : 0, q_col = QUAD ? rank - (rank / Wo) * Wo : 0;
+    int q_s = l_s, q_row = l_row, q_col = l_col;
     for (int chunk = 0; chunk < nchunks_c; ++chunk) {
       const int q = chunk * LPC + rank;
-      bool active = q < ns * g.LPS && n < N;
-      // (sample, row, column) of the lane: pooled row-major lanes walk Wo
-      // columns, the others RS columns (those >= Wo idle). Idle lanes read
-      // at the start of the staged region.
-      constexpr bool LINEAR = PHASE || !POOL;
-      int s, row, col;
-      if constexpr (QUAD) {
-        s = 0;
-        row = q_row;
-        col = q_col;
-        q_col += d_col;
-        q_row += d_row;
-        if (q_col >= Wo) { q_col -= Wo; ++q_row; }
-      } else {
-        s = active ? div_small(q, g.LPS, inv_lps) : 0;
-        const int rem = active ? q - (int)__umul24(s, g.LPS) : 0;
-        row = div_small(rem, LINEAR ? g.RS : Wo, inv_col);
-        col = rem - (int)__umul24(row, LINEAR ? g.RS : Wo);
-      }
+      // idle lanes (past the workgroup's samples) read at the start of the
+      // staged region
+      const int s = q_s, row = q_row, col = q_col;
+      bool active = (QUAD ? q < ns * g.LPS : s < ns) && n < N;
+      q_col += d_col;
+      if (q_col >= WW) { q_col -= WW; ++q_row; }
+      q_row += d_row;
+      if (q_row >= HH) { q_row -= HH; ++q_s; }
+      q_s += d_s;
       active = active && col < Wo;
       const int p = (int)__umul24(row, Wo) + col;
       const int bofs = QUAD ? 4 * ((int)__umul24(row, g.BW) + col)
