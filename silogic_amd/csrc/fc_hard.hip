@@ -1338,10 +1338,12 @@ __global__ void __launch_bounds__(kPlaceThreads) fc_hard_place_kernel(PlaceNet n
 // the fewest repeated operand bank classes (word index mod 32, only for the
 // operands its gate reads: the highest count first, then the sum, then the
 // lowest group), among groups with a free slot (bins of up to 64 groups keep
-// their counts in registers, saturating at 3). Each wave places the outputs
-// of its own rows (the k-th wave of type T takes that type's ranks
-// [64 U k, 64 U (k + 1))), all waves at once; then four waves place the
-// generic bin, each every fourth output into every fourth group. Uniform
+// their counts in registers, saturating at 3). The outputs of a wave's own
+// rows (the k-th wave of type T takes that type's ranks [64 U k, 64 U
+// (k + 1))) are placed in two halves, the first 32 U into the groups of its
+// lanes 0-31 and the rest into those of lanes 32-63, all halves at once;
+// four more place the generic bin, each every fourth output into every
+// fourth group. Uniform
 // rows get codes (a << 16) | b with absolute word indices (the read buffer
 // of layer l starts at word (l & 1) * MAXO * 1024); generic rows get compact
 // codes on the renamed operands; unused slots get codes reading word 0 of
@@ -1436,8 +1438,8 @@ struct RegBin {
   int fill = 0;
   uint32_t a1 = 0, a2 = 0, a3 = 0, b1 = 0, b2 = 0, b3 = 0;
 
-  // group q of the bin: bin_group(generic, q, U, w0), or for a generic
-  // sub-bin of every gs-th group from go: U * 32 + q * gs + go
+  // group q of the bin: every gs-th group from go, bin_group(false, q * gs +
+  // go, U, w0) of a type bin or U * 32 + q * gs + go of the generic bin
   __device__ int place(bool generic, int G, int U, int w0, bool na, bool nb, int ca, int cb,
                        int lane, int gs = 1, int go = 0) {
     const uint32_t ba = 1u << ca, bb = 1u << cb;
@@ -1454,7 +1456,7 @@ struct RegBin {
       if (na) { a3 |= a2 & ba; a2 |= a1 & ba; a1 |= ba; }
       if (nb) { b3 |= b2 & bb; b2 |= b1 & bb; b1 |= bb; }
     }
-    return (generic ? U * 32 + q * gs + go : bin_group(false, q, U, w0)) * 32 + f;
+    return (generic ? U * 32 + q * gs + go : bin_group(false, q * gs + go, U, w0)) * 32 + f;
   }
 };
 
@@ -1484,23 +1486,64 @@ enum { kMetaU = 0, kMetaRows = 1, kMetaNGen = 2, kMetaM = 3, kMetaW0 = 19, kMeta
 // order, and the generic outputs in index order.
 __global__ void __launch_bounds__(kPlaceThreads)
 fc_hard_type_plan_kernel(TypePlaceNet n, TypePlaceScratch ws, int l) {
-  __shared__ uint16_t info[kPlaceMax];   // as ws.info, read back here from LDS
-  __shared__ uint8_t generic[kPlaceMax];
+  // as ws.info (classes and type in bits 0-13), read back here from LDS; bit
+  // 14 marks the generic outputs
+  __shared__ uint16_t info[kPlaceMax];
   __shared__ int hist[16], m[16], w0[16], wtt[16], tstart[16];
   __shared__ int plan_u;
+  __shared__ int ccount[kPlaceMax / 64][16];   // per chunk and type: count, then prefix
+  __shared__ int gcount[kPlaceMax / 64];       // per chunk: generic count, then prefix
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int maxo = n.maxo, W = n.W[l];
   if (tid < 16) hist[tid] = 0;
   for (int i = tid; i < kTypeMaxGroups; i += kPlaceThreads) ws.fill[i] = 0;
   __syncthreads();
-  for (int o = tid; o < W; o += kPlaceThreads) {
-    uint32_t a, b, tt;
-    type_operands(n, l, o, a, b, tt);
-    const uint32_t v = (a & 31u) | ((b & 31u) << 5) | (tt << 10);
-    info[o] = (uint16_t)v;
-    ws.info[o] = v;
-    atomicAdd(&hist[tt], 1);
+  // every output's code, then the renaming of its operands, loaded with all
+  // of a thread's outputs in flight (two memory round trips, not two per
+  // output); the type histogram by wave ballots (lane T of a wave counts
+  // type T), one LDS add per type and wave
+  constexpr int PER = kPlaceMax / kPlaceThreads;
+  uint32_t cv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int o = tid + i * kPlaceThreads;
+    cv[i] = o < W ? n.in[l][o] : 0u;
   }
+  uint32_t av[PER], bv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    av[i] = (cv[i] >> 14) & 0x3FFFu;
+    bv[i] = cv[i] & 0x3FFFu;
+  }
+  if (l > 0) {   // the prep clamps operands below the input width; kept in range here too
+    const uint32_t lim = (uint32_t)n.W[l - 1] - 1u;
+    const int32_t* pm = n.perm[l - 1];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (tid + i * kPlaceThreads < W) {
+        av[i] = (uint32_t)pm[min(av[i], lim)];
+        bv[i] = (uint32_t)pm[min(bv[i], lim)];
+      }
+    }
+  }
+  int my_count = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int o = tid + i * kPlaceThreads;
+    uint32_t tt = 16u;  // past the layer: no type
+    if (o < W) {
+      tt = cv[i] >> 28;
+      const uint32_t v = (av[i] & 31u) | ((bv[i] & 31u) << 5) | (tt << 10);
+      info[o] = (uint16_t)v;
+      ws.info[o] = v;
+    }
+#pragma unroll
+    for (int T = 0; T < 16; ++T) {
+      const int c = (int)__popcll(__ballot(tt == (uint32_t)T));
+      if (lane == T) my_count += c;
+    }
+  }
+  if (lane < 16 && my_count) atomicAdd(&hist[lane], my_count);
   __syncthreads();
   if (tid == 0) {
     int U = 0, rows = (W + kNetThreads - 1) / kNetThreads;
@@ -1553,60 +1596,127 @@ fc_hard_type_plan_kernel(TypePlaceNet n, TypePlaceScratch ws, int l) {
   }
   __syncthreads();
   const int U = plan_u;
-  // ranks within each type (wave T scans type T in index order, one ballot
-  // prefix per 64 outputs): ranks below the type's waves' capacity go to
-  // the type's list in rank order, the rest are generic
-  {
-    const int T = wave, cap = 64 * U * m[T];
-    int base = 0;
-    for (int o0 = 0; o0 < W; o0 += 64) {
-      const int o = o0 + lane;
-      const bool mine = o < W && (info[o] >> 10) == (uint32_t)T;
-      const uint64_t mk = __ballot(mine);
-      const int r = base + (int)__popcll(mk & ((1ull << lane) - 1ull));
-      if (mine) {
-        if (r < cap) ws.olist[tstart[T] + r] = o;
-        generic[o] = r >= cap ? 1 : 0;
-      }
-      base += (int)__popcll(mk);
+  // ranks within each type and the generic outputs, from per-chunk counts:
+  // chunk c = outputs [64c, 64c + 64); each type's outputs of rank below its
+  // waves' capacity go to the type's list in rank order, the rest (and the
+  // types without a wave) are generic, listed in index order
+  const int nch = (W + 63) >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int c = wave; c < nch; c += kPlaceThreads / 64) {
+    const int o = c * 64 + lane;
+    const uint32_t t = o < W ? (uint32_t)(info[o] >> 10) : 16u;
+#pragma unroll
+    for (int T = 0; T < 16; ++T) {
+      const int k = (int)__popcll(__ballot(t == (uint32_t)T));
+      if (lane == T) ccount[c][T] = k;
     }
   }
   __syncthreads();
-  // the generic outputs in index order (wave 0)
-  if (wave == 0) {
-    int gbase = 0;
-    for (int o0 = 0; o0 < W; o0 += 64) {
-      const int o = o0 + lane;
-      const bool left = o < W && generic[o];
-      const uint64_t ml = __ballot(left);
-      if (left) ws.glist[gbase + (int)__popcll(ml & ((1ull << lane) - 1ull))] = o;
-      gbase += (int)__popcll(ml);
+  // exclusive prefix over the chunks, per type: wave T scans type T, lane j
+  // holding chunks [4j, 4j + 4)
+  if (wave < 16) {
+    const int T = wave;
+    int v4[4], sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = 4 * lane + u;
+      v4[u] = c < nch ? ccount[c][T] : 0;
+      sum += v4[u];
     }
-    if (lane == 0) ws.meta[kMetaNGen] = gbase;
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d);
+      if (lane >= d) incl += y;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = 4 * lane + u;
+      if (c < nch) ccount[c][T] = run;
+      run += v4[u];
+    }
+  }
+  __syncthreads();
+  for (int c = wave; c < nch; c += kPlaceThreads / 64) {
+    const int o = c * 64 + lane;
+    const uint32_t t = o < W ? (uint32_t)(info[o] >> 10) : 16u;
+    int r = 0;
+#pragma unroll
+    for (int T = 0; T < 16; ++T) {
+      const uint64_t mk = __ballot(t == (uint32_t)T);
+      if (t == (uint32_t)T) r = ccount[c][T] + (int)__popcll(mk & below);
+    }
+    bool gen = false;
+    if (o < W) {
+      const int cap = 64 * U * m[t];
+      if (r < cap) ws.olist[tstart[t] + r] = o;
+      gen = r >= cap;
+    }
+    const int k = (int)__popcll(__ballot(gen));
+    if (lane == 0) gcount[c] = k;
+    if (o < W && gen) info[o] = (uint16_t)(info[o] | 0x4000u);
+  }
+  __syncthreads();
+  // the generic outputs in index order: a prefix over the chunks' counts
+  if (wave == 0) {
+    int v4[4], sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = 4 * lane + u;
+      v4[u] = c < nch ? gcount[c] : 0;
+      sum += v4[u];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d);
+      if (lane >= d) incl += y;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = 4 * lane + u;
+      if (c < nch) gcount[c] = run;
+      run += v4[u];
+    }
+    if (lane == 63) ws.meta[kMetaNGen] = incl;
+  }
+  __syncthreads();
+  for (int c = wave; c < nch; c += kPlaceThreads / 64) {
+    const int o = c * 64 + lane;
+    const bool left = o < W && (info[o] & 0x4000u);
+    const uint64_t ml = __ballot(left);
+    if (left) ws.glist[gcount[c] + (int)__popcll(ml & below)] = o;
   }
 }
 
-// The bins of layer l: workgroup w < 16 is wave w of the type-uniform rows
-// (the k-th wave of type T places that type's ranks [64 U k, 64 U (k + 1))
-// into its own 2 U groups), workgroups 16.. the generic sub-bins (up to 256
-// groups: sub-bin j takes the generic outputs of rank j, j + NS, ... into
-// groups j, j + NS, ...; larger bins: one workgroup places them all, with
-// the counts in LDS). Each places its outputs greedily in index order and
-// writes their slots and its groups' fill.
+// The bins of layer l: workgroups 2w and 2w + 1 (w < 16) are the two lane
+// halves of wave w of the type-uniform rows (the k-th wave of type T holds
+// that type's ranks [64 U k, 64 U (k + 1)); half h places the h-th 32 U of
+// them into the wave's U groups of lane half h), workgroups 32.. the
+// generic sub-bins (up to 256 groups: sub-bin j takes the generic outputs of
+// rank j, j + NS, ... into groups j, j + NS, ...; larger bins: one workgroup
+// places them all, with the counts in LDS). Each places its outputs
+// greedily in index order and writes their slots and its groups' fill.
 __global__ void __launch_bounds__(64) fc_hard_type_bins_kernel(TypePlaceNet n, TypePlaceScratch ws) {
   __shared__ uint8_t cnt[kTypeMaxGroups][64];
   __shared__ int fill[kTypeMaxGroups];
   const int lane = threadIdx.x;
   const int U = ws.meta[kMetaU], rows = ws.meta[kMetaRows];
-  const int bin = blockIdx.x;
-  if (bin < 16) {
-    const int T = ws.meta[kMetaWtt + bin], k = bin - ws.meta[kMetaW0 + T];
+  if (blockIdx.x < 2 * 16) {
+    // half h of the type bin of wave w: the wave's groups of lane half h
+    // (one per row) and half of the bin's ranks, so that the two halves'
+    // greedy steps run side by side
+    const int w = blockIdx.x >> 1, h = blockIdx.x & 1;
+    const int T = ws.meta[kMetaWtt + w], k = w - ws.meta[kMetaW0 + T];
     const int mT = ws.meta[kMetaM + T];
     if (U == 0 || mT == 0 || k < 0 || k >= mT) return;
     // the type's list holds its first min(count, 64 U m) outputs by rank:
-    // this bin takes ranks [lo, hi) of them
+    // this wave's bin takes ranks [64 U k, 64 U (k + 1)) of them, and half
+    // h the h-th 32 U of those
     const int start = ws.meta[kMetaTStart + T], count = ws.meta[kMetaTCount + T];
-    const int lo = 64 * U * k, hi = min(lo + 64 * U, count), G = 2 * U;
+    const int lo = 64 * U * k + 32 * U * h, hi = min(lo + 32 * U, count), G = U;
     const bool na = tt_needs_a(T), nb = tt_needs_b(T);
     RegBin rb;
     for (int r0 = lo; r0 < hi; r0 += 64) {
@@ -1621,16 +1731,16 @@ __global__ void __launch_bounds__(64) fc_hard_type_bins_kernel(TypePlaceNet n, T
         const int ca = __builtin_amdgcn_readlane((int)(in & 31u), src);
         const int cb = __builtin_amdgcn_readlane((int)((in >> 5) & 31u), src);
         const int oo = __builtin_amdgcn_readlane(o, src);
-        const int sl = rb.place(false, G, U, bin, na, nb, ca, cb, lane);
+        const int sl = rb.place(false, G, U, w, na, nb, ca, cb, lane, 2, h);
         if (lane == 0) ws.slot[oo] = sl;
       }
     }
-    if (lane < G) ws.fill[bin_group(false, lane, U, bin)] = rb.fill;
+    if (lane < G) ws.fill[bin_group(false, 2 * lane + h, U, w)] = rb.fill;
     return;
   }
   const int G = 32 * (rows - U);
   const int NS = G <= 256 ? 4 : 1;
-  const int j = bin - 16;
+  const int j = blockIdx.x - 2 * 16;
   if (j >= NS || G == 0) return;
   const int Gs = G / NS;
   const bool regs = Gs <= 64;
@@ -2019,7 +2129,7 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
   const int S_i = (int)S;
   for (int l = 0; l + 1 < n_layers; ++l) {
     hipLaunchKernelGGL(fc_hard_type_plan_kernel, dim3(1), dim3(kPlaceThreads), 0, st, n, ws, l);
-    hipLaunchKernelGGL(fc_hard_type_bins_kernel, dim3(16 + 4), dim3(64), 0, st, n, ws);
+    hipLaunchKernelGGL(fc_hard_type_bins_kernel, dim3(2 * 16 + 4), dim3(64), 0, st, n, ws);
     hipLaunchKernelGGL(fc_hard_type_codes_kernel, dim3((unsigned)cdiv(std::max(S_i, n.W[l]), 256)),
                        dim3(256), 0, st, n, ws, l);
   }
