@@ -494,7 +494,11 @@ def hard_launches(cfg, model, x_hard):
             cus = torch.cuda.get_device_properties(x_hard.device).multi_processor_count
             if a[1] in (0, 1):       # rows: packing inside
                 nbytes = B * in_dim * isz + B * C * 4 + codes
-                kname = f"fc_hard_net_rows_kernel (packing + {len(widths)} layers + GroupSum)"
+                if in_dim <= 1024 and ops.fc_hard_net_supported(in_dim, widths, C) == 64:
+                    kname = f"fc_hard_net_rows_kernel (packing + {len(widths)} layers + GroupSum)"
+                else:                # a tile per workgroup, packed in LDS
+                    kname = (f"fc_hard_net_packed_kernel (packing per tile + {len(widths)} "
+                             "layers + GroupSum)")
             elif len(widths) == 1 and 2 * nw < cus and widths[0] // C <= 8192:
                 # one layer, few words: a workgroup per (word, class)
                 nbytes = in_dim * nw * 8 + B * C * 4 + codes

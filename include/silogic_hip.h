@@ -331,9 +331,11 @@ int slg_fc_hard_layer(const uint64_t* xin, int64_t IN, int64_t nw,
  * models.py:99-101, with GroupSum.forward_hard, heads.py:41-45). codes[l]
  * are compact 4-byte codes [width_l] from slg_fc_hard_prep_net(compact = 1);
  * operand indices are clamped to the layer's input width. Input x:
- * in_kind 0 = fp32 rows [B,IN0], 1 = uint8 rows [B,IN0] (packed on the fly,
- * bit = uint8(x) != 0; needs IN0 <= 1024 and 64-sample tiles), 2 = packed
- * [IN0, ceil(B/64)] uint64, 3 = packed word-major [ceil(B/64), IN0]. It runs
+ * in_kind 0 = fp32 rows [B,IN0] (bit = x >= 1), 1 = uint8 rows [B,IN0]
+ * (bit = x != 0), both packed inside the launch (streamed per persistent
+ * workgroup for IN0 <= 1024 with 64-sample tiles, else packed per tile in
+ * LDS), 2 = packed [IN0, ceil(B/64)] uint64, 3 = packed word-major
+ * [ceil(B/64), IN0]. It runs
  * n_layers arity-2 layers whose widths and device code arrays are given
  * by the host arrays widths[n_layers] and codes[n_layers], then writes logits [B,C] fp32 = per-class popcounts of
  * the last layer (no tau). One workgroup keeps a 64-sample (or, for wide
@@ -394,9 +396,8 @@ int slg_fc_hard_type_place_net(int32_t n_layers, int64_t IN0, const int64_t* wid
                                slg_stream_t stream);
 /* slg_fc_hard_net (no wire residual) on the placed codes and plan of
  * slg_fc_hard_type_place_net; widths are the layers' widths, as given to the
- * placement. Unpacked rows (in_kind 0 or 1) need IN0 <= 1024 and 64-sample
- * tiles (slg_fc_hard_net_supported() == 64); packed input (2 or 3) takes
- * either. Same logits, bit for bit. A plan placed for another IN0 (hence
+ * placement; every input kind of slg_fc_hard_net. Same logits, bit for
+ * bit. A plan placed for another IN0 (hence
  * another slot count) is detected on the device from its own record: the
  * logits are then NaN. No counterpart in the reference beyond
  * slg_fc_hard_net's. */

@@ -6,6 +6,8 @@
 // words is three bit-field-inserts per 32-bit half:
 //   out = bfi(a, bfi(b, T3, T2), bfi(b, T1, T0)),  T_g = tt bit g ? ~0 : 0,
 // so one output word costs the same whatever the gate, with no branching.
+#include <type_traits>
+
 #include "pack_cols.h"
 #include "slg_common.h"
 
@@ -666,7 +668,7 @@ __device__ __forceinline__ void csa(uint32_t& h, uint32_t& l, uint32_t a, uint32
   l = xor3(a, b, c);
 }
 
-constexpr int kGsChunk = 1024;  // words of a class per pass
+constexpr int kGsSlices = 12;   // bit slices of a lane's counts (at most 2048)
 
 // Harley-Seal step over 16 words: ones..eights carry across calls, the
 // 16s word of this block is returned.
@@ -694,7 +696,7 @@ __device__ __forceinline__ uint32_t hs16(uint32_t& ones, uint32_t& twos, uint32_
 // Bit-sliced add x += y of NB-bit counts (x[NB] is 0 on entry and takes the
 // carry out): a ripple of full adders, slice by slice.
 template <int NB>
-__device__ __forceinline__ void add_slices(uint32_t (&x)[11], const uint32_t (&y)[11]) {
+__device__ __forceinline__ void add_slices(uint32_t (&x)[kGsSlices], const uint32_t (&y)[kGsSlices]) {
   uint32_t carry = 0;
 #pragma unroll
   for (int k = 0; k < NB; ++k) {
@@ -710,8 +712,8 @@ __device__ __forceinline__ void add_slices(uint32_t (&x)[11], const uint32_t (&y
 // 8 with 7 - i: joins the two quads' totals) and row_mirror (i of 16 with
 // 15 - i: joins the two 8-lane totals).
 template <int NB, int CTRL>
-__device__ __forceinline__ void add_dpp(uint32_t (&x)[11]) {
-  uint32_t y[11];
+__device__ __forceinline__ void add_dpp(uint32_t (&x)[kGsSlices]) {
+  uint32_t y[kGsSlices];
 #pragma unroll
   for (int k = 0; k < NB; ++k) y[k] = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[k], CTRL, 0xF, 0xF, false);
   add_slices<NB>(x, y);
@@ -721,8 +723,8 @@ __device__ __forceinline__ void add_dpp(uint32_t (&x)[11]) {
 // value with itself returns, in every lane, the lane's own value and that of
 // lane ^ 16 (^ 32) as the pair (a, b), so the sum is a + b.
 template <int NB, bool P32>
-__device__ __forceinline__ void add_swap(uint32_t (&x)[11]) {
-  uint32_t a[11], b[11];
+__device__ __forceinline__ void add_swap(uint32_t (&x)[kGsSlices]) {
+  uint32_t a[kGsSlices], b[kGsSlices];
 #pragma unroll
   for (int k = 0; k < NB; ++k) {
     if constexpr (P32) {
@@ -743,15 +745,21 @@ __device__ __forceinline__ void add_swap(uint32_t (&x)[11]) {
 
 // Class total of this lane's sample over the class's G words `cls32`
 // (32-bit halves, NH per word): sample lane for NH == 2, lane & 31 for
-// NH == 1.
-template <int NH>
+// NH == 1. A pass takes WPL words per lane: 32 for 64-bit words (1024 words
+// per pass); 16 or 32 for 32-bit words (1024 or 2048 words per pass: one
+// butterfly for classes of up to 2048 words, where 1024-word passes would
+// take two).
+template <int NH, int WPL1 = 16>
 __device__ __forceinline__ int class_count(const uint32_t* cls32, int G, int lane) {
-  constexpr int WPL = NH == 2 ? 32 : 16;                 // words per lane per chunk
+  constexpr int WPL = NH == 2 ? 32 : WPL1;               // words per lane per pass
   constexpr int LSTRIDE = NH == 2 ? 32 : 64;             // word stride between them
+  constexpr int CHUNK = WPL * LSTRIDE;                   // words per pass
+  constexpr int NBITS = (NH == 1 && WPL == 32) ? 12 : 11;  // slices of the pass's total
+  static_assert(WPL == 16 || WPL == 32, "16 or 32 words per lane");
   const int l = NH == 2 ? (lane & 31) : lane;
   const int h = NH == 2 ? (lane >> 5) : 0;
   int total = 0;
-  for (int q0 = 0; q0 < G; q0 += kGsChunk) {
+  for (int q0 = 0; q0 < G; q0 += CHUNK) {
     // rows of the pass wholly inside the class load without a lane guard
     // (a wave-uniform test); only the class's last partial row is guarded
     const int nvalid = G - q0;
@@ -764,20 +772,22 @@ __device__ __forceinline__ int class_count(const uint32_t* cls32, int G, int lan
       else w[j] = j * LSTRIDE + l < nvalid ? p[j * LSTRIDE * NH] : 0u;
     }
     reads_end();
-    uint32_t x[11];
+    uint32_t x[kGsSlices];
 #pragma unroll
-    for (int k = 0; k < 11; ++k) x[k] = 0;
-    if constexpr (NH == 2) {
+    for (int k = 0; k < kGsSlices; ++k) x[k] = 0;
+    if constexpr (WPL == 32) {
       const uint32_t s16a = hs16(x[0], x[1], x[2], x[3], w);
       const uint32_t s16b = hs16(x[0], x[1], x[2], x[3], w + 16);
       x[4] = s16a ^ s16b;
       x[5] = s16a & s16b;
-      // 6 bits (<= 32) grow one bit per round to 11 (<= 1024)
+      // 6 bits (<= 32) grow one bit per round: 11 (<= 1024) after five
+      // rounds inside each 32-lane group, 12 (<= 2048) after the sixth
       add_dpp<6, 0xB1>(x);    // quad_perm [1,0,3,2]
       add_dpp<7, 0x4E>(x);    // quad_perm [2,3,0,1]
       add_dpp<8, 0x141>(x);   // row_half_mirror
       add_dpp<9, 0x140>(x);   // row_mirror
       add_swap<10, false>(x);  // lane ^ 16
+      if constexpr (NH == 1) add_swap<11, true>(x);  // lane ^ 32
     } else {
       x[4] = hs16(x[0], x[1], x[2], x[3], w);
       add_dpp<5, 0xB1>(x);
@@ -790,7 +800,7 @@ __device__ __forceinline__ int class_count(const uint32_t* cls32, int G, int lan
     const int sh = lane & 31;
     int cnt = 0;
 #pragma unroll
-    for (int k = 0; k < 11; ++k) cnt |= (int)((x[k] >> sh) & 1u) << k;
+    for (int k = 0; k < NBITS; ++k) cnt |= (int)((x[k] >> sh) & 1u) << k;
     total += cnt;
   }
   return total;
@@ -806,7 +816,9 @@ __device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int b
   const int nwaves = kNetThreads >> 6;
   const int G = W / C;
   for (int c = wave; c < C; c += nwaves) {
-    const int n = class_count<NH>(reinterpret_cast<const uint32_t*>(cur + c * G), G, lane);
+    const uint32_t* cls = reinterpret_cast<const uint32_t*>(cur + c * G);
+    const int n = (NH == 1 && G > 1024) ? class_count<NH, 32>(cls, G, lane)
+                                        : class_count<NH>(cls, G, lane);
     const int b = b0 + lane;
     if (lane < SPW && b < B) logits[(int64_t)b * C + c] = (float)n;
   }
@@ -878,10 +890,98 @@ static int launch_head(const uint64_t* xp, int in_kind, int64_t B, int64_t IN0, 
   return 0;
 }
 
-// Pre-packed input: LAYOUT 0 = [in0][nw] (reference layout), 1 = [nw][in0].
+// A row element's bit: x >= 1 for fp32, x != 0 for bytes.
+template <typename IT>
+__device__ inline bool input_bit(IT v) {
+  if constexpr (sizeof(IT) == 1) return v != 0;
+  else return v >= (IT)1;
+}
+
+// One element of a row through a buffer resource (offsets past it read 0).
+template <typename IT>
+__device__ inline IT load_row(__amdgpu_buffer_rsrc_t r, int voff) {
+  if constexpr (sizeof(IT) == 1) return (IT)__builtin_amdgcn_raw_buffer_load_b8(r, voff, 0, 0);
+  else return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+
+// The tile's rows [B][in0] (fp32: bit = x >= 1; bytes: bit = x != 0) packed
+// into LDS words, sample b0 + s at bit s: thread t builds the words of
+// features 4t + 4096k from 4-feature vectors (16 bytes of fp32, 4 bytes of
+// uint8; in0 % 4 == 0 and an aligned row pointer), else of features
+// t + 1024k one at a time, RB rows in flight. The rows are read through a
+// buffer resource spanning the tile's samples that exist: rows past it
+// read 0, bit 0, with no clamp or branch.
+template <typename IT, typename WT>
+__device__ __forceinline__ void rows_to_lds(WT* lds, const IT* __restrict__ x, int B, int in0,
+                                            int b0) {
+  constexpr int SPW = (int)sizeof(WT) * 8;
+  constexpr int RB = 16;
+  const int nr = max(0, min(SPW, B - b0));
+  const int rowb = in0 * (int)sizeof(IT);
+  const __amdgpu_buffer_rsrc_t r =
+      uniform_rsrc(x + (int64_t)min(b0, B) * in0, nr * rowb);
+  const bool vec = in0 % 4 == 0 && (uintptr_t)x % (4 * sizeof(IT)) == 0;
+  if (vec) {
+    for (int f = threadIdx.x * 4; f < in0; f += 4 * kNetThreads) {
+      WT w[4] = {0, 0, 0, 0};
+      const int v0 = f * (int)sizeof(IT);
+#pragma unroll
+      for (int c = 0; c < SPW; c += RB) {
+        uint32_t m[4] = {0u, 0u, 0u, 0u};
+        if constexpr (sizeof(IT) == 4) {
+          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+          u32x4 q[RB];
+#pragma unroll
+          for (int i = 0; i < RB; ++i)
+            q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, v0 + (c + i) * rowb, 0, 0));
+#pragma unroll
+          for (int i = RB - 1; i >= 0; --i) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              m[v] = (m[v] << 1) | (__uint_as_float(q[i][v]) >= 1.0f ? 1u : 0u);
+          }
+        } else {
+          uint32_t q[RB];
+#pragma unroll
+          for (int i = 0; i < RB; ++i) q[i] = __builtin_amdgcn_raw_buffer_load_b32(r, v0 + (c + i) * rowb, 0, 0);
+#pragma unroll
+          for (int i = RB - 1; i >= 0; --i) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) m[v] = (m[v] << 1) | (((q[i] >> (8 * v)) & 0xFFu) ? 1u : 0u);
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) w[v] |= (WT)m[v] << c;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) lds[f + v] = w[v];
+    }
+  } else {
+    for (int f = threadIdx.x; f < in0; f += kNetThreads) {
+      WT w = 0;
+      const int v0 = f * (int)sizeof(IT);
+#pragma unroll
+      for (int c = 0; c < SPW; c += RB) {
+        IT q[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) q[i] = load_row<IT>(r, v0 + (c + i) * rowb);
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = RB - 1; i >= 0; --i) m = (m << 1) | (input_bit(q[i]) ? 1u : 0u);
+        w |= (WT)m << c;
+      }
+      lds[f] = w;
+    }
+  }
+}
+
+// Input: LAYOUT 0 = packed [in0][nw] (reference layout), 1 = packed
+// [nw][in0], 2 = fp32 rows [B][in0], 3 = uint8 rows (packed per tile here,
+// for inputs the streaming rows kernel does not take: more than 1024
+// features or 32-sample tiles).
 template <int LAYOUT, typename WT, int MAXO, bool TYPED>
 __global__ void __launch_bounds__(kNetThreads)
-fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, int nw,
+fc_hard_net_packed_kernel(NetDesc desc, const void* __restrict__ xin, int B, int nw,
                           float* __restrict__ logits) {
   const_netdesc_t& d = *(const_netdesc_t*)__builtin_amdgcn_kernarg_segment_ptr();
   constexpr int SPW = (int)sizeof(WT) * 8;
@@ -897,11 +997,17 @@ fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, 
   uint32_t cb[MAXO];
   if constexpr (TYPED) load_codes_tm(cb, d.codes[0]);
   else load_codes(cb, d.codes[0], d.width[0]);
-  const int w64 = tile / (64 / SPW);
-  for (int i = threadIdx.x; i < d.in0; i += kNetThreads) {
-    const uint64_t word = LAYOUT == 0 ? xp[(int64_t)i * nw + w64] : xp[(int64_t)w64 * d.in0 + i];
-    if constexpr (SPW == 64) lds[i] = (WT)word;
-    else lds[i] = (WT)(word >> (32 * (tile & 1)));
+  if constexpr (LAYOUT >= 2) {
+    using IT = std::conditional_t<LAYOUT == 2, float, uint8_t>;
+    rows_to_lds<IT, WT>(lds, (const IT*)xin, B, d.in0, tile * SPW);
+  } else {
+    const uint64_t* xp = (const uint64_t*)xin;
+    const int w64 = tile / (64 / SPW);
+    for (int i = threadIdx.x; i < d.in0; i += kNetThreads) {
+      const uint64_t word = LAYOUT == 0 ? xp[(int64_t)i * nw + w64] : xp[(int64_t)w64 * d.in0 + i];
+      if constexpr (SPW == 64) lds[i] = (WT)word;
+      else lds[i] = (WT)(word >> (32 * (tile & 1)));
+    }
   }
   __syncthreads();
   int cur = 0, nxt = d.maxw, cur_w = d.in0;
@@ -950,23 +1056,11 @@ fc_hard_net_packed_kernel(NetDesc desc, const uint64_t* __restrict__ xp, int B, 
 // resource spanning the tile's samples that exist: the hardware returns 0
 // for any offset past it (the padding samples of the last tile read as 0,
 // bit 0), so the loads need no clamps or branches.
-template <typename IT>
-__device__ inline bool input_bit(IT v) {
-  if constexpr (sizeof(IT) == 1) return v != 0;
-  else return v >= (IT)1;
-}
-
 // The tile's rows as a wave-uniform buffer resource.
 template <typename IT>
 __device__ inline __amdgpu_buffer_rsrc_t tile_rows(const IT* x, int B, int in0, int b0) {
   const int64_t rows = max(0, min(64, B - b0));
   return uniform_rsrc(x + (int64_t)min(b0, B) * in0, (int)(rows * in0 * (int64_t)sizeof(IT)));
-}
-
-template <typename IT>
-__device__ inline IT load_row(__amdgpu_buffer_rsrc_t r, int voff) {
-  if constexpr (sizeof(IT) == 1) return (IT)__builtin_amdgcn_raw_buffer_load_b8(r, voff, 0, 0);
-  else return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
 }
 
 // The next tile streams as chunks of CH samples (16 for networks of up to 4
@@ -1882,7 +1976,7 @@ static int set_lds(K kern, size_t lds, const char* what) {
 }
 
 template <int LAYOUT, typename WT, int MAXO>
-static int launch_net_packed(const uint64_t* xp, int B, const NetDesc& d, size_t lds, int64_t tiles,
+static int launch_net_packed(const void* xp, int B, const NetDesc& d, size_t lds, int64_t tiles,
                              float* logits, hipStream_t st) {
   auto kern = d.plan ? fc_hard_net_packed_kernel<LAYOUT, WT, MAXO, true>
                      : fc_hard_net_packed_kernel<LAYOUT, WT, MAXO, false>;
@@ -1894,7 +1988,7 @@ static int launch_net_packed(const uint64_t* xp, int B, const NetDesc& d, size_t
 }
 
 template <int LAYOUT, typename WT>
-static int net_packed_maxo(int maxo, const uint64_t* xp, int B, const NetDesc& d, size_t lds,
+static int net_packed_maxo(int maxo, const void* xp, int B, const NetDesc& d, size_t lds,
                            int64_t tiles, float* logits, hipStream_t st) {
   switch (maxo) {
     case 2: return launch_net_packed<LAYOUT, WT, 2>(xp, B, d, lds, tiles, logits, st);
@@ -1930,6 +2024,33 @@ static int net_rows_maxo(int maxo, const IT* x, int B, const NetDesc& d, size_t 
     case 4: return launch_net_rows<IT, 4>(x, B, d, lds, logits, st);
     case 8: return launch_net_rows<IT, 8>(x, B, d, lds, logits, st);
     default: return launch_net_rows<IT, 10>(x, B, d, lds, logits, st);
+  }
+}
+
+// The fused network on any input kind: fp32 / byte rows stream through
+// the persistent rows kernel when 64-sample tiles hold at most 1024
+// features, else each workgroup packs its own tile's rows (LAYOUT 2, 3);
+// packed words by their layout.
+static int launch_net_any(const void* x, int in_kind, int B, const NetDesc& d, int spw, int maxo,
+                          size_t lds, float* logits, hipStream_t st) {
+  if (in_kind <= 1 && spw == 64 && d.in0 <= kNetThreads) {
+    if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, B, d, lds, logits, st);
+    return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, B, d, lds, logits, st);
+  }
+  const int64_t tiles = cdiv(B, spw);
+  switch (in_kind) {
+    case 0:
+      return spw == 64 ? net_packed_maxo<2, uint64_t>(maxo, x, B, d, lds, tiles, logits, st)
+                       : net_packed_maxo<2, uint32_t>(maxo, x, B, d, lds, tiles, logits, st);
+    case 1:
+      return spw == 64 ? net_packed_maxo<3, uint64_t>(maxo, x, B, d, lds, tiles, logits, st)
+                       : net_packed_maxo<3, uint32_t>(maxo, x, B, d, lds, tiles, logits, st);
+    case 2:
+      return spw == 64 ? net_packed_maxo<0, uint64_t>(maxo, x, B, d, lds, tiles, logits, st)
+                       : net_packed_maxo<0, uint32_t>(maxo, x, B, d, lds, tiles, logits, st);
+    default:
+      return spw == 64 ? net_packed_maxo<1, uint64_t>(maxo, x, B, d, lds, tiles, logits, st)
+                       : net_packed_maxo<1, uint32_t>(maxo, x, B, d, lds, tiles, logits, st);
   }
 }
 
@@ -2158,10 +2279,6 @@ int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0
   const int64_t S = slg_fc_hard_type_slots(IN0, n_layers, widths);
   SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "fc_hard_net_typed: widths do not fit LDS");
   const int spw = net_spw(IN0, n_layers, widths, 1);
-  const bool rows = in_kind <= 1;
-  SLG_REQUIRE(!rows || (spw == 64 && IN0 <= kNetThreads), SLG_E_UNSUPPORTED,
-              "fc_hard_net_typed: unpacked rows need 64-sample tiles and IN0 <= %d; pack first",
-              kNetThreads);
   NetDesc d{};
   for (int l = 0; l < n_layers; ++l) {
     SLG_REQUIRE(codes[l], SLG_E_ARG, "fc_hard_net_typed: layer %d", l);
@@ -2182,15 +2299,7 @@ int slg_fc_hard_net_typed(const void* x, int32_t in_kind, int64_t B, int64_t IN0
   if (use_head(n_layers, 0, in_kind, B, widths[0], C))
     return launch_head((const uint64_t*)x, in_kind, B, IN0, widths[0], C, codes[0], maxo, plan,
                        logits, st);
-  if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
-  if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
-  const int64_t tiles = cdiv(B, spw);
-  const uint64_t* xp = (const uint64_t*)x;
-  if (in_kind == 2)
-    return spw == 64 ? net_packed_maxo<0, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
-                     : net_packed_maxo<0, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
-  return spw == 64 ? net_packed_maxo<1, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
-                   : net_packed_maxo<1, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
+  return launch_net_any(x, in_kind, (int)B, d, spw, maxo, lds, logits, st);
 }
 
 int slg_fc_hard_net_supported(int64_t IN0, int32_t n_layers, const int64_t* widths, int32_t C) {
@@ -2219,10 +2328,6 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
               (long long)widths[n_layers - 1], C);
   const int spw = net_spw(IN0, n_layers, widths, C);
   SLG_REQUIRE(spw > 0, SLG_E_UNSUPPORTED, "fc_hard_net: widths do not fit LDS");
-  const bool rows = in_kind <= 1;
-  SLG_REQUIRE(!rows || (spw == 64 && IN0 <= kNetThreads), SLG_E_UNSUPPORTED,
-              "fc_hard_net: unpacked rows need 64-sample tiles and IN0 <= %d; pack first",
-              kNetThreads);
   if (B == 0) return 0;
   d.n_layers = n_layers; d.in0 = (int)IN0; d.C = C; d.wire_r = (int)std::max<int64_t>(0, wire_r);
   int64_t maxw = IN0;
@@ -2236,15 +2341,7 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
   if (use_head(n_layers, wire_r, in_kind, B, widths[0], C))
     return launch_head((const uint64_t*)x, in_kind, B, IN0, widths[0], C, codes[0], 0, nullptr,
                        logits, st);
-  if (in_kind == 0) return net_rows_maxo<float>(maxo, (const float*)x, (int)B, d, lds, logits, st);
-  if (in_kind == 1) return net_rows_maxo<uint8_t>(maxo, (const uint8_t*)x, (int)B, d, lds, logits, st);
-  const int64_t tiles = cdiv(B, spw);
-  const uint64_t* xp = (const uint64_t*)x;
-  if (in_kind == 2)
-    return spw == 64 ? net_packed_maxo<0, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
-                     : net_packed_maxo<0, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
-  return spw == 64 ? net_packed_maxo<1, uint64_t>(maxo, xp, (int)B, d, lds, tiles, logits, st)
-                   : net_packed_maxo<1, uint32_t>(maxo, xp, (int)B, d, lds, tiles, logits, st);
+  return launch_net_any(x, in_kind, (int)B, d, spw, maxo, lds, logits, st);
 }
 
 int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C, float* logits,

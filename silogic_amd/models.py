@@ -108,9 +108,8 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
     """Run arity-2 FC layers as a packed circuit and return class counts.
 
     ``in_kind`` is ROWS_F32 / ROWS_U8 for ``[B, in_dim]`` inputs or PACKED for
-    ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, packing
-    fused into it when the input is at most 1024 features wide; otherwise one
-    packed kernel per layer."""
+    ``[in_dim, nw]`` words. Depth-fused in LDS when the widths fit, with the
+    packing of rows fused into it; otherwise one packed kernel per layer."""
     lut, widths, spw, typable = _hard_fc_plan(layers, in_dim, C)
     if lut:
         # LUT layers: one packed kernel per layer (gate or LUT)
@@ -122,15 +121,12 @@ def _hard_fc_stack(layers, x, in_kind, B, in_dim, C, wire_r):
             xp = yp
         return ops.groupsum_packed(xp, B, C)
     if spw:
-        rows = in_kind in (ops.ROWS_F32, ops.ROWS_U8) and spw == 64 and in_dim <= 1024
         # one gate type per wave row where the layout fits, else a bank-aware
         # output order; both relabel the circuit (the logits are the same
         # bits). The wire residual copies inputs by position, so it keeps
         # the order.
         typed = bool(not wire_r and typable)
         codes = _hard_fc_net_codes(layers, in_dim, wire_r, typed)
-        if in_kind in (ops.ROWS_F32, ops.ROWS_U8) and not rows:
-            x, in_kind = ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR
         return ops.fc_hard_net(x, in_kind, B, in_dim, codes, C, wire_r)
     codes = ops.fc_hard_codes_net([layer.hard_spec() for layer in layers])
     xp = x if in_kind == ops.PACKED else ops.pack_bits(x)
@@ -452,9 +448,8 @@ class _HardStep:
 
     @staticmethod
     def for_fc(model, x):
-        """LogicNet: the fused network on rows (packed by a launch of its own
-        where the fused packing does not apply); None for LUT layers or
-        widths past LDS."""
+        """LogicNet: the fused network on rows (packed inside it); None for
+        LUT layers or widths past LDS."""
         from . import _lib
         layers, n_cls = list(model.layers), model.head.num_classes
         B, in_dim = x.shape
@@ -464,18 +459,10 @@ class _HardStep:
         wire_r = model.wire_r
         codes = _hard_fc_net_codes(layers, in_dim, wire_r, bool(not wire_r and typable))
         kind = 1 if x.dtype == torch.uint8 else 0
-        step, bufs = _lib.HardStep(), []
-        step.dtype, step.B = kind, B
-        if spw == 64 and in_dim <= 1024:
-            step.pack = 0
-            _HardStep._head(step, None, kind, in_dim, codes, n_cls, wire_r)
-        else:
-            xp = torch.empty((ops.n_words(B), in_dim), device=x.device, dtype=torch.int64)
-            step.pack, step.C, step.H, step.W, step.packed = 2, in_dim, 1, 1, ops._p(xp)
-            _HardStep._head(step, ops._p(xp), ops.PACKED_WORD_MAJOR, in_dim, codes, n_cls,
-                            wire_r)
-            bufs.append(xp)
-        return _HardStep(step, (B, n_cls), ops._stream(x), bufs, [codes])
+        step = _lib.HardStep()
+        step.dtype, step.B, step.pack = kind, B, 0
+        _HardStep._head(step, None, kind, in_dim, codes, n_cls, wire_r)
+        return _HardStep(step, (B, n_cls), ops._stream(x), [], [codes])
 
     @staticmethod
     def for_conv(model, x):

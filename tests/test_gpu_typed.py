@@ -10,7 +10,6 @@ import torch
 import silogic_amd as sl
 from oracle import torch_ref
 from silogic_amd import ops
-from silogic_amd._lib import HipError
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -99,23 +98,28 @@ def test_typed_network_on_packed_input_is_bit_exact(in_dim, widths, C, skew):
     g = torch.Generator().manual_seed(7)
     B = 64 * 5 + 29
     x = (torch.rand(B, in_dim, generator=g) < 0.45).float().to(DEV)
-    ref = ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, codes, C) if in_dim <= 1024 else None
+    ref = ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, codes, C)
+    assert torch.equal(ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, typed, C), ref)
     for word_major, kind in ((False, ops.PACKED), (True, ops.PACKED_WORD_MAJOR)):
         xp = ops.pack_bits(x, word_major=word_major)
         plain = ops.fc_hard_net(xp, kind, B, in_dim, codes, C)
-        if ref is not None:
-            assert torch.equal(plain, ref)
+        assert torch.equal(plain, ref)
         assert torch.equal(ops.fc_hard_net(xp, kind, B, in_dim, typed, C), plain)
 
 
-def test_typed_codes_refuse_rows_wider_than_a_workgroup():
+def test_typed_codes_take_rows_wider_than_a_workgroup():
+    """Rows wider than 1024 features are packed per tile inside the network
+    kernel: the logits of the packed input's, bit for bit; a wire residual
+    with type-placed codes is refused."""
     net = _net(1500, [1500, 30])
-    typed = ops.fc_hard_type_place_net(_codes(net), 1500)
-    x = torch.zeros(64, 1500, device=DEV)
-    with pytest.raises(HipError):
-        ops.fc_hard_net(x, ops.ROWS_F32, 64, 1500, typed, 10)
+    codes = _codes(net)
+    typed = ops.fc_hard_type_place_net(codes, 1500)
+    g = torch.Generator().manual_seed(3)
+    x = (torch.rand(64 + 7, 1500, generator=g) < 0.5).float().to(DEV)
+    want = ops.fc_hard_net(ops.pack_bits(x), ops.PACKED, 71, 1500, codes, 10)
+    assert torch.equal(ops.fc_hard_net(x, ops.ROWS_F32, 71, 1500, typed, 10), want)
     with pytest.raises(ValueError):
-        ops.fc_hard_net(ops.pack_bits(x), ops.PACKED, 64, 1500, typed, 10, wire_r=8)
+        ops.fc_hard_net(ops.pack_bits(x), ops.PACKED, 71, 1500, typed, 10, wire_r=8)
 
 
 def test_config_2_typed_forward_hard_matches_the_oracle():
