@@ -457,12 +457,21 @@ def hard_launches(cfg, model, x_hard):
     elif d.pack == 2:
         calls.append((L.slg_pack_bits, "slg_pack_bits",
                       [xv, d.dtype, B, d.C * d.H * d.W, 1, d.packed, st]))
-    for c in d.conv[:d.n_conv]:
+    # a one-layer head at a small batch evaluates the last conv block itself
+    fused = step.fuses_head
+    for c in d.conv[:d.n_conv - (1 if fused else 0)]:
         calls.append((L.slg_conv_hard_fwd_wm, "slg_conv_hard_fwd_wm",
                       [c.inp, B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity, c.leaf, c.tt,
                        c.kernel, c.pad, c.out, c.out_pad, st]))
     hin = d.head_in if d.head_in else xv
-    if d.plan:
+    if fused:
+        c = d.conv[d.n_conv - 1]
+        width = ctypes.cast(d.widths, ctypes.POINTER(ctypes.c_int64))[0]
+        codes0 = ctypes.cast(d.codes, ctypes.POINTER(ctypes.c_void_p))[0]
+        calls.append((L.slg_conv_hard_head_wm, "slg_conv_hard_head_wm",
+                      [c.inp, B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity, c.leaf, c.tt,
+                       c.kernel, c.pad, width, codes0, d.plan, d.n_classes, ov, st]))
+    elif d.plan:
         calls.append((L.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
                       [hin, d.head_in_kind, B, d.head_in_dim, d.n_layers, d.widths, d.codes,
                        d.plan, d.n_classes, ov, st]))
@@ -485,6 +494,17 @@ def hard_launches(cfg, model, x_hard):
             res.append((f"conv_hard block {conv_i}: {Cin}->{conv.n} channels, {H}x{W}, "
                         f"{conv.node_name} arity {conv.node_arity}, pooled",
                         launch, nbytes, B * conv_block_bitops(conv, H, W, Ho, Wo)))
+            conv_i += 1
+        elif name == "slg_conv_hard_head_wm":
+            # counted as the launches it replaces: the whole conv block and the head
+            conv, H, W, Ho, Wo = geo[conv_i]
+            layers, C = model.head_layers, model.head.num_classes
+            nbytes = a[2] * H * W * nw * 8 + B * C * 4 + sum(l.out_dim for l in layers) * 4
+            res.append((f"conv_head_kernel (conv block {conv_i}: {a[2]}->{conv.n} channels, "
+                        f"{H}x{W}, {conv.node_name} arity {conv.node_arity}, pooled, evaluated "
+                        f"inside the 1-layer head + GroupSum, {nw} words x {C} classes)",
+                        launch, nbytes,
+                        B * (conv_block_bitops(conv, H, W, Ho, Wo) + fc_bitops(layers))))
             conv_i += 1
         else:
             layers = model.layers if hasattr(model, "layers") else model.head_layers

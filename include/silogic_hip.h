@@ -612,7 +612,9 @@ int slg_pack_image_wm(const void* x, int32_t dtype, int64_t B, int64_t C, int64_
  * (slg_pack_image_wm or slg_pack_bits, word-major), of slg_conv_hard_fwd_wm
  * for each conv block and of slg_fc_hard_net_typed (plan set) or
  * slg_fc_hard_net for the head, in that order on one stream, from a
- * descriptor built once per input shape. Every pointer in it must stay
+ * descriptor built once per input shape; where slg_hard_step_fuses_head()
+ * is 1, the last conv block and the head run as slg_conv_hard_head_wm (the
+ * same logits). Every pointer in it must stay
  * valid while it is used; the intermediate buffers are the descriptor's,
  * so calls that overlap on one descriptor race (serialise them). For
  * callers that run one network many times and would otherwise pay each
@@ -648,6 +650,35 @@ typedef struct {
 } slg_hard_step_t;
 int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
                   slg_stream_t stream);
+/* 1 when slg_hard_step evaluates the descriptor's last conv block inside
+ * its head (slg_conv_hard_head_wm): a one-layer head without wire
+ * residual on the block's own output (no border), at a batch where the head
+ * takes a workgroup per (word, class), with a node the fused kernel
+ * evaluates (gate16 trees of depth 1-3, LUTs of arity 2-6); else 0. No
+ * counterpart in the reference. */
+int slg_hard_step_fuses_head(const slg_hard_step_t* step);
+
+/* The last pooled conv block of a conv network and its one-layer head +
+ * GroupSum in one launch (replaces the last ConvLogicTree + OrPool of
+ * LogicConvNet.forward_hard with its head layer and GroupSum.forward_hard,
+ * models.py:283-293, heads.py:41-45; no single counterpart in the
+ * reference). xp, B, C, H, W, N, node_kind, depth, arity, leaf, tt, kernel
+ * and pad are slg_conv_hard_fwd_wm's (the block's word-major,
+ * zero-bordered input); the head is one layer of `width` gates on the
+ * block's N*Ho*Wo outputs (feature n*Ho*Wo + oy*Wo + ox, <= 16384) with
+ * compact codes, type-placed with `plan` (codes stored thread-major, as
+ * slg_fc_hard_type_place_net writes them) or in index order (plan null),
+ * and n_classes classes of width/n_classes <= 8192 gates. A workgroup per
+ * (64-sample word, class) evaluates only the conv outputs its gates read.
+ * logits [B, n_classes] fp32: the class counts of slg_conv_hard_fwd_wm
+ * followed by slg_fc_hard_net(_typed) on its output, bit for bit. Gate16
+ * trees of depth 1-3 and LUTs of arity 2-6; other nodes return
+ * SLG_E_UNSUPPORTED. */
+int slg_conv_hard_head_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, int64_t W,
+                          int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
+                          const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
+                          int64_t width, const uint32_t* codes, const int32_t* plan,
+                          int32_t n_classes, float* logits, slg_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Packed building blocks of the silogic.bitpacking API                      */

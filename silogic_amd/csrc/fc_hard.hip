@@ -8,6 +8,7 @@
 // so one output word costs the same whatever the gate, with no branching.
 #include <type_traits>
 
+#include "conv_hard_tree.h"
 #include "pack_cols.h"
 #include "slg_common.h"
 
@@ -887,6 +888,122 @@ static int launch_head(const uint64_t* xp, int in_kind, int64_t B, int64_t IN0, 
   hipLaunchKernelGGL(kern, dim3((unsigned)nw, (unsigned)C), dim3(kHeadThreads), (size_t)G * 8, st,
                      xp, (int)B, (int)nw, (int)IN0, G, C, codes, tm, plan, logits);
   SLG_LAUNCH_CHECK("fc_hard_head");
+  return 0;
+}
+
+// The last pooled conv block of a conv network evaluated inside its
+// one-layer head (LogicConvNet.forward_hard's last ConvLogicTree + OrPool
+// and the head layer + GroupSum, models.py:283-293, heads.py:41-45):
+// workgroup (w, c) evaluates the G gates of class c on word w as
+// fc_hard_head_kernel does, each operand being the conv block's output
+// feature f = n * Ho * Wo + oy * Wo + ox (channel n, pooled position) of
+// word w, computed here from the block's input words instead of read from
+// the block's output, one operand per lane. Only the 2G conv outputs the
+// class reads are evaluated (config 5: 2560 of the block's 16384 per word),
+// an operand the gate ignores not at all. A conv output is the same bits as
+// conv_hard_wm_kernel's: the same leaf taps of the zero-bordered input
+// [nw][C][Hp][Wp], the same tree, the OR of the 2x2 pool window; the
+// channel's table is held per lane (lanes take different channels), so LUTs
+// take the multiplexer tree, not the block kernel's wave-uniform typed
+// branches.
+struct ConvTap {
+  const uint64_t* xp;        // block input, word-major [nw][C][Hp][Wp], border zero
+  const int32_t* leaf;       // [N][NLEAF] leaf codes c << 8 | h << 4 | w
+  const uint64_t* tt;        // [N] truth tables
+  int C, Hp, Wp, Ho, Wo, kernel;
+};
+
+template <int NODE, int NLEAF>
+__device__ __forceinline__ uint64_t conv_word_lane(const ConvTap& cv, __amdgpu_buffer_rsrc_t rs,
+                                                   int w, int f) {
+  constexpr int NM = n_mux_masks<NODE, NLEAF>();
+  const int P = cv.Ho * cv.Wo;
+  const int n = f / P, p = f - n * P;
+  const int oy = p / cv.Wo, ox = p - oy * cv.Wo;
+  const int base = (int)(((int64_t)w * cv.C * cv.Hp * cv.Wp + (int64_t)(2 * oy) * cv.Wp + 2 * ox) * 8);
+  uint32_t lo[4][NLEAF], hi[4][NLEAF];
+#pragma unroll
+  for (int l = 0; l < NLEAF; ++l) {
+    const int code = cv.leaf[n * NLEAF + l];
+    const int lc = min(max(code >> 8, 0), cv.C - 1);
+    const int lh = min((code >> 4) & 15, cv.kernel - 1), lw = min(code & 15, cv.kernel - 1);
+    const int o = base + ((lc * cv.Hp + lh) * cv.Wp + lw) * 8;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o + ((q >> 1) * cv.Wp + (q & 1)) * 8, 0, 0);
+      lo[q][l] = v[0];
+      hi[q][l] = v[1];
+    }
+  }
+  const uint64_t t = cv.tt[n];
+  uint32_t ev[NM], es[NM];
+  tree_masks_lane<NODE, NLEAF>((uint32_t)t, (uint32_t)(t >> 32), ev, es);
+  uint32_t rl = 0, rh = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    rl |= tree_eval32<NODE, NLEAF>(lo[q], ev, es);
+    rh |= tree_eval32<NODE, NLEAF>(hi[q], ev, es);
+  }
+  return ((uint64_t)rh << 32) | rl;
+}
+
+template <int NODE, int NLEAF>
+__global__ void __launch_bounds__(kHeadThreads)
+conv_head_kernel(ConvTap cv, int B, int nw, int in0, int G, int C,
+                 const uint32_t* __restrict__ codes, int tm, const int32_t* plan,
+                 float* __restrict__ logits) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* cls = reinterpret_cast<uint64_t*>(smem);
+  const int w = blockIdx.x, c = blockIdx.y;
+  if (plan && !plan_fits(plan, tm, in0)) {   // typed codes placed for another layout
+    if (threadIdx.x < 64 && w * 64 + (int)threadIdx.x < B)
+      logits[(int64_t)(w * 64 + threadIdx.x) * C + c] = __int_as_float(0x7FC00000);
+    return;
+  }
+  // the block input as one buffer: byte offsets fit 32 bits (checked on the host)
+  const __amdgpu_buffer_rsrc_t rs =
+      uniform_rsrc(cv.xp, (int)((int64_t)nw * cv.C * cv.Hp * cv.Wp * 8));
+  // a pair of lanes per gate: the even lane evaluates operand a, the odd
+  // one operand b, and the odd lane's word joins the even lane's by a DPP
+  // swap of neighbouring lanes (quad_perm [1,0,3,2])
+  const int e = threadIdx.x;
+  for (int g0 = 0; g0 < G; g0 += kHeadThreads / 2) {
+    const int i = g0 + (e >> 1);
+    uint32_t code = 0;
+    uint64_t v = 0;
+    if (i < G) {
+      const int o = c * G + i;
+      code = codes[tm ? (o & (kNetThreads - 1)) * tm + (o >> 10) : o];
+      const int t4 = (int)(code >> 28);
+      const bool second = e & 1;
+      if (second ? tt_needs_b(t4) : tt_needs_a(t4)) {
+        const int f = second ? (int)(code & 0x3FFFu) : (int)((code >> 14) & 0x3FFFu);
+        v = conv_word_lane<NODE, NLEAF>(cv, rs, w, min(f, in0 - 1));
+      }
+    }
+    const uint32_t ol = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, 0xB1, 0xF, 0xF, false);
+    const uint32_t oh = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), 0xB1, 0xF, 0xF, false);
+    if (!(e & 1) && i < G) cls[i] = gate_compact<uint64_t>(v, ((uint64_t)oh << 32) | ol, code);
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int n = class_count<2>(reinterpret_cast<const uint32_t*>(cls), G, lane);
+    const int b = w * 64 + lane;
+    if (b < B) logits[(int64_t)b * C + c] = (float)n;
+  }
+}
+
+template <int NODE, int NLEAF>
+static int launch_conv_head(const ConvTap& cv, int64_t B, int64_t in0, int64_t width, int C,
+                            const uint32_t* codes, int tm, const int32_t* plan, float* logits,
+                            hipStream_t st) {
+  const int64_t nw = cdiv(B, 64);
+  const int G = (int)(width / C);
+  hipLaunchKernelGGL((conv_head_kernel<NODE, NLEAF>), dim3((unsigned)nw, (unsigned)C),
+                     dim3(kHeadThreads), (size_t)G * 8, st, cv, (int)B, (int)nw, (int)in0, G, C,
+                     codes, tm, plan, logits);
+  SLG_LAUNCH_CHECK("conv_head");
   return 0;
 }
 
@@ -2342,6 +2459,77 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
     return launch_head((const uint64_t*)x, in_kind, B, IN0, widths[0], C, codes[0], 0, nullptr,
                        logits, st);
   return launch_net_any(x, in_kind, (int)B, d, spw, maxo, lds, logits, st);
+}
+
+int slg_conv_hard_head_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, int64_t W,
+                          int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
+                          const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
+                          int64_t width, const uint32_t* codes, const int32_t* plan,
+                          int32_t n_classes, float* logits, slg_stream_t stream) {
+  SLG_REQUIRE(leaf && tt && codes && ((xp && logits) || B == 0), SLG_E_ARG,
+              "conv_hard_head_wm: null pointer");
+  SLG_REQUIRE(C > 0 && H > 0 && W > 0 && B >= 0 && B < (1LL << 31) && N > 0 && N < 65536 &&
+                  kernel >= 1 && kernel <= 15 && pad >= 0 && pad <= 7 && H < 4096 && W < 4096 &&
+                  C < (1LL << 23),
+              SLG_E_SHAPE, "conv_hard_head_wm: bad conv sizes");
+  const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
+  SLG_REQUIRE(Hf > 1 && Wf > 1, SLG_E_SHAPE, "conv_hard_head_wm: empty pooled output");
+  const int64_t Ho = Hf / 2, Wo = Wf / 2, nw = cdiv(B, 64);
+  const int64_t Hp = H + 2 * pad, Wp = W + 2 * pad, in0 = N * Ho * Wo;
+  SLG_REQUIRE(nw * C * Hp * Wp * 8 < (1LL << 31), SLG_E_SHAPE, "conv_hard_head_wm: maps too large");
+  SLG_REQUIRE(in0 <= kMaxCompactIn, SLG_E_SHAPE,
+              "conv_hard_head_wm: %lld conv outputs, compact codes take at most %d",
+              (long long)in0, kMaxCompactIn);
+  SLG_REQUIRE(n_classes > 0 && n_classes <= 64 && width > 0 && width % n_classes == 0 &&
+                  width / n_classes <= kHeadMaxG && nw * n_classes < (1LL << 31),
+              SLG_E_SHAPE, "conv_hard_head_wm: head width %lld, %d classes", (long long)width,
+              n_classes);
+  int tm = 0;
+  if (plan) {
+    const int64_t S = slg_fc_hard_type_slots(in0, 1, &width);
+    SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "conv_hard_head_wm: no type-uniform layout here");
+    tm = (int)(S / kNetThreads);
+  }
+  if (B == 0) return 0;
+  const ConvTap cv{xp, leaf, tt, (int)C, (int)Hp, (int)Wp, (int)Ho, (int)Wo, kernel};
+  hipStream_t st = as_stream(stream);
+#define SLG_CH(ND, NL) \
+  return launch_conv_head<ND, NL>(cv, B, in0, width, n_classes, codes, tm, plan, logits, st)
+  if (node_kind == SLG_NODE_GATE16) {
+    switch (depth) {
+      case 1: SLG_CH(SLG_NODE_GATE16, 2);
+      case 2: SLG_CH(SLG_NODE_GATE16, 4);
+      case 3: SLG_CH(SLG_NODE_GATE16, 8);
+      default: break;
+    }
+  } else if ((node_kind == SLG_NODE_MULTILINEAR2 || node_kind == SLG_NODE_HYBRID) && depth == 1) {
+    switch (arity) {
+      case 2: SLG_CH(SLG_NODE_MULTILINEAR2, 2);
+      case 3: SLG_CH(SLG_NODE_MULTILINEAR2, 3);
+      case 4: SLG_CH(SLG_NODE_MULTILINEAR2, 4);
+      case 5: SLG_CH(SLG_NODE_MULTILINEAR2, 5);
+      case 6: SLG_CH(SLG_NODE_MULTILINEAR2, 6);
+      default: break;
+    }
+  }
+#undef SLG_CH
+  set_error("conv_hard_head_wm: node %d depth %d / arity %d", node_kind, depth, arity);
+  return SLG_E_UNSUPPORTED;
+}
+
+int slg_hard_step_fuses_head(const slg_hard_step_t* step) {
+  if (!step || step->n_conv < 1 || step->n_conv > SLG_STEP_MAX_CONV) return 0;
+  const slg_hard_step_t& s = *step;
+  const slg_step_conv_t& c = s.conv[s.n_conv - 1];
+  const bool node_ok = (c.node_kind == SLG_NODE_GATE16 && c.depth >= 1 && c.depth <= 3) ||
+                       ((c.node_kind == SLG_NODE_MULTILINEAR2 || c.node_kind == SLG_NODE_HYBRID) &&
+                        c.depth == 1 && c.arity >= 2 && c.arity <= 6);
+  if (!node_ok || s.n_layers != 1 || !s.widths || s.n_classes < 1 || s.head_in != c.out ||
+      s.head_in_kind != 3 || c.out_pad != 0 || c.kernel < 1)
+    return 0;
+  const int64_t Ho = (c.H + 2 * c.pad - c.kernel + 1) / 2, Wo = (c.W + 2 * c.pad - c.kernel + 1) / 2;
+  return s.head_in_dim == c.N * Ho * Wo &&
+         use_head(1, s.wire_r, 3, s.B, s.widths[0], s.n_classes);
 }
 
 int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C, float* logits,

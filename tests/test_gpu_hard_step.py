@@ -29,7 +29,10 @@ def test_hard_step_matches_the_general_path(cfg, B):
         for seed in (3, 4, 5):
             x = config_inputs(cfg, B, seed=seed).to(DEV)
             got = model.forward_hard(x)
-            assert model.__dict__["_derived_hard_step"][1] is not None
+            step = model.__dict__["_derived_hard_step"][1]
+            assert step is not None
+            # config 5's one-layer head evaluates the last conv block itself
+            assert step.fuses_head == (cfg == 5)
             assert torch.equal(got, _general(model, x))
             x8 = x.to(torch.uint8)
             assert torch.equal(model.forward_hard(x8), got)

@@ -1,4 +1,5 @@
-"""Register and scratch use of the fused hard-network kernels, read from the
+"""Register and scratch use of the fused hard-network kernels (and of the
+conv block evaluated inside a conv network's head), read from the
 gfx950 assembly (no GPU needed). A private (scratch) access in these
 persistent kernels is a vector memory load that retires in order behind the
 streamed input rows, so it stalls every layer: a spilled register or a
@@ -13,7 +14,7 @@ import pytest
 
 from silogic_amd import _build
 
-KERNEL = re.compile(r"^(_ZN3slg\d+fc_hard_net_(?:rows|packed)_kernel\w*):", re.M)
+KERNEL = re.compile(r"^(_ZN3slg\d+(?:fc_hard_net_(?:rows|packed)|conv_head)_kernel\w*):", re.M)
 
 
 @pytest.fixture(scope="module")
@@ -36,6 +37,7 @@ def test_fused_network_kernels_use_no_scratch(fc_hard_asm):
     text = fc_hard_asm
     names = KERNEL.findall(text)
     assert len(names) >= 32, len(names)
+    assert sum("conv_head" in n for n in names) == 8, names
     bad = []
     for name in names:
         start = text.index(name + ":")
