@@ -464,13 +464,19 @@ def hard_launches(cfg, model, x_hard):
                       [c.inp, B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity, c.leaf, c.tt,
                        c.kernel, c.pad, c.out, c.out_pad, st]))
     hin = d.head_in if d.head_in else xv
-    if fused:
+    if fused == 1:
         c = d.conv[d.n_conv - 1]
         width = ctypes.cast(d.widths, ctypes.POINTER(ctypes.c_int64))[0]
         codes0 = ctypes.cast(d.codes, ctypes.POINTER(ctypes.c_void_p))[0]
         calls.append((L.slg_conv_hard_head_wm, "slg_conv_hard_head_wm",
                       [c.inp, B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity, c.leaf, c.tt,
                        c.kernel, c.pad, width, codes0, d.plan, d.n_classes, ov, st]))
+    elif fused == 2:
+        c = d.conv[d.n_conv - 1]
+        calls.append((L.slg_conv_hard_net_wm, "slg_conv_hard_net_wm",
+                      [c.inp, B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity, c.leaf, c.tt,
+                       c.kernel, c.pad, d.n_layers, d.widths, d.codes, d.plan, d.n_classes, ov,
+                       st]))
     elif d.plan:
         calls.append((L.slg_fc_hard_net_typed, "slg_fc_hard_net_typed",
                       [hin, d.head_in_kind, B, d.head_in_dim, d.n_layers, d.widths, d.codes,
@@ -495,15 +501,17 @@ def hard_launches(cfg, model, x_hard):
                         f"{conv.node_name} arity {conv.node_arity}, pooled",
                         launch, nbytes, B * conv_block_bitops(conv, H, W, Ho, Wo)))
             conv_i += 1
-        elif name == "slg_conv_hard_head_wm":
+        elif name in ("slg_conv_hard_head_wm", "slg_conv_hard_net_wm"):
             # counted as the launches it replaces: the whole conv block and the head
             conv, H, W, Ho, Wo = geo[conv_i]
-            layers, C = model.head_layers, model.head.num_classes
+            layers, C = list(model.head_layers), model.head.num_classes
             nbytes = a[2] * H * W * nw * 8 + B * C * 4 + sum(l.out_dim for l in layers) * 4
-            res.append((f"conv_head_kernel (conv block {conv_i}: {a[2]}->{conv.n} channels, "
-                        f"{H}x{W}, {conv.node_name} arity {conv.node_arity}, pooled, evaluated "
-                        f"inside the 1-layer head + GroupSum, {nw} words x {C} classes)",
-                        launch, nbytes,
+            what = (f"conv block {conv_i}: {a[2]}->{conv.n} channels, {H}x{W}, "
+                    f"{conv.node_name} arity {conv.node_arity}, pooled, evaluated inside the")
+            kname = (f"conv_head_kernel ({what} 1-layer head + GroupSum, {nw} words x {C} "
+                     "classes)" if name == "slg_conv_hard_head_wm" else
+                     f"conv_net_kernel ({what} {len(layers)}-layer head + GroupSum, {nw} words)")
+            res.append((kname, launch, nbytes,
                         B * (conv_block_bitops(conv, H, W, Ho, Wo) + fc_bitops(layers))))
             conv_i += 1
         else:

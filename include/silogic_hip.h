@@ -613,8 +613,8 @@ int slg_pack_image_wm(const void* x, int32_t dtype, int64_t B, int64_t C, int64_
  * for each conv block and of slg_fc_hard_net_typed (plan set) or
  * slg_fc_hard_net for the head, in that order on one stream, from a
  * descriptor built once per input shape; where slg_hard_step_fuses_head()
- * is 1, the last conv block and the head run as slg_conv_hard_head_wm (the
- * same logits). Every pointer in it must stay
+ * is 1 or 2, the last conv block and the head run as one launch of
+ * slg_conv_hard_head_wm or slg_conv_hard_net_wm (the same logits). Every pointer in it must stay
  * valid while it is used; the intermediate buffers are the descriptor's,
  * so calls that overlap on one descriptor race (serialise them). For
  * callers that run one network many times and would otherwise pay each
@@ -650,12 +650,15 @@ typedef struct {
 } slg_hard_step_t;
 int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
                   slg_stream_t stream);
-/* 1 when slg_hard_step evaluates the descriptor's last conv block inside
- * its head (slg_conv_hard_head_wm): a one-layer head without wire
- * residual on the block's own output (no border), at a batch where the head
- * takes a workgroup per (word, class), with a node the fused kernel
- * evaluates (gate16 trees of depth 1-3, LUTs of arity 2-6); else 0. No
- * counterpart in the reference. */
+/* Whether slg_hard_step evaluates the descriptor's last conv block inside
+ * its head: 1 (slg_conv_hard_head_wm) for a one-layer head at a batch where
+ * the head takes a workgroup per (word, class); 2 (slg_conv_hard_net_wm)
+ * for other heads at batches of at most one 64-sample word per CU whose
+ * fused network has 64-sample words and activation buffers of 2048 or 4096
+ * words that fit LDS beside one word's block input; both need a head
+ * without wire residual on the block's own output
+ * (no border) and a node the fused kernels evaluate (gate16 trees of depth
+ * 1-3, LUTs of arity 2-6); else 0. No counterpart in the reference. */
 int slg_hard_step_fuses_head(const slg_hard_step_t* step);
 
 /* The last pooled conv block of a conv network and its one-layer head +
@@ -679,6 +682,27 @@ int slg_conv_hard_head_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, i
                           const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
                           int64_t width, const uint32_t* codes, const int32_t* plan,
                           int32_t n_classes, float* logits, slg_stream_t stream);
+/* The last pooled conv block of a conv network and its whole head (the
+ * depth-fused network of slg_fc_hard_net / slg_fc_hard_net_typed, no wire
+ * residual) in one launch (replaces the last ConvLogicTree + OrPool of
+ * LogicConvNet.forward_hard with the head layers and GroupSum.forward_hard,
+ * models.py:283-293, heads.py:41-45; no single counterpart in the
+ * reference): the workgroup of each 64-sample word evaluates every conv
+ * output of the word into LDS, then runs the layers and the GroupSum. Conv
+ * arguments as slg_conv_hard_head_wm; n_layers, widths, codes, plan and
+ * n_classes as slg_fc_hard_net_typed (plan set) or slg_fc_hard_net (plan
+ * null) on the block's N*Ho*Wo outputs (<= 16384). logits [B, n_classes]:
+ * the class counts of slg_conv_hard_fwd_wm followed by that call, bit for
+ * bit. SLG_E_UNSUPPORTED unless the network takes 64-sample words with
+ * activation buffers of 2048 or 4096 words, LDS holds them and one word's
+ * block input (C*(H+2pad)*(W+2pad) words, staged there), and the node is a
+ * gate16 tree of depth 1-3 or a LUT of arity 2-6. */
+int slg_conv_hard_net_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, int64_t W,
+                         int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
+                         const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
+                         int32_t n_layers, const int64_t* widths, const uint32_t* const* codes,
+                         const int32_t* plan, int32_t n_classes, float* logits,
+                         slg_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Packed building blocks of the silogic.bitpacking API                      */

@@ -104,6 +104,8 @@ SIGNATURES = {
     "slg_hard_step_fuses_head": (C.c_int, [_P]),
     "slg_conv_hard_head_wm": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P,
                                         _P, _I32, _I32, _I64, _P, _P, _I32, _P, _P]),
+    "slg_conv_hard_net_wm": (C.c_int, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P,
+                                       _P, _I32, _I32, _I32, _P, _P, _P, _I32, _P, _P]),
 }
 
 _lock = threading.Lock()

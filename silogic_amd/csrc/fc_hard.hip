@@ -8,7 +8,7 @@
 // so one output word costs the same whatever the gate, with no branching.
 #include <type_traits>
 
-#include "conv_hard_tree.h"
+#include "fc_net.h"
 #include "pack_cols.h"
 #include "slg_common.h"
 
@@ -275,556 +275,6 @@ __global__ void __launch_bounds__(256) fc_hard_layer_kernel(const uint64_t* __re
 }
 
 
-// ---------------------------------------------------------------------------
-// depth-fused FC network + GroupSum
-// ---------------------------------------------------------------------------
-// One workgroup of 1024 threads owns a column of SPW samples (a 64- or 32-bit
-// word per feature) and keeps the whole activation column in LDS, ping-
-// ponging between two buffers of max-width words, through every layer. Per
-// layer each thread owns outputs tid, tid+1024, ...: it holds their codes in
-// registers (prefetched one layer ahead: codes do not depend on the data),
-// reads its two operand words from LDS and writes the result word. The
-// GroupSum counts are bit-sliced sums (carry-save adders and lane
-// butterflies) per class.
-constexpr int kMaxLayers = 16;
-constexpr int kNetThreads = 1024;
-struct NetDesc {
-  const uint32_t* codes[kMaxLayers];  // compact codes, one word per output
-  int width[kMaxLayers];
-  int n_layers, in0, C, wire_r;
-  int maxw;  // words per activation buffer: MAXO * 1024 (every row of every layer)
-  const int32_t* plan;  // type-uniform layout ([n_layers][kPlanStride]), or null
-};
-// The network kernels take the descriptor as their first argument and read
-// it through the kernel-argument segment (constant memory): its per-layer
-// arrays are indexed by the layer number, and read that way the loads stay
-// scalar instead of going through a private copy of the struct.
-typedef __attribute__((address_space(4))) const NetDesc const_netdesc_t;
-
-// Codes of this thread's outputs o = tid + j*1024 of a W-wide layer, read
-// through a raw buffer resource of W codes: offsets past it read 0 (a valid
-// code), so the loads need no clamp.
-template <int MAXO>
-__device__ inline void load_codes(uint32_t (&cb)[MAXO], const uint32_t* __restrict__ codes, int W) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(codes), (short)0, W * 4, kBufferWord3);
-  const int v = threadIdx.x * 4;
-#pragma unroll
-  for (int j = 0; j < MAXO; ++j) cb[j] = __builtin_amdgcn_raw_buffer_load_b32(r, v + j * kNetThreads * 4, 0, 0);
-}
-
-// Codes of a placed (type-uniform) layer, stored thread-major: the MAXO
-// codes of thread tid are contiguous at tid * MAXO, so one address register
-// and immediate offsets read them (the wave's loads stay contiguous).
-template <int MAXO>
-__device__ inline void load_codes_tm(uint32_t (&cb)[MAXO], const uint32_t* __restrict__ codes) {
-  const uint32_t* p = codes + threadIdx.x * MAXO;
-#pragma unroll
-  for (int j = 0; j < MAXO; ++j) cb[j] = p[j];
-}
-
-__device__ inline uint32_t bfi32(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }
-
-// gate16 on words from a compact code: T_g = all-ones iff tt bit g, read by
-// a sign-extending 1-bit field extract; out = a ? (b ? T3 : T2) : (b ? T1 : T0).
-template <typename WT>
-__device__ inline WT gate_compact(WT a, WT b, uint32_t c) {
-  const uint32_t t0 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 28, 1);
-  const uint32_t t1 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 29, 1);
-  const uint32_t t2 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 30, 1);
-  const uint32_t t3 = (uint32_t)__builtin_amdgcn_sbfe((int)c, 31, 1);
-  if constexpr (sizeof(WT) == 8) {
-    const uint32_t al = (uint32_t)a, ah = (uint32_t)(a >> 32);
-    const uint32_t bl = (uint32_t)b, bh = (uint32_t)(b >> 32);
-    const uint32_t lo = bfi32(al, bfi32(bl, t3, t2), bfi32(bl, t1, t0));
-    const uint32_t hi = bfi32(ah, bfi32(bh, t3, t2), bfi32(bh, t1, t0));
-    return ((uint64_t)hi << 32) | lo;
-  } else {
-    return bfi32(a, bfi32(b, t3, t2), bfi32(b, t1, t0));
-  }
-}
-
-// Operand reads are issued at raised wave priority. Every wave of the
-// workgroup is in the same phase of a layer (a barrier ends each one), so
-// the waves that still have LDS reads to issue would otherwise wait behind
-// those already computing gates; with the reads first, the LDS queue fills
-// sooner and the gate math overlaps it (config 2's fused network 63.2 ->
-// 61.4 us, the same bits).
-__device__ __forceinline__ void reads_begin() { __builtin_amdgcn_s_setprio(1); }
-__device__ __forceinline__ void reads_end() { __builtin_amdgcn_s_setprio(0); }
-
-// One layer on the LDS column: lds[nxt + o] = gate_o(lds[cur + a_o], lds[cur + b_o])
-// for this thread's outputs o = tid + j*1024, in groups of GRP outputs: all
-// operand reads of a group are issued before its results are computed, so
-// the LDS latency of a thread's gates overlaps; the group's gate math runs
-// between its reads and its writes, with no LDS access in between. Each
-// buffer holds MAXO*1024 words, so every row of a group is computed and
-// written without a mask: rows past the layer have code 0 (read past the
-// codes' buffer resource) and write their word into the buffer's unused
-// tail. Operand indices are below the layer's input width by construction
-// (the prep kernel clamps them). Groups wholly past the layer are skipped.
-template <typename WT, int MAXO, int GRP>
-__device__ __forceinline__ void layer_step(WT* lds, int cur, int nxt, int W,
-                                           const uint32_t (&cb)[MAXO]) {
-  static_assert(MAXO % GRP == 0, "groups must tile MAXO");
-  const int rows = (W + kNetThreads - 1) / kNetThreads;
-  const WT* src = lds + cur;
-  WT* dst = lds + nxt + threadIdx.x;
-#pragma unroll
-  for (int g0 = 0; g0 < MAXO; g0 += GRP) {
-    if (g0 >= rows) break;                               // wave-uniform
-    WT va[GRP], vb[GRP];
-    reads_begin();
-#pragma unroll
-    for (int u = 0; u < GRP; ++u) {
-      const uint32_t c = cb[g0 + u];
-      va[u] = src[(c >> 14) & 0x3FFFu];
-      vb[u] = src[c & 0x3FFFu];
-    }
-    reads_end();
-    // all gate math, then all writes: no LDS access between the computes
-    WT r[GRP];
-#pragma unroll
-    for (int u = 0; u < GRP; ++u) r[u] = gate_compact<WT>(va[u], vb[u], cb[g0 + u]);
-#pragma unroll
-    for (int u = 0; u < GRP; ++u) dst[(g0 + u) * kNetThreads] = r[u];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// type-uniform rows
-// ---------------------------------------------------------------------------
-// With a placement plan (slg_fc_hard_type_place_net) the first U rows of a
-// layer hold, in each wave, outputs of one gate type: wave w computes gate
-// tt[w] in rows 0..U-1 and generic gates (compact codes) in rows U..rows-1.
-// A wave then branches once per layer to code specialised for its gate, where
-// a 32-bit half of an output word is one v_bitop3 with the truth table as
-// immediate (or nothing: constants and pass-throughs), and gates that ignore
-// an operand do not read it. A uniform row's code is (a << 16) | b with a, b
-// word indices counted from the start of the first activation buffer (the
-// read buffer's offset included), so an operand's LDS byte address is one
-// v_mad_u32_u16 (16-bit field x word size + LDS base).
-// per layer: U, rows, truth table of waves 0..15, then the slots per thread
-// (MAXO) and the input width the layout was placed for
-constexpr int kPlanStride = 20;
-
-// tt bit k = output for address k = (a << 1) | b (compact-code order)
-__host__ __device__ constexpr bool tt_needs_a(int tt) { return (tt & 3) != (tt >> 2); }
-__host__ __device__ constexpr bool tt_needs_b(int tt) { return (tt & 5) != ((tt >> 1) & 5); }
-// v_bitop3 truth table of (a, b, 0): entry (a << 2 | b << 1 | c) = tt bit (a << 1 | b)
-__host__ __device__ constexpr uint32_t tt_bitop3(int tt) {
-  return ((tt & 1) ? 0x03u : 0u) | ((tt & 2) ? 0x0Cu : 0u) | ((tt & 4) ? 0x30u : 0u) |
-         ((tt & 8) ? 0xC0u : 0u);
-}
-
-template <int TT>
-__device__ __forceinline__ uint32_t gate_tt32(uint32_t a, uint32_t b) {
-  if constexpr (TT == 0) return 0u;
-  else if constexpr (TT == 15) return 0xFFFFFFFFu;
-  else if constexpr (TT == 12) return a;
-  else if constexpr (TT == 10) return b;
-  else if constexpr (TT == 3) return ~a;
-  else if constexpr (TT == 5) return ~b;
-  else return __builtin_amdgcn_bitop3_b32(a, b, 0u, (unsigned char)tt_bitop3(TT));
-}
-
-template <int TT, typename WT>
-__device__ __forceinline__ WT gate_tt(WT a, WT b) {
-  if constexpr (sizeof(WT) == 8) {
-    const uint32_t lo = gate_tt32<TT>((uint32_t)a, (uint32_t)b);
-    const uint32_t hi = gate_tt32<TT>((uint32_t)(a >> 32), (uint32_t)(b >> 32));
-    return ((uint64_t)hi << 32) | lo;
-  } else {
-    return gate_tt32<TT>(a, b);
-  }
-}
-
-typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
-typedef __attribute__((address_space(3))) uint64_t lds_u64_t;
-
-// LDS byte address of word (c >> 16) (HI) or (c & 0xFFFF) of words of SZ bytes
-// counted from LDS byte `base`
-template <int SZ, bool HI>
-__device__ __forceinline__ uint32_t field_addr(uint32_t c, uint32_t base) {
-  uint32_t r;
-  if constexpr (SZ == 8 && HI) asm("v_mad_u32_u16 %0, %1, 8, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(c), "s"(base));
-  else if constexpr (SZ == 8) asm("v_mad_u32_u16 %0, %1, 8, %2" : "=v"(r) : "v"(c), "s"(base));
-  else if constexpr (HI) asm("v_mad_u32_u16 %0, %1, 4, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(c), "s"(base));
-  else asm("v_mad_u32_u16 %0, %1, 4, %2" : "=v"(r) : "v"(c), "s"(base));
-  return r;
-}
-
-template <typename WT>
-__device__ __forceinline__ WT lds_word(uint32_t addr) {
-  if constexpr (sizeof(WT) == 8) return *(const lds_u64_t*)(uintptr_t)addr;
-  else return *(const lds_u32_t*)(uintptr_t)addr;
-}
-
-// Rows [g0, g0 + N) of gate TT: every operand read first, then `between`
-// (work that overlaps the reads), then the gates, then the writes.
-struct NoWork {
-  __device__ void operator()() const {}
-};
-
-template <typename WT, int MAXO, int TT, int N, typename F = NoWork>
-__device__ __forceinline__ void uniform_group(uint32_t base, WT* dst, int g0,
-                                              const uint32_t (&cb)[MAXO], F&& between = F()) {
-  constexpr int SZ = (int)sizeof(WT);
-  WT va[N], vb[N];
-  reads_begin();
-#pragma unroll
-  for (int u = 0; u < N; ++u) {
-    va[u] = vb[u] = (WT)0;
-    if constexpr (tt_needs_a(TT)) va[u] = lds_word<WT>(field_addr<SZ, true>(cb[g0 + u], base));
-    if constexpr (tt_needs_b(TT)) vb[u] = lds_word<WT>(field_addr<SZ, false>(cb[g0 + u], base));
-  }
-  reads_end();
-  between();
-  WT r[N];
-#pragma unroll
-  for (int u = 0; u < N; ++u) r[u] = gate_tt<TT, WT>(va[u], vb[u]);
-#pragma unroll
-  for (int u = 0; u < N; ++u) dst[(g0 + u) * kNetThreads] = r[u];
-}
-
-// A group of N = 1..GRP-1 rows at g0 (N wave-uniform), as one batch.
-template <typename WT, int MAXO, int TT, int G0, int N>
-__device__ __forceinline__ void uniform_tail(uint32_t base, WT* dst, int n,
-                                             const uint32_t (&cb)[MAXO]) {
-  if constexpr (N >= 1 && G0 + N <= MAXO) {
-    if (n == N) uniform_group<WT, MAXO, TT, N>(base, dst, G0, cb);
-    else uniform_tail<WT, MAXO, TT, G0, N - 1>(base, dst, n, cb);
-  }
-}
-
-// Rows 0..U-1 of a wave of gate TT (U wave-uniform), in groups of GRP rows
-// and one shorter group for the rest.
-template <typename WT, int MAXO, int GRP, int TT, int G0 = 0>
-__device__ __forceinline__ void uniform_rows(uint32_t base, WT* dst, int U,
-                                             const uint32_t (&cb)[MAXO]) {
-  if constexpr (G0 < MAXO) {
-    if (G0 + GRP <= U) {
-      uniform_group<WT, MAXO, TT, GRP>(base, dst, G0, cb);
-      uniform_rows<WT, MAXO, GRP, TT, G0 + GRP>(base, dst, U, cb);
-    } else if (U > G0) {
-      uniform_tail<WT, MAXO, TT, G0, GRP - 1>(base, dst, U - G0, cb);
-    }
-  }
-}
-
-// Generic rows J..rows-1 (U == J) from compact codes, one at a time; the
-// compile-time start keeps the register indexing static.
-template <typename WT, int MAXO, int J>
-__device__ __forceinline__ void generic_rows(const WT* src, WT* dst, int U, int rows,
-                                             const uint32_t (&cb)[MAXO]) {
-  if constexpr (J <= MAXO) {
-    if (U != J) {
-      generic_rows<WT, MAXO, J + 1>(src, dst, U, rows, cb);
-      return;
-    }
-#pragma unroll
-    for (int j = J; j < MAXO; ++j) {
-      if (j >= rows) break;                              // wave-uniform
-      const uint32_t c = cb[j];
-      reads_begin();
-      const WT a = src[(c >> 14) & 0x3FFFu], b = src[c & 0x3FFFu];
-      reads_end();
-      dst[j * kNetThreads] = gate_compact<WT>(a, b, c);
-    }
-  }
-}
-
-// The usual plan, U = MAXO - 1 and rows = MAXO: uniform rows in groups of
-// GRP, the last group read and computed in one batch with the generic row
-// MAXO - 1. No branch inside. `filler` (the layer's input-row work) runs
-// while the first group's reads are in flight.
-template <typename WT, int MAXO, int GRP, int TT, typename F>
-__device__ __forceinline__ void typed_rows_full(uint32_t base, const WT* src, WT* dst,
-                                                const uint32_t (&cb)[MAXO], F&& filler) {
-  constexpr int SZ = (int)sizeof(WT);
-  constexpr int LG = ((MAXO - 2) / GRP) * GRP;       // first row of the last group
-  constexpr int N = MAXO - 1 - LG;                   // its uniform rows (>= 1)
-  if constexpr (LG >= GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, 0, cb, filler);
-  else filler();
-#pragma unroll
-  for (int g0 = GRP; g0 < LG; g0 += GRP) uniform_group<WT, MAXO, TT, GRP>(base, dst, g0, cb);
-  WT va[N], vb[N];
-  reads_begin();
-#pragma unroll
-  for (int u = 0; u < N; ++u) {
-    va[u] = vb[u] = (WT)0;
-    if constexpr (tt_needs_a(TT)) va[u] = lds_word<WT>(field_addr<SZ, true>(cb[LG + u], base));
-    if constexpr (tt_needs_b(TT)) vb[u] = lds_word<WT>(field_addr<SZ, false>(cb[LG + u], base));
-  }
-  const uint32_t c = cb[MAXO - 1];
-  const WT ga = src[(c >> 14) & 0x3FFFu], gb = src[c & 0x3FFFu];
-  reads_end();
-  WT r[N];
-#pragma unroll
-  for (int u = 0; u < N; ++u) r[u] = gate_tt<TT, WT>(va[u], vb[u]);
-#pragma unroll
-  for (int u = 0; u < N; ++u) dst[(LG + u) * kNetThreads] = r[u];
-  dst[(MAXO - 1) * kNetThreads] = gate_compact<WT>(ga, gb, c);
-}
-
-// A layer's plan as the wave reads it: U, the rows computed, its truth
-// table. The plan is read as constant memory, so its loads are scalar: a
-// vector load would retire in order behind the layer's input-row loads and
-// wait for them.
-typedef __attribute__((address_space(4))) const int32_t const_i32_t;
-
-struct PlanRow {
-  int U, rows, tt;
-};
-
-// The codes of a placed layout are read at a stride of MAXO slots, which
-// follows the input width it was placed for: a plan placed for another
-// width or slot count would index past its codes, so the network kernels
-// check the plan's own record first and write NaN logits instead.
-__device__ __forceinline__ bool plan_fits(const int32_t* plan, int maxo, int in0) {
-  const const_i32_t* pl = (const const_i32_t*)plan;
-  return __builtin_amdgcn_readfirstlane(pl[18]) == maxo &&
-         __builtin_amdgcn_readfirstlane(pl[19]) == in0;
-}
-
-__device__ inline void nan_logits(float* __restrict__ logits, int B, int C) {
-  const int64_t n = (int64_t)B * C, step = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
-    logits[i] = __int_as_float(0x7FC00000);
-}
-
-__device__ __forceinline__ PlanRow plan_row(const int32_t* plan, int l) {
-  const const_i32_t* pl = (const const_i32_t*)(plan + l * kPlanStride);
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  return {__builtin_amdgcn_readfirstlane(pl[0]), __builtin_amdgcn_readfirstlane(pl[1]),
-          __builtin_amdgcn_readfirstlane(pl[2 + wave])};
-}
-
-// One layer of a planned network: the wave's uniform rows, then rows
-// U..rows-1 from compact codes (as layer_step).
-template <typename WT, int MAXO, int GRP, typename F>
-__device__ __forceinline__ void typed_step(WT* lds, int cur, int nxt, PlanRow pr,
-                                           const uint32_t (&cb)[MAXO], F&& filler) {
-  const int U = pr.U, rows = pr.rows, tt = pr.tt;
-  const uint32_t base = (uint32_t)(uintptr_t)lds;
-  const WT* src = lds + cur;
-  WT* dst = lds + nxt + threadIdx.x;
-  if (MAXO > 1 && U == MAXO - 1 && rows == MAXO) {
-    switch (tt & 15) {
-#define SLG_TT_CASE(T) \
-      case T: typed_rows_full<WT, MAXO, GRP, T>(base, src, dst, cb, filler); break;
-      SLG_TT_CASE(0) SLG_TT_CASE(1) SLG_TT_CASE(2) SLG_TT_CASE(3)
-      SLG_TT_CASE(4) SLG_TT_CASE(5) SLG_TT_CASE(6) SLG_TT_CASE(7)
-      SLG_TT_CASE(8) SLG_TT_CASE(9) SLG_TT_CASE(10) SLG_TT_CASE(11)
-      SLG_TT_CASE(12) SLG_TT_CASE(13) SLG_TT_CASE(14) SLG_TT_CASE(15)
-#undef SLG_TT_CASE
-    }
-    return;
-  }
-  filler();
-  switch (tt & 15) {
-#define SLG_TT_CASE(T) \
-    case T: uniform_rows<WT, MAXO, GRP, T>(base, dst, U, cb); break;
-    SLG_TT_CASE(0) SLG_TT_CASE(1) SLG_TT_CASE(2) SLG_TT_CASE(3)
-    SLG_TT_CASE(4) SLG_TT_CASE(5) SLG_TT_CASE(6) SLG_TT_CASE(7)
-    SLG_TT_CASE(8) SLG_TT_CASE(9) SLG_TT_CASE(10) SLG_TT_CASE(11)
-    SLG_TT_CASE(12) SLG_TT_CASE(13) SLG_TT_CASE(14) SLG_TT_CASE(15)
-#undef SLG_TT_CASE
-  }
-  generic_rows<WT, MAXO, 0>(src, dst, U, rows, cb);
-}
-
-// wire residual (models.py:88-94): the first `keep` outputs copy the inputs
-template <typename WT, int MAXO>
-__device__ inline void keep_inputs(WT* lds, int cur, int nxt, int keep) {
-#pragma unroll
-  for (int j = 0; j < MAXO; ++j) {
-    const int o = threadIdx.x + j * kNetThreads;
-    if (o < keep) lds[nxt + o] = lds[cur + o];
-  }
-}
-
-// Per-class sample counts without a bit transpose. One wave takes a class:
-// for 64-bit words lanes 0..31 count the low 32 samples and lanes 32..63 the
-// high 32, each lane carry-save adding (Harley-Seal) the half-words of 32
-// words into a bit-sliced 6-bit count per sample (slice k holds bit k of
-// every sample's count); five butterfly rounds inside each 32-lane group
-// then add the lanes' bit-sliced counts (ripple-carry adders on the slices),
-// after which every lane of a group holds its 32 samples' class totals in
-// 11 slices and lane s reads its own bits. 32-bit words take 16 words per
-// lane over all 64 lanes and a sixth round across the two groups. The
-// exchanges are DPP moves and permlane swaps, no LDS; words past the class
-// read 0; every lane of the wave must be active.
-// Majority and 3-input xor as one v_bitop3 each (truth tables 0xE8 and
-// 0x96, both symmetric in their inputs).
-__device__ __forceinline__ uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) {
-  return __builtin_amdgcn_bitop3_b32(a, b, c, 0xE8);
-}
-__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
-  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
-}
-
-__device__ __forceinline__ void csa(uint32_t& h, uint32_t& l, uint32_t a, uint32_t b, uint32_t c) {
-  h = maj3(a, b, c);
-  l = xor3(a, b, c);
-}
-
-constexpr int kGsSlices = 12;   // bit slices of a lane's counts (at most 2048)
-
-// Harley-Seal step over 16 words: ones..eights carry across calls, the
-// 16s word of this block is returned.
-__device__ __forceinline__ uint32_t hs16(uint32_t& ones, uint32_t& twos, uint32_t& fours,
-                                         uint32_t& eights, const uint32_t* w) {
-  uint32_t twosA, twosB, foursA, foursB, eightsA, eightsB, sixteens;
-  csa(twosA, ones, ones, w[0], w[1]);
-  csa(twosB, ones, ones, w[2], w[3]);
-  csa(foursA, twos, twos, twosA, twosB);
-  csa(twosA, ones, ones, w[4], w[5]);
-  csa(twosB, ones, ones, w[6], w[7]);
-  csa(foursB, twos, twos, twosA, twosB);
-  csa(eightsA, fours, fours, foursA, foursB);
-  csa(twosA, ones, ones, w[8], w[9]);
-  csa(twosB, ones, ones, w[10], w[11]);
-  csa(foursA, twos, twos, twosA, twosB);
-  csa(twosA, ones, ones, w[12], w[13]);
-  csa(twosB, ones, ones, w[14], w[15]);
-  csa(foursB, twos, twos, twosA, twosB);
-  csa(eightsB, fours, fours, foursA, foursB);
-  csa(sixteens, eights, eights, eightsA, eightsB);
-  return sixteens;
-}
-
-// Bit-sliced add x += y of NB-bit counts (x[NB] is 0 on entry and takes the
-// carry out): a ripple of full adders, slice by slice.
-template <int NB>
-__device__ __forceinline__ void add_slices(uint32_t (&x)[kGsSlices], const uint32_t (&y)[kGsSlices]) {
-  uint32_t carry = 0;
-#pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    const uint32_t t = xor3(x[k], y[k], carry);
-    carry = maj3(x[k], y[k], carry);
-    x[k] = t;
-  }
-  x[NB] = carry;
-}
-
-// Butterfly step within 16-lane rows by a DPP lane pattern: quad_perm
-// [1,0,3,2] (lane ^ 1), [2,3,0,1] (lane ^ 2), then row_half_mirror (lane i of
-// 8 with 7 - i: joins the two quads' totals) and row_mirror (i of 16 with
-// 15 - i: joins the two 8-lane totals).
-template <int NB, int CTRL>
-__device__ __forceinline__ void add_dpp(uint32_t (&x)[kGsSlices]) {
-  uint32_t y[kGsSlices];
-#pragma unroll
-  for (int k = 0; k < NB; ++k) y[k] = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[k], CTRL, 0xF, 0xF, false);
-  add_slices<NB>(x, y);
-}
-
-// Butterfly step across 16- or 32-lane halves: v_permlane16/32_swap of a
-// value with itself returns, in every lane, the lane's own value and that of
-// lane ^ 16 (^ 32) as the pair (a, b), so the sum is a + b.
-template <int NB, bool P32>
-__device__ __forceinline__ void add_swap(uint32_t (&x)[kGsSlices]) {
-  uint32_t a[kGsSlices], b[kGsSlices];
-#pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    if constexpr (P32) {
-      const auto r = __builtin_amdgcn_permlane32_swap(x[k], x[k], false, false);
-      a[k] = r[0];
-      b[k] = r[1];
-    } else {
-      const auto r = __builtin_amdgcn_permlane16_swap(x[k], x[k], false, false);
-      a[k] = r[0];
-      b[k] = r[1];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < NB; ++k) x[k] = a[k];
-  x[NB] = 0;
-  add_slices<NB>(x, b);
-}
-
-// Class total of this lane's sample over the class's G words `cls32`
-// (32-bit halves, NH per word): sample lane for NH == 2, lane & 31 for
-// NH == 1. A pass takes WPL words per lane: 32 for 64-bit words (1024 words
-// per pass); 16 or 32 for 32-bit words (1024 or 2048 words per pass: one
-// butterfly for classes of up to 2048 words, where 1024-word passes would
-// take two).
-template <int NH, int WPL1 = 16>
-__device__ __forceinline__ int class_count(const uint32_t* cls32, int G, int lane) {
-  constexpr int WPL = NH == 2 ? 32 : WPL1;               // words per lane per pass
-  constexpr int LSTRIDE = NH == 2 ? 32 : 64;             // word stride between them
-  constexpr int CHUNK = WPL * LSTRIDE;                   // words per pass
-  constexpr int NBITS = (NH == 1 && WPL == 32) ? 12 : 11;  // slices of the pass's total
-  static_assert(WPL == 16 || WPL == 32, "16 or 32 words per lane");
-  const int l = NH == 2 ? (lane & 31) : lane;
-  const int h = NH == 2 ? (lane >> 5) : 0;
-  int total = 0;
-  for (int q0 = 0; q0 < G; q0 += CHUNK) {
-    // rows of the pass wholly inside the class load without a lane guard
-    // (a wave-uniform test); only the class's last partial row is guarded
-    const int nvalid = G - q0;
-    const uint32_t* p = cls32 + (q0 + l) * NH + h;
-    uint32_t w[WPL];
-    reads_begin();
-#pragma unroll
-    for (int j = 0; j < WPL; ++j) {
-      if (j * LSTRIDE + LSTRIDE <= nvalid) w[j] = p[j * LSTRIDE * NH];
-      else w[j] = j * LSTRIDE + l < nvalid ? p[j * LSTRIDE * NH] : 0u;
-    }
-    reads_end();
-    uint32_t x[kGsSlices];
-#pragma unroll
-    for (int k = 0; k < kGsSlices; ++k) x[k] = 0;
-    if constexpr (WPL == 32) {
-      const uint32_t s16a = hs16(x[0], x[1], x[2], x[3], w);
-      const uint32_t s16b = hs16(x[0], x[1], x[2], x[3], w + 16);
-      x[4] = s16a ^ s16b;
-      x[5] = s16a & s16b;
-      // 6 bits (<= 32) grow one bit per round: 11 (<= 1024) after five
-      // rounds inside each 32-lane group, 12 (<= 2048) after the sixth
-      add_dpp<6, 0xB1>(x);    // quad_perm [1,0,3,2]
-      add_dpp<7, 0x4E>(x);    // quad_perm [2,3,0,1]
-      add_dpp<8, 0x141>(x);   // row_half_mirror
-      add_dpp<9, 0x140>(x);   // row_mirror
-      add_swap<10, false>(x);  // lane ^ 16
-      if constexpr (NH == 1) add_swap<11, true>(x);  // lane ^ 32
-    } else {
-      x[4] = hs16(x[0], x[1], x[2], x[3], w);
-      add_dpp<5, 0xB1>(x);
-      add_dpp<6, 0x4E>(x);
-      add_dpp<7, 0x141>(x);
-      add_dpp<8, 0x140>(x);
-      add_swap<9, false>(x);
-      add_swap<10, true>(x);  // lane ^ 32
-    }
-    const int sh = lane & 31;
-    int cnt = 0;
-#pragma unroll
-    for (int k = 0; k < NBITS; ++k) cnt |= (int)((x[k] >> sh) & 1u) << k;
-    total += cnt;
-  }
-  return total;
-}
-
-// Per-class popcounts of a tile written as logits: one wave per class.
-template <typename WT>
-__device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int b0, int B,
-                                              float* __restrict__ logits) {
-  constexpr int NH = (int)sizeof(WT) / 4;                // 32-sample halves per word
-  constexpr int SPW = NH * 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nwaves = kNetThreads >> 6;
-  const int G = W / C;
-  for (int c = wave; c < C; c += nwaves) {
-    const uint32_t* cls = reinterpret_cast<const uint32_t*>(cur + c * G);
-    const int n = (NH == 1 && G > 1024) ? class_count<NH, 32>(cls, G, lane)
-                                        : class_count<NH>(cls, G, lane);
-    const int b = b0 + lane;
-    if (lane < SPW && b < B) logits[(int64_t)b * C + c] = (float)n;
-  }
-}
-
 // One-layer networks at small batches (a conv network's head on a few
 // sample words): the fused kernel's one workgroup per word would leave most
 // CUs idle and stage every input word in LDS although each gate reads two.
@@ -836,9 +286,6 @@ __device__ __forceinline__ void groupsum_tile(const WT* cur, int W, int C, int b
 // thread, output o at (o % 1024) * TM + o / 1024. (Two-layer heads, layer 0
 // evaluated per workgroup from memory, measured no faster than the fused
 // kernel at config 3's head and are left to it.)
-constexpr int kHeadThreads = 256;
-constexpr int kHeadMaxG = 8192;   // a class's gate words in 64 KiB of LDS
-
 template <int LAYOUT>
 __global__ void __launch_bounds__(kHeadThreads)
 fc_hard_head_kernel(const uint64_t* __restrict__ xp, int B, int nw, int in0, int G, int C,
@@ -871,14 +318,6 @@ fc_hard_head_kernel(const uint64_t* __restrict__ xp, int B, int nw, int in0, int
   }
 }
 
-// Whether a one-layer network on packed words takes fc_hard_head_kernel:
-// fewer sample words than half the CUs (the fused kernel's workgroups), no
-// wire residual, a class in LDS.
-static bool use_head(int n_layers, int64_t wire_r, int in_kind, int64_t B, int64_t width, int C) {
-  return n_layers == 1 && wire_r <= 0 && in_kind >= 2 && B > 0 &&
-         2 * cdiv(B, 64) < device_cus() && width / C <= kHeadMaxG;
-}
-
 static int launch_head(const uint64_t* xp, int in_kind, int64_t B, int64_t IN0, int64_t width,
                        int C, const uint32_t* codes, int tm, const int32_t* plan, float* logits,
                        hipStream_t st) {
@@ -888,122 +327,6 @@ static int launch_head(const uint64_t* xp, int in_kind, int64_t B, int64_t IN0, 
   hipLaunchKernelGGL(kern, dim3((unsigned)nw, (unsigned)C), dim3(kHeadThreads), (size_t)G * 8, st,
                      xp, (int)B, (int)nw, (int)IN0, G, C, codes, tm, plan, logits);
   SLG_LAUNCH_CHECK("fc_hard_head");
-  return 0;
-}
-
-// The last pooled conv block of a conv network evaluated inside its
-// one-layer head (LogicConvNet.forward_hard's last ConvLogicTree + OrPool
-// and the head layer + GroupSum, models.py:283-293, heads.py:41-45):
-// workgroup (w, c) evaluates the G gates of class c on word w as
-// fc_hard_head_kernel does, each operand being the conv block's output
-// feature f = n * Ho * Wo + oy * Wo + ox (channel n, pooled position) of
-// word w, computed here from the block's input words instead of read from
-// the block's output, one operand per lane. Only the 2G conv outputs the
-// class reads are evaluated (config 5: 2560 of the block's 16384 per word),
-// an operand the gate ignores not at all. A conv output is the same bits as
-// conv_hard_wm_kernel's: the same leaf taps of the zero-bordered input
-// [nw][C][Hp][Wp], the same tree, the OR of the 2x2 pool window; the
-// channel's table is held per lane (lanes take different channels), so LUTs
-// take the multiplexer tree, not the block kernel's wave-uniform typed
-// branches.
-struct ConvTap {
-  const uint64_t* xp;        // block input, word-major [nw][C][Hp][Wp], border zero
-  const int32_t* leaf;       // [N][NLEAF] leaf codes c << 8 | h << 4 | w
-  const uint64_t* tt;        // [N] truth tables
-  int C, Hp, Wp, Ho, Wo, kernel;
-};
-
-template <int NODE, int NLEAF>
-__device__ __forceinline__ uint64_t conv_word_lane(const ConvTap& cv, __amdgpu_buffer_rsrc_t rs,
-                                                   int w, int f) {
-  constexpr int NM = n_mux_masks<NODE, NLEAF>();
-  const int P = cv.Ho * cv.Wo;
-  const int n = f / P, p = f - n * P;
-  const int oy = p / cv.Wo, ox = p - oy * cv.Wo;
-  const int base = (int)(((int64_t)w * cv.C * cv.Hp * cv.Wp + (int64_t)(2 * oy) * cv.Wp + 2 * ox) * 8);
-  uint32_t lo[4][NLEAF], hi[4][NLEAF];
-#pragma unroll
-  for (int l = 0; l < NLEAF; ++l) {
-    const int code = cv.leaf[n * NLEAF + l];
-    const int lc = min(max(code >> 8, 0), cv.C - 1);
-    const int lh = min((code >> 4) & 15, cv.kernel - 1), lw = min(code & 15, cv.kernel - 1);
-    const int o = base + ((lc * cv.Hp + lh) * cv.Wp + lw) * 8;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o + ((q >> 1) * cv.Wp + (q & 1)) * 8, 0, 0);
-      lo[q][l] = v[0];
-      hi[q][l] = v[1];
-    }
-  }
-  const uint64_t t = cv.tt[n];
-  uint32_t ev[NM], es[NM];
-  tree_masks_lane<NODE, NLEAF>((uint32_t)t, (uint32_t)(t >> 32), ev, es);
-  uint32_t rl = 0, rh = 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    rl |= tree_eval32<NODE, NLEAF>(lo[q], ev, es);
-    rh |= tree_eval32<NODE, NLEAF>(hi[q], ev, es);
-  }
-  return ((uint64_t)rh << 32) | rl;
-}
-
-template <int NODE, int NLEAF>
-__global__ void __launch_bounds__(kHeadThreads)
-conv_head_kernel(ConvTap cv, int B, int nw, int in0, int G, int C,
-                 const uint32_t* __restrict__ codes, int tm, const int32_t* plan,
-                 float* __restrict__ logits) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint64_t* cls = reinterpret_cast<uint64_t*>(smem);
-  const int w = blockIdx.x, c = blockIdx.y;
-  if (plan && !plan_fits(plan, tm, in0)) {   // typed codes placed for another layout
-    if (threadIdx.x < 64 && w * 64 + (int)threadIdx.x < B)
-      logits[(int64_t)(w * 64 + threadIdx.x) * C + c] = __int_as_float(0x7FC00000);
-    return;
-  }
-  // the block input as one buffer: byte offsets fit 32 bits (checked on the host)
-  const __amdgpu_buffer_rsrc_t rs =
-      uniform_rsrc(cv.xp, (int)((int64_t)nw * cv.C * cv.Hp * cv.Wp * 8));
-  // a pair of lanes per gate: the even lane evaluates operand a, the odd
-  // one operand b, and the odd lane's word joins the even lane's by a DPP
-  // swap of neighbouring lanes (quad_perm [1,0,3,2])
-  const int e = threadIdx.x;
-  for (int g0 = 0; g0 < G; g0 += kHeadThreads / 2) {
-    const int i = g0 + (e >> 1);
-    uint32_t code = 0;
-    uint64_t v = 0;
-    if (i < G) {
-      const int o = c * G + i;
-      code = codes[tm ? (o & (kNetThreads - 1)) * tm + (o >> 10) : o];
-      const int t4 = (int)(code >> 28);
-      const bool second = e & 1;
-      if (second ? tt_needs_b(t4) : tt_needs_a(t4)) {
-        const int f = second ? (int)(code & 0x3FFFu) : (int)((code >> 14) & 0x3FFFu);
-        v = conv_word_lane<NODE, NLEAF>(cv, rs, w, min(f, in0 - 1));
-      }
-    }
-    const uint32_t ol = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, 0xB1, 0xF, 0xF, false);
-    const uint32_t oh = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), 0xB1, 0xF, 0xF, false);
-    if (!(e & 1) && i < G) cls[i] = gate_compact<uint64_t>(v, ((uint64_t)oh << 32) | ol, code);
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const int n = class_count<2>(reinterpret_cast<const uint32_t*>(cls), G, lane);
-    const int b = w * 64 + lane;
-    if (b < B) logits[(int64_t)b * C + c] = (float)n;
-  }
-}
-
-template <int NODE, int NLEAF>
-static int launch_conv_head(const ConvTap& cv, int64_t B, int64_t in0, int64_t width, int C,
-                            const uint32_t* codes, int tm, const int32_t* plan, float* logits,
-                            hipStream_t st) {
-  const int64_t nw = cdiv(B, 64);
-  const int G = (int)(width / C);
-  hipLaunchKernelGGL((conv_head_kernel<NODE, NLEAF>), dim3((unsigned)nw, (unsigned)C),
-                     dim3(kHeadThreads), (size_t)G * 8, st, cv, (int)B, (int)nw, (int)in0, G, C,
-                     codes, tm, plan, logits);
-  SLG_LAUNCH_CHECK("conv_head");
   return 0;
 }
 
@@ -1127,39 +450,7 @@ fc_hard_net_packed_kernel(NetDesc desc, const void* __restrict__ xin, int B, int
     }
   }
   __syncthreads();
-  int cur = 0, nxt = d.maxw, cur_w = d.in0;
-  const int L = d.n_layers;
-  // typed: plan row and next codes pointer scalar-loaded a layer ahead
-  PlanRow pc{};
-  const uint32_t* cn = nullptr;
-  if constexpr (TYPED) {
-    pc = plan_row(d.plan, 0);
-    cn = d.codes[L > 1 ? 1 : 0];
-  }
-  for (int l = 0; l < L; ++l) {
-    const int W = d.width[l];
-    uint32_t nb[MAXO];
-    const int ln = (l + 1 < L) ? l + 1 : l;
-    if constexpr (TYPED) {
-      load_codes_tm(nb, cn);
-      const PlanRow pn = plan_row(d.plan, ln);
-      const uint32_t* cnn = d.codes[(ln + 1 < L) ? ln + 1 : ln];
-      typed_step<WT, MAXO, (MAXO % 2 == 0 && MAXO > 4) ? MAXO / 2 : MAXO>(
-          lds, cur, nxt, pc, cb, NoWork());
-      pc = pn;
-      cn = cnn;
-    } else {
-      load_codes(nb, d.codes[ln], d.width[ln]);
-      layer_step<WT, MAXO, MAXO>(lds, cur, nxt, W, cb);
-      if (d.wire_r > 0 && cur_w == W) keep_inputs<WT, MAXO>(lds, cur, nxt, min(d.wire_r, W));
-    }
-    __syncthreads();
-    const int t = cur; cur = nxt; nxt = t;
-    cur_w = W;
-#pragma unroll
-    for (int j = 0; j < MAXO; ++j) cb[j] = nb[j];
-  }
-  groupsum_tile<WT>(lds + cur, cur_w, d.C, tile * SPW, B, logits);
+  net_tile_layers<WT, MAXO, TYPED>(d, lds, cb, tile, B, logits);
 }
 
 // Unpacked rows [B][in0] (fp32, or uint8) with the packing fused: thread f
@@ -2061,37 +1352,6 @@ __global__ void __launch_bounds__(256) groupsum_packed_kernel(const uint64_t* __
 }
 
 
-static int pick_maxo(int64_t maxw) {
-  const int64_t m = cdiv(maxw, kNetThreads);
-  for (int c : {2, 4, 8, 10, 16})
-    if (m <= c) return c;
-  return 0;
-}
-
-static int net_spw(int64_t IN0, int n_layers, const int64_t* widths, int C) {
-  if (!widths || n_layers < 1 || n_layers > kMaxLayers || C < 1 || C > 64) return 0;
-  int64_t maxw = IN0;
-  for (int l = 0; l < n_layers; ++l) maxw = std::max<int64_t>(maxw, widths[l]);
-  if (maxw > 16 * kNetThreads) return 0;
-  const int64_t words = (int64_t)pick_maxo(maxw) * kNetThreads;  // per activation buffer
-  const int64_t lds = device_lds_bytes();
-  if (2 * words * 8 <= lds) return 64;
-  if (2 * words * 4 <= lds) return 32;
-  return 0;
-}
-
-
-template <typename K>
-static int set_lds(K kern, size_t lds, const char* what) {
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)lds);
-  if (e != hipSuccess) {
-    set_error("%s: LDS %zu: %s", what, lds, hipGetErrorString(e));
-    return (int)e;
-  }
-  return 0;
-}
-
 template <int LAYOUT, typename WT, int MAXO>
 static int launch_net_packed(const void* xp, int B, const NetDesc& d, size_t lds, int64_t tiles,
                              float* logits, hipStream_t st) {
@@ -2459,77 +1719,6 @@ int slg_fc_hard_net(const void* x, int32_t in_kind, int64_t B, int64_t IN0, int3
     return launch_head((const uint64_t*)x, in_kind, B, IN0, widths[0], C, codes[0], 0, nullptr,
                        logits, st);
   return launch_net_any(x, in_kind, (int)B, d, spw, maxo, lds, logits, st);
-}
-
-int slg_conv_hard_head_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, int64_t W,
-                          int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
-                          const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,
-                          int64_t width, const uint32_t* codes, const int32_t* plan,
-                          int32_t n_classes, float* logits, slg_stream_t stream) {
-  SLG_REQUIRE(leaf && tt && codes && ((xp && logits) || B == 0), SLG_E_ARG,
-              "conv_hard_head_wm: null pointer");
-  SLG_REQUIRE(C > 0 && H > 0 && W > 0 && B >= 0 && B < (1LL << 31) && N > 0 && N < 65536 &&
-                  kernel >= 1 && kernel <= 15 && pad >= 0 && pad <= 7 && H < 4096 && W < 4096 &&
-                  C < (1LL << 23),
-              SLG_E_SHAPE, "conv_hard_head_wm: bad conv sizes");
-  const int64_t Hf = H + 2 * pad - kernel + 1, Wf = W + 2 * pad - kernel + 1;
-  SLG_REQUIRE(Hf > 1 && Wf > 1, SLG_E_SHAPE, "conv_hard_head_wm: empty pooled output");
-  const int64_t Ho = Hf / 2, Wo = Wf / 2, nw = cdiv(B, 64);
-  const int64_t Hp = H + 2 * pad, Wp = W + 2 * pad, in0 = N * Ho * Wo;
-  SLG_REQUIRE(nw * C * Hp * Wp * 8 < (1LL << 31), SLG_E_SHAPE, "conv_hard_head_wm: maps too large");
-  SLG_REQUIRE(in0 <= kMaxCompactIn, SLG_E_SHAPE,
-              "conv_hard_head_wm: %lld conv outputs, compact codes take at most %d",
-              (long long)in0, kMaxCompactIn);
-  SLG_REQUIRE(n_classes > 0 && n_classes <= 64 && width > 0 && width % n_classes == 0 &&
-                  width / n_classes <= kHeadMaxG && nw * n_classes < (1LL << 31),
-              SLG_E_SHAPE, "conv_hard_head_wm: head width %lld, %d classes", (long long)width,
-              n_classes);
-  int tm = 0;
-  if (plan) {
-    const int64_t S = slg_fc_hard_type_slots(in0, 1, &width);
-    SLG_REQUIRE(S > 0, SLG_E_UNSUPPORTED, "conv_hard_head_wm: no type-uniform layout here");
-    tm = (int)(S / kNetThreads);
-  }
-  if (B == 0) return 0;
-  const ConvTap cv{xp, leaf, tt, (int)C, (int)Hp, (int)Wp, (int)Ho, (int)Wo, kernel};
-  hipStream_t st = as_stream(stream);
-#define SLG_CH(ND, NL) \
-  return launch_conv_head<ND, NL>(cv, B, in0, width, n_classes, codes, tm, plan, logits, st)
-  if (node_kind == SLG_NODE_GATE16) {
-    switch (depth) {
-      case 1: SLG_CH(SLG_NODE_GATE16, 2);
-      case 2: SLG_CH(SLG_NODE_GATE16, 4);
-      case 3: SLG_CH(SLG_NODE_GATE16, 8);
-      default: break;
-    }
-  } else if ((node_kind == SLG_NODE_MULTILINEAR2 || node_kind == SLG_NODE_HYBRID) && depth == 1) {
-    switch (arity) {
-      case 2: SLG_CH(SLG_NODE_MULTILINEAR2, 2);
-      case 3: SLG_CH(SLG_NODE_MULTILINEAR2, 3);
-      case 4: SLG_CH(SLG_NODE_MULTILINEAR2, 4);
-      case 5: SLG_CH(SLG_NODE_MULTILINEAR2, 5);
-      case 6: SLG_CH(SLG_NODE_MULTILINEAR2, 6);
-      default: break;
-    }
-  }
-#undef SLG_CH
-  set_error("conv_hard_head_wm: node %d depth %d / arity %d", node_kind, depth, arity);
-  return SLG_E_UNSUPPORTED;
-}
-
-int slg_hard_step_fuses_head(const slg_hard_step_t* step) {
-  if (!step || step->n_conv < 1 || step->n_conv > SLG_STEP_MAX_CONV) return 0;
-  const slg_hard_step_t& s = *step;
-  const slg_step_conv_t& c = s.conv[s.n_conv - 1];
-  const bool node_ok = (c.node_kind == SLG_NODE_GATE16 && c.depth >= 1 && c.depth <= 3) ||
-                       ((c.node_kind == SLG_NODE_MULTILINEAR2 || c.node_kind == SLG_NODE_HYBRID) &&
-                        c.depth == 1 && c.arity >= 2 && c.arity <= 6);
-  if (!node_ok || s.n_layers != 1 || !s.widths || s.n_classes < 1 || s.head_in != c.out ||
-      s.head_in_kind != 3 || c.out_pad != 0 || c.kernel < 1)
-    return 0;
-  const int64_t Ho = (c.H + 2 * c.pad - c.kernel + 1) / 2, Wo = (c.W + 2 * c.pad - c.kernel + 1) / 2;
-  return s.head_in_dim == c.N * Ho * Wo &&
-         use_head(1, s.wire_r, 3, s.B, s.widths[0], s.n_classes);
 }
 
 int slg_groupsum_packed(const uint64_t* xp, int64_t W, int64_t B, int32_t C, float* logits,

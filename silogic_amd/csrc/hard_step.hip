@@ -23,8 +23,9 @@ int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
     rc = slg_pack_bits(x, s.dtype, s.B, s.C * s.H * s.W, 1, s.packed, stream);  // word-major
   }
   if (rc) return rc;
-  // a one-layer head at a small batch evaluates the last conv block itself
-  const bool fused = slg_hard_step_fuses_head(step) != 0;
+  // the head may evaluate the last conv block itself (1: a one-layer head
+  // at a small batch, 2: the fused head network)
+  const int fused = slg_hard_step_fuses_head(step);
   for (int i = 0; i < s.n_conv - (fused ? 1 : 0); ++i) {
     const slg_step_conv_t& c = s.conv[i];
     rc = slg_conv_hard_fwd_wm(c.in, s.B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity,
@@ -33,9 +34,13 @@ int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
   }
   if (fused) {
     const slg_step_conv_t& c = s.conv[s.n_conv - 1];
-    return slg_conv_hard_head_wm(c.in, s.B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity,
-                                 c.leaf, c.tt, c.kernel, c.pad, s.widths[0], s.codes[0], s.plan,
-                                 s.n_classes, logits, stream);
+    if (fused == 1)
+      return slg_conv_hard_head_wm(c.in, s.B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity,
+                                   c.leaf, c.tt, c.kernel, c.pad, s.widths[0], s.codes[0], s.plan,
+                                   s.n_classes, logits, stream);
+    return slg_conv_hard_net_wm(c.in, s.B, c.C, c.H, c.W, c.N, c.node_kind, c.depth, c.arity,
+                                c.leaf, c.tt, c.kernel, c.pad, s.n_layers, s.widths, s.codes,
+                                s.plan, s.n_classes, logits, stream);
   }
   const void* hin = s.head_in ? s.head_in : x;
   if (s.plan)

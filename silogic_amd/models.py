@@ -413,9 +413,9 @@ class LogicConvNet(nn.Module):
 class _HardStep:
     """A network's ``forward_hard`` for one input shape on one stream as one
     C-ABI call (``slg_hard_step``): for a conv network packing, every conv
-    block (pooled) and the fused head (a one-layer head at a small batch
-    evaluating the last block itself, ``fuses_head``); for an FC network the
-    fused network on the rows. The per-call host
+    block (pooled) and the fused head (which evaluates the last block itself
+    where ``fuses_head`` is set); for an FC network the fused network on the
+    rows. The per-call host
     work of the general path (parameter walks for each table, shape checks,
     wrapper calls, an allocation per intermediate, a C-ABI call per launch
     with its argument conversion) is done once here, into a
@@ -430,7 +430,8 @@ class _HardStep:
         self.step, self.out_shape, self.st = step, out_shape, st
         self.bufs, self.tables = bufs, tables          # kept alive for the pointers
         self.fn, self.ref = _lib.lib().slg_hard_step, ctypes.byref(step)
-        self.fuses_head = bool(_lib.lib().slg_hard_step_fuses_head(self.ref))
+        # 1: the one-layer head evaluates the last conv block, 2: the fused head network does
+        self.fuses_head = int(_lib.lib().slg_hard_step_fuses_head(self.ref))
         # the descriptor's buffers are shared by every call: a second host
         # thread's packing must not land between this call's packing and
         # the launches that read it

@@ -1195,6 +1195,35 @@ def conv_hard_head_wm(xp, B, shape_chw, leaf, tt, node_kind, depth, arity, kerne
     return out
 
 
+def conv_hard_net_wm(xp, B, shape_chw, leaf, tt, node_kind, depth, arity, kernel, pad, codes, C):
+    """The last pooled conv block and a whole fused head network + GroupSum
+    in one launch (``slg_conv_hard_net_wm``): arguments as
+    :func:`conv_hard_head_wm`, ``codes`` the head's compact per-layer codes
+    (a list, or a :class:`NetCodes`, type-placed or not; no wire residual).
+    Returns logits ``[B, C]``, those of ``conv_hard_wm`` followed by
+    ``fc_hard_net`` on its output."""
+    if not isinstance(codes, NetCodes):
+        codes = NetCodes(codes)
+    require_gpu(xp, leaf, tt)
+    Cc, H, W = shape_chw
+    N = leaf.shape[0]
+    leaves = 2 ** depth if node_kind == GATE16 else arity
+    if (tuple(xp.shape) != (n_words(B), Cc, H + 2 * pad, W + 2 * pad) or not xp.is_contiguous()
+            or leaf.shape != (N, leaves) or tt.shape != (N,)):
+        raise ValueError("conv_hard_net_wm: packed input / leaf / truth-table shapes are "
+                         "inconsistent")
+    in_dim = N * ((H + 2 * pad - kernel + 1) // 2) * ((W + 2 * pad - kernel + 1) // 2)
+    if codes.plan is not None and codes.in_dim != in_dim:
+        raise ValueError("conv_hard_net_wm: type-placed codes take inputs %s wide, the block "
+                         "gives %d" % (codes.in_dim, in_dim))
+    out = torch.empty((B, C), device=xp.device, dtype=torch.float32)
+    plan = _p(codes.plan) if codes.plan is not None else None
+    _lib.call("slg_conv_hard_net_wm", _p(xp), B, Cc, H, W, N, node_kind, depth, arity, _p(leaf),
+              _p(tt), kernel, pad, len(codes), codes.widths, codes.ptrs, plan, C, _p(out),
+              _stream(xp))
+    return out
+
+
 # the custom operators the autograd paths above dispatch to (library.py uses
 # this module's launch helpers, so it is imported once they are defined)
 from . import library as _library  # noqa: E402,F401

@@ -31,8 +31,9 @@ def test_hard_step_matches_the_general_path(cfg, B):
             got = model.forward_hard(x)
             step = model.__dict__["_derived_hard_step"][1]
             assert step is not None
-            # config 5's one-layer head evaluates the last conv block itself
-            assert step.fuses_head == (cfg == 5)
+            # the heads evaluate the last conv block themselves: config 5's one
+            # layer per (word, class), config 3's two-layer network per word
+            assert step.fuses_head == {3: 2, 5: 1}.get(cfg, 0)
             assert torch.equal(got, _general(model, x))
             x8 = x.to(torch.uint8)
             assert torch.equal(model.forward_hard(x8), got)

@@ -1,5 +1,5 @@
 """Register and scratch use of the fused hard-network kernels (and of the
-conv block evaluated inside a conv network's head), read from the
+kernels that evaluate a conv block inside a conv network's head), read from the
 gfx950 assembly (no GPU needed). A private (scratch) access in these
 persistent kernels is a vector memory load that retires in order behind the
 streamed input rows, so it stalls every layer: a spilled register or a
@@ -14,7 +14,8 @@ import pytest
 
 from silogic_amd import _build
 
-KERNEL = re.compile(r"^(_ZN3slg\d+(?:fc_hard_net_(?:rows|packed)|conv_head)_kernel\w*):", re.M)
+KERNEL = re.compile(
+    r"^(_ZN3slg\d+(?:fc_hard_net_(?:rows|packed)|conv_head|conv_net)_kernel\w*):", re.M)
 
 
 @pytest.fixture(scope="module")
@@ -25,12 +26,18 @@ def fc_hard_asm(tmp_path_factory):
         pytest.skip(str(e))
     if not shutil.which(hipcc) and not os.path.exists(hipcc):
         pytest.skip("hipcc not found")
-    out = tmp_path_factory.mktemp("asm") / "fc_hard.s"
-    src = os.path.join(_build.CSRC, "fc_hard.hip")
-    r = subprocess.run([hipcc] + _build.FLAGS + ["--cuda-device-only", "-S", "-I", _build.CSRC,
-                        src, "-o", str(out)], capture_output=True, text=True)
-    assert r.returncode == 0, r.stderr[-3000:]
-    return out.read_text()
+    tmp = tmp_path_factory.mktemp("asm")
+    procs = []
+    for name in ("fc_hard", "conv_net"):
+        src = os.path.join(_build.CSRC, name + ".hip")
+        procs.append(subprocess.Popen(
+            [hipcc] + _build.FLAGS + ["--cuda-device-only", "-S", "-I", _build.CSRC, src, "-o",
+                                      str(tmp / (name + ".s"))],
+            stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    for p in procs:
+        _, err = p.communicate()
+        assert p.returncode == 0, err[-3000:]
+    return (tmp / "fc_hard.s").read_text() + (tmp / "conv_net.s").read_text()
 
 
 def test_fused_network_kernels_use_no_scratch(fc_hard_asm):
@@ -38,6 +45,7 @@ def test_fused_network_kernels_use_no_scratch(fc_hard_asm):
     names = KERNEL.findall(text)
     assert len(names) >= 32, len(names)
     assert sum("conv_head" in n for n in names) == 8, names
+    assert sum("conv_net" in n for n in names) == 32, names
     bad = []
     for name in names:
         start = text.index(name + ":")
