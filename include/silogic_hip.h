@@ -656,9 +656,9 @@ int slg_hard_step(const slg_hard_step_t* step, const void* x, float* logits,
  * for other heads at batches of at most one 64-sample word per CU whose
  * fused network has 64-sample words and activation buffers of 2048 or 4096
  * words that fit LDS beside one word's block input; both need a head
- * without wire residual on the block's own output
- * (no border) and a node the fused kernels evaluate (gate16 trees of depth
- * 1-3, LUTs of arity 2-6); else 0. No counterpart in the reference. */
+ * without wire residual on the block's own output (no border) and a node
+ * the fused kernel evaluates (gate16 trees of depth 1-3; LUTs of arity 2-6
+ * for 1, 2-4 for 2); else 0. No counterpart in the reference. */
 int slg_hard_step_fuses_head(const slg_hard_step_t* step);
 
 /* The last pooled conv block of a conv network and its one-layer head +
@@ -696,7 +696,7 @@ int slg_conv_hard_head_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, i
  * bit. SLG_E_UNSUPPORTED unless the network takes 64-sample words with
  * activation buffers of 2048 or 4096 words, LDS holds them and one word's
  * block input (C*(H+2pad)*(W+2pad) words, staged there), and the node is a
- * gate16 tree of depth 1-3 or a LUT of arity 2-6. */
+ * gate16 tree of depth 1-3 or a LUT of arity 2-4. */
 int slg_conv_hard_net_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, int64_t W,
                          int64_t N, int32_t node_kind, int32_t depth, int32_t arity,
                          const int32_t* leaf, const uint64_t* tt, int32_t kernel, int32_t pad,

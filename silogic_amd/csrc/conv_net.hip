@@ -14,13 +14,17 @@ namespace slg {
 
 constexpr int kConvHeadMaxIn = 1 << 14;   // operand indices of compact codes: 14 bits
 
-// Nodes the kernels here evaluate: gate16 trees of depth 1-3, LUTs of
-// arity 2-6 (the conv block kernel's nodes, gate16 depth 4 aside).
-inline bool conv_node_fuses(int kind, int depth, int arity) {
+// Nodes the kernels here evaluate: gate16 trees of depth 1-3 and LUTs of
+// arity 2 to max_arity (the conv block kernel's nodes, gate16 depth 4
+// aside): 6 in the head kernel; 4 in the network kernel, whose 1024-thread
+// workgroups leave a thread 128 VGPRs, fewer than a LUT5 or LUT6 tree with
+// per-lane masks holds.
+inline bool conv_node_fuses(int kind, int depth, int arity, int max_arity = 6) {
   return (kind == SLG_NODE_GATE16 && depth >= 1 && depth <= 3) ||
          ((kind == SLG_NODE_MULTILINEAR2 || kind == SLG_NODE_HYBRID) && depth == 1 &&
-          arity >= 2 && arity <= 6);
+          arity >= 2 && arity <= max_arity);
 }
+constexpr int kNetMaxArity = 4;
 
 // The last pooled conv block of a conv network evaluated inside its
 // one-layer head (LogicConvNet.forward_hard's last ConvLogicTree + OrPool
@@ -344,7 +348,8 @@ int slg_hard_step_fuses_head(const slg_hard_step_t* step) {
   if (use_head(s.n_layers, 0, 3, s.B, s.widths[0], s.n_classes)) return 1;
   const int nleaf = c.node_kind == SLG_NODE_GATE16 ? 1 << c.depth : c.arity;
   const int64_t img = conv_stage_words(c.C, c.H + 2 * c.pad, c.W + 2 * c.pad, c.N, nleaf);
-  return cdiv(s.B, 64) <= device_cus() &&
+  return conv_node_fuses(c.node_kind, c.depth, c.arity, kNetMaxArity) &&
+                 cdiv(s.B, 64) <= device_cus() &&
                  conv_net_maxo(s.head_in_dim, s.n_layers, s.widths, s.plan, s.n_classes, img) > 0
              ? 2
              : 0;
@@ -377,7 +382,7 @@ int slg_conv_hard_net_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, in
   SLG_REQUIRE(n_classes > 0 && n_classes <= 64 && widths[n_layers - 1] % n_classes == 0,
               SLG_E_SHAPE, "conv_hard_net_wm: last width %lld, %d classes",
               (long long)widths[n_layers - 1], n_classes);
-  SLG_REQUIRE(conv_node_fuses(node_kind, depth, arity), SLG_E_UNSUPPORTED,
+  SLG_REQUIRE(conv_node_fuses(node_kind, depth, arity, kNetMaxArity), SLG_E_UNSUPPORTED,
               "conv_hard_net_wm: node %d depth %d / arity %d", node_kind, depth, arity);
   const int nleaf = node_kind == SLG_NODE_GATE16 ? 1 << depth : arity;
   const int maxo = conv_net_maxo(in0, n_layers, widths, plan, n_classes,
@@ -406,9 +411,7 @@ int slg_conv_hard_net_wm(const uint64_t* xp, int64_t B, int64_t C, int64_t H, in
   switch (arity) {
     case 2: SLG_CN(SLG_NODE_MULTILINEAR2, 2);
     case 3: SLG_CN(SLG_NODE_MULTILINEAR2, 3);
-    case 4: SLG_CN(SLG_NODE_MULTILINEAR2, 4);
-    case 5: SLG_CN(SLG_NODE_MULTILINEAR2, 5);
-    default: SLG_CN(SLG_NODE_MULTILINEAR2, 6);
+    default: SLG_CN(SLG_NODE_MULTILINEAR2, 4);
   }
 #undef SLG_CN
 }

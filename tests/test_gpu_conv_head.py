@@ -5,7 +5,10 @@ block's output (slg_fc_hard_net / slg_fc_hard_net_typed): the logits bit for
 bit. Cases: gate16 trees of depth 1-3 and LUTs of arity 2-6 (random tables,
 so every 3-input byte of a LUT6 takes some value); kernels 1-3 with their
 paddings; compact codes in index order and type-placed codes; batches that
-end inside a word; config 5's block 1 and head shape."""
+end inside a word; config 5's block 1 and head shape. The same for
+slg_conv_hard_net_wm (the last block inside a multi-layer head network:
+gate16 depths 1-3, LUT arities 2-4, config 3's block 2 and head) and its
+refusals."""
 import pytest
 import torch
 
@@ -121,7 +124,7 @@ def test_net_gate16_trees(depth, typed):
 
 
 @pytest.mark.parametrize("typed", [False, True])
-@pytest.mark.parametrize("arity", [2, 3, 4, 5, 6])
+@pytest.mark.parametrize("arity", [2, 3, 4])
 def test_net_lut_trees(arity, typed):
     _check_net(B=64 + 33, C=12, H=8, W=8, N=40, kind=ops.MULTILINEAR2, depth=1, arity=arity,
                kernel=3, pad=1, widths=[3000, 300], n_cls=10, typed=typed, seed=40 + arity)
@@ -146,3 +149,17 @@ def test_net_refuses_wide_heads():
     codes = ops.fc_hard_codes_net([l.hard_spec() for l in layers], compact=True)
     with pytest.raises(HipError):
         ops.conv_hard_net_wm(xw, 64, (4, 8, 8), leaf, tt, ops.GATE16, 2, 2, 3, 1, codes, 10)
+
+
+@pytest.mark.parametrize("arity", [5, 6])
+def test_net_refuses_luts_past_arity_4(arity):
+    from silogic_amd._lib import HipError
+    g = torch.Generator().manual_seed(2)
+    leaf, tt = _conv_params(8, 4, 3, arity, g)
+    xw = torch.zeros((1, 4, 10, 10), dtype=torch.int64, device=DEV)
+    layers = [sl.LogicLayer(8 * 16, 1000, k=4, seed=1).to(DEV),
+              sl.LogicLayer(1000, 100, k=4, seed=2).to(DEV)]
+    codes = ops.fc_hard_codes_net([l.hard_spec() for l in layers], compact=True)
+    with pytest.raises(HipError):
+        ops.conv_hard_net_wm(xw, 64, (4, 8, 8), leaf, tt, ops.MULTILINEAR2, 1, arity, 3, 1,
+                             codes, 10)
