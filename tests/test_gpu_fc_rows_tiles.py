@@ -145,3 +145,43 @@ def test_groupsum_of_32_sample_words(C, G):
         xp = ops.fc_hard_layer(xp, c)
     want = ops.groupsum_packed(xp, B, C)
     assert torch.equal(got, want), int((got != want).any(1).sum())
+
+
+@pytest.mark.parametrize("C,G", [
+    (1, 7),
+    (3, 250),
+    (10, 1000),      # config 2's classes
+    (5, 1024),       # one full pass
+    (9, 1025),       # a second pass of one word
+    (4, 2047),
+    (3, 3000),       # three passes
+    (13, 640),
+])
+def test_groupsum_of_64_sample_words(C, G):
+    """The fused network's class counts on 64-sample words: constant-1 last
+    layers count G for every sample; random last layers match the per-layer
+    kernels followed by the separate packed GroupSum kernel. Rows here
+    stream through the rows kernel (1000 features) and, packed, through the
+    packed-network kernel; class counts from 1 to 13 and class sizes across
+    one to three 1024-word passes."""
+    in_dim, widths, B = 1000, [3000, C * G], 64 * 2 + 21
+    assert ops.fc_hard_net_supported(in_dim, widths, C) == 64
+    g = torch.Generator().manual_seed(C * G + 1)
+    x = (torch.rand(B, in_dim, generator=g) < 0.5).float().to(DEV)
+    print(f"groupsum 64: C {C} G {G}", flush=True)
+    ones = _stack(in_dim, widths, 81, ones_last=True)
+    codes = ops.fc_hard_codes_net([l.hard_spec() for l in ones], compact=True)
+    full = torch.full((B, C), float(G), device=DEV)
+    assert torch.equal(ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, codes, C), full)
+    xw = ops.pack_bits(x, word_major=True)
+    assert torch.equal(ops.fc_hard_net(xw, ops.PACKED_WORD_MAJOR, B, in_dim, codes, C), full)
+    rnd = _stack(in_dim, widths, 91)
+    codes = ops.fc_hard_codes_net([l.hard_spec() for l in rnd], compact=True)
+    got = ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, codes, C)
+    got_p = ops.fc_hard_net(xw, ops.PACKED_WORD_MAJOR, B, in_dim, codes, C)
+    xp = ops.pack_bits(x)
+    for c in ops.fc_hard_codes_net([l.hard_spec() for l in rnd]):
+        xp = ops.fc_hard_layer(xp, c)
+    want = ops.groupsum_packed(xp, B, C)
+    assert torch.equal(got, want), int((got != want).any(1).sum())
+    assert torch.equal(got_p, want)
