@@ -279,3 +279,35 @@ def test_derived_cache_follows_parameter_versions():
     assert get() == 4
     derived.clear(m)
     assert get() == 5
+    m.idx = torch.arange(5)                 # buffer replaced by assignment
+    assert get() == 6
+    m.double()                              # Module._apply: new buffer objects in _buffers
+    assert get() == 7 and get() == 7
+
+
+def test_derived_cache_follows_the_module_tree():
+    """The key's tensors come from a list of the module tree's dictionaries
+    kept per module: a child module replaced, added to a ModuleList or set
+    to None, and a parameter registered on a child, all change the key."""
+    from silogic_amd import derived
+    net = torch.nn.Module()
+    net.a = torch.nn.Linear(3, 2)
+    net.seq = torch.nn.ModuleList([torch.nn.Linear(2, 2)])
+    k0 = derived.state_key(net)
+    assert derived.state_key(net) == k0
+    net.a = torch.nn.Linear(3, 2)                     # child replaced
+    k1 = derived.state_key(net)
+    assert k1 != k0
+    net.seq.append(torch.nn.Linear(2, 2))             # child added
+    k2 = derived.state_key(net)
+    assert len(k2) == len(k1) + 2
+    net.seq[0].extra = torch.nn.Parameter(torch.ones(1))   # parameter on a child
+    k3 = derived.state_key(net)
+    assert len(k3) == len(k2) + 1
+    net.a = None                                      # child removed
+    assert len(derived.state_key(net)) == len(k3) - 2
+    # the same tensors as a full walk, in the same order
+    ts = []
+    derived._tensors(net, ts)
+    assert derived.state_key(net) == tuple((t.data_ptr(), t._version) for t in ts
+                                           if t is not None)
