@@ -792,7 +792,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the workload shards by batch; see DESIGN.md). Run with --gpus 1.",
+              "(the workload would shard by batch, one slice per GPU). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     if args.config:
