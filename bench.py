@@ -522,7 +522,8 @@ def hard_launches(cfg, model, x_hard):
             cus = torch.cuda.get_device_properties(x_hard.device).multi_processor_count
             if a[1] in (0, 1):       # rows: packing inside
                 nbytes = B * in_dim * isz + B * C * 4 + codes
-                if in_dim <= 1024 and ops.fc_hard_net_supported(in_dim, widths, C) == 64:
+                spw = ops.fc_hard_net_supported(in_dim, widths, C)
+                if in_dim <= 1024 and spw == 64 and 4 * nw > cus:
                     kname = f"fc_hard_net_rows_kernel (packing + {len(widths)} layers + GroupSum)"
                 else:                # a tile per workgroup, packed in LDS
                     kname = (f"fc_hard_net_packed_kernel (packing per tile + {len(widths)} "

@@ -185,3 +185,22 @@ def test_groupsum_of_64_sample_words(C, G):
     want = ops.groupsum_packed(xp, B, C)
     assert torch.equal(got, want), int((got != want).any(1).sum())
     assert torch.equal(got_p, want)
+
+
+@pytest.mark.parametrize("B", [1, 64, 200, 64 * 64, 64 * 65])
+def test_small_batches_take_32_sample_tiles(B):
+    """Rows of a 64-sample-word network at batches of at most one tile per
+    four CUs are packed per 32-sample tile (256 CUs: B <= 4096); above, the
+    streaming rows kernel. Both match the packed 64-sample words' path."""
+    in_dim, widths, C = 784, [2000, 2000, 2000], 10
+    assert ops.fc_hard_net_supported(in_dim, widths, C) == 64
+    codes = _codes(in_dim, widths, 51)
+    typed = ops.fc_hard_type_place_net(codes, in_dim)
+    g = torch.Generator().manual_seed(B)
+    x = (torch.rand(B, in_dim, generator=g) < 0.4).float().to(DEV)
+    print(f"small batch rows: B {B}", flush=True)
+    want = ops.fc_hard_net(ops.pack_bits(x, word_major=True), ops.PACKED_WORD_MAJOR, B, in_dim,
+                           codes, C)
+    for c in (codes, typed):
+        assert torch.equal(ops.fc_hard_net(x, ops.ROWS_F32, B, in_dim, c, C), want)
+        assert torch.equal(ops.fc_hard_net(x.to(torch.uint8), ops.ROWS_U8, B, in_dim, c, C), want)
